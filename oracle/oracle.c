@@ -1,0 +1,772 @@
+/*
+ * oracle.c -- CPU restatement of the reference's quantized mat-vec hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for the HIP library,
+ * never part of it. Built with -ffp-contract=off so that every `a*b + c` below
+ * is two IEEE roundings; explicit fmaf() is used exactly where the compiled
+ * reference fuses (its _mm256_fmadd_ps calls, and the scalar accumulations g++
+ * contracts under its default -ffp-contract=fast).
+ *
+ * Reference paths cited as file:line relative to the reference repository.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static const uint32_t k_iq3xxs_grid[256] = {
+#include "iq3xxs_grid.inc"
+};
+
+uint32_t oc_type_size(int type) {
+    /* src/cpp/core/GGUFLoader.cpp:64 (ggmlTypeSize); pinned by
+     * unit_tests/DequantizeTest.cpp:570 (Q4_K=144, IQ3_XXS=98). */
+    switch (type) {
+        case OC_TYPE_Q8_0: return 34;
+        case OC_TYPE_Q4_K: return 144;
+        case OC_TYPE_Q6_K: return 210;
+        case OC_TYPE_IQ3_XXS: return 98;
+        default: return 0;
+    }
+}
+
+uint32_t oc_block_size(int type) {
+    return type == OC_TYPE_Q8_0 ? 32u : (oc_type_size(type) ? 256u : 0u);
+}
+
+/* ---- fp16 <-> fp32 -------------------------------------------------------- */
+
+/* include/GGMLDequantize.hpp:89-141 (halfToFloat): exact IEEE widening with
+ * subnormal normalisation. */
+float oc_half_to_float(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) & 1u;
+    uint32_t exp = (uint32_t)(h >> 10) & 0x1Fu;
+    uint32_t mant = (uint32_t)h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign << 31;
+        } else {
+            int shift = 0;
+            while ((mant & 0x400u) == 0) {
+                mant <<= 1;
+                ++shift;
+            }
+            mant &= 0x3FFu;
+            bits = (sign << 31) | ((uint32_t)(113 - shift) << 23) | (mant << 13);
+        }
+    } else if (exp == 31) {
+        bits = (sign << 31) | (0xFFu << 23) | (mant << 13);
+    } else {
+        bits = (sign << 31) | ((exp + 112u) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* include/GGMLDequantize.hpp:61-87 (floatToHalf): TRUNCATES the mantissa (no
+ * rounding), saturates exponents above 15 to inf, flushes below 2^-24. */
+uint16_t oc_float_to_half(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    uint32_t sign = (b >> 31) & 1u;
+    int32_t exp = (int32_t)((b >> 23) & 0xFFu) - 127;
+    uint32_t mant = b & 0x7FFFFFu;
+    uint32_t h;
+    if (exp > 15) {
+        h = (sign << 15) | (0x1Fu << 10) | (mant != 0 ? 0x200u : 0u);
+    } else if (exp > -14) {
+        h = (sign << 15) | ((uint32_t)(exp + 15) << 10) | (mant >> 13);
+    } else if (exp > -24) {
+        mant = (mant | 0x800000u) >> (14 - exp);
+        h = (sign << 15) | (mant >> 13);
+    } else {
+        h = sign << 15;
+    }
+    return (uint16_t)h;
+}
+
+/* IEEE fp32 -> fp16, round to nearest even (used by this build's own
+ * encoders; the reference's floatToHalf truncates and flushes every value below
+ * 2^-13 to zero because its subnormal branch also takes exponent -14). */
+static uint16_t f2h_rne(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (ax < 0x38800000u) {
+        float a;
+        memcpy(&a, &ax, 4);
+        return (uint16_t)(sign | (uint32_t)lrintf(a * 16777216.0f));
+    }
+    uint32_t h = ((((ax >> 23) - 112u)) << 10) | ((ax & 0x7FFFFFu) >> 13);
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+}
+
+static float h2f_at(const uint8_t *p) {
+    uint16_t h;
+    memcpy(&h, p, 2);
+    return oc_half_to_float(h);
+}
+
+/* ---- activation quantizers ------------------------------------------------- */
+
+/* Signed value of the FIRST element with the largest |x| (strict '>' scan). */
+static float first_abs_max(const float *x, uint32_t n, float *amax_out) {
+    float amax = 0.0f, maxv = 0.0f;
+    for (uint32_t j = 0; j < n; ++j) {
+        float ax = fabsf(x[j]);
+        if (ax > amax) {
+            amax = ax;
+            maxv = x[j];
+        }
+    }
+    *amax_out = amax;
+    return maxv;
+}
+
+static int8_t quant_one(float iscale, float v) {
+    long q = lrintf(iscale * v);
+    return (int8_t)(q < 127 ? q : 127);
+}
+
+/* include/GGMLDequantize.hpp:2769-2807 (quantizeQ8K). */
+void oc_quantize_q8k(const float *x, uint32_t n, int8_t *qs, float *d, int16_t *bsums) {
+    for (uint32_t b = 0; b < n / 256; ++b) {
+        const float *xb = x + (size_t)b * 256;
+        int8_t *q = qs + (size_t)b * 256;
+        float amax;
+        float maxv = first_abs_max(xb, 256, &amax);
+        if (amax == 0.0f) {
+            d[b] = 0.0f;
+            memset(q, 0, 256);
+            memset(bsums + (size_t)b * 16, 0, 32);
+            continue;
+        }
+        const float iscale = -127.0f / maxv;
+        for (uint32_t j = 0; j < 256; ++j) q[j] = quant_one(iscale, xb[j]);
+        for (uint32_t g = 0; g < 16; ++g) {
+            int s = 0;
+            for (uint32_t i = 0; i < 16; ++i) s += q[g * 16 + i];
+            bsums[(size_t)b * 16 + g] = (int16_t)s;
+        }
+        d[b] = 1.0f / iscale;
+    }
+}
+
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:4296-4326 (per-call Q8_0 activation
+ * quantization inside matMulVecBatchQ8_0_Q8K_AVX2): same rule as quantizeQ8K
+ * on 32-element blocks, fp32 scale, no bsums. */
+void oc_quantize_q8_0_act(const float *x, uint32_t n, int8_t *qs, float *d) {
+    for (uint32_t b = 0; b < n / 32; ++b) {
+        const float *xb = x + (size_t)b * 32;
+        int8_t *q = qs + (size_t)b * 32;
+        float amax;
+        float maxv = first_abs_max(xb, 32, &amax);
+        if (amax == 0.0f) {
+            d[b] = 0.0f;
+            memset(q, 0, 32);
+            continue;
+        }
+        const float iscale = -127.0f / maxv;
+        for (uint32_t j = 0; j < 32; ++j) q[j] = quant_one(iscale, xb[j]);
+        d[b] = 1.0f / iscale;
+    }
+}
+
+/* ---- block decoders ---------------------------------------------------------- */
+
+/* Q4_K 6-bit scale/min unpack: include/GGMLDequantize.hpp:444-453
+ * (getScaleMin, ggml get_scale_min_k4 order). */
+static void q4k_scale_min(const uint8_t *s, int j, uint8_t *sc, uint8_t *m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+        *m = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+/* Q6_K raw 6-bit value (0..63) of element e of a block:
+ * include/GGMLDequantize.hpp:503-527. */
+static int q6k_raw(const uint8_t *blk, int e) {
+    const int half = e >> 7, r = e & 127, quad = r >> 5, l = r & 31;
+    const uint8_t *ql = blk + 64 * half;
+    const uint8_t *qh = blk + 128 + 32 * half;
+    int lo = (quad & 1) ? ql[l + 32] : ql[l];
+    lo = (quad & 2) ? (lo >> 4) : (lo & 0xF);
+    int hi = (qh[l] >> (2 * quad)) & 3;
+    return lo | (hi << 4);
+}
+
+/* IQ3_XXS signed integer weight (grid magnitude with sign) of element e:
+ * include/GGMLDequantize.hpp:1135-1161 and the sign table :671-674
+ * (ksigns_iq2xs[i] = i | parity(i) << 7). Returns the integer value; the
+ * per-32 scale is (2*ls+1) (dot form :2064) or d*(0.5+ls)*0.5 (float form). */
+static int iq3_signed(const uint8_t *blk, int e, int *ls_out) {
+    const uint8_t *qs = blk + 2;
+    const uint8_t *sas = blk + 2 + 64;
+    const int ib32 = e >> 5, r = e & 31, l = r >> 3, j = r & 7;
+    uint32_t aux;
+    memcpy(&aux, sas + 4 * ib32, 4);
+    const uint32_t idx7 = (aux >> (7 * l)) & 127u;
+    const uint32_t signs = idx7 | ((uint32_t)__builtin_parity(idx7) << 7);
+    const uint8_t gi = qs[8 * ib32 + 2 * l + (j >> 2)];
+    const int mag = (int)((k_iq3xxs_grid[gi] >> (8 * (j & 3))) & 0xFFu);
+    *ls_out = (int)(aux >> 28);
+    return (signs >> j) & 1u ? -mag : mag;
+}
+
+int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
+    const uint32_t bs = oc_block_size(type), ts = oc_type_size(type);
+    if (bs == 0 || n % bs) return -1;
+    for (uint32_t b = 0; b < n / bs; ++b) {
+        const uint8_t *blk = w + (size_t)b * ts;
+        float *y = out + (size_t)b * bs;
+        if (type == OC_TYPE_Q8_0) {
+            /* include/GGMLDequantize.hpp:243-250 */
+            const float d = h2f_at(blk);
+            for (int i = 0; i < 32; ++i) y[i] = (float)(int8_t)blk[2 + i] * d;
+        } else if (type == OC_TYPE_Q4_K) {
+            /* include/GGMLDequantize.hpp:436-477 */
+            const float d = h2f_at(blk), dmin = h2f_at(blk + 2);
+            for (int g = 0; g < 8; ++g) {
+                uint8_t sc, m;
+                q4k_scale_min(blk + 4, g, &sc, &m);
+                const float d1 = d * (float)sc, m1 = dmin * (float)m;
+                const uint8_t *q = blk + 16 + 32 * (g >> 1);
+                for (int l = 0; l < 32; ++l) {
+                    const int v = (g & 1) ? (q[l] >> 4) : (q[l] & 0xF);
+                    y[32 * g + l] = d1 * (float)v - m1;
+                }
+            }
+        } else if (type == OC_TYPE_Q6_K) {
+            /* include/GGMLDequantize.hpp:503-527: y = d * sc * q, evaluated
+             * left to right as (d*sc)*q with q = raw-32. */
+            const float d = h2f_at(blk + 208);
+            const int8_t *sc = (const int8_t *)(blk + 192);
+            for (int e = 0; e < 256; ++e) {
+                const int q = q6k_raw(blk, e) - 32;
+                y[e] = d * (float)sc[e >> 4] * (float)q;
+            }
+        } else {
+            /* include/GGMLDequantize.hpp:1135-1161:
+             * y = db * grid * sign, db = d * (0.5 + ls) * 0.5. */
+            const float d = h2f_at(blk);
+            for (int e = 0; e < 256; ++e) {
+                int ls;
+                const int v = iq3_signed(blk, e, &ls);
+                const float db = d * (0.5f + (float)ls) * 0.5f;
+                const float mag = (float)(v < 0 ? -v : v);
+                y[e] = db * mag * (v < 0 ? -1.0f : 1.0f);
+            }
+        }
+    }
+    return 0;
+}
+
+/* ---- per-block integer dots --------------------------------------------------- */
+
+/* Q4_K sub-block integer sums s32q[i] = sum_32 nibble * q8 (the maddubs/madd
+ * chain of src/cpp/core/SIMDMatMulVecAVX2.cpp:3690-3702). */
+static void q4k_subsums(const uint8_t *blk, const int8_t *xq, int32_t s[8]) {
+    const uint8_t *qs = blk + 16;
+    for (int i = 0; i < 8; ++i) {
+        int32_t acc = 0;
+        const uint8_t *q = qs + 32 * (i >> 1);
+        for (int l = 0; l < 32; ++l) {
+            const int v = (i & 1) ? (q[l] >> 4) : (q[l] & 0xF);
+            acc += v * xq[32 * i + l];
+        }
+        s[i] = acc;
+    }
+}
+
+/* Q6_K block integer sum_g sc[g] * sum_16 (raw - 32) * q8: the exact integer
+ * that matMulVecBatchQ6K_Q8K_AVX2's blockDot scales by d*d8
+ * (src/cpp/core/SIMDMatMulVecAVX2.cpp:4636-4667, -32 folded via bsums). */
+static int32_t q6k_isum(const uint8_t *blk, const int8_t *xq) {
+    const int8_t *sc = (const int8_t *)(blk + 192);
+    int32_t tot = 0;
+    for (int g = 0; g < 16; ++g) {
+        int32_t s = 0;
+        for (int i = 0; i < 16; ++i) s += (q6k_raw(blk, 16 * g + i) - 32) * xq[16 * g + i];
+        tot += (int32_t)sc[g] * s;
+    }
+    return tot;
+}
+
+/* IQ3_XXS block integer bsum = sum_ib32 (2*ls+1) * sum_32 grid*sign*q8:
+ * include/GGMLDequantize.hpp:2064-2097 (dotProductIQ3_XXS_Q8K). */
+static int32_t iq3_isum(const uint8_t *blk, const int8_t *xq) {
+    int32_t bsum = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+        int32_t sumi = 0;
+        int ls = 0;
+        for (int r = 0; r < 32; ++r) sumi += iq3_signed(blk, 32 * ib + r, &ls) * xq[32 * ib + r];
+        bsum += sumi * (2 * ls + 1);
+    }
+    return bsum;
+}
+
+/* Q8_0 block sum_32 w*q8, the true integer product (the reference kernel's
+ * sum, src/cpp/core/SIMDMatMulVecAVX2.cpp:4346-4356, equals it whenever no
+ * weight byte is -128). */
+static int32_t q80_isum(const uint8_t *blk, const int8_t *xq) {
+    int32_t s = 0;
+    for (int i = 0; i < 32; ++i) s += (int8_t)blk[2 + i] * xq[i];
+    return s;
+}
+
+typedef struct {
+    int8_t *qs;
+    float *d;
+    int16_t *bsums;
+} act_t;
+
+static int quantize_acts(int type, const float *X, uint32_t S, uint32_t cols, act_t *a) {
+    a->qs = (int8_t *)malloc((size_t)S * cols);
+    a->d = (float *)malloc(sizeof(float) * ((size_t)S * cols / 32 + 1));
+    a->bsums = (int16_t *)malloc(sizeof(int16_t) * ((size_t)S * cols / 16 + 1));
+    if (!a->qs || !a->d || !a->bsums) return -1;
+    for (uint32_t s = 0; s < S; ++s) {
+        if (type == OC_TYPE_Q8_0)
+            oc_quantize_q8_0_act(X + (size_t)s * cols, cols, a->qs + (size_t)s * cols,
+                                 a->d + (size_t)s * (cols / 32));
+        else
+            oc_quantize_q8k(X + (size_t)s * cols, cols, a->qs + (size_t)s * cols,
+                            a->d + (size_t)s * (cols / 256), a->bsums + (size_t)s * (cols / 16));
+    }
+    return 0;
+}
+
+static void free_acts(act_t *a) {
+    free(a->qs);
+    free(a->d);
+    free(a->bsums);
+}
+
+static int shape_ok(int type, uint32_t cols) {
+    const uint32_t bs = oc_block_size(type);
+    return bs != 0 && cols != 0 && cols % bs == 0;
+}
+
+int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
+                   uint32_t rows, uint32_t cols, int32_t *isums) {
+    if (!shape_ok(type, cols)) return -1;
+    act_t a;
+    if (quantize_acts(type, X, S, cols, &a)) return -1;
+    const uint32_t bs = oc_block_size(type), ts = oc_type_size(type), nb = cols / bs;
+    const uint32_t k = type == OC_TYPE_Q4_K ? 8 : 1;
+    for (uint32_t s = 0; s < S; ++s)
+        for (uint32_t r = 0; r < rows; ++r)
+            for (uint32_t b = 0; b < nb; ++b) {
+                const uint8_t *blk = W + ((size_t)r * nb + b) * ts;
+                const int8_t *xq = a.qs + (size_t)s * cols + (size_t)b * bs;
+                int32_t *o = isums + (((size_t)s * rows + r) * nb + b) * k;
+                switch (type) {
+                    case OC_TYPE_Q4_K: q4k_subsums(blk, xq, o); break;
+                    case OC_TYPE_Q6_K: o[0] = q6k_isum(blk, xq); break;
+                    case OC_TYPE_IQ3_XXS: o[0] = iq3_isum(blk, xq); break;
+                    default: o[0] = q80_isum(blk, xq); break;
+                }
+            }
+    free_acts(&a);
+    return 0;
+}
+
+/* ---- row kernels with the reference float evaluation order ---------------- */
+
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:3649-3715 (seqLen==1 row path; the batch
+ * path :3719-3830 has the same per-block math and block-order accumulation).
+ * The three accumulations `x += a*b` are fused multiply-adds: g++ compiles C++
+ * with -ffp-contract=fast, and with -mfma it contracts them (verified by the
+ * bit-exact golden vectors from the compiled reference). */
+static float row_q4k(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff,
+                     size_t boff) {
+    float sum = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 144;
+        const float d = h2f_at(blk), dmin = h2f_at(blk + 2);
+        int32_t s32[8];
+        q4k_subsums(blk, a->qs + qoff + (size_t)b * 256, s32);
+        const int16_t *bsums = a->bsums + boff + (size_t)b * 16;
+        float mainS = 0.0f, minS = 0.0f;
+        for (int i = 0; i < 8; ++i) {
+            uint8_t sc, m;
+            q4k_scale_min(blk + 4, i, &sc, &m);
+            const float ds = d * (float)sc;
+            const float mn = dmin * (float)m;
+            mainS = fmaf(ds, (float)s32[i], mainS);
+            minS = fmaf(mn, (float)(bsums[2 * i] + bsums[2 * i + 1]), minS);
+        }
+        sum = fmaf(a->d[doff + b], mainS - minS, sum);
+    }
+    return sum;
+}
+
+/* AVX2 horizontal float sum used by the reference store paths:
+ * lo+hi, then two _mm_hadd_ps (SIMDMatMulVecAVX2.cpp:4353-4356, 4729-4735). */
+static float hsum8(const float v[8]) {
+    const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+    return (s0 + s1) + (s2 + s3);
+}
+
+/* Product w*x as the reference Q8_0 kernel forms it: |x| * sign(w, x) through
+ * _mm256_sign_epi8 / _mm256_maddubs_epi16 (SIMDMatMulVecAVX2.cpp:4348-4351).
+ * sign_epi8 cannot negate -128, so w = -128 with x < 0 contributes -128*|x|
+ * instead of +128*|x|. Encoders never emit -128 (they clamp to +-127); the
+ * true product is what oc_block_isums reports. */
+static int32_t q80_maddubs_product(int8_t w, int8_t x) {
+    if (x == 0) return 0;
+    const int ax = x < 0 ? -x : x;
+    const int8_t ws = x < 0 ? (int8_t)(uint8_t)(0u - (uint8_t)w) : w;
+    return ax * ws;
+}
+
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:4239-4383 (matMulVecBatchQ8_0_Q8K_AVX2):
+ * per block, 8 int32 lanes of 4-byte partial dots scaled by d*d8 in fp32,
+ * horizontally summed, added to a scalar accumulator; blocks with d8 == 0 are
+ * skipped. */
+static float row_q80(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff) {
+    float acc = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 34;
+        const float d = h2f_at(blk);
+        const float d8 = a->d[doff + b];
+        if (d8 == 0.0f) continue;
+        const int8_t *xq = a->qs + qoff + (size_t)b * 32;
+        const float dd8 = d * d8;
+        float v[8];
+        for (int j = 0; j < 8; ++j) {
+            int32_t s = 0;
+            for (int k = 0; k < 4; ++k) s += q80_maddubs_product((int8_t)blk[2 + 4 * j + k], xq[4 * j + k]);
+            v[j] = dd8 * (float)s;
+        }
+        acc += hsum8(v);
+    }
+    return acc;
+}
+
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:4410-4743 (matMulVecBatchQ6K_Q8K_AVX2):
+ * blockDot keeps 8 float lanes: lane j starts at (-32*d*d8) * (sc[2j]*bsum[2j] +
+ * sc[2j+1]*bsum[2j+1]); each 128-element chunk adds fma(d*d8, sumi_j, acc_j),
+ * where sumi_j = sum over the chunk's 4 sub-blocks of the scale for lane j's
+ * 16-half times the 4-byte partial dot of bytes 4j..4j+3. Blocks are summed
+ * lane-wise and the 8 lanes are horizontally summed once per row. */
+static float row_q6k(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff,
+                     size_t boff) {
+    float racc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 210;
+        const float d = h2f_at(blk + 208);
+        const int8_t *sc = (const int8_t *)(blk + 192);
+        const float d8 = a->d[doff + b];
+        const int8_t *xq = a->qs + qoff + (size_t)b * 256;
+        const int16_t *bsums = a->bsums + boff + (size_t)b * 16;
+        const float c0 = -32.0f * d * d8;
+        const float dd8 = d * d8;
+        float acc[8];
+        for (int j = 0; j < 8; ++j) {
+            const int32_t bp = (int32_t)sc[2 * j] * bsums[2 * j] + (int32_t)sc[2 * j + 1] * bsums[2 * j + 1];
+            acc[j] = c0 * (float)bp;
+        }
+        for (int chunk = 0; chunk < 2; ++chunk) {
+            int32_t sumi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int sub = 0; sub < 4; ++sub) {
+                const int idx = chunk * 4 + sub;
+                for (int j = 0; j < 8; ++j) {
+                    int32_t p = 0;
+                    for (int k = 0; k < 4; ++k) {
+                        const int e = 32 * idx + 4 * j + k;
+                        p += q6k_raw(blk, e) * xq[e];
+                    }
+                    sumi[j] += (int32_t)sc[2 * idx + (j >= 4)] * p;
+                }
+            }
+            for (int j = 0; j < 8; ++j) acc[j] = fmaf(dd8, (float)sumi[j], acc[j]);
+        }
+        for (int j = 0; j < 8; ++j) racc[j] = racc[j] + acc[j];
+    }
+    return hsum8(racc);
+}
+
+/* include/GGMLDequantize.hpp:2231-2269 (matMulVecBatchQ8K) with the IQ3_XXS
+ * block dot :2064-2097 and the row scale 0.25 (:2148-2159). */
+static float row_iq3(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff) {
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 98;
+        const float d = h2f_at(blk) * a->d[doff + b];
+        const int32_t bsum = iq3_isum(blk, a->qs + qoff + (size_t)b * 256);
+        sumf += d * (float)bsum;
+    }
+    return 0.25f * sumf;
+}
+
+int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t rows,
+              uint32_t cols, float *out) {
+    if (!shape_ok(type, cols)) return -1;
+    act_t a;
+    if (quantize_acts(type, X, S, cols, &a)) return -1;
+    const uint32_t bs = oc_block_size(type), ts = oc_type_size(type), nb = cols / bs;
+    for (uint32_t s = 0; s < S; ++s) {
+        const size_t qoff = (size_t)s * cols;
+        const size_t doff = (size_t)s * (cols / bs);
+        const size_t boff = (size_t)s * (cols / 16);
+        for (uint32_t r = 0; r < rows; ++r) {
+            const uint8_t *rp = W + (size_t)r * nb * ts;
+            float v;
+            switch (type) {
+                case OC_TYPE_Q4_K: v = row_q4k(rp, nb, &a, qoff, doff, boff); break;
+                case OC_TYPE_Q6_K: v = row_q6k(rp, nb, &a, qoff, doff, boff); break;
+                case OC_TYPE_IQ3_XXS: v = row_iq3(rp, nb, &a, qoff, doff); break;
+                default: v = row_q80(rp, nb, &a, qoff, doff); break;
+            }
+            out[(size_t)s * rows + r] = v;
+        }
+    }
+    free_acts(&a);
+    return 0;
+}
+
+/* ---- weight encoders ----------------------------------------------------------- */
+
+/* src/cpp/core/GGMLQuantize.cpp:47-95 (quantizeQ4KBlock): per 32-group affine
+ * fit scale=(max-min)/15, min=-min (clamped at 0 by starting the scan at 0),
+ * 6-bit sub-scales against fp16 super-scales maxScale/63 and maxMin/63, packed
+ * in get_scale_min_k4 order (GGMLQuantize.cpp:37-45). */
+void oc_encode_q4k_block(const float *x, uint8_t *out) {
+    float scale[8], minv[8];
+    uint8_t q[256];
+    float maxScale = 0.0f, maxMin = 0.0f;
+    for (int g = 0; g < 8; ++g) {
+        const float *xp = x + 32 * g;
+        float mn = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            mn = xp[i] < mn ? xp[i] : mn;
+            mx = mx < xp[i] ? xp[i] : mx;
+        }
+        const float sc = (mx - mn) / 15.0f;
+        scale[g] = sc;
+        minv[g] = -mn;
+        maxScale = maxScale < sc ? sc : maxScale;
+        maxMin = maxMin < minv[g] ? minv[g] : maxMin;
+        for (int i = 0; i < 32; ++i) {
+            int v = sc > 1e-30f ? (int)lrintf((xp[i] - mn) / sc) : 0;
+            v = v < 0 ? 0 : (v > 15 ? 15 : v);
+            q[32 * g + i] = (uint8_t)v;
+        }
+    }
+    const uint16_t hd = maxScale > 0.0f ? oc_float_to_half(maxScale / 63.0f) : 0;
+    const uint16_t hdm = maxMin > 0.0f ? oc_float_to_half(maxMin / 63.0f) : 0;
+    const float d = oc_half_to_float(hd), dm = oc_half_to_float(hdm);
+    uint8_t sc6[8], m6[8];
+    for (int g = 0; g < 8; ++g) {
+        int s = d > 1e-30f ? (int)lrintf(scale[g] / d) : 0;
+        int m = dm > 1e-30f ? (int)lrintf(minv[g] / dm) : 0;
+        sc6[g] = (uint8_t)(s < 0 ? 0 : (s > 63 ? 63 : s));
+        m6[g] = (uint8_t)(m < 0 ? 0 : (m > 63 ? 63 : m));
+    }
+    memcpy(out, &hd, 2);
+    memcpy(out + 2, &hdm, 2);
+    for (int j = 0; j < 4; ++j) {
+        out[4 + j] = (uint8_t)(sc6[j] | ((sc6[j + 4] >> 4) << 6));
+        out[4 + j + 4] = (uint8_t)(m6[j] | ((m6[j + 4] >> 4) << 6));
+        out[4 + j + 8] = (uint8_t)((sc6[j + 4] & 0x0F) | ((m6[j + 4] & 0x0F) << 4));
+    }
+    uint8_t *qs = out + 16;
+    memset(qs, 0, 128);
+    for (int g = 0; g < 8; ++g)
+        for (int i = 0; i < 32; ++i) qs[32 * (g >> 1) + i] |= (uint8_t)(q[32 * g + i] << (4 * (g & 1)));
+}
+
+/* Q8_0 weight encoder (the reference ships none; BASELINE config #1 defines it):
+ * d = max|w|/127 stored as fp16 (round to nearest even), q = round to
+ * nearest even of w / d_fp16,
+ * clamped to [-127, 127]. */
+void oc_encode_q8_0_block(const float *x, uint8_t *out) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) amax = fabsf(x[i]) > amax ? fabsf(x[i]) : amax;
+    const uint16_t hd = f2h_rne(amax / 127.0f);
+    const float d = oc_half_to_float(hd);
+    memcpy(out, &hd, 2);
+    for (int i = 0; i < 32; ++i) {
+        long q = d > 0.0f ? lrintf(x[i] / d) : 0;
+        q = q < -127 ? -127 : (q > 127 ? 127 : q);
+        out[2 + i] = (uint8_t)(int8_t)q;
+    }
+}
+
+/* Q6_K weight encoder (the reference ships none; this build defines it).
+ * Per 16-group: signed first-abs-max m, group scale m/-32. Block: signed
+ * first-abs-max of the group scales M, iscale = -128/M, sc = min(127,
+ * rne(iscale*scale)), d = 1/iscale stored as fp16 (RNE). Weights:
+ * q = clamp(rne(x / (d_fp16*sc)), -32, 31) + 32, packed as the decoder
+ * include/GGMLDequantize.hpp:503-527 reads them. */
+void oc_encode_q6k_block(const float *x, uint8_t *out) {
+    float gs[16];
+    for (int g = 0; g < 16; ++g) {
+        float amax;
+        const float m = first_abs_max(x + 16 * g, 16, &amax);
+        gs[g] = amax == 0.0f ? 0.0f : m / -32.0f;
+    }
+    float amaxs;
+    const float M = first_abs_max(gs, 16, &amaxs);
+    memset(out, 0, 210);
+    uint8_t L[256];
+    if (amaxs == 0.0f) {
+        for (int e = 0; e < 256; ++e) L[e] = 32;
+    } else {
+        const float iscale = -128.0f / M;
+        int8_t *sc = (int8_t *)(out + 192);
+        for (int g = 0; g < 16; ++g) {
+            long v = lrintf(iscale * gs[g]);
+            sc[g] = (int8_t)(v > 127 ? 127 : v);
+        }
+        const uint16_t hd = f2h_rne(1.0f / iscale);
+        memcpy(out + 208, &hd, 2);
+        const float dh = oc_half_to_float(hd);
+        for (int e = 0; e < 256; ++e) {
+            const float dg = dh * (float)sc[e >> 4];
+            long q = dg != 0.0f ? lrintf(x[e] / dg) : 0;
+            q = q < -32 ? -32 : (q > 31 ? 31 : q);
+            L[e] = (uint8_t)(q + 32);
+        }
+    }
+    for (int half = 0; half < 2; ++half) {
+        uint8_t *ql = out + 64 * half;
+        uint8_t *qh = out + 128 + 32 * half;
+        const uint8_t *Lh = L + 128 * half;
+        for (int l = 0; l < 32; ++l) {
+            const int q1 = Lh[l], q2 = Lh[l + 32], q3 = Lh[l + 64], q4 = Lh[l + 96];
+            ql[l] = (uint8_t)((q1 & 0xF) | ((q3 & 0xF) << 4));
+            ql[l + 32] = (uint8_t)((q2 & 0xF) | ((q4 & 0xF) << 4));
+            qh[l] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+        }
+    }
+}
+
+/* IQ3_XXS weight encoder (the reference ships none; this build defines it).
+ * Per 32-chunk c: s_c = max|x| / 62 (62 = largest grid magnitude). Block:
+ * d = max_c s_c / 7.75 stored as fp16 (RNE); ls_c = clamp(rne(s_c /
+ * (0.5*d) - 0.5), 0, 15); db = d*(0.5+ls)*0.5 (the decoder's expression).
+ * Signs per 8: the negative elements, with the smallest-|x| (first) element's
+ * sign flipped when the count is odd (the format stores 7 sign bits and
+ * implies the 8th by even parity). Magnitudes per 4: the grid entry with the
+ * least sum of squared differences to |x|/db (first on ties), sums formed in
+ * index order without FMA. */
+void oc_encode_iq3xxs_block(const float *x, uint8_t *out) {
+    float sc[8], smax = 0.0f;
+    for (int c = 0; c < 8; ++c) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fabsf(x[32 * c + i]) > amax ? fabsf(x[32 * c + i]) : amax;
+        sc[c] = amax / 62.0f;
+        smax = sc[c] > smax ? sc[c] : smax;
+    }
+    memset(out, 0, 98);
+    const uint16_t hd = f2h_rne(smax / 7.75f);
+    const float d = oc_half_to_float(hd);
+    if (d == 0.0f) return;
+    memcpy(out, &hd, 2);
+    uint8_t *qs = out + 2;
+    uint8_t *sas = out + 66;
+    for (int c = 0; c < 8; ++c) {
+        long lsl = lrintf(sc[c] / (0.5f * d) - 0.5f);
+        const int ls = lsl < 0 ? 0 : (lsl > 15 ? 15 : (int)lsl);
+        const float db = d * (0.5f + (float)ls) * 0.5f;
+        uint32_t aux = (uint32_t)ls << 28;
+        for (int l = 0; l < 4; ++l) {
+            const float *xv = x + 32 * c + 8 * l;
+            uint32_t neg = 0;
+            int minj = 0;
+            for (int j = 0; j < 8; ++j) {
+                if (xv[j] < 0.0f) neg |= 1u << j;
+                if (fabsf(xv[j]) < fabsf(xv[minj])) minj = j;
+            }
+            if (__builtin_parity(neg)) neg ^= 1u << minj;
+            aux |= (neg & 127u) << (7 * l);
+            for (int h = 0; h < 2; ++h) {
+                float t[4];
+                for (int j = 0; j < 4; ++j) t[j] = fabsf(xv[4 * h + j]) / db;
+                int best = 0;
+                float berr = 0.0f;
+                for (int gi = 0; gi < 256; ++gi) {
+                    float err = 0.0f;
+                    for (int j = 0; j < 4; ++j) {
+                        const float diff = (float)((k_iq3xxs_grid[gi] >> (8 * j)) & 0xFFu) - t[j];
+                        err = err + diff * diff;
+                    }
+                    if (gi == 0 || err < berr) {
+                        berr = err;
+                        best = gi;
+                    }
+                }
+                qs[8 * c + 2 * l + h] = (uint8_t)best;
+            }
+        }
+        memcpy(sas + 4 * c, &aux, 4);
+    }
+}
+
+int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8_t *out) {
+    if (!shape_ok(type, cols)) return -1;
+    const uint32_t bs = oc_block_size(type), ts = oc_type_size(type);
+    const size_t nblk = (size_t)rows * (cols / bs);
+    for (size_t i = 0; i < nblk; ++i) {
+        const float *xb = x + i * bs;
+        uint8_t *o = out + i * ts;
+        switch (type) {
+            case OC_TYPE_Q8_0: oc_encode_q8_0_block(xb, o); break;
+            case OC_TYPE_Q4_K: oc_encode_q4k_block(xb, o); break;
+            case OC_TYPE_Q6_K: oc_encode_q6k_block(xb, o); break;
+            default: oc_encode_iq3xxs_block(xb, o); break;
+        }
+    }
+    return 0;
+}
+
+/* ---- MoE expert FFN ----------------------------------------------------------- */
+
+/* src/cpp/core/ModelMoE.cpp:660-672 (the math statement) with the per-expert
+ * path :566-600 and the rank-order reduction :990-1002: per (token s, rank r):
+ * g = Wg[e] x, u = Wu[e] x (Q4_K mat-vec, Q8_K activations), h = g/(1+exp(-g))*u,
+ * down = Wd[e] h (Q8_K quantization of h), partial = wg*down; out[s] starts at
+ * 0 and adds partial for r = 0..K-1 in order. */
+int oc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t S, uint32_t K,
+               const uint8_t *wg, const uint8_t *wu, const uint8_t *wd, uint32_t E, uint32_t H,
+               uint32_t FF, float *out) {
+    if (H % 256 || FF % 256) return -1;
+    const size_t gBytes = (size_t)FF * (H / 256) * 144;
+    const size_t dBytes = (size_t)H * (FF / 256) * 144;
+    float *g = (float *)malloc(sizeof(float) * FF);
+    float *u = (float *)malloc(sizeof(float) * FF);
+    float *dn = (float *)malloc(sizeof(float) * H);
+    if (!g || !u || !dn) return -1;
+    for (uint32_t s = 0; s < S; ++s) {
+        float *o = out + (size_t)s * H;
+        for (uint32_t i = 0; i < H; ++i) o[i] = 0.0f;
+        for (uint32_t r = 0; r < K; ++r) {
+            const int32_t e = ids[(size_t)s * K + r];
+            if (e < 0 || (uint32_t)e >= E) continue;
+            const float *xs = x + (size_t)s * H;
+            oc_matmul(OC_TYPE_Q4_K, wg + (size_t)e * gBytes, xs, 1, FF, H, g);
+            oc_matmul(OC_TYPE_Q4_K, wu + (size_t)e * gBytes, xs, 1, FF, H, u);
+            for (uint32_t i = 0; i < FF; ++i) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+            oc_matmul(OC_TYPE_Q4_K, wd + (size_t)e * dBytes, g, 1, H, FF, dn);
+            const float w = wts[(size_t)s * K + r];
+            for (uint32_t i = 0; i < H; ++i) o[i] += w * dn[i];
+        }
+    }
+    free(g);
+    free(u);
+    free(dn);
+    return 0;
+}

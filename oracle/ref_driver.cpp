@@ -1,0 +1,89 @@
+// ref_driver.cpp -- C-ABI wrappers over the reference's OWN CPU functions,
+// linked against the reference translation units compiled in place from the
+// reference tree (see oracle/Makefile). TEST INFRASTRUCTURE ONLY: used to write
+// the golden vectors under tests/golden and as the "reference" CPU baseline in
+// bench.py; never linked into the product.
+//
+// Nothing here restates arithmetic: each wrapper forwards to the reference
+// function named in its comment (paths relative to the reference root).
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "GGMLDequantize.hpp"
+#include "GGMLQuantize.hpp"
+#include "SIMDMatMulVecInternal.hpp"
+#include "ThreadPool.hpp"
+
+using namespace tinycoder;
+
+extern "C" {
+
+// src/cpp/core/ThreadPool.cpp:236 (initialize) with
+// ThreadPool::recommendedThreadCount() (:68) when n == 0. Returns the count.
+int ref_init_threads(int n) {
+    size_t t = n > 0 ? static_cast<size_t>(n) : ThreadPool::recommendedThreadCount();
+    ThreadPool::instance().initialize(t);
+    return static_cast<int>(ThreadPool::instance().numThreads());
+}
+
+// include/GGMLDequantize.hpp:89
+float ref_half_to_float(uint16_t h) { return GGMLDequantize::halfToFloat(h); }
+// include/GGMLDequantize.hpp:61
+uint16_t ref_float_to_half(float f) { return GGMLDequantize::floatToHalf(f); }
+
+// include/GGMLDequantize.hpp:2769 -> unpacked qs[n], d[n/256], bsums[n/16].
+void ref_quantize_q8k(const float *x, uint32_t n, int8_t *qs, float *d, int16_t *bsums) {
+    std::vector<Q8KBlock> b(n / 256);
+    GGMLDequantize::quantizeQ8K(x, n, b.data());
+    for (uint32_t i = 0; i < n / 256; ++i) {
+        std::memcpy(qs + 256 * i, b[i].qs, 256);
+        d[i] = b[i].d;
+        std::memcpy(bsums + 16 * i, b[i].bsums, 32);
+    }
+}
+
+// include/GGMLDequantize.hpp:243 / :436 / :503 / :1135 (one block each).
+void ref_dequant_block(int type, const uint8_t *blk, float *out) {
+    switch (type) {
+        case 8: GGMLDequantize::dequantizeQ8_0Block(blk, out); break;
+        case 12: GGMLDequantize::dequantizeQ4_KBlock(blk, out); break;
+        case 14: GGMLDequantize::dequantizeQ6_KBlock(blk, out); break;
+        case 18: GGMLDequantize::dequantizeIQ3_XXSBlock(blk, out); break;
+        default: break;
+    }
+}
+
+// src/cpp/core/GGMLQuantize.cpp:47
+void ref_quantize_q4k_block(const float *x, uint8_t *out) {
+    GGMLQuantize::quantizeQ4KBlock(x, out);
+}
+
+// include/GGMLDequantize.hpp:2064 (per-block d*bsum, unscaled).
+float ref_dot_iq3xxs_q8k(const uint8_t *blk, const float *x256) {
+    Q8KBlock q;
+    GGMLDequantize::quantizeQ8K(x256, 256, &q);
+    return GGMLDequantize::dotProductIQ3_XXS_Q8K(blk, &q);
+}
+
+// The CPU kernels the reference dispatches to for each type:
+//   Q4_K  src/cpp/core/SIMDMatMulVecAVX2.cpp:3614
+//   Q8_0  src/cpp/core/SIMDMatMulVecAVX2.cpp:4239
+//   Q6_K  src/cpp/core/SIMDMatMulVecAVX2.cpp:4410
+//   IQ3_XXS include/GGMLDequantize.hpp:2231 (scalar matMulVecBatchQ8K; the
+//         type has no SIMD kernel, src/cpp/core/ModelInternal.cpp:499)
+// out[seqLen][rows]. Returns 0 on success.
+int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint32_t rows,
+               uint32_t cols, float *out) {
+    switch (type) {
+        case 12: simd::matMulVecBatchQ4K_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
+        case 8: simd::matMulVecBatchQ8_0_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
+        case 14: simd::matMulVecBatchQ6K_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
+        case 18:
+            GGMLDequantize::matMulVecBatchQ8K(GGML_TYPE_IQ3_XXS, W, X, seqLen, rows, cols, out);
+            return 0;
+        default: return -1;
+    }
+}
+
+}  // extern "C"
