@@ -1,0 +1,233 @@
+"""Benchmark of the quantized mat-vec hot path on one MI355X.
+
+Default workload (BASELINE config #2): one Qwen2.5-7B-shaped decoder layer of
+Q4_K decode mat-vecs at batch 1 -- q 3584x3584, k/v 512x3584, o 3584x3584,
+gate/up 18944x3584, down 3584x18944 -- with weights drawn from N(0, 0.02)
+and quantized by the reference's own Q4_K quantizer (bit-exact GPU port),
+activations N(0, 1). A step is one pass over the layer in decode order, as 4
+launches: q/k/v in one launch on the shared input, o, gate/up as a pair with
+the SwiGLU epilogue, down (each launch quantizes its input in-kernel). The weights of 8 identical layer copies are rotated step by
+step (1.05 GB working set) so that the 256 MB Infinity Cache cannot serve them.
+
+Prints one JSON line. `value` is whole-step weight+activation bytes per
+second (GB/s); `roofline` is the Q4_K mat-vec kernel alone, timed with HIP
+events on the stream it runs on; `cpu_baseline` is the reference's own AVX2
+kernel (compiled from its sources, oracle/_ref) on the host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tinycoder-inference_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Q4_K decode GEMV GB/s (% HBM peak) at batch 1; int8 prefill GEMM TOPS"
+LAYER = [("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584), ("o", 3584, 3584),
+         ("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)]
+# activation groups: matrices that read the same input vector
+GROUPS = [("attn", 3584, ["q", "k", "v"]), ("o_in", 3584, ["o"]), ("ffn", 3584, ["gate", "up"]),
+          ("down_in", 18944, ["down"])]
+N_COPIES = 8
+
+
+def algorithmic_bytes(rows, cols, row_bytes):
+    # weights + fp32 activation read + fp32 output write, per mat-vec
+    return rows * row_bytes + 4 * cols + 4 * rows
+
+
+def cpu_baseline(weights_host, xs_host, row_bytes):
+    """The reference's CPU kernel (or the C port if the reference build is
+    absent) over full layer passes for a bounded ~8 s sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    threads = min(os.cpu_count() or 1, 16)
+    try:
+        impl = O.Reference(threads=threads)
+        kind = "reference"
+        threads = impl.threads
+    except (FileNotFoundError, OSError):
+        impl = O.Oracle()
+        kind = "port"
+        threads = 1
+    outs = {n: np.zeros((1, r), np.float32) for n, r, _ in LAYER}
+    xmap = {}
+    for g, _, names in GROUPS:
+        for n in names:
+            xmap[n] = xs_host[g]
+
+    def one_pass():
+        for n, r, c in LAYER:
+            if kind == "reference":
+                impl.matmul(12, weights_host[n], xmap[n], r, c, out=outs[n])
+            else:
+                outs[n][:] = impl.matmul(12, weights_host[n], xmap[n], r, c)
+
+    one_pass()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        one_pass()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 8.0 or reps >= 2000:
+            break
+    per_pass = sum(algorithmic_bytes(r, c, row_bytes(12, c)) for _, r, c in LAYER)
+    return {"value": round(per_pass * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{reps} full-layer passes (7 Q4_K mat-vecs, {per_pass / 1e6:.1f} MB each) in {el:.1f} s, "
+                      f"{'reference AVX2 matMulVecBatchQ4K_Q8K_AVX2 + ThreadPool' if kind == 'reference' else 'C port, 1 thread'}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
+              "(the hot path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import tc_hip
+
+    dev = torch.device("cuda:0")
+    tc = tc_hip.Library()
+    Q4K = tc_hip.Q4_K
+    gen = torch.Generator(device=dev).manual_seed(20261201)
+
+    # ---- weights: encode once, replicate into rotating copies --------------------
+    base = {}
+    for n, r, c in LAYER:
+        wf = torch.randn((r, c), generator=gen, device=dev) * 0.02
+        base[n] = tc.encode(Q4K, wf)
+        del wf
+    copies = [{n: base[n].clone() for n in base} for _ in range(N_COPIES)]
+    xs = {g: torch.randn((1, c), generator=gen, device=dev) for g, c, _ in GROUPS}
+    outs = {n: torch.empty((1, r), device=dev) for n, r, _ in LAYER}
+    dims = {n: (r, c) for n, r, c in LAYER}
+    torch.cuda.synchronize()
+
+    h_out = torch.empty((1, 18944), device=dev)
+    u_out = torch.empty((1, 18944), device=dev)
+    LAUNCHES = [("qkv", ["q", "k", "v"]), ("o", ["o"]), ("gate_up", ["gate", "up"]), ("down", ["down"])]
+
+    def launch(name, ws):
+        if name == "qkv":
+            tc.gemv_multi(Q4K, [ws["q"], ws["k"], ws["v"]], [xs["attn"]] * 3, [3584, 512, 512], [3584] * 3,
+                          outs=[outs["q"], outs["k"], outs["v"]])
+        elif name == "o":
+            tc.gemv(Q4K, ws["o"], xs["o_in"], 3584, 3584, out=outs["o"])
+        elif name == "gate_up":
+            tc.lib.tc_gemv_dual(Q4K, tc_hip._ptr(ws["gate"]), tc_hip._ptr(ws["up"]), tc_hip._ptr(xs["ffn"]),
+                                tc_hip._ptr(h_out), tc_hip._ptr(u_out), 18944, 3584, tc._stream())
+        else:
+            tc.gemv(Q4K, ws["down"], xs["down_in"], 3584, 18944, out=outs["down"])
+
+    def step(i, events=None):
+        ws = copies[i % N_COPIES]
+        for name, _ in LAUNCHES:
+            if events is not None:
+                events[name].append((torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)))
+                events[name][-1][0].record()
+            launch(name, ws)
+            if events is not None:
+                events[name][-1][1].record()
+
+    def step_one_launch(i):
+        ws = copies[i % N_COPIES]
+        names = [n for n, _, _ in LAYER]
+        xin = {"q": "attn", "k": "attn", "v": "attn", "o": "o_in", "gate": "ffn", "up": "ffn", "down": "down_in"}
+        tc.gemv_multi(Q4K, [ws[n] for n in names], [xs[xin[n]] for n in names], [dims[n][0] for n in names],
+                      [dims[n][1] for n in names], outs=[outs[n] for n in names])
+
+    for i in range(args.warmup):
+        step(i)
+        step_one_launch(i)
+    torch.cuda.synchronize()
+
+    def head_start():
+        # Keep the GPU busy for a bounded time while the host queues the timed
+        # launches, so that events measure back-to-back GPU execution and not
+        # the Python launch rate.
+        try:
+            torch.cuda._sleep(int(60e6))
+        except (AttributeError, RuntimeError):
+            pass
+
+    # ---- timed region: K steps ------------------------------------------------------
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    head_start()
+    t_start.record()
+    for i in range(args.steps):
+        step(i)
+    t_end.record()
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+
+    # the same layer as one launch (7 independent mat-vecs, one kernel)
+    t1s = torch.cuda.Event(enable_timing=True)
+    t1e = torch.cuda.Event(enable_timing=True)
+    head_start()
+    t1s.record()
+    for i in range(args.steps):
+        step_one_launch(i)
+    t1e.record()
+    torch.cuda.synchronize()
+    one_launch_ms = t1s.elapsed_time(t1e) / args.steps
+
+    # ---- per-launch kernel durations (events around each launch) -----------------------
+    events = {n: [] for n, _ in LAUNCHES}
+    head_start()
+    for i in range(args.steps):
+        step(i, events)
+    torch.cuda.synchronize()
+    rb = tc_hip.row_bytes
+    per_launch = {}
+    tot_bytes = tot_us = 0.0
+    for name, mats in LAUNCHES:
+        us = float(np.mean([a.elapsed_time(b) for a, b in events[name]])) * 1e3
+        by = sum(algorithmic_bytes(dims[m][0], dims[m][1], rb(Q4K, dims[m][1])) for m in mats)
+        per_launch[name] = {"mats": mats, "us": round(us, 2), "GB/s": round(by / us / 1e3, 1),
+                            "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 3)}
+        tot_bytes += by
+        tot_us += us
+    achieved = tot_bytes / tot_us / 1e3
+
+    step_bytes = sum(algorithmic_bytes(r, c, rb(Q4K, c)) for _, r, c in LAYER)
+    ms_per_step = total_ms / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    one_launch_gbs = step_bytes / (one_launch_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: W ~ N(0,0.02) -> reference Q4_K quantizer, x ~ N(0,1)",
+        "config": {"workload": "qwen2.5-7b layer, Q4_K decode mat-vec, batch 1 (q,k,v,o,gate,up,down)",
+                   "batch": 1, "weight_bytes_per_step": int(sum(r * rb(Q4K, c) for _, r, c in LAYER)),
+                   "rotating_copies": N_COPIES, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv<Q4_K,1>, bytes-weighted over the 4 launches of a step"},
+        "per_launch": per_launch,
+        "layer_one_launch": {"us": round(one_launch_ms * 1e3, 2), "GB/s": round(one_launch_gbs, 1),
+                             "frac": round(one_launch_gbs / HBM_PEAK_GBS, 4)},
+    }
+    if not args.no_cpu:
+        wh = {n: base[n].cpu().numpy() for n in base}
+        xh = {g: xs[g].cpu().numpy() for g in xs}
+        line["cpu_baseline"] = cpu_baseline(wh, xh, rb)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,146 @@
+/*
+ * tc_qmatmul.h -- C-ABI of the MI355X (gfx950) quantized mat-vec / GEMM
+ * library (libtc_hip.so). Plain pointers and sizes only.
+ *
+ * Conventions shared by every entry point:
+ *   - Device pointers: weights `w` are raw row-major GGUF blocks
+ *     (row bytes = cols / block_elems * block_bytes), activations `x` are fp32
+ *     [seq_len][cols], outputs are fp32 [seq_len][rows] (token-major), exactly
+ *     the layouts of the reference's int8Gemm/int8Gemv (include/Int8Gemm.hpp:42-107).
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - Weight type ids are GGML's: TC_Q8_0 = 8, TC_Q4_K = 12, TC_Q6_K = 14,
+ *     TC_IQ3_XXS = 18 (reference include/IModelLoader.hpp:51-62).
+ *   - Return value: TC_OK (0) on success, a negative TC_E_* code otherwise;
+ *     nothing is written to outputs when a shape or type is refused.
+ *     tc_last_error() gives a message for the calling thread's last failure.
+ *   - Numerics: activations are quantized with the reference CPU rule for the
+ *     weight type (Q8_K, 256-wide, for Q4_K / Q6_K / IQ3_XXS; 32-wide with an
+ *     fp32 scale for Q8_0), bit-identical to the CPU; per-block integer sums are
+ *     exact; fp32 outputs agree with the CPU reference within 1e-3 relative /
+ *     1e-4 absolute.
+ *   - Not thread-safe per device: calls share the library's grow-only scratch
+ *     and must be serialized (as the reference's, GemmDispatch.cu:236-252).
+ */
+#ifndef TC_QMATMUL_H
+#define TC_QMATMUL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { TC_Q8_0 = 8, TC_Q4_K = 12, TC_Q6_K = 14, TC_IQ3_XXS = 18 };
+
+enum {
+    TC_OK = 0,
+    TC_E_UNSUPPORTED = -1, /* type or shape not handled: caller falls back */
+    TC_E_LAUNCH = -2,      /* a HIP launch or allocation failed */
+    TC_E_ARG = -3,         /* null pointer or inconsistent argument */
+};
+
+/* Device query (once per process, like GemmDispatch.cu:208-234 ctx()).
+ * Replaces tinycoder::gpu::int8GemmAvailable (include/Int8Gemm.hpp:45):
+ * 1 when a gfx950 device is present and TINYCODER_INT8_GEMM is not "0". */
+int tc_available(void);
+
+/* Decode mat-vec, seq_len 1..8: out[s][r] = x[s] . W[r].
+ * Replaces tinycoder::gpu::int8Gemv (include/Int8Gemm.hpp:77-78,
+ * src/cpp/core/cuda/gemm/GemmDispatch.cu:788). cols % 256 == 0. */
+int tc_gemv(int type, const void *w, const float *x, float *out, uint32_t seq_len, uint32_t rows,
+            uint32_t cols, void *stream);
+
+/* Several decode mat-vecs of one weight type in ONE launch, each with its own
+ * input: out[i][s][r] = x[i][s] . W[i][r] for i < n (n <= 8). Host arrays of
+ * device pointers / sizes. The reference's fused Q+K+V decode kernel
+ * (TINYCODER_FUSE_QKV, ENVIRONMENT.md:29; include/gpu/GpuGemvIQ.hpp:806) is
+ * the case n = 3 with x[0] = x[1] = x[2]. seq_len 1..8. */
+int tc_gemv_multi(int type, uint32_t n, const void *const *w, const float *const *x, float *const *out,
+                  const uint32_t *rows, const uint32_t *cols, uint32_t seq_len, void *stream);
+
+/* Two-phase decode: quantize once, reuse for every matrix that reads the same
+ * activation (q/k/v, gate/up). `act` is a caller-owned device buffer of
+ * tc_act_bytes(type, seq_len, cols) bytes (256-byte aligned). Activations
+ * quantized for Q4_K, Q6_K and IQ3_XXS are interchangeable (Q8_K); Q8_0 needs
+ * its own (32-wide). */
+size_t tc_act_bytes(int type, uint32_t seq_len, uint32_t cols);
+int tc_act_quantize(int type, const float *x, uint32_t seq_len, uint32_t cols, void *act, void *stream);
+
+/* Decode mat-vec on pre-quantized activations (filled by tc_act_quantize for
+ * the same seq_len and cols). Replaces launchQGemvQ81
+ * (include/gpu/GpuGemvIQInt8.hpp:891), which takes a pre-quantized
+ * activation buffer. seq_len 1..8. */
+int tc_gemv_q8(int type, const void *w, const void *act, float *out, uint32_t seq_len, uint32_t rows,
+               uint32_t cols, void *stream);
+
+/* Pre-size the activation scratch so that later tc_gemv / tc_gemm calls of
+ * at most this size allocate nothing (e.g. before a hipGraph capture).
+ * Replaces tinycoder::gpu::int8GemvReserve (include/Int8Gemm.hpp:82). */
+int tc_gemv_reserve(uint32_t cols, uint32_t seq_len);
+
+/* Fused gate/up decode mat-vec (seq_len 1): uout = Wu x, gout = silu(Wg x) * uout.
+ * Replaces int8GemvDualQ4K / int8GemvDualIQ3 (include/Int8Gemm.hpp:90-107). */
+int tc_gemv_dual(int type, const void *wg, const void *wu, const float *x, float *gout, float *uout,
+                 uint32_t rows, uint32_t cols, void *stream);
+
+/* Prefill GEMM, seq_len >= 1: out[seq_len][rows] = x[seq_len][cols] @ W^T with
+ * the int8 MFMA kernel. Replaces tinycoder::gpu::int8Gemm
+ * (include/Int8Gemm.hpp:57-59, GemmDispatch.cu:595). blocks_per_row must
+ * equal cols / block_elems. */
+int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_len, uint32_t rows,
+            uint32_t cols, uint32_t blocks_per_row, void *stream);
+
+/* Shape-based preference of the int8 path over an fp16 twin. The fp16-twin
+ * path does not exist in this build, so it answers 1 for every supported type.
+ * Replaces tinycoder::gpu::int8GemmPreferred (include/Int8Gemm.hpp:73). */
+int tc_gemm_preferred(uint32_t type, uint32_t rows, uint32_t cols);
+
+/* Enable / disable the Q8_0 GEMM path at run time.
+ * Replaces tinycoder::gpu::int8GemmSetQ8Enabled (include/Int8Gemm.hpp:88). */
+void tc_gemm_set_q8_enabled(int enabled);
+
+/* Activation quantizer for weight type `type`, into caller buffers:
+ * qs int8 [seq_len][cols], d fp32 [seq_len][cols/256] (Q8_K) or [cols/32]
+ * (Q8_0 weights), bsums int16 [seq_len][cols/16] (Q8_K only; may be NULL for
+ * Q8_0). Test/parity hook equal to the CPU's quantizeQ8K
+ * (include/GGMLDequantize.hpp:2769) / the Q8_0 kernel's quantizer
+ * (SIMDMatMulVecAVX2.cpp:4296). */
+int tc_quantize_act(int type, const float *x, uint32_t seq_len, uint32_t cols, int8_t *qs, float *d,
+                    int16_t *bsums, void *stream);
+
+/* Per-block integer sums of the decode kernel (the GPU side of the
+ * reference's parity hooks GPUModel::debugQ8KBlocks / debugQ8_0Blocks,
+ * include/GPUCompute.hpp:399-460, as a free function over a whole matrix):
+ * isums[seq_len][rows][nblk][k], k = 8 sub-block sums for Q4_K, else 1
+ * (nblk = cols/32 for Q8_0). The same kernel as tc_gemv computes them. */
+int tc_block_isums(int type, const void *w, const float *x, int32_t *isums, uint32_t seq_len,
+                   uint32_t rows, uint32_t cols, void *stream);
+
+/* Weight encoder: fp32 [rows][cols] -> raw GGUF blocks of `type`. Q4_K is the
+ * reference's own quantizer (src/cpp/core/GGMLQuantize.cpp:47, bit-exact);
+ * Q8_0 / Q6_K / IQ3_XXS are this library's encoders (the reference has none).
+ * Replaces GGMLQuantize::quantizeQ4KBlock (include/GGMLQuantize.hpp:56). */
+int tc_encode(int type, const float *x, void *out, uint32_t rows, uint32_t cols, void *stream);
+
+/* Bytes of one row of `type` with `cols` weights (0 when unsupported). */
+size_t tc_row_bytes(int type, uint32_t cols);
+
+/* MoE expert FFN over Q4_K experts (qwen35moe routed experts, reference
+ * src/cpp/core/ModelMoE.cpp:660-672 and :990-1002): for every token s and
+ * rank r < top_k, e = ids[s][r]: h = silu(Wg[e] x_s) * (Wu[e] x_s),
+ * out[s] += wts[s][r] * (Wd[e] h), summed over r in rank order.
+ * wg, wu: [n_experts][ff][hidden]; wd: [n_experts][hidden][ff] (Q4_K blocks).
+ * ids int32 [seq_len][top_k], wts fp32 [seq_len][top_k], x [seq_len][hidden],
+ * out [seq_len][hidden]; all device pointers. */
+int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t seq_len, uint32_t top_k,
+               const void *wg, const void *wu, const void *wd, uint32_t n_experts, uint32_t hidden,
+               uint32_t ff, float *out, void *stream);
+
+/* Message for the calling thread's last failed call ("" if none). */
+const char *tc_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

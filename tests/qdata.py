@@ -1,0 +1,50 @@
+"""Seeded synthetic weight/activation generators shared by the tests."""
+import numpy as np
+
+Q8_0, Q4_K, Q6_K, IQ3_XXS = 8, 12, 14, 18
+TYPE_SIZE = {Q8_0: 34, Q4_K: 144, Q6_K: 210, IQ3_XXS: 98}
+BLOCK_SIZE = {Q8_0: 32, Q4_K: 256, Q6_K: 256, IQ3_XXS: 256}
+ALL = (Q8_0, Q4_K, Q6_K, IQ3_XXS)
+NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ3_XXS: "IQ3_XXS"}
+
+
+def row_bytes(qt, cols):
+    return cols // BLOCK_SIZE[qt] * TYPE_SIZE[qt]
+
+
+def _fp16_bytes(v):
+    return np.ascontiguousarray(v.astype(np.float16)).view(np.uint8).reshape(-1, 2)
+
+
+def random_blocks(qt, rng, rows, cols):
+    """Random block bytes (every bit pattern path) with realistic fp16 scales
+    (normal and, for a share of blocks, subnormal). Q8_0 weights stay within
+    [-127, 127] as every Q8_0 encoder emits."""
+    nblk = rows * cols // BLOCK_SIZE[qt]
+    b = rng.integers(0, 256, size=(nblk, TYPE_SIZE[qt]), dtype=np.uint8)
+    mag = rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-16, -5, nblk)
+    if qt == Q4_K:
+        b[:, 0:2] = _fp16_bytes(mag)
+        b[:, 2:4] = _fp16_bytes(rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-12, -5, nblk))
+    elif qt == Q6_K:
+        b[:, 208:210] = _fp16_bytes(mag)
+    elif qt == IQ3_XXS:
+        b[:, 0:2] = _fp16_bytes(mag)
+    else:
+        b[:, 0:2] = _fp16_bytes(mag)
+        q = b[:, 2:].view(np.int8)
+        q[q == -128] = -127
+    return b.ravel()
+
+
+def gaussian(rng, shape, std=1.0):
+    return (rng.standard_normal(shape) * std).astype(np.float32)
+
+
+def close(got, ref, rtol=1e-3, atol=1e-4):
+    """The stated fp32 tolerance: |got - ref| <= atol + rtol * |ref|."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    return bool((err <= bound).all()), float((err / bound).max()) if err.size else 0.0

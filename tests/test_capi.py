@@ -1,0 +1,57 @@
+"""CPU tests of the C-ABI boundary: the built library loads and exports every
+function that include/*.h declares (no compute call without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(ROOT, "include", fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(tc_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for must in ("tc_gemv", "tc_gemm", "tc_gemv_dual", "tc_moe_ffn", "tc_quantize_act", "tc_block_isums"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    import tc_hip
+    lib = tc_hip.load_library()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(declared_functions()) == set(tc_hip.SIGNATURES)
+
+
+def test_no_device_is_reported_cleanly():
+    import tc_hip
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    lib = tc_hip.load_library()
+    assert lib.tc_available() == 0
+    rc = lib.tc_gemv(12, None, None, None, 1, 1, 256, None)
+    assert rc == tc_hip.TC_E_UNSUPPORTED
+    assert b"gfx950" in lib.tc_last_error()
+
+
+def test_row_bytes():
+    import tc_hip
+    lib = tc_hip.load_library()
+    assert lib.tc_row_bytes(12, 3584) == 14 * 144
+    assert lib.tc_row_bytes(8, 4096) == 128 * 34
+    assert lib.tc_row_bytes(14, 18944) == 74 * 210
+    assert lib.tc_row_bytes(18, 3584) == 14 * 98
+    assert lib.tc_row_bytes(13, 256) == 0

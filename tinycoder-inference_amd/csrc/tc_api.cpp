@@ -1,0 +1,350 @@
+// tc_api.cpp -- host side of libtc_hip.so: device query, grow-only scratch,
+// argument checks and the extern "C" entry points declared in
+// include/tc_qmatmul.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "tc_kernels.hpp"
+#include "tc_qmatmul.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(e == hipErrorInvalidValue ? TC_E_UNSUPPORTED : TC_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
+struct Device {
+    bool ok = false;
+    int id = 0, num_cu = 0;
+    void *act = nullptr;  // quantized activations
+    size_t act_bytes = 0;
+    void *aux = nullptr;  // kernel intermediates (MoE hidden, GEMM partials)
+    size_t aux_bytes = 0;
+};
+
+std::mutex g_mu;
+std::vector<Device> g_dev;
+
+// Device attributes are read once per device (the reference's ctx(),
+// GemmDispatch.cu:208-234).
+Device *device() {
+    int id = 0;
+    if (hipGetDevice(&id) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_dev.size() <= size_t(id)) g_dev.resize(id + 1);
+    Device &d = g_dev[id];
+    if (!d.ok) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, id) != hipSuccess) return nullptr;
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return nullptr;
+        d.id = id;
+        d.num_cu = prop.multiProcessorCount;
+        d.ok = true;
+    }
+    return &d;
+}
+
+bool ensure(void *&p, size_t &cap, size_t need) {
+    if (cap >= need) return true;
+    if (p != nullptr) {
+        // The buffer may still be read by work queued earlier on any stream.
+        (void)hipDeviceSynchronize();
+        (void)hipFree(p);
+    }
+    p = nullptr;
+    cap = 0;
+    if (hipMalloc(&p, need) != hipSuccess) {
+        p = nullptr;
+        return false;
+    }
+    cap = need;
+    return true;
+}
+
+bool type_ok(int t) { return t == TC_Q8_0 || t == TC_Q4_K || t == TC_Q6_K || t == TC_IQ3_XXS; }
+
+bool g_q8_gemm_enabled = true;
+
+tc::ActView act_view(void *buf, const tc::ActLayout &L, size_t tok, int type, uint32_t cols) {
+    const uint32_t blk = type == TC_Q8_0 ? 32u : 256u;
+    char *b = static_cast<char *>(buf);
+    tc::ActView v;
+    v.qs = reinterpret_cast<const int8_t *>(b + L.qs_off) + tok * cols;
+    v.d = reinterpret_cast<const float *>(b + L.d_off) + tok * (cols / blk);
+    v.bsums = reinterpret_cast<const int16_t *>(b + L.bs_off) + tok * (cols / 16);
+    return v;
+}
+
+// Activations wider than 16 Q8_K blocks (per launch) are quantized once by a
+// small kernel into the device scratch instead of in every workgroup of the
+// mat-vec (whose prologue would repeat the work hundreds of times). The
+// tiled kernels (Q4_K, Q8_0) take that path; the others quantize in-kernel.
+bool prequantize_wide(int type, uint32_t S, uint32_t cols) {
+    return (type == TC_Q4_K || type == TC_Q8_0) && size_t(S) * cols > 16 * 256;
+}
+
+int launch_jobs(Device *dev, int type, uint32_t S, tc::GemvJob *jobs, uint32_t n, hipStream_t st) {
+    size_t need = 0;
+    for (uint32_t i = 0; i < n; ++i)
+        if (jobs[i].x && prequantize_wide(type, S, jobs[i].cols)) need += tc::act_layout(type, S, jobs[i].cols).bytes;
+    if (need) {
+        if (!ensure(dev->act, dev->act_bytes, need)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", need);
+        size_t off = 0;
+        for (uint32_t i = 0; i < n; ++i) {
+            if (!(jobs[i].x && prequantize_wide(type, S, jobs[i].cols))) continue;
+            const tc::ActLayout L = tc::act_layout(type, S, jobs[i].cols);
+            void *buf = static_cast<char *>(dev->act) + off;
+            hipError_t e = tc::launch_quant_act(type, jobs[i].x, S, jobs[i].cols, L, buf, st);
+            if (e != hipSuccess) return hip_fail(e, "activation quantizer");
+            jobs[i].act = act_view(buf, L, 0, type, jobs[i].cols);
+            jobs[i].x = nullptr;
+            off += L.bytes;
+        }
+    }
+    const hipError_t e = tc::launch_gemv_jobs(type, S, jobs, n, dev->num_cu, st);
+    if (e != hipSuccess) return hip_fail(e, "decode mat-vec");
+    return TC_OK;
+}
+
+// Run one decode job over token chunks that fit the kernel's LDS budget.
+// `x` (fp32) is quantized inside the kernel; with x == null the activations
+// come from the pre-quantized buffer `act`.
+int run_gemv(Device *dev, int type, const void *w, const void *w2, const float *x, const void *act, float *out,
+             float *out2, int epi, int32_t *dbg, uint32_t S, uint32_t rows, uint32_t cols, hipStream_t st) {
+    const uint32_t smax = tc::gemv_max_tokens(type, cols);
+    if (smax == 0) return fail(TC_E_UNSUPPORTED, "cols=%u too wide for the decode kernel", cols);
+    const tc::ActLayout L = tc::act_layout(type, S, cols);
+    const uint32_t nbr = type == TC_Q8_0 ? cols / 32 : cols / 256;
+    const size_t per = type == TC_Q4_K ? 8 : 1;
+    for (uint32_t s0 = 0; s0 < S; s0 += smax) {
+        const uint32_t n = std::min(smax, S - s0);
+        tc::GemvJob job;
+        job.W = static_cast<const uint8_t *>(w);
+        job.W2 = static_cast<const uint8_t *>(w2);
+        if (x)
+            job.x = x + size_t(s0) * cols;
+        else
+            job.act = act_view(const_cast<void *>(act), L, s0, type, cols);
+        job.out = out + size_t(s0) * rows;
+        job.out2 = out2 ? out2 + size_t(s0) * rows : nullptr;
+        job.epi = epi;
+        job.rows = rows;
+        job.cols = cols;
+        job.out_ld = rows;
+        job.dbg = dbg ? dbg + size_t(s0) * rows * nbr * per : nullptr;
+        const int rc = launch_jobs(dev, type, n, &job, 1, st);
+        if (rc) return rc;
+    }
+    return TC_OK;
+}
+
+int check_common(int type, const void *w, const void *x, const void *out, uint32_t S, uint32_t rows,
+                 uint32_t cols) {
+    if (!type_ok(type)) return fail(TC_E_UNSUPPORTED, "unsupported type %d", type);
+    if (!w || !x || !out) return fail(TC_E_ARG, "null pointer");
+    if (S == 0 || rows == 0 || cols == 0) return fail(TC_E_UNSUPPORTED, "empty shape");
+    if (cols % 256 != 0) return fail(TC_E_UNSUPPORTED, "cols=%u is not a multiple of 256", cols);
+    if ((reinterpret_cast<uintptr_t>(w) & 15) || (reinterpret_cast<uintptr_t>(x) & 15))
+        return fail(TC_E_UNSUPPORTED, "weights and activations must be 16-byte aligned");
+    return TC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tc_available(void) {
+    static const int avail = [] {
+        const char *e = std::getenv("TINYCODER_INT8_GEMM");
+        if (e != nullptr && e[0] == '0') return 0;
+        return device() != nullptr ? 1 : 0;
+    }();
+    return avail;
+}
+
+size_t tc_row_bytes(int type, uint32_t cols) {
+    if (!type_ok(type)) return 0;
+    const uint32_t be = tc::block_elems(type);
+    if (cols % be) return 0;
+    return size_t(cols / be) * tc::block_bytes(type);
+}
+
+int tc_gemv(int type, const void *w, const float *x, float *out, uint32_t seq_len, uint32_t rows, uint32_t cols,
+            void *stream) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    int rc = check_common(type, w, x, out, seq_len, rows, cols);
+    if (rc) return rc;
+    if (seq_len > 8) return fail(TC_E_UNSUPPORTED, "seq_len=%u > 8 (use tc_gemm)", seq_len);
+    return run_gemv(dev, type, w, nullptr, x, nullptr, out, nullptr, 0, nullptr, seq_len, rows, cols,
+                    static_cast<hipStream_t>(stream));
+}
+
+int tc_gemv_multi(int type, uint32_t n, const void *const *w, const float *const *x, float *const *out,
+                  const uint32_t *rows, const uint32_t *cols, uint32_t seq_len, void *stream) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!w || !x || !out || !rows || !cols) return fail(TC_E_ARG, "null pointer");
+    if (n == 0 || n > 8) return fail(TC_E_UNSUPPORTED, "n=%u matrices (1..8)", n);
+    if (seq_len > 8) return fail(TC_E_UNSUPPORTED, "seq_len=%u > 8", seq_len);
+    tc::GemvJob jobs[8];
+    for (uint32_t i = 0; i < n; ++i) {
+        int rc = check_common(type, w[i], x[i], out[i], seq_len, rows[i], cols[i]);
+        if (rc) return rc;
+        if (seq_len > tc::gemv_max_tokens(type, cols[i]))
+            return fail(TC_E_UNSUPPORTED, "seq_len=%u too large for cols=%u in one launch", seq_len, cols[i]);
+        jobs[i].W = static_cast<const uint8_t *>(w[i]);
+        jobs[i].x = x[i];
+        jobs[i].out = out[i];
+        jobs[i].rows = rows[i];
+        jobs[i].cols = cols[i];
+        jobs[i].out_ld = rows[i];
+    }
+    return launch_jobs(dev, type, seq_len, jobs, n, static_cast<hipStream_t>(stream));
+}
+
+size_t tc_act_bytes(int type, uint32_t seq_len, uint32_t cols) {
+    if (!type_ok(type) || cols % 256) return 0;
+    return tc::act_layout(type, seq_len, cols).bytes;
+}
+
+int tc_act_quantize(int type, const float *x, uint32_t seq_len, uint32_t cols, void *act, void *stream) {
+    if (!device()) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    int rc = check_common(type, act, x, act, seq_len, 1, cols);
+    if (rc) return rc;
+    if (reinterpret_cast<uintptr_t>(act) & 255) return fail(TC_E_ARG, "act must be 256-byte aligned");
+    const tc::ActLayout L = tc::act_layout(type, seq_len, cols);
+    hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, act, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "activation quantizer");
+    return TC_OK;
+}
+
+int tc_gemv_q8(int type, const void *w, const void *act, float *out, uint32_t seq_len, uint32_t rows, uint32_t cols,
+               void *stream) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    int rc = check_common(type, w, act, out, seq_len, rows, cols);
+    if (rc) return rc;
+    if (seq_len > 8) return fail(TC_E_UNSUPPORTED, "seq_len=%u > 8 (use tc_gemm)", seq_len);
+    if (reinterpret_cast<uintptr_t>(act) & 255) return fail(TC_E_ARG, "act must be 256-byte aligned");
+    return run_gemv(dev, type, w, nullptr, nullptr, act, out, nullptr, 0, nullptr, seq_len, rows, cols,
+                    static_cast<hipStream_t>(stream));
+}
+
+int tc_gemv_reserve(uint32_t cols, uint32_t seq_len) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    size_t need = 0;
+    for (int t : {TC_Q8_0, TC_Q4_K}) need = std::max(need, tc::act_layout(t, seq_len, cols).bytes);
+    if (!ensure(dev->act, dev->act_bytes, need)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", need);
+    return TC_OK;
+}
+
+int tc_gemv_dual(int type, const void *wg, const void *wu, const float *x, float *gout, float *uout, uint32_t rows,
+                 uint32_t cols, void *stream) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    int rc = check_common(type, wg, x, gout, 1, rows, cols);
+    if (rc) return rc;
+    if (!wu || !uout) return fail(TC_E_ARG, "null pointer");
+    if ((reinterpret_cast<uintptr_t>(wu) & 15)) return fail(TC_E_UNSUPPORTED, "weights must be 16-byte aligned");
+    return run_gemv(dev, type, wg, wu, x, nullptr, gout, uout, 1, nullptr, 1, rows, cols,
+                    static_cast<hipStream_t>(stream));
+}
+
+int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_len, uint32_t rows, uint32_t cols,
+            uint32_t blocks_per_row, void *stream) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    int rc = check_common(type, w, x, out, seq_len, rows, cols);
+    if (rc) return rc;
+    if (blocks_per_row != cols / uint32_t(tc::block_elems(type)))
+        return fail(TC_E_ARG, "blocks_per_row=%u does not match cols=%u", blocks_per_row, cols);
+    if (type == TC_Q8_0 && !g_q8_gemm_enabled) return fail(TC_E_UNSUPPORTED, "Q8_0 GEMM disabled");
+    (void)stream;
+    return fail(TC_E_UNSUPPORTED, "int8 MFMA GEMM not built yet");
+}
+
+int tc_gemm_preferred(uint32_t type, uint32_t, uint32_t) { return type_ok(int(type)) ? 1 : 0; }
+
+void tc_gemm_set_q8_enabled(int enabled) { g_q8_gemm_enabled = enabled != 0; }
+
+int tc_quantize_act(int type, const float *x, uint32_t seq_len, uint32_t cols, int8_t *qs, float *d, int16_t *bsums,
+                    void *stream) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!type_ok(type)) return fail(TC_E_UNSUPPORTED, "unsupported type %d", type);
+    if (!x || !qs || !d || (type != TC_Q8_0 && !bsums)) return fail(TC_E_ARG, "null pointer");
+    const uint32_t blk = type == TC_Q8_0 ? 32 : 256;
+    if (seq_len == 0 || cols == 0 || cols % blk) return fail(TC_E_UNSUPPORTED, "cols=%u", cols);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const tc::ActLayout L = tc::act_layout(type, seq_len, cols);
+    if (!ensure(dev->act, dev->act_bytes, L.bytes)) return fail(TC_E_LAUNCH, "hipMalloc failed");
+    hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, dev->act, st);
+    if (e != hipSuccess) return hip_fail(e, "activation quantizer");
+    const char *b = static_cast<const char *>(dev->act);
+    e = hipMemcpyAsync(qs, b + L.qs_off, size_t(seq_len) * cols, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d, b + L.d_off, size_t(seq_len) * (cols / blk) * 4, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess && type != TC_Q8_0)
+        e = hipMemcpyAsync(bsums, b + L.bs_off, size_t(seq_len) * (cols / 16) * 2, hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return hip_fail(e, "copy");
+    return TC_OK;
+}
+
+int tc_block_isums(int type, const void *w, const float *x, int32_t *isums, uint32_t seq_len, uint32_t rows,
+                   uint32_t cols, void *stream) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    int rc = check_common(type, w, x, isums, seq_len, rows, cols);
+    if (rc) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // The decode kernel writes the integer sums as a side output; its fp32
+    // results land in a scratch row buffer.
+    const size_t need = size_t(seq_len) * rows * 4;
+    if (!ensure(dev->aux, dev->aux_bytes, need)) return fail(TC_E_LAUNCH, "hipMalloc failed");
+    return run_gemv(dev, type, w, nullptr, x, nullptr, static_cast<float *>(dev->aux), nullptr, 0, isums, seq_len,
+                    rows, cols, st);
+}
+
+int tc_encode(int type, const float *x, void *out, uint32_t rows, uint32_t cols, void *stream) {
+    if (!device()) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!type_ok(type)) return fail(TC_E_UNSUPPORTED, "unsupported type %d", type);
+    if (!x || !out) return fail(TC_E_ARG, "null pointer");
+    if (cols % 256) return fail(TC_E_UNSUPPORTED, "cols=%u is not a multiple of 256", cols);
+    const uint64_t units = uint64_t(rows) * (cols / 256);
+    if (units >= (1ull << 32)) return fail(TC_E_UNSUPPORTED, "too many blocks");
+    hipError_t e = tc::launch_encode(type, x, out, uint32_t(units), static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "encoder");
+    return TC_OK;
+}
+
+int tc_moe_ffn(const float *, const int32_t *, const float *, uint32_t, uint32_t, const void *, const void *,
+               const void *, uint32_t, uint32_t, uint32_t, float *, void *) {
+    return fail(TC_E_UNSUPPORTED, "MoE path not built yet");
+}
+
+const char *tc_last_error(void) { return g_err.c_str(); }
+
+}  // extern "C"

@@ -1,0 +1,1160 @@
+// tc_gemv.hip -- decode-time quantized mat-vec for gfx950 (batch 1..8).
+//
+// One launch runs a list of jobs (matrices); each job has its own weights,
+// input vector(s) and output, so q/k/v (one shared input), a gate/up pair
+// (SwiGLU epilogue) or any set of independent mat-vecs go out in one launch.
+//
+// Weights are read as raw GGUF blocks straight from HBM. A 512-thread
+// workgroup (8 waves, one per CU) owns a contiguous range of rows of one
+// job, i.e. a contiguous byte range of the weight stream. Every group of 4
+// lanes decodes one 256-weight unit (one K-quant / IQ3_XXS block, or 8 Q8_0
+// blocks): each lane takes 64 weights, unpacks them in registers and forms
+// int8 dot products (v_dot4_i32_i8) against activation bytes in LDS. The 4
+// lanes combine their integer sums with DPP quad permutes, apply the block's
+// float scales once and park the unit value in LDS; at the end of a row chunk
+// one thread per (token, row) sums its row's units in block order.
+//
+// Each lane keeps D passes of weight loads in flight in a register ring. The
+// first D passes are issued before the prologue quantizes the input vector
+// into LDS (the reference CPU rule, bit-exact), so that work hides under the
+// first HBM round trip.
+#include <type_traits>
+
+#include "tc_actquant.hpp"
+#include "tc_kernels.hpp"
+
+namespace tc {
+
+namespace {
+
+__constant__ uint32_t c_grid[256] = {
+#include "iq3xxs_grid.inc"
+};
+
+constexpr int NT = 512;
+constexpr int kUnitsPerPass = NT / 4;
+constexpr uint32_t kLdsBudget = 64 * 1024;
+constexpr uint32_t kPartBudget = 24 * 1024;
+constexpr int kMaxJobs = 8;
+
+struct JobDev {
+    const uint8_t *W, *W2;
+    const float *x;
+    ActView act;
+    float *out, *out2;
+    int32_t *dbg;
+    uint32_t rows, cols, nu, out_ld;
+    uint32_t rows_per_wg, chunk_rows, wg_begin;
+    int epi;
+    DivMod nu_div;
+};
+
+struct LaunchArgs {
+    JobDev jobs[kMaxJobs];
+    uint32_t njobs;
+    uint32_t off_d, off_b, off_g, off_p;
+};
+
+__host__ __device__ constexpr bool uses_bsums(int type) { return type == kQ4_K || type == kQ6_K; }
+// Passes of weight loads each lane keeps in flight (register ring), sized so
+// that the kernel stays within the 256 VGPRs of an 8-wave-per-CU launch.
+__host__ __device__ constexpr int ring_depth(int type, int S) {
+    return type == kQ4_K ? (S <= 2 ? 6 : S <= 4 ? 4 : 3)
+           : type == kQ8_0 ? (S <= 2 ? 4 : 3)
+           : type == kQ6_K ? (S <= 2 ? 4 : 3)
+                           : (S <= 2 ? 6 : 4);
+}
+
+// ---- per-type raw loads (one lane = 64 weights of one unit) -----------------
+
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+__device__ __forceinline__ uint32_t ld16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+__device__ __forceinline__ uint4 ld128(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ uint32_t align2(uint32_t hi, uint32_t lo, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+
+template <int TYPE>
+struct Raw;
+
+// Q4_K (144 B, 16-B aligned): header (d, dmin, 12 scale bytes) and the lane's
+// 32 quant bytes (low nibbles = sub-block 2q, high = 2q+1).
+template <>
+struct Raw<kQ4_K> {
+    uint4 h, a, b;
+    __device__ __forceinline__ void load(const uint8_t *u, uint32_t q) {
+        h = ld128(u);
+        a = ld128(u + 16 + 32 * q);
+        b = ld128(u + 32 + 32 * q);
+    }
+};
+
+// Q8_0 unit = 8 blocks of 34 B; lane q reads blocks 2q, 2q+1 (68 B at a
+// 4-byte-aligned offset).
+template <>
+struct Raw<kQ8_0> {
+    uint4 a, b, c, d;
+    uint32_t e;
+    __device__ __forceinline__ void load(const uint8_t *u, uint32_t q) {
+        const uint8_t *p = u + 68 * q;
+        a = ld128(p);
+        b = ld128(p + 16);
+        c = ld128(p + 32);
+        d = ld128(p + 48);
+        e = ld32(p + 64);
+    }
+};
+
+// Q6_K (210 B, 2-B aligned): lane q takes sub-blocks sA = (q&1) + 4(q>>1) and
+// sA + 2: 32 ql bytes, 32 qh bytes, 4 scale bytes and d. The 32-byte runs are
+// read as 9 aligned dwords and realigned in registers; no byte outside the
+// block is read.
+template <>
+struct Raw<kQ6_K> {
+    uint4 l0, l1, h0, h1;
+    uint32_t l2, h2, sc01, sc45, dh, sh;
+    __device__ __forceinline__ void load(const uint8_t *u, uint32_t q) {
+        const uintptr_t ua = reinterpret_cast<uintptr_t>(u);
+        sh = uint32_t(ua & 3);
+        const uint8_t *ql = reinterpret_cast<const uint8_t *>((ua + 32 * (q & 1) + 64 * (q >> 1)) & ~uintptr_t(3));
+        const uint8_t *qh = reinterpret_cast<const uint8_t *>((ua + 128 + 32 * (q >> 1)) & ~uintptr_t(3));
+        l0 = ld128(ql);
+        l1 = ld128(ql + 16);
+        l2 = ld32(ql + 32);
+        h0 = ld128(qh);
+        h1 = ld128(qh + 16);
+        h2 = ld32(qh + 32);
+        const uint32_t sA = (q & 1) + 4 * (q >> 1);
+        sc01 = ld16(u + 192 + 2 * sA);
+        sc45 = ld16(u + 196 + 2 * sA);
+        dh = ld16(u + 208);
+    }
+};
+
+// IQ3_XXS (98 B, 2-B aligned): lane q takes 32-chunks 2q, 2q+1: 16 grid-index
+// bytes (5 aligned dwords, realigned) and 8 scale/sign bytes (16-bit loads so
+// that nothing past the block is touched).
+template <>
+struct Raw<kIQ3_XXS> {
+    uint4 g;
+    uint32_t g4, a0, a1, a2, a3, dh, sh;
+    __device__ __forceinline__ void load(const uint8_t *u, uint32_t q) {
+        const uintptr_t qa = reinterpret_cast<uintptr_t>(u) + 2 + 16 * q;
+        sh = uint32_t(qa & 3);
+        const uint8_t *qp = reinterpret_cast<const uint8_t *>(qa & ~uintptr_t(3));
+        g = ld128(qp);
+        g4 = ld32(qp + 16);
+        const uint8_t *ap = u + 66 + 8 * q;
+        a0 = ld16(ap);
+        a1 = ld16(ap + 2);
+        a2 = ld16(ap + 4);
+        a3 = ld16(ap + 6);
+        dh = ld16(u);
+    }
+};
+
+// ---- per-type unit dot ------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, uint32_t k) { return (w >> (8 * k)) & 0xFFu; }
+
+// Activation context of one job in LDS.
+struct XCtx {
+    const int8_t *sx;      // qs [S][cols]
+    const float *sd;       // d [S][cols/blk]
+    const int16_t *sb;     // bsums [S][cols/16]
+    const uint32_t *grid;  // IQ3_XXS codebook
+    uint32_t cols;
+    size_t dbg_tok;        // token stride of the per-block integer-sum output
+};
+
+__device__ __forceinline__ void load_x16(const int8_t *p, int *xs) {
+    const uint4 *xv = reinterpret_cast<const uint4 *>(p);
+    const uint4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+    xs[0] = int(x0.x), xs[1] = int(x0.y), xs[2] = int(x0.z), xs[3] = int(x0.w);
+    xs[4] = int(x1.x), xs[5] = int(x1.y), xs[6] = int(x1.z), xs[7] = int(x1.w);
+    xs[8] = int(x2.x), xs[9] = int(x2.y), xs[10] = int(x2.z), xs[11] = int(x2.w);
+    xs[12] = int(x3.x), xs[13] = int(x3.y), xs[14] = int(x3.z), xs[15] = int(x3.w);
+}
+
+template <int TYPE, int S>
+struct Dot;
+
+// Q4_K: sub-block sums s0 (2q), s1 (2q+1) exact in int32; the quad sums
+// sum_i sc_i*s_i and sum_i m_i*(bsum pair) over the block, then
+// d8 * (d*main - dmin*min) (reference SIMDMatMulVecAVX2.cpp:3678-3711).
+template <int S>
+struct Dot<kQ4_K, S> {
+    __device__ __forceinline__ static void run(const Raw<kQ4_K> &r, uint32_t q, uint32_t b, const XCtx &c,
+                                               float *val, int32_t *dbg) {
+        const uint32_t jj = 2 * (q & 1);
+        const bool lo = q < 2;
+        uint32_t sc[2], mn[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t A = byte_of(r.h.y, jj + t), B = byte_of(r.h.z, jj + t), C = byte_of(r.h.w, jj + t);
+            sc[t] = lo ? (A & 63u) : ((C & 0xFu) | ((A >> 6) << 4));
+            mn[t] = lo ? (B & 63u) : ((C >> 4) | ((B >> 6) << 4));
+        }
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        const uint32_t nb = c.cols / 256;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            int xs[16];
+            load_x16(c.sx + size_t(s) * c.cols + b * 256 + 64 * q, xs);
+            int s0 = 0, s1 = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                s0 = sdot4(int(w[k] & 0x0F0F0F0Fu), xs[k], s0);
+                s1 = sdot4(int((w[k] >> 4) & 0x0F0F0F0Fu), xs[8 + k], s1);
+            }
+            const uint2 bs = *reinterpret_cast<const uint2 *>(c.sb + (size_t(s) * (c.cols / 16) + b * 16 + 4 * q));
+            const int bp0 = int(int16_t(bs.x)) + int(int16_t(bs.x >> 16));
+            const int bp1 = int(int16_t(bs.y)) + int(int16_t(bs.y >> 16));
+            int mainI = int(sc[0]) * s0 + int(sc[1]) * s1;
+            int minI = int(mn[0]) * bp0 + int(mn[1]) * bp1;
+            if (dbg) {
+                dbg[s * c.dbg_tok + 2 * q] = s0;
+                dbg[s * c.dbg_tok + 2 * q + 1] = s1;
+            }
+            mainI = quad_sum(mainI);
+            minI = quad_sum(minI);
+            const float d8 = c.sd[size_t(s) * nb + b];
+            val[s] = d8 * (d * float(mainI) - dmin * float(minI));
+        }
+    }
+};
+
+// Q8_0: two 34-byte blocks per lane; value = sum_blk (d_w*d8) * isum
+// (reference SIMDMatMulVecAVX2.cpp:4339-4366).
+template <int S>
+struct Dot<kQ8_0, S> {
+    __device__ __forceinline__ static void run(const Raw<kQ8_0> &r, uint32_t q, uint32_t b, const XCtx &c,
+                                               float *val, int32_t *dbg) {
+        const uint32_t w[17] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c.x,
+                                r.c.y, r.c.z, r.c.w, r.d.x, r.d.y, r.d.z, r.d.w, r.e};
+        uint32_t q0[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q0[k] = align2(w[k + 1], w[k], 2);
+        const float dw0 = h2f(w[0] & 0xFFFFu), dw1 = h2f(w[8] >> 16);
+        const uint32_t nb32 = c.cols / 32;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            int xs[16];
+            load_x16(c.sx + size_t(s) * c.cols + b * 256 + 64 * q, xs);
+            int s0 = 0, s1 = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                s0 = sdot4(int(q0[k]), xs[k], s0);
+                s1 = sdot4(int(w[9 + k]), xs[8 + k], s1);
+            }
+            if (dbg) {
+                dbg[s * c.dbg_tok + 2 * q] = s0;
+                dbg[s * c.dbg_tok + 2 * q + 1] = s1;
+            }
+            const float *d8 = c.sd + size_t(s) * nb32 + b * 8 + 2 * q;
+            const float v = (dw0 * d8[0]) * float(s0) + (dw1 * d8[1]) * float(s1);
+            val[s] = quad_sum(v);
+        }
+    }
+};
+
+// Q6_K: isum = sum_g sc_g * (sum_16 raw*x - 32*bsum_g), exact; value =
+// (d*d8) * isum (reference SIMDMatMulVecAVX2.cpp:4636-4667 folds the -32 the
+// same way).
+template <int S>
+struct Dot<kQ6_K, S> {
+    __device__ __forceinline__ static void run(const Raw<kQ6_K> &r, uint32_t q, uint32_t b, const XCtx &c,
+                                               float *val, int32_t *dbg) {
+        const uint32_t lr[9] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w, r.l1.x, r.l1.y, r.l1.z, r.l1.w, r.l2};
+        const uint32_t hr[9] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w, r.h2};
+        const uint32_t shA = 2 * (q & 1), shB = shA + 4;
+        uint32_t wA[8], wB[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t L = align2(lr[k + 1], lr[k], r.sh);
+            const uint32_t H = align2(hr[k + 1], hr[k], r.sh);
+            wA[k] = (L & 0x0F0F0F0Fu) | (((H >> shA) & 0x03030303u) << 4);
+            wB[k] = ((L >> 4) & 0x0F0F0F0Fu) | (((H >> shB) & 0x03030303u) << 4);
+        }
+        const int scA0 = int(int8_t(r.sc01)), scA1 = int(int8_t(r.sc01 >> 8));
+        const int scB0 = int(int8_t(r.sc45)), scB1 = int(int8_t(r.sc45 >> 8));
+        const float dw = h2f(r.dh);
+        const uint32_t sA = (q & 1) + 4 * (q >> 1);
+        const uint32_t nb = c.cols / 256;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int8_t *xb = c.sx + size_t(s) * c.cols + b * 256;
+            const uint4 *xa = reinterpret_cast<const uint4 *>(xb + 32 * sA);
+            const uint4 *xc = reinterpret_cast<const uint4 *>(xb + 32 * sA + 64);
+            const uint4 a0 = xa[0], a1 = xa[1], c0 = xc[0], c1 = xc[1];
+            const int xA[8] = {int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
+            const int xC[8] = {int(c0.x), int(c0.y), int(c0.z), int(c0.w), int(c1.x), int(c1.y), int(c1.z), int(c1.w)};
+            int sA0 = 0, sA1 = 0, sB0 = 0, sB1 = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sA0 = sdot4(int(wA[k]), xA[k], sA0);
+                sA1 = sdot4(int(wA[4 + k]), xA[4 + k], sA1);
+                sB0 = sdot4(int(wB[k]), xC[k], sB0);
+                sB1 = sdot4(int(wB[4 + k]), xC[4 + k], sB1);
+            }
+            const int16_t *bs = c.sb + size_t(s) * (c.cols / 16) + b * 16 + 2 * sA;
+            const uint32_t bA = *reinterpret_cast<const uint32_t *>(bs);
+            const uint32_t bB = *reinterpret_cast<const uint32_t *>(bs + 4);
+            int isum = scA0 * (sA0 - 32 * int(int16_t(bA))) + scA1 * (sA1 - 32 * int(int16_t(bA >> 16))) +
+                       scB0 * (sB0 - 32 * int(int16_t(bB))) + scB1 * (sB1 - 32 * int(int16_t(bB >> 16)));
+            isum = quad_sum(isum);
+            if (dbg && q == 0) dbg[s * c.dbg_tok] = isum;
+            const float d8 = c.sd[size_t(s) * nb + b];
+            val[s] = (dw * d8) * float(isum);
+        }
+    }
+};
+
+// IQ3_XXS: signed grid bytes (codebook in LDS, sign parity rule), isum =
+// sum_ib32 (2ls+1) * sum_32 w*x, value = (d*d8) * isum; the row is scaled by
+// 0.25 at the end (reference include/GGMLDequantize.hpp:2064-2097, :2148).
+template <int S>
+struct Dot<kIQ3_XXS, S> {
+    __device__ __forceinline__ static void run(const Raw<kIQ3_XXS> &r, uint32_t q, uint32_t b, const XCtx &c,
+                                               float *val, int32_t *dbg) {
+        const uint32_t gi[4] = {align2(r.g.y, r.g.x, r.sh), align2(r.g.z, r.g.y, r.sh), align2(r.g.w, r.g.z, r.sh),
+                                align2(r.g4, r.g.w, r.sh)};
+        const uint32_t aux[2] = {r.a0 | (r.a1 << 16), r.a2 | (r.a3 << 16)};
+        uint32_t wv[16];
+        int mult[2];
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+            mult[ch] = 2 * int(aux[ch] >> 28) + 1;
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t idx7 = (aux[ch] >> (7 * l)) & 127u;
+                const uint32_t s8 = idx7 | ((__builtin_popcount(idx7) & 1u) << 7);
+                const uint32_t g1 = c.grid[byte_of(gi[2 * ch + (l >> 1)], 2 * (l & 1))];
+                const uint32_t g2 = c.grid[byte_of(gi[2 * ch + (l >> 1)], 2 * (l & 1) + 1)];
+                const uint32_t m1 = spread_sign4(s8 & 15u), m2 = spread_sign4(s8 >> 4);
+                wv[8 * ch + 2 * l] = (g1 ^ m1) + (m1 & 0x01010101u);
+                wv[8 * ch + 2 * l + 1] = (g2 ^ m2) + (m2 & 0x01010101u);
+            }
+        }
+        const float dw = h2f(r.dh);
+        const uint32_t nb = c.cols / 256;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            int xs[16];
+            load_x16(c.sx + size_t(s) * c.cols + b * 256 + 64 * q, xs);
+            int c0 = 0, c1 = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                c0 = sdot4(int(wv[k]), xs[k], c0);
+                c1 = sdot4(int(wv[8 + k]), xs[8 + k], c1);
+            }
+            int isum = c0 * mult[0] + c1 * mult[1];
+            isum = quad_sum(isum);
+            if (dbg && q == 0) dbg[s * c.dbg_tok] = isum;
+            const float d = dw * c.sd[size_t(s) * nb + b];
+            val[s] = d * float(isum);
+        }
+    }
+};
+
+// ---- prologue: the job's activations into LDS ------------------------------------
+
+template <int TYPE, int S>
+__device__ __forceinline__ void stage_activations(const JobDev &jb, int8_t *sx, float *sd, int16_t *sb) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr uint32_t NW = NT / 64;
+    constexpr uint32_t BATCH = 8;
+    const uint32_t ngroups = S * (jb.cols / 256);  // 256-element groups over all tokens
+    if (jb.x != nullptr) {
+        // Each wave quantizes groups wave, wave+NW, ...; the fp32 loads of up to
+        // BATCH groups are issued together, then quantized one by one.
+        for (uint32_t g0 = wave; g0 < ngroups; g0 += NW * BATCH) {
+            float4 v[BATCH];
+#pragma unroll
+            for (uint32_t i = 0; i < BATCH; ++i) {
+                const uint32_t g = g0 + i * NW;
+                if (g < ngroups) v[i] = reinterpret_cast<const float4 *>(jb.x + size_t(g) * 256)[lane];
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < BATCH; ++i) {
+                const uint32_t g = g0 + i * NW;
+                if (g < ngroups) {
+                    if constexpr (TYPE == kQ8_0)
+                        quant_q8_0_blocks_wave_v(v[i], sx + size_t(g) * 256, sd + size_t(g) * 8);
+                    else
+                        quant_q8k_block_wave_v(v[i], sx + size_t(g) * 256, sd + g, sb + size_t(g) * 16);
+                }
+            }
+        }
+    } else {
+        const uint32_t nq = S * jb.cols / 16;
+        const uint4 *qsrc = reinterpret_cast<const uint4 *>(jb.act.qs);
+        for (uint32_t i = threadIdx.x; i < nq; i += NT) reinterpret_cast<uint4 *>(sx)[i] = qsrc[i];
+        const uint32_t nd = TYPE == kQ8_0 ? S * jb.cols / 32 : S * jb.cols / 256;
+        for (uint32_t i = threadIdx.x; i < nd; i += NT) sd[i] = jb.act.d[i];
+        if constexpr (uses_bsums(TYPE)) {
+            const uint32_t nb = S * jb.cols / 32;  // int16 pairs
+            const uint32_t *bsrc = reinterpret_cast<const uint32_t *>(jb.act.bsums);
+            for (uint32_t i = threadIdx.x; i < nb; i += NT) reinterpret_cast<uint32_t *>(sb)[i] = bsrc[i];
+        }
+    }
+}
+
+template <int TYPE, int S>
+__global__ __launch_bounds__(NT) void k_gemv(LaunchArgs L) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    int8_t *sx = reinterpret_cast<int8_t *>(smem);
+    float *sd = reinterpret_cast<float *>(smem + L.off_d);
+    int16_t *sb = reinterpret_cast<int16_t *>(smem + L.off_b);
+    uint32_t *sg = reinterpret_cast<uint32_t *>(smem + L.off_g);
+    float *spart = reinterpret_cast<float *>(smem + L.off_p);
+    constexpr uint32_t UB = unit_bytes(TYPE);
+    constexpr int D = ring_depth(TYPE, S);
+
+    uint32_t j = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxJobs; ++k)
+        if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
+    // By value: the descriptor lands in SGPRs once. (A reference into the
+    // kernel-argument array with a runtime index makes the compiler re-load
+    // fields with vector loads whose s_waitcnt drains the weight ring.)
+    const JobDev jb = L.jobs[j];
+    const uint8_t *const W1 = jb.W;
+    const uint8_t *const W2p = jb.W2;
+
+    const uint32_t tid = threadIdx.x, q = tid & 3, ul = tid >> 2;
+    const uint32_t nu = jb.nu;
+    const uint32_t pairs = W2p != nullptr ? 2 : 1;
+    const uint32_t row_begin = (blockIdx.x - jb.wg_begin) * jb.rows_per_wg;
+    const uint32_t row_end = min(jb.rows, row_begin + jb.rows_per_wg);
+    const size_t nbr = TYPE == kQ8_0 ? jb.cols / 32 : jb.cols / 256;
+    const size_t per = TYPE == kQ4_K ? 8 : 1;
+
+    XCtx c;
+    c.sx = sx;
+    c.sd = sd;
+    c.sb = sb;
+    c.grid = sg;
+    c.cols = jb.cols;
+    c.dbg_tok = size_t(jb.rows) * nbr * per;
+
+    bool staged = false;
+    for (uint32_t r0 = row_begin; r0 < row_end; r0 += jb.chunk_rows) {
+        const uint32_t nr = min(jb.chunk_rows, row_end - r0);
+        const uint32_t per_mat = nr * nu;
+        const uint32_t nunits = per_mat * pairs;
+        const uint32_t npass = (nunits + kUnitsPerPass - 1) / kUnitsPerPass;
+        const uint8_t *const base1 = W1 + size_t(r0) * nu * UB;
+        const uint8_t *const base2 = pairs == 2 ? W2p + size_t(r0) * nu * UB - size_t(per_mat) * UB : base1;
+        auto unit_ptr = [&](uint32_t uu) -> const uint8_t * {
+            return (uu >= per_mat ? base2 : base1) + size_t(uu) * UB;
+        };
+
+        // Bursts: each iteration issues D passes of unit loads into fresh
+        // registers, then consumes them in issue order, so the compiler's
+        // in-order vmcnt waits let all D passes overlap. Loads are
+        // unconditional (lanes past the end re-read the last unit): no
+        // exec-masked branch sits between a load and its wait.
+        const uint32_t ulast = nunits - 1;
+        for (uint32_t p0 = 0; p0 < npass; p0 += D) {
+            Raw<TYPE> buf[D];
+#pragma unroll
+            for (int i = 0; i < D; ++i) buf[i].load(unit_ptr(min((p0 + i) * kUnitsPerPass + ul, ulast)), q);
+            if (!staged) {
+                stage_activations<TYPE, S>(jb, sx, sd, sb);
+                if constexpr (TYPE == kIQ3_XXS) {
+                    if (tid < 256) sg[tid] = c_grid[tid];
+                }
+                __syncthreads();
+                staged = true;
+            }
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                const uint32_t uu = (p0 + i) * kUnitsPerPass + ul;
+                if (uu < nunits) {
+                    const uint32_t m = uu >= per_mat ? 1u : 0u;
+                    const uint32_t um = uu - m * per_mat;
+                    const uint32_t rl = div_fast(um, jb.nu_div);
+                    const uint32_t b = um - rl * nu;
+                    int32_t *dbg = nullptr;
+                    if (jb.dbg)
+                        dbg = jb.dbg + (size_t(r0 + rl) * nbr + (TYPE == kQ8_0 ? size_t(b) * 8 : b)) * per;
+                    float val[S];
+                    Dot<TYPE, S>::run(buf[i], q, b, c, val, dbg);
+                    if (q == 0) {
+#pragma unroll
+                        for (int s = 0; s < S; ++s)
+                            spart[((size_t(m) * S + s) * jb.chunk_rows + rl) * nu + b] = val[s];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        for (uint32_t t = tid; t < S * nr; t += NT) {
+            const uint32_t s = t / nr, rl = t - s * nr;
+            const float *pg = spart + (size_t(s) * jb.chunk_rows + rl) * nu;
+            float g = 0.0f;
+            for (uint32_t b = 0; b < nu; ++b) g += pg[b];
+            if constexpr (TYPE == kIQ3_XXS) g = 0.25f * g;
+            if (pairs == 2) {
+                const float *pu = spart + ((size_t(S) + s) * jb.chunk_rows + rl) * nu;
+                float u = 0.0f;
+                for (uint32_t b = 0; b < nu; ++b) u += pu[b];
+                if constexpr (TYPE == kIQ3_XXS) u = 0.25f * u;
+                jb.out2[size_t(s) * jb.out_ld + r0 + rl] = u;
+                if (jb.epi == 1) g = g / (1.0f + expf(-g)) * u;
+            }
+            jb.out[size_t(s) * jb.out_ld + r0 + rl] = g;
+        }
+        __syncthreads();
+    }
+}
+
+// ============================================================================
+// Tiled variant for 16-byte-multiple units (Q4_K, Q8_0).
+//
+// Each wave streams "tiles" of 64 consecutive units: a tile is a contiguous
+// byte range, read with fully coalesced 16-byte-per-lane raw buffer loads (one
+// wave instruction = 1 KB contiguous; the buffer descriptor bounds every read
+// to the workgroup's rows, so tails need no clamping and read nothing) into a
+// register ring, copied to a per-wave LDS buffer, and every lane then decodes
+// one whole unit (lane-per-unit: scale unpack, float math and the row
+// bookkeeping happen once per unit, not once per lane-quad).
+//
+// Activations sit in LDS as padded 304-byte records per 256-element block:
+// [qs 256][bsums 16 x int16][d][pad] for Q8_K, [qs 256][d 8 x fp32][pad] for
+// the 32-wide Q8_0 rule. The 76-dword stride puts the b128 reads of 16 lanes
+// with consecutive blocks on distinct banks, and every field is reached
+// through an immediate offset.
+// ============================================================================
+
+#ifndef TC_TNT
+#define TC_TNT 256
+#endif
+#ifndef TC_TDEPTH
+#define TC_TDEPTH 2
+#endif
+#ifndef TC_TWPE
+#define TC_TWPE 3
+#endif
+constexpr int TNT = TC_TNT;                 // threads per workgroup
+constexpr int TNW = TNT / 64;
+constexpr int kTileUnits = 64;
+constexpr uint32_t XB = 304;                // LDS bytes per 256-element activation block
+constexpr uint32_t XB_BS = 256, XB_D = 288;  // bsums and d offsets inside a record
+
+__host__ __device__ constexpr int tile_dwordx4(int type) { return unit_bytes(type) * kTileUnits / 1024; }
+__host__ __device__ constexpr int tile_depth(int type, int S) { return type == kQ4_K && S <= 2 ? TC_TDEPTH : 2; }
+
+struct TJobDev {
+    const uint8_t *W, *W2;
+    const float *x;
+    ActView act;
+    float *out, *out2;
+    int32_t *dbg;
+    uint32_t rows, cols, nu, out_ld;
+    uint32_t rows_per_wg, wg_begin;
+    int epi;
+    DivMod nu_div;
+};
+
+struct TLaunchArgs {
+    TJobDev jobs[kMaxJobs];
+    uint32_t njobs;
+    uint32_t off_t, off_p;  // LDS: activation records at 0, wave tiles, partials
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 lds128(const unsigned char *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+// N 16-byte registers addressed only through compile-time indices. (Native
+// vectors: HIP's uint4 is a class whose copies become memcpy calls that keep
+// a local array in scratch memory.)
+template <int N>
+struct Regs {
+    u32x4 h;
+    Regs<N - 1> t;
+};
+template <>
+struct Regs<1> {
+    u32x4 h;
+};
+template <int I, int N>
+__device__ __forceinline__ u32x4 &reg(Regs<N> &r) {
+    if constexpr (I == 0)
+        return r.h;
+    else
+        return reg<I - 1, N - 1>(r.t);
+}
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// Raw buffer descriptor (gfx9 word 3: 32-bit raw data) over [p, p+bytes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), short(0), int(bytes), 0x00020000);
+}
+
+// (q & 0xF0F0F0F0) ^ 0x80808080: each byte = 16*high_nibble - 128 as int8.
+__device__ __forceinline__ uint32_t hi_nib_s8(uint32_t q) {
+    return (q & 0xF0F0F0F0u) ^ 0x80808080u;  // one v_bitop3 on gfx950
+}
+__device__ __forceinline__ int sdot2_ones(uint32_t pair) {
+    typedef short s16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, pair), __builtin_bit_cast(s16x2, 0x00010001u), 0, false);
+}
+
+// ---- activation prologue -------------------------------------------------------
+// In two halves so that its global loads are issued ahead of the weight ring
+// (vmcnt counts loads in issue order: a load issued after the weights would
+// make the prologue wait for them). Fused mode (x fp32): 16 lanes per
+// 256-element block quantize with the reference rule (a lane owns one
+// 16-value chunk = one bsum group); the first TNT/16 blocks are preloaded, any
+// further ones are handled in a loop. Pre-quantized mode: int8 values, scales
+// and bsums are copied into the records.
+struct XPre {
+    float4 v0, v1, v2, v3;
+};
+
+template <int TYPE, int S>
+__device__ __forceinline__ XPre tstage_preload(const TJobDev &jb) {
+    XPre p{};
+    const uint32_t tid = threadIdx.x;
+    const uint32_t nblk = S * (jb.cols / 256);
+    if (jb.x != nullptr) {
+        const uint32_t g = min(tid / 16, nblk - 1), k = tid & 15;
+        const float4 *src = reinterpret_cast<const float4 *>(jb.x + size_t(g) * 256 + 16 * k);
+        p.v0 = src[0];
+        p.v1 = src[1];
+        p.v2 = src[2];
+        p.v3 = src[3];
+    }
+    return p;
+}
+
+template <int TYPE>
+__device__ __forceinline__ void tquant_chunk(const float *e, uint32_t g, uint32_t k, bool ok, unsigned char *xr) {
+    constexpr int WIDTH = TYPE == kQ8_0 ? 2 : 16;  // lanes per activation block
+    AbsMax m{0.0f, 0.0f, 1 << 20};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float a = fabsf(e[i]);
+        if (a > m.amax) {
+            m.amax = a;
+            m.maxv = e[i];
+            m.idx = int(16 * (k % WIDTH)) + i;
+        }
+    }
+    m = absmax_reduce<WIDTH>(m);
+    uint32_t w[4] = {0, 0, 0, 0};
+    int bsum = 0;
+    float dv = 0.0f;
+    if (m.amax != 0.0f) {
+        const float iscale = __fdiv_rn(-127.0f, m.maxv);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int qv = int(rintf(iscale * e[i]));
+            qv = qv < 127 ? qv : 127;
+            bsum += qv;
+            w[i >> 2] |= uint32_t(uint8_t(int8_t(qv))) << (8 * (i & 3));
+        }
+        dv = __fdiv_rn(1.0f, iscale);
+    }
+    if (ok) {
+        unsigned char *r = xr + size_t(g) * XB;
+        *reinterpret_cast<u32x4 *>(r + 16 * k) = u32x4{w[0], w[1], w[2], w[3]};
+        if constexpr (TYPE == kQ8_0) {
+            if ((k & 1) == 0) reinterpret_cast<float *>(r + XB_BS)[k / 2] = dv;
+        } else {
+            reinterpret_cast<int16_t *>(r + XB_BS)[k] = int16_t(bsum);
+            if (k == 0) *reinterpret_cast<float *>(r + XB_D) = dv;
+        }
+    }
+}
+
+template <int TYPE, int S>
+__device__ __forceinline__ void tstage_finish(const TJobDev &jb, const XPre &p, unsigned char *xr) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t nblk = S * (jb.cols / 256);
+    if (jb.x != nullptr) {
+        {
+            const float e[16] = {p.v0.x, p.v0.y, p.v0.z, p.v0.w, p.v1.x, p.v1.y, p.v1.z, p.v1.w,
+                                 p.v2.x, p.v2.y, p.v2.z, p.v2.w, p.v3.x, p.v3.y, p.v3.z, p.v3.w};
+            tquant_chunk<TYPE>(e, tid / 16, tid & 15, tid / 16 < nblk, xr);
+        }
+        for (uint32_t g0 = TNT / 16; g0 < nblk; g0 += TNT / 16) {
+            const uint32_t g = g0 + tid / 16, k = tid & 15;
+            const bool ok = g < nblk;
+            const float4 *src = reinterpret_cast<const float4 *>(jb.x + size_t(ok ? g : 0) * 256 + 16 * k);
+            const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+            const float e[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                                 v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+            tquant_chunk<TYPE>(e, g, k, ok, xr);
+        }
+    } else {
+        for (uint32_t i = tid; i < nblk * 16; i += TNT)
+            *reinterpret_cast<u32x4 *>(xr + size_t(i / 16) * XB + 16 * (i & 15)) =
+                reinterpret_cast<const u32x4 *>(jb.act.qs)[i];
+        if constexpr (TYPE == kQ8_0) {
+            for (uint32_t i = tid; i < nblk * 8; i += TNT)
+                reinterpret_cast<float *>(xr + size_t(i / 8) * XB + XB_BS)[i & 7] = jb.act.d[i];
+        } else {
+            for (uint32_t i = tid; i < nblk; i += TNT) *reinterpret_cast<float *>(xr + size_t(i) * XB + XB_D) = jb.act.d[i];
+            for (uint32_t i = tid; i < nblk * 8; i += TNT)
+                reinterpret_cast<uint32_t *>(xr + size_t(i / 8) * XB + XB_BS)[i & 7] =
+                    reinterpret_cast<const uint32_t *>(jb.act.bsums)[i];
+        }
+    }
+}
+
+// ---- per-unit dot products (one lane = one 256-weight unit) -----------------------
+
+template <int TYPE, int S>
+struct TDot;
+
+// Q4_K: the 8 sub-block integer sums are exact (reference
+// SIMDMatMulVecAVX2.cpp:3690-3702); main = sum sc_i*s_i and min = sum
+// m_i*(bsum pair) in int32, then d8*(d*main - dmin*min). High nibbles enter
+// the dot products as 16h-128 and are corrected with 128*sum(x), which the
+// bsums hold, before the exact division by 16.
+template <int S>
+struct TDot<kQ4_K, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        const u32x4 h = lds128(u);
+        const uint32_t scl = h.y & 0x3F3F3F3Fu, mnl = h.z & 0x3F3F3F3Fu;
+        const uint32_t sch = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+        const uint32_t mnh = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+        const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
+        int mainI[S], minI[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) mainI[s] = minI[s] = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 qa = lds128(u + 16 + 32 * j), qb = lds128(u + 32 + 32 * j);
+            const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                lo[k] = q[k] & 0x0F0F0F0Fu;
+                hi[k] = hi_nib_s8(q[k]);
+            }
+            const uint32_t scw = j < 2 ? scl : sch, mnw = j < 2 ? mnl : mnh;
+            const int sc0 = int(byte_of(scw, (2 * j) & 3)), sc1 = int(byte_of(scw, (2 * j + 1) & 3));
+            const int m0 = int(byte_of(mnw, (2 * j) & 3)), m1 = int(byte_of(mnw, (2 * j + 1) & 3));
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const unsigned char *xr = xr0 + s * xtok;
+                const u32x4 x0 = lds128(xr + 64 * j), x1 = lds128(xr + 64 * j + 16);
+                const u32x4 x2 = lds128(xr + 64 * j + 32), x3 = lds128(xr + 64 * j + 48);
+                const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+                const uint2 bs = *reinterpret_cast<const uint2 *>(xr + XB_BS + 8 * j);
+                const int bp0 = sdot2_ones(bs.x), bp1 = sdot2_ones(bs.y);
+                int s0 = 0, t1 = 0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    s0 = sdot4(int(lo[k]), int(xl[k]), s0);
+                    t1 = sdot4(int(hi[k]), int(xh[k]), t1);
+                }
+                const int s1 = (t1 + 128 * bp1) >> 4;
+                if (dbg) {
+                    dbg[s * dbg_tok + 2 * j] = s0;
+                    dbg[s * dbg_tok + 2 * j + 1] = s1;
+                }
+                mainI[s] += sc0 * s0 + sc1 * s1;
+                minI[s] += m0 * bp0 + m1 * bp1;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = d8 * (d * float(mainI[s]) - dmin * float(minI[s]));
+        }
+    }
+};
+
+// Q8_0, one unit (8 blocks of 34 B) per lane: value = sum_blk (d_w*d8) * isum
+// (reference SIMDMatMulVecAVX2.cpp:4339-4366).
+template <int S>
+struct TDot<kQ8_0, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[s] = 0.0f;
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {  // block pairs (68 B, 4-byte aligned)
+            const uint32_t *w = reinterpret_cast<const uint32_t *>(u + 68 * pr);
+            uint32_t wd[17];
+#pragma unroll
+            for (int k = 0; k < 17; ++k) wd[k] = w[k];
+            uint32_t q0[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q0[k] = align2(wd[k + 1], wd[k], 2);
+            const float dw0 = h2f(wd[0] & 0xFFFFu), dw1 = h2f(wd[8] >> 16);
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const unsigned char *xr = xr0 + s * xtok;
+                const u32x4 x0 = lds128(xr + 64 * pr), x1 = lds128(xr + 64 * pr + 16);
+                const u32x4 x2 = lds128(xr + 64 * pr + 32), x3 = lds128(xr + 64 * pr + 48);
+                const uint32_t xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const uint32_t xb[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+                int s0 = 0, s1 = 0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    s0 = sdot4(int(q0[k]), int(xa[k]), s0);
+                    s1 = sdot4(int(wd[9 + k]), int(xb[k]), s1);
+                }
+                if (dbg) {
+                    dbg[s * dbg_tok + 2 * pr] = s0;
+                    dbg[s * dbg_tok + 2 * pr + 1] = s1;
+                }
+                const float2 d8 = *reinterpret_cast<const float2 *>(xr + XB_BS + 8 * pr);
+                acc[s] += (dw0 * d8.x) * float(s0) + (dw1 * d8.y) * float(s1);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) val[s] = acc[s];
+    }
+};
+
+template <int TYPE, int S, bool DBG>
+__global__ __launch_bounds__(TNT) __attribute__((amdgpu_waves_per_eu(1, TC_TWPE))) void k_gemv_t(TLaunchArgs L) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned char *xr = smem;
+    constexpr uint32_t UB = unit_bytes(TYPE);
+    constexpr uint32_t TILE_BYTES = kTileUnits * UB;
+    constexpr int NX = tile_dwordx4(TYPE);  // 16-byte loads per lane per tile
+    constexpr int D = tile_depth(TYPE, S);
+    // The wave index is read as a scalar so that the tile schedule, the
+    // descriptor choice and the buffer offsets stay in SGPRs.
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    unsigned char *tile = smem + L.off_t + wave * TILE_BYTES;
+    float *spart = reinterpret_cast<float *>(smem + L.off_p);
+
+    uint32_t j = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxJobs; ++k)
+        if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
+    const TJobDev jb = L.jobs[j];
+    const uint32_t nu = jb.nu;
+    const uint32_t pairs = jb.W2 != nullptr ? 2 : 1;
+    const uint32_t r0 = (blockIdx.x - jb.wg_begin) * jb.rows_per_wg;
+    const uint32_t nr = min(jb.rows_per_wg, jb.rows - r0);
+    const uint32_t per_mat = nr * nu;
+    const uint32_t ntiles_mat = (per_mat + kTileUnits - 1) / kTileUnits;
+    const uint32_t ntiles = ntiles_mat * pairs;
+    const size_t nbr = TYPE == kQ8_0 ? jb.cols / 32 : jb.cols / 256;
+    const size_t per = TYPE == kQ4_K ? 8 : 1;
+    const size_t dbg_tok = size_t(jb.rows) * nbr * per;
+    const size_t xtok = size_t(nu) * XB;
+    // Descriptors over exactly this workgroup's rows of each matrix.
+    const __amdgpu_buffer_rsrc_t rs1 = make_rsrc(jb.W + size_t(r0) * nu * UB, per_mat * UB);
+    const __amdgpu_buffer_rsrc_t rs2 = make_rsrc((pairs == 2 ? jb.W2 : jb.W) + size_t(r0) * nu * UB, per_mat * UB);
+
+
+    // Register ring: the wave's tiles are t = wave, wave+TNW, ...; slot i holds
+    // tile k (k mod D == i) from its load until it is copied to the wave's LDS
+    // buffer, after which the slot refills with tile k+D. D-1 tiles stay in
+    // flight while one is decoded. Copies and refills are unconditional so
+    // every path issues the same loads and the in-order vmcnt bookkeeping never
+    // drains at a control-flow join.
+    const uint32_t nmine = wave < ntiles ? (ntiles - wave + TNW - 1) / TNW : 0;
+    const XPre xp = tstage_preload<TYPE, S>(jb);
+    Regs<D * NX> buf;
+    auto ld = [&](auto i, uint32_t t) __attribute__((always_inline)) {
+        const bool second = t >= ntiles_mat;
+        const uint32_t tt = second ? t - ntiles_mat : t;
+        const uint32_t soff = t < ntiles ? tt * TILE_BYTES : 0x40000000u;
+        const __amdgpu_buffer_rsrc_t rs = second ? rs2 : rs1;
+        static_for<0, NX>([&](auto c) __attribute__((always_inline)) {
+            reg<decltype(i)::value * NX + c.value>(buf) =
+                __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + c.value * 1024, soff, 0);
+        });
+    };
+    static_for<0, D>([&](auto i) __attribute__((always_inline)) { ld(i, wave + i.value * TNW); });
+    tstage_finish<TYPE, S>(jb, xp, xr);
+    __syncthreads();
+
+    for (uint32_t k0 = 0; k0 < nmine; k0 += D) {
+        static_for<0, D>([&](auto i) __attribute__((always_inline)) {
+            const uint32_t kk = k0 + i.value;
+            const uint32_t t = wave + kk * TNW;
+            static_for<0, NX>([&](auto c) __attribute__((always_inline)) {
+                *reinterpret_cast<u32x4 *>(tile + (c.value * 64 + lane) * 16) = reg<i.value * NX + c.value>(buf);
+            });
+            ld(i, t + D * TNW);
+            if (kk < nmine) {
+                const uint32_t m = t >= ntiles_mat ? 1u : 0u;
+                const uint32_t um = (t - m * ntiles_mat) * kTileUnits + lane;
+                if (um < per_mat) {
+                    const uint32_t rl = div_fast(um, jb.nu_div);
+                    const uint32_t b = um - rl * nu;
+                    int32_t *dbg = nullptr;
+                    if constexpr (DBG)
+                        dbg = jb.dbg + (size_t(r0 + rl) * nbr + (TYPE == kQ8_0 ? size_t(b) * 8 : b)) * per;
+                    float val[S];
+                    TDot<TYPE, S>::run(tile + lane * UB, xr + size_t(b) * XB, xtok, val, dbg, dbg_tok);
+#pragma unroll
+                    for (int s = 0; s < S; ++s) spart[((size_t(m) * S + s) * nr + rl) * nu + b] = val[s];
+                }
+            }
+        });
+    }
+    __syncthreads();
+    // Row sums: 4 lanes per (token, row), each summing a strided quarter of
+    // the row's units, combined with DPP quad sums (fixed order).
+    const uint32_t nout = S * nr;
+    for (uint32_t o0 = 0; o0 < nout; o0 += TNT / 4) {
+        const uint32_t o = o0 + tid / 4, q = tid & 3;
+        const uint32_t oc = o < nout ? o : nout - 1;
+        const uint32_t s = oc / nr, rl = oc - s * nr;
+        const float *pg = spart + (size_t(s) * nr + rl) * nu;
+        float g = 0.0f;
+        for (uint32_t bb = q; bb < nu; bb += 4) g += pg[bb];
+        g = quad_sum(g);
+        float u = 0.0f;
+        if (pairs == 2) {
+            const float *pu = spart + ((size_t(S) + s) * nr + rl) * nu;
+            for (uint32_t bb = q; bb < nu; bb += 4) u += pu[bb];
+            u = quad_sum(u);
+        }
+        if (o < nout && q == 0) {
+            if (pairs == 2) {
+                jb.out2[size_t(s) * jb.out_ld + r0 + rl] = u;
+                if (jb.epi == 1) g = g / (1.0f + expf(-g)) * u;
+            }
+            jb.out[size_t(s) * jb.out_ld + r0 + rl] = g;
+        }
+    }
+}
+
+template <int TYPE, int S, bool DBG>
+hipError_t launch_tiled_sd(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
+    // Dynamic LDS above 64 KB needs the per-kernel opt-in, once per process.
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    k_gemv_t<TYPE, S, DBG><<<g, TNT, lds, st>>>(a);
+    return hipSuccess;
+}
+
+template <int TYPE, int S>
+hipError_t launch_tiled_s(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
+    // The per-block integer-sum test hook is its own instantiation: its
+    // global stores would otherwise sit in the production loop.
+    bool dbg = false;
+    for (uint32_t j = 0; j < a.njobs; ++j) dbg = dbg || a.jobs[j].dbg != nullptr;
+    return dbg ? launch_tiled_sd<TYPE, S, true>(a, g, lds, st) : launch_tiled_sd<TYPE, S, false>(a, g, lds, st);
+}
+
+template <int TYPE>
+hipError_t launch_tiled(uint32_t S, const TLaunchArgs &a, uint32_t grid, uint32_t lds, hipStream_t st) {
+    const dim3 g{grid, 1u, 1u};
+    hipError_t e = hipSuccess;
+    switch (S) {
+#define TC_CASE(n) \
+    case n: e = launch_tiled_s<TYPE, n>(a, g, lds, st); break;
+        TC_CASE(1) TC_CASE(2) TC_CASE(3) TC_CASE(4) TC_CASE(5) TC_CASE(6) TC_CASE(7) TC_CASE(8)
+#undef TC_CASE
+        default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    return hipGetLastError();
+}
+
+template <int TYPE>
+hipError_t launch_typed(uint32_t S, const LaunchArgs &a, uint32_t grid, uint32_t lds, hipStream_t st) {
+    const dim3 g{grid, 1u, 1u};
+    switch (S) {
+#define TC_CASE(n) \
+    case n: k_gemv<TYPE, n><<<g, NT, lds, st>>>(a); break;
+        TC_CASE(1) TC_CASE(2) TC_CASE(3) TC_CASE(4) TC_CASE(5) TC_CASE(6) TC_CASE(7) TC_CASE(8)
+#undef TC_CASE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+uint32_t lds_act_bytes(int type, uint32_t S, uint32_t cols, uint32_t *off_d, uint32_t *off_b, uint32_t *off_g) {
+    auto up = [](uint32_t v) { return (v + 15u) & ~15u; };
+    const uint32_t blk = type == kQ8_0 ? 32 : 256;
+    uint32_t o = up(S * cols);
+    *off_d = o;
+    o = up(o + S * (cols / blk) * 4);
+    *off_b = o;
+    // The Q8_K quantizer writes bsums for every K-type input (IQ3_XXS too),
+    // so the region exists even where the dot product does not read it.
+    if (type != kQ8_0) o = up(o + S * (cols / 16) * 2);
+    *off_g = o;
+    if (type == kIQ3_XXS) o += 1024;
+    return o;
+}
+
+}  // namespace
+
+namespace {
+
+constexpr uint32_t kTLdsBudget = 96 * 1024;
+
+uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
+    uint32_t o = S * (cols / 256) * XB;
+    a->off_t = o;
+    o += TNW * kTileUnits * unit_bytes(type);
+    a->off_p = o;
+    return o;
+}
+
+hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t njobs, int num_cu,
+                             hipStream_t st) {
+    TLaunchArgs a{};
+    a.njobs = njobs;
+    uint32_t maxcols = 0;
+    uint64_t total_units = 0;
+    for (uint32_t j = 0; j < njobs; ++j) {
+        maxcols = std::max(maxcols, jobs[j].cols);
+        total_units += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * (jobs[j].W2 ? 2 : 1);
+    }
+    const uint32_t fixed = tlds_layout(type, S, maxcols, &a);
+    if (fixed >= kTLdsBudget) return hipErrorInvalidValue;
+    const uint32_t part_avail = kTLdsBudget - fixed;
+    // About 2 workgroups per CU, each with at least 4 tiles of work.
+    const uint64_t want = std::max<uint64_t>(
+        1, std::min<uint64_t>(uint64_t(num_cu) * 2, (total_units + 4 * kTileUnits - 1) / (4 * kTileUnits)));
+    uint32_t wg = 0, max_part = 0;
+    for (uint32_t j = 0; j < njobs; ++j) {
+        const GemvJob &g = jobs[j];
+        TJobDev &d = a.jobs[j];
+        const uint32_t pairs = g.W2 ? 2 : 1;
+        d.W = g.W;
+        d.W2 = g.W2;
+        d.x = g.x;
+        d.act = g.act;
+        d.out = g.out;
+        d.out2 = g.out2;
+        d.dbg = g.dbg;
+        d.rows = g.rows;
+        d.cols = g.cols;
+        d.nu = g.cols / 256;
+        d.out_ld = g.out_ld;
+        d.epi = g.epi;
+        d.nu_div = make_divmod(d.nu);
+        const uint64_t units = uint64_t(g.rows) * d.nu * pairs;
+        uint64_t gj = std::max<uint64_t>(1, (want * units + total_units / 2) / total_units);
+        gj = std::min<uint64_t>(gj, g.rows);
+        uint32_t rpw = uint32_t((g.rows + gj - 1) / gj);
+        const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
+        if (fit == 0) return hipErrorInvalidValue;
+        rpw = std::min(rpw, fit);
+        d.rows_per_wg = rpw;
+        gj = (g.rows + rpw - 1) / rpw;
+        d.wg_begin = wg;
+        wg += uint32_t(gj);
+        max_part = std::max(max_part, pairs * S * rpw * d.nu * 4);
+    }
+    const uint32_t lds = fixed + max_part;
+    switch (type) {
+        case kQ4_K: return launch_tiled<kQ4_K>(S, a, wg, lds, st);
+        case kQ8_0: return launch_tiled<kQ8_0>(S, a, wg, lds, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+uint32_t gemv_max_tokens(int type, uint32_t cols) {
+    uint32_t best = 0;
+    if (type == kQ4_K || type == kQ8_0) {
+        for (uint32_t S = 1; S <= 8; ++S) {
+            TLaunchArgs a;
+            if (tlds_layout(type, S, cols, &a) + 2 * S * (cols / 256) * 4 <= kTLdsBudget) best = S;
+        }
+        return best;
+    }
+    for (uint32_t S = 1; S <= 8; ++S) {
+        uint32_t a, b, c;
+        const uint32_t act = lds_act_bytes(type, S, cols, &a, &b, &c);
+        if (act + 2 * S * (cols / 256) * 4 <= kLdsBudget) best = S;
+    }
+    return best;
+}
+
+hipError_t launch_gemv_jobs(int type, uint32_t S, const GemvJob *jobs, uint32_t njobs, int num_cu,
+                            hipStream_t st) {
+    if (S == 0 || S > 8 || njobs == 0 || njobs > uint32_t(kMaxJobs)) return hipErrorInvalidValue;
+    for (uint32_t j = 0; j < njobs; ++j) {
+        const GemvJob &g = jobs[j];
+        if (g.rows == 0 || g.cols == 0 || g.cols % 256 != 0) return hipErrorInvalidValue;
+        if ((reinterpret_cast<uintptr_t>(g.W) & 15) || (g.W2 && (reinterpret_cast<uintptr_t>(g.W2) & 15)))
+            return hipErrorInvalidValue;
+    }
+    if (type == kQ4_K || type == kQ8_0) return launch_gemv_tiled(type, S, jobs, njobs, num_cu, st);
+    LaunchArgs a{};
+    a.njobs = njobs;
+    uint32_t maxcols = 0;
+    uint64_t total_units = 0;
+    for (uint32_t j = 0; j < njobs; ++j) {
+        const GemvJob &g = jobs[j];
+        if (g.rows == 0 || g.cols == 0 || g.cols % 256 != 0) return hipErrorInvalidValue;
+        if ((reinterpret_cast<uintptr_t>(g.W) & 15) || (g.W2 && (reinterpret_cast<uintptr_t>(g.W2) & 15)))
+            return hipErrorInvalidValue;
+        maxcols = std::max(maxcols, g.cols);
+        total_units += uint64_t(g.rows) * (g.cols / 256) * (g.W2 ? 2 : 1);
+    }
+    const uint32_t act = lds_act_bytes(type, S, maxcols, &a.off_d, &a.off_b, &a.off_g);
+    a.off_p = act;
+    if (act >= kLdsBudget) return hipErrorInvalidValue;
+    const uint32_t part_avail = std::min(kPartBudget, kLdsBudget - act);
+    // One 16-wave workgroup per CU; each job gets a share of the CUs in
+    // proportion to its units, and at least 2 passes of units per workgroup.
+    const uint64_t want = std::max<uint64_t>(1, std::min<uint64_t>(uint64_t(num_cu), (total_units + 2 * kUnitsPerPass - 1) /
+                                                                                       (2 * kUnitsPerPass)));
+    uint32_t wg = 0;
+    uint32_t max_part = 0;
+    for (uint32_t j = 0; j < njobs; ++j) {
+        const GemvJob &g = jobs[j];
+        JobDev &d = a.jobs[j];
+        const uint32_t pairs = g.W2 ? 2 : 1;
+        d.W = g.W;
+        d.W2 = g.W2;
+        d.x = g.x;
+        d.act = g.act;
+        d.out = g.out;
+        d.out2 = g.out2;
+        d.dbg = g.dbg;
+        d.rows = g.rows;
+        d.cols = g.cols;
+        d.nu = g.cols / 256;
+        d.out_ld = g.out_ld;
+        d.epi = g.epi;
+        d.nu_div = make_divmod(d.nu);
+        const uint64_t units = uint64_t(g.rows) * d.nu * pairs;
+        uint64_t gj = std::max<uint64_t>(1, (want * units + total_units / 2) / total_units);
+        gj = std::min<uint64_t>(gj, g.rows);
+        d.rows_per_wg = uint32_t((g.rows + gj - 1) / gj);
+        gj = (g.rows + d.rows_per_wg - 1) / d.rows_per_wg;
+        const uint32_t fit = std::max<uint32_t>(1, part_avail / (pairs * S * d.nu * 4));
+        d.chunk_rows = std::min(d.rows_per_wg, fit);
+        d.wg_begin = wg;
+        wg += uint32_t(gj);
+        max_part = std::max(max_part, pairs * S * d.chunk_rows * d.nu * 4);
+    }
+    const uint32_t lds = act + max_part;
+    if (lds > kLdsBudget) return hipErrorInvalidValue;
+    switch (type) {
+        case kQ4_K: return launch_typed<kQ4_K>(S, a, wg, lds, st);
+        case kQ8_0: return launch_typed<kQ8_0>(S, a, wg, lds, st);
+        case kQ6_K: return launch_typed<kQ6_K>(S, a, wg, lds, st);
+        case kIQ3_XXS: return launch_typed<kIQ3_XXS>(S, a, wg, lds, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace tc

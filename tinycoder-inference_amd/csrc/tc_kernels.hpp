@@ -1,0 +1,41 @@
+// tc_kernels.hpp -- launchers shared between the kernel translation units and
+// the host dispatch (tc_api.cpp).
+#pragma once
+
+#include "tc_common.hpp"
+
+namespace tc {
+
+// Activation quantizer for weight type `wtype` (Q8_K for the K-quants and
+// IQ3_XXS, 32-wide Q8_0-style for Q8_0) of x[S][cols] into `buf` laid out by
+// act_layout(wtype, S, cols).
+hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols, const ActLayout &L,
+                            void *buf, hipStream_t st);
+
+// Weight encoder: x[nunits][256] fp32 -> nunits units of `type`.
+hipError_t launch_encode(int type, const float *x, void *out, uint32_t nunits, hipStream_t st);
+
+// One mat-vec job: out[s][r] (row stride out_ld per token) = W[r] . x[s].
+// With W2 set the job is a pair over the same rows (gate/up): out2 = W2 x and,
+// for epi == 1, out = silu(W x) * out2. Activations come from `x` (fp32,
+// quantized in the kernel prologue) or, when x is null, from `act`
+// (quantized by launch_quant_act).
+struct GemvJob {
+    const uint8_t *W = nullptr, *W2 = nullptr;
+    const float *x = nullptr;
+    ActView act{};
+    float *out = nullptr, *out2 = nullptr;
+    int32_t *dbg = nullptr;  // optional per-block integer sums (test hook)
+    uint32_t rows = 0, cols = 0, out_ld = 0;
+    int epi = 0;
+};
+
+// Up to 8 jobs of one weight type and token count in one launch. Returns
+// hipErrorInvalidValue when a shape does not fit the kernel.
+hipError_t launch_gemv_jobs(int type, uint32_t S, const GemvJob *jobs, uint32_t njobs, int num_cu,
+                            hipStream_t st);
+
+// Largest token count per mat-vec launch for this width (LDS budget).
+uint32_t gemv_max_tokens(int type, uint32_t cols);
+
+}  // namespace tc

@@ -1,0 +1,307 @@
+// tc_quant.hip -- activation quantizers and weight encoders for gfx950.
+//
+// This translation unit is compiled with -ffp-contract=off: every multiply and
+// add below is one IEEE rounding, and division goes through __fdiv_rn, so the
+// results are bit-identical to the reference CPU code they follow.
+#include "tc_common.hpp"
+#include "tc_actquant.hpp"
+#include "tc_kernels.hpp"
+
+namespace tc {
+
+__constant__ uint32_t c_iq3xxs_grid[256] = {
+#include "iq3xxs_grid.inc"
+};
+
+// ---- activation quantizers ---------------------------------------------------
+
+// Q8_K (reference include/GGMLDequantize.hpp:2769-2807): one wave per
+// 256-element block. nblk_total = S * cols / 256 (token rows are contiguous,
+// so block g covers x[256g, 256g+256)).
+__global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int8_t *__restrict__ qs,
+                                                   float *__restrict__ d, int16_t *__restrict__ bsums,
+                                                   uint32_t nblk_total) {
+    const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= nblk_total) return;
+    quant_q8k_block_wave(x + size_t(g) * 256, qs + size_t(g) * 256, d + g, bsums + size_t(g) * 16);
+}
+
+// 32-wide rule used for Q8_0 weights (reference
+// src/cpp/core/SIMDMatMulVecAVX2.cpp:4296-4326): one wave per 8 blocks.
+__global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int8_t *__restrict__ qs,
+                                                    float *__restrict__ d, uint32_t ngroups) {
+    const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= ngroups) return;
+    quant_q8_0_blocks_wave(x + size_t(g) * 256, qs + size_t(g) * 256, d + size_t(g) * 8);
+}
+
+// ---- fp16 encodings ----------------------------------------------------------
+
+// The reference's fp32 -> fp16 (include/GGMLDequantize.hpp:61-87): mantissa
+// truncation; its subnormal branch also takes exponent -14, so values below
+// 2^-13 become signed zero. Reproduced as-is for the Q4_K encoder.
+__device__ uint16_t f2h_trunc_ref(float f) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (b >> 31) & 1u;
+    const int exp = int((b >> 23) & 0xFFu) - 127;
+    uint32_t mant = b & 0x7FFFFFu;
+    uint32_t h;
+    if (exp > 15) {
+        h = (sign << 15) | (0x1Fu << 10) | (mant != 0 ? 0x200u : 0u);
+    } else if (exp > -14) {
+        h = (sign << 15) | (uint32_t(exp + 15) << 10) | (mant >> 13);
+    } else if (exp > -24) {
+        mant = (mant | 0x800000u) >> (14 - exp);
+        h = (sign << 15) | (mant >> 13);
+    } else {
+        h = sign << 15;
+    }
+    return uint16_t(h);
+}
+
+// IEEE fp32 -> fp16, round to nearest even (this build's own encoders).
+__device__ uint16_t f2h_rne(float f) {
+    const uint32_t x = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return uint16_t(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return uint16_t(sign | 0x7C00u);
+    if (ax < 0x38800000u) {
+        const float a = __builtin_bit_cast(float, ax);
+        return uint16_t(sign | uint32_t(rintf(a * 16777216.0f)));
+    }
+    uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7FFFFFu) >> 13);
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+    return uint16_t(sign | h);
+}
+
+__device__ __forceinline__ float first_abs_max(const float *x, int n, float *amax_out) {
+    float amax = 0.0f, maxv = 0.0f;
+    for (int j = 0; j < n; ++j) {
+        const float a = fabsf(x[j]);
+        if (a > amax) {
+            amax = a;
+            maxv = x[j];
+        }
+    }
+    *amax_out = amax;
+    return maxv;
+}
+
+// ---- weight encoders (one thread per 256-weight unit) ------------------------
+
+// Q4_K: the reference's quantizeQ4KBlock (src/cpp/core/GGMLQuantize.cpp:47-95).
+__device__ void enc_q4k(const float *x, uint8_t *out) {
+    float scale[8], minv[8];
+    uint8_t q[256];
+    float maxScale = 0.0f, maxMin = 0.0f;
+    for (int g = 0; g < 8; ++g) {
+        const float *xp = x + 32 * g;
+        float mn = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            mn = xp[i] < mn ? xp[i] : mn;
+            mx = mx < xp[i] ? xp[i] : mx;
+        }
+        const float sc = __fdiv_rn(mx - mn, 15.0f);
+        scale[g] = sc;
+        minv[g] = -mn;
+        maxScale = maxScale < sc ? sc : maxScale;
+        maxMin = maxMin < minv[g] ? minv[g] : maxMin;
+        for (int i = 0; i < 32; ++i) {
+            int v = sc > 1e-30f ? int(rintf(__fdiv_rn(xp[i] - mn, sc))) : 0;
+            v = v < 0 ? 0 : (v > 15 ? 15 : v);
+            q[32 * g + i] = uint8_t(v);
+        }
+    }
+    const uint16_t hd = maxScale > 0.0f ? f2h_trunc_ref(__fdiv_rn(maxScale, 63.0f)) : 0;
+    const uint16_t hdm = maxMin > 0.0f ? f2h_trunc_ref(__fdiv_rn(maxMin, 63.0f)) : 0;
+    const float d = h2f(hd), dm = h2f(hdm);
+    uint8_t sc6[8], m6[8];
+    for (int g = 0; g < 8; ++g) {
+        const int s = d > 1e-30f ? int(rintf(__fdiv_rn(scale[g], d))) : 0;
+        const int m = dm > 1e-30f ? int(rintf(__fdiv_rn(minv[g], dm))) : 0;
+        sc6[g] = uint8_t(s < 0 ? 0 : (s > 63 ? 63 : s));
+        m6[g] = uint8_t(m < 0 ? 0 : (m > 63 ? 63 : m));
+    }
+    out[0] = uint8_t(hd);
+    out[1] = uint8_t(hd >> 8);
+    out[2] = uint8_t(hdm);
+    out[3] = uint8_t(hdm >> 8);
+    for (int j = 0; j < 4; ++j) {
+        out[4 + j] = uint8_t(sc6[j] | ((sc6[j + 4] >> 4) << 6));
+        out[8 + j] = uint8_t(m6[j] | ((m6[j + 4] >> 4) << 6));
+        out[12 + j] = uint8_t((sc6[j + 4] & 0x0F) | ((m6[j + 4] & 0x0F) << 4));
+    }
+    for (int i = 0; i < 128; ++i) {
+        const int g0 = 2 * (i >> 5), l = i & 31;
+        out[16 + i] = uint8_t(q[32 * g0 + l] | (q[32 * (g0 + 1) + l] << 4));
+    }
+}
+
+// Q8_0 (8 blocks of 32): d = max|w|/127 as fp16 (RNE), q = rne(w/d), +-127.
+__device__ void enc_q8_0(const float *x, uint8_t *out) {
+    for (int b = 0; b < 8; ++b) {
+        const float *xb = x + 32 * b;
+        uint8_t *o = out + 34 * b;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fabsf(xb[i]) > amax ? fabsf(xb[i]) : amax;
+        const uint16_t hd = f2h_rne(__fdiv_rn(amax, 127.0f));
+        const float d = h2f(hd);
+        o[0] = uint8_t(hd);
+        o[1] = uint8_t(hd >> 8);
+        for (int i = 0; i < 32; ++i) {
+            int q = d > 0.0f ? int(rintf(__fdiv_rn(xb[i], d))) : 0;
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            o[2 + i] = uint8_t(int8_t(q));
+        }
+    }
+}
+
+// Q6_K (this build's encoder; the reference ships none): per-16 group scale
+// m/-32 from the signed first-abs-max, block iscale = -128/M over the group
+// scales, int8 sub-scales, fp16 (RNE) d = 1/iscale, q = clamp(rne(x/(d*sc)),
+// -32, 31) + 32, packed as the reference decoder reads
+// (include/GGMLDequantize.hpp:503-527).
+__device__ void enc_q6k(const float *x, uint8_t *out) {
+    float gs[16];
+    for (int g = 0; g < 16; ++g) {
+        float amax;
+        const float m = first_abs_max(x + 16 * g, 16, &amax);
+        gs[g] = amax == 0.0f ? 0.0f : __fdiv_rn(m, -32.0f);
+    }
+    float amaxs;
+    const float M = first_abs_max(gs, 16, &amaxs);
+    for (int i = 0; i < 210; ++i) out[i] = 0;
+    uint8_t L[256];
+    if (amaxs == 0.0f) {
+        for (int e = 0; e < 256; ++e) L[e] = 32;
+    } else {
+        const float iscale = __fdiv_rn(-128.0f, M);
+        int8_t sc[16];
+        for (int g = 0; g < 16; ++g) {
+            const int v = int(rintf(iscale * gs[g]));
+            sc[g] = int8_t(v > 127 ? 127 : v);
+            out[192 + g] = uint8_t(sc[g]);
+        }
+        const uint16_t hd = f2h_rne(__fdiv_rn(1.0f, iscale));
+        out[208] = uint8_t(hd);
+        out[209] = uint8_t(hd >> 8);
+        const float dh = h2f(hd);
+        for (int e = 0; e < 256; ++e) {
+            const float dg = dh * float(sc[e >> 4]);
+            int q = dg != 0.0f ? int(rintf(__fdiv_rn(x[e], dg))) : 0;
+            q = q < -32 ? -32 : (q > 31 ? 31 : q);
+            L[e] = uint8_t(q + 32);
+        }
+    }
+    for (int half = 0; half < 2; ++half) {
+        uint8_t *ql = out + 64 * half;
+        uint8_t *qh = out + 128 + 32 * half;
+        const uint8_t *Lh = L + 128 * half;
+        for (int l = 0; l < 32; ++l) {
+            const int q1 = Lh[l], q2 = Lh[l + 32], q3 = Lh[l + 64], q4 = Lh[l + 96];
+            ql[l] = uint8_t((q1 & 0xF) | ((q3 & 0xF) << 4));
+            ql[l + 32] = uint8_t((q2 & 0xF) | ((q4 & 0xF) << 4));
+            qh[l] = uint8_t((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+        }
+    }
+}
+
+// IQ3_XXS (this build's encoder; the reference ships none): per-32 scale
+// s = max|x|/62, block d = max s / 7.75 (fp16 RNE), ls = clamp(rne(s/(0.5d) -
+// 0.5), 0, 15), db = d*(0.5+ls)*0.5; per 8 the negative signs with the
+// smallest-|x| one flipped on odd count (even parity is implied by the
+// format); per 4 the grid entry nearest |x|/db in squared error (first wins).
+__device__ void enc_iq3xxs(const float *x, uint8_t *out) {
+    float sc[8], smax = 0.0f;
+    for (int c = 0; c < 8; ++c) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fabsf(x[32 * c + i]) > amax ? fabsf(x[32 * c + i]) : amax;
+        sc[c] = __fdiv_rn(amax, 62.0f);
+        smax = sc[c] > smax ? sc[c] : smax;
+    }
+    for (int i = 0; i < 98; ++i) out[i] = 0;
+    const uint16_t hd = f2h_rne(__fdiv_rn(smax, 7.75f));
+    const float d = h2f(hd);
+    if (d == 0.0f) return;
+    out[0] = uint8_t(hd);
+    out[1] = uint8_t(hd >> 8);
+    uint8_t *qs = out + 2;
+    uint8_t *sas = out + 66;
+    for (int c = 0; c < 8; ++c) {
+        const int lsl = int(rintf(__fdiv_rn(sc[c], 0.5f * d) - 0.5f));
+        const int ls = lsl < 0 ? 0 : (lsl > 15 ? 15 : lsl);
+        const float db = d * (0.5f + float(ls)) * 0.5f;
+        uint32_t aux = uint32_t(ls) << 28;
+        for (int l = 0; l < 4; ++l) {
+            const float *xv = x + 32 * c + 8 * l;
+            uint32_t neg = 0;
+            int minj = 0;
+            for (int j = 0; j < 8; ++j) {
+                if (xv[j] < 0.0f) neg |= 1u << j;
+                if (fabsf(xv[j]) < fabsf(xv[minj])) minj = j;
+            }
+            if (__builtin_popcount(neg) & 1) neg ^= 1u << minj;
+            aux |= (neg & 127u) << (7 * l);
+            for (int h = 0; h < 2; ++h) {
+                float t[4];
+                for (int j = 0; j < 4; ++j) t[j] = __fdiv_rn(fabsf(xv[4 * h + j]), db);
+                int best = 0;
+                float berr = 0.0f;
+                for (int gi = 0; gi < 256; ++gi) {
+                    const uint32_t gv = c_iq3xxs_grid[gi];
+                    float err = 0.0f;
+                    for (int j = 0; j < 4; ++j) {
+                        const float diff = float((gv >> (8 * j)) & 0xFFu) - t[j];
+                        err = err + diff * diff;
+                    }
+                    if (gi == 0 || err < berr) {
+                        berr = err;
+                        best = gi;
+                    }
+                }
+                qs[8 * c + 2 * l + h] = uint8_t(best);
+            }
+        }
+        for (int k = 0; k < 4; ++k) sas[4 * c + k] = uint8_t(aux >> (8 * k));
+    }
+}
+
+__global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict__ x, uint8_t *__restrict__ out,
+                                               uint32_t nunits) {
+    const uint32_t u = blockIdx.x * 64 + threadIdx.x;
+    if (u >= nunits) return;
+    const float *xu = x + size_t(u) * 256;
+    uint8_t *o = out + size_t(u) * unit_bytes(type);
+    switch (type) {
+        case kQ4_K: enc_q4k(xu, o); break;
+        case kQ8_0: enc_q8_0(xu, o); break;
+        case kQ6_K: enc_q6k(xu, o); break;
+        default: enc_iq3xxs(xu, o); break;
+    }
+}
+
+// ---- launchers -----------------------------------------------------------------
+
+hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols, const ActLayout &L,
+                            void *buf, hipStream_t st) {
+    int8_t *qs = reinterpret_cast<int8_t *>(static_cast<char *>(buf) + L.qs_off);
+    float *d = reinterpret_cast<float *>(static_cast<char *>(buf) + L.d_off);
+    if (wtype == kQ8_0) {
+        const uint32_t ng = S * (cols / 256);
+        k_quant_q8_0<<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, ng);
+    } else {
+        int16_t *bs = reinterpret_cast<int16_t *>(static_cast<char *>(buf) + L.bs_off);
+        const uint32_t nb = S * (cols / 256);
+        k_quant_q8k<<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, nb);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_encode(int type, const float *x, void *out, uint32_t nunits, hipStream_t st) {
+    k_encode<<<(nunits + 63) / 64, 64, 0, st>>>(type, x, static_cast<uint8_t *>(out), nunits);
+    return hipGetLastError();
+}
+
+}  // namespace tc

@@ -1,0 +1,189 @@
+"""Python binding of libtc_hip.so (the C-ABI in include/tc_qmatmul.h).
+
+The library is the product; this module only passes device pointers, sizes
+and the current HIP stream through ctypes, and raises when a call fails.
+PyTorch supplies device memory and streams. There is no CPU fallback: if the
+library is missing or a call is refused, the call raises.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtc_hip.so")
+
+Q8_0, Q4_K, Q6_K, IQ3_XXS = 8, 12, 14, 18
+TYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ3_XXS": IQ3_XXS}
+TYPE_SIZE = {Q8_0: 34, Q4_K: 144, Q6_K: 210, IQ3_XXS: 98}
+BLOCK_SIZE = {Q8_0: 32, Q4_K: 256, Q6_K: 256, IQ3_XXS: 256}
+
+TC_OK, TC_E_UNSUPPORTED, TC_E_LAUNCH, TC_E_ARG = 0, -1, -2, -3
+
+# Every function the C header declares, with its ctypes signature.
+_P, _U32, _I = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int
+SIGNATURES = {
+    "tc_available": (_I, []),
+    "tc_gemv": (_I, [_I, _P, _P, _P, _U32, _U32, _U32, _P]),
+    "tc_gemv_reserve": (_I, [_U32, _U32]),
+    "tc_gemv_multi": (_I, [_I, _U32, _P, _P, _P, _P, _P, _U32, _P]),
+    "tc_act_bytes": (ctypes.c_size_t, [_I, _U32, _U32]),
+    "tc_act_quantize": (_I, [_I, _P, _U32, _U32, _P, _P]),
+    "tc_gemv_q8": (_I, [_I, _P, _P, _P, _U32, _U32, _U32, _P]),
+    "tc_gemv_dual": (_I, [_I, _P, _P, _P, _P, _P, _U32, _U32, _P]),
+    "tc_gemm": (_I, [_I, _P, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "tc_gemm_preferred": (_I, [_U32, _U32, _U32]),
+    "tc_gemm_set_q8_enabled": (None, [_I]),
+    "tc_quantize_act": (_I, [_I, _P, _U32, _U32, _P, _P, _P, _P]),
+    "tc_block_isums": (_I, [_I, _P, _P, _P, _U32, _U32, _U32, _P]),
+    "tc_encode": (_I, [_I, _P, _P, _U32, _U32, _P]),
+    "tc_row_bytes": (ctypes.c_size_t, [_I, _U32]),
+    "tc_moe_ffn": (_I, [_P, _P, _P, _U32, _U32, _P, _P, _P, _U32, _U32, _U32, _P, _P]),
+    "tc_last_error": (ctypes.c_char_p, []),
+}
+
+
+class TCError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"libtc_hip error {code}: {msg}")
+        self.code = code
+
+
+def row_bytes(qtype, cols):
+    return cols // BLOCK_SIZE[qtype] * TYPE_SIZE[qtype]
+
+
+def load_library(path=LIB_PATH):
+    # torch ships its own libamdhip64.so.7; it must be the HIP runtime this
+    # library binds to, or the streams and memory torch hands over belong to
+    # another runtime instance. Importing torch first makes the loader reuse it.
+    import torch  # noqa: F401
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() "
+                                "(make -C tinycoder-inference_amd)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+class Library:
+    """Thin callable wrapper; tensors are torch CUDA tensors."""
+
+    def __init__(self, path=LIB_PATH):
+        self.lib = load_library(path)
+        self.path = path
+
+    # -- helpers ---------------------------------------------------------------
+    def _stream(self):
+        import torch
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def _check(self, rc):
+        if rc != TC_OK:
+            raise TCError(rc, self.lib.tc_last_error().decode())
+        return rc
+
+    def available(self):
+        return bool(self.lib.tc_available())
+
+    # -- entry points -------------------------------------------------------------
+    def gemv(self, qtype, w, x, rows, cols, out=None):
+        import torch
+        S = x.numel() // cols
+        if out is None:
+            out = torch.empty((S, rows), dtype=torch.float32, device=x.device)
+        self._check(self.lib.tc_gemv(qtype, _ptr(w), _ptr(x), _ptr(out), S, rows, cols, self._stream()))
+        return out
+
+    def gemv_multi(self, qtype, ws, xs, rows, cols, outs=None):
+        """One launch over several matrices; xs[i] is [S][cols[i]]."""
+        import torch
+        n = len(ws)
+        S = xs[0].numel() // cols[0]
+        if outs is None:
+            outs = [torch.empty((S, rows[i]), dtype=torch.float32, device=xs[0].device) for i in range(n)]
+        arr = ctypes.c_void_p * n
+        u32 = ctypes.c_uint32 * n
+        self._check(self.lib.tc_gemv_multi(qtype, n, arr(*[w.data_ptr() for w in ws]),
+                                           arr(*[x.data_ptr() for x in xs]), arr(*[o.data_ptr() for o in outs]),
+                                           u32(*rows), u32(*cols), S, self._stream()))
+        return outs
+
+    def act_buffer(self, qtype, seq_len, cols, device="cuda"):
+        import torch
+        n = self.lib.tc_act_bytes(qtype, seq_len, cols)
+        if n == 0:
+            raise TCError(TC_E_UNSUPPORTED, f"no activation layout for type {qtype}, cols {cols}")
+        return torch.empty(n, dtype=torch.uint8, device=device)
+
+    def act_quantize(self, qtype, x, cols, act):
+        S = x.numel() // cols
+        self._check(self.lib.tc_act_quantize(qtype, _ptr(x), S, cols, _ptr(act), self._stream()))
+        return act
+
+    def gemv_q8(self, qtype, w, act, seq_len, rows, cols, out=None):
+        import torch
+        if out is None:
+            out = torch.empty((seq_len, rows), dtype=torch.float32, device=act.device)
+        self._check(self.lib.tc_gemv_q8(qtype, _ptr(w), _ptr(act), _ptr(out), seq_len, rows, cols,
+                                        self._stream()))
+        return out
+
+    def gemm(self, qtype, w, x, rows, cols, out=None):
+        import torch
+        S = x.numel() // cols
+        if out is None:
+            out = torch.empty((S, rows), dtype=torch.float32, device=x.device)
+        self._check(self.lib.tc_gemm(qtype, _ptr(w), _ptr(x), _ptr(out), S, rows, cols,
+                                     cols // BLOCK_SIZE[qtype], self._stream()))
+        return out
+
+    def gemv_dual(self, qtype, wg, wu, x, rows, cols):
+        import torch
+        g = torch.empty(rows, dtype=torch.float32, device=x.device)
+        u = torch.empty(rows, dtype=torch.float32, device=x.device)
+        self._check(self.lib.tc_gemv_dual(qtype, _ptr(wg), _ptr(wu), _ptr(x), _ptr(g), _ptr(u), rows,
+                                          cols, self._stream()))
+        return g, u
+
+    def quantize_act(self, qtype, x, cols):
+        import torch
+        S = x.numel() // cols
+        blk = 32 if qtype == Q8_0 else 256
+        qs = torch.empty((S, cols), dtype=torch.int8, device=x.device)
+        d = torch.empty((S, cols // blk), dtype=torch.float32, device=x.device)
+        bs = None if qtype == Q8_0 else torch.empty((S, cols // 16), dtype=torch.int16, device=x.device)
+        self._check(self.lib.tc_quantize_act(qtype, _ptr(x), S, cols, _ptr(qs), _ptr(d), _ptr(bs),
+                                             self._stream()))
+        return qs, d, bs
+
+    def block_isums(self, qtype, w, x, rows, cols):
+        import torch
+        S = x.numel() // cols
+        nb = cols // BLOCK_SIZE[qtype]
+        k = 8 if qtype == Q4_K else 1
+        out = torch.empty((S, rows, nb, k), dtype=torch.int32, device=x.device)
+        self._check(self.lib.tc_block_isums(qtype, _ptr(w), _ptr(x), _ptr(out), S, rows, cols,
+                                            self._stream()))
+        return out
+
+    def encode(self, qtype, x):
+        import torch
+        rows, cols = x.shape
+        out = torch.empty(rows * row_bytes(qtype, cols), dtype=torch.uint8, device=x.device)
+        self._check(self.lib.tc_encode(qtype, _ptr(x), _ptr(out), rows, cols, self._stream()))
+        return out
+
+    def moe_ffn(self, x, ids, wts, wg, wu, wd, n_experts, hidden, ff, out=None):
+        import torch
+        S, K = ids.shape
+        if out is None:
+            out = torch.empty((S, hidden), dtype=torch.float32, device=x.device)
+        self._check(self.lib.tc_moe_ffn(_ptr(x), _ptr(ids), _ptr(wts), S, K, _ptr(wg), _ptr(wu), _ptr(wd),
+                                        n_experts, hidden, ff, _ptr(out), self._stream()))
+        return out
