@@ -217,7 +217,7 @@ def main():
                    "rotating_copies": N_COPIES, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv<Q4_K,1>, bytes-weighted over the 4 launches of a step"},
+                     "kernel": "k_gemv_t<Q4_K,1>, bytes-weighted over the 4 launches of a step"},
         "per_launch": per_launch,
         "layer_one_launch": {"us": round(one_launch_ms * 1e3, 2), "GB/s": round(one_launch_gbs, 1),
                              "frac": round(one_launch_gbs / HBM_PEAK_GBS, 4)},

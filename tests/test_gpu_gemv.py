@@ -212,20 +212,28 @@ def test_gemv_multi_matches_single(tc, dev, oracle):
 
 @pytest.mark.parametrize("qt", ALL)
 def test_gemv_dual_swiglu(tc, dev, oracle, qt):
+    """gate/up pair in one launch: uout = up row sums, gout = silu(gate) * up.
+    The gate pre-activation is not an output, so its tolerance is carried
+    through silu (|silu'| <= 1.1): |d(silu(g) u)| <= 1.1 |u| dg + |silu(g)| du."""
     rng = np.random.default_rng(5 + qt)
     rows, cols = 517, 1536
-    wg = random_blocks(qt, rng, rows, cols)
-    wu = random_blocks(qt, rng, rows, cols)
+    sd = 1.0 if qt == Q4_K else 0.02
+    wg = oracle.encode(qt, gaussian(rng, (rows, cols), sd))
+    wu = oracle.encode(qt, gaussian(rng, (rows, cols), sd))
     x = gaussian(rng, (1, cols))
     g, u = tc.gemv_dual(qt, to_dev(wg, dev), to_dev(wu, dev), to_dev(x, dev), rows, cols)
-    g, u = g.cpu().numpy(), u.cpu().numpy()
-    rg = oracle.matmul(qt, wg, x, rows, cols)[0]
-    ru = oracle.matmul(qt, wu, x, rows, cols)[0]
+    g, u = g.cpu().numpy().astype(np.float64), u.cpu().numpy().astype(np.float64)
+    rg = oracle.matmul(qt, wg, x, rows, cols)[0].astype(np.float64)
+    ru = oracle.matmul(qt, wu, x, rows, cols)[0].astype(np.float64)
     ok, worst = close(u, ru)
     assert ok, worst
-    ref = (rg / (np.float32(1.0) + np.exp(-rg.astype(np.float64)))) * ru
-    ok, worst = close(g, ref)
-    assert ok, worst
+    silu = rg / (1.0 + np.exp(-rg))
+    ref = silu * ru
+    dg = 1e-4 + 1e-3 * np.abs(rg)
+    du = 1e-4 + 1e-3 * np.abs(ru)
+    bound = 1.1 * np.abs(ru) * dg + np.abs(silu) * du + 1e-6
+    err = np.abs(g - ref)
+    assert (err <= bound).all(), float((err / bound).max())
 
 
 @pytest.mark.parametrize("qt", ALL)

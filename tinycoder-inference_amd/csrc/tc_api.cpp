@@ -100,19 +100,20 @@ tc::ActView act_view(void *buf, const tc::ActLayout &L, size_t tok, int type, ui
 // small kernel into the device scratch instead of in every workgroup of the
 // mat-vec (whose prologue would repeat the work hundreds of times). The
 // tiled kernels (Q4_K, Q8_0) take that path; the others quantize in-kernel.
-bool prequantize_wide(int type, uint32_t S, uint32_t cols) {
-    return (type == TC_Q4_K || type == TC_Q8_0) && size_t(S) * cols > 16 * 256;
+bool prequantize_wide(int type, uint32_t S, uint32_t cols, uint64_t weight_bytes) {
+    return size_t(S) * cols > tc::gemv_fused_quant_limit(type, weight_bytes);
 }
 
 int launch_jobs(Device *dev, int type, uint32_t S, tc::GemvJob *jobs, uint32_t n, hipStream_t st) {
+    const uint64_t wbytes = tc::jobs_weight_bytes(type, jobs, n);
     size_t need = 0;
     for (uint32_t i = 0; i < n; ++i)
-        if (jobs[i].x && prequantize_wide(type, S, jobs[i].cols)) need += tc::act_layout(type, S, jobs[i].cols).bytes;
+        if (jobs[i].x && prequantize_wide(type, S, jobs[i].cols, wbytes)) need += tc::act_layout(type, S, jobs[i].cols).bytes;
     if (need) {
         if (!ensure(dev->act, dev->act_bytes, need)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", need);
         size_t off = 0;
         for (uint32_t i = 0; i < n; ++i) {
-            if (!(jobs[i].x && prequantize_wide(type, S, jobs[i].cols))) continue;
+            if (!(jobs[i].x && prequantize_wide(type, S, jobs[i].cols, wbytes))) continue;
             const tc::ActLayout L = tc::act_layout(type, S, jobs[i].cols);
             void *buf = static_cast<char *>(dev->act) + off;
             hipError_t e = tc::launch_quant_act(type, jobs[i].x, S, jobs[i].cols, L, buf, st);

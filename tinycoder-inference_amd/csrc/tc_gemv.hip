@@ -529,23 +529,41 @@ __global__ __launch_bounds__(NT) void k_gemv(LaunchArgs L) {
 // through an immediate offset.
 // ============================================================================
 
-#ifndef TC_TNT
-#define TC_TNT 256
-#endif
-#ifndef TC_TDEPTH
-#define TC_TDEPTH 2
-#endif
-#ifndef TC_TWPE
-#define TC_TWPE 3
-#endif
-constexpr int TNT = TC_TNT;                 // threads per workgroup
-constexpr int TNW = TNT / 64;
+// Two launch shapes (chosen per launch on the host): big streams use 512
+// threads with one tile in flight per wave (the activation loads, which miss
+// in L2, then see a short memory queue); small ones, and Q8_0 whose 17 KB
+// wave tiles would not fit eight to a CU, use 256 threads with two.
+struct CfgBig {
+    static constexpr int NT = 512, DEPTH = 1;
+};
+struct CfgSmall {
+    static constexpr int NT = 256, DEPTH = 2;
+};
 constexpr int kTileUnits = 64;
 constexpr uint32_t XB = 304;                // LDS bytes per 256-element activation block
 constexpr uint32_t XB_BS = 256, XB_D = 288;  // bsums and d offsets inside a record
 
 __host__ __device__ constexpr int tile_dwordx4(int type) { return unit_bytes(type) * kTileUnits / 1024; }
-__host__ __device__ constexpr int tile_depth(int type, int S) { return type == kQ4_K && S <= 2 ? TC_TDEPTH : 2; }
+template <class C>
+__host__ __device__ constexpr int tile_depth(int type, int S) {
+    // Register slots in flight per wave: fewer where the accumulators of S
+    // tokens would otherwise spill at 2 waves per SIMD (a Q8_0 slot is 68
+    // registers, a Q4_K slot 36).
+    const int d = type == kQ4_K ? (S <= 6 ? 2 : 1) : (S >= 4 ? 1 : 2);
+    return d < C::DEPTH ? d : C::DEPTH;
+}
+
+#ifdef TC_TRACE
+__device__ unsigned long long g_trace[8192 * 4];
+#define TC_TRACE_PT(k)                                                                                       \
+    do {                                                                                                    \
+        if (threadIdx.x == 0 && blockIdx.x < 8192) g_trace[blockIdx.x * 4 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define TC_TRACE_PT(k) \
+    do {               \
+    } while (0)
+#endif
 
 struct TJobDev {
     const uint8_t *W, *W2;
@@ -588,6 +606,13 @@ __device__ __forceinline__ u32x4 &reg(Regs<N> &r) {
     else
         return reg<I - 1, N - 1>(r.t);
 }
+template <int I, int N>
+__device__ __forceinline__ const u32x4 &reg(const Regs<N> &r) {
+    if constexpr (I == 0)
+        return r.h;
+    else
+        return reg<I - 1, N - 1>(r.t);
+}
 template <int I, int N, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
     if constexpr (I < N) {
@@ -613,28 +638,63 @@ __device__ __forceinline__ int sdot2_ones(uint32_t pair) {
 // ---- activation prologue -------------------------------------------------------
 // In two halves so that its global loads are issued ahead of the weight ring
 // (vmcnt counts loads in issue order: a load issued after the weights would
-// make the prologue wait for them). Fused mode (x fp32): 16 lanes per
-// 256-element block quantize with the reference rule (a lane owns one
-// 16-value chunk = one bsum group); the first TNT/16 blocks are preloaded, any
-// further ones are handled in a loop. Pre-quantized mode: int8 values, scales
-// and bsums are copied into the records.
+// make the prologue wait for them). The loads go through a buffer descriptor
+// sized to the activation, so the fixed number of preload slots costs no
+// memory traffic past its end.
+//
+// Fused mode (x fp32): 16 lanes per 256-element block quantize with the
+// reference rule (a lane owns one 16-value chunk = one bsum group); chunks
+// tid + i*TNT (i < kXPre) are preloaded, any further ones are loaded after the
+// weights in a loop. Pre-quantized mode: the int8 values (kXPreQ chunks of 16
+// bytes per thread), the bsums or per-32 scales, and the per-block scales are
+// preloaded likewise and copied into the records.
+constexpr int kXPre = 3;   // fused: 64-byte x chunks per thread
+constexpr int kXPreQ = 8;  // pre-quantized: 16-byte qs chunks per thread
+constexpr int kXSlots = 4 * kXPre > kXPreQ + 2 ? 4 * kXPre : kXPreQ + 2;
+
 struct XPre {
-    float4 v0, v1, v2, v3;
+    Regs<kXSlots> r;
+};
+
+struct XRsrc {
+    __amdgpu_buffer_rsrc_t a, b, c;  // fused: x; pre-quantized: qs, bsums or d32, d
 };
 
 template <int TYPE, int S>
-__device__ __forceinline__ XPre tstage_preload(const TJobDev &jb) {
-    XPre p{};
-    const uint32_t tid = threadIdx.x;
+__device__ __forceinline__ XRsrc tstage_rsrc(const TJobDev &jb) {
     const uint32_t nblk = S * (jb.cols / 256);
-    if (jb.x != nullptr) {
-        const uint32_t g = min(tid / 16, nblk - 1), k = tid & 15;
-        const float4 *src = reinterpret_cast<const float4 *>(jb.x + size_t(g) * 256 + 16 * k);
-        p.v0 = src[0];
-        p.v1 = src[1];
-        p.v2 = src[2];
-        p.v3 = src[3];
+    XRsrc r;
+    const bool fused = jb.x != nullptr;
+    r.a = fused ? make_rsrc(jb.x, nblk * 1024u) : make_rsrc(jb.act.qs, nblk * 256u);
+    if constexpr (TYPE == kQ8_0) {
+        r.b = make_rsrc(jb.act.d, fused ? 0u : nblk * 32u);
+        r.c = r.b;
+    } else {
+        r.b = make_rsrc(jb.act.bsums, fused ? 0u : nblk * 32u);
+        r.c = make_rsrc(jb.act.d, fused ? 0u : nblk * 4u);
     }
+    return r;
+}
+
+// The same kXSlots 16-byte loads in both modes (one straight-line sequence,
+// so no register state merges across a branch): fused slot s holds x chunk
+// tid + (s/4)*TNT, quarter s%4; pre-quantized slots 0..kXPreQ-1 hold qs chunks
+// tid + s*TNT, slot kXPreQ side dwords 4tid..4tid+3, slot kXPreQ+1 block
+// scales 4tid..4tid+3. Unused slots read past the descriptor (zeros, no traffic).
+template <int TYPE, int S, int TNT>
+__device__ __forceinline__ XPre tstage_preload(const TJobDev &jb, const XRsrc &rs) {
+    XPre p;
+    const uint32_t tid = threadIdx.x;
+    const bool fused = jb.x != nullptr;
+    static_for<0, kXSlots>([&](auto sl) __attribute__((always_inline)) {
+        constexpr int s = decltype(sl)::value;
+        const uint32_t off_f = s < 4 * kXPre ? (tid + (s / 4) * TNT) * 64u + 16u * (s % 4) : 0x80000000u;
+        uint32_t off_q = 0x80000000u;
+        if constexpr (s < kXPreQ) off_q = (tid + s * TNT) * 16u;
+        if constexpr (s == kXPreQ || s == kXPreQ + 1) off_q = tid * 16u;
+        const __amdgpu_buffer_rsrc_t r = fused ? rs.a : (s < kXPreQ ? rs.a : (s == kXPreQ ? rs.b : rs.c));
+        reg<s>(p.r) = __builtin_amdgcn_raw_buffer_load_b128(r, fused ? off_f : off_q, 0, 0);
+    });
     return p;
 }
 
@@ -678,37 +738,70 @@ __device__ __forceinline__ void tquant_chunk(const float *e, uint32_t g, uint32_
     }
 }
 
-template <int TYPE, int S>
-__device__ __forceinline__ void tstage_finish(const TJobDev &jb, const XPre &p, unsigned char *xr) {
+template <int TYPE>
+__device__ __forceinline__ void tquant_regs(const u32x4 &a, const u32x4 &b, const u32x4 &c, const u32x4 &d, uint32_t g,
+                                            uint32_t k, bool ok, unsigned char *xr) {
+// (the uint32_t copy is needed: clang's __builtin_bit_cast applied directly to
+// an ext_vector element reads element 0)
+#define TC_F(v) __builtin_bit_cast(float, uint32_t(v))
+    const float e[16] = {TC_F(a.x), TC_F(a.y), TC_F(a.z), TC_F(a.w), TC_F(b.x), TC_F(b.y), TC_F(b.z), TC_F(b.w),
+                         TC_F(c.x), TC_F(c.y), TC_F(c.z), TC_F(c.w), TC_F(d.x), TC_F(d.y), TC_F(d.z), TC_F(d.w)};
+#undef TC_F
+    tquant_chunk<TYPE>(e, g, k, ok, xr);
+}
+
+template <int TYPE>
+__device__ __forceinline__ void tstore_side(unsigned char *xr, uint32_t i, uint32_t v) {
+    // dword i of the bsums (Q8_K: 8 per block) or per-32 scales (Q8_0: 8 per block)
+    reinterpret_cast<uint32_t *>(xr + size_t(i / 8) * XB + XB_BS)[i & 7] = v;
+}
+
+template <int TYPE, int S, int TNT>
+__device__ __forceinline__ void tstage_finish(const TJobDev &jb, const XRsrc &rs, const XPre &p, unsigned char *xr) {
     const uint32_t tid = threadIdx.x;
     const uint32_t nblk = S * (jb.cols / 256);
     if (jb.x != nullptr) {
-        {
-            const float e[16] = {p.v0.x, p.v0.y, p.v0.z, p.v0.w, p.v1.x, p.v1.y, p.v1.z, p.v1.w,
-                                 p.v2.x, p.v2.y, p.v2.z, p.v2.w, p.v3.x, p.v3.y, p.v3.z, p.v3.w};
-            tquant_chunk<TYPE>(e, tid / 16, tid & 15, tid / 16 < nblk, xr);
-        }
-        for (uint32_t g0 = TNT / 16; g0 < nblk; g0 += TNT / 16) {
-            const uint32_t g = g0 + tid / 16, k = tid & 15;
-            const bool ok = g < nblk;
-            const float4 *src = reinterpret_cast<const float4 *>(jb.x + size_t(ok ? g : 0) * 256 + 16 * k);
-            const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
-            const float e[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
-                                 v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
-            tquant_chunk<TYPE>(e, g, k, ok, xr);
+        const uint32_t nchunk = nblk * 16;
+        static_for<0, kXPre>([&](auto i) __attribute__((always_inline)) {
+            if (i.value * TNT < nchunk) {
+                const uint32_t c = tid + i.value * TNT;
+                tquant_regs<TYPE>(reg<4 * i.value>(p.r), reg<4 * i.value + 1>(p.r), reg<4 * i.value + 2>(p.r),
+                                  reg<4 * i.value + 3>(p.r), c / 16, c & 15, c < nchunk, xr);
+            }
+        });
+        for (uint32_t c0 = kXPre * TNT; c0 < nchunk; c0 += TNT) {
+            const uint32_t c = c0 + tid;
+            const uint32_t off = c * 64u;
+            tquant_regs<TYPE>(__builtin_amdgcn_raw_buffer_load_b128(rs.a, off, 0, 0),
+                              __builtin_amdgcn_raw_buffer_load_b128(rs.a, off + 16, 0, 0),
+                              __builtin_amdgcn_raw_buffer_load_b128(rs.a, off + 32, 0, 0),
+                              __builtin_amdgcn_raw_buffer_load_b128(rs.a, off + 48, 0, 0), c / 16, c & 15, c < nchunk, xr);
         }
     } else {
-        for (uint32_t i = tid; i < nblk * 16; i += TNT)
-            *reinterpret_cast<u32x4 *>(xr + size_t(i / 16) * XB + 16 * (i & 15)) =
-                reinterpret_cast<const u32x4 *>(jb.act.qs)[i];
-        if constexpr (TYPE == kQ8_0) {
-            for (uint32_t i = tid; i < nblk * 8; i += TNT)
-                reinterpret_cast<float *>(xr + size_t(i / 8) * XB + XB_BS)[i & 7] = jb.act.d[i];
-        } else {
-            for (uint32_t i = tid; i < nblk; i += TNT) *reinterpret_cast<float *>(xr + size_t(i) * XB + XB_D) = jb.act.d[i];
-            for (uint32_t i = tid; i < nblk * 8; i += TNT)
-                reinterpret_cast<uint32_t *>(xr + size_t(i / 8) * XB + XB_BS)[i & 7] =
-                    reinterpret_cast<const uint32_t *>(jb.act.bsums)[i];
+        const uint32_t nq = nblk * 16, nside = nblk * 8;
+        static_for<0, kXPreQ>([&](auto i) __attribute__((always_inline)) {
+            const uint32_t c = tid + i.value * TNT;
+            if (c < nq) *reinterpret_cast<u32x4 *>(xr + size_t(c / 16) * XB + 16 * (c & 15)) = reg<i.value>(p.r);
+        });
+        for (uint32_t c = tid + kXPreQ * TNT; c < nq; c += TNT)
+            *reinterpret_cast<u32x4 *>(xr + size_t(c / 16) * XB + 16 * (c & 15)) =
+                __builtin_amdgcn_raw_buffer_load_b128(rs.a, c * 16u, 0, 0);
+        const u32x4 side = reg<kXPreQ>(p.r);
+        const uint32_t sv[4] = {side.x, side.y, side.z, side.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (4 * tid + i < nside) tstore_side<TYPE>(xr, 4 * tid + i, sv[i]);
+        for (uint32_t c = tid + 4 * TNT; c < nside; c += TNT)
+            tstore_side<TYPE>(xr, c, __builtin_amdgcn_raw_buffer_load_b32(rs.b, c * 4u, 0, 0));
+        if constexpr (TYPE != kQ8_0) {
+            const u32x4 dv = reg<kXPreQ + 1>(p.r);
+            const uint32_t dd[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * tid + i < nblk) *reinterpret_cast<uint32_t *>(xr + size_t(4 * tid + i) * XB + XB_D) = dd[i];
+            for (uint32_t c = tid + 4 * TNT; c < nblk; c += TNT)
+                *reinterpret_cast<uint32_t *>(xr + size_t(c) * XB + XB_D) =
+                    __builtin_amdgcn_raw_buffer_load_b32(rs.c, c * 4u, 0, 0);
         }
     }
 }
@@ -825,14 +918,15 @@ struct TDot<kQ8_0, S> {
     }
 };
 
-template <int TYPE, int S, bool DBG>
-__global__ __launch_bounds__(TNT) __attribute__((amdgpu_waves_per_eu(1, TC_TWPE))) void k_gemv_t(TLaunchArgs L) {
+template <int TYPE, int S, bool DBG, class C>
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
+    constexpr int TNT = C::NT, TNW = TNT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char *xr = smem;
     constexpr uint32_t UB = unit_bytes(TYPE);
     constexpr uint32_t TILE_BYTES = kTileUnits * UB;
     constexpr int NX = tile_dwordx4(TYPE);  // 16-byte loads per lane per tile
-    constexpr int D = tile_depth(TYPE, S);
+    constexpr int D = tile_depth<C>(TYPE, S);
     // The wave index is read as a scalar so that the tile schedule, the
     // descriptor choice and the buffer offsets stay in SGPRs.
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -844,6 +938,7 @@ __global__ __launch_bounds__(TNT) __attribute__((amdgpu_waves_per_eu(1, TC_TWPE)
     for (int k = 1; k < kMaxJobs; ++k)
         if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
     const TJobDev jb = L.jobs[j];
+    TC_TRACE_PT(0);
     const uint32_t nu = jb.nu;
     const uint32_t pairs = jb.W2 != nullptr ? 2 : 1;
     const uint32_t r0 = (blockIdx.x - jb.wg_begin) * jb.rows_per_wg;
@@ -867,7 +962,14 @@ __global__ __launch_bounds__(TNT) __attribute__((amdgpu_waves_per_eu(1, TC_TWPE)
     // every path issues the same loads and the in-order vmcnt bookkeeping never
     // drains at a control-flow join.
     const uint32_t nmine = wave < ntiles ? (ntiles - wave + TNW - 1) / TNW : 0;
-    const XPre xp = tstage_preload<TYPE, S>(jb);
+    const XRsrc xrs = tstage_rsrc<TYPE, S>(jb);
+    const XPre xp = tstage_preload<TYPE, S, TNT>(jb, xrs);
+#ifndef TC_NO_XBAR
+    // Every wave's activation loads enter the CU's memory queue before any
+    // wave's weight loads (a barrier without a memory fence: it does not wait
+    // for the loads).
+    __builtin_amdgcn_s_barrier();
+#endif
     Regs<D * NX> buf;
     auto ld = [&](auto i, uint32_t t) __attribute__((always_inline)) {
         const bool second = t >= ntiles_mat;
@@ -879,9 +981,26 @@ __global__ __launch_bounds__(TNT) __attribute__((amdgpu_waves_per_eu(1, TC_TWPE)
                 __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + c.value * 1024, soff, 0);
         });
     };
-    static_for<0, D>([&](auto i) __attribute__((always_inline)) { ld(i, wave + i.value * TNW); });
-    tstage_finish<TYPE, S>(jb, xp, xr);
+    // Staged ring: D0 slots are requested before the activations are
+    // quantized, the rest after. A short memory queue at kernel start lets
+    // the activation loads (which miss in L2: every launch streams the
+    // weights through it) return in about one unloaded latency; the full
+    // depth then keeps HBM busy for the rest of the stream.
+    constexpr int D0 = 1;
+    static_for<0, D0>([&](auto i) __attribute__((always_inline)) { ld(i, wave + i.value * TNW); });
+    tstage_finish<TYPE, S, TNT>(jb, xrs, xp, xr);
+    static_for<D0, D>([&](auto i) __attribute__((always_inline)) { ld(i, wave + i.value * TNW); });
     __syncthreads();
+    TC_TRACE_PT(1);
+#ifdef TC_XDUMP
+    if constexpr (DBG) {
+        if (blockIdx.x == 0) {
+            const uint32_t nbytes = S * (jb.cols / 256) * XB;
+            for (uint32_t i = tid; i < nbytes / 4; i += TNT) jb.dbg[i] = reinterpret_cast<const int32_t *>(xr)[i];
+        }
+        return;
+    }
+#endif
 
     for (uint32_t k0 = 0; k0 < nmine; k0 += D) {
         static_for<0, D>([&](auto i) __attribute__((always_inline)) {
@@ -908,6 +1027,7 @@ __global__ __launch_bounds__(TNT) __attribute__((amdgpu_waves_per_eu(1, TC_TWPE)
             }
         });
     }
+    TC_TRACE_PT(2);
     __syncthreads();
     // Row sums: 4 lanes per (token, row), each summing a strided quarter of
     // the row's units, combined with DPP quad sums (fixed order).
@@ -934,34 +1054,35 @@ __global__ __launch_bounds__(TNT) __attribute__((amdgpu_waves_per_eu(1, TC_TWPE)
             jb.out[size_t(s) * jb.out_ld + r0 + rl] = g;
         }
     }
+    TC_TRACE_PT(3);
 }
 
-template <int TYPE, int S, bool DBG>
+template <int TYPE, int S, bool DBG, class C>
 hipError_t launch_tiled_sd(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
     // Dynamic LDS above 64 KB needs the per-kernel opt-in, once per process.
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG>),
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG, C>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    k_gemv_t<TYPE, S, DBG><<<g, TNT, lds, st>>>(a);
+    k_gemv_t<TYPE, S, DBG, C><<<g, C::NT, lds, st>>>(a);
     return hipSuccess;
 }
 
-template <int TYPE, int S>
+template <int TYPE, int S, class C>
 hipError_t launch_tiled_s(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
     // The per-block integer-sum test hook is its own instantiation: its
     // global stores would otherwise sit in the production loop.
     bool dbg = false;
     for (uint32_t j = 0; j < a.njobs; ++j) dbg = dbg || a.jobs[j].dbg != nullptr;
-    return dbg ? launch_tiled_sd<TYPE, S, true>(a, g, lds, st) : launch_tiled_sd<TYPE, S, false>(a, g, lds, st);
+    return dbg ? launch_tiled_sd<TYPE, S, true, C>(a, g, lds, st) : launch_tiled_sd<TYPE, S, false, C>(a, g, lds, st);
 }
 
-template <int TYPE>
+template <int TYPE, class C>
 hipError_t launch_tiled(uint32_t S, const TLaunchArgs &a, uint32_t grid, uint32_t lds, hipStream_t st) {
     const dim3 g{grid, 1u, 1u};
     hipError_t e = hipSuccess;
     switch (S) {
 #define TC_CASE(n) \
-    case n: e = launch_tiled_s<TYPE, n>(a, g, lds, st); break;
+    case n: e = launch_tiled_s<TYPE, n, C>(a, g, lds, st); break;
         TC_CASE(1) TC_CASE(2) TC_CASE(3) TC_CASE(4) TC_CASE(5) TC_CASE(6) TC_CASE(7) TC_CASE(8)
 #undef TC_CASE
         default: return hipErrorInvalidValue;
@@ -1002,18 +1123,26 @@ uint32_t lds_act_bytes(int type, uint32_t S, uint32_t cols, uint32_t *off_d, uin
 
 namespace {
 
-constexpr uint32_t kTLdsBudget = 96 * 1024;
+// One workgroup per CU: its LDS holds the activation records, the wave
+// tiles and the partial sums.
+constexpr uint32_t kTLdsBudget = 152 * 1024;
+// Streams of at least this many weight bytes use the 512-thread shape.
+constexpr uint64_t kBigBytes = 24ull << 20;
 
+template <class C>
 uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     uint32_t o = S * (cols / 256) * XB;
     a->off_t = o;
-    o += TNW * kTileUnits * unit_bytes(type);
+    o += (C::NT / 64) * kTileUnits * unit_bytes(type);
     a->off_p = o;
     return o;
 }
 
-hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t njobs, int num_cu,
-                             hipStream_t st) {
+bool use_big(int type, uint64_t weight_bytes) { return type == kQ4_K && weight_bytes >= kBigBytes; }
+
+template <class C>
+hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32_t njobs, int num_cu,
+                               hipStream_t st) {
     TLaunchArgs a{};
     a.njobs = njobs;
     uint32_t maxcols = 0;
@@ -1022,12 +1151,12 @@ hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t
         maxcols = std::max(maxcols, jobs[j].cols);
         total_units += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * (jobs[j].W2 ? 2 : 1);
     }
-    const uint32_t fixed = tlds_layout(type, S, maxcols, &a);
+    const uint32_t fixed = tlds_layout<C>(type, S, maxcols, &a);
     if (fixed >= kTLdsBudget) return hipErrorInvalidValue;
     const uint32_t part_avail = kTLdsBudget - fixed;
-    // About 2 workgroups per CU, each with at least 4 tiles of work.
+    // One workgroup per CU, each with at least 2 tiles of work.
     const uint64_t want = std::max<uint64_t>(
-        1, std::min<uint64_t>(uint64_t(num_cu) * 2, (total_units + 4 * kTileUnits - 1) / (4 * kTileUnits)));
+        1, std::min<uint64_t>(uint64_t(num_cu), (total_units + 2 * kTileUnits - 1) / (2 * kTileUnits)));
     uint32_t wg = 0, max_part = 0;
     for (uint32_t j = 0; j < njobs; ++j) {
         const GemvJob &g = jobs[j];
@@ -1061,20 +1190,48 @@ hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t
     }
     const uint32_t lds = fixed + max_part;
     switch (type) {
-        case kQ4_K: return launch_tiled<kQ4_K>(S, a, wg, lds, st);
-        case kQ8_0: return launch_tiled<kQ8_0>(S, a, wg, lds, st);
+        case kQ4_K: return launch_tiled<kQ4_K, C>(S, a, wg, lds, st);
+        case kQ8_0:
+            if constexpr (C::NT == CfgSmall::NT) return launch_tiled<kQ8_0, C>(S, a, wg, lds, st);
+            return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
+uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs) {
+    uint64_t b = 0;
+    for (uint32_t j = 0; j < njobs; ++j)
+        b += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * unit_bytes(type) * (jobs[j].W2 ? 2 : 1);
+    return b;
+}
+
+namespace {
+
+hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t njobs, int num_cu,
+                             hipStream_t st) {
+    return use_big(type, jobs_weight_bytes(type, jobs, njobs))
+               ? launch_gemv_tiled_c<CfgBig>(type, S, jobs, njobs, num_cu, st)
+               : launch_gemv_tiled_c<CfgSmall>(type, S, jobs, njobs, num_cu, st);
+}
+
+}  // namespace
+
+uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes) {
+    // S*cols up to which the tiled kernels preload all of x ahead of the weights
+    if (type != kQ4_K && type != kQ8_0) return 0xFFFFFFFFu;
+    return uint32_t(kXPre) * (use_big(type, weight_bytes) ? CfgBig::NT : CfgSmall::NT) * 16u;
+}
+
 uint32_t gemv_max_tokens(int type, uint32_t cols) {
     uint32_t best = 0;
     if (type == kQ4_K || type == kQ8_0) {
         for (uint32_t S = 1; S <= 8; ++S) {
             TLaunchArgs a;
-            if (tlds_layout(type, S, cols, &a) + 2 * S * (cols / 256) * 4 <= kTLdsBudget) best = S;
+            const uint32_t f = std::max(tlds_layout<CfgBig>(type, S, cols, &a), tlds_layout<CfgSmall>(type, S, cols, &a));
+            if ((type == kQ4_K ? f : tlds_layout<CfgSmall>(type, S, cols, &a)) + 2 * S * (cols / 256) * 4 <= kTLdsBudget)
+                best = S;
         }
         return best;
     }
@@ -1158,3 +1315,9 @@ hipError_t launch_gemv_jobs(int type, uint32_t S, const GemvJob *jobs, uint32_t 
 }
 
 }  // namespace tc
+
+#ifdef TC_TRACE
+extern "C" int tc_trace_dump(unsigned long long *host) {
+    return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(tc::g_trace), sizeof(tc::g_trace)));
+}
+#endif

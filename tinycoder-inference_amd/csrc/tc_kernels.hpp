@@ -36,6 +36,12 @@ hipError_t launch_gemv_jobs(int type, uint32_t S, const GemvJob *jobs, uint32_t 
                             hipStream_t st);
 
 // Largest token count per mat-vec launch for this width (LDS budget).
+// Weight bytes one mat-vec launch streams over the jobs (both matrices of a pair).
+uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs);
+// Largest S*cols a mat-vec launch over `weight_bytes` quantizes in-kernel
+// without loading x after the weights; wider inputs are quantized by a
+// separate launch first.
+uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes);
 uint32_t gemv_max_tokens(int type, uint32_t cols);
 
 }  // namespace tc
