@@ -10,8 +10,9 @@ the SwiGLU epilogue, down (each launch quantizes its input in-kernel). The weigh
 step (1.05 GB working set) so that the 256 MB Infinity Cache cannot serve them.
 
 Prints one JSON line. `value` is whole-step weight+activation bytes per
-second (GB/s); `roofline` is the Q4_K mat-vec kernel alone, timed with HIP
-events on the stream it runs on; `cpu_baseline` is the reference's own AVX2
+second (GB/s); `roofline` is the step's largest launch (the gate/up pair),
+its average duration timed with HIP events around back-to-back launches on the
+stream it runs on, its HBM traffic read from the committed rocprofv3 summary; `cpu_baseline` is the reference's own AVX2
 kernel (compiled from its sources, oracle/_ref) on the host cores.
 """
 import argparse
@@ -38,6 +39,22 @@ N_COPIES = 8
 def algorithmic_bytes(rows, cols, row_bytes):
     # weights + fp32 activation read + fp32 output write, per mat-vec
     return rows * row_bytes + 4 * cols + 4 * rows
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gate_up_pair_18944x3584_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per gate/up launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-kernel calibrated), or None if absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(weights_host, xs_host, row_bytes):
@@ -88,6 +105,9 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="counter-collection run: a 256 MiB device copy (the calibration kernel of known "
+                         "traffic), then --steps passes over the layer's launches; prints nothing else")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
@@ -130,15 +150,10 @@ def main():
         else:
             tc.gemv(Q4K, ws["down"], xs["down_in"], 3584, 18944, out=outs["down"])
 
-    def step(i, events=None):
+    def step(i):
         ws = copies[i % N_COPIES]
         for name, _ in LAUNCHES:
-            if events is not None:
-                events[name].append((torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)))
-                events[name][-1][0].record()
             launch(name, ws)
-            if events is not None:
-                events[name][-1][1].record()
 
     def step_one_launch(i):
         ws = copies[i % N_COPIES]
@@ -151,6 +166,20 @@ def main():
         step(i)
         step_one_launch(i)
     torch.cuda.synchronize()
+
+    if args.pmc_probe:
+        # Calibration: one copy kernel that reads and writes exactly 256 MiB.
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": True, "copy_bytes": 2 * src.numel() * 4, "steps": args.steps}), flush=True)
+        return
 
     def head_start():
         # Keep the GPU busy for a bounded time while the host queues the timed
@@ -184,23 +213,28 @@ def main():
     torch.cuda.synchronize()
     one_launch_ms = t1s.elapsed_time(t1e) / args.steps
 
-    # ---- per-launch kernel durations (events around each launch) -----------------------
-    events = {n: [] for n, _ in LAUNCHES}
-    head_start()
-    for i in range(args.steps):
-        step(i, events)
-    torch.cuda.synchronize()
+    # ---- per-launch kernel durations ----------------------------------------------------
+    # Each launch kind alone, K back-to-back launches over the rotating copies
+    # between two events on the launch stream (the kernels run back to back,
+    # so total / K is the kernel's average duration).
     rb = tc_hip.row_bytes
     per_launch = {}
-    tot_bytes = tot_us = 0.0
+    stream = torch.cuda.current_stream()
     for name, mats in LAUNCHES:
-        us = float(np.mean([a.elapsed_time(b) for a, b in events[name]])) * 1e3
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        head_start()
+        a.record(stream)
+        for i in range(args.steps):
+            launch(name, copies[i % N_COPIES])
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / args.steps
         by = sum(algorithmic_bytes(dims[m][0], dims[m][1], rb(Q4K, dims[m][1])) for m in mats)
-        per_launch[name] = {"mats": mats, "us": round(us, 2), "GB/s": round(by / us / 1e3, 1),
+        per_launch[name] = {"mats": mats, "bytes": by, "us": round(us, 2), "GB/s": round(by / us / 1e3, 1),
                             "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 3)}
-        tot_bytes += by
-        tot_us += us
-    achieved = tot_bytes / tot_us / 1e3
+    dom = per_launch["gate_up"]
+    achieved = dom["bytes"] / dom["us"] / 1e3
 
     step_bytes = sum(algorithmic_bytes(r, c, rb(Q4K, c)) for _, r, c in LAYER)
     ms_per_step = total_ms / args.steps
@@ -216,8 +250,9 @@ def main():
                    "batch": 1, "weight_bytes_per_step": int(sum(r * rb(Q4K, c) for _, r, c in LAYER)),
                    "rotating_copies": N_COPIES, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv_t<Q4_K,1>, bytes-weighted over the 4 launches of a step"},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "k_gemv_t<Q4_K,1,CfgBig> gate/up pair 2x18944x3584 with SwiGLU epilogue "
+                               "(the step's largest launch); bytes = weights + x + both outputs per launch"},
         "per_launch": per_launch,
         "layer_one_launch": {"us": round(one_launch_ms * 1e3, 2), "GB/s": round(one_launch_gbs, 1),
                              "frac": round(one_launch_gbs / HBM_PEAK_GBS, 4)},
