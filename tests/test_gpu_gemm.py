@@ -1,0 +1,107 @@
+"""GPU parity tests for the prefill GEMM (tc_gemm, int8 MFMA for Q4_K / Q8_0,
+the exact batched mat-vec path for Q6_K / IQ3_XXS), through the C-ABI.
+
+Bar: fp32 outputs within 1e-3 relative / 1e-4 absolute of the oracle (the C
+restatement of the reference CPU kernels, itself bit-exact with the compiled
+reference in tests/test_oracle.py). The activation quantizer the GEMM runs is
+the one whose bytes are checked bit-exact in test_gpu_gemv.py.
+"""
+import numpy as np
+import pytest
+
+from qdata import ALL, IQ3_XXS, NAMES, Q4_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def enc_weights(oracle, qt, rng, rows, cols):
+    # Q4_K from N(0,1): at N(0,0.02) the reference quantizer stores most
+    # scales as 0 (its fp16 conversion flushes values below 2^-13).
+    return oracle.encode(qt, gaussian(rng, (rows, cols), 1.0 if qt == Q4_K else 0.02))
+
+
+# (M tokens, N rows, K cols): ragged tiles, a K-split case (few output tiles),
+# a single token, and a multi-tile case.
+SHAPES = [(1, 64, 256), (37, 200, 1024), (128, 256, 5120), (130, 136, 2048), (300, 384, 768)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("qt", [Q4_K, Q8_0])
+def test_gemm_vs_oracle(tc, dev, oracle, qt, M, N, K):
+    rng = np.random.default_rng(M * 7 + N + K + qt)
+    w = enc_weights(oracle, qt, rng, N, K)
+    x = gaussian(rng, (M, K))
+    got = tc.gemm(qt, to_dev(w, dev), to_dev(x, dev), N, K).cpu().numpy()
+    ref = oracle.matmul(qt, w, x, N, K)
+    ok, worst = close(got, ref)
+    assert ok, f"{NAMES[qt]} M={M} N={N} K={K}: worst err/bound {worst:.3g}"
+
+
+@pytest.mark.parametrize("qt", [Q4_K, Q8_0])
+def test_gemm_random_blocks(tc, dev, oracle, qt):
+    """Arbitrary block bytes (all scale/min codes, subnormal fp16 scales)."""
+    rng = np.random.default_rng(99 + qt)
+    M, N, K = 70, 96, 1536
+    w = random_blocks(qt, rng, N, K)
+    x = gaussian(rng, (M, K))
+    got = tc.gemm(qt, to_dev(w, dev), to_dev(x, dev), N, K).cpu().numpy()
+    ref = oracle.matmul(qt, w, x, N, K)
+    ok, worst = close(got, ref)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("qt", [Q6_K, IQ3_XXS])
+def test_gemm_exact_batched_types(tc, dev, oracle, qt):
+    rng = np.random.default_rng(5 + qt)
+    M, N, K = 21, 80, 512
+    w = enc_weights(oracle, qt, rng, N, K)
+    x = gaussian(rng, (M, K))
+    got = tc.gemm(qt, to_dev(w, dev), to_dev(x, dev), N, K).cpu().numpy()
+    ok, worst = close(got, oracle.matmul(qt, w, x, N, K))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("qt,N,K", [(Q4_K, 17408, 5120), (Q8_0, 5120, 17408)])
+def test_gemm_full_shape_sampled_rows(tc, dev, oracle, qt, N, K):
+    """Prefill shape at full size (M=512): weights from the GPU encoder, the
+    oracle evaluated on 48 sampled rows (all 512 tokens)."""
+    import torch
+    M = 512
+    gen = torch.Generator(device=dev).manual_seed(4 + qt)
+    wf = torch.randn((N, K), generator=gen, device=dev) * (1.0 if qt == Q4_K else 0.02)
+    w = tc.encode(qt, wf)
+    del wf
+    x = torch.randn((M, K), generator=gen, device=dev)
+    got = tc.gemm(qt, w, x, N, K).cpu().numpy()
+    rb = row_bytes(qt, K)
+    wh = w.cpu().numpy().reshape(N, rb)
+    rows = np.sort(np.random.default_rng(1).choice(N, 48, replace=False))
+    ref = oracle.matmul(qt, wh[rows].copy(), x.cpu().numpy(), len(rows), K)
+    ok, worst = close(got[:, rows], ref)
+    assert ok, worst
+
+
+def test_gemm_matches_gemv_small_batch(tc, dev):
+    """M <= 8: the MFMA GEMM and the decode kernel agree within tolerance."""
+    rng = np.random.default_rng(3)
+    N, K = 300, 2048
+    w = random_blocks(Q4_K, rng, N, K)
+    x = gaussian(rng, (5, K))
+    wd, xd = to_dev(w, dev), to_dev(x, dev)
+    g = tc.gemm(Q4_K, wd, xd, N, K).cpu().numpy()
+    v = tc.gemv(Q4_K, wd, xd, N, K).cpu().numpy()
+    ok, worst = close(g, v)
+    assert ok, worst
+
+
+def test_gemm_refuses_bad_shapes(tc, dev):
+    import tc_hip
+    w = to_dev(np.zeros(row_bytes(Q4_K, 512) * 4, np.uint8), dev)
+    x = to_dev(np.zeros((3, 500), np.float32), dev)
+    with pytest.raises(tc_hip.TCError):
+        tc.gemm(Q4_K, w, x, 4, 500)

@@ -283,8 +283,29 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
     if (blocks_per_row != cols / uint32_t(tc::block_elems(type)))
         return fail(TC_E_ARG, "blocks_per_row=%u does not match cols=%u", blocks_per_row, cols);
     if (type == TC_Q8_0 && !g_q8_gemm_enabled) return fail(TC_E_UNSUPPORTED, "Q8_0 GEMM disabled");
-    (void)stream;
-    return fail(TC_E_UNSUPPORTED, "int8 MFMA GEMM not built yet");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (type != TC_Q4_K && type != TC_Q8_0) {
+        // Q6_K / IQ3_XXS: the exact batched path (the reference's launchQGemm,
+        // GpuGemvIQInt8.hpp:771-847) -- the decode kernel over token groups.
+        for (uint32_t s0 = 0; s0 < seq_len; s0 += 8) {
+            const uint32_t S = std::min(8u, seq_len - s0);
+            rc = run_gemv(dev, type, w, nullptr, x + size_t(s0) * cols, nullptr, out + size_t(s0) * rows, nullptr, 0,
+                          nullptr, S, rows, cols, st);
+            if (rc) return rc;
+        }
+        return TC_OK;
+    }
+    // Quantize all tokens once, then the MFMA kernel.
+    const tc::ActLayout L = tc::act_layout(type, seq_len, cols);
+    const size_t ws = tc::gemm_workspace_bytes(type, seq_len, rows, cols, dev->num_cu);
+    if (!ensure(dev->act, dev->act_bytes, L.bytes)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", L.bytes);
+    if (ws && !ensure(dev->aux, dev->aux_bytes, ws)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", ws);
+    hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, dev->act, st);
+    if (e != hipSuccess) return hip_fail(e, "activation quantizer");
+    e = tc::launch_gemm(type, w, act_view(dev->act, L, 0, type, cols), out, seq_len, rows, cols, dev->num_cu,
+                        ws ? dev->aux : nullptr, st);
+    if (e != hipSuccess) return hip_fail(e, "int8 MFMA GEMM");
+    return TC_OK;
 }
 
 int tc_gemm_preferred(uint32_t type, uint32_t, uint32_t) { return type_ok(int(type)) ? 1 : 0; }

@@ -44,4 +44,13 @@ uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs);
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes);
 uint32_t gemv_max_tokens(int type, uint32_t cols);
 
+// Prefill GEMM (int8 MFMA) for Q4_K / Q8_0 weights: out[M][N] = W x^T with
+// activations already quantized (launch_quant_act over M tokens). Splits K
+// across workgroups when the output tiles do not fill the chip; the partial
+// sums then need gemm_workspace_bytes() of device scratch.
+uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
+size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
+hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
+                       int num_cu, void *workspace, hipStream_t st);
+
 }  // namespace tc
