@@ -99,12 +99,53 @@ def cpu_baseline(weights_host, xs_host, row_bytes):
                       f"{'reference AVX2 matMulVecBatchQ4K_Q8K_AVX2 + ThreadPool' if kind == 'reference' else 'C port, 1 thread'}"}
 
 
+GEMM_SHAPES = [(17408, 5120), (5120, 17408)]   # (rows N, cols K), out x in
+GEMM_TOKENS = [128, 512, 2048]
+INT8_PEAK_TOPS = 5000.0
+
+
+def gemm_bench(torch, tc, tc_hip, dev, reps):
+    """Prefill GEMM (tc_gemm: activation quantization + int8 MFMA GEMM [+ split-K
+    reduce]) at every M x shape x type; weights N(0,0.02) through the GPU
+    encoders, 4 rotating copies; x ~ N(0,1). Returns one record per config."""
+    gen = torch.Generator(device=dev).manual_seed(7)
+    res = []
+    for qt, tname in ((tc_hip.Q4_K, "Q4_K"), (tc_hip.Q8_0, "Q8_0")):
+        for N, K in GEMM_SHAPES:
+            wf = torch.randn((N, K), generator=gen, device=dev) * 0.02
+            w0 = tc.encode(qt, wf)
+            del wf
+            ws = [w0] + [w0.clone() for _ in range(3)]
+            for M in GEMM_TOKENS:
+                x = torch.randn((M, K), generator=gen, device=dev)
+                out = torch.empty((M, N), device=dev)
+                for i in range(3):
+                    tc.gemm(qt, ws[i % 4], x, N, K, out=out)
+                torch.cuda.synchronize()
+                n = max(3, reps if M < 2048 else reps // 4)
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record()
+                for i in range(n):
+                    tc.gemm(qt, ws[i % 4], x, N, K, out=out)
+                b.record()
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / n
+                tops = 2.0 * M * N * K / us / 1e6
+                res.append({"type": tname, "N": N, "K": K, "M": M, "us": round(us, 1), "TOPS": round(tops, 1),
+                            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
+            del ws, w0
+            torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="counter-collection run: a 256 MiB device copy (the calibration kernel of known "
                          "traffic), then --steps passes over the layer's launches; prints nothing else")
@@ -257,6 +298,13 @@ def main():
         "layer_one_launch": {"us": round(one_launch_ms * 1e3, 2), "GB/s": round(one_launch_gbs, 1),
                              "frac": round(one_launch_gbs / HBM_PEAK_GBS, 4)},
     }
+    if not args.no_gemm:
+        del copies
+        torch.cuda.empty_cache()
+        g = gemm_bench(torch, tc, tc_hip, dev, max(10, args.steps // 4))
+        best = max(g, key=lambda r: r["TOPS"])
+        line["prefill_gemm"] = {"unit": "TOPS (2*M*N*K / time, int8 MFMA; includes the activation quantizer)",
+                                "peak_TOPS": INT8_PEAK_TOPS, "best": best, "configs": g}
     if not args.no_cpu:
         wh = {n: base[n].cpu().numpy() for n in base}
         xh = {g: xs[g].cpu().numpy() for g in xs}

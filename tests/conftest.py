@@ -8,6 +8,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, os.path.join(ROOT, "tinycoder-inference_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
 GOLDEN = os.path.join(ROOT, "tests", "golden", "golden.npz")
 
 

@@ -362,9 +362,69 @@ int tc_encode(int type, const float *x, void *out, uint32_t rows, uint32_t cols,
     return TC_OK;
 }
 
-int tc_moe_ffn(const float *, const int32_t *, const float *, uint32_t, uint32_t, const void *, const void *,
-               const void *, uint32_t, uint32_t, uint32_t, float *, void *) {
-    return fail(TC_E_UNSUPPORTED, "MoE path not built yet");
+int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t seq_len, uint32_t top_k,
+               const void *wg, const void *wu, const void *wd, uint32_t n_experts, uint32_t hidden, uint32_t ff,
+               float *out, void *stream) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!x || !ids || !wts || !wg || !wu || !wd || !out) return fail(TC_E_ARG, "null pointer");
+    if (seq_len == 0 || top_k == 0 || n_experts == 0) return fail(TC_E_ARG, "empty MoE call");
+    if (hidden % 256 || ff % 256) return fail(TC_E_UNSUPPORTED, "hidden=%u / ff=%u not multiples of 256", hidden, ff);
+    for (const void *p : {wg, wu, wd})
+        if (reinterpret_cast<uintptr_t>(p) & 15) return fail(TC_E_UNSUPPORTED, "weights must be 16-byte aligned");
+    const uint64_t npairs = uint64_t(seq_len) * top_k;
+    if (npairs > (1u << 20)) return fail(TC_E_UNSUPPORTED, "too many (token, rank) pairs");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // Scratch: h and u [pairs][ff], per-pair down outputs [pairs][hidden].
+    const size_t hb = (npairs * ff * 4 + 255) & ~size_t(255);
+    const size_t need = 2 * hb + npairs * hidden * 4;
+    if (!ensure(dev->aux, dev->aux_bytes, need)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", need);
+    float *h = static_cast<float *>(dev->aux);
+    float *u = reinterpret_cast<float *>(static_cast<char *>(dev->aux) + hb);
+    float *y = reinterpret_cast<float *>(static_cast<char *>(dev->aux) + 2 * hb);
+    const uint64_t gstride = uint64_t(ff) * (hidden / 256) * 144;
+    const uint64_t dstride = uint64_t(hidden) * (ff / 256) * 144;
+
+    tc::GemvJob up{};
+    up.W = static_cast<const uint8_t *>(wg);
+    up.W2 = static_cast<const uint8_t *>(wu);
+    up.x = x;
+    up.out = h;
+    up.out2 = u;
+    up.rows = ff;
+    up.cols = hidden;
+    up.out_ld = ff;
+    up.epi = 1;
+    up.ids = ids;
+    up.wstride = gstride;
+    up.npairs = uint32_t(npairs);
+    up.x_div = top_k;
+    up.x_stride = hidden;
+    up.out_stride = ff;
+    up.n_experts = n_experts;
+    hipError_t e = tc::launch_gemv_jobs(TC_Q4_K, 1, &up, 1, dev->num_cu, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE gate/up");
+
+    tc::GemvJob dn{};
+    dn.W = static_cast<const uint8_t *>(wd);
+    dn.x = h;
+    dn.out = y;
+    dn.rows = hidden;
+    dn.cols = ff;
+    dn.out_ld = hidden;
+    dn.ids = ids;
+    dn.wstride = dstride;
+    dn.npairs = uint32_t(npairs);
+    dn.x_div = 1;
+    dn.x_stride = ff;
+    dn.out_stride = hidden;
+    dn.n_experts = n_experts;
+    e = tc::launch_gemv_jobs(TC_Q4_K, 1, &dn, 1, dev->num_cu, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE down");
+
+    e = tc::launch_moe_combine(y, wts, out, seq_len, top_k, hidden, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE combine");
+    return TC_OK;
 }
 
 const char *tc_last_error(void) { return g_err.c_str(); }

@@ -575,6 +575,12 @@ struct TJobDev {
     uint32_t rows_per_wg, wg_begin;
     int epi;
     DivMod nu_div;
+    // Expert-pair mode (ids != null): the job is npairs mat-vecs, pair p using
+    // expert ids[p] (matrix at W + ids[p]*wstride), input x + (p/x_div)*x_stride
+    // and output out + p*out_stride; wg_per_pair workgroups each.
+    const int32_t *ids;
+    uint64_t wstride;
+    uint32_t wg_per_pair, x_div, x_stride, out_stride, n_experts;
 };
 
 struct TLaunchArgs {
@@ -937,11 +943,25 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
 #pragma unroll
     for (int k = 1; k < kMaxJobs; ++k)
         if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
-    const TJobDev jb = L.jobs[j];
+    TJobDev jb = L.jobs[j];
     TC_TRACE_PT(0);
+    uint32_t lw = blockIdx.x - jb.wg_begin;
+    bool no_expert = false;
+    if (jb.ids != nullptr) {
+        const uint32_t p = lw / jb.wg_per_pair;
+        lw -= p * jb.wg_per_pair;
+        const int32_t e = jb.ids[p];
+        no_expert = e < 0 || uint32_t(e) >= jb.n_experts;
+        const uint64_t off = no_expert ? 0 : uint64_t(e) * jb.wstride;
+        jb.W += off;
+        if (jb.W2 != nullptr) jb.W2 += off;
+        jb.x += size_t(p / jb.x_div) * jb.x_stride;
+        jb.out += size_t(p) * jb.out_stride;
+        if (jb.out2 != nullptr) jb.out2 += size_t(p) * jb.out_stride;
+    }
     const uint32_t nu = jb.nu;
     const uint32_t pairs = jb.W2 != nullptr ? 2 : 1;
-    const uint32_t r0 = (blockIdx.x - jb.wg_begin) * jb.rows_per_wg;
+    const uint32_t r0 = lw * jb.rows_per_wg;
     const uint32_t nr = min(jb.rows_per_wg, jb.rows - r0);
     const uint32_t per_mat = nr * nu;
     const uint32_t ntiles_mat = (per_mat + kTileUnits - 1) / kTileUnits;
@@ -1048,10 +1068,12 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         }
         if (o < nout && q == 0) {
             if (pairs == 2) {
+                if (no_expert) u = 0.0f;
                 jb.out2[size_t(s) * jb.out_ld + r0 + rl] = u;
                 if (jb.epi == 1) g = g / (1.0f + expf(-g)) * u;
             }
-            jb.out[size_t(s) * jb.out_ld + r0 + rl] = g;
+            // An out-of-range expert id contributes nothing (the reference skips it).
+            jb.out[size_t(s) * jb.out_ld + r0 + rl] = no_expert ? 0.0f : g;
         }
     }
     TC_TRACE_PT(3);
@@ -1149,7 +1171,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
     uint64_t total_units = 0;
     for (uint32_t j = 0; j < njobs; ++j) {
         maxcols = std::max(maxcols, jobs[j].cols);
-        total_units += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * (jobs[j].W2 ? 2 : 1);
+        total_units += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * (jobs[j].W2 ? 2 : 1) * jobs[j].npairs;
     }
     const uint32_t fixed = tlds_layout<C>(type, S, maxcols, &a);
     if (fixed >= kTLdsBudget) return hipErrorInvalidValue;
@@ -1175,8 +1197,15 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         d.out_ld = g.out_ld;
         d.epi = g.epi;
         d.nu_div = make_divmod(d.nu);
-        const uint64_t units = uint64_t(g.rows) * d.nu * pairs;
-        uint64_t gj = std::max<uint64_t>(1, (want * units + total_units / 2) / total_units);
+        d.ids = g.ids;
+        d.wstride = g.wstride;
+        d.x_div = g.x_div;
+        d.x_stride = g.x_stride;
+        d.out_stride = g.out_stride;
+        d.n_experts = g.n_experts;
+        const uint64_t units = uint64_t(g.rows) * d.nu * pairs * g.npairs;
+        // workgroups per mat-vec (per expert pair in expert-pair mode)
+        uint64_t gj = std::max<uint64_t>(1, (want * units + total_units / 2) / total_units / g.npairs);
         gj = std::min<uint64_t>(gj, g.rows);
         uint32_t rpw = uint32_t((g.rows + gj - 1) / gj);
         const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
@@ -1184,8 +1213,9 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         rpw = std::min(rpw, fit);
         d.rows_per_wg = rpw;
         gj = (g.rows + rpw - 1) / rpw;
+        d.wg_per_pair = uint32_t(gj);
         d.wg_begin = wg;
-        wg += uint32_t(gj);
+        wg += uint32_t(gj) * g.npairs;
         max_part = std::max(max_part, pairs * S * rpw * d.nu * 4);
     }
     const uint32_t lds = fixed + max_part;
@@ -1203,7 +1233,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
 uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs) {
     uint64_t b = 0;
     for (uint32_t j = 0; j < njobs; ++j)
-        b += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * unit_bytes(type) * (jobs[j].W2 ? 2 : 1);
+        b += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * unit_bytes(type) * (jobs[j].W2 ? 2 : 1) * jobs[j].npairs;
     return b;
 }
 
@@ -1253,6 +1283,8 @@ hipError_t launch_gemv_jobs(int type, uint32_t S, const GemvJob *jobs, uint32_t 
             return hipErrorInvalidValue;
     }
     if (type == kQ4_K || type == kQ8_0) return launch_gemv_tiled(type, S, jobs, njobs, num_cu, st);
+    for (uint32_t j = 0; j < njobs; ++j)
+        if (jobs[j].ids != nullptr || jobs[j].npairs != 1) return hipErrorInvalidValue;
     LaunchArgs a{};
     a.njobs = njobs;
     uint32_t maxcols = 0;
@@ -1312,6 +1344,31 @@ hipError_t launch_gemv_jobs(int type, uint32_t S, const GemvJob *jobs, uint32_t 
         case kIQ3_XXS: return launch_typed<kIQ3_XXS>(S, a, wg, lds, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+namespace {
+
+// Rank-order weighted sum of the per-(token, rank) expert outputs
+// (reference ModelMoE.cpp:990-1002: the output starts at 0 and adds
+// w_r * down_r for r = 0..top_k-1 in order).
+__global__ __launch_bounds__(256) void k_moe_combine(const float *__restrict__ y, const float *__restrict__ wts,
+                                                     float *__restrict__ out, uint32_t top_k, uint32_t H) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= H) return;
+    float acc = 0.0f;
+    for (uint32_t r = 0; r < top_k; ++r)
+        acc = fmaf(wts[size_t(t) * top_k + r], y[(size_t(t) * top_k + r) * H + i], acc);
+    out[size_t(t) * H + i] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_moe_combine(const float *y, const float *wts, float *out, uint32_t T, uint32_t top_k, uint32_t H,
+                              hipStream_t st) {
+    if (T == 0 || H == 0) return hipErrorInvalidValue;
+    k_moe_combine<<<dim3{(H + 255) / 256, T, 1u}, 256, 0, st>>>(y, wts, out, top_k, H);
+    return hipGetLastError();
 }
 
 }  // namespace tc

@@ -28,7 +28,18 @@ struct GemvJob {
     int32_t *dbg = nullptr;  // optional per-block integer sums (test hook)
     uint32_t rows = 0, cols = 0, out_ld = 0;
     int epi = 0;
+    // Expert-pair mode (tiled types, fused x only): npairs mat-vecs, pair p
+    // using the matrix at W (and W2) + ids[p]*wstride, input x +
+    // (p/x_div)*x_stride, outputs out (and out2) + p*out_stride. An id outside
+    // [0, n_experts) gives zero outputs.
+    const int32_t *ids = nullptr;
+    uint64_t wstride = 0;
+    uint32_t npairs = 1, x_div = 1, x_stride = 0, out_stride = 0, n_experts = 0;
 };
+
+// out[t][i] = sum over r < top_k, in rank order, of wts[t][r] * y[t*top_k + r][i].
+hipError_t launch_moe_combine(const float *y, const float *wts, float *out, uint32_t T, uint32_t top_k, uint32_t H,
+                              hipStream_t st);
 
 // Up to 8 jobs of one weight type and token count in one launch. Returns
 // hipErrorInvalidValue when a shape does not fit the kernel.
