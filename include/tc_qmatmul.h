@@ -137,6 +137,25 @@ int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t se
                const void *wg, const void *wu, const void *wd, uint32_t n_experts, uint32_t hidden,
                uint32_t ff, float *out, void *stream);
 
+/* Parity hooks over host data (the reference's GPUModel::debugQ8KRow,
+ * debugQ8_0Row, debugQ8KBlocks and debugQ8_0Blocks, include/GPUCompute.hpp:
+ * 399-460, as free functions; GPUModel itself is outside this library).
+ * w_row: one host row of raw blocks; x: host fp32 [cols]; cols % 256 == 0.
+ * *_row: *result = the decode kernel's output for that row.
+ * *_blocks: out_quant = the GPU-quantized activation blocks, block_q8_K
+ * {float d; int8 qs[256]; int16 bsums[16]} (292 B) or {float d; int8 qs[32]}
+ * (36 B) for Q8_0; out_blk[b] = block b's float contribution as the decode
+ * kernel forms it (the kernel run on the row with every other block's scale
+ * zeroed, so those blocks add exactly 0). q8k: Q4_K, Q6_K, IQ3_XXS. */
+int tc_debug_q8k_row(int type, const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
+                     float *result);
+int tc_debug_q8_0_row(const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
+                      float *result);
+int tc_debug_q8k_blocks(int type, const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
+                        float *out_blk, uint8_t *out_quant);
+int tc_debug_q8_0_blocks(const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
+                         float *out_blk, uint8_t *out_quant);
+
 /* Message for the calling thread's last failed call ("" if none). */
 const char *tc_last_error(void);
 

@@ -55,3 +55,36 @@ def test_row_bytes():
     assert lib.tc_row_bytes(14, 18944) == 74 * 210
     assert lib.tc_row_bytes(18, 3584) == 14 * 98
     assert lib.tc_row_bytes(13, 256) == 0
+
+
+def test_reference_interface_header_compiles_and_links(tmp_path):
+    """include/tc_int8gemm.hpp (the reference's tinycoder::gpu interface over
+    the C ABI) compiles as C++17, links against the library, and reports no
+    device and refuses calls cleanly on a machine without a GPU."""
+    import shutil
+    import subprocess
+    import tc_hip
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("no host C++ compiler")
+    lib = tc_hip.load_library()
+    so = lib._name
+    src = tmp_path / "iface.cpp"
+    src.write_text(
+        '#include "tc_int8gemm.hpp"\n'
+        "int main() {\n"
+        "  namespace g = tinycoder::gpu;\n"
+        "  if (g::int8GemmAvailable()) return 2;\n"
+        "  if (g::int8Gemv(12, nullptr, nullptr, nullptr, 1, 1, 256, nullptr)) return 3;\n"
+        "  if (g::int8Gemm(12, nullptr, nullptr, nullptr, 16, 1, 256, 1, nullptr)) return 4;\n"
+        "  if (g::int8GemvDualIQ2XS(nullptr, nullptr, nullptr, nullptr, nullptr, 1, 256, nullptr)) return 5;\n"
+        "  return 0;\n"
+        "}\n")
+    exe = tmp_path / "iface"
+    subprocess.run([gxx, "-std=c++17", "-I", os.path.join(ROOT, "include"), str(src), so,
+                    "-Wl,-rpath," + os.path.dirname(so), "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, timeout=60)
+    assert r.returncode == 0, (r.returncode, r.stderr)

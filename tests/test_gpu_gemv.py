@@ -249,3 +249,59 @@ def test_gemv_prequantized_equals_fused(tc, dev, qt):
     a = tc.gemv_q8(qt, w, act, S, rows, cols).cpu().numpy()
     b = tc.gemv(qt, w, x, rows, cols).cpu().numpy()
     assert np.array_equal(a, b)
+
+
+# ---- parity hooks (reference GPUModel::debugQ8KRow / debugQ8_0Row / debugQ8KBlocks /
+# debugQ8_0Blocks, include/GPUCompute.hpp:399-460) -----------------------------------------------
+
+@pytest.mark.parametrize("qt", ALL)
+def test_debug_row_hook(tc, dev, oracle, qt):
+    rng = np.random.default_rng(400 + qt)
+    cols = 2048
+    w = random_blocks(qt, rng, 3, cols)
+    x = gaussian(rng, (1, cols))
+    rb = row_bytes(qt, cols)
+    full = tc.gemv(qt, to_dev(w, dev), to_dev(x, dev), 3, cols).cpu().numpy()[0]
+    for r in range(3):
+        v = tc.debug_row(qt, w[r * rb:(r + 1) * rb], x)
+        assert np.float32(v) == full[r]  # same kernel, same order
+        ok, worst = close(v, oracle.matmul(qt, w[r * rb:(r + 1) * rb], x, 1, cols)[0, 0])
+        assert ok, worst
+
+
+@pytest.mark.parametrize("qt", ALL)
+def test_debug_blocks_hook(tc, dev, oracle, qt):
+    rng = np.random.default_rng(500 + qt)
+    cols = 1536
+    w = random_blocks(qt, rng, 1, cols)
+    x = gaussian(rng, (1, cols))
+    blk, q = tc.debug_blocks(qt, w, x)
+    bs = O.oc_block_size(qt) if hasattr(O, "oc_block_size") else (32 if qt == Q8_0 else 256)
+    nb = cols // bs
+    # activation blocks: bit-exact against the oracle's quantizer
+    if qt == Q8_0:
+        qs, d = oracle.quantize_q8_0_act(x)
+        rec = q.reshape(nb, 36)
+        assert np.array_equal(rec[:, :4].copy().view(np.float32).ravel().view(np.uint32), d.view(np.uint32))
+        assert np.array_equal(rec[:, 4:].copy().view(np.int8).ravel(), qs)
+    else:
+        qs, d, bsum = oracle.quantize_q8k(x)
+        rec = q.reshape(nb, 292)
+        assert np.array_equal(rec[:, :4].copy().view(np.float32).ravel().view(np.uint32), d.view(np.uint32))
+        assert np.array_equal(rec[:, 4:260].copy().view(np.int8).ravel(), qs)
+        assert np.array_equal(rec[:, 260:].copy().view(np.int16).ravel(), bsum)
+    # each block's contribution: the oracle on the row with every other block zeroed
+    tb = row_bytes(qt, bs)
+    for b in range(nb):
+        wz = w.copy().reshape(nb, tb)
+        for k in range(nb):
+            if k == b:
+                continue
+            if qt == Q4_K:
+                wz[k, :4] = 0
+            elif qt == Q6_K:
+                wz[k, 208:210] = 0
+            else:
+                wz[k, :2] = 0
+        ok, worst = close(blk[b], oracle.matmul(qt, wz.ravel(), x, 1, cols)[0, 0])
+        assert ok, (b, worst)

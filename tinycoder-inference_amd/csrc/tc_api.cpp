@@ -427,6 +427,128 @@ int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t se
     return TC_OK;
 }
 
+// ---- parity hooks (reference GPUModel::debugQ8KRow / debugQ8_0Row /
+// debugQ8KBlocks / debugQ8_0Blocks, include/GPUCompute.hpp:399-460, as free
+// functions over host data) --------------------------------------------------
+
+namespace {
+
+struct DevBuf {
+    void *p = nullptr;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+// Scale fields of one block zeroed: the block then contributes exactly 0 in
+// every kernel (Q4_K d and dmin, Q6_K d, IQ3_XXS d, Q8_0 d).
+void zero_block_scales(int type, uint8_t *blk) {
+    switch (type) {
+        case TC_Q4_K: std::memset(blk, 0, 4); break;
+        case TC_Q6_K: std::memset(blk + 208, 0, 2); break;
+        default: std::memset(blk, 0, 2); break;
+    }
+}
+
+// Row results of `nrows` host rows against one host activation vector.
+int debug_rows(int type, const uint8_t *w_host, uint32_t nrows, const float *x_host, uint32_t cols, float *res) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    const size_t rb = tc_row_bytes(type, cols);
+    DevBuf w, x, o;
+    if (hipMalloc(&w.p, rb * nrows) != hipSuccess || hipMalloc(&x.p, cols * 4) != hipSuccess ||
+        hipMalloc(&o.p, nrows * 4) != hipSuccess)
+        return fail(TC_E_LAUNCH, "hipMalloc failed");
+    if (hipMemcpy(w.p, w_host, rb * nrows, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(x.p, x_host, cols * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(TC_E_LAUNCH, "copy to device failed");
+    int rc = run_gemv(dev, type, w.p, nullptr, static_cast<const float *>(x.p), nullptr, static_cast<float *>(o.p),
+                      nullptr, 0, nullptr, 1, nrows, cols, nullptr);
+    if (rc) return rc;
+    if (hipMemcpy(res, o.p, nrows * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(TC_E_LAUNCH, "copy to host failed");
+    return TC_OK;
+}
+
+// Per-block contributions: row b of a scratch matrix is the input row with
+// every block but b zeroed (unit u = 8 Q8_0 blocks is split the same way).
+int debug_blocks(int type, const uint8_t *w_row, uint32_t nblk, const float *x_host, uint32_t cols, float *out_blk) {
+    const size_t rb = tc_row_bytes(type, cols), bb = tc::block_bytes(type);
+    std::vector<uint8_t> m(rb * nblk);
+    for (uint32_t b = 0; b < nblk; ++b) {
+        uint8_t *row = m.data() + rb * b;
+        std::memcpy(row, w_row, rb);
+        for (uint32_t k = 0; k < nblk; ++k)
+            if (k != b) zero_block_scales(type, row + bb * k);
+    }
+    return debug_rows(type, m.data(), nblk, x_host, cols, out_blk);
+}
+
+int debug_quant(int type, const float *x_host, uint32_t cols, uint8_t *out_quant) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    const tc::ActLayout L = tc::act_layout(type, 1, cols);
+    DevBuf x, a;
+    if (hipMalloc(&x.p, cols * 4) != hipSuccess || hipMalloc(&a.p, L.bytes) != hipSuccess)
+        return fail(TC_E_LAUNCH, "hipMalloc failed");
+    if (hipMemcpy(x.p, x_host, cols * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(TC_E_LAUNCH, "copy to device failed");
+    hipError_t e = tc::launch_quant_act(type, static_cast<const float *>(x.p), 1, cols, L, a.p, nullptr);
+    if (e != hipSuccess) return hip_fail(e, "activation quantizer");
+    std::vector<uint8_t> h(L.bytes);
+    if (hipMemcpy(h.data(), a.p, L.bytes, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(TC_E_LAUNCH, "copy to host failed");
+    const int8_t *qs = reinterpret_cast<const int8_t *>(h.data() + L.qs_off);
+    const float *d = reinterpret_cast<const float *>(h.data() + L.d_off);
+    const int16_t *bs = reinterpret_cast<const int16_t *>(h.data() + L.bs_off);
+    if (type == TC_Q8_0) {
+        for (uint32_t b = 0; b < cols / 32; ++b) {  // {float d; int8 qs[32]}
+            std::memcpy(out_quant + 36 * b, d + b, 4);
+            std::memcpy(out_quant + 36 * b + 4, qs + 32 * b, 32);
+        }
+    } else {
+        for (uint32_t b = 0; b < cols / 256; ++b) {  // block_q8_K {float d; int8 qs[256]; int16 bsums[16]}
+            std::memcpy(out_quant + 292 * b, d + b, 4);
+            std::memcpy(out_quant + 292 * b + 4, qs + 256 * b, 256);
+            std::memcpy(out_quant + 292 * b + 260, bs + 16 * b, 32);
+        }
+    }
+    return TC_OK;
+}
+
+}  // namespace
+
+int tc_debug_q8k_row(int type, const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
+                     float *result) {
+    if (type == TC_Q8_0 || !type_ok(type)) return fail(TC_E_UNSUPPORTED, "type %d is not a Q8_K-activation type", type);
+    if (!w_row || !x || !result) return fail(TC_E_ARG, "null pointer");
+    if (cols % 256 || blocks_per_row != cols / 256) return fail(TC_E_ARG, "blocks_per_row/cols mismatch");
+    return debug_rows(type, w_row, 1, x, cols, result);
+}
+
+int tc_debug_q8_0_row(const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols, float *result) {
+    if (!w_row || !x || !result) return fail(TC_E_ARG, "null pointer");
+    if (cols % 256 || blocks_per_row != cols / 32) return fail(TC_E_ARG, "blocks_per_row/cols mismatch");
+    return debug_rows(TC_Q8_0, w_row, 1, x, cols, result);
+}
+
+int tc_debug_q8k_blocks(int type, const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
+                        float *out_blk, uint8_t *out_quant) {
+    if (type == TC_Q8_0 || !type_ok(type)) return fail(TC_E_UNSUPPORTED, "type %d is not a Q8_K-activation type", type);
+    if (!w_row || !x || !out_blk || !out_quant) return fail(TC_E_ARG, "null pointer");
+    if (cols % 256 || blocks_per_row != cols / 256) return fail(TC_E_ARG, "blocks_per_row/cols mismatch");
+    int rc = debug_quant(type, x, cols, out_quant);
+    return rc ? rc : debug_blocks(type, w_row, blocks_per_row, x, cols, out_blk);
+}
+
+int tc_debug_q8_0_blocks(const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
+                         float *out_blk, uint8_t *out_quant) {
+    if (!w_row || !x || !out_blk || !out_quant) return fail(TC_E_ARG, "null pointer");
+    if (cols % 256 || blocks_per_row != cols / 32) return fail(TC_E_ARG, "blocks_per_row/cols mismatch");
+    int rc = debug_quant(TC_Q8_0, x, cols, out_quant);
+    return rc ? rc : debug_blocks(TC_Q8_0, w_row, blocks_per_row, x, cols, out_blk);
+}
+
 const char *tc_last_error(void) { return g_err.c_str(); }
 
 }  // extern "C"

@@ -37,6 +37,10 @@ SIGNATURES = {
     "tc_encode": (_I, [_I, _P, _P, _U32, _U32, _P]),
     "tc_row_bytes": (ctypes.c_size_t, [_I, _U32]),
     "tc_moe_ffn": (_I, [_P, _P, _P, _U32, _U32, _P, _P, _P, _U32, _U32, _U32, _P, _P]),
+    "tc_debug_q8k_row": (_I, [_I, _P, _U32, _P, _U32, _P]),
+    "tc_debug_q8_0_row": (_I, [_P, _U32, _P, _U32, _P]),
+    "tc_debug_q8k_blocks": (_I, [_I, _P, _U32, _P, _U32, _P, _P]),
+    "tc_debug_q8_0_blocks": (_I, [_P, _U32, _P, _U32, _P, _P]),
     "tc_last_error": (ctypes.c_char_p, []),
 }
 
@@ -178,6 +182,39 @@ class Library:
         out = torch.empty(rows * row_bytes(qtype, cols), dtype=torch.uint8, device=x.device)
         self._check(self.lib.tc_encode(qtype, _ptr(x), _ptr(out), rows, cols, self._stream()))
         return out
+
+    def debug_row(self, qtype, w_row, x):
+        """Host numpy row + host x -> the decode kernel's row result."""
+        import numpy as np
+        w_row = np.ascontiguousarray(w_row, np.uint8)
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        res = np.zeros(1, np.float32)
+        cols = x.size
+        if qtype == Q8_0:
+            self._check(self.lib.tc_debug_q8_0_row(w_row.ctypes.data, cols // 32, x.ctypes.data, cols,
+                                                   res.ctypes.data))
+        else:
+            self._check(self.lib.tc_debug_q8k_row(qtype, w_row.ctypes.data, cols // 256, x.ctypes.data, cols,
+                                                  res.ctypes.data))
+        return float(res[0])
+
+    def debug_blocks(self, qtype, w_row, x):
+        """-> (per-block float contributions, quantized activation block bytes)."""
+        import numpy as np
+        w_row = np.ascontiguousarray(w_row, np.uint8)
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        cols = x.size
+        if qtype == Q8_0:
+            nb = cols // 32
+            blk, q = np.zeros(nb, np.float32), np.zeros(nb * 36, np.uint8)
+            self._check(self.lib.tc_debug_q8_0_blocks(w_row.ctypes.data, nb, x.ctypes.data, cols, blk.ctypes.data,
+                                                      q.ctypes.data))
+        else:
+            nb = cols // 256
+            blk, q = np.zeros(nb, np.float32), np.zeros(nb * 292, np.uint8)
+            self._check(self.lib.tc_debug_q8k_blocks(qtype, w_row.ctypes.data, nb, x.ctypes.data, cols,
+                                                     blk.ctypes.data, q.ctypes.data))
+        return blk, q
 
     def moe_ffn(self, x, ids, wts, wg, wu, wd, n_experts, hidden, ff, out=None):
         import torch
