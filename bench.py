@@ -139,6 +139,99 @@ def gemm_bench(torch, tc, tc_hip, dev, reps):
     return res
 
 
+def timed(torch, fn, n):
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    fn(0)
+    torch.cuda.synchronize()
+    a.record()
+    for i in range(n):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / n
+
+
+def other_decode_bench(torch, tc, tc_hip, dev, reps):
+    """BASELINE configs #1 and #3 (batch-1 decode mat-vecs of other formats):
+    weights N(0,0.02) through the GPU encoders, rotating copies so that every
+    working set exceeds the 256 MB Infinity Cache."""
+    gen = torch.Generator(device=dev).manual_seed(11)
+    rb = tc_hip.row_bytes
+    cases = [("cfg1 Q8_0 4096x4096", tc_hip.Q8_0, 4096, 4096, False, 16),
+             ("cfg3 Q6_K LM head 152064x3584", tc_hip.Q6_K, 152064, 3584, False, 1),
+             ("cfg3 Q6_K down 3584x18944", tc_hip.Q6_K, 3584, 18944, False, 6),
+             ("cfg3 IQ3_XXS gate/up pair 18944x3584 (SwiGLU)", tc_hip.IQ3_XXS, 18944, 3584, True, 6)]
+    res = []
+    for name, qt, rows, cols, dual, ncopy in cases:
+        mats = 2 if dual else 1
+        ws = []
+        for _ in range(mats):
+            wf = torch.randn((rows, cols), generator=gen, device=dev) * 0.02
+            ws.append(tc.encode(qt, wf))
+            del wf
+        copies = [[w if c == 0 else w.clone() for w in ws] for c in range(ncopy)]
+        x = torch.randn((1, cols), generator=gen, device=dev)
+        out = torch.empty((1, rows), device=dev)
+        out2 = torch.empty((1, rows), device=dev)
+
+        def fn(i):
+            c = copies[i % ncopy]
+            if dual:
+                tc.lib.tc_gemv_dual(qt, tc_hip._ptr(c[0]), tc_hip._ptr(c[1]), tc_hip._ptr(x), tc_hip._ptr(out),
+                                    tc_hip._ptr(out2), rows, cols, tc._stream())
+            else:
+                tc.gemv(qt, c[0], x, rows, cols, out=out)
+
+        us = timed(torch, fn, reps)
+        by = mats * rows * rb(qt, cols) + 4 * cols + 4 * rows * mats
+        res.append({"config": name, "us": round(us, 2), "bytes": by, "GB/s": round(by / us / 1e3, 1),
+                    "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4)})
+        del copies, ws
+        torch.cuda.empty_cache()
+    return res
+
+
+def moe_bench(torch, tc, tc_hip, dev, reps):
+    """BASELINE config #5: 128 Q4_K experts (gate/up 768x2048, down 2048x768,
+    W ~ N(0,0.02) through the reference Q4_K quantizer), top-8 routing uniform
+    without replacement, softmax(N(0,1)) weights, batch 1 and 16. A fresh
+    routing per repetition (so a repeated expert set cannot sit in the
+    Infinity Cache); bytes = distinct experts of that routing x 2,654,208."""
+    E, K, H, FF = 128, 8, 2048, 768
+    gen = torch.Generator(device=dev).manual_seed(13)
+
+    def enc(r, c):
+        return tc.encode(tc_hip.Q4_K, torch.randn((r, c), generator=gen, device=dev) * 0.02)
+
+    wg, wu, wd = enc(E * FF, H), enc(E * FF, H), enc(E * H, FF)
+    per_expert = 3 * FF * (H // 256) * 144
+    rng = np.random.default_rng(17)
+    res = []
+    for T in (1, 16):
+        ids_l, wts_l, nbytes = [], [], []
+        for _ in range(reps):
+            ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+            lg = rng.standard_normal((T, K)).astype(np.float32)
+            w = np.exp(lg) / np.exp(lg).sum(1, keepdims=True)
+            ids_l.append(torch.from_numpy(ids).to(dev))
+            wts_l.append(torch.from_numpy(w.astype(np.float32)).to(dev))
+            nbytes.append(len(np.unique(ids)) * per_expert)
+        x = torch.randn((T, H), generator=gen, device=dev)
+        out = torch.empty((T, H), device=dev)
+
+        def fn(i):
+            tc.moe_ffn(x, ids_l[i % reps], wts_l[i % reps], wg, wu, wd, E, H, FF, out=out)
+
+        us = timed(torch, fn, reps)
+        by = float(np.mean(nbytes)) + 4 * T * H * 2
+        res.append({"batch": T, "us": round(us, 2), "bytes": int(by), "GB/s": round(by / us / 1e3, 1),
+                    "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4), "launches": 3})
+    del wg, wu, wd
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +239,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
+    ap.add_argument("--no-other", action="store_true", help="skip the other-format decode and MoE legs")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="counter-collection run: a 256 MiB device copy (the calibration kernel of known "
                          "traffic), then --steps passes over the layer's launches; prints nothing else")
@@ -298,6 +392,9 @@ def main():
         "layer_one_launch": {"us": round(one_launch_ms * 1e3, 2), "GB/s": round(one_launch_gbs, 1),
                              "frac": round(one_launch_gbs / HBM_PEAK_GBS, 4)},
     }
+    if not args.no_other:
+        line["decode_other_formats"] = other_decode_bench(torch, tc, tc_hip, dev, max(20, args.steps // 2))
+        line["moe"] = moe_bench(torch, tc, tc_hip, dev, max(20, args.steps // 2))
     if not args.no_gemm:
         del copies
         torch.cuda.empty_cache()
