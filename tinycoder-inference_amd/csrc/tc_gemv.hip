@@ -554,10 +554,10 @@ __host__ __device__ constexpr int tile_depth(int type, int S) {
 }
 
 #ifdef TC_TRACE
-__device__ unsigned long long g_trace[8192 * 4];
+__device__ unsigned long long g_trace[8192 * 8];
 #define TC_TRACE_PT(k)                                                                                       \
     do {                                                                                                    \
-        if (threadIdx.x == 0 && blockIdx.x < 8192) g_trace[blockIdx.x * 4 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+        if (threadIdx.x == 0 && blockIdx.x < 8192) g_trace[blockIdx.x * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define TC_TRACE_PT(k) \
@@ -691,16 +691,33 @@ template <int TYPE, int S, int TNT>
 __device__ __forceinline__ XPre tstage_preload(const TJobDev &jb, const XRsrc &rs) {
     XPre p;
     const uint32_t tid = threadIdx.x;
-    const bool fused = jb.x != nullptr;
-    static_for<0, kXSlots>([&](auto sl) __attribute__((always_inline)) {
-        constexpr int s = decltype(sl)::value;
-        const uint32_t off_f = s < 4 * kXPre ? (tid + (s / 4) * TNT) * 64u + 16u * (s % 4) : 0x80000000u;
-        uint32_t off_q = 0x80000000u;
-        if constexpr (s < kXPreQ) off_q = (tid + s * TNT) * 16u;
-        if constexpr (s == kXPreQ || s == kXPreQ + 1) off_q = tid * 16u;
-        const __amdgpu_buffer_rsrc_t r = fused ? rs.a : (s < kXPreQ ? rs.a : (s == kXPreQ ? rs.b : rs.c));
-        reg<s>(p.r) = __builtin_amdgcn_raw_buffer_load_b128(r, fused ? off_f : off_q, 0, 0);
-    });
+    const uint32_t wbase = __builtin_amdgcn_readfirstlane(tid & ~63u);  // first thread of this wave
+    const uint32_t nblk = S * (jb.cols / 256);
+    // Every load instruction costs the CU's address unit ~16 cycles whatever
+    // its lanes read, so a wave issues only the slots that hold some of its
+    // data (wave-uniform tests); the others stay zero.
+    static_for<0, kXSlots>([&](auto sl) __attribute__((always_inline)) { reg<decltype(sl)::value>(p.r) = u32x4{0, 0, 0, 0}; });
+    if (jb.x != nullptr) {
+        static_for<0, kXPre>([&](auto g) __attribute__((always_inline)) {
+            constexpr int G = decltype(g)::value;
+            if (wbase + G * TNT < nblk * 16) {
+                const uint32_t off = (tid + G * TNT) * 64u;
+                static_for<0, 4>([&](auto q) __attribute__((always_inline)) {
+                    reg<4 * G + decltype(q)::value>(p.r) =
+                        __builtin_amdgcn_raw_buffer_load_b128(rs.a, off + 16u * decltype(q)::value, 0, 0);
+                });
+            }
+        });
+    } else {
+        static_for<0, kXPreQ>([&](auto g) __attribute__((always_inline)) {
+            constexpr int G = decltype(g)::value;
+            if (wbase + G * TNT < nblk * 16)
+                reg<G>(p.r) = __builtin_amdgcn_raw_buffer_load_b128(rs.a, (tid + G * TNT) * 16u, 0, 0);
+        });
+        if (4 * wbase < nblk * 8) reg<kXPreQ>(p.r) = __builtin_amdgcn_raw_buffer_load_b128(rs.b, tid * 16u, 0, 0);
+        if constexpr (TYPE != kQ8_0)
+            if (4 * wbase < nblk) reg<kXPreQ + 1>(p.r) = __builtin_amdgcn_raw_buffer_load_b128(rs.c, tid * 16u, 0, 0);
+    }
     return p;
 }
 
@@ -945,6 +962,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
     TJobDev jb = L.jobs[j];
     TC_TRACE_PT(0);
+#ifdef TC_TRACE
+    if (threadIdx.x == TNT - 64 && blockIdx.x < 8192) g_trace[blockIdx.x * 8 + 7] = __builtin_amdgcn_s_memrealtime();
+#endif
     uint32_t lw = blockIdx.x - jb.wg_begin;
     bool no_expert = false;
     if (jb.ids != nullptr) {
@@ -1008,7 +1028,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     // depth then keeps HBM busy for the rest of the stream.
     constexpr int D0 = 1;
     static_for<0, D0>([&](auto i) __attribute__((always_inline)) { ld(i, wave + i.value * TNW); });
+    TC_TRACE_PT(4);
     tstage_finish<TYPE, S, TNT>(jb, xrs, xp, xr);
+    TC_TRACE_PT(5);
     static_for<D0, D>([&](auto i) __attribute__((always_inline)) { ld(i, wave + i.value * TNW); });
     __syncthreads();
     TC_TRACE_PT(1);
@@ -1023,6 +1045,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
 #endif
 
     for (uint32_t k0 = 0; k0 < nmine; k0 += D) {
+#ifdef TC_TRACE
+        if (k0 == D) TC_TRACE_PT(6);
+#endif
         static_for<0, D>([&](auto i) __attribute__((always_inline)) {
             const uint32_t kk = k0 + i.value;
             const uint32_t t = wave + kk * TNW;
