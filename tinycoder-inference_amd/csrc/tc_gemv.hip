@@ -543,7 +543,10 @@ constexpr int kTileUnits = 64;
 constexpr uint32_t XB = 304;                // LDS bytes per 256-element activation block
 constexpr uint32_t XB_BS = 256, XB_D = 288;  // bsums and d offsets inside a record
 
-__host__ __device__ constexpr int tile_dwordx4(int type) { return unit_bytes(type) * kTileUnits / 1024; }
+// 16-byte loads per lane per tile (the last one partial for Q6_K / IQ3_XXS,
+// whose 64-unit tiles are 13440 / 6272 bytes) and the LDS bytes of one tile.
+__host__ __device__ constexpr int tile_dwordx4(int type) { return (unit_bytes(type) * kTileUnits + 1023) / 1024; }
+__host__ __device__ constexpr int tile_slot_bytes(int type) { return tile_dwordx4(type) * 1024; }
 template <class C>
 __host__ __device__ constexpr int tile_depth(int type, int S) {
     // Register slots in flight per wave: fewer where the accumulators of S
@@ -586,7 +589,7 @@ struct TJobDev {
 struct TLaunchArgs {
     TJobDev jobs[kMaxJobs];
     uint32_t njobs;
-    uint32_t off_t, off_p;  // LDS: activation records at 0, wave tiles, partials
+    uint32_t off_t, off_p, off_g;  // LDS: activation records at 0, wave tiles, partials, IQ3_XXS grid
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -941,6 +944,120 @@ struct TDot<kQ8_0, S> {
     }
 };
 
+// Q6_K, one unit (210 B, 2-byte aligned in LDS) per lane: 6-bit weights q
+// (ql low nibbles | qh 2-bit highs), isum = sum_g sc_g * (sum_16 q*x -
+// 32*bsum_g) exactly (the -32 folded through the bsums as the reference does,
+// SIMDMatMulVecAVX2.cpp:4636-4667); value = (d*d8) * isum.
+template <int S>
+struct TDot<kQ6_K, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        const u32x4 scv = lds128(u + 192);
+        const int8_t *sc = reinterpret_cast<const int8_t *>(u + 192);
+        (void)scv;
+        int tot[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) tot[s] = 0;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {  // 16-element halves of each 32-run
+                const u32x4 la = lds128(u + 64 * n + 16 * h), lb = lds128(u + 64 * n + 32 + 16 * h);
+                const u32x4 hv = lds128(u + 128 + 32 * n + 16 * h);
+                const uint32_t LA[4] = {la.x, la.y, la.z, la.w}, LB[4] = {lb.x, lb.y, lb.z, lb.w};
+                const uint32_t HV[4] = {hv.x, hv.y, hv.z, hv.w};
+                uint32_t q[4][4];  // [k][dword]: elements 128n + 32k + 16h + 4j
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    q[0][j] = (LA[j] & 0x0F0F0F0Fu) | ((HV[j] << 4) & 0x30303030u);
+                    q[1][j] = (LB[j] & 0x0F0F0F0Fu) | ((HV[j] << 2) & 0x30303030u);
+                    q[2][j] = ((LA[j] >> 4) & 0x0F0F0F0Fu) | (HV[j] & 0x30303030u);
+                    q[3][j] = ((LB[j] >> 4) & 0x0F0F0F0Fu) | ((HV[j] >> 2) & 0x30303030u);
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const unsigned char *xr = xr0 + s * xtok;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int g = 8 * n + 2 * k + h;  // sub-block of 16
+                        const u32x4 xv = lds128(xr + 128 * n + 32 * k + 16 * h);
+                        int p = sdot4(int(q[k][0]), int(xv.x), 0);
+                        p = sdot4(int(q[k][1]), int(xv.y), p);
+                        p = sdot4(int(q[k][2]), int(xv.z), p);
+                        p = sdot4(int(q[k][3]), int(xv.w), p);
+                        const int bs = int(reinterpret_cast<const int16_t *>(xr + XB_BS)[g]);
+                        tot[s] += int(sc[g]) * (p - 32 * bs);
+                    }
+                }
+            }
+        }
+        const float d = h2f(uint32_t(u[208]) | (uint32_t(u[209]) << 8));
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (dbg) dbg[s * dbg_tok] = tot[s];
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = (d * d8) * float(tot[s]);
+        }
+    }
+};
+
+// IQ3_XXS, one unit (98 B, 2-byte aligned in LDS) per lane: per 32-run ib,
+// 8 grid indices (4 bytes of magnitudes each, codebook in LDS) and 4 7-bit
+// sign indices (sign byte = idx | parity(idx) << 7) in aux = sas[ib], scale
+// 2*(aux >> 28) + 1; isum = sum_ib (2ls+1) * sum_32 w*x; value = (d*d8) *
+// isum, and the row is scaled by 0.25 at the end (reference
+// include/GGMLDequantize.hpp:2064-2097, :2148).
+template <int S>
+struct TDot<kIQ3_XXS, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               const uint32_t *grid, float *val, int32_t *dbg, size_t dbg_tok) {
+        const uint16_t *u16 = reinterpret_cast<const uint16_t *>(u);
+        int tot[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) tot[s] = 0;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            const uint32_t aux = uint32_t(u16[33 + 2 * ib]) | (uint32_t(u16[34 + 2 * ib]) << 16);
+            const uint32_t gi0 = uint32_t(u16[1 + 4 * ib]) | (uint32_t(u16[2 + 4 * ib]) << 16);
+            const uint32_t gi1 = uint32_t(u16[3 + 4 * ib]) | (uint32_t(u16[4 + 4 * ib]) << 16);
+            uint32_t w[8];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t idx7 = (aux >> (7 * l)) & 127u;
+                const uint32_t s8 = idx7 | ((__builtin_popcount(idx7) & 1u) << 7);
+                const uint32_t gw = l < 2 ? gi0 : gi1;
+                const uint32_t g1 = grid[(gw >> (16 * (l & 1))) & 0xFF];
+                const uint32_t g2 = grid[(gw >> (16 * (l & 1) + 8)) & 0xFF];
+                const uint32_t m1 = spread_sign4(s8 & 15u), m2 = spread_sign4(s8 >> 4);
+                w[2 * l] = (g1 ^ m1) + (m1 & 0x01010101u);  // grid bytes are nonzero: no carries
+                w[2 * l + 1] = (g2 ^ m2) + (m2 & 0x01010101u);
+            }
+            const int mult = 2 * int(aux >> 28) + 1;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const unsigned char *xr = xr0 + s * xtok + 32 * ib;
+                const u32x4 x0 = lds128(xr), x1 = lds128(xr + 16);
+                int p = sdot4(int(w[0]), int(x0.x), 0);
+                p = sdot4(int(w[1]), int(x0.y), p);
+                p = sdot4(int(w[2]), int(x0.z), p);
+                p = sdot4(int(w[3]), int(x0.w), p);
+                p = sdot4(int(w[4]), int(x1.x), p);
+                p = sdot4(int(w[5]), int(x1.y), p);
+                p = sdot4(int(w[6]), int(x1.z), p);
+                p = sdot4(int(w[7]), int(x1.w), p);
+                tot[s] += mult * p;
+            }
+        }
+        const float d = h2f(u16[0]);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (dbg) dbg[s * dbg_tok] = tot[s];
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = (d * d8) * float(tot[s]);
+        }
+    }
+};
+
 template <int TYPE, int S, bool DBG, class C>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
@@ -953,7 +1070,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     // The wave index is read as a scalar so that the tile schedule, the
     // descriptor choice and the buffer offsets stay in SGPRs.
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    unsigned char *tile = smem + L.off_t + wave * TILE_BYTES;
+    unsigned char *tile = smem + L.off_t + wave * tile_slot_bytes(TYPE);
     float *spart = reinterpret_cast<float *>(smem + L.off_p);
 
     uint32_t j = 0;
@@ -1011,14 +1128,22 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     __builtin_amdgcn_s_barrier();
 #endif
     Regs<D * NX> buf;
+    // Loads past the workgroup's tiles (the ring's last refills) and lanes
+    // past a partial tile's end carry a per-lane offset beyond the descriptor's
+    // range: they return zeros and touch no memory. (The range check covers
+    // the per-lane offset, so the marker goes there, not in the scalar offset.)
     auto ld = [&](auto i, uint32_t t) __attribute__((always_inline)) {
         const bool second = t >= ntiles_mat;
         const uint32_t tt = second ? t - ntiles_mat : t;
-        const uint32_t soff = t < ntiles ? tt * TILE_BYTES : 0x40000000u;
+        const bool live = t < ntiles;
+        const uint32_t soff = live ? tt * TILE_BYTES : 0u;
+        const uint32_t vbase = live ? lane * 16 : 0x80000000u;
         const __amdgpu_buffer_rsrc_t rs = second ? rs2 : rs1;
         static_for<0, NX>([&](auto c) __attribute__((always_inline)) {
-            reg<decltype(i)::value * NX + c.value>(buf) =
-                __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + c.value * 1024, soff, 0);
+            uint32_t voff = vbase + c.value * 1024;
+            if constexpr (c.value == NX - 1 && TILE_BYTES % 1024 != 0)
+                voff = lane * 16 + c.value * 1024 < TILE_BYTES ? voff : 0x80000000u;
+            reg<decltype(i)::value * NX + c.value>(buf) = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
         });
     };
     // Staged ring: D0 slots are requested before the activations are
@@ -1028,6 +1153,9 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     // depth then keeps HBM busy for the rest of the stream.
     constexpr int D0 = 1;
     static_for<0, D0>([&](auto i) __attribute__((always_inline)) { ld(i, wave + i.value * TNW); });
+    if constexpr (TYPE == kIQ3_XXS) {
+        if (tid < 256) reinterpret_cast<uint32_t *>(smem + L.off_g)[tid] = c_grid[tid];
+    }
     TC_TRACE_PT(4);
     tstage_finish<TYPE, S, TNT>(jb, xrs, xp, xr);
     TC_TRACE_PT(5);
@@ -1065,7 +1193,11 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
                     if constexpr (DBG)
                         dbg = jb.dbg + (size_t(r0 + rl) * nbr + (TYPE == kQ8_0 ? size_t(b) * 8 : b)) * per;
                     float val[S];
-                    TDot<TYPE, S>::run(tile + lane * UB, xr + size_t(b) * XB, xtok, val, dbg, dbg_tok);
+                    if constexpr (TYPE == kIQ3_XXS)
+                        TDot<TYPE, S>::run(tile + lane * UB, xr + size_t(b) * XB, xtok,
+                                           reinterpret_cast<const uint32_t *>(smem + L.off_g), val, dbg, dbg_tok);
+                    else
+                        TDot<TYPE, S>::run(tile + lane * UB, xr + size_t(b) * XB, xtok, val, dbg, dbg_tok);
 #pragma unroll
                     for (int s = 0; s < S; ++s) spart[((size_t(m) * S + s) * nr + rl) * nu + b] = val[s];
                 }
@@ -1090,6 +1222,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
             const float *pu = spart + ((size_t(S) + s) * nr + rl) * nu;
             for (uint32_t bb = q; bb < nu; bb += 4) u += pu[bb];
             u = quad_sum(u);
+        }
+        if constexpr (TYPE == kIQ3_XXS) {
+            g = 0.25f * g;
+            u = 0.25f * u;
         }
         if (o < nout && q == 0) {
             if (pairs == 2) {
@@ -1179,13 +1315,17 @@ constexpr uint64_t kBigBytes = 24ull << 20;
 template <class C>
 uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     uint32_t o = S * (cols / 256) * XB;
+    a->off_g = o;
+    if (type == kIQ3_XXS) o += 1024;
     a->off_t = o;
-    o += (C::NT / 64) * kTileUnits * unit_bytes(type);
+    o += (C::NT / 64) * tile_slot_bytes(type);
     a->off_p = o;
     return o;
 }
 
-bool use_big(int type, uint64_t weight_bytes) { return type == kQ4_K && weight_bytes >= kBigBytes; }
+bool tiled_type(int type) { return type == kQ4_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+
+bool use_big(int type, uint64_t weight_bytes) { return type != kQ8_0 && weight_bytes >= kBigBytes; }
 
 template <class C>
 hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32_t njobs, int num_cu,
@@ -1236,6 +1376,14 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
         if (fit == 0) return hipErrorInvalidValue;
         rpw = std::min(rpw, fit);
+        // Q6_K / IQ3_XXS rows are not 16-byte multiples: 8-row groups keep
+        // every workgroup's first row 16-byte aligned (8*210 and 8*98 bytes
+        // per 256 columns are multiples of 16).
+        if ((type == kQ6_K || type == kIQ3_XXS) && rpw < g.rows) {
+            rpw = (rpw + 7) / 8 * 8;
+            if (rpw > fit) rpw = fit / 8 * 8;
+            if (rpw == 0) return hipErrorInvalidValue;
+        }
         d.rows_per_wg = rpw;
         gj = (g.rows + rpw - 1) / rpw;
         d.wg_per_pair = uint32_t(gj);
@@ -1246,6 +1394,8 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
     const uint32_t lds = fixed + max_part;
     switch (type) {
         case kQ4_K: return launch_tiled<kQ4_K, C>(S, a, wg, lds, st);
+        case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
+        case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:
             if constexpr (C::NT == CfgSmall::NT) return launch_tiled<kQ8_0, C>(S, a, wg, lds, st);
             return hipErrorInvalidValue;
@@ -1275,17 +1425,18 @@ hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t
 
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes) {
     // S*cols up to which the tiled kernels preload all of x ahead of the weights
-    if (type != kQ4_K && type != kQ8_0) return 0xFFFFFFFFu;
+    if (!tiled_type(type)) return 0xFFFFFFFFu;
     return uint32_t(kXPre) * (use_big(type, weight_bytes) ? CfgBig::NT : CfgSmall::NT) * 16u;
 }
 
 uint32_t gemv_max_tokens(int type, uint32_t cols) {
     uint32_t best = 0;
-    if (type == kQ4_K || type == kQ8_0) {
+    if (tiled_type(type)) {
         for (uint32_t S = 1; S <= 8; ++S) {
             TLaunchArgs a;
             const uint32_t f = std::max(tlds_layout<CfgBig>(type, S, cols, &a), tlds_layout<CfgSmall>(type, S, cols, &a));
-            if ((type == kQ4_K ? f : tlds_layout<CfgSmall>(type, S, cols, &a)) + 2 * S * (cols / 256) * 4 <= kTLdsBudget)
+            if ((type != kQ8_0 ? f : tlds_layout<CfgSmall>(type, S, cols, &a)) + 2 * 8 * S * (cols / 256) * 4 <=
+                kTLdsBudget)
                 best = S;
         }
         return best;
@@ -1307,7 +1458,7 @@ hipError_t launch_gemv_jobs(int type, uint32_t S, const GemvJob *jobs, uint32_t 
         if ((reinterpret_cast<uintptr_t>(g.W) & 15) || (g.W2 && (reinterpret_cast<uintptr_t>(g.W2) & 15)))
             return hipErrorInvalidValue;
     }
-    if (type == kQ4_K || type == kQ8_0) return launch_gemv_tiled(type, S, jobs, njobs, num_cu, st);
+    if (tiled_type(type)) return launch_gemv_tiled(type, S, jobs, njobs, num_cu, st);
     for (uint32_t j = 0; j < njobs; ++j)
         if (jobs[j].ids != nullptr || jobs[j].npairs != 1) return hipErrorInvalidValue;
     LaunchArgs a{};
