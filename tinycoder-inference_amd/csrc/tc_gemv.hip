@@ -1108,8 +1108,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     const size_t dbg_tok = size_t(jb.rows) * nbr * per;
     const size_t xtok = size_t(nu) * XB;
     // Descriptors over exactly this workgroup's rows of each matrix.
-    const __amdgpu_buffer_rsrc_t rs1 = make_rsrc(jb.W + size_t(r0) * nu * UB, per_mat * UB);
-    const __amdgpu_buffer_rsrc_t rs2 = make_rsrc((pairs == 2 ? jb.W2 : jb.W) + size_t(r0) * nu * UB, per_mat * UB);
+    const uint8_t *const wbase1 = jb.W + size_t(r0) * nu * UB;
+    const uint8_t *const wbase2 = (pairs == 2 ? jb.W2 : jb.W) + size_t(r0) * nu * UB;
 
 
     // Register ring: the wave's tiles are t = wave, wave+TNW, ...; slot i holds
@@ -1128,21 +1128,20 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     __builtin_amdgcn_s_barrier();
 #endif
     Regs<D * NX> buf;
-    // Loads past the workgroup's tiles (the ring's last refills) and lanes
-    // past a partial tile's end carry a per-lane offset beyond the descriptor's
-    // range: they return zeros and touch no memory. (The range check covers
-    // the per-lane offset, so the marker goes there, not in the scalar offset.)
+    // Loads past the workgroup's tiles (the ring's last refills) go through a
+    // descriptor of size 0, and lanes past a partial tile's end carry a
+    // per-lane offset beyond the range: both return zeros and touch no memory.
+    // (The range check covers the per-lane offset, not the scalar one, so the
+    // scalar offset never carries an out-of-range marker.)
     auto ld = [&](auto i, uint32_t t) __attribute__((always_inline)) {
         const bool second = t >= ntiles_mat;
         const uint32_t tt = second ? t - ntiles_mat : t;
         const bool live = t < ntiles;
         const uint32_t soff = live ? tt * TILE_BYTES : 0u;
-        const uint32_t vbase = live ? lane * 16 : 0x80000000u;
-        const __amdgpu_buffer_rsrc_t rs = second ? rs2 : rs1;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(second ? wbase2 : wbase1, live ? per_mat * UB : 0u);
         static_for<0, NX>([&](auto c) __attribute__((always_inline)) {
-            uint32_t voff = vbase + c.value * 1024;
-            if constexpr (c.value == NX - 1 && TILE_BYTES % 1024 != 0)
-                voff = lane * 16 + c.value * 1024 < TILE_BYTES ? voff : 0x80000000u;
+            uint32_t voff = lane * 16 + c.value * 1024;
+            if constexpr (c.value == NX - 1 && TILE_BYTES % 1024 != 0) voff = voff < TILE_BYTES ? voff : 0x80000000u;
             reg<decltype(i)::value * NX + c.value>(buf) = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
         });
     };
