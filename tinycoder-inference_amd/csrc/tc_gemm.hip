@@ -37,24 +37,28 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-constexpr int GT = 512;       // threads per workgroup (8 waves)
-constexpr int GN = 128;       // weight rows per workgroup tile
+constexpr int GT = 256;       // threads per workgroup (4 waves; two workgroups per CU)
+constexpr int GN = 64;        // weight rows per workgroup tile
 constexpr int GM = 128;       // tokens per workgroup tile
 constexpr int PL = 272;       // LDS plane row stride (256 + 16: conflict-free b128 reads)
 
-// LDS layout (bytes), shared by both weight types where the field exists.
+// LDS layout (bytes); 75,776 B for either weight type, so that two
+// workgroups fit a CU and one's conversion / epilogue overlaps the other's
+// MFMA work.
+template <int TYPE>
 struct GLds {
-    static constexpr uint32_t A0 = 0;                      // Q4_K hi plane / Q8_0 weights [GN][PL]
-    static constexpr uint32_t A1 = A0 + GN * PL;           // Q4_K lo plane [GN][PL]
-    static constexpr uint32_t AM = A1 + GN * PL;           // Q4_K mins, 8 bytes + 8 zero [GN][16]
-    static constexpr uint32_t AS = AM + GN * 16;           // Q4_K d [GN] | Q8_0 dw [GN][8]
-    static constexpr uint32_t AD = AS + GN * 32;           // Q4_K dmin [GN]
-    static constexpr uint32_t B = AD + GN * 4;             // activation int8 [GM][PL]
-    static constexpr uint32_t BL = B + GM * PL;            // Q4_K pair-sum low digits [GM][16]
-    static constexpr uint32_t BH = BL + GM * 16;           // Q4_K pair-sum high digits [GM][16]
-    static constexpr uint32_t BD = BH + GM * 16;           // Q8_K d [GM] | Q8_0 d [GM][8]
-    static constexpr uint32_t RAW = BD + GM * 32;          // raw weight tile [GN][unit bytes]
-    static constexpr uint32_t bytes(int type) { return RAW + GN * unit_bytes(type); }
+    static constexpr bool K = TYPE == kQ4_K;
+    static constexpr uint32_t A0 = 0;                                 // Q4_K hi plane / Q8_0 weights [GN][PL]
+    static constexpr uint32_t A1 = A0 + GN * PL;                      // Q4_K lo plane [GN][PL]
+    static constexpr uint32_t AM = A1 + (K ? GN * PL : 0);            // Q4_K mins, 8 bytes + 8 zero [GN][16]
+    static constexpr uint32_t AS = AM + (K ? GN * 16 : 0);            // Q4_K d [GN] | Q8_0 dw [GN][8]
+    static constexpr uint32_t AD = AS + (K ? GN * 4 : GN * 32);       // Q4_K dmin [GN]
+    static constexpr uint32_t B = AD + (K ? GN * 4 : 0);              // activation int8 [GM][PL]
+    static constexpr uint32_t BL = B + GM * PL;                       // Q4_K pair-sum low digits [GM][16]
+    static constexpr uint32_t BH = BL + (K ? GM * 16 : 0);            // Q4_K pair-sum high digits [GM][16]
+    static constexpr uint32_t BD = BH + (K ? GM * 16 : 0);            // Q8_K d [GM] | Q8_0 d [GM][8]
+    static constexpr uint32_t RAW = BD + (K ? GM * 4 : GM * 32);      // Q8_0 raw weight tile [GN][272]
+    static constexpr uint32_t bytes = RAW + (K ? 0 : GN * 272);
 };
 
 struct GemmArgs {
@@ -96,28 +100,38 @@ __device__ __forceinline__ void digits4(uint32_t q, uint32_t sc, uint32_t &hi, u
 
 template <int TYPE>
 struct GPrefetch {
-    static constexpr int RAWC = (GN * unit_bytes(TYPE) / 16 + GT - 1) / GT;  // raw weight chunks / thread
+    // Q4_K: the 16-byte header and the 32 quant bytes this thread converts
+    // (row tid/4, quarter tid%4); Q8_0: raw 16-byte chunks of the tile.
+    static constexpr int RAWC = TYPE == kQ4_K ? 3 : (GN * 272 / 16 + GT - 1) / GT;
     u4 raw[RAWC];
-    u4 act[4];   // 2048 chunks of 16 activation bytes
-    u4 side;     // Q8_K bsums (256 chunks) or Q8_0 d (256 chunks)
-    float d8;    // Q8_K d (128 tokens)
+    u4 act[GM * 16 / GT];  // 16-byte activation chunks
+    u4 side;               // Q8_K bsums (256 chunks) or Q8_0 d (256 chunks)
+    float d8;              // Q8_K d (128 tokens)
 };
 
 template <int TYPE>
 __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t b,
                                               GPrefetch<TYPE> &p) {
     constexpr uint32_t UB = unit_bytes(TYPE);
-    constexpr uint32_t CPR = UB / 16;  // raw chunks per row
     const uint32_t tid = threadIdx.x;
+    if constexpr (TYPE == kQ4_K) {
+        const uint32_t r = tid / 4, qq = tid & 3;
+        const uint8_t *u = a.W + size_t(min(n0 + r, a.N - 1)) * a.row_bytes + size_t(b) * UB;
+        p.raw[0] = *reinterpret_cast<const u4 *>(u);
+        p.raw[1] = *reinterpret_cast<const u4 *>(u + 16 + 32 * qq);
+        p.raw[2] = *reinterpret_cast<const u4 *>(u + 32 + 32 * qq);
+    } else {
+        constexpr uint32_t CPR = UB / 16;  // raw chunks per row
 #pragma unroll
-    for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
-        const uint32_t c = min(tid + i * GT, GN * CPR - 1);
-        const uint32_t r = c / CPR, w = c - r * CPR;
-        const uint32_t n = min(n0 + r, a.N - 1);
-        p.raw[i] = *reinterpret_cast<const u4 *>(a.W + size_t(n) * a.row_bytes + size_t(b) * UB + 16 * w);
+        for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
+            const uint32_t c = min(tid + i * GT, GN * CPR - 1);
+            const uint32_t r = c / CPR, w = c - r * CPR;
+            const uint32_t n = min(n0 + r, a.N - 1);
+            p.raw[i] = *reinterpret_cast<const u4 *>(a.W + size_t(n) * a.row_bytes + size_t(b) * UB + 16 * w);
+        }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < GM * 16 / GT; ++i) {
         const uint32_t c = tid + i * GT;
         const uint32_t m = min(m0 + c / 16, a.M - 1);
         p.act[i] = *reinterpret_cast<const u4 *>(a.qs + size_t(m) * a.K + size_t(b) * 256 + 16 * (c & 15));
@@ -136,27 +150,74 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, uint32_t n0, ui
     }
 }
 
-// Staged data -> LDS (raw weights, activation plane, activation side data).
+// Q4_K weights of this thread (row tid/4: header + qs[32qq .. 32qq+31]) ->
+// the two digit planes, the mins and the row scales.
+__device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u4 &qb, unsigned char *lds) {
+    using L = GLds<kQ4_K>;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t r = tid / 4, qq = tid & 3;
+    uint8_t sc12[12];
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+        const uint32_t w = i < 4 ? hdr.y : i < 8 ? hdr.z : hdr.w;
+        sc12[i] = uint8_t(w >> (8 * (i & 3)));
+    }
+    uint32_t sc0, mn0, sc1, mn1;
+    q4k_scale_min(sc12, 2 * qq, sc0, mn0);
+    q4k_scale_min(sc12, 2 * qq + 1, sc1, mn1);
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    uint32_t hl[8], ll[8], hh[8], lh[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        digits4(q[k] & 0x0F0F0F0Fu, sc0, hl[k], ll[k]);
+        digits4((q[k] >> 4) & 0x0F0F0F0Fu, sc1, hh[k], lh[k]);
+    }
+    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
+    const uint32_t s0 = 64 * qq, s1 = 64 * qq + 32;  // k offsets of sub-blocks 2qq, 2qq+1
+    *reinterpret_cast<u4 *>(a0 + s0) = u4{hl[0], hl[1], hl[2], hl[3]};
+    *reinterpret_cast<u4 *>(a0 + s0 + 16) = u4{hl[4], hl[5], hl[6], hl[7]};
+    *reinterpret_cast<u4 *>(a1 + s0) = u4{ll[0], ll[1], ll[2], ll[3]};
+    *reinterpret_cast<u4 *>(a1 + s0 + 16) = u4{ll[4], ll[5], ll[6], ll[7]};
+    *reinterpret_cast<u4 *>(a0 + s1) = u4{hh[0], hh[1], hh[2], hh[3]};
+    *reinterpret_cast<u4 *>(a0 + s1 + 16) = u4{hh[4], hh[5], hh[6], hh[7]};
+    *reinterpret_cast<u4 *>(a1 + s1) = u4{lh[0], lh[1], lh[2], lh[3]};
+    *reinterpret_cast<u4 *>(a1 + s1 + 16) = u4{lh[4], lh[5], lh[6], lh[7]};
+    reinterpret_cast<uint16_t *>(lds + L::AM + r * 16)[qq] = uint16_t(mn0 | (mn1 << 8));
+    reinterpret_cast<uint16_t *>(lds + L::AM + r * 16)[4 + qq] = 0;
+    if (qq == 0) {
+        reinterpret_cast<float *>(lds + L::AS)[r] = h2f(hdr.x & 0xFFFF);
+        reinterpret_cast<float *>(lds + L::AD)[r] = h2f(hdr.x >> 16);
+    }
+}
+
+// Staged registers -> LDS: the activation plane and its side data; Q4_K
+// weights converted to the digit planes straight from registers, Q8_0 raw
+// rows to a staging area (converted after the barrier).
 template <int TYPE>
 __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned char *lds) {
-    constexpr uint32_t UB = unit_bytes(TYPE);
+    using L = GLds<TYPE>;
     const uint32_t tid = threadIdx.x;
+    if constexpr (TYPE == kQ4_K) {
+        q4k_convert(p.raw[0], p.raw[1], p.raw[2], lds);
+    } else {
 #pragma unroll
-    for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
-        const uint32_t c = tid + i * GT;
-        if (c < GN * UB / 16) *reinterpret_cast<u4 *>(lds + GLds::RAW + 16 * c) = p.raw[i];
+        for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
+            const uint32_t c = tid + i * GT;
+            if (c < GN * 272 / 16) *reinterpret_cast<u4 *>(lds + L::RAW + 16 * c) = p.raw[i];
+        }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < GM * 16 / GT; ++i) {
         const uint32_t c = tid + i * GT;
-        *reinterpret_cast<u4 *>(lds + GLds::B + (c / 16) * PL + 16 * (c & 15)) = p.act[i];
+        *reinterpret_cast<u4 *>(lds + L::B + (c / 16) * PL + 16 * (c & 15)) = p.act[i];
     }
-    if (tid < 256) {
-        const uint32_t m = tid / 2, h = tid & 1;
+    {
+        const uint32_t m = (tid & 255) / 2, h = tid & 1;
         if constexpr (TYPE == kQ8_0) {
-            *reinterpret_cast<u4 *>(lds + GLds::BD + m * 32 + 16 * h) = p.side;
+            *reinterpret_cast<u4 *>(lds + L::BD + m * 32 + 16 * h) = p.side;
         } else {
-            // bsums (16 int16) -> 8 pair sums; this thread has pairs 4h..4h+3
+            // bsums (16 int16) -> 8 pair sums, split into int8 digits; this
+            // thread has pairs 4h..4h+3
             uint32_t lo = 0, hi = 0;
             const uint32_t w[4] = {p.side.x, p.side.y, p.side.z, p.side.w};
 #pragma unroll
@@ -165,75 +226,35 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
                 lo |= uint32_t(ps & 127) << (8 * i);
                 hi |= uint32_t(uint8_t(int8_t(ps >> 7))) << (8 * i);
             }
-            reinterpret_cast<uint32_t *>(lds + GLds::BL + m * 16)[h] = lo;
-            reinterpret_cast<uint32_t *>(lds + GLds::BH + m * 16)[h] = hi;
-            if (h == 0) {
-                reinterpret_cast<uint32_t *>(lds + GLds::BL + m * 16)[2] = 0;
-                reinterpret_cast<uint32_t *>(lds + GLds::BL + m * 16)[3] = 0;
-                reinterpret_cast<uint32_t *>(lds + GLds::BH + m * 16)[2] = 0;
-                reinterpret_cast<uint32_t *>(lds + GLds::BH + m * 16)[3] = 0;
-            }
+            reinterpret_cast<uint32_t *>(lds + L::BL + m * 16)[h] = lo;
+            reinterpret_cast<uint32_t *>(lds + L::BH + m * 16)[h] = hi;
+            reinterpret_cast<uint32_t *>(lds + L::BL + m * 16)[2 + h] = 0;
+            reinterpret_cast<uint32_t *>(lds + L::BH + m * 16)[2 + h] = 0;
         }
     }
     if constexpr (TYPE == kQ4_K) {
-        if (tid < GM) reinterpret_cast<float *>(lds + GLds::BD)[tid] = p.d8;
+        if (tid < GM) reinterpret_cast<float *>(lds + L::BD)[tid] = p.d8;
     }
 }
 
-// Raw weight tile in LDS -> MFMA operand planes and per-row scales.
-template <int TYPE>
-__device__ __forceinline__ void gemm_convert(unsigned char *lds) {
+// Q8_0 raw rows in LDS -> the weight plane and the per-block scales.
+__device__ __forceinline__ void q80_convert(unsigned char *lds) {
+    using L = GLds<kQ8_0>;
     const uint32_t tid = threadIdx.x;
     const uint32_t r = tid / 4, qq = tid & 3;
-    if constexpr (TYPE == kQ4_K) {
-        // 4 threads per row; thread qq converts sub-blocks 2qq (low nibbles)
-        // and 2qq+1 (high nibbles) of qs[32qq .. 32qq+31].
-        const unsigned char *raw = lds + GLds::RAW + r * 144;
-        const uint32_t dh = *reinterpret_cast<const uint32_t *>(raw);
-        const uint8_t *sc12 = raw + 4;
-        uint32_t sc0, mn0, sc1, mn1;
-        q4k_scale_min(sc12, 2 * qq, sc0, mn0);
-        q4k_scale_min(sc12, 2 * qq + 1, sc1, mn1);
-        const u4 qa = lds4(raw + 16 + 32 * qq), qb = lds4(raw + 32 + 32 * qq);
-        const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        uint32_t hl[8], ll[8], hh[8], lh[8];
+    // 8 blocks of 34 bytes per row (2-byte aligned); thread qq: blocks 2qq, 2qq+1.
+    const unsigned char *raw = lds + L::RAW + r * 272;
+    unsigned char *a0 = lds + L::A0 + r * PL;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            digits4(q[k] & 0x0F0F0F0Fu, sc0, hl[k], ll[k]);
-            digits4((q[k] >> 4) & 0x0F0F0F0Fu, sc1, hh[k], lh[k]);
-        }
-        unsigned char *a0 = lds + GLds::A0 + r * PL, *a1 = lds + GLds::A1 + r * PL;
-        const uint32_t s0 = 64 * qq, s1 = 64 * qq + 32;  // k offsets of sub-blocks 2qq, 2qq+1
-        *reinterpret_cast<u4 *>(a0 + s0) = u4{hl[0], hl[1], hl[2], hl[3]};
-        *reinterpret_cast<u4 *>(a0 + s0 + 16) = u4{hl[4], hl[5], hl[6], hl[7]};
-        *reinterpret_cast<u4 *>(a1 + s0) = u4{ll[0], ll[1], ll[2], ll[3]};
-        *reinterpret_cast<u4 *>(a1 + s0 + 16) = u4{ll[4], ll[5], ll[6], ll[7]};
-        *reinterpret_cast<u4 *>(a0 + s1) = u4{hh[0], hh[1], hh[2], hh[3]};
-        *reinterpret_cast<u4 *>(a0 + s1 + 16) = u4{hh[4], hh[5], hh[6], hh[7]};
-        *reinterpret_cast<u4 *>(a1 + s1) = u4{lh[0], lh[1], lh[2], lh[3]};
-        *reinterpret_cast<u4 *>(a1 + s1 + 16) = u4{lh[4], lh[5], lh[6], lh[7]};
-        reinterpret_cast<uint16_t *>(lds + GLds::AM + r * 16)[qq] = uint16_t(mn0 | (mn1 << 8));
-        reinterpret_cast<uint16_t *>(lds + GLds::AM + r * 16)[4 + qq] = 0;
-        if (qq == 0) {
-            reinterpret_cast<float *>(lds + GLds::AS)[r] = h2f(dh & 0xFFFF);
-            reinterpret_cast<float *>(lds + GLds::AD)[r] = h2f(dh >> 16);
-        }
-    } else {
-        // Q8_0: 8 blocks of 34 bytes per row (2-byte aligned); thread qq
-        // handles blocks 2qq, 2qq+1.
-        const unsigned char *raw = lds + GLds::RAW + r * 272;
-        unsigned char *a0 = lds + GLds::A0 + r * PL;
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t blk = 2 * qq + j;
+        const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + 34 * blk);
+        uint32_t w[8];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t blk = 2 * qq + j;
-            const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + 34 * blk);
-            uint32_t w[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) w[k] = uint32_t(src[1 + 2 * k]) | (uint32_t(src[2 + 2 * k]) << 16);
-            *reinterpret_cast<u4 *>(a0 + 32 * blk) = u4{w[0], w[1], w[2], w[3]};
-            *reinterpret_cast<u4 *>(a0 + 32 * blk + 16) = u4{w[4], w[5], w[6], w[7]};
-            reinterpret_cast<float *>(lds + GLds::AS + r * 32)[blk] = h2f(src[0]);
-        }
+        for (int k = 0; k < 8; ++k) w[k] = uint32_t(src[1 + 2 * k]) | (uint32_t(src[2 + 2 * k]) << 16);
+        *reinterpret_cast<u4 *>(a0 + 32 * blk) = u4{w[0], w[1], w[2], w[3]};
+        *reinterpret_cast<u4 *>(a0 + 32 * blk + 16) = u4{w[4], w[5], w[6], w[7]};
+        reinterpret_cast<float *>(lds + L::AS + r * 32)[blk] = h2f(src[0]);
     }
 }
 
@@ -242,11 +263,12 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
 }
 
 template <int TYPE>
-__global__ __launch_bounds__(GT) void k_gemm(GemmArgs a) {
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t wn = wave & 3, wm = wave >> 2;  // 32-row group, 64-token group
+    const uint32_t wn = wave & 1, wm = wave >> 1;  // 32-row group, 64-token group
+    using L = GLds<TYPE>;
     const uint32_t li = lane & 31, lg = lane >> 5;
 
     const uint32_t tile = blockIdx.x;
@@ -268,71 +290,82 @@ __global__ __launch_bounds__(GT) void k_gemm(GemmArgs a) {
         gemm_stage<TYPE>(pf, lds);
         if (b + 1 < b1) gemm_prefetch<TYPE>(a, n0, m0, b + 1, pf);
         __syncthreads();
-        gemm_convert<TYPE>(lds);
-        __syncthreads();
+        if constexpr (TYPE == kQ8_0) {
+            q80_convert(lds);
+            __syncthreads();
+        }
 
         const unsigned char *arow = lds + (32 * wn + li) * PL + 16 * lg;
-        const unsigned char *brow0 = lds + GLds::B + (64 * wm + li) * PL + 16 * lg;
+        const unsigned char *brow0 = lds + L::B + (64 * wm + li) * PL + 16 * lg;
         const unsigned char *brow1 = brow0 + 32 * PL;
         if constexpr (TYPE == kQ4_K) {
-            v16i hi0 = {}, lo0 = {}, hi1 = {}, lo1 = {};
+            // One accumulator per token tile: the hi-digit chain, then
+            // C = hi << 7 and the lo-digit chain on top (= 128*hi + lo exactly).
+            v16i c0 = {}, c1 = {};
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const v4i ah = as_v4i(lds4(arow + GLds::A0 + 32 * s));
-                const v4i al = as_v4i(lds4(arow + GLds::A1 + 32 * s));
-                const v4i x0 = as_v4i(lds4(brow0 + 32 * s));
-                const v4i x1 = as_v4i(lds4(brow1 + 32 * s));
-                hi0 = mfma(ah, x0, hi0);
-                lo0 = mfma(al, x0, lo0);
-                hi1 = mfma(ah, x1, hi1);
-                lo1 = mfma(al, x1, lo1);
+                const v4i ah = as_v4i(lds4(arow + L::A0 + 32 * s));
+                c0 = mfma(ah, as_v4i(lds4(brow0 + 32 * s)), c0);
+                c1 = mfma(ah, as_v4i(lds4(brow1 + 32 * s)), c1);
             }
-            // min term over 8 useful k slots (k-group 0, bytes 0..7)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                c0[r] <<= 7;
+                c1[r] <<= 7;
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const v4i al = as_v4i(lds4(arow + L::A1 + 32 * s));
+                c0 = mfma(al, as_v4i(lds4(brow0 + 32 * s)), c0);
+                c1 = mfma(al, as_v4i(lds4(brow1 + 32 * s)), c1);
+            }
+            // min term over 8 useful k slots (k-group 0, bytes 0..7), folded the same way
             const v4i zero = {0, 0, 0, 0};
-            const v4i am = lg == 0 ? as_v4i(lds4(lds + GLds::AM + (32 * wn + li) * 16)) : zero;
+            const v4i am = lg == 0 ? as_v4i(lds4(lds + L::AM + (32 * wn + li) * 16)) : zero;
             const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
-            const v4i bl0 = lg == 0 ? as_v4i(lds4(lds + GLds::BL + tb0 * 16)) : zero;
-            const v4i bh0 = lg == 0 ? as_v4i(lds4(lds + GLds::BH + tb0 * 16)) : zero;
-            const v4i bl1 = lg == 0 ? as_v4i(lds4(lds + GLds::BL + tb1 * 16)) : zero;
-            const v4i bh1 = lg == 0 ? as_v4i(lds4(lds + GLds::BH + tb1 * 16)) : zero;
             const v16i z16 = {};
-            const v16i ml0 = mfma(am, bl0, z16), mh0 = mfma(am, bh0, z16);
-            const v16i ml1 = mfma(am, bl1, z16), mh1 = mfma(am, bh1, z16);
-            const float d80 = reinterpret_cast<const float *>(lds + GLds::BD)[tb0];
-            const float d81 = reinterpret_cast<const float *>(lds + GLds::BD)[tb1];
+            v16i m0 = mfma(am, lg == 0 ? as_v4i(lds4(lds + L::BH + tb0 * 16)) : zero, z16);
+            v16i m1 = mfma(am, lg == 0 ? as_v4i(lds4(lds + L::BH + tb1 * 16)) : zero, z16);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                m0[r] <<= 7;
+                m1[r] <<= 7;
+            }
+            m0 = mfma(am, lg == 0 ? as_v4i(lds4(lds + L::BL + tb0 * 16)) : zero, m0);
+            m1 = mfma(am, lg == 0 ? as_v4i(lds4(lds + L::BL + tb1 * 16)) : zero, m1);
+            const float d80 = reinterpret_cast<const float *>(lds + L::BD)[tb0];
+            const float d81 = reinterpret_cast<const float *>(lds + L::BD)[tb1];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t rr = 32 * wn + 8 * q + 4 * lg;
-                const float4 dv = *reinterpret_cast<const float4 *>(lds + GLds::AS + 4 * rr);
-                const float4 mv = *reinterpret_cast<const float4 *>(lds + GLds::AD + 4 * rr);
+                const float4 dv = *reinterpret_cast<const float4 *>(lds + L::AS + 4 * rr);
+                const float4 mv = *reinterpret_cast<const float4 *>(lds + L::AD + 4 * rr);
                 const float dd[4] = {dv.x, dv.y, dv.z, dv.w}, dm[4] = {mv.x, mv.y, mv.z, mv.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int r = 4 * q + e;
-                    const int main0 = (hi0[r] << 7) + lo0[r], min0 = (mh0[r] << 7) + ml0[r];
-                    const int main1 = (hi1[r] << 7) + lo1[r], min1 = (mh1[r] << 7) + ml1[r];
-                    acc[0][r] = fmaf(d80, dd[e] * float(main0) - dm[e] * float(min0), acc[0][r]);
-                    acc[1][r] = fmaf(d81, dd[e] * float(main1) - dm[e] * float(min1), acc[1][r]);
+                    acc[0][r] = fmaf(d80, dd[e] * float(c0[r]) - dm[e] * float(m0[r]), acc[0][r]);
+                    acc[1][r] = fmaf(d81, dd[e] * float(c1[r]) - dm[e] * float(m1[r]), acc[1][r]);
                 }
             }
         } else {
             const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
 #pragma unroll 2
             for (int s = 0; s < 8; ++s) {
-                const v4i aw = as_v4i(lds4(arow + GLds::A0 + 32 * s));
+                const v4i aw = as_v4i(lds4(arow + L::A0 + 32 * s));
                 const v4i x0 = as_v4i(lds4(brow0 + 32 * s));
                 const v4i x1 = as_v4i(lds4(brow1 + 32 * s));
                 const v16i z16 = {};
                 const v16i c0 = mfma(aw, x0, z16), c1 = mfma(aw, x1, z16);
-                const float d80 = reinterpret_cast<const float *>(lds + GLds::BD + tb0 * 32)[s];
-                const float d81 = reinterpret_cast<const float *>(lds + GLds::BD + tb1 * 32)[s];
+                const float d80 = reinterpret_cast<const float *>(lds + L::BD + tb0 * 32)[s];
+                const float d81 = reinterpret_cast<const float *>(lds + L::BD + tb1 * 32)[s];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int r = 4 * q + e;
                         const float dw = reinterpret_cast<const float *>(
-                            lds + GLds::AS + (32 * wn + 8 * q + 4 * lg + e) * 32)[s];
+                            lds + L::AS + (32 * wn + 8 * q + 4 * lg + e) * 32)[s];
                         acc[0][r] = fmaf(dw * d80, float(c0[r]), acc[0][r]);
                         acc[1][r] = fmaf(dw * d81, float(c1[r]), acc[1][r]);
                     }
@@ -380,7 +413,7 @@ hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<TYPE>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    k_gemm<TYPE><<<grid, GT, GLds::bytes(TYPE), st>>>(a);
+    k_gemm<TYPE><<<grid, GT, GLds<TYPE>::bytes, st>>>(a);
     return hipGetLastError();
 }
 
