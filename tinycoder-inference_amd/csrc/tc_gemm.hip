@@ -42,7 +42,7 @@ constexpr int GN = 64;        // weight rows per workgroup tile
 constexpr int GM = 128;       // tokens per workgroup tile
 constexpr int PL = 272;       // LDS plane row stride (256 + 16: conflict-free b128 reads)
 
-// LDS layout (bytes); 75,776 B for either weight type, so that two
+// LDS layout (bytes); at most 80 KB for either weight type, so that two
 // workgroups fit a CU and one's conversion / epilogue overlaps the other's
 // MFMA work.
 template <int TYPE>
@@ -50,13 +50,13 @@ struct GLds {
     static constexpr bool K = TYPE == kQ4_K;
     static constexpr uint32_t A0 = 0;                                 // Q4_K hi plane / Q8_0 weights [GN][PL]
     static constexpr uint32_t A1 = A0 + GN * PL;                      // Q4_K lo plane [GN][PL]
-    static constexpr uint32_t AM = A1 + (K ? GN * PL : 0);            // Q4_K mins, 8 bytes + 8 zero [GN][16]
-    static constexpr uint32_t AS = AM + (K ? GN * 16 : 0);            // Q4_K d [GN] | Q8_0 dw [GN][8]
+    static constexpr uint32_t AM = A1 + (K ? GN * PL : 0);            // Q4_K mins, 8 bytes + 24 zero [GN][32]
+    static constexpr uint32_t AS = AM + (K ? GN * 32 : 0);            // Q4_K d [GN] | Q8_0 dw [GN][8]
     static constexpr uint32_t AD = AS + (K ? GN * 4 : GN * 32);       // Q4_K dmin [GN]
     static constexpr uint32_t B = AD + (K ? GN * 4 : 0);              // activation int8 [GM][PL]
-    static constexpr uint32_t BL = B + GM * PL;                       // Q4_K pair-sum low digits [GM][16]
-    static constexpr uint32_t BH = BL + (K ? GM * 16 : 0);            // Q4_K pair-sum high digits [GM][16]
-    static constexpr uint32_t BD = BH + (K ? GM * 16 : 0);            // Q8_K d [GM] | Q8_0 d [GM][8]
+    static constexpr uint32_t BL = B + GM * PL;                       // Q4_K pair-sum low digits, 8 + 24 zero [GM][32]
+    static constexpr uint32_t BH = BL + (K ? GM * 32 : 0);            // Q4_K pair-sum high digits [GM][32]
+    static constexpr uint32_t BD = BH + (K ? GM * 32 : 0);            // Q8_K d [GM] | Q8_0 d [GM][8]
     static constexpr uint32_t RAW = BD + (K ? GM * 4 : GM * 32);      // Q8_0 raw weight tile [GN][272]
     static constexpr uint32_t bytes = RAW + (K ? 0 : GN * 272);
 };
@@ -109,45 +109,61 @@ struct GPrefetch {
     float d8;              // Q8_K d (128 tokens)
 };
 
+// Buffer descriptors over the operands and this thread's fixed per-lane
+// offsets; superblock b only moves the scalar offsets. Rows past N and tokens
+// past M fall outside the descriptors and load zeros (never stored).
+struct GSrc {
+    __amdgpu_buffer_rsrc_t w, q, d, bs;
+    uint32_t vw, vw2, vq, vd, vbs;  // per-lane offsets (vw2: Q4_K quant bytes / unused)
+    uint32_t vr[5];                 // Q8_0 raw chunks
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t grsrc(const void *p, uint64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), short(0), int(uint32_t(bytes)), 0x00020000);
+}
+
 template <int TYPE>
-__device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t b,
-                                              GPrefetch<TYPE> &p) {
-    constexpr uint32_t UB = unit_bytes(TYPE);
+__device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0) {
     const uint32_t tid = threadIdx.x;
+    GSrc g;
+    g.w = grsrc(a.W, uint64_t(a.N) * a.row_bytes);
+    g.q = grsrc(a.qs, uint64_t(a.M) * a.K);
+    g.d = grsrc(a.d8, uint64_t(a.M) * (a.K / (TYPE == kQ8_0 ? 32 : 256)) * 4);
+    g.bs = grsrc(a.bsums, TYPE == kQ8_0 ? 0 : uint64_t(a.M) * (a.K / 16) * 2);
+    g.vw = (n0 + tid / 4) * a.row_bytes;
+    g.vw2 = g.vw + 16 + 32 * (tid & 3);
+    g.vq = (m0 + tid / 16) * a.K + 16 * (tid & 15);
+    const uint32_t ms = m0 + (tid & 255) / 2;
+    g.vbs = TYPE == kQ8_0 ? ms * (a.K / 32) * 4 + 16 * (tid & 1) : ms * (a.K / 16) * 2 + 16 * (tid & 1);
+    g.vd = (m0 + (tid & 127)) * (a.K / 256) * 4;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const uint32_t c = tid + i * GT, r = c / 17, w = c - r * 17;
+        g.vr[i] = c < GN * 17 ? (n0 + r) * a.row_bytes + 16 * w : 0x80000000u;
+    }
+    return g;
+}
+
+template <int TYPE>
+__device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, uint32_t b, GPrefetch<TYPE> &p) {
+    constexpr uint32_t UB = unit_bytes(TYPE);
     if constexpr (TYPE == kQ4_K) {
-        const uint32_t r = tid / 4, qq = tid & 3;
-        const uint8_t *u = a.W + size_t(min(n0 + r, a.N - 1)) * a.row_bytes + size_t(b) * UB;
-        p.raw[0] = *reinterpret_cast<const u4 *>(u);
-        p.raw[1] = *reinterpret_cast<const u4 *>(u + 16 + 32 * qq);
-        p.raw[2] = *reinterpret_cast<const u4 *>(u + 32 + 32 * qq);
+        p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw, b * UB, 0);
+        p.raw[1] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2, b * UB, 0);
+        p.raw[2] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2 + 16, b * UB, 0);
     } else {
-        constexpr uint32_t CPR = UB / 16;  // raw chunks per row
 #pragma unroll
-        for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
-            const uint32_t c = min(tid + i * GT, GN * CPR - 1);
-            const uint32_t r = c / CPR, w = c - r * CPR;
-            const uint32_t n = min(n0 + r, a.N - 1);
-            p.raw[i] = *reinterpret_cast<const u4 *>(a.W + size_t(n) * a.row_bytes + size_t(b) * UB + 16 * w);
-        }
+        for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i)
+            p.raw[i] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vr[i], b * UB, 0);
     }
 #pragma unroll
-    for (int i = 0; i < GM * 16 / GT; ++i) {
-        const uint32_t c = tid + i * GT;
-        const uint32_t m = min(m0 + c / 16, a.M - 1);
-        p.act[i] = *reinterpret_cast<const u4 *>(a.qs + size_t(m) * a.K + size_t(b) * 256 + 16 * (c & 15));
-    }
-    {
-        const uint32_t c = tid & 255;
-        const uint32_t m = min(m0 + c / 2, a.M - 1);
-        if constexpr (TYPE == kQ8_0)
-            p.side = *reinterpret_cast<const u4 *>(a.d8 + size_t(m) * (a.K / 32) + size_t(b) * 8 + 4 * (c & 1));
-        else
-            p.side = *reinterpret_cast<const u4 *>(a.bsums + size_t(m) * (a.K / 16) + size_t(b) * 16 + 8 * (c & 1));
-    }
-    if constexpr (TYPE == kQ4_K) {
-        const uint32_t m = min(m0 + (tid & 127), a.M - 1);
-        p.d8 = a.d8[size_t(m) * (a.K / 256) + b];
-    }
+    for (int i = 0; i < GM * 16 / GT; ++i)  // chunk tid + 256 i: token + 16 i
+        p.act[i] = __builtin_amdgcn_raw_buffer_load_b128(g.q, g.vq, b * 256 + i * 16 * a.K, 0);
+    if constexpr (TYPE == kQ8_0)
+        p.side = __builtin_amdgcn_raw_buffer_load_b128(g.d, g.vbs, b * 32, 0);
+    else
+        p.side = __builtin_amdgcn_raw_buffer_load_b128(g.bs, g.vbs, b * 32, 0);
+    if constexpr (TYPE == kQ4_K) p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * 4, 0));
 }
 
 // Q4_K weights of this thread (row tid/4: header + qs[32qq .. 32qq+31]) ->
@@ -156,15 +172,15 @@ __device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u
     using L = GLds<kQ4_K>;
     const uint32_t tid = threadIdx.x;
     const uint32_t r = tid / 4, qq = tid & 3;
-    uint8_t sc12[12];
-#pragma unroll
-    for (int i = 0; i < 12; ++i) {
-        const uint32_t w = i < 4 ? hdr.y : i < 8 ? hdr.z : hdr.w;
-        sc12[i] = uint8_t(w >> (8 * (i & 3)));
-    }
-    uint32_t sc0, mn0, sc1, mn1;
-    q4k_scale_min(sc12, 2 * qq, sc0, mn0);
-    q4k_scale_min(sc12, 2 * qq + 1, sc1, mn1);
+    // the 8 6-bit scales / mins as bytes (reference get_scale_min_k4,
+    // GGMLDequantize.hpp:436-447): sub-blocks 0-3 from the low words, 4-7 from
+    // the packed high bits
+    const uint32_t scl = hdr.y & 0x3F3F3F3Fu, mnl = hdr.z & 0x3F3F3F3Fu;
+    const uint32_t sch = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+    const uint32_t mnh = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+    const uint32_t sh = 16 * (qq & 1);
+    const uint32_t scw = (qq < 2 ? scl : sch) >> sh, mnw = (qq < 2 ? mnl : mnh) >> sh;
+    const uint32_t sc0 = scw & 0xFF, sc1 = (scw >> 8) & 0xFF, mn0 = mnw & 0xFF, mn1 = (mnw >> 8) & 0xFF;
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     uint32_t hl[8], ll[8], hh[8], lh[8];
 #pragma unroll
@@ -182,8 +198,12 @@ __device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u
     *reinterpret_cast<u4 *>(a0 + s1 + 16) = u4{hh[4], hh[5], hh[6], hh[7]};
     *reinterpret_cast<u4 *>(a1 + s1) = u4{lh[0], lh[1], lh[2], lh[3]};
     *reinterpret_cast<u4 *>(a1 + s1 + 16) = u4{lh[4], lh[5], lh[6], lh[7]};
-    reinterpret_cast<uint16_t *>(lds + L::AM + r * 16)[qq] = uint16_t(mn0 | (mn1 << 8));
-    reinterpret_cast<uint16_t *>(lds + L::AM + r * 16)[4 + qq] = 0;
+    // 32-byte rows: bytes 0..7 the mins of sub-blocks 0..7, 8..31 zero
+    reinterpret_cast<uint16_t *>(lds + L::AM + r * 32)[qq] = uint16_t(mn0 | (mn1 << 8));
+    if (qq < 3) {
+        reinterpret_cast<uint32_t *>(lds + L::AM + r * 32)[2 + 2 * qq] = 0;
+        reinterpret_cast<uint32_t *>(lds + L::AM + r * 32)[3 + 2 * qq] = 0;
+    }
     if (qq == 0) {
         reinterpret_cast<float *>(lds + L::AS)[r] = h2f(hdr.x & 0xFFFF);
         reinterpret_cast<float *>(lds + L::AD)[r] = h2f(hdr.x >> 16);
@@ -226,10 +246,17 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
                 lo |= uint32_t(ps & 127) << (8 * i);
                 hi |= uint32_t(uint8_t(int8_t(ps >> 7))) << (8 * i);
             }
-            reinterpret_cast<uint32_t *>(lds + L::BL + m * 16)[h] = lo;
-            reinterpret_cast<uint32_t *>(lds + L::BH + m * 16)[h] = hi;
-            reinterpret_cast<uint32_t *>(lds + L::BL + m * 16)[2 + h] = 0;
-            reinterpret_cast<uint32_t *>(lds + L::BH + m * 16)[2 + h] = 0;
+            // 32-byte rows: bytes 0..7 the digits, 8..31 zero (the k slots
+            // the min-term MFMA must not count)
+            uint32_t *bl = reinterpret_cast<uint32_t *>(lds + L::BL + m * 32);
+            uint32_t *bh = reinterpret_cast<uint32_t *>(lds + L::BH + m * 32);
+            bl[h] = lo;
+            bh[h] = hi;
+#pragma unroll
+            for (int z = 0; z < 3; ++z) {
+                bl[2 + 3 * h + z] = 0;
+                bh[2 + 3 * h + z] = 0;
+            }
         }
     }
     if constexpr (TYPE == kQ4_K) {
@@ -284,11 +311,12 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
+    const GSrc gs = gemm_src<TYPE>(a, n0, m0);
     GPrefetch<TYPE> pf;
-    if (b0 < b1) gemm_prefetch<TYPE>(a, n0, m0, b0, pf);
+    if (b0 < b1) gemm_prefetch<TYPE>(a, gs, b0, pf);
     for (uint32_t b = b0; b < b1; ++b) {
         gemm_stage<TYPE>(pf, lds);
-        if (b + 1 < b1) gemm_prefetch<TYPE>(a, n0, m0, b + 1, pf);
+        if (b + 1 < b1) gemm_prefetch<TYPE>(a, gs, b + 1, pf);
         __syncthreads();
         if constexpr (TYPE == kQ8_0) {
             q80_convert(lds);
@@ -320,19 +348,18 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                 c1 = mfma(al, as_v4i(lds4(brow1 + 32 * s)), c1);
             }
             // min term over 8 useful k slots (k-group 0, bytes 0..7), folded the same way
-            const v4i zero = {0, 0, 0, 0};
-            const v4i am = lg == 0 ? as_v4i(lds4(lds + L::AM + (32 * wn + li) * 16)) : zero;
+            const v4i am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
             const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
             const v16i z16 = {};
-            v16i m0 = mfma(am, lg == 0 ? as_v4i(lds4(lds + L::BH + tb0 * 16)) : zero, z16);
-            v16i m1 = mfma(am, lg == 0 ? as_v4i(lds4(lds + L::BH + tb1 * 16)) : zero, z16);
+            v16i m0 = mfma(am, as_v4i(lds4(lds + L::BH + tb0 * 32 + 16 * lg)), z16);
+            v16i m1 = mfma(am, as_v4i(lds4(lds + L::BH + tb1 * 32 + 16 * lg)), z16);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 m0[r] <<= 7;
                 m1[r] <<= 7;
             }
-            m0 = mfma(am, lg == 0 ? as_v4i(lds4(lds + L::BL + tb0 * 16)) : zero, m0);
-            m1 = mfma(am, lg == 0 ? as_v4i(lds4(lds + L::BL + tb1 * 16)) : zero, m1);
+            m0 = mfma(am, as_v4i(lds4(lds + L::BL + tb0 * 32 + 16 * lg)), m0);
+            m1 = mfma(am, as_v4i(lds4(lds + L::BL + tb1 * 32 + 16 * lg)), m1);
             const float d80 = reinterpret_cast<const float *>(lds + L::BD)[tb0];
             const float d81 = reinterpret_cast<const float *>(lds + L::BD)[tb1];
 #pragma unroll
