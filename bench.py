@@ -226,7 +226,7 @@ def moe_bench(torch, tc, tc_hip, dev, reps):
         us = timed(torch, fn, reps)
         by = float(np.mean(nbytes)) + 4 * T * H * 2
         res.append({"batch": T, "us": round(us, 2), "bytes": int(by), "GB/s": round(by / us / 1e3, 1),
-                    "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4), "launches": 3})
+                    "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4), "launches": 2})
     del wg, wu, wd
     torch.cuda.empty_cache()
     return res

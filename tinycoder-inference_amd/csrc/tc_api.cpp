@@ -408,17 +408,30 @@ int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t se
     tc::GemvJob dn{};
     dn.W = static_cast<const uint8_t *>(wd);
     dn.x = h;
-    dn.out = y;
     dn.rows = hidden;
     dn.cols = ff;
     dn.out_ld = hidden;
     dn.ids = ids;
     dn.wstride = dstride;
+    dn.n_experts = n_experts;
+    if (top_k <= 8) {
+        // down projections of a token's ranks and their rank-order weighted
+        // sum in one launch (rank-group mode)
+        dn.out = out;
+        dn.npairs = seq_len;
+        dn.x_stride = top_k * ff;
+        dn.out_stride = hidden;
+        dn.rk = top_k;
+        dn.wts = wts;
+        e = tc::launch_gemv_jobs(TC_Q4_K, 1, &dn, 1, dev->num_cu, st);
+        if (e != hipSuccess) return hip_fail(e, "MoE down");
+        return TC_OK;
+    }
+    dn.out = y;
     dn.npairs = uint32_t(npairs);
     dn.x_div = 1;
     dn.x_stride = ff;
     dn.out_stride = hidden;
-    dn.n_experts = n_experts;
     e = tc::launch_gemv_jobs(TC_Q4_K, 1, &dn, 1, dev->num_cu, st);
     if (e != hipSuccess) return hip_fail(e, "MoE down");
 

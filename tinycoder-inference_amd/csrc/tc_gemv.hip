@@ -584,6 +584,12 @@ struct TJobDev {
     const int32_t *ids;
     uint64_t wstride;
     uint32_t wg_per_pair, x_div, x_stride, out_stride, n_experts;
+    // Activation tokens staged in LDS (S, or the rank-group size), and the
+    // rank-group mode (rk > 0, with ids): the job's pair p is a token whose rk
+    // ranks use experts ids[p*rk + k] with inputs x + p*x_stride + k*cols;
+    // out = sum over k in rank order of wts[p*rk + k] * (W[e_k] x_k).
+    uint32_t nx, rk;
+    const float *wts;
 };
 
 struct TLaunchArgs {
@@ -671,7 +677,7 @@ struct XRsrc {
 
 template <int TYPE, int S>
 __device__ __forceinline__ XRsrc tstage_rsrc(const TJobDev &jb) {
-    const uint32_t nblk = S * (jb.cols / 256);
+    const uint32_t nblk = jb.nx * (jb.cols / 256);
     XRsrc r;
     const bool fused = jb.x != nullptr;
     r.a = fused ? make_rsrc(jb.x, nblk * 1024u) : make_rsrc(jb.act.qs, nblk * 256u);
@@ -695,7 +701,7 @@ __device__ __forceinline__ XPre tstage_preload(const TJobDev &jb, const XRsrc &r
     XPre p;
     const uint32_t tid = threadIdx.x;
     const uint32_t wbase = __builtin_amdgcn_readfirstlane(tid & ~63u);  // first thread of this wave
-    const uint32_t nblk = S * (jb.cols / 256);
+    const uint32_t nblk = jb.nx * (jb.cols / 256);
     // Every load instruction costs the CU's address unit ~16 cycles whatever
     // its lanes read, so a wave issues only the slots that hold some of its
     // data (wave-uniform tests); the others stay zero.
@@ -785,7 +791,7 @@ __device__ __forceinline__ void tstore_side(unsigned char *xr, uint32_t i, uint3
 template <int TYPE, int S, int TNT>
 __device__ __forceinline__ void tstage_finish(const TJobDev &jb, const XRsrc &rs, const XPre &p, unsigned char *xr) {
     const uint32_t tid = threadIdx.x;
-    const uint32_t nblk = S * (jb.cols / 256);
+    const uint32_t nblk = jb.nx * (jb.cols / 256);
     if (jb.x != nullptr) {
         const uint32_t nchunk = nblk * 16;
         static_for<0, kXPre>([&](auto i) __attribute__((always_inline)) {
@@ -1058,7 +1064,7 @@ struct TDot<kIQ3_XXS, S> {
     }
 };
 
-template <int TYPE, int S, bool DBG, class C>
+template <int TYPE, int S, bool DBG, class C, bool RG = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1084,20 +1090,29 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
 #endif
     uint32_t lw = blockIdx.x - jb.wg_begin;
     bool no_expert = false;
+    const int32_t *rids = nullptr;  // rank-group mode: this token's expert ids
+    const float *rwts = nullptr;
     if (jb.ids != nullptr) {
         const uint32_t p = lw / jb.wg_per_pair;
         lw -= p * jb.wg_per_pair;
-        const int32_t e = jb.ids[p];
-        no_expert = e < 0 || uint32_t(e) >= jb.n_experts;
-        const uint64_t off = no_expert ? 0 : uint64_t(e) * jb.wstride;
-        jb.W += off;
-        if (jb.W2 != nullptr) jb.W2 += off;
-        jb.x += size_t(p / jb.x_div) * jb.x_stride;
+        if constexpr (!RG) {
+            const int32_t e = jb.ids[p];
+            no_expert = e < 0 || uint32_t(e) >= jb.n_experts;
+            const uint64_t off = no_expert ? 0 : uint64_t(e) * jb.wstride;
+            jb.W += off;
+            if (jb.W2 != nullptr) jb.W2 += off;
+            jb.x += size_t(p / jb.x_div) * jb.x_stride;
+        } else {
+            rids = jb.ids + size_t(p) * jb.rk;
+            rwts = jb.wts + size_t(p) * jb.rk;
+            jb.x += size_t(p) * jb.x_stride;
+        }
         jb.out += size_t(p) * jb.out_stride;
         if (jb.out2 != nullptr) jb.out2 += size_t(p) * jb.out_stride;
     }
     const uint32_t nu = jb.nu;
-    const uint32_t pairs = jb.W2 != nullptr ? 2 : 1;
+    // matrices per workgroup: 2 for a gate/up pair, rk in rank-group mode
+    const uint32_t pairs = RG ? jb.rk : jb.W2 != nullptr ? 2 : 1;
     const uint32_t r0 = lw * jb.rows_per_wg;
     const uint32_t nr = min(jb.rows_per_wg, jb.rows - r0);
     const uint32_t per_mat = nr * nu;
@@ -1109,7 +1124,14 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     const size_t xtok = size_t(nu) * XB;
     // Descriptors over exactly this workgroup's rows of each matrix.
     const uint8_t *const wbase1 = jb.W + size_t(r0) * nu * UB;
-    const uint8_t *const wbase2 = (pairs == 2 ? jb.W2 : jb.W) + size_t(r0) * nu * UB;
+    const uint8_t *const wbase2 = (jb.W2 != nullptr ? jb.W2 : jb.W) + size_t(r0) * nu * UB;
+    // Matrix of tile t (0 or 1 for a pair, the rank in rank-group mode).
+    auto mat_of = [&](uint32_t t) __attribute__((always_inline)) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int k = 1; k < 8; ++k) m += t >= uint32_t(k) * ntiles_mat ? 1u : 0u;
+        return m;
+    };
 
 
     // Register ring: the wave's tiles are t = wave, wave+TNW, ...; slot i holds
@@ -1134,11 +1156,22 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     // (The range check covers the per-lane offset, not the scalar one, so the
     // scalar offset never carries an out-of-range marker.)
     auto ld = [&](auto i, uint32_t t) __attribute__((always_inline)) {
-        const bool second = t >= ntiles_mat;
-        const uint32_t tt = second ? t - ntiles_mat : t;
-        const bool live = t < ntiles;
+        bool live = t < ntiles;
+        const uint8_t *base;
+        uint32_t tt;
+        if constexpr (!RG) {
+            const bool second = t >= ntiles_mat;
+            tt = second ? t - ntiles_mat : t;
+            base = second ? wbase2 : wbase1;
+        } else {
+            const uint32_t m = live ? mat_of(t) : 0u;
+            tt = t - m * ntiles_mat;
+            const int32_t e = rids[m];
+            live = live && e >= 0 && uint32_t(e) < jb.n_experts;
+            base = wbase1 + (live ? uint64_t(e) * jb.wstride : 0);
+        }
         const uint32_t soff = live ? tt * TILE_BYTES : 0u;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(second ? wbase2 : wbase1, live ? per_mat * UB : 0u);
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, live ? per_mat * UB : 0u);
         static_for<0, NX>([&](auto c) __attribute__((always_inline)) {
             uint32_t voff = lane * 16 + c.value * 1024;
             if constexpr (c.value == NX - 1 && TILE_BYTES % 1024 != 0) voff = voff < TILE_BYTES ? voff : 0x80000000u;
@@ -1183,7 +1216,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
             });
             ld(i, t + D * TNW);
             if (kk < nmine) {
-                const uint32_t m = t >= ntiles_mat ? 1u : 0u;
+                const uint32_t m = RG ? mat_of(t) : t >= ntiles_mat ? 1u : 0u;
                 const uint32_t um = (t - m * ntiles_mat) * kTileUnits + lane;
                 if (um < per_mat) {
                     const uint32_t rl = div_fast(um, jb.nu_div);
@@ -1192,11 +1225,13 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
                     if constexpr (DBG)
                         dbg = jb.dbg + (size_t(r0 + rl) * nbr + (TYPE == kQ8_0 ? size_t(b) * 8 : b)) * per;
                     float val[S];
+                    // rank-group mode: tile of rank m against that rank's activations (S == 1)
+                    const unsigned char *xb = xr + (RG ? size_t(m) * xtok : 0) + size_t(b) * XB;
                     if constexpr (TYPE == kIQ3_XXS)
-                        TDot<TYPE, S>::run(tile + lane * UB, xr + size_t(b) * XB, xtok,
+                        TDot<TYPE, S>::run(tile + lane * UB, xb, xtok,
                                            reinterpret_cast<const uint32_t *>(smem + L.off_g), val, dbg, dbg_tok);
                     else
-                        TDot<TYPE, S>::run(tile + lane * UB, xr + size_t(b) * XB, xtok, val, dbg, dbg_tok);
+                        TDot<TYPE, S>::run(tile + lane * UB, xb, xtok, val, dbg, dbg_tok);
 #pragma unroll
                     for (int s = 0; s < S; ++s) spart[((size_t(m) * S + s) * nr + rl) * nu + b] = val[s];
                 }
@@ -1208,6 +1243,27 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     // Row sums: 4 lanes per (token, row), each summing a strided quarter of
     // the row's units, combined with DPP quad sums (fixed order).
     const uint32_t nout = S * nr;
+    if constexpr (RG) {
+        // rank-group mode: out = sum_k w_k * rowsum_k in rank order (as the
+        // separate reference reduction, ModelMoE.cpp:990-1002)
+        for (uint32_t o0 = 0; o0 < nr; o0 += TNT / 4) {
+            const uint32_t o = o0 + tid / 4, q = tid & 3;
+            const uint32_t rl = o < nr ? o : nr - 1;
+            float acc = 0.0f;
+            for (uint32_t k = 0; k < pairs; ++k) {
+                const float *pg = spart + (size_t(k) * nr + rl) * nu;
+                float g = 0.0f;
+                for (uint32_t bb = q; bb < nu; bb += 4) g += pg[bb];
+                g = quad_sum(g);
+                if constexpr (TYPE == kIQ3_XXS) g = 0.25f * g;
+                const int32_t e = rids[k];
+                if (e < 0 || uint32_t(e) >= jb.n_experts) g = 0.0f;
+                acc = fmaf(rwts[k], g, acc);
+            }
+            if (o < nr && q == 0) jb.out[r0 + rl] = acc;
+        }
+        return;
+    }
     for (uint32_t o0 = 0; o0 < nout; o0 += TNT / 4) {
         const uint32_t o = o0 + tid / 4, q = tid & 3;
         const uint32_t oc = o < nout ? o : nout - 1;
@@ -1239,22 +1295,33 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     TC_TRACE_PT(3);
 }
 
-template <int TYPE, int S, bool DBG, class C>
+template <int TYPE, int S, bool DBG, class C, bool RG = false>
 hipError_t launch_tiled_sd(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
     // Dynamic LDS above 64 KB needs the per-kernel opt-in, once per process.
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG, C>),
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG, C, RG>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    k_gemv_t<TYPE, S, DBG, C><<<g, C::NT, lds, st>>>(a);
+    k_gemv_t<TYPE, S, DBG, C, RG><<<g, C::NT, lds, st>>>(a);
     return hipSuccess;
 }
 
 template <int TYPE, int S, class C>
 hipError_t launch_tiled_s(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
     // The per-block integer-sum test hook is its own instantiation: its
-    // global stores would otherwise sit in the production loop.
-    bool dbg = false;
-    for (uint32_t j = 0; j < a.njobs; ++j) dbg = dbg || a.jobs[j].dbg != nullptr;
+    // global stores would otherwise sit in the production loop. So is the
+    // MoE rank-group mode (Q4_K experts, one token per launch).
+    bool dbg = false, rg = false;
+    for (uint32_t j = 0; j < a.njobs; ++j) {
+        dbg = dbg || a.jobs[j].dbg != nullptr;
+        rg = rg || a.jobs[j].rk != 0;
+    }
+    if (rg) {
+        if constexpr (TYPE == kQ4_K && S == 1) {
+            if (dbg || a.njobs != 1) return hipErrorInvalidValue;
+            return launch_tiled_sd<TYPE, S, false, C, true>(a, g, lds, st);
+        }
+        return hipErrorInvalidValue;
+    }
     return dbg ? launch_tiled_sd<TYPE, S, true, C>(a, g, lds, st) : launch_tiled_sd<TYPE, S, false, C>(a, g, lds, st);
 }
 
@@ -1324,6 +1391,10 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
 
 bool tiled_type(int type) { return type == kQ4_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
+// Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
+// rank-group mode, else 1.
+uint32_t job_mats(const GemvJob &g) { return g.rk ? g.rk : g.W2 ? 2 : 1; }
+
 bool use_big(int type, uint64_t weight_bytes) { return type != kQ8_0 && weight_bytes >= kBigBytes; }
 
 template <class C>
@@ -1331,13 +1402,14 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
                                hipStream_t st) {
     TLaunchArgs a{};
     a.njobs = njobs;
-    uint32_t maxcols = 0;
+    uint32_t maxcols = 0, maxnx = S;
     uint64_t total_units = 0;
     for (uint32_t j = 0; j < njobs; ++j) {
         maxcols = std::max(maxcols, jobs[j].cols);
-        total_units += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * (jobs[j].W2 ? 2 : 1) * jobs[j].npairs;
+        if (jobs[j].rk) maxnx = std::max(maxnx, jobs[j].rk);
+        total_units += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * job_mats(jobs[j]) * jobs[j].npairs;
     }
-    const uint32_t fixed = tlds_layout<C>(type, S, maxcols, &a);
+    const uint32_t fixed = tlds_layout<C>(type, maxnx, maxcols, &a);
     if (fixed >= kTLdsBudget) return hipErrorInvalidValue;
     const uint32_t part_avail = kTLdsBudget - fixed;
     // One workgroup per CU, each with at least 2 tiles of work.
@@ -1347,7 +1419,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
     for (uint32_t j = 0; j < njobs; ++j) {
         const GemvJob &g = jobs[j];
         TJobDev &d = a.jobs[j];
-        const uint32_t pairs = g.W2 ? 2 : 1;
+        const uint32_t pairs = job_mats(g);
         d.W = g.W;
         d.W2 = g.W2;
         d.x = g.x;
@@ -1367,6 +1439,9 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         d.x_stride = g.x_stride;
         d.out_stride = g.out_stride;
         d.n_experts = g.n_experts;
+        d.rk = g.rk;
+        d.wts = g.wts;
+        d.nx = g.rk ? g.rk : S;
         const uint64_t units = uint64_t(g.rows) * d.nu * pairs * g.npairs;
         // workgroups per mat-vec (per expert pair in expert-pair mode)
         uint64_t gj = std::max<uint64_t>(1, (want * units + total_units / 2) / total_units / g.npairs);
@@ -1407,7 +1482,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
 uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs) {
     uint64_t b = 0;
     for (uint32_t j = 0; j < njobs; ++j)
-        b += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * unit_bytes(type) * (jobs[j].W2 ? 2 : 1) * jobs[j].npairs;
+        b += uint64_t(jobs[j].rows) * (jobs[j].cols / 256) * unit_bytes(type) * job_mats(jobs[j]) * jobs[j].npairs;
     return b;
 }
 

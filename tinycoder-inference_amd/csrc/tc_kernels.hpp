@@ -35,6 +35,12 @@ struct GemvJob {
     const int32_t *ids = nullptr;
     uint64_t wstride = 0;
     uint32_t npairs = 1, x_div = 1, x_stride = 0, out_stride = 0, n_experts = 0;
+    // Rank-group mode (rk > 0, with ids, single-token launch): pair p is a
+    // token with rk ranks; rank k uses the matrix at W + ids[p*rk+k]*wstride
+    // and input x + p*x_stride + k*cols, and out + p*out_stride receives
+    // sum over k in rank order of wts[p*rk+k] * (that product).
+    uint32_t rk = 0;
+    const float *wts = nullptr;
 };
 
 // out[t][i] = sum over r < top_k, in rank order, of wts[t][r] * y[t*top_k + r][i].
