@@ -27,7 +27,8 @@ def enc_weights(oracle, qt, rng, rows, cols):
 
 # (M tokens, N rows, K cols): ragged tiles, a K-split case (few output tiles),
 # a single token, and a multi-tile case.
-SHAPES = [(1, 64, 256), (37, 200, 1024), (128, 256, 5120), (130, 136, 2048), (300, 384, 768)]
+# (40, 72, 2304): two K-slices of 5 and 4 superblocks (odd and even counts)
+SHAPES = [(1, 64, 256), (37, 200, 1024), (128, 256, 5120), (130, 136, 2048), (300, 384, 768), (40, 72, 2304)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)

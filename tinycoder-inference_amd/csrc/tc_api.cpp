@@ -300,7 +300,7 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
     const size_t ws = tc::gemm_workspace_bytes(type, seq_len, rows, cols, dev->num_cu);
     if (!ensure(dev->act, dev->act_bytes, L.bytes)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", L.bytes);
     if (ws && !ensure(dev->aux, dev->aux_bytes, ws)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", ws);
-    hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, dev->act, st);
+    hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, dev->act, st, true);
     if (e != hipSuccess) return hip_fail(e, "activation quantizer");
     e = tc::launch_gemm(type, w, act_view(dev->act, L, 0, type, cols), out, seq_len, rows, cols, dev->num_cu,
                         ws ? dev->aux : nullptr, st);

@@ -8,10 +8,15 @@
 // with an activation block is exact, and only the final per-block scale
 // combination runs in fp32.
 //
-// Decomposition. One workgroup (8 waves) owns a tile of 128 weight rows x 128
-// tokens and walks K one 256-element superblock at a time (optionally a
-// K-slice of them, for split-K). Per superblock the raw weight rows, the
-// quantized activations and their scales are staged through LDS:
+// Decomposition. One workgroup owns a tile of 64 weight rows x 128 tokens and
+// walks K one 256-element superblock at a time (optionally a K-slice of them,
+// for split-K). The activations arrive block-major (256-column block b of
+// token m at b*M + m), so one superblock of a token tile is one contiguous
+// 32 KB run. Per superblock the raw weight rows, the quantized activations and
+// their scales are staged through LDS. Q4_K runs 8 waves, 4 producers (global
+// loads two superblocks ahead, conversion into one half of a double-buffered
+// LDS) and 4 consumers (MFMAs on the other half); Q8_0 runs 4 waves that do
+// both, two workgroups per CU.
 //
 //  * Q4_K: a weight of sub-block s is w = d*sc_s*q - dmin*m_s (q in 0..15,
 //    sc_s, m_s in 0..63). The product sc_s*q (<= 945) is written to two int8
@@ -37,7 +42,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-constexpr int GT = 256;       // threads per workgroup (4 waves; two workgroups per CU)
+constexpr int GT = 256;       // threads per workgroup (Q8_0; Q4_K has 2*GT, half producers)
 constexpr int GN = 64;        // weight rows per workgroup tile
 constexpr int GM = 128;       // tokens per workgroup tile
 constexpr int PL = 272;       // LDS plane row stride (256 + 16: conflict-free b128 reads)
@@ -123,8 +128,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t grsrc(const void *p, uint64_t 
 }
 
 template <int TYPE>
-__device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0) {
-    const uint32_t tid = threadIdx.x;
+__device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t tid) {
     GSrc g;
     g.w = grsrc(a.W, uint64_t(a.N) * a.row_bytes);
     g.q = grsrc(a.qs, uint64_t(a.M) * a.K);
@@ -132,10 +136,11 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
     g.bs = grsrc(a.bsums, TYPE == kQ8_0 ? 0 : uint64_t(a.M) * (a.K / 16) * 2);
     g.vw = (n0 + tid / 4) * a.row_bytes;
     g.vw2 = g.vw + 16 + 32 * (tid & 3);
-    g.vq = (m0 + tid / 16) * a.K + 16 * (tid & 15);
+    // Activations are block-major: 256-column block b of token m at b * M + m.
+    g.vq = (m0 + tid / 16) * 256 + 16 * (tid & 15);
     const uint32_t ms = m0 + (tid & 255) / 2;
-    g.vbs = TYPE == kQ8_0 ? ms * (a.K / 32) * 4 + 16 * (tid & 1) : ms * (a.K / 16) * 2 + 16 * (tid & 1);
-    g.vd = (m0 + (tid & 127)) * (a.K / 256) * 4;
+    g.vbs = ms * 32 + 16 * (tid & 1);
+    g.vd = (m0 + (tid & 127)) * 4;
 #pragma unroll
     for (int i = 0; i < 5; ++i) {
         const uint32_t c = tid + i * GT, r = c / 17, w = c - r * 17;
@@ -158,19 +163,19 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
     }
 #pragma unroll
     for (int i = 0; i < GM * 16 / GT; ++i)  // chunk tid + 256 i: token + 16 i
-        p.act[i] = __builtin_amdgcn_raw_buffer_load_b128(g.q, g.vq, b * 256 + i * 16 * a.K, 0);
+        p.act[i] = __builtin_amdgcn_raw_buffer_load_b128(g.q, g.vq, b * a.M * 256 + i * 16 * 256, 0);
     if constexpr (TYPE == kQ8_0)
-        p.side = __builtin_amdgcn_raw_buffer_load_b128(g.d, g.vbs, b * 32, 0);
+        p.side = __builtin_amdgcn_raw_buffer_load_b128(g.d, g.vbs, b * a.M * 32, 0);
     else
-        p.side = __builtin_amdgcn_raw_buffer_load_b128(g.bs, g.vbs, b * 32, 0);
-    if constexpr (TYPE == kQ4_K) p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * 4, 0));
+        p.side = __builtin_amdgcn_raw_buffer_load_b128(g.bs, g.vbs, b * a.M * 32, 0);
+    if constexpr (TYPE == kQ4_K) p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * a.M * 4, 0));
 }
 
 // Q4_K weights of this thread (row tid/4: header + qs[32qq .. 32qq+31]) ->
 // the two digit planes, the mins and the row scales.
-__device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u4 &qb, unsigned char *lds) {
+__device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u4 &qb, unsigned char *lds,
+                                            uint32_t tid) {
     using L = GLds<kQ4_K>;
-    const uint32_t tid = threadIdx.x;
     const uint32_t r = tid / 4, qq = tid & 3;
     // the 8 6-bit scales / mins as bytes (reference get_scale_min_k4,
     // GGMLDequantize.hpp:436-447): sub-blocks 0-3 from the low words, 4-7 from
@@ -200,25 +205,21 @@ __device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u
     *reinterpret_cast<u4 *>(a1 + s1 + 16) = u4{lh[4], lh[5], lh[6], lh[7]};
     // 32-byte rows: bytes 0..7 the mins of sub-blocks 0..7, 8..31 zero
     reinterpret_cast<uint16_t *>(lds + L::AM + r * 32)[qq] = uint16_t(mn0 | (mn1 << 8));
-    if (qq < 3) {
-        reinterpret_cast<uint32_t *>(lds + L::AM + r * 32)[2 + 2 * qq] = 0;
-        reinterpret_cast<uint32_t *>(lds + L::AM + r * 32)[3 + 2 * qq] = 0;
-    }
-    if (qq == 0) {
-        reinterpret_cast<float *>(lds + L::AS)[r] = h2f(hdr.x & 0xFFFF);
-        reinterpret_cast<float *>(lds + L::AD)[r] = h2f(hdr.x >> 16);
-    }
+    // Unconditional stores (the threads of a row that overlap write the same
+    // values), so no lane-masked branch splits the producer's wait counts.
+    *reinterpret_cast<uint2 *>(lds + L::AM + r * 32 + 8 + 8 * min(qq, 2u)) = uint2{0u, 0u};
+    reinterpret_cast<float *>(lds + L::AS)[r] = h2f(hdr.x & 0xFFFF);
+    reinterpret_cast<float *>(lds + L::AD)[r] = h2f(hdr.x >> 16);
 }
 
 // Staged registers -> LDS: the activation plane and its side data; Q4_K
 // weights converted to the digit planes straight from registers, Q8_0 raw
 // rows to a staging area (converted after the barrier).
 template <int TYPE>
-__device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned char *lds) {
+__device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned char *lds, uint32_t tid) {
     using L = GLds<TYPE>;
-    const uint32_t tid = threadIdx.x;
     if constexpr (TYPE == kQ4_K) {
-        q4k_convert(p.raw[0], p.raw[1], p.raw[2], lds);
+        q4k_convert(p.raw[0], p.raw[1], p.raw[2], lds, tid);
     } else {
 #pragma unroll
         for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
@@ -260,7 +261,7 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
         }
     }
     if constexpr (TYPE == kQ4_K) {
-        if (tid < GM) reinterpret_cast<float *>(lds + L::BD)[tid] = p.d8;
+        reinterpret_cast<float *>(lds + L::BD)[tid & (GM - 1)] = p.d8;  // threads tid and tid+128 hold the same d
     }
 }
 
@@ -289,6 +290,75 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
+// One superblock of a consumer wave's 32-row x 64-token Q4_K tile from the
+// LDS planes at `lds` (MFMA chains and the fp32 combination into acc).
+__device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t wn, uint32_t wm, uint32_t li,
+                                            uint32_t lg, float (&acc)[2][16]) {
+    using L = GLds<kQ4_K>;
+    const unsigned char *arow = lds + (32 * wn + li) * PL + 16 * lg;
+    const unsigned char *brow0 = lds + L::B + (64 * wm + li) * PL + 16 * lg;
+    const unsigned char *brow1 = brow0 + 32 * PL;
+        // All fragments are read up front so that one LDS latency, not one
+        // per sub-block, precedes the MFMA chains (one consumer wave per SIMD
+        // has no other wave to hide it).
+        v4i ah[8], al[8], x0[8], x1[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            ah[s] = as_v4i(lds4(arow + L::A0 + 32 * s));
+            x0[s] = as_v4i(lds4(brow0 + 32 * s));
+            x1[s] = as_v4i(lds4(brow1 + 32 * s));
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) al[s] = as_v4i(lds4(arow + L::A1 + 32 * s));
+        __builtin_amdgcn_sched_barrier(0);
+        // One accumulator per token tile: the hi-digit chain, then
+        // C = hi << 7 and the lo-digit chain on top (= 128*hi + lo exactly).
+        v16i c0 = {}, c1 = {};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            c0 = mfma(ah[s], x0[s], c0);
+            c1 = mfma(ah[s], x1[s], c1);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            c0[r] <<= 7;
+            c1[r] <<= 7;
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            c0 = mfma(al[s], x0[s], c0);
+            c1 = mfma(al[s], x1[s], c1);
+        }
+        // min term over 8 useful k slots (k-group 0, bytes 0..7), folded the same way
+        const v4i am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
+        const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
+        const v16i z16 = {};
+        v16i m0 = mfma(am, as_v4i(lds4(lds + L::BH + tb0 * 32 + 16 * lg)), z16);
+        v16i m1 = mfma(am, as_v4i(lds4(lds + L::BH + tb1 * 32 + 16 * lg)), z16);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            m0[r] <<= 7;
+            m1[r] <<= 7;
+        }
+        m0 = mfma(am, as_v4i(lds4(lds + L::BL + tb0 * 32 + 16 * lg)), m0);
+        m1 = mfma(am, as_v4i(lds4(lds + L::BL + tb1 * 32 + 16 * lg)), m1);
+        const float d80 = reinterpret_cast<const float *>(lds + L::BD)[tb0];
+        const float d81 = reinterpret_cast<const float *>(lds + L::BD)[tb1];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t rr = 32 * wn + 8 * q + 4 * lg;
+            const float4 dv = *reinterpret_cast<const float4 *>(lds + L::AS + 4 * rr);
+            const float4 mv = *reinterpret_cast<const float4 *>(lds + L::AD + 4 * rr);
+            const float dd[4] = {dv.x, dv.y, dv.z, dv.w}, dm[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * q + e;
+                acc[0][r] = fmaf(d80, dd[e] * float(c0[r]) - dm[e] * float(m0[r]), acc[0][r]);
+                acc[1][r] = fmaf(d81, dd[e] * float(c1[r]) - dm[e] * float(m1[r]), acc[1][r]);
+            }
+        }
+}
+
 template <int TYPE>
 __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -311,11 +381,11 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
-    const GSrc gs = gemm_src<TYPE>(a, n0, m0);
+    const GSrc gs = gemm_src<TYPE>(a, n0, m0, tid);
     GPrefetch<TYPE> pf;
     if (b0 < b1) gemm_prefetch<TYPE>(a, gs, b0, pf);
     for (uint32_t b = b0; b < b1; ++b) {
-        gemm_stage<TYPE>(pf, lds);
+        gemm_stage<TYPE>(pf, lds, tid);
         if (b + 1 < b1) gemm_prefetch<TYPE>(a, gs, b + 1, pf);
         __syncthreads();
         if constexpr (TYPE == kQ8_0) {
@@ -327,54 +397,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const unsigned char *brow0 = lds + L::B + (64 * wm + li) * PL + 16 * lg;
         const unsigned char *brow1 = brow0 + 32 * PL;
         if constexpr (TYPE == kQ4_K) {
-            // One accumulator per token tile: the hi-digit chain, then
-            // C = hi << 7 and the lo-digit chain on top (= 128*hi + lo exactly).
-            v16i c0 = {}, c1 = {};
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const v4i ah = as_v4i(lds4(arow + L::A0 + 32 * s));
-                c0 = mfma(ah, as_v4i(lds4(brow0 + 32 * s)), c0);
-                c1 = mfma(ah, as_v4i(lds4(brow1 + 32 * s)), c1);
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                c0[r] <<= 7;
-                c1[r] <<= 7;
-            }
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const v4i al = as_v4i(lds4(arow + L::A1 + 32 * s));
-                c0 = mfma(al, as_v4i(lds4(brow0 + 32 * s)), c0);
-                c1 = mfma(al, as_v4i(lds4(brow1 + 32 * s)), c1);
-            }
-            // min term over 8 useful k slots (k-group 0, bytes 0..7), folded the same way
-            const v4i am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
-            const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
-            const v16i z16 = {};
-            v16i m0 = mfma(am, as_v4i(lds4(lds + L::BH + tb0 * 32 + 16 * lg)), z16);
-            v16i m1 = mfma(am, as_v4i(lds4(lds + L::BH + tb1 * 32 + 16 * lg)), z16);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                m0[r] <<= 7;
-                m1[r] <<= 7;
-            }
-            m0 = mfma(am, as_v4i(lds4(lds + L::BL + tb0 * 32 + 16 * lg)), m0);
-            m1 = mfma(am, as_v4i(lds4(lds + L::BL + tb1 * 32 + 16 * lg)), m1);
-            const float d80 = reinterpret_cast<const float *>(lds + L::BD)[tb0];
-            const float d81 = reinterpret_cast<const float *>(lds + L::BD)[tb1];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t rr = 32 * wn + 8 * q + 4 * lg;
-                const float4 dv = *reinterpret_cast<const float4 *>(lds + L::AS + 4 * rr);
-                const float4 mv = *reinterpret_cast<const float4 *>(lds + L::AD + 4 * rr);
-                const float dd[4] = {dv.x, dv.y, dv.z, dv.w}, dm[4] = {mv.x, mv.y, mv.z, mv.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * q + e;
-                    acc[0][r] = fmaf(d80, dd[e] * float(c0[r]) - dm[e] * float(m0[r]), acc[0][r]);
-                    acc[1][r] = fmaf(d81, dd[e] * float(c1[r]) - dm[e] * float(m1[r]), acc[1][r]);
-                }
-            }
+            q4k_consume(lds, wn, wm, li, lg, acc);
         } else {
             const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
 #pragma unroll 2
@@ -425,6 +448,92 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     }
 }
 
+// Q4_K with producer and consumer waves: 4 producer waves load superblock
+// b+2 and convert b+1 into one half of a double-buffered LDS while 4 consumer
+// waves run the MFMAs and the fp32 combination of superblock b from the other
+// half -- the conversion's VALU work overlaps the matrix work on the same
+// SIMDs, with one barrier per superblock.
+__global__ __launch_bounds__(2 * GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k_ws(GemmArgs a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    using L = GLds<kQ4_K>;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool producer = wave >= 4;
+    const uint32_t wn = wave & 1, wm = (wave >> 1) & 1;  // consumer: 32-row group, 64-token group
+    const uint32_t li = lane & 31, lg = lane >> 5;
+    const uint32_t ptid = tid - GT;                       // producer thread index 0..255
+
+    const uint32_t tile = blockIdx.x;
+    const uint32_t split = blockIdx.y;
+    const uint32_t tm = tile % a.ntm, tn = tile / a.ntm;
+    const uint32_t n0 = tn * GN, m0 = tm * GM;
+    const uint32_t b0 = split * a.split_blk;
+    const uint32_t b1 = min(b0 + a.split_blk, a.nblk);
+    auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
+    // Producers step in pairs of superblocks; both sides run bend - b0 barriers.
+    const uint32_t nb = b1 > b0 ? b1 - b0 : 0;
+    const uint32_t bend = b0 + ((nb + 1) & ~1u);
+
+    float acc[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+
+    // Producer and consumer waves run separate loops with the same number of
+    // barriers, so neither keeps the other's registers live.
+    if (producer) {
+        // Two superblocks of loads in flight per producer thread: global
+        // latency under load exceeds one superblock's compute time.
+        const GSrc gs = gemm_src<kQ4_K>(a, n0, m0, ptid);
+        GPrefetch<kQ4_K> pa, pb;
+        if (b0 < b1) {
+            gemm_prefetch<kQ4_K>(a, gs, b0, pa);
+            gemm_stage<kQ4_K>(pa, buf(b0), ptid);
+            gemm_prefetch<kQ4_K>(a, gs, min(b0 + 1, b1 - 1), pa);
+            gemm_prefetch<kQ4_K>(a, gs, min(b0 + 2, b1 - 1), pb);
+        }
+        __syncthreads();
+        // Straight-line steps (past the end they stage into the idle buffer and
+        // reload the last superblock), so the compiler's wait counts stay exact.
+        auto step = [&](GPrefetch<kQ4_K> &pf, uint32_t b) __attribute__((always_inline)) {
+            gemm_stage<kQ4_K>(pf, buf(b + 1), ptid);
+            gemm_prefetch<kQ4_K>(a, gs, min(b + 3, b1 - 1), pf);
+            __syncthreads();
+        };
+        for (uint32_t b = b0; b < bend; b += 2) {
+            step(pa, b);
+            step(pb, b + 1);
+        }
+        return;
+    }
+    __syncthreads();
+    for (uint32_t b = b0; b < bend; ++b) {
+        if (b < b1) q4k_consume(buf(b), wn, wm, li, lg, acc);
+        __syncthreads();
+    }
+
+    float *out = a.out + size_t(split) * a.M * a.N;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t m = m0 + 64 * wm + 32 * t + li;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t n = n0 + 32 * wn + 8 * q + 4 * lg;
+            float *o = out + size_t(m) * a.N + n;
+            if (n + 3 < a.N && (a.N & 3) == 0) {
+                *reinterpret_cast<float4 *>(o) = make_float4(acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2],
+                                                             acc[t][4 * q + 3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n + e < a.N) o[e] = acc[t][4 * q + e];
+            }
+        }
+    }
+}
+
 // Split-K partials [nsplit][M][N] -> out[M][N], summed in slice order.
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part, float *__restrict__ out,
                                                      size_t mn, uint32_t nsplit) {
@@ -437,10 +546,17 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
 
 template <int TYPE>
 hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<TYPE>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (attr != hipSuccess) return attr;
-    k_gemm<TYPE><<<grid, GT, GLds<TYPE>::bytes, st>>>(a);
+    if constexpr (TYPE == kQ4_K) {
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_q4k_ws),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (attr != hipSuccess) return attr;
+        k_gemm_q4k_ws<<<grid, 2 * GT, 2 * GLds<TYPE>::bytes, st>>>(a);
+    } else {
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<TYPE>),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (attr != hipSuccess) return attr;
+        k_gemm<TYPE><<<grid, GT, GLds<TYPE>::bytes, st>>>(a);
+    }
     return hipGetLastError();
 }
 
@@ -491,3 +607,4 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
 }
 
 }  // namespace tc
+

@@ -9,8 +9,10 @@ namespace tc {
 // Activation quantizer for weight type `wtype` (Q8_K for the K-quants and
 // IQ3_XXS, 32-wide Q8_0-style for Q8_0) of x[S][cols] into `buf` laid out by
 // act_layout(wtype, S, cols).
+// With block_major the blocks are stored block-major (block j of token t at
+// j * S + t), the layout launch_gemm reads.
 hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols, const ActLayout &L,
-                            void *buf, hipStream_t st);
+                            void *buf, hipStream_t st, bool block_major = false);
 
 // Weight encoder: x[nunits][256] fp32 -> nunits units of `type`.
 hipError_t launch_encode(int type, const float *x, void *out, uint32_t nunits, hipStream_t st);

@@ -15,24 +15,36 @@ __constant__ uint32_t c_iq3xxs_grid[256] = {
 
 // ---- activation quantizers ---------------------------------------------------
 
+// Destination block of source block g (token g / nbk, block g % nbk): the
+// same index (token-major), or block-major (all tokens of 256-column block j
+// together, j * S + token) when S != 0.
+__device__ __forceinline__ uint32_t act_dst_block(uint32_t g, uint32_t nbk, uint32_t S) {
+    if (S == 0) return g;
+    const uint32_t t = g / nbk;
+    return (g - t * nbk) * S + t;
+}
+
 // Q8_K (reference include/GGMLDequantize.hpp:2769-2807): one wave per
 // 256-element block. nblk_total = S * cols / 256 (token rows are contiguous,
 // so block g covers x[256g, 256g+256)).
 __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int8_t *__restrict__ qs,
                                                    float *__restrict__ d, int16_t *__restrict__ bsums,
-                                                   uint32_t nblk_total) {
+                                                   uint32_t nblk_total, uint32_t nbk, uint32_t bm_S) {
     const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (g >= nblk_total) return;
-    quant_q8k_block_wave(x + size_t(g) * 256, qs + size_t(g) * 256, d + g, bsums + size_t(g) * 16);
+    const uint32_t o = act_dst_block(g, nbk, bm_S);
+    quant_q8k_block_wave(x + size_t(g) * 256, qs + size_t(o) * 256, d + o, bsums + size_t(o) * 16);
 }
 
 // 32-wide rule used for Q8_0 weights (reference
 // src/cpp/core/SIMDMatMulVecAVX2.cpp:4296-4326): one wave per 8 blocks.
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int8_t *__restrict__ qs,
-                                                    float *__restrict__ d, uint32_t ngroups) {
+                                                    float *__restrict__ d, uint32_t ngroups, uint32_t nbk,
+                                                    uint32_t bm_S) {
     const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (g >= ngroups) return;
-    quant_q8_0_blocks_wave(x + size_t(g) * 256, qs + size_t(g) * 256, d + size_t(g) * 8);
+    const uint32_t o = act_dst_block(g, nbk, bm_S);
+    quant_q8_0_blocks_wave(x + size_t(g) * 256, qs + size_t(o) * 256, d + size_t(o) * 8);
 }
 
 // ---- fp16 encodings ----------------------------------------------------------
@@ -285,16 +297,17 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
 // ---- launchers -----------------------------------------------------------------
 
 hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols, const ActLayout &L,
-                            void *buf, hipStream_t st) {
+                            void *buf, hipStream_t st, bool block_major) {
+    const uint32_t nbk = cols / 256, bm_S = block_major ? S : 0;
     int8_t *qs = reinterpret_cast<int8_t *>(static_cast<char *>(buf) + L.qs_off);
     float *d = reinterpret_cast<float *>(static_cast<char *>(buf) + L.d_off);
     if (wtype == kQ8_0) {
         const uint32_t ng = S * (cols / 256);
-        k_quant_q8_0<<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, ng);
+        k_quant_q8_0<<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
     } else {
         int16_t *bs = reinterpret_cast<int16_t *>(static_cast<char *>(buf) + L.bs_off);
         const uint32_t nb = S * (cols / 256);
-        k_quant_q8k<<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, nb);
+        k_quant_q8k<<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, nb, nbk, bm_S);
     }
     return hipGetLastError();
 }
