@@ -25,6 +25,11 @@
 
 namespace tc {
 
+// Cache policy of the weight stream: non-temporal (nt). Each weight byte is
+// read once per launch, so its lines are marked for early eviction and the
+// activations and partial sums keep their L2 and Infinity Cache residency.
+constexpr int kWeightCachePolicy = 2;
+
 namespace {
 
 __constant__ uint32_t c_grid[256] = {
@@ -1175,7 +1180,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         static_for<0, NX>([&](auto c) __attribute__((always_inline)) {
             uint32_t voff = lane * 16 + c.value * 1024;
             if constexpr (c.value == NX - 1 && TILE_BYTES % 1024 != 0) voff = voff < TILE_BYTES ? voff : 0x80000000u;
-            reg<decltype(i)::value * NX + c.value>(buf) = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+            reg<decltype(i)::value * NX + c.value>(buf) = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, kWeightCachePolicy);
         });
     };
     // Staged ring: D0 slots are requested before the activations are
