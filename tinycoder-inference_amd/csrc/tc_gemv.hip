@@ -1021,7 +1021,7 @@ struct TDot<kQ6_K, S> {
 template <int S>
 struct TDot<kIQ3_XXS, S> {
     __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
-                                               const uint32_t *grid, float *val, int32_t *dbg, size_t dbg_tok) {
+                                               const uint32_t *sgrid, float *val, int32_t *dbg, size_t dbg_tok) {
         const uint16_t *u16 = reinterpret_cast<const uint16_t *>(u);
         int tot[S];
 #pragma unroll
@@ -1037,11 +1037,9 @@ struct TDot<kIQ3_XXS, S> {
                 const uint32_t idx7 = (aux >> (7 * l)) & 127u;
                 const uint32_t s8 = idx7 | ((__builtin_popcount(idx7) & 1u) << 7);
                 const uint32_t gw = l < 2 ? gi0 : gi1;
-                const uint32_t g1 = grid[(gw >> (16 * (l & 1))) & 0xFF];
-                const uint32_t g2 = grid[(gw >> (16 * (l & 1) + 8)) & 0xFF];
-                const uint32_t m1 = spread_sign4(s8 & 15u), m2 = spread_sign4(s8 >> 4);
-                w[2 * l] = (g1 ^ m1) + (m1 & 0x01010101u);  // grid bytes are nonzero: no carries
-                w[2 * l + 1] = (g2 ^ m2) + (m2 & 0x01010101u);
+                // signed-grid entries (16 * index + sign nibble)
+                w[2 * l] = sgrid[((gw >> (16 * (l & 1))) & 0xFF) * 16 + (s8 & 15u)];
+                w[2 * l + 1] = sgrid[((gw >> (16 * (l & 1) + 8)) & 0xFF) * 16 + (s8 >> 4)];
             }
             const int mult = 2 * int(aux >> 28) + 1;
 #pragma unroll
@@ -1191,7 +1189,14 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     constexpr int D0 = 1;
     static_for<0, D0>([&](auto i) __attribute__((always_inline)) { ld(i, wave + i.value * TNW); });
     if constexpr (TYPE == kIQ3_XXS) {
-        if (tid < 256) reinterpret_cast<uint32_t *>(smem + L.off_g)[tid] = c_grid[tid];
+        // Signed grid: entry 16*i + n is grid[i] with the signs of the 4-bit
+        // pattern n applied bytewise (n's bit k negates byte k).
+        uint32_t *sg = reinterpret_cast<uint32_t *>(smem + L.off_g);
+#pragma unroll
+        for (uint32_t e = tid; e < 4096u; e += TNT) {
+            const uint32_t g = c_grid[e >> 4], m = spread_sign4(e & 15u);
+            sg[e] = (g ^ m) + (m & 0x01010101u);  // grid bytes are nonzero: no carries
+        }
     }
     TC_TRACE_PT(4);
     tstage_finish<TYPE, S, TNT>(jb, xrs, xp, xr);
@@ -1387,7 +1392,7 @@ template <class C>
 uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     uint32_t o = S * (cols / 256) * XB;
     a->off_g = o;
-    if (type == kIQ3_XXS) o += 1024;
+    if (type == kIQ3_XXS) o += 16384;  // signed grid, 256 x 16 words
     a->off_t = o;
     o += (C::NT / 64) * tile_slot_bytes(type);
     a->off_p = o;
