@@ -1142,8 +1142,13 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     // buffer, after which the slot refills with tile k+D. D-1 tiles stay in
     // flight while one is decoded. Copies and refills are unconditional so
     // every path issues the same loads and the in-order vmcnt bookkeeping never
-    // drains at a control-flow join.
+    // drains at a control-flow join. (A dynamic schedule -- waves taking tiles
+    // from an LDS counter -- measured no faster: a workgroup finishes when its
+    // last bytes arrive, whichever wave decodes them.)
     const uint32_t nmine = wave < ntiles ? (ntiles - wave + TNW - 1) / TNW : 0;
+    // IQ3_XXS grid words, requested ahead of everything else
+    uint32_t gword = 0;
+    if constexpr (TYPE == kIQ3_XXS) gword = c_grid[tid & 255];
     const XRsrc xrs = tstage_rsrc<TYPE, S>(jb);
     const XPre xp = tstage_preload<TYPE, S, TNT>(jb, xrs);
 #ifndef TC_NO_XBAR
@@ -1191,11 +1196,17 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     if constexpr (TYPE == kIQ3_XXS) {
         // Signed grid: entry 16*i + n is grid[i] with the signs of the 4-bit
         // pattern n applied bytewise (n's bit k negates byte k).
-        uint32_t *sg = reinterpret_cast<uint32_t *>(smem + L.off_g);
+        if (tid < 256) {
+            u32x4 *sg = reinterpret_cast<u32x4 *>(smem + L.off_g + tid * 64);
+            static_for<0, 4>([&](auto q) __attribute__((always_inline)) {
+                uint32_t e[4];
 #pragma unroll
-        for (uint32_t e = tid; e < 4096u; e += TNT) {
-            const uint32_t g = c_grid[e >> 4], m = spread_sign4(e & 15u);
-            sg[e] = (g ^ m) + (m & 0x01010101u);  // grid bytes are nonzero: no carries
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t m = spread_sign4(4u * decltype(q)::value + j);
+                    e[j] = (gword ^ m) + (m & 0x01010101u);  // grid bytes are nonzero: no carries
+                }
+                sg[decltype(q)::value] = u32x4{e[0], e[1], e[2], e[3]};
+            });
         }
     }
     TC_TRACE_PT(4);
