@@ -28,6 +28,9 @@ namespace tc {
 // Cache policy of the weight stream: non-temporal (nt). Each weight byte is
 // read once per launch, so its lines are marked for early eviction and the
 // activations and partial sums keep their L2 and Infinity Cache residency.
+// MoE expert launches keep the default policy: an expert chosen by several
+// tokens is read once per (token, rank) pair, and the later reads hit the
+// Infinity Cache.
 constexpr int kWeightCachePolicy = 2;
 
 namespace {
@@ -1067,7 +1070,7 @@ struct TDot<kIQ3_XXS, S> {
     }
 };
 
-template <int TYPE, int S, bool DBG, class C, bool RG = false>
+template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1183,7 +1186,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         static_for<0, NX>([&](auto c) __attribute__((always_inline)) {
             uint32_t voff = lane * 16 + c.value * 1024;
             if constexpr (c.value == NX - 1 && TILE_BYTES % 1024 != 0) voff = voff < TILE_BYTES ? voff : 0x80000000u;
-            reg<decltype(i)::value * NX + c.value>(buf) = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, kWeightCachePolicy);
+            reg<decltype(i)::value * NX + c.value>(buf) = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, KEEP ? 0 : kWeightCachePolicy);
         });
     };
     // Staged ring: D0 slots are requested before the activations are
@@ -1316,13 +1319,14 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     TC_TRACE_PT(3);
 }
 
-template <int TYPE, int S, bool DBG, class C, bool RG = false>
+template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false>
 hipError_t launch_tiled_sd(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
     // Dynamic LDS above 64 KB needs the per-kernel opt-in, once per process.
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG, C, RG>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG, C, RG, KEEP>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        160 * 1024);
     if (attr != hipSuccess) return attr;
-    k_gemv_t<TYPE, S, DBG, C, RG><<<g, C::NT, lds, st>>>(a);
+    k_gemv_t<TYPE, S, DBG, C, RG, KEEP><<<g, C::NT, lds, st>>>(a);
     return hipSuccess;
 }
 
@@ -1330,19 +1334,23 @@ template <int TYPE, int S, class C>
 hipError_t launch_tiled_s(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
     // The per-block integer-sum test hook is its own instantiation: its
     // global stores would otherwise sit in the production loop. So is the
-    // MoE rank-group mode (Q4_K experts, one token per launch).
-    bool dbg = false, rg = false;
+    // MoE rank-group mode (Q4_K experts, one token per launch), and the
+    // Q4_K one-token expert-pair launches (default cache policy).
+    bool dbg = false, rg = false, experts = false;
     for (uint32_t j = 0; j < a.njobs; ++j) {
         dbg = dbg || a.jobs[j].dbg != nullptr;
         rg = rg || a.jobs[j].rk != 0;
+        experts = experts || a.jobs[j].ids != nullptr;
     }
     if (rg) {
         if constexpr (TYPE == kQ4_K && S == 1) {
             if (dbg || a.njobs != 1) return hipErrorInvalidValue;
-            return launch_tiled_sd<TYPE, S, false, C, true>(a, g, lds, st);
+            return launch_tiled_sd<TYPE, S, false, C, true, true>(a, g, lds, st);
         }
         return hipErrorInvalidValue;
     }
+    if constexpr (TYPE == kQ4_K && S == 1)
+        if (experts && !dbg) return launch_tiled_sd<TYPE, S, false, C, false, true>(a, g, lds, st);
     return dbg ? launch_tiled_sd<TYPE, S, true, C>(a, g, lds, st) : launch_tiled_sd<TYPE, S, false, C>(a, g, lds, st);
 }
 
