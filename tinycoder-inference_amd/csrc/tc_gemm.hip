@@ -58,8 +58,11 @@ struct GLds {
     static constexpr uint32_t AM = A1 + (K ? GN * PL : 0);            // Q4_K mins, 8 bytes + 24 zero [GN][32]
     static constexpr uint32_t AS = AM + (K ? GN * 32 : 0);            // Q4_K d [GN] | Q8_0 dw [GN][8]
     static constexpr uint32_t AD = AS + (K ? GN * 4 : GN * 32);       // Q4_K dmin [GN]
-    static constexpr uint32_t B = AD + (K ? GN * 4 : 0);              // activation int8 [GM][PL]
-    static constexpr uint32_t BL = B + GM * PL;                       // Q4_K pair-sum low digits, 8 + 24 zero [GM][32]
+    // activation int8 [GM][BP]; Q4_K: 256-byte rows, 16-byte chunk j of
+    // token t at slot j ^ (t & 15) (written by direct-to-LDS loads)
+    static constexpr uint32_t BP = K ? 256 : PL;
+    static constexpr uint32_t B = AD + (K ? GN * 4 : 0);
+    static constexpr uint32_t BL = B + GM * BP;                       // Q4_K pair-sum low digits, 8 + 24 zero [GM][32]
     static constexpr uint32_t BH = BL + (K ? GM * 32 : 0);            // Q4_K pair-sum high digits [GM][32]
     static constexpr uint32_t BD = BH + (K ? GM * 32 : 0);            // Q8_K d [GM] | Q8_0 d [GM][8]
     static constexpr uint32_t RAW = BD + (K ? GM * 4 : GM * 32);      // Q8_0 raw weight tile [GN][272]
@@ -109,7 +112,8 @@ struct GPrefetch {
     // (row tid/4, quarter tid%4); Q8_0: raw 16-byte chunks of the tile.
     static constexpr int RAWC = TYPE == kQ4_K ? 3 : (GN * 272 / 16 + GT - 1) / GT;
     u4 raw[RAWC];
-    u4 act[GM * 16 / GT];  // 16-byte activation chunks
+    static constexpr int ACTC = TYPE == kQ8_0 ? GM * 16 / GT : 0;
+    u4 act[ACTC > 0 ? ACTC : 1];  // 16-byte activation chunks (Q8_0; Q4_K loads them straight into LDS)
     u4 side;               // Q8_K bsums (256 chunks) or Q8_0 d (256 chunks)
     float d8;              // Q8_K d (128 tokens)
 };
@@ -162,7 +166,7 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
             p.raw[i] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vr[i], b * UB, 0);
     }
 #pragma unroll
-    for (int i = 0; i < GM * 16 / GT; ++i)  // chunk tid + 256 i: token + 16 i
+    for (int i = 0; i < GPrefetch<TYPE>::ACTC; ++i)  // chunk tid + 256 i: token + 16 i
         p.act[i] = __builtin_amdgcn_raw_buffer_load_b128(g.q, g.vq, b * a.M * 256 + i * 16 * 256, 0);
     if constexpr (TYPE == kQ8_0)
         p.side = __builtin_amdgcn_raw_buffer_load_b128(g.d, g.vbs, b * a.M * 32, 0);
@@ -228,7 +232,7 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
         }
     }
 #pragma unroll
-    for (int i = 0; i < GM * 16 / GT; ++i) {
+    for (int i = 0; i < GPrefetch<TYPE>::ACTC; ++i) {
         const uint32_t c = tid + i * GT;
         *reinterpret_cast<u4 *>(lds + L::B + (c / 16) * PL + 16 * (c & 15)) = p.act[i];
     }
@@ -290,60 +294,76 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
+// The activation plane of superblock b of this tile straight into LDS
+// (buffer loads with the LDS destination: no registers, no LDS stores). Each
+// wave instruction fills 1 KB = 4 token rows; lane l of wave w, instruction i
+// writes token t = 16i + 4w + l/16, slot l%16, and so reads chunk
+// (l%16) ^ (t%16) of that token's 256 bytes. Tokens past M read the next
+// superblock's bytes (their outputs are never stored); past the buffer, zeros.
+__device__ __forceinline__ void q4k_act_to_lds(const GemmArgs &a, uint32_t m0, uint32_t b, unsigned char *ldsb,
+                                               uint32_t w, uint32_t lane) {
+    using L = GLds<kQ4_K>;
+    typedef int v4i32 __attribute__((ext_vector_type(4)));
+    const uint64_t base = reinterpret_cast<uint64_t>(a.qs);
+    const v4i32 rs = {int(uint32_t(base)), int(uint32_t(base >> 32) & 0xFFFF), int(a.M * a.K), 0x00020000};
+    const uint32_t t0 = 4 * w + lane / 16;  // = t % 16
+    const uint32_t voff = (m0 + t0) * 256 + 16 * ((lane & 15) ^ t0);
+    const uint32_t dst =
+        uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)(ldsb + L::B))) + 1024 * w;
+    // Inline so that the compiler, which cannot tell which LDS bytes these
+    // loads write, does not wait for them before this wave's next LDS reads
+    // (of the other buffer); the caller waits (vmcnt) before the barrier.
+#pragma unroll
+    for (uint32_t i = 0; i < GM / 16; ++i)
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :
+                     : "s"(dst + 4096 * i), "v"(voff), "s"(rs), "s"(b * a.M * 256 + i * 4096)
+                     : "memory", "m0");
+}
+
 // One superblock of a consumer wave's 32-row x 64-token Q4_K tile from the
 // LDS planes at `lds` (MFMA chains and the fp32 combination into acc).
 __device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t wn, uint32_t wm, uint32_t li,
                                             uint32_t lg, float (&acc)[2][16]) {
     using L = GLds<kQ4_K>;
     const unsigned char *arow = lds + (32 * wn + li) * PL + 16 * lg;
-    const unsigned char *brow0 = lds + L::B + (64 * wm + li) * PL + 16 * lg;
-    const unsigned char *brow1 = brow0 + 32 * PL;
-        // All fragments are read up front so that one LDS latency, not one
-        // per sub-block, precedes the MFMA chains (one consumer wave per SIMD
-        // has no other wave to hide it).
-        v4i ah[8], al[8], x0[8], x1[8];
+    // token rows 64wm + li and +32 (same t % 16 = li % 16)
+    const unsigned char *brow0 = lds + L::B + (64 * wm + li) * L::BP;
+    const unsigned char *brow1 = brow0 + 32 * L::BP;
+    auto bslot = [&](int s) __attribute__((always_inline)) { return 16u * ((2u * s + lg) ^ (li & 15)); };
+    // Token tile 0's fragments are read up front (one LDS latency, not one
+    // per sub-block); tile 1's are read while tile 0's MFMA chains run, and
+    // tile 0's fp32 combination runs while tile 1's chains do.
+    const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
+    v4i ah[8], al[8], x0[8], x1[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            ah[s] = as_v4i(lds4(arow + L::A0 + 32 * s));
-            x0[s] = as_v4i(lds4(brow0 + 32 * s));
-            x1[s] = as_v4i(lds4(brow1 + 32 * s));
-        }
+    for (int s = 0; s < 8; ++s) {
+        ah[s] = as_v4i(lds4(arow + L::A0 + 32 * s));
+        x0[s] = as_v4i(lds4(brow0 + bslot(s)));
+    }
 #pragma unroll
-        for (int s = 0; s < 8; ++s) al[s] = as_v4i(lds4(arow + L::A1 + 32 * s));
-        __builtin_amdgcn_sched_barrier(0);
-        // One accumulator per token tile: the hi-digit chain, then
-        // C = hi << 7 and the lo-digit chain on top (= 128*hi + lo exactly).
-        v16i c0 = {}, c1 = {};
+    for (int s = 0; s < 8; ++s) al[s] = as_v4i(lds4(arow + L::A1 + 32 * s));
+    const v4i am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
+    const v4i bh0 = as_v4i(lds4(lds + L::BH + tb0 * 32 + 16 * lg));
+    const v4i bl0 = as_v4i(lds4(lds + L::BL + tb0 * 32 + 16 * lg));
+    __builtin_amdgcn_sched_barrier(0);
+    // One accumulator per token tile: the hi-digit chain, then C = hi << 7
+    // and the lo-digit chain on top (= 128*hi + lo exactly); the min term over
+    // the 8 useful k slots (k-group 0, bytes 0..7) folded the same way.
+    auto chain = [&](const v4i(&x)[8], v4i bh, v4i bl, v16i &c, v16i &m) __attribute__((always_inline)) {
+        c = v16i{};
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            c0 = mfma(ah[s], x0[s], c0);
-            c1 = mfma(ah[s], x1[s], c1);
-        }
+        for (int s = 0; s < 8; ++s) c = mfma(ah[s], x[s], c);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            c0[r] <<= 7;
-            c1[r] <<= 7;
-        }
+        for (int r = 0; r < 16; ++r) c[r] <<= 7;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            c0 = mfma(al[s], x0[s], c0);
-            c1 = mfma(al[s], x1[s], c1);
-        }
-        // min term over 8 useful k slots (k-group 0, bytes 0..7), folded the same way
-        const v4i am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
-        const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
-        const v16i z16 = {};
-        v16i m0 = mfma(am, as_v4i(lds4(lds + L::BH + tb0 * 32 + 16 * lg)), z16);
-        v16i m1 = mfma(am, as_v4i(lds4(lds + L::BH + tb1 * 32 + 16 * lg)), z16);
+        for (int s = 0; s < 8; ++s) c = mfma(al[s], x[s], c);
+        m = mfma(am, bh, v16i{});
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            m0[r] <<= 7;
-            m1[r] <<= 7;
-        }
-        m0 = mfma(am, as_v4i(lds4(lds + L::BL + tb0 * 32 + 16 * lg)), m0);
-        m1 = mfma(am, as_v4i(lds4(lds + L::BL + tb1 * 32 + 16 * lg)), m1);
-        const float d80 = reinterpret_cast<const float *>(lds + L::BD)[tb0];
-        const float d81 = reinterpret_cast<const float *>(lds + L::BD)[tb1];
+        for (int r = 0; r < 16; ++r) m[r] <<= 7;
+        m = mfma(am, bl, m);
+    };
+    auto combine = [&](int t, float d8, const v16i &c, const v16i &m) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t rr = 32 * wn + 8 * q + 4 * lg;
@@ -353,10 +373,21 @@ __device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t w
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = 4 * q + e;
-                acc[0][r] = fmaf(d80, dd[e] * float(c0[r]) - dm[e] * float(m0[r]), acc[0][r]);
-                acc[1][r] = fmaf(d81, dd[e] * float(c1[r]) - dm[e] * float(m1[r]), acc[1][r]);
+                acc[t][r] = fmaf(d8, dd[e] * float(c[r]) - dm[e] * float(m[r]), acc[t][r]);
             }
         }
+    };
+    v16i c0, m0, c1, m1;
+    chain(x0, bh0, bl0, c0, m0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) x1[s] = as_v4i(lds4(brow1 + bslot(s)));
+    const v4i bh1 = as_v4i(lds4(lds + L::BH + tb1 * 32 + 16 * lg));
+    const v4i bl1 = as_v4i(lds4(lds + L::BL + tb1 * 32 + 16 * lg));
+    const float d80 = reinterpret_cast<const float *>(lds + L::BD)[tb0];
+    const float d81 = reinterpret_cast<const float *>(lds + L::BD)[tb1];
+    chain(x1, bh1, bl1, c1, m1);
+    combine(0, d80, c0, m0);
+    combine(1, d81, c1, m1);
 }
 
 template <int TYPE>
@@ -507,9 +538,17 @@ __global__ __launch_bounds__(2 * GT) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         }
         return;
     }
+    // Consumers fill the activation planes: superblock b+1 goes into the
+    // other buffer while b is multiplied (their only memory loads, so the
+    // wait before each barrier waits for nothing else).
+    const uint32_t cw = wave;  // consumer wave 0..3
+    if (b0 < b1) q4k_act_to_lds(a, m0, b0, buf(b0), cw, lane);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     for (uint32_t b = b0; b < bend; ++b) {
+        q4k_act_to_lds(a, m0, min(b + 1, b1 - 1), buf(b + 1), cw, lane);
         if (b < b1) q4k_consume(buf(b), wn, wm, li, lg, acc);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this superblock's plane is in LDS
         __syncthreads();
     }
 
