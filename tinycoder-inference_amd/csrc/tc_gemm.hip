@@ -34,6 +34,9 @@
 // same k positions of both; the 32x32 int32 result holds row
 // 8*(r/4) + 4*(l>>5) + (r%4) and column (l & 31) in register r.
 #include "tc_kernels.hpp"
+#ifndef TC_GEMM_CW
+#define TC_GEMM_CW 8
+#endif
 
 namespace tc {
 namespace {
@@ -296,61 +299,63 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
 
 // The activation plane of superblock b of this tile straight into LDS
 // (buffer loads with the LDS destination: no registers, no LDS stores). Each
-// wave instruction fills 1 KB = 4 token rows; lane l of wave w, instruction i
-// writes token t = 16i + 4w + l/16, slot l%16, and so reads chunk
-// (l%16) ^ (t%16) of that token's 256 bytes. Tokens past M read the next
+// wave instruction fills 1 KB = 4 token rows; lane l writes slot l%16 of
+// token 4k + l/16 and so reads chunk (l%16) ^ (t%16) of its 256 bytes. Tokens past M read the next
 // superblock's bytes (their outputs are never stored); past the buffer, zeros.
+template <int CW>
 __device__ __forceinline__ void q4k_act_to_lds(const GemmArgs &a, uint32_t m0, uint32_t b, unsigned char *ldsb,
                                                uint32_t w, uint32_t lane) {
     using L = GLds<kQ4_K>;
     typedef int v4i32 __attribute__((ext_vector_type(4)));
     const uint64_t base = reinterpret_cast<uint64_t>(a.qs);
     const v4i32 rs = {int(uint32_t(base)), int(uint32_t(base >> 32) & 0xFFFF), int(a.M * a.K), 0x00020000};
-    const uint32_t t0 = 4 * w + lane / 16;  // = t % 16
-    const uint32_t voff = (m0 + t0) * 256 + 16 * ((lane & 15) ^ t0);
+    // wave w, instruction i fills 1 KB block k = CW*i + w: tokens 4k..4k+3
+    const uint32_t t0 = (4 * w + lane / 16) & 15;  // = t % 16 (CW*4*i is a multiple of 16)
+    const uint32_t voff = (m0 + 4 * w + lane / 16) * 256 + 16 * ((lane & 15) ^ t0);
     const uint32_t dst =
         uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)(ldsb + L::B))) + 1024 * w;
     // Inline so that the compiler, which cannot tell which LDS bytes these
     // loads write, does not wait for them before this wave's next LDS reads
     // (of the other buffer); the caller waits (vmcnt) before the barrier.
 #pragma unroll
-    for (uint32_t i = 0; i < GM / 16; ++i)
+    for (uint32_t i = 0; i < 32 / CW; ++i)
         asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                      :
-                     : "s"(dst + 4096 * i), "v"(voff), "s"(rs), "s"(b * a.M * 256 + i * 4096)
+                     : "s"(dst + 1024 * CW * i), "v"(voff), "s"(rs), "s"(b * a.M * 256 + i * 1024 * CW)
                      : "memory", "m0");
 }
 
-// One superblock of a consumer wave's 32-row x 64-token Q4_K tile from the
-// LDS planes at `lds` (MFMA chains and the fp32 combination into acc).
-__device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t wn, uint32_t wm, uint32_t li,
-                                            uint32_t lg, float (&acc)[2][16]) {
+// One superblock of a consumer wave's 32-row x (32 NTT)-token Q4_K tile from
+// the LDS planes at `lds` (MFMA chains and the fp32 combination into acc).
+// tok0: the wave's first token row in the tile.
+template <int NTT>
+__device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t wn, uint32_t tok0, uint32_t li,
+                                            uint32_t lg, float (&acc)[NTT][16]) {
     using L = GLds<kQ4_K>;
     const unsigned char *arow = lds + (32 * wn + li) * PL + 16 * lg;
-    // token rows 64wm + li and +32 (same t % 16 = li % 16)
-    const unsigned char *brow0 = lds + L::B + (64 * wm + li) * L::BP;
-    const unsigned char *brow1 = brow0 + 32 * L::BP;
+    // token rows tok0 + 32t + li (all with t % 16 = li % 16)
+    auto brow = [&](int t) __attribute__((always_inline)) { return lds + L::B + (tok0 + 32 * t + li) * L::BP; };
     auto bslot = [&](int s) __attribute__((always_inline)) { return 16u * ((2u * s + lg) ^ (li & 15)); };
     // Token tile 0's fragments are read up front (one LDS latency, not one
     // per sub-block); tile 1's are read while tile 0's MFMA chains run, and
     // tile 0's fp32 combination runs while tile 1's chains do.
-    const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
-    v4i ah[8], al[8], x0[8], x1[8];
+    v4i ah[8], al[8], x[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         ah[s] = as_v4i(lds4(arow + L::A0 + 32 * s));
-        x0[s] = as_v4i(lds4(brow0 + bslot(s)));
+        x[s] = as_v4i(lds4(brow(0) + bslot(s)));
     }
 #pragma unroll
     for (int s = 0; s < 8; ++s) al[s] = as_v4i(lds4(arow + L::A1 + 32 * s));
     const v4i am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
-    const v4i bh0 = as_v4i(lds4(lds + L::BH + tb0 * 32 + 16 * lg));
-    const v4i bl0 = as_v4i(lds4(lds + L::BL + tb0 * 32 + 16 * lg));
     __builtin_amdgcn_sched_barrier(0);
     // One accumulator per token tile: the hi-digit chain, then C = hi << 7
     // and the lo-digit chain on top (= 128*hi + lo exactly); the min term over
     // the 8 useful k slots (k-group 0, bytes 0..7) folded the same way.
-    auto chain = [&](const v4i(&x)[8], v4i bh, v4i bl, v16i &c, v16i &m) __attribute__((always_inline)) {
+    auto chain = [&](int t, v16i &c, v16i &m) __attribute__((always_inline)) {
+        const uint32_t tb = tok0 + 32 * t + li;
+        const v4i bh = as_v4i(lds4(lds + L::BH + tb * 32 + 16 * lg));
+        const v4i bl = as_v4i(lds4(lds + L::BL + tb * 32 + 16 * lg));
         c = v16i{};
 #pragma unroll
         for (int s = 0; s < 8; ++s) c = mfma(ah[s], x[s], c);
@@ -363,7 +368,8 @@ __device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t w
         for (int r = 0; r < 16; ++r) m[r] <<= 7;
         m = mfma(am, bl, m);
     };
-    auto combine = [&](int t, float d8, const v16i &c, const v16i &m) __attribute__((always_inline)) {
+    auto combine = [&](int t, const v16i &c, const v16i &m) __attribute__((always_inline)) {
+        const float d8 = reinterpret_cast<const float *>(lds + L::BD)[tok0 + 32 * t + li];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t rr = 32 * wn + 8 * q + 4 * lg;
@@ -377,17 +383,18 @@ __device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t w
             }
         }
     };
-    v16i c0, m0, c1, m1;
-    chain(x0, bh0, bl0, c0, m0);
+    v16i c0, m0;
+    chain(0, c0, m0);
+    if constexpr (NTT == 2) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) x1[s] = as_v4i(lds4(brow1 + bslot(s)));
-    const v4i bh1 = as_v4i(lds4(lds + L::BH + tb1 * 32 + 16 * lg));
-    const v4i bl1 = as_v4i(lds4(lds + L::BL + tb1 * 32 + 16 * lg));
-    const float d80 = reinterpret_cast<const float *>(lds + L::BD)[tb0];
-    const float d81 = reinterpret_cast<const float *>(lds + L::BD)[tb1];
-    chain(x1, bh1, bl1, c1, m1);
-    combine(0, d80, c0, m0);
-    combine(1, d81, c1, m1);
+        for (int s = 0; s < 8; ++s) x[s] = as_v4i(lds4(brow(1) + bslot(s)));
+        v16i c1, m1;
+        chain(1, c1, m1);
+        combine(0, c0, m0);
+        combine(1, c1, m1);
+    } else {
+        combine(0, c0, m0);
+    }
 }
 
 template <int TYPE>
@@ -428,7 +435,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const unsigned char *brow0 = lds + L::B + (64 * wm + li) * PL + 16 * lg;
         const unsigned char *brow1 = brow0 + 32 * PL;
         if constexpr (TYPE == kQ4_K) {
-            q4k_consume(lds, wn, wm, li, lg, acc);
+            static_assert(TYPE != kQ4_K, "Q4_K runs k_gemm_q4k_ws");
         } else {
             const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
 #pragma unroll 2
@@ -484,15 +491,19 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 // waves run the MFMAs and the fp32 combination of superblock b from the other
 // half -- the conversion's VALU work overlaps the matrix work on the same
 // SIMDs, with one barrier per superblock.
-__global__ __launch_bounds__(2 * GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_q4k_ws(GemmArgs a) {
+template <int CW>
+__global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 + CW / 4, 1 + CW / 4))) void k_gemm_q4k_ws(
+    GemmArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
     using L = GLds<kQ4_K>;
+    constexpr int NTT = 8 / CW;  // 32-token tiles per consumer wave
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool producer = wave >= 4;
-    const uint32_t wn = wave & 1, wm = (wave >> 1) & 1;  // consumer: 32-row group, 64-token group
+    const bool producer = wave >= CW;
+    // consumer: 32-row group wn, token rows 32*NTT*wm ..
+    const uint32_t wn = wave & 1, wm = (wave >> 1) & (CW / 2 - 1), tok0 = 32 * NTT * wm;
     const uint32_t li = lane & 31, lg = lane >> 5;
-    const uint32_t ptid = tid - GT;                       // producer thread index 0..255
+    const uint32_t ptid = tid - 64 * CW;  // producer thread index 0..255
 
     const uint32_t tile = blockIdx.x;
     const uint32_t split = blockIdx.y;
@@ -505,9 +516,9 @@ __global__ __launch_bounds__(2 * GT) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const uint32_t nb = b1 > b0 ? b1 - b0 : 0;
     const uint32_t bend = b0 + ((nb + 1) & ~1u);
 
-    float acc[2][16];
+    float acc[NTT][16];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NTT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
@@ -541,21 +552,20 @@ __global__ __launch_bounds__(2 * GT) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // Consumers fill the activation planes: superblock b+1 goes into the
     // other buffer while b is multiplied (their only memory loads, so the
     // wait before each barrier waits for nothing else).
-    const uint32_t cw = wave;  // consumer wave 0..3
-    if (b0 < b1) q4k_act_to_lds(a, m0, b0, buf(b0), cw, lane);
+    if (b0 < b1) q4k_act_to_lds<CW>(a, m0, b0, buf(b0), wave, lane);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     for (uint32_t b = b0; b < bend; ++b) {
-        q4k_act_to_lds(a, m0, min(b + 1, b1 - 1), buf(b + 1), cw, lane);
-        if (b < b1) q4k_consume(buf(b), wn, wm, li, lg, acc);
+        q4k_act_to_lds<CW>(a, m0, min(b + 1, b1 - 1), buf(b + 1), wave, lane);
+        if (b < b1) q4k_consume<NTT>(buf(b), wn, tok0, li, lg, acc);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this superblock's plane is in LDS
         __syncthreads();
     }
 
     float *out = a.out + size_t(split) * a.M * a.N;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const uint32_t m = m0 + 64 * wm + 32 * t + li;
+    for (int t = 0; t < NTT; ++t) {
+        const uint32_t m = m0 + tok0 + 32 * t + li;
         if (m >= a.M) continue;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -586,10 +596,11 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
 template <int TYPE>
 hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
     if constexpr (TYPE == kQ4_K) {
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_q4k_ws),
+        constexpr int CW = TC_GEMM_CW;
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_q4k_ws<CW>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (attr != hipSuccess) return attr;
-        k_gemm_q4k_ws<<<grid, 2 * GT, 2 * GLds<TYPE>::bytes, st>>>(a);
+        k_gemm_q4k_ws<CW><<<grid, GT + 64 * CW, 2 * GLds<TYPE>::bytes, st>>>(a);
     } else {
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<TYPE>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
