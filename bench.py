@@ -152,6 +152,37 @@ def timed(torch, fn, n):
     return a.elapsed_time(b) * 1e3 / n
 
 
+def roof_probes(torch, tc, tc_hip, dev):
+    """What this part sustains, measured in the same run: the int8 MFMA rate
+    from registers (tc_probe_mfma_i8), and the HBM read rate of a plain
+    streaming kernel (tc_probe_read: non-temporal 16-byte loads, one
+    contiguous chunk per workgroup, no decode work) over 2 GiB and at the
+    byte counts of the decode launches (rotating buffers, back-to-back
+    launches): the ceiling a single launch of that size can reach."""
+    sink = torch.empty(tc.lib.tc_probe_sink_bytes(), dtype=torch.uint8, device=dev)
+    st = tc._stream()
+    wgs, iters = 2048, 2000
+    mf = timed(torch, lambda i: tc._check(tc.lib.tc_probe_mfma_i8(wgs, iters, tc_hip._ptr(sink), st)), 5)
+    mfma_tops = wgs * 4 * 4 * iters * 65536 / mf / 1e6
+    read = {}
+    for name, nbytes, nbuf in (("2GiB", 2 << 30, 1), ("gate_up", 76562432, 12), ("down", 38281216, 16),
+                               ("o", 7254016, 32)):
+        nbytes = nbytes // 16384 * 16384
+        bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+        best = 0.0
+        for nwg in (256, 512, 1024):
+            us = timed(torch, lambda i: tc._check(tc.lib.tc_probe_read(tc_hip._ptr(bufs[i % nbuf]), nbytes, nwg,
+                                                                       tc_hip._ptr(sink), st)), 5 if nbuf == 1 else 60)
+            best = max(best, nbytes / us / 1e3)
+        read[name] = {"GB/s": round(best, 1), "frac": round(best / HBM_PEAK_GBS, 4)}
+        del bufs
+        torch.cuda.empty_cache()
+    del sink
+    return {"int8_mfma_TOPS": round(mfma_tops, 1), "hbm_read": read,
+            "note": "tc_probe_mfma_i8: v_mfma_i32_32x32x32_i8 from registers, 4 chains x 2 waves per SIMD; "
+                    "tc_probe_read: each buffer read once per launch, best of 256/512/1024 workgroups"}
+
+
 def other_decode_bench(torch, tc, tc_hip, dev, reps):
     """BASELINE configs #1 and #3 (batch-1 decode mat-vecs of other formats):
     weights N(0,0.02) through the GPU encoders, rotating copies so that every
@@ -402,6 +433,7 @@ def main():
         best = max(g, key=lambda r: r["TOPS"])
         line["prefill_gemm"] = {"unit": "TOPS (2*M*N*K / time, int8 MFMA; includes the activation quantizer)",
                                 "peak_TOPS": INT8_PEAK_TOPS, "best": best, "configs": g}
+    line["roof_probes"] = roof_probes(torch, tc, tc_hip, dev)
     if not args.no_cpu:
         wh = {n: base[n].cpu().numpy() for n in base}
         xh = {g: xs[g].cpu().numpy() for g in xs}

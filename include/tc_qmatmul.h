@@ -159,6 +159,16 @@ int tc_debug_q8_0_blocks(const uint8_t *w_row, uint32_t blocks_per_row, const fl
 /* Message for the calling thread's last failed call ("" if none). */
 const char *tc_last_error(void);
 
+/* Roof probes (no counterpart in the reference: measurement aids for reading
+ * the kernels' rates). `sink` is device scratch of tc_probe_sink_bytes().
+ * tc_probe_mfma_i8: workgroups x 256 threads, each wave issuing 4*iters
+ * v_mfma_i32_32x32x32_i8 (65536 int8 ops each) from registers.
+ * tc_probe_read: reads `bytes` of `buf` once with 16-byte non-temporal loads,
+ * one contiguous chunk per workgroup of 512 threads. Time them with events. */
+size_t tc_probe_sink_bytes(void);
+int tc_probe_mfma_i8(uint32_t workgroups, uint32_t iters, void *sink, void *stream);
+int tc_probe_read(const void *buf, size_t bytes, uint32_t workgroups, void *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -319,10 +319,16 @@ __device__ __forceinline__ void q4k_act_to_lds(const GemmArgs &a, uint32_t m0, u
     // (of the other buffer); the caller waits (vmcnt) before the barrier.
 #pragma unroll
     for (uint32_t i = 0; i < 32 / CW; ++i)
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                     :
-                     : "s"(dst + 1024 * CW * i), "v"(voff), "s"(rs), "s"(b * a.M * 256 + i * 1024 * CW)
-                     : "memory", "m0");
+    {
+        // m0 (the LDS destination) is restored afterwards: the compiler
+        // treats it as reserved and may hold its own value there.
+        uint32_t saved;
+        asm volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(dst + 1024 * CW * i), "v"(voff), "s"(rs), "s"(b * a.M * 256 + i * 1024 * CW)
+            : "memory");
+    }
 }
 
 // One superblock of a consumer wave's 32-row x (32 NTT)-token Q4_K tile from

@@ -42,6 +42,9 @@ SIGNATURES = {
     "tc_debug_q8k_blocks": (_I, [_I, _P, _U32, _P, _U32, _P, _P]),
     "tc_debug_q8_0_blocks": (_I, [_P, _U32, _P, _U32, _P, _P]),
     "tc_last_error": (ctypes.c_char_p, []),
+    "tc_probe_sink_bytes": (ctypes.c_size_t, []),
+    "tc_probe_mfma_i8": (_I, [_U32, _U32, _P, _P]),
+    "tc_probe_read": (_I, [_P, ctypes.c_size_t, _U32, _P, _P]),
 }
 
 
