@@ -27,8 +27,11 @@ def enc_weights(oracle, qt, rng, rows, cols):
 
 # (M tokens, N rows, K cols): ragged tiles, a K-split case (few output tiles),
 # a single token, and a multi-tile case.
-# (40, 72, 2304): two K-slices of 5 and 4 superblocks (odd and even counts)
-SHAPES = [(1, 64, 256), (37, 200, 1024), (128, 256, 5120), (130, 136, 2048), (300, 384, 768), (40, 72, 2304)]
+# (40, 72, 2304): K-slices of 5 and 4 superblocks (odd and even counts);
+# (200, 1000, 4096): Q4_K stream-K with every tile split over 4 workgroups and
+# ragged rows and tokens.
+SHAPES = [(1, 64, 256), (37, 200, 1024), (128, 256, 5120), (130, 136, 2048), (300, 384, 768), (40, 72, 2304),
+          (200, 1000, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)

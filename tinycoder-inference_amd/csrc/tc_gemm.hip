@@ -9,14 +9,17 @@
 // combination runs in fp32.
 //
 // Decomposition. One workgroup owns a tile of 64 weight rows x 128 tokens and
-// walks K one 256-element superblock at a time (optionally a K-slice of them,
-// for split-K). The activations arrive block-major (256-column block b of
-// token m at b*M + m), so one superblock of a token tile is one contiguous
-// 32 KB run. Per superblock the raw weight rows, the quantized activations and
-// their scales are staged through LDS. Q4_K runs 8 waves, 4 producers (global
-// loads two superblocks ahead, conversion into one half of a double-buffered
-// LDS) and 4 consumers (MFMAs on the other half); Q8_0 runs 4 waves that do
-// both, two workgroups per CU.
+// walks K one 256-element superblock at a time. Q4_K spreads the (tile,
+// superblock) units evenly over one workgroup per CU (stream-K, partial tiles
+// summed by k_gemm_fixup); Q8_0 runs one workgroup per tile (split-K when the
+// tiles do not fill the chip). The activations arrive block-major
+// (256-column block b of token m at b*M + m), so one superblock of a token
+// tile is one contiguous 32 KB run. Per superblock the raw weight rows, the
+// quantized activations and their scales are staged through LDS. Q4_K runs 12
+// waves: 4 producers (weight loads two superblocks ahead, conversion into one
+// half of a double-buffered LDS) and 8 consumers (the activation plane loaded
+// straight into LDS, MFMAs on the other half); Q8_0 runs 4 waves that do both,
+// two workgroups per CU.
 //
 //  * Q4_K: a weight of sub-block s is w = d*sc_s*q - dmin*m_s (q in 0..15,
 //    sc_s, m_s in 0..63). The product sc_s*q (<= 945) is written to two int8
@@ -34,9 +37,6 @@
 // same k positions of both; the 32x32 int32 result holds row
 // 8*(r/4) + 4*(l>>5) + (r%4) and column (l & 31) in register r.
 #include "tc_kernels.hpp"
-#ifndef TC_GEMM_CW
-#define TC_GEMM_CW 8
-#endif
 
 namespace tc {
 namespace {
@@ -82,7 +82,10 @@ struct GemmArgs {
     uint32_t row_bytes;     // bytes per weight row
     uint32_t ntm;           // token tiles
     uint32_t nblk;          // superblocks per row
-    uint32_t split_blk;     // superblocks per K-slice
+    uint32_t split_blk;     // superblocks per K-slice (Q8_0 split-K)
+    uint32_t ntiles;        // output tiles (Q4_K stream-K)
+    uint32_t skg;           // stream-K workgroups
+    float *ws;              // Q4_K stream-K partial tiles [grid][2][GM][GN]
 };
 
 __device__ __forceinline__ u4 lds4(const unsigned char *p) { return *reinterpret_cast<const u4 *>(p); }
@@ -497,6 +500,25 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 // waves run the MFMAs and the fp32 combination of superblock b from the other
 // half -- the conversion's VALU work overlaps the matrix work on the same
 // SIMDs, with one barrier per superblock.
+// Stream-K: the (tile, superblock) units, tile-major, are split evenly over
+// the workgroups (one per CU). A workgroup walks its range one tile segment
+// at a time; a segment that covers a whole tile is stored to `out`, a partial
+// one to the workgroup's slot in `ws` (slot 0: its first segment, 1: its
+// last), and k_gemm_fixup sums the partial segments of each tile in
+// workgroup order.
+// Tile t -> (token tile, row block), token tiles fastest: a stream-K
+// workgroup's consecutive tiles reuse one block of weight rows. (Row blocks
+// fastest measured 3-13% slower.)
+__device__ __forceinline__ void sk_tile(const GemmArgs &a, uint32_t t, uint32_t &m0, uint32_t &n0) {
+    const uint32_t tm = t % a.ntm, tn = t / a.ntm;
+    m0 = tm * GM;
+    n0 = tn * GN;
+}
+
+__host__ __device__ inline uint32_t sk_begin(uint32_t units, uint32_t grid, uint32_t w) {
+    return uint32_t(uint64_t(units) * w / grid);
+}
+
 template <int CW>
 __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 + CW / 4, 1 + CW / 4))) void k_gemm_q4k_ws(
     GemmArgs a) {
@@ -510,82 +532,121 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
     const uint32_t wn = wave & 1, wm = (wave >> 1) & (CW / 2 - 1), tok0 = 32 * NTT * wm;
     const uint32_t li = lane & 31, lg = lane >> 5;
     const uint32_t ptid = tid - 64 * CW;  // producer thread index 0..255
-
-    const uint32_t tile = blockIdx.x;
-    const uint32_t split = blockIdx.y;
-    const uint32_t tm = tile % a.ntm, tn = tile / a.ntm;
-    const uint32_t n0 = tn * GN, m0 = tm * GM;
-    const uint32_t b0 = split * a.split_blk;
-    const uint32_t b1 = min(b0 + a.split_blk, a.nblk);
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
-    // Producers step in pairs of superblocks; both sides run bend - b0 barriers.
-    const uint32_t nb = b1 > b0 ? b1 - b0 : 0;
-    const uint32_t bend = b0 + ((nb + 1) & ~1u);
 
-    float acc[NTT][16];
-#pragma unroll
-    for (int t = 0; t < NTT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+    const uint32_t units = a.ntiles * a.nblk;
+    const uint32_t ub = sk_begin(units, gridDim.x, blockIdx.x), ue = sk_begin(units, gridDim.x, blockIdx.x + 1);
+    for (uint32_t u = ub; u < ue;) {
+        const uint32_t tile = u / a.nblk;
+        const uint32_t b0 = u - tile * a.nblk;
+        const uint32_t b1 = min(a.nblk, b0 + (ue - u));
+        const bool whole = b0 == 0 && b1 == a.nblk;
+        float *const part = whole ? nullptr : a.ws + (size_t(blockIdx.x) * 2 + (u == ub ? 0 : 1)) * (GM * GN);
+        u += b1 - b0;
+        uint32_t m0, n0;
+        sk_tile(a, tile, m0, n0);
+        // Producers step in pairs of superblocks; both sides run bend - b0 barriers.
+        const uint32_t bend = b0 + ((b1 - b0 + 1) & ~1u);
 
-    // Producer and consumer waves run separate loops with the same number of
-    // barriers, so neither keeps the other's registers live.
-    if (producer) {
-        // Two superblocks of loads in flight per producer thread: global
-        // latency under load exceeds one superblock's compute time.
-        const GSrc gs = gemm_src<kQ4_K>(a, n0, m0, ptid);
-        GPrefetch<kQ4_K> pa, pb;
-        if (b0 < b1) {
+        // Producer and consumer waves run separate loops with the same number
+        // of barriers, so neither keeps the other's registers live.
+        if (producer) {
+            // Two superblocks of loads in flight per producer thread: global
+            // latency under load exceeds one superblock's compute time.
+            const GSrc gs = gemm_src<kQ4_K>(a, n0, m0, ptid);
+            GPrefetch<kQ4_K> pa, pb;
             gemm_prefetch<kQ4_K>(a, gs, b0, pa);
             gemm_stage<kQ4_K>(pa, buf(b0), ptid);
             gemm_prefetch<kQ4_K>(a, gs, min(b0 + 1, b1 - 1), pa);
             gemm_prefetch<kQ4_K>(a, gs, min(b0 + 2, b1 - 1), pb);
-        }
-        __syncthreads();
-        // Straight-line steps (past the end they stage into the idle buffer and
-        // reload the last superblock), so the compiler's wait counts stay exact.
-        auto step = [&](GPrefetch<kQ4_K> &pf, uint32_t b) __attribute__((always_inline)) {
-            gemm_stage<kQ4_K>(pf, buf(b + 1), ptid);
-            gemm_prefetch<kQ4_K>(a, gs, min(b + 3, b1 - 1), pf);
             __syncthreads();
-        };
-        for (uint32_t b = b0; b < bend; b += 2) {
-            step(pa, b);
-            step(pb, b + 1);
+            // Straight-line steps (past the end they stage into the idle buffer
+            // and reload the last superblock), so the compiler's wait counts
+            // stay exact.
+            auto step = [&](GPrefetch<kQ4_K> &pf, uint32_t b) __attribute__((always_inline)) {
+                gemm_stage<kQ4_K>(pf, buf(b + 1), ptid);
+                gemm_prefetch<kQ4_K>(a, gs, min(b + 3, b1 - 1), pf);
+                __syncthreads();
+            };
+            for (uint32_t b = b0; b < bend; b += 2) {
+                step(pa, b);
+                step(pb, b + 1);
+            }
+            continue;
         }
-        return;
-    }
-    // Consumers fill the activation planes: superblock b+1 goes into the
-    // other buffer while b is multiplied (their only memory loads, so the
-    // wait before each barrier waits for nothing else).
-    if (b0 < b1) q4k_act_to_lds<CW>(a, m0, b0, buf(b0), wave, lane);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    for (uint32_t b = b0; b < bend; ++b) {
-        q4k_act_to_lds<CW>(a, m0, min(b + 1, b1 - 1), buf(b + 1), wave, lane);
-        if (b < b1) q4k_consume<NTT>(buf(b), wn, tok0, li, lg, acc);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this superblock's plane is in LDS
+        float acc[NTT][16];
+#pragma unroll
+        for (int t = 0; t < NTT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+        // Consumers fill the activation planes: superblock b+1 goes into the
+        // other buffer while b is multiplied (their only memory loads, so the
+        // wait before each barrier waits for nothing else).
+        q4k_act_to_lds<CW>(a, m0, b0, buf(b0), wave, lane);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
-    }
+        for (uint32_t b = b0; b < bend; ++b) {
+            q4k_act_to_lds<CW>(a, m0, min(b + 1, b1 - 1), buf(b + 1), wave, lane);
+            if (b < b1) q4k_consume<NTT>(buf(b), wn, tok0, li, lg, acc);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this superblock's plane is in LDS
+            __syncthreads();
+        }
 
-    float *out = a.out + size_t(split) * a.M * a.N;
 #pragma unroll
-    for (int t = 0; t < NTT; ++t) {
-        const uint32_t m = m0 + tok0 + 32 * t + li;
-        if (m >= a.M) continue;
+        for (int t = 0; t < NTT; ++t) {
+            const uint32_t ml = tok0 + 32 * t + li, m = m0 + ml;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t n = n0 + 32 * wn + 8 * q + 4 * lg;
-            float *o = out + size_t(m) * a.N + n;
-            if (n + 3 < a.N && (a.N & 3) == 0) {
-                *reinterpret_cast<float4 *>(o) = make_float4(acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2],
-                                                             acc[t][4 * q + 3]);
-            } else {
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t nl = 32 * wn + 8 * q + 4 * lg, n = n0 + nl;
+                const float4 v = make_float4(acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]);
+                if (part != nullptr) {
+                    *reinterpret_cast<float4 *>(part + ml * GN + nl) = v;  // [token][row] of the tile
+                } else if (m < a.M) {
+                    float *o = a.out + size_t(m) * a.N + n;
+                    if (n + 3 < a.N && (a.N & 3) == 0) {
+                        *reinterpret_cast<float4 *>(o) = v;
+                    } else {
+                        const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (n + e < a.N) o[e] = acc[t][4 * q + e];
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < a.N) o[e] = vv[e];
+                    }
+                }
             }
         }
+    }
+}
+
+// Tiles split over several stream-K workgroups: out = the partial segments
+// summed in workgroup order (one workgroup per tile; whole tiles exit).
+__global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
+    const uint32_t tile = blockIdx.x, units = a.ntiles * a.nblk, G = a.skg;
+    const uint32_t t0 = tile * a.nblk, t1 = t0 + a.nblk;
+    // first workgroup whose range holds unit t0
+    uint32_t w = uint32_t(uint64_t(t0) * G / units);
+    while (w + 1 < G && sk_begin(units, G, w + 1) <= t0) ++w;
+    while (w > 0 && sk_begin(units, G, w) > t0) --w;
+    if (sk_begin(units, G, w) <= t0 && sk_begin(units, G, w + 1) >= t1) return;  // one workgroup: stored directly
+    uint32_t m0, n0;
+    sk_tile(a, tile, m0, n0);
+    for (uint32_t i = threadIdx.x; i < GM * GN / 4; i += 256) {
+        const uint32_t ml = (4 * i) / GN, nl = (4 * i) % GN;
+        float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (uint32_t v = w; v < G && sk_begin(units, G, v) < t1; ++v) {
+            if (sk_begin(units, G, v + 1) <= t0 || sk_begin(units, G, v + 1) == sk_begin(units, G, v)) continue;
+            const uint32_t slot = sk_begin(units, G, v) >= t0 ? 0u : 1u;
+            const float4 p = *reinterpret_cast<const float4 *>(a.ws + (size_t(v) * 2 + slot) * (GM * GN) + ml * GN + nl);
+            s.x += p.x;
+            s.y += p.y;
+            s.z += p.z;
+            s.w += p.w;
+        }
+        const uint32_t m = m0 + ml, n = n0 + nl;
+        if (m >= a.M) continue;
+        const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < a.N) a.out[size_t(m) * a.N + n + e] = sv[e];
     }
 }
 
@@ -602,7 +663,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
 template <int TYPE>
 hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
     if constexpr (TYPE == kQ4_K) {
-        constexpr int CW = TC_GEMM_CW;
+        constexpr int CW = 8;  // consumer waves (4 measured 10-15% slower)
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_q4k_ws<CW>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (attr != hipSuccess) return attr;
@@ -618,8 +679,14 @@ hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
 
 }  // namespace
 
+// Q4_K stream-K grid: one workgroup per CU, each with at least 4 units.
+uint32_t sk_grid(uint32_t M, uint32_t N, uint32_t K, int num_cu) {
+    const uint32_t units = ((M + GM - 1) / GM) * ((N + GN - 1) / GN) * (K / 256);
+    return std::max(1u, std::min(uint32_t(num_cu), units / 4));
+}
+
 uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
-    (void)type;
+    if (type == kQ4_K) return 1;  // stream-K instead
     const uint32_t tiles = ((M + GM - 1) / GM) * ((N + GN - 1) / GN);
     const uint32_t nblk = K / 256;
     uint32_t s = 1;
@@ -630,6 +697,7 @@ uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
 }
 
 size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
+    if (type == kQ4_K) return size_t(sk_grid(M, N, K, num_cu)) * 2 * GM * GN * 4;
     const uint32_t s = gemm_splits(type, M, N, K, num_cu);
     return s > 1 ? size_t(s) * M * N * 4 : 0;
 }
@@ -639,7 +707,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
     if (M == 0 || N == 0 || K == 0 || K % 256) return hipErrorInvalidValue;
     if (type != kQ4_K && type != kQ8_0) return hipErrorInvalidValue;
     const uint32_t nsplit = gemm_splits(type, M, N, K, num_cu);
-    if (nsplit > 1 && workspace == nullptr) return hipErrorInvalidValue;
+    if ((nsplit > 1 || type == kQ4_K) && workspace == nullptr) return hipErrorInvalidValue;
     GemmArgs a{};
     a.W = static_cast<const uint8_t *>(W);
     a.qs = act.qs;
@@ -652,9 +720,24 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
     a.row_bytes = a.nblk * unit_bytes(type);
     a.ntm = (M + GM - 1) / GM;
     a.split_blk = (a.nblk + nsplit - 1) / nsplit;
+    a.ntiles = a.ntm * ((N + GN - 1) / GN);
+    if (type == kQ4_K) {
+        const uint32_t G = sk_grid(M, N, K, num_cu);
+        a.out = out;
+        a.ws = static_cast<float *>(workspace);
+        a.skg = G;
+        hipError_t e = launch_gemm_t<kQ4_K>(a, dim3{G, 1u, 1u}, st);
+        if (e != hipSuccess) return e;
+        // Any tile split over workgroups? (a range boundary inside a tile)
+        bool split = false;
+        for (uint32_t w = 1; w < G && !split; ++w) split = sk_begin(a.ntiles * a.nblk, G, w) % a.nblk != 0;
+        if (!split) return hipSuccess;
+        k_gemm_fixup<<<dim3{a.ntiles, 1u, 1u}, 256, 0, st>>>(a);
+        return hipGetLastError();
+    }
     a.out = nsplit > 1 ? static_cast<float *>(workspace) : out;
-    const dim3 grid{a.ntm * ((N + GN - 1) / GN), nsplit, 1u};
-    hipError_t e = type == kQ4_K ? launch_gemm_t<kQ4_K>(a, grid, st) : launch_gemm_t<kQ8_0>(a, grid, st);
+    const dim3 grid{a.ntiles, nsplit, 1u};
+    hipError_t e = launch_gemm_t<kQ8_0>(a, grid, st);
     if (e != hipSuccess || nsplit == 1) return e;
     const size_t mn = size_t(M) * N;
     k_gemm_reduce<<<dim3{uint32_t((mn + 255) / 256), 1u, 1u}, 256, 0, st>>>(static_cast<const float *>(workspace),
