@@ -139,11 +139,22 @@ def gemm_bench(torch, tc, tc_hip, dev, reps):
     return res
 
 
+def head_start(torch):
+    """Keep the GPU busy for a bounded time (~25 ms) while the host queues the
+    timed launches, so that events measure back-to-back GPU execution and not
+    the Python launch rate."""
+    try:
+        torch.cuda._sleep(int(60e6))
+    except (AttributeError, RuntimeError):
+        pass
+
+
 def timed(torch, fn, n):
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     fn(0)
     torch.cuda.synchronize()
+    head_start(torch)
     a.record()
     for i in range(n):
         fn(i)
@@ -347,20 +358,11 @@ def main():
         print(json.dumps({"pmc_probe": True, "copy_bytes": 2 * src.numel() * 4, "steps": args.steps}), flush=True)
         return
 
-    def head_start():
-        # Keep the GPU busy for a bounded time while the host queues the timed
-        # launches, so that events measure back-to-back GPU execution and not
-        # the Python launch rate.
-        try:
-            torch.cuda._sleep(int(60e6))
-        except (AttributeError, RuntimeError):
-            pass
-
     # ---- timed region: K steps ------------------------------------------------------
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    head_start()
+    head_start(torch)
     t_start.record()
     for i in range(args.steps):
         step(i)
@@ -371,7 +373,7 @@ def main():
     # the same layer as one launch (7 independent mat-vecs, one kernel)
     t1s = torch.cuda.Event(enable_timing=True)
     t1e = torch.cuda.Event(enable_timing=True)
-    head_start()
+    head_start(torch)
     t1s.record()
     for i in range(args.steps):
         step_one_launch(i)
@@ -389,7 +391,7 @@ def main():
     for name, mats in LAUNCHES:
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
-        head_start()
+        head_start(torch)
         a.record(stream)
         for i in range(args.steps):
             launch(name, copies[i % N_COPIES])
