@@ -1096,20 +1096,25 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
 #endif
     uint32_t lw = blockIdx.x - jb.wg_begin;
     bool no_expert = false;
-    const int32_t *rids = nullptr;  // rank-group mode: this token's expert ids
+    // Expert ids are loaded here and first used after the activation loads
+    // are issued, so their latency overlaps the activations'.
+    int32_t eid = 0;                // expert-pair mode: this pair's expert
+    typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+    i32x8 reid = {-1, -1, -1, -1, -1, -1, -1, -1};  // rank-group mode: this token's experts (-1 past rk)
     const float *rwts = nullptr;
     if (jb.ids != nullptr) {
         const uint32_t p = lw / jb.wg_per_pair;
         lw -= p * jb.wg_per_pair;
         if constexpr (!RG) {
-            const int32_t e = jb.ids[p];
-            no_expert = e < 0 || uint32_t(e) >= jb.n_experts;
-            const uint64_t off = no_expert ? 0 : uint64_t(e) * jb.wstride;
-            jb.W += off;
-            if (jb.W2 != nullptr) jb.W2 += off;
+            eid = jb.ids[p];
             jb.x += size_t(p / jb.x_div) * jb.x_stride;
         } else {
-            rids = jb.ids + size_t(p) * jb.rk;
+            const int32_t *rids = jb.ids + size_t(p) * jb.rk;
+            static_for<0, 8>([&](auto k) __attribute__((always_inline)) {
+                constexpr uint32_t K = decltype(k)::value;
+                const int32_t v = rids[K < jb.rk ? K : 0];  // always in bounds
+                reid[K] = K < jb.rk ? v : -1;
+            });
             rwts = jb.wts + size_t(p) * jb.rk;
             jb.x += size_t(p) * jb.x_stride;
         }
@@ -1128,9 +1133,14 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     const size_t per = TYPE == kQ4_K ? 8 : 1;
     const size_t dbg_tok = size_t(jb.rows) * nbr * per;
     const size_t xtok = size_t(nu) * XB;
-    // Descriptors over exactly this workgroup's rows of each matrix.
-    const uint8_t *const wbase1 = jb.W + size_t(r0) * nu * UB;
-    const uint8_t *const wbase2 = (jb.W2 != nullptr ? jb.W2 : jb.W) + size_t(r0) * nu * UB;
+    // Expert of rank m (rank-group mode; m is wave-uniform).
+    auto rank_expert = [&](uint32_t m) __attribute__((always_inline)) {
+        int32_t e = reid[0];
+        static_for<1, 8>([&](auto k) __attribute__((always_inline)) {
+            e = m == uint32_t(decltype(k)::value) ? reid[decltype(k)::value] : e;
+        });
+        return e;
+    };
     // Matrix of tile t (0 or 1 for a pair, the rank in rank-group mode).
     auto mat_of = [&](uint32_t t) __attribute__((always_inline)) {
         uint32_t m = 0;
@@ -1160,6 +1170,17 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     // for the loads).
     __builtin_amdgcn_s_barrier();
 #endif
+    if constexpr (!RG) {
+        if (jb.ids != nullptr) {
+            no_expert = eid < 0 || uint32_t(eid) >= jb.n_experts;
+            const uint64_t off = no_expert ? 0 : uint64_t(eid) * jb.wstride;
+            jb.W += off;
+            if (jb.W2 != nullptr) jb.W2 += off;
+        }
+    }
+    // Descriptors over exactly this workgroup's rows of each matrix.
+    const uint8_t *const wbase1 = jb.W + size_t(r0) * nu * UB;
+    const uint8_t *const wbase2 = (jb.W2 != nullptr ? jb.W2 : jb.W) + size_t(r0) * nu * UB;
     Regs<D * NX> buf;
     // Loads past the workgroup's tiles (the ring's last refills) go through a
     // descriptor of size 0, and lanes past a partial tile's end carry a
@@ -1177,7 +1198,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         } else {
             const uint32_t m = live ? mat_of(t) : 0u;
             tt = t - m * ntiles_mat;
-            const int32_t e = rids[m];
+            const int32_t e = rank_expert(m);
             live = live && e >= 0 && uint32_t(e) < jb.n_experts;
             base = wbase1 + (live ? uint64_t(e) * jb.wstride : 0);
         }
@@ -1280,7 +1301,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
                 for (uint32_t bb = q; bb < nu; bb += 4) g += pg[bb];
                 g = quad_sum(g);
                 if constexpr (TYPE == kIQ3_XXS) g = 0.25f * g;
-                const int32_t e = rids[k];
+                const int32_t e = rank_expert(k);
                 if (e < 0 || uint32_t(e) >= jb.n_experts) g = 0.0f;
                 acc = fmaf(rwts[k], g, acc);
             }
