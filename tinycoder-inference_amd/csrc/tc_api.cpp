@@ -295,6 +295,10 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
         }
         return TC_OK;
     }
+    // 32-bit buffer offsets in the MFMA kernels
+    if (uint64_t(seq_len) * cols >= (uint64_t(1) << 32) ||
+        uint64_t(rows) * tc_row_bytes(type, cols) >= (uint64_t(1) << 32))
+        return fail(TC_E_UNSUPPORTED, "activations or weights of 4 GiB or more");
     // Quantize all tokens once, then the MFMA kernel.
     const tc::ActLayout L = tc::act_layout(type, seq_len, cols);
     const size_t ws = tc::gemm_workspace_bytes(type, seq_len, rows, cols, dev->num_cu);

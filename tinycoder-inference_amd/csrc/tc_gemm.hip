@@ -705,6 +705,10 @@ size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int nu
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
                        int num_cu, void *workspace, hipStream_t st) {
     if (M == 0 || N == 0 || K == 0 || K % 256) return hipErrorInvalidValue;
+    // 32-bit buffer offsets: the quantized activations (M*K bytes) and one
+    // weight matrix must each stay below 4 GiB.
+    if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
+        return hipErrorInvalidValue;
     if (type != kQ4_K && type != kQ8_0) return hipErrorInvalidValue;
     const uint32_t nsplit = gemm_splits(type, M, N, K, num_cu);
     if ((nsplit > 1 || type == kQ4_K) && workspace == nullptr) return hipErrorInvalidValue;
