@@ -25,6 +25,7 @@ uint32_t oc_type_size(int type) {
     switch (type) {
         case OC_TYPE_Q8_0: return 34;
         case OC_TYPE_Q4_K: return 144;
+        case OC_TYPE_Q5_K: return 176;
         case OC_TYPE_Q6_K: return 210;
         case OC_TYPE_IQ3_XXS: return 98;
         default: return 0;
@@ -196,6 +197,15 @@ static void q4k_scale_min(const uint8_t *s, int j, uint8_t *sc, uint8_t *m) {
 
 /* Q6_K raw 6-bit value (0..63) of element e of a block:
  * include/GGMLDequantize.hpp:503-527. */
+/* Q5_K 5-bit value of weight l of sub-block g (include/GGMLDequantize.hpp:
+ * 392-402; the byte layout of SIMDMatMulVecAVX2.cpp:3890-3903): qs at 48,
+ * qh at 16. */
+static int q5k_value(const uint8_t *blk, int g, int l) {
+    const int c = g >> 1, h = g & 1;
+    const uint8_t *qs = blk + 48, *qh = blk + 16;
+    return ((qs[32 * c + l] >> (4 * h)) & 0xF) | (((qh[l] >> (2 * c + h)) & 1) << 4);
+}
+
 static int q6k_raw(const uint8_t *blk, int e) {
     const int half = e >> 7, r = e & 127, quad = r >> 5, l = r & 31;
     const uint8_t *ql = blk + 64 * half;
@@ -247,6 +257,17 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
                     y[32 * g + l] = d1 * (float)v - m1;
                 }
             }
+        } else if (type == OC_TYPE_Q5_K) {
+            /* include/GGMLDequantize.hpp:346-411: sub-block g = 2c + h of chunk
+             * c: q5 = (qs[32c+l] >> 4h & 15) | (qh[l] bit 2c+h) << 4 (the same
+             * 32 qh bytes serve every chunk), y = d1 * q5 - m1. */
+            const float d = h2f_at(blk), dmin = h2f_at(blk + 2);
+            for (int g = 0; g < 8; ++g) {
+                uint8_t sc, m;
+                q4k_scale_min(blk + 4, g, &sc, &m);
+                const float d1 = d * (float)sc, m1 = dmin * (float)m;
+                for (int l = 0; l < 32; ++l) y[32 * g + l] = d1 * (float)q5k_value(blk, g, l) - m1;
+            }
         } else if (type == OC_TYPE_Q6_K) {
             /* include/GGMLDequantize.hpp:503-527: y = d * sc * q, evaluated
              * left to right as (d*sc)*q with q = raw-32. */
@@ -285,6 +306,16 @@ static void q4k_subsums(const uint8_t *blk, const int8_t *xq, int32_t s[8]) {
             const int v = (i & 1) ? (q[l] >> 4) : (q[l] & 0xF);
             acc += v * xq[32 * i + l];
         }
+        s[i] = acc;
+    }
+}
+
+/* Q5_K sub-block integer sums s32q[i] = sum_32 q5 * q8 (the maddubs/madd
+ * chain of src/cpp/core/SIMDMatMulVecAVX2.cpp:3924-3933). */
+static void q5k_subsums(const uint8_t *blk, const int8_t *xq, int32_t s[8]) {
+    for (int i = 0; i < 8; ++i) {
+        int32_t acc = 0;
+        for (int l = 0; l < 32; ++l) acc += q5k_value(blk, i, l) * xq[32 * i + l];
         s[i] = acc;
     }
 }
@@ -364,7 +395,7 @@ int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
     act_t a;
     if (quantize_acts(type, X, S, cols, &a)) return -1;
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type), nb = cols / bs;
-    const uint32_t k = type == OC_TYPE_Q4_K ? 8 : 1;
+    const uint32_t k = (type == OC_TYPE_Q4_K || type == OC_TYPE_Q5_K) ? 8 : 1;
     for (uint32_t s = 0; s < S; ++s)
         for (uint32_t r = 0; r < rows; ++r)
             for (uint32_t b = 0; b < nb; ++b) {
@@ -373,6 +404,7 @@ int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                 int32_t *o = isums + (((size_t)s * rows + r) * nb + b) * k;
                 switch (type) {
                     case OC_TYPE_Q4_K: q4k_subsums(blk, xq, o); break;
+                    case OC_TYPE_Q5_K: q5k_subsums(blk, xq, o); break;
                     case OC_TYPE_Q6_K: o[0] = q6k_isum(blk, xq); break;
                     case OC_TYPE_IQ3_XXS: o[0] = iq3_isum(blk, xq); break;
                     default: o[0] = q80_isum(blk, xq); break;
@@ -406,6 +438,35 @@ static float row_q4k(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff
             const float mn = dmin * (float)m;
             mainS = fmaf(ds, (float)s32[i], mainS);
             minS = fmaf(mn, (float)(bsums[2 * i] + bsums[2 * i + 1]), minS);
+        }
+        sum = fmaf(a->d[doff + b], mainS - minS, sum);
+    }
+    return sum;
+}
+
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:3842-3955 (matMulVecBatchQ5K_Q8K_AVX2):
+ * per block ds = d*sc, mn = dmin*m; mainS += ds*s32, minS += mn*pairsum,
+ * acc += d8*(mainS - minS), accumulated over blocks in order; the three
+ * accumulations contract to fused multiply-adds as in the Q4_K kernel. */
+static float row_q5k(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff,
+                     size_t boff) {
+    float sum = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 176;
+        const float d = h2f_at(blk), dmin = h2f_at(blk + 2);
+        int32_t s32[8];
+        q5k_subsums(blk, a->qs + qoff + (size_t)b * 256, s32);
+        const int16_t *bsums = a->bsums + boff + (size_t)b * 16;
+        float mainS = 0.0f, minS = 0.0f;
+        for (int i = 0; i < 8; ++i) {
+            uint8_t sc, m;
+            q4k_scale_min(blk + 4, i, &sc, &m);
+            mainS = fmaf(d * (float)sc, (float)s32[i], mainS);
+        }
+        for (int i = 0; i < 8; ++i) {
+            uint8_t sc, m;
+            q4k_scale_min(blk + 4, i, &sc, &m);
+            minS = fmaf(dmin * (float)m, (float)(bsums[2 * i] + bsums[2 * i + 1]), minS);
         }
         sum = fmaf(a->d[doff + b], mainS - minS, sum);
     }
@@ -526,6 +587,7 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t r
             float v;
             switch (type) {
                 case OC_TYPE_Q4_K: v = row_q4k(rp, nb, &a, qoff, doff, boff); break;
+                case OC_TYPE_Q5_K: v = row_q5k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_Q6_K: v = row_q6k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_IQ3_XXS: v = row_iq3(rp, nb, &a, qoff, doff); break;
                 default: v = row_q80(rp, nb, &a, qoff, doff); break;
@@ -602,6 +664,60 @@ void oc_encode_q8_0_block(const float *x, uint8_t *out) {
         long q = d > 0.0f ? lrintf(x[i] / d) : 0;
         q = q < -127 ? -127 : (q > 127 ? 127 : q);
         out[2 + i] = (uint8_t)(int8_t)q;
+    }
+}
+
+/* Q5_K weight encoder (the reference ships none; this build defines it, in
+ * the shape of the Q4_K one, src/cpp/core/GGMLQuantize.cpp:47-95): per
+ * 32-group affine fit scale = (max-min)/31, min = -min (the scan starts at 0);
+ * 6-bit sub-scales and mins against fp16 super-scales maxScale/63, maxMin/63
+ * (round to nearest even); q = clamp(rne((x + m6*dmin) / (sc6*d)), 0, 31)
+ * against the stored scales, packed as include/GGMLDequantize.hpp:346-411
+ * reads them. */
+void oc_encode_q5k_block(const float *x, uint8_t *out) {
+    float scale[8], minv[8];
+    float maxScale = 0.0f, maxMin = 0.0f;
+    for (int g = 0; g < 8; ++g) {
+        const float *xp = x + 32 * g;
+        float mn = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            mn = xp[i] < mn ? xp[i] : mn;
+            mx = mx < xp[i] ? xp[i] : mx;
+        }
+        scale[g] = (mx - mn) / 31.0f;
+        minv[g] = -mn;
+        maxScale = maxScale < scale[g] ? scale[g] : maxScale;
+        maxMin = maxMin < minv[g] ? minv[g] : maxMin;
+    }
+    const uint16_t hd = maxScale > 0.0f ? f2h_rne(maxScale / 63.0f) : 0;
+    const uint16_t hdm = maxMin > 0.0f ? f2h_rne(maxMin / 63.0f) : 0;
+    const float d = oc_half_to_float(hd), dm = oc_half_to_float(hdm);
+    uint8_t sc6[8], m6[8];
+    for (int g = 0; g < 8; ++g) {
+        int sv = d > 0.0f ? (int)lrintf(scale[g] / d) : 0;
+        int mv = dm > 0.0f ? (int)lrintf(minv[g] / dm) : 0;
+        sc6[g] = (uint8_t)(sv < 0 ? 0 : (sv > 63 ? 63 : sv));
+        m6[g] = (uint8_t)(mv < 0 ? 0 : (mv > 63 ? 63 : mv));
+    }
+    memcpy(out, &hd, 2);
+    memcpy(out + 2, &hdm, 2);
+    for (int j = 0; j < 4; ++j) {
+        out[4 + j] = (uint8_t)(sc6[j] | ((sc6[j + 4] >> 4) << 6));
+        out[4 + j + 4] = (uint8_t)(m6[j] | ((m6[j + 4] >> 4) << 6));
+        out[4 + j + 8] = (uint8_t)((sc6[j + 4] & 0x0F) | ((m6[j + 4] & 0x0F) << 4));
+    }
+    uint8_t *qh = out + 16, *qs = out + 48;
+    memset(qh, 0, 32);
+    memset(qs, 0, 128);
+    for (int g = 0; g < 8; ++g) {
+        const float es = d * (float)sc6[g], em = dm * (float)m6[g];
+        const int c = g >> 1, h = g & 1;
+        for (int l = 0; l < 32; ++l) {
+            int v = es > 0.0f ? (int)lrintf((x[32 * g + l] + em) / es) : 0;
+            v = v < 0 ? 0 : (v > 31 ? 31 : v);
+            qs[32 * c + l] |= (uint8_t)((v & 15) << (4 * h));
+            qh[l] |= (uint8_t)((v >> 4) << (2 * c + h));
+        }
     }
 }
 
@@ -726,6 +842,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
         switch (type) {
             case OC_TYPE_Q8_0: oc_encode_q8_0_block(xb, o); break;
             case OC_TYPE_Q4_K: oc_encode_q4k_block(xb, o); break;
+            case OC_TYPE_Q5_K: oc_encode_q5k_block(xb, o); break;
             case OC_TYPE_Q6_K: oc_encode_q6k_block(xb, o); break;
             default: oc_encode_iq3xxs_block(xb, o); break;
         }

@@ -14,9 +14,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libtcref.so")
 
-Q8_0, Q4_K, Q6_K, IQ3_XXS = 8, 12, 14, 18
-TYPE_SIZE = {Q8_0: 34, Q4_K: 144, Q6_K: 210, IQ3_XXS: 98}
-BLOCK_SIZE = {Q8_0: 32, Q4_K: 256, Q6_K: 256, IQ3_XXS: 256}
+Q8_0, Q4_K, Q5_K, Q6_K, IQ3_XXS = 8, 12, 13, 14, 18
+TYPE_SIZE = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98}
+BLOCK_SIZE = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ3_XXS: 256}
 
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
@@ -95,7 +95,7 @@ class Oracle(_Lib):
         x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
         S = x.shape[0]
         nb = cols // BLOCK_SIZE[qtype]
-        k = 8 if qtype == Q4_K else 1
+        k = 8 if qtype in (Q4_K, Q5_K) else 1
         out = np.zeros((S, rows, nb, k), np.int32)
         rc = self.lib.oc_block_isums(qtype, _ptr(w), _ptr(x), S, rows, cols, _ptr(out))
         assert rc == 0

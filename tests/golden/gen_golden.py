@@ -61,6 +61,15 @@ def q4k_random_blocks(rng, nblk):
     return b.ravel()
 
 
+def q5k_random_blocks(rng, nblk):
+    """Random Q5_K bytes (every scale/min code, qh and qs bit pattern) with
+    fixed normal fp16 d and dmin."""
+    b = rng.integers(0, 256, (nblk, 176), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(np.float16(0.0131).tobytes(), np.uint8)
+    b[:, 2:4] = np.frombuffer(np.float16(0.0042).tobytes(), np.uint8)
+    return b.ravel()
+
+
 def q80_random_blocks(rng, nblk):
     b = rng.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
     d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-10, -6, nblk)).astype(np.float16)
@@ -206,6 +215,22 @@ def main():
     digest = hashlib.sha256(wg.tobytes() + wu.tobytes() + wd.tobytes()).digest()
     g.update(moe_wsha256=np.frombuffer(digest, np.uint8), moe_x=xm, moe_ids=ids, moe_wts=wts,
              moe_y=out, moe_dims=np.array([E, K, H, FF, S, MOE_SEED], np.int64))
+
+    # Q5_K (a type the reference dispatches beyond BASELINE's configs): its
+    # dequant and matMulVecBatchQ5K_Q8K_AVX2 (SIMDMatMulVecAVX2.cpp:3842) on
+    # random blocks and on this build's encoder output (the reference has no
+    # Q5_K encoder). Own generator, so the vectors above are unchanged.
+    r5 = np.random.default_rng(20261202)
+    g["deq_q5k_w"] = q5k_random_blocks(r5, 8)
+    g["deq_q5k_y"] = ref.dequant(O.Q5_K, g["deq_q5k_w"], 8, 256)
+    cases5 = {
+        "q5k_rand": q5k_random_blocks(r5, rows * nb),
+        "q5k_enc1": O.Oracle().encode(O.Q5_K, r5.standard_normal((rows, cols)).astype(np.float32)),
+    }
+    for name, w in cases5.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.Q5_K, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.Q5_K, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")
