@@ -195,7 +195,8 @@ def roof_probes(torch, tc, tc_hip, dev):
 
 
 def other_decode_bench(torch, tc, tc_hip, dev, reps):
-    """BASELINE configs #1 and #3 (batch-1 decode mat-vecs of other formats):
+    """BASELINE configs #1 and #3 (batch-1 decode mat-vecs of other formats), and
+    Q5_K at the 7B FFN shape:
     weights N(0,0.02) through the GPU encoders, rotating copies so that every
     working set exceeds the 256 MB Infinity Cache."""
     gen = torch.Generator(device=dev).manual_seed(11)
@@ -203,7 +204,9 @@ def other_decode_bench(torch, tc, tc_hip, dev, reps):
     cases = [("cfg1 Q8_0 4096x4096", tc_hip.Q8_0, 4096, 4096, False, 16),
              ("cfg3 Q6_K LM head 152064x3584", tc_hip.Q6_K, 152064, 3584, False, 1),
              ("cfg3 Q6_K down 3584x18944", tc_hip.Q6_K, 3584, 18944, False, 6),
-             ("cfg3 IQ3_XXS gate/up pair 18944x3584 (SwiGLU)", tc_hip.IQ3_XXS, 18944, 3584, True, 6)]
+             ("cfg3 IQ3_XXS gate/up pair 18944x3584 (SwiGLU)", tc_hip.IQ3_XXS, 18944, 3584, True, 6),
+             ("Q5_K gate/up pair 18944x3584 (SwiGLU; format beyond the BASELINE configs)", tc_hip.Q5_K, 18944,
+              3584, True, 6)]
     res = []
     for name, qt, rows, cols, dual, ncopy in cases:
         mats = 2 if dual else 1

@@ -1,11 +1,11 @@
 """Seeded synthetic weight/activation generators shared by the tests."""
 import numpy as np
 
-Q8_0, Q4_K, Q6_K, IQ3_XXS = 8, 12, 14, 18
-TYPE_SIZE = {Q8_0: 34, Q4_K: 144, Q6_K: 210, IQ3_XXS: 98}
-BLOCK_SIZE = {Q8_0: 32, Q4_K: 256, Q6_K: 256, IQ3_XXS: 256}
-ALL = (Q8_0, Q4_K, Q6_K, IQ3_XXS)
-NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ3_XXS: "IQ3_XXS"}
+Q8_0, Q4_K, Q5_K, Q6_K, IQ3_XXS = 8, 12, 13, 14, 18
+TYPE_SIZE = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98}
+BLOCK_SIZE = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ3_XXS: 256}
+ALL = (Q8_0, Q4_K, Q5_K, Q6_K, IQ3_XXS)
+NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ3_XXS: "IQ3_XXS"}
 
 
 def row_bytes(qt, cols):
@@ -23,7 +23,7 @@ def random_blocks(qt, rng, rows, cols):
     nblk = rows * cols // BLOCK_SIZE[qt]
     b = rng.integers(0, 256, size=(nblk, TYPE_SIZE[qt]), dtype=np.uint8)
     mag = rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-16, -5, nblk)
-    if qt == Q4_K:
+    if qt in (Q4_K, Q5_K):
         b[:, 0:2] = _fp16_bytes(mag)
         b[:, 2:4] = _fp16_bytes(rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-12, -5, nblk))
     elif qt == Q6_K:

@@ -54,7 +54,7 @@ def test_row_bytes():
     assert lib.tc_row_bytes(8, 4096) == 128 * 34
     assert lib.tc_row_bytes(14, 18944) == 74 * 210
     assert lib.tc_row_bytes(18, 3584) == 14 * 98
-    assert lib.tc_row_bytes(13, 256) == 0
+    assert lib.tc_row_bytes(11, 256) == 0
 
 
 def test_reference_interface_header_compiles_and_links(tmp_path):

@@ -63,7 +63,7 @@ struct LaunchArgs {
     uint32_t off_d, off_b, off_g, off_p;
 };
 
-__host__ __device__ constexpr bool uses_bsums(int type) { return type == kQ4_K || type == kQ6_K; }
+__host__ __device__ constexpr bool uses_bsums(int type) { return type == kQ4_K || type == kQ5_K || type == kQ6_K; }
 // Passes of weight loads each lane keeps in flight (register ring), sized so
 // that the kernel stays within the 256 VGPRs of an 8-wave-per-CU launch.
 __host__ __device__ constexpr int ring_depth(int type, int S) {
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(NT) void k_gemv(LaunchArgs L) {
     const uint32_t row_begin = (blockIdx.x - jb.wg_begin) * jb.rows_per_wg;
     const uint32_t row_end = min(jb.rows, row_begin + jb.rows_per_wg);
     const size_t nbr = TYPE == kQ8_0 ? jb.cols / 32 : jb.cols / 256;
-    const size_t per = TYPE == kQ4_K ? 8 : 1;
+    const size_t per = TYPE == kQ4_K || TYPE == kQ5_K ? 8 : 1;
 
     XCtx c;
     c.sx = sx;
@@ -560,7 +560,7 @@ __host__ __device__ constexpr int tile_depth(int type, int S) {
     // Register slots in flight per wave: fewer where the accumulators of S
     // tokens would otherwise spill at 2 waves per SIMD (a Q8_0 slot is 68
     // registers, a Q4_K slot 36).
-    const int d = type == kQ4_K ? (S <= 6 ? 2 : 1) : (S >= 4 ? 1 : 2);
+    const int d = type == kQ4_K || type == kQ5_K ? (S <= 6 ? 2 : 1) : (S >= 4 ? 1 : 2);
     return d < C::DEPTH ? d : C::DEPTH;
 }
 
@@ -913,6 +913,76 @@ struct TDot<kQ4_K, S> {
     }
 };
 
+// Q5_K, one unit (176 B, 16-byte aligned) per lane: the Q4_K header and
+// nibble layout (qs at 48) plus the fifth bits in qh (bit 2j+h of qh[l] for
+// element l of sub-block 2j+h). The 8 sub-block sums s_g = sum q5*x are exact
+// int32 (q5 in 0..31), and main = sum sc_g*s_g, min = sum m_g*(bsum pair) in
+// int32, value d8*(d*main - dmin*min). The reference CPU kernel
+// (SIMDMatMulVecAVX2.cpp:3842-3960) forms the same two sums per sub-block in
+// fp32 (d*sc and dmin*m as float factors); the results differ by rounding
+// only.
+template <int S>
+struct TDot<kQ5_K, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        const u32x4 h = lds128(u);
+        const uint32_t scl = h.y & 0x3F3F3F3Fu, mnl = h.z & 0x3F3F3F3Fu;
+        const uint32_t sch = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+        const uint32_t mnh = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+        const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
+        const u32x4 ha = lds128(u + 16), hb = lds128(u + 32);
+        const uint32_t qh[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+        int mainI[S], minI[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) mainI[s] = minI[s] = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 qa = lds128(u + 48 + 32 * j), qb = lds128(u + 64 + 32 * j);
+            const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                // fifth bits of sub-blocks 2j and 2j+1 (qh bits 2j, 2j+1 of each
+                // byte) rotated to bit 4 of each byte (one v_alignbit each)
+                const uint32_t b0 = __builtin_amdgcn_alignbit(qh[k], qh[k], (2 * j + 28) & 31) & 0x10101010u;
+                const uint32_t b1 = __builtin_amdgcn_alignbit(qh[k], qh[k], (2 * j + 29) & 31) & 0x10101010u;
+                lo[k] = (q[k] & 0x0F0F0F0Fu) | b0;
+                hi[k] = ((q[k] >> 4) & 0x0F0F0F0Fu) | b1;
+            }
+            const uint32_t scw = j < 2 ? scl : sch, mnw = j < 2 ? mnl : mnh;
+            const int sc0 = int(byte_of(scw, (2 * j) & 3)), sc1 = int(byte_of(scw, (2 * j + 1) & 3));
+            const int m0 = int(byte_of(mnw, (2 * j) & 3)), m1 = int(byte_of(mnw, (2 * j + 1) & 3));
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const unsigned char *xr = xr0 + s * xtok;
+                const u32x4 x0 = lds128(xr + 64 * j), x1 = lds128(xr + 64 * j + 16);
+                const u32x4 x2 = lds128(xr + 64 * j + 32), x3 = lds128(xr + 64 * j + 48);
+                const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+                const uint2 bs = *reinterpret_cast<const uint2 *>(xr + XB_BS + 8 * j);
+                const int bp0 = sdot2_ones(bs.x), bp1 = sdot2_ones(bs.y);
+                int s0 = 0, s1 = 0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    s0 = sdot4(int(lo[k]), int(xl[k]), s0);
+                    s1 = sdot4(int(hi[k]), int(xh[k]), s1);
+                }
+                if (dbg) {
+                    dbg[s * dbg_tok + 2 * j] = s0;
+                    dbg[s * dbg_tok + 2 * j + 1] = s1;
+                }
+                mainI[s] += sc0 * s0 + sc1 * s1;
+                minI[s] += m0 * bp0 + m1 * bp1;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = d8 * (d * float(mainI[s]) - dmin * float(minI[s]));
+        }
+    }
+};
+
 // Q8_0, one unit (8 blocks of 34 B) per lane: value = sum_blk (d_w*d8) * isum
 // (reference SIMDMatMulVecAVX2.cpp:4339-4366).
 template <int S>
@@ -1130,7 +1200,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     const uint32_t ntiles_mat = (per_mat + kTileUnits - 1) / kTileUnits;
     const uint32_t ntiles = ntiles_mat * pairs;
     const size_t nbr = TYPE == kQ8_0 ? jb.cols / 32 : jb.cols / 256;
-    const size_t per = TYPE == kQ4_K ? 8 : 1;
+    const size_t per = TYPE == kQ4_K || TYPE == kQ5_K ? 8 : 1;
     const size_t dbg_tok = size_t(jb.rows) * nbr * per;
     const size_t xtok = size_t(nu) * XB;
     // Expert of rank m (rank-group mode; m is wave-uniform).
@@ -1439,7 +1509,7 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     return o;
 }
 
-bool tiled_type(int type) { return type == kQ4_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -1518,6 +1588,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
     const uint32_t lds = fixed + max_part;
     switch (type) {
         case kQ4_K: return launch_tiled<kQ4_K, C>(S, a, wg, lds, st);
+        case kQ5_K: return launch_tiled<kQ5_K, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:

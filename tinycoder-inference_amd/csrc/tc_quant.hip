@@ -151,6 +151,59 @@ __device__ void enc_q4k(const float *x, uint8_t *out) {
     }
 }
 
+// Q5_K (this build's encoder; the reference ships none): per-32 affine scale
+// (max-min)/31 and min -min, fp16 (RNE) super-scales max/63, 6-bit sub-scales
+// and mins packed like Q4_K's, q = clamp(rne((x + dmin*m)/(d*sc)), 0, 31) with
+// the low nibbles in qs and the fifth bits in qh, as the reference decoder
+// reads them (include/GGMLDequantize.hpp:346-380).
+__device__ void enc_q5k(const float *x, uint8_t *out) {
+    float scale[8], minv[8];
+    float maxScale = 0.0f, maxMin = 0.0f;
+    for (int g = 0; g < 8; ++g) {
+        const float *xp = x + 32 * g;
+        float mn = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            mn = xp[i] < mn ? xp[i] : mn;
+            mx = mx < xp[i] ? xp[i] : mx;
+        }
+        scale[g] = __fdiv_rn(mx - mn, 31.0f);
+        minv[g] = -mn;
+        maxScale = maxScale < scale[g] ? scale[g] : maxScale;
+        maxMin = maxMin < minv[g] ? minv[g] : maxMin;
+    }
+    const uint16_t hd = maxScale > 0.0f ? f2h_rne(__fdiv_rn(maxScale, 63.0f)) : 0;
+    const uint16_t hdm = maxMin > 0.0f ? f2h_rne(__fdiv_rn(maxMin, 63.0f)) : 0;
+    const float d = h2f(hd), dm = h2f(hdm);
+    uint8_t sc6[8], m6[8];
+    for (int g = 0; g < 8; ++g) {
+        const int s = d > 0.0f ? int(rintf(__fdiv_rn(scale[g], d))) : 0;
+        const int m = dm > 0.0f ? int(rintf(__fdiv_rn(minv[g], dm))) : 0;
+        sc6[g] = uint8_t(s < 0 ? 0 : (s > 63 ? 63 : s));
+        m6[g] = uint8_t(m < 0 ? 0 : (m > 63 ? 63 : m));
+    }
+    out[0] = uint8_t(hd);
+    out[1] = uint8_t(hd >> 8);
+    out[2] = uint8_t(hdm);
+    out[3] = uint8_t(hdm >> 8);
+    for (int j = 0; j < 4; ++j) {
+        out[4 + j] = uint8_t(sc6[j] | ((sc6[j + 4] >> 4) << 6));
+        out[8 + j] = uint8_t(m6[j] | ((m6[j + 4] >> 4) << 6));
+        out[12 + j] = uint8_t((sc6[j + 4] & 0x0F) | ((m6[j + 4] & 0x0F) << 4));
+    }
+    uint8_t *qh = out + 16, *qs = out + 48;
+    for (int i = 0; i < 160; ++i) out[16 + i] = 0;
+    for (int g = 0; g < 8; ++g) {
+        const float es = d * float(sc6[g]), em = dm * float(m6[g]);
+        const int c = g >> 1, h = g & 1;
+        for (int l = 0; l < 32; ++l) {
+            int v = es > 0.0f ? int(rintf(__fdiv_rn(x[32 * g + l] + em, es))) : 0;
+            v = v < 0 ? 0 : (v > 31 ? 31 : v);
+            qs[32 * c + l] |= uint8_t((v & 15) << (4 * h));
+            qh[l] |= uint8_t((v >> 4) << (2 * c + h));
+        }
+    }
+}
+
 // Q8_0 (8 blocks of 32): d = max|w|/127 as fp16 (RNE), q = rne(w/d), +-127.
 __device__ void enc_q8_0(const float *x, uint8_t *out) {
     for (int b = 0; b < 8; ++b) {
@@ -289,6 +342,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
     switch (type) {
         case kQ4_K: enc_q4k(xu, o); break;
         case kQ8_0: enc_q8_0(xu, o); break;
+        case kQ5_K: enc_q5k(xu, o); break;
         case kQ6_K: enc_q6k(xu, o); break;
         default: enc_iq3xxs(xu, o); break;
     }
