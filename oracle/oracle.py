@@ -148,6 +148,19 @@ class Reference(_Lib):
         L.ref_dot_iq3xxs_q8k.restype = ctypes.c_float
         L.ref_dot_iq3xxs_q8k.argtypes = [_P, _P]
         L.ref_matmul.argtypes = [ctypes.c_int, _P, _P, _U32, _U32, _U32, _P]
+        L.ref_gguf_open.restype = _P
+        L.ref_gguf_open.argtypes = [ctypes.c_char_p, ctypes.c_int]
+        L.ref_gguf_close.argtypes = [_P]
+        L.ref_gguf_count.restype = ctypes.c_uint64
+        L.ref_gguf_count.argtypes = [_P]
+        L.ref_gguf_record.argtypes = [_P, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_uint64, _P, _P, _P, _P]
+        L.ref_gguf_tensor.restype = _P
+        L.ref_gguf_tensor.argtypes = [_P, ctypes.c_char_p]
+        L.ref_gguf_config.argtypes = [_P, _P, _P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_uint64]
+        L.ref_ggml_type_size.restype = _U32
+        L.ref_ggml_type_size.argtypes = [_U32]
+        L.ref_ggml_block_size.restype = _U32
+        L.ref_ggml_block_size.argtypes = [_U32]
         self.threads = L.ref_init_threads(threads)
 
     def quantize_q8k(self, x):
@@ -187,6 +200,50 @@ class Reference(_Lib):
         rc = self.lib.ref_matmul(qtype, _ptr(w), _ptr(x), S, rows, cols, _ptr(out))
         assert rc == 0
         return out
+
+
+class RefGGUF:
+    """The reference's own GGUFLoader (compiled from its sources) on one file:
+    records, tensor bytes and the parsed config."""
+
+    def __init__(self, ref, path, metadata_only=False):
+        self.ref, self.L = ref, ref.lib
+        self.h = self.L.ref_gguf_open(os.fsencode(path), int(metadata_only))
+
+    @property
+    def ok(self):
+        return bool(self.h)
+
+    def close(self):
+        if self.h:
+            self.L.ref_gguf_close(self.h)
+            self.h = None
+
+    def records(self):
+        out = []
+        for i in range(self.L.ref_gguf_count(self.h)):
+            name = ctypes.create_string_buffer(4096)
+            t, nd = np.zeros(1, np.uint32), np.zeros(1, np.uint32)
+            dims, off = np.zeros(4, np.uint32), np.zeros(1, np.uint64)
+            assert self.L.ref_gguf_record(self.h, i, name, 4096, _ptr(t), _ptr(nd), _ptr(dims), _ptr(off)) == 0
+            out.append((name.value.decode(), int(t[0]), tuple(int(d) for d in dims[:nd[0]]), int(off[0])))
+        return out
+
+    def tensor(self, name, nbytes):
+        p = self.L.ref_gguf_tensor(self.h, name.encode())
+        return None if not p else np.frombuffer((ctypes.c_uint8 * nbytes).from_address(p), np.uint8).copy()
+
+    def config(self):
+        u, f = np.zeros(16, np.uint32), np.zeros(2, np.float32)
+        arch, name = ctypes.create_string_buffer(256), ctypes.create_string_buffer(256)
+        self.L.ref_gguf_config(self.h, _ptr(u), _ptr(f), arch, name, 256)
+        keys = ["numLayers", "maxSeqLen", "hiddenSize", "intermediateSize", "numAttentionHeads", "numKVHeads",
+                "vocabSize", "expertCount", "expertUsedCount", "expertFeedForwardLength", "ropeDimensionCount",
+                "sec0", "sec1", "sec2", "sec3", "headDim"]
+        c = {k: int(v) for k, v in zip(keys, u)}
+        c["ropeTheta"], c["finalLogitSoftcapping"] = float(f[0]), float(f[1])
+        c["architecture"], c["modelName"] = arch.value.decode(), name.value.decode()
+        return c
 
 
 def available_reference():

@@ -7,11 +7,13 @@
 // Nothing here restates arithmetic: each wrapper forwards to the reference
 // function named in its comment (paths relative to the reference root).
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <vector>
 
 #include "GGMLDequantize.hpp"
 #include "GGMLQuantize.hpp"
+#include "GGUFLoader.hpp"
 #include "SIMDMatMulVecInternal.hpp"
 #include "ThreadPool.hpp"
 
@@ -88,5 +90,54 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
         default: return -1;
     }
 }
+
+// ---- GGUF reader (include/GGUFLoader.hpp:48) ---------------------------------
+// A loader handle; load() or loadMetadata() per `metadata_only`. NULL on failure.
+void *ref_gguf_open(const char *path, int metadata_only) {
+    auto *g = new GGUFLoader();
+    const bool ok = metadata_only ? g->loadMetadata(path) : g->load(path);
+    if (!ok) {
+        delete g;
+        return nullptr;
+    }
+    return g;
+}
+void ref_gguf_close(void *h) { delete static_cast<GGUFLoader *>(h); }
+// tensorRecords() (GGUFLoader.cpp:1020): count, then record i.
+uint64_t ref_gguf_count(void *h) { return static_cast<GGUFLoader *>(h)->tensorRecords().size(); }
+int ref_gguf_record(void *h, uint64_t i, char *name, uint64_t cap, uint32_t *type, uint32_t *n_dims,
+                    uint32_t *dims, uint64_t *offset) {
+    const auto &recs = static_cast<GGUFLoader *>(h)->tensorRecords();
+    if (i >= recs.size()) return -1;
+    const TensorInfo &r = recs[i];
+    std::snprintf(name, cap, "%s", r.name.c_str());
+    *type = r.type;
+    *n_dims = static_cast<uint32_t>(r.shape.size());
+    for (size_t d = 0; d < r.shape.size() && d < 4; ++d) dims[d] = r.shape[d];
+    *offset = r.offset;
+    return 0;
+}
+// getTensor (GGUFLoader.cpp:987).
+const uint8_t *ref_gguf_tensor(void *h, const char *name) { return static_cast<GGUFLoader *>(h)->getTensor(name); }
+// config() fields parsed from the metadata (GGUFLoader.cpp:595-690):
+// u[0..15] = numLayers, maxSeqLen, hiddenSize, intermediateSize,
+// numAttentionHeads, numKVHeads, vocabSize, expertCount, expertUsedCount,
+// expertFeedForwardLength, ropeDimensionCount, ropeDimensionSections[0..3],
+// headDim; f[0..1] = ropeTheta, finalLogitSoftcapping; arch / name strings.
+void ref_gguf_config(void *h, uint32_t *u, float *f, char *arch, char *name, uint64_t cap) {
+    const ModelConfig &c = static_cast<GGUFLoader *>(h)->config();
+    const uint32_t v[16] = {c.numLayers, c.maxSeqLen, c.hiddenSize, c.intermediateSize, c.numAttentionHeads,
+                            c.numKVHeads, c.vocabSize, c.expertCount, c.expertUsedCount, c.expertFeedForwardLength,
+                            c.ropeDimensionCount, c.ropeDimensionSections[0], c.ropeDimensionSections[1],
+                            c.ropeDimensionSections[2], c.ropeDimensionSections[3], c.headDim};
+    std::memcpy(u, v, sizeof v);
+    f[0] = c.ropeTheta;
+    f[1] = c.finalLogitSoftcapping;
+    std::snprintf(arch, cap, "%s", c.architecture.c_str());
+    std::snprintf(name, cap, "%s", c.modelName.c_str());
+}
+// ggmlTypeSize / ggmlBlockSize (GGUFLoader.cpp:64, :130).
+uint32_t ref_ggml_type_size(uint32_t t) { return ggmlTypeSize(t); }
+uint32_t ref_ggml_block_size(uint32_t t) { return ggmlBlockSize(t); }
 
 }  // extern "C"

@@ -173,6 +173,11 @@ int check_common(int type, const void *w, const void *x, const void *out, uint32
 
 }  // namespace
 
+namespace tc {
+// Error text for the calling thread's tc_last_error() (used by tc_gguf.cpp).
+void set_error(const std::string &msg) { g_err = msg; }
+}  // namespace tc
+
 extern "C" {
 
 int tc_available(void) {

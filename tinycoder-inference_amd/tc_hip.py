@@ -45,6 +45,22 @@ SIGNATURES = {
     "tc_probe_sink_bytes": (ctypes.c_size_t, []),
     "tc_probe_mfma_i8": (_I, [_U32, _U32, _P, _P]),
     "tc_probe_read": (_I, [_P, ctypes.c_size_t, _U32, _P, _P]),
+    "tc_gguf_open": (_P, [ctypes.c_char_p]),
+    "tc_gguf_open_metadata": (_P, [ctypes.c_char_p]),
+    "tc_gguf_close": (None, [_P]),
+    "tc_gguf_version": (_U32, [_P]),
+    "tc_gguf_tensor_count": (ctypes.c_uint64, [_P]),
+    "tc_gguf_metadata_count": (ctypes.c_uint64, [_P]),
+    "tc_gguf_data_offset": (ctypes.c_uint64, [_P]),
+    "tc_gguf_find_tensor": (ctypes.c_int64, [_P, ctypes.c_char_p]),
+    "tc_gguf_tensor_info": (_I, [_P, ctypes.c_uint64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U32),
+                                 ctypes.POINTER(_U32), ctypes.POINTER(ctypes.c_uint64),
+                                 ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "tc_gguf_tensor_data": (_P, [_P, ctypes.c_uint64]),
+    "tc_gguf_upload": (_I, [_P, ctypes.c_uint64, _P, ctypes.c_uint64, _P]),
+    "tc_gguf_meta": (ctypes.c_char_p, [_P, ctypes.c_char_p]),
+    "tc_gguf_type_size": (_U32, [_U32]),
+    "tc_gguf_block_size": (_U32, [_U32]),
 }
 
 
@@ -226,4 +242,116 @@ class Library:
             out = torch.empty((S, hidden), dtype=torch.float32, device=x.device)
         self._check(self.lib.tc_moe_ffn(_ptr(x), _ptr(ids), _ptr(wts), S, K, _ptr(wg), _ptr(wu), _ptr(wd),
                                         n_experts, hidden, ff, _ptr(out), self._stream()))
+        return out
+
+
+class TensorRecord:
+    """One GGUF tensor record (the reference's TensorInfo, IModelLoader.hpp:145:
+    name, offset into the data section, shape in file order, GGML type), plus
+    its byte size."""
+
+    __slots__ = ("index", "name", "type", "shape", "offset", "bytes")
+
+    def __init__(self, index, name, type_, shape, offset, nbytes):
+        self.index, self.name, self.type, self.shape = index, name, type_, shape
+        self.offset, self.bytes = offset, nbytes
+
+    def __repr__(self):
+        return f"TensorRecord({self.name!r}, type={self.type}, shape={self.shape}, bytes={self.bytes})"
+
+
+class GGUFLoader:
+    """GGUF v3 reader over the C-ABI (tc_gguf_*), shaped like the reference's
+    tinycoder::GGUFLoader (include/GGUFLoader.hpp:48): load / loadMetadata,
+    getTensor (host bytes, a read-only numpy view of the mapping),
+    getTensorInfo, tensorRecords, and upload() to put a tensor's raw blocks in
+    device memory for the mat-vec / GEMM entry points. load() returns False on
+    failure like the reference; the reason is in last_error."""
+
+    def __init__(self, lib=None):
+        self.lib = lib if lib is not None else load_library()
+        self.h = None
+        self.last_error = ""
+
+    def _open(self, path, fn):
+        self.close()
+        h = fn(os.fsencode(path))
+        if not h:
+            self.last_error = self.lib.tc_last_error().decode()
+            return False
+        self.h = h
+        return True
+
+    def load(self, path):
+        return self._open(path, self.lib.tc_gguf_open)
+
+    def loadMetadata(self, path):  # noqa: N802 (the reference's name)
+        return self._open(path, self.lib.tc_gguf_open_metadata)
+
+    def close(self):
+        if self.h:
+            self.lib.tc_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def version(self):
+        return self.lib.tc_gguf_version(self.h)
+
+    @property
+    def data_offset(self):
+        return self.lib.tc_gguf_data_offset(self.h)
+
+    def metadata(self, key):
+        v = self.lib.tc_gguf_meta(self.h, key.encode())
+        return None if v is None else v.decode("utf-8", "surrogateescape")
+
+    def _record(self, i):
+        name = ctypes.c_char_p()
+        t, nd = ctypes.c_uint32(), ctypes.c_uint32()
+        dims = (ctypes.c_uint64 * 4)()
+        off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+        rc = self.lib.tc_gguf_tensor_info(self.h, i, ctypes.byref(name), ctypes.byref(t), ctypes.byref(nd),
+                                          dims, ctypes.byref(off), ctypes.byref(nb))
+        if rc != TC_OK:
+            raise TCError(rc, self.lib.tc_last_error().decode())
+        return TensorRecord(i, name.value.decode("utf-8", "surrogateescape"), t.value,
+                            tuple(dims[k] for k in range(nd.value)), off.value, nb.value)
+
+    def tensorRecords(self):  # noqa: N802
+        return [self._record(i) for i in range(self.lib.tc_gguf_tensor_count(self.h))]
+
+    def getTensorInfo(self, name):  # noqa: N802
+        i = self.lib.tc_gguf_find_tensor(self.h, name.encode())
+        return None if i < 0 else self._record(i)
+
+    def getTensor(self, name):  # noqa: N802
+        import numpy as np
+        rec = self.getTensorInfo(name)
+        if rec is None:
+            return None
+        p = self.lib.tc_gguf_tensor_data(self.h, rec.index)
+        if not p:
+            return None
+        buf = (ctypes.c_uint8 * rec.bytes).from_address(p)
+        a = np.frombuffer(buf, dtype=np.uint8)
+        a.flags.writeable = False
+        return a
+
+    def upload(self, name, device="cuda"):
+        """Raw block bytes of tensor `name` as a uint8 device tensor."""
+        import torch
+        rec = self.getTensorInfo(name)
+        if rec is None:
+            raise KeyError(name)
+        out = torch.empty(rec.bytes, dtype=torch.uint8, device=device)
+        rc = self.lib.tc_gguf_upload(self.h, rec.index, _ptr(out), rec.bytes,
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != TC_OK:
+            raise TCError(rc, self.lib.tc_last_error().decode())
         return out
