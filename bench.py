@@ -277,6 +277,43 @@ def moe_bench(torch, tc, tc_hip, dev, reps):
     return res
 
 
+def moe_prefill_bench(torch, tc, tc_hip, dev, reps):
+    """MoE prefill (the reference's moeBatchExperts case, MoeBatch.cu:37-197)
+    at the config-5 expert shapes: T tokens x top-8, routed on the device,
+    each matrix one grouped int8 MFMA GEMM over all experts ("gemm"); beside
+    it the per-(token, rank) mat-vec path ("pairs") on the same inputs (the
+    library takes the GEMM from 160 tokens). TOPS = 2 * T * 8 *
+    3 * 768 * 2048 int8 ops / time (the whole FFN, router and combine
+    included)."""
+    E, K, H, FF = 128, 8, 2048, 768
+    gen = torch.Generator(device=dev).manual_seed(19)
+
+    def enc(r, c):
+        return tc.encode(tc_hip.Q4_K, torch.randn((r, c), generator=gen, device=dev) * 0.02)
+
+    wg, wu, wd = enc(E * FF, H), enc(E * FF, H), enc(E * H, FF)
+    rng = np.random.default_rng(23)
+    res = []
+    for T in (16, 64, 256, 1024):
+        ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+        lg = rng.standard_normal((T, K)).astype(np.float32)
+        w = (np.exp(lg) / np.exp(lg).sum(1, keepdims=True)).astype(np.float32)
+        idd, wd_ = torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev)
+        x = torch.randn((T, H), generator=gen, device=dev)
+        out = torch.empty((T, H), device=dev)
+        ops = 2.0 * T * K * 3 * FF * H
+        row = {"tokens": T}
+        for name, thr in (("gemm", 0), ("pairs", 1 << 30)):
+            tc.lib.tc_moe_set_gemm_min_tokens(thr)
+            us = timed(torch, lambda i: tc.moe_ffn(x, idd, wd_, wg, wu, wd, E, H, FF, out=out), reps)
+            row[name] = {"us": round(us, 1), "TOPS": round(ops / us / 1e6, 1)}
+        tc.lib.tc_moe_set_gemm_min_tokens(160)
+        res.append(row)
+    del wg, wu, wd
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -431,6 +468,7 @@ def main():
     if not args.no_other:
         line["decode_other_formats"] = other_decode_bench(torch, tc, tc_hip, dev, max(20, args.steps // 2))
         line["moe"] = moe_bench(torch, tc, tc_hip, dev, max(20, args.steps // 2))
+        line["moe_prefill"] = moe_prefill_bench(torch, tc, tc_hip, dev, 10)
     if not args.no_gemm:
         del copies
         torch.cuda.empty_cache()

@@ -132,10 +132,19 @@ size_t tc_row_bytes(int type, uint32_t cols);
  * out[s] += wts[s][r] * (Wd[e] h), summed over r in rank order.
  * wg, wu: [n_experts][ff][hidden]; wd: [n_experts][hidden][ff] (Q4_K blocks).
  * ids int32 [seq_len][top_k], wts fp32 [seq_len][top_k], x [seq_len][hidden],
- * out [seq_len][hidden]; all device pointers. */
+ * out [seq_len][hidden]; all device pointers.
+ * From tc_moe_set_gemm_min_tokens tokens on (default 160; the prefill case
+ * of the reference's moeBatchExperts, MoeBatch.cu:37-197) the pairs are
+ * sorted by expert on the device and each matrix runs as ONE grouped int8
+ * MFMA GEMM over all experts; below it, one mat-vec per (token, rank) pair. */
 int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t seq_len, uint32_t top_k,
                const void *wg, const void *wu, const void *wd, uint32_t n_experts, uint32_t hidden,
                uint32_t ff, float *out, void *stream);
+
+/* Token count from which tc_moe_ffn takes the grouped-GEMM path (no
+ * reference counterpart: a tuning knob like int8GemmSetQ8Enabled; 0 = always,
+ * UINT32_MAX = never). Process-wide. */
+void tc_moe_set_gemm_min_tokens(uint32_t n);
 
 /* Parity hooks over host data (the reference's GPUModel::debugQ8KRow,
  * debugQ8_0Row, debugQ8KBlocks and debugQ8_0Blocks, include/GPUCompute.hpp:

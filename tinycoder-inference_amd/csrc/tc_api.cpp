@@ -82,6 +82,10 @@ bool ensure(void *&p, size_t &cap, size_t need) {
     return true;
 }
 
+// Bytes past a GEMM activation buffer that the MFMA kernel's tail loads may
+// touch: one 128-token tile of 256-byte rows.
+constexpr size_t kGemmActSlack = 128 * 256;
+
 bool type_ok(int t) { return t == TC_Q8_0 || t == TC_Q4_K || t == TC_Q5_K || t == TC_Q6_K || t == TC_IQ3_XXS; }
 
 bool g_q8_gemm_enabled = true;
@@ -307,7 +311,11 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
     // Quantize all tokens once, then the MFMA kernel.
     const tc::ActLayout L = tc::act_layout(type, seq_len, cols);
     const size_t ws = tc::gemm_workspace_bytes(type, seq_len, rows, cols, dev->num_cu);
-    if (!ensure(dev->act, dev->act_bytes, L.bytes)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", L.bytes);
+    // + kGemmActSlack: the MFMA kernel's loads for token rows past M in the
+    // last superblock run up to one token tile past the buffer (values never
+    // stored; the buffer range check covers only the per-lane offset).
+    if (!ensure(dev->act, dev->act_bytes, L.bytes + kGemmActSlack))
+        return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", L.bytes + kGemmActSlack);
     if (ws && !ensure(dev->aux, dev->aux_bytes, ws)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", ws);
     hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, dev->act, st, true);
     if (e != hipSuccess) return hip_fail(e, "activation quantizer");
@@ -371,6 +379,74 @@ int tc_encode(int type, const float *x, void *out, uint32_t rows, uint32_t cols,
     return TC_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Token count from which tc_moe_ffn runs the grouped GEMM. Below it the
+// per-pair mat-vecs win: at these sizes every expert sits in the Infinity
+// Cache and the mat-vec work, not HBM, sets the time, while the GEMM pays
+// for whole 128-row token tiles per expert (measured crossover 128-256
+// tokens for 128 experts x top-8).
+uint32_t g_moe_gemm_min_tokens = 160;
+
+// MoE prefill over expert-sorted rows: device-side routing, the grouped Q4_K
+// MFMA GEMM for gate and up (one launch each over all experts), SwiGLU, the
+// grouped down GEMM, and the rank-order combination.
+int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wts, uint32_t T, uint32_t top_k,
+                const void *wg, const void *wu, const void *wd, uint32_t E, uint32_t H, uint32_t FF, float *out,
+                hipStream_t st) {
+    const uint32_t P = T * top_k;
+    const uint32_t ntm_max = tc::moe_max_tiles(P, E, 128);
+    auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
+    const tc::ActLayout LX = tc::act_layout(TC_Q4_K, P, H), LH = tc::act_layout(TC_Q4_K, P, FF);
+    const size_t ws = std::max(tc::gemm_grouped_workspace_bytes(ntm_max, FF, H, dev->num_cu),
+                               tc::gemm_grouped_workspace_bytes(ntm_max, H, FF, dev->num_cu));
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += up(bytes);
+        return o;
+    };
+    const size_t o_pos = take(size_t(P) * 4), o_tok = take(size_t(P) * 4), o_mt = take(size_t(ntm_max) * 12),
+                 o_ntm = take(4), o_g = take(size_t(P) * FF * 4), o_u = take(size_t(P) * FF * 4),
+                 o_y = take(size_t(P) * H * 4), o_ax = take(LX.bytes + kGemmActSlack),
+                 o_ah = take(LH.bytes + kGemmActSlack), o_ws = take(ws);
+    if (!ensure(dev->aux, dev->aux_bytes, off)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", off);
+    char *b = static_cast<char *>(dev->aux);
+    int32_t *pos = reinterpret_cast<int32_t *>(b + o_pos);
+    uint32_t *tok = reinterpret_cast<uint32_t *>(b + o_tok), *mt = reinterpret_cast<uint32_t *>(b + o_mt);
+    uint32_t *ntm = reinterpret_cast<uint32_t *>(b + o_ntm);
+    float *g = reinterpret_cast<float *>(b + o_g), *u = reinterpret_cast<float *>(b + o_u);
+    float *y = reinterpret_cast<float *>(b + o_y);
+    const uint64_t gstride = uint64_t(FF) * (H / 256) * 144, dstride = uint64_t(H) * (FF / 256) * 144;
+
+    hipError_t e = tc::launch_moe_route(ids, P, top_k, E, 1, 128, pos, tok, mt, ntm, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE router");
+    e = tc::launch_quant_act_rows(x, tok, P, H, LX, b + o_ax, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE activation gather");
+    const tc::ActView ax = act_view(b + o_ax, LX, 0, TC_Q4_K, H);
+    e = tc::launch_gemm_grouped(wg, gstride, ax, g, P, FF, H, mt, ntm, ntm_max, dev->num_cu, b + o_ws, st);
+    if (e == hipSuccess)
+        e = tc::launch_gemm_grouped(wu, gstride, ax, u, P, FF, H, mt, ntm, ntm_max, dev->num_cu, b + o_ws, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE gate/up GEMM");
+    e = tc::launch_moe_swiglu(g, u, P, FF, st);
+    if (e == hipSuccess) e = tc::launch_quant_act(TC_Q4_K, g, P, FF, LH, b + o_ah, st, true);
+    if (e != hipSuccess) return hip_fail(e, "MoE SwiGLU");
+    const tc::ActView ah = act_view(b + o_ah, LH, 0, TC_Q4_K, FF);
+    e = tc::launch_gemm_grouped(wd, dstride, ah, y, P, H, FF, mt, ntm, ntm_max, dev->num_cu, b + o_ws, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE down GEMM");
+    e = tc::launch_moe_combine_rows(y, pos, wts, out, T, top_k, H, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE combine");
+    return TC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void tc_moe_set_gemm_min_tokens(uint32_t n) { g_moe_gemm_min_tokens = n; }
+
 int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t seq_len, uint32_t top_k,
                const void *wg, const void *wu, const void *wd, uint32_t n_experts, uint32_t hidden, uint32_t ff,
                float *out, void *stream) {
@@ -384,6 +460,9 @@ int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t se
     const uint64_t npairs = uint64_t(seq_len) * top_k;
     if (npairs > (1u << 20)) return fail(TC_E_UNSUPPORTED, "too many (token, rank) pairs");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (seq_len >= g_moe_gemm_min_tokens && n_experts <= 4096 &&
+        uint64_t(npairs) * std::max(hidden, ff) < (uint64_t(1) << 32))
+        return moe_grouped(dev, x, ids, wts, seq_len, top_k, wg, wu, wd, n_experts, hidden, ff, out, st);
     // Scratch: h and u [pairs][ff], per-pair down outputs [pairs][hidden].
     const size_t hb = (npairs * ff * 4 + 255) & ~size_t(255);
     const size_t need = 2 * hb + npairs * hidden * 4;

@@ -86,6 +86,14 @@ struct GemmArgs {
     uint32_t ntiles;        // output tiles (Q4_K stream-K)
     uint32_t skg;           // stream-K workgroups
     float *ws;              // Q4_K stream-K partial tiles [grid][2][GM][GN]
+    // Grouped (MoE) mode: token tile i covers rows [mt[3i], mt[3i+1]) of the
+    // expert-sorted activations and uses expert mt[3i+2]'s matrix at
+    // W + expert * wstride; the tile count is read from *ntm_dev (written on
+    // the device by the router).
+    const uint32_t *mt;
+    const uint32_t *ntm_dev;
+    uint64_t wstride;
+    uint32_t ntn;           // row blocks (N tiles)
 };
 
 __device__ __forceinline__ u4 lds4(const unsigned char *p) { return *reinterpret_cast<const u4 *>(p); }
@@ -138,9 +146,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t grsrc(const void *p, uint64_t 
 }
 
 template <int TYPE>
-__device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t tid) {
+__device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t tid,
+                                         const uint8_t *W = nullptr) {
     GSrc g;
-    g.w = grsrc(a.W, uint64_t(a.N) * a.row_bytes);
+    g.w = grsrc(W != nullptr ? W : a.W, uint64_t(a.N) * a.row_bytes);
     g.q = grsrc(a.qs, uint64_t(a.M) * a.K);
     g.d = grsrc(a.d8, uint64_t(a.M) * (a.K / (TYPE == kQ8_0 ? 32 : 256)) * 4);
     g.bs = grsrc(a.bsums, TYPE == kQ8_0 ? 0 : uint64_t(a.M) * (a.K / 16) * 2);
@@ -509,17 +518,41 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 // Tile t -> (token tile, row block), token tiles fastest: a stream-K
 // workgroup's consecutive tiles reuse one block of weight rows. (Row blocks
 // fastest measured 3-13% slower.)
-__device__ __forceinline__ void sk_tile(const GemmArgs &a, uint32_t t, uint32_t &m0, uint32_t &n0) {
-    const uint32_t tm = t % a.ntm, tn = t / a.ntm;
-    m0 = tm * GM;
-    n0 = tn * GN;
+// Grouped mode: the same order over the device tile table; mend bounds the
+// stored rows and W is the tile's expert matrix.
+struct TileGeom {
+    uint32_t m0, mend, n0;
+    const uint8_t *W;
+};
+template <bool GRP>
+__device__ __forceinline__ TileGeom sk_tile(const GemmArgs &a, uint32_t ntm, uint32_t t) {
+    const uint32_t tm = t % ntm, tn = t / ntm;
+    TileGeom g;
+    g.n0 = tn * GN;
+    if constexpr (GRP) {
+        g.m0 = a.mt[3 * tm];
+        g.mend = a.mt[3 * tm + 1];
+        g.W = a.W + uint64_t(a.mt[3 * tm + 2]) * a.wstride;
+    } else {
+        g.m0 = tm * GM;
+        g.mend = a.M;
+        g.W = a.W;
+    }
+    return g;
+}
+template <bool GRP>
+__device__ __forceinline__ uint32_t sk_ntm(const GemmArgs &a) {
+    if constexpr (GRP)
+        return *a.ntm_dev;
+    else
+        return a.ntm;
 }
 
 __host__ __device__ inline uint32_t sk_begin(uint32_t units, uint32_t grid, uint32_t w) {
     return uint32_t(uint64_t(units) * w / grid);
 }
 
-template <int CW>
+template <int CW, bool GRP>
 __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 + CW / 4, 1 + CW / 4))) void k_gemm_q4k_ws(
     GemmArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -534,7 +567,8 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
     const uint32_t ptid = tid - 64 * CW;  // producer thread index 0..255
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
 
-    const uint32_t units = a.ntiles * a.nblk;
+    const uint32_t ntm = sk_ntm<GRP>(a);
+    const uint32_t units = (GRP ? ntm * a.ntn : a.ntiles) * a.nblk;
     const uint32_t ub = sk_begin(units, gridDim.x, blockIdx.x), ue = sk_begin(units, gridDim.x, blockIdx.x + 1);
     for (uint32_t u = ub; u < ue;) {
         const uint32_t tile = u / a.nblk;
@@ -543,8 +577,8 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
         const bool whole = b0 == 0 && b1 == a.nblk;
         float *const part = whole ? nullptr : a.ws + (size_t(blockIdx.x) * 2 + (u == ub ? 0 : 1)) * (GM * GN);
         u += b1 - b0;
-        uint32_t m0, n0;
-        sk_tile(a, tile, m0, n0);
+        const TileGeom tg = sk_tile<GRP>(a, ntm, tile);
+        const uint32_t m0 = tg.m0, n0 = tg.n0;
         // Producers step in pairs of superblocks; both sides run bend - b0 barriers.
         const uint32_t bend = b0 + ((b1 - b0 + 1) & ~1u);
 
@@ -553,7 +587,7 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
         if (producer) {
             // Two superblocks of loads in flight per producer thread: global
             // latency under load exceeds one superblock's compute time.
-            const GSrc gs = gemm_src<kQ4_K>(a, n0, m0, ptid);
+            const GSrc gs = gemm_src<kQ4_K>(a, n0, m0, ptid, tg.W);
             GPrefetch<kQ4_K> pa, pb;
             gemm_prefetch<kQ4_K>(a, gs, b0, pa);
             gemm_stage<kQ4_K>(pa, buf(b0), ptid);
@@ -601,7 +635,7 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
                 const float4 v = make_float4(acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]);
                 if (part != nullptr) {
                     *reinterpret_cast<float4 *>(part + ml * GN + nl) = v;  // [token][row] of the tile
-                } else if (m < a.M) {
+                } else if (m < tg.mend) {
                     float *o = a.out + size_t(m) * a.N + n;
                     if (n + 3 < a.N && (a.N & 3) == 0) {
                         *reinterpret_cast<float4 *>(o) = v;
@@ -619,16 +653,20 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
 
 // Tiles split over several stream-K workgroups: out = the partial segments
 // summed in workgroup order (one workgroup per tile; whole tiles exit).
+template <bool GRP>
 __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
-    const uint32_t tile = blockIdx.x, units = a.ntiles * a.nblk, G = a.skg;
+    const uint32_t ntm = sk_ntm<GRP>(a);
+    const uint32_t ntiles = GRP ? ntm * a.ntn : a.ntiles;
+    const uint32_t tile = blockIdx.x, units = ntiles * a.nblk, G = a.skg;
+    if (tile >= ntiles) return;  // grouped mode: the grid covers the largest possible tile count
     const uint32_t t0 = tile * a.nblk, t1 = t0 + a.nblk;
     // first workgroup whose range holds unit t0
     uint32_t w = uint32_t(uint64_t(t0) * G / units);
     while (w + 1 < G && sk_begin(units, G, w + 1) <= t0) ++w;
     while (w > 0 && sk_begin(units, G, w) > t0) --w;
     if (sk_begin(units, G, w) <= t0 && sk_begin(units, G, w + 1) >= t1) return;  // one workgroup: stored directly
-    uint32_t m0, n0;
-    sk_tile(a, tile, m0, n0);
+    const TileGeom tg = sk_tile<GRP>(a, ntm, tile);
+    const uint32_t m0 = tg.m0, n0 = tg.n0;
     for (uint32_t i = threadIdx.x; i < GM * GN / 4; i += 256) {
         const uint32_t ml = (4 * i) / GN, nl = (4 * i) % GN;
         float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -642,7 +680,7 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
             s.w += p.w;
         }
         const uint32_t m = m0 + ml, n = n0 + nl;
-        if (m >= a.M) continue;
+        if (m >= tg.mend) continue;
         const float sv[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -660,14 +698,14 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
     out[i] = s;
 }
 
-template <int TYPE>
+template <int TYPE, bool GRP = false>
 hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
     if constexpr (TYPE == kQ4_K) {
         constexpr int CW = 8;  // consumer waves (4 measured 10-15% slower)
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_q4k_ws<CW>),
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_q4k_ws<CW, GRP>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (attr != hipSuccess) return attr;
-        k_gemm_q4k_ws<CW><<<grid, GT + 64 * CW, 2 * GLds<TYPE>::bytes, st>>>(a);
+        k_gemm_q4k_ws<CW, GRP><<<grid, GT + 64 * CW, 2 * GLds<TYPE>::bytes, st>>>(a);
     } else {
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<TYPE>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -700,6 +738,52 @@ size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int nu
     if (type == kQ4_K) return size_t(sk_grid(M, N, K, num_cu)) * 2 * GM * GN * 4;
     const uint32_t s = gemm_splits(type, M, N, K, num_cu);
     return s > 1 ? size_t(s) * M * N * 4 : 0;
+}
+
+namespace {
+uint32_t grouped_grid(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
+    const uint64_t units = uint64_t(ntm_max) * ((N + GN - 1) / GN) * (K / 256);
+    return uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(uint64_t(num_cu), units / 4)));
+}
+}  // namespace
+
+size_t gemm_grouped_workspace_bytes(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
+    return size_t(grouped_grid(ntm_max, N, K, num_cu)) * 2 * GM * GN * 4;
+}
+
+hipError_t launch_gemm_grouped(const void *W, uint64_t wstride, const ActView &act, float *out, uint32_t rows_total,
+                               uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm, uint32_t ntm_max,
+                               int num_cu, void *workspace, hipStream_t st) {
+    if (rows_total == 0 || N == 0 || K == 0 || K % 256 || ntm_max == 0 || workspace == nullptr)
+        return hipErrorInvalidValue;
+    const uint32_t ntn = (N + GN - 1) / GN;
+    // 32-bit buffer offsets and unit counts
+    if (uint64_t(rows_total) * K >= (uint64_t(1) << 32) || wstride >= (uint64_t(1) << 32) ||
+        uint64_t(ntm_max) * ntn * (K / 256) >= (uint64_t(1) << 32))
+        return hipErrorInvalidValue;
+    GemmArgs a{};
+    a.W = static_cast<const uint8_t *>(W);
+    a.qs = act.qs;
+    a.d8 = act.d;
+    a.bsums = act.bsums;
+    a.M = rows_total;
+    a.N = N;
+    a.K = K;
+    a.nblk = K / 256;
+    a.row_bytes = a.nblk * unit_bytes(kQ4_K);
+    a.mt = mt;
+    a.ntm_dev = ntm;
+    a.wstride = wstride;
+    a.ntn = ntn;
+    a.out = out;
+    a.ws = static_cast<float *>(workspace);
+    a.skg = grouped_grid(ntm_max, N, K, num_cu);
+    hipError_t e = launch_gemm_t<kQ4_K, true>(a, dim3{a.skg, 1u, 1u}, st);
+    if (e != hipSuccess) return e;
+    // The split tiles are known on the device only: one fixup workgroup per
+    // possible tile (those past the count, or stored whole, exit at once).
+    k_gemm_fixup<true><<<dim3{ntm_max * ntn, 1u, 1u}, 256, 0, st>>>(a);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
@@ -736,7 +820,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
         bool split = false;
         for (uint32_t w = 1; w < G && !split; ++w) split = sk_begin(a.ntiles * a.nblk, G, w) % a.nblk != 0;
         if (!split) return hipSuccess;
-        k_gemm_fixup<<<dim3{a.ntiles, 1u, 1u}, 256, 0, st>>>(a);
+        k_gemm_fixup<false><<<dim3{a.ntiles, 1u, 1u}, 256, 0, st>>>(a);
         return hipGetLastError();
     }
     a.out = nsplit > 1 ? static_cast<float *>(workspace) : out;

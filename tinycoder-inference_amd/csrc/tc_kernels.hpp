@@ -15,6 +15,10 @@ hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols
                             void *buf, hipStream_t st, bool block_major = false);
 
 // Weight encoder: x[nunits][256] fp32 -> nunits units of `type`.
+// Q8_K block-major quantization of the gathered rows x[rows[s]], s < S.
+hipError_t launch_quant_act_rows(const float *x, const uint32_t *rows, uint32_t S, uint32_t cols, const ActLayout &L,
+                                 void *buf, hipStream_t st);
+
 hipError_t launch_encode(int type, const float *x, void *out, uint32_t nunits, hipStream_t st);
 
 // One mat-vec job: out[s][r] (row stride out_ld per token) = W[r] . x[s].
@@ -71,5 +75,31 @@ uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
 size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
                        int num_cu, void *workspace, hipStream_t st);
+
+// ---- MoE prefill over expert-sorted rows ----
+// Device-side router: pairs p = t*top_k + r (ids[p] in [0, E), others
+// skipped) sorted by expert; each expert's segment starts at a multiple of
+// `pad` rows and is cut into tiles of at most `tile` rows. pos[p] = the
+// pair's row (-1 for a skipped pair), row_tok[i] = the token of row i (~0 for
+// rows no pair lands on), mt = (row begin, row end, expert) per tile, *ntm =
+// the tile count. Sizes: moe_max_rows rows and moe_max_tiles tiles.
+uint32_t moe_max_tiles(uint32_t npairs, uint32_t n_experts, uint32_t tile);
+uint32_t moe_max_rows(uint32_t npairs, uint32_t n_experts, uint32_t pad);
+hipError_t launch_moe_route(const int32_t *ids, uint32_t npairs, uint32_t top_k, uint32_t n_experts, uint32_t pad,
+                            uint32_t tile, int32_t *pos, uint32_t *row_tok, uint32_t *mt, uint32_t *ntm,
+                            hipStream_t st);
+// h = silu(g) * u elementwise over nrows_max rows of ff values, written over g
+// (rows past the routed ones hold values nothing reads).
+hipError_t launch_moe_swiglu(float *g, const float *u, uint32_t nrows_max, uint32_t ff, hipStream_t st);
+// out[t] = sum over r in rank order of wts[t*top_k+r] * y[pos[t*top_k+r]]
+// (pairs with pos < 0 skipped), from 0.
+hipError_t launch_moe_combine_rows(const float *y, const int32_t *pos, const float *wts, float *out, uint32_t T,
+                                   uint32_t top_k, uint32_t H, hipStream_t st);
+// Q4_K GEMM over expert-sorted rows: out[i][n] = act row i . W[e(i)] row n,
+// for the token tiles of mt (count *ntm, at most ntm_max).
+size_t gemm_grouped_workspace_bytes(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu);
+hipError_t launch_gemm_grouped(const void *W, uint64_t wstride, const ActView &act, float *out, uint32_t rows_total,
+                               uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm, uint32_t ntm_max,
+                               int num_cu, void *workspace, hipStream_t st);
 
 }  // namespace tc

@@ -36,6 +36,20 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, 
     quant_q8k_block_wave(x + size_t(g) * 256, qs + size_t(o) * 256, d + o, bsums + size_t(o) * 16);
 }
 
+// The same with a row gather: output row s quantizes x row rows[s] (MoE
+// activations in expert-sorted order).
+__global__ __launch_bounds__(256) void k_quant_q8k_rows(const float *__restrict__ x, const uint32_t *__restrict__ rows,
+                                                        int8_t *__restrict__ qs, float *__restrict__ d,
+                                                        int16_t *__restrict__ bsums, uint32_t nblk_total,
+                                                        uint32_t nbk, uint32_t bm_S) {
+    const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= nblk_total) return;
+    const uint32_t s = g / nbk, j = g - s * nbk;
+    const uint32_t o = act_dst_block(g, nbk, bm_S);
+    const uint32_t r = rows[s] == ~0u ? 0u : rows[s];  // unrouted rows: any valid row (never stored)
+    quant_q8k_block_wave(x + (size_t(r) * nbk + j) * 256, qs + size_t(o) * 256, d + o, bsums + size_t(o) * 16);
+}
+
 // 32-wide rule used for Q8_0 weights (reference
 // src/cpp/core/SIMDMatMulVecAVX2.cpp:4296-4326): one wave per 8 blocks.
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int8_t *__restrict__ qs,
@@ -363,6 +377,16 @@ hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols
         const uint32_t nb = S * (cols / 256);
         k_quant_q8k<<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, nb, nbk, bm_S);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_act_rows(const float *x, const uint32_t *rows, uint32_t S, uint32_t cols, const ActLayout &L,
+                                 void *buf, hipStream_t st) {
+    const uint32_t nbk = cols / 256, nb = S * nbk;
+    char *b = static_cast<char *>(buf);
+    k_quant_q8k_rows<<<(nb + 3) / 4, 256, 0, st>>>(x, rows, reinterpret_cast<int8_t *>(b + L.qs_off),
+                                                   reinterpret_cast<float *>(b + L.d_off),
+                                                   reinterpret_cast<int16_t *>(b + L.bs_off), nb, nbk, S);
     return hipGetLastError();
 }
 

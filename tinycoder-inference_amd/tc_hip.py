@@ -45,6 +45,7 @@ SIGNATURES = {
     "tc_probe_sink_bytes": (ctypes.c_size_t, []),
     "tc_probe_mfma_i8": (_I, [_U32, _U32, _P, _P]),
     "tc_probe_read": (_I, [_P, ctypes.c_size_t, _U32, _P, _P]),
+    "tc_moe_set_gemm_min_tokens": (None, [_U32]),
     "tc_gguf_open": (_P, [ctypes.c_char_p]),
     "tc_gguf_open_metadata": (_P, [ctypes.c_char_p]),
     "tc_gguf_close": (None, [_P]),
