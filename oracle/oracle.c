@@ -24,6 +24,7 @@ uint32_t oc_type_size(int type) {
      * unit_tests/DequantizeTest.cpp:570 (Q4_K=144, IQ3_XXS=98). */
     switch (type) {
         case OC_TYPE_Q8_0: return 34;
+        case OC_TYPE_Q3_K: return 110;
         case OC_TYPE_Q4_K: return 144;
         case OC_TYPE_Q5_K: return 176;
         case OC_TYPE_Q6_K: return 210;
@@ -206,6 +207,30 @@ static int q5k_value(const uint8_t *blk, int g, int l) {
     return ((qs[32 * c + l] >> (4 * h)) & 0xF) | (((qh[l] >> (2 * c + h)) & 1) << 4);
 }
 
+/* Q3_K (110 B: hmask[32] at 0, qs[64] at 32, 12 scale bytes at 96, d at
+ * 108): the 16 6-bit scales as unpacked by include/GGMLDequantize.hpp:612-630
+ * (kmask1/kmask2 on three little-endian words), returned minus 32. */
+static void q3k_scales(const uint8_t *blk, int sc[16]) {
+    uint32_t aux[4];
+    memcpy(aux, blk + 96, 12);
+    const uint32_t km1 = 0x03030303u, km2 = 0x0f0f0f0fu, tmp = aux[2];
+    aux[2] = ((aux[0] >> 4) & km2) | (((tmp >> 4) & km1) << 4);
+    aux[3] = ((aux[1] >> 4) & km2) | (((tmp >> 6) & km1) << 4);
+    aux[0] = (aux[0] & km2) | (((tmp >> 0) & km1) << 4);
+    aux[1] = (aux[1] & km2) | (((tmp >> 2) & km1) << 4);
+    const int8_t *b = (const int8_t *)aux;
+    for (int i = 0; i < 16; ++i) sc[i] = b[i] - 32;
+}
+
+/* Q3_K signed value (-4..3) of element e = 128n + 32j + l: 2 bits of
+ * qs[32n + l] at 2j, minus 4 unless bit 4n+j of hmask[l] is set
+ * (include/GGMLDequantize.hpp:632-648); its scale is sc[e/16]. */
+static int q3k_value(const uint8_t *blk, int e) {
+    const int n = e >> 7, j = (e >> 5) & 3, l = e & 31;
+    const int q2 = (blk[32 + 32 * n + l] >> (2 * j)) & 3;
+    return q2 - (((blk[l] >> (4 * n + j)) & 1) ? 0 : 4);
+}
+
 static int q6k_raw(const uint8_t *blk, int e) {
     const int half = e >> 7, r = e & 127, quad = r >> 5, l = r & 31;
     const uint8_t *ql = blk + 64 * half;
@@ -268,6 +293,13 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
                 const float d1 = d * (float)sc, m1 = dmin * (float)m;
                 for (int l = 0; l < 32; ++l) y[32 * g + l] = d1 * (float)q5k_value(blk, g, l) - m1;
             }
+        } else if (type == OC_TYPE_Q3_K) {
+            /* include/GGMLDequantize.hpp:612-648: dl = d * (sc - 32) per 16,
+             * y = dl * q with q = q2 - (hmask bit ? 0 : 4). */
+            const float d = h2f_at(blk + 108);
+            int sc[16];
+            q3k_scales(blk, sc);
+            for (int e = 0; e < 256; ++e) y[e] = (d * (float)sc[e >> 4]) * (float)q3k_value(blk, e);
         } else if (type == OC_TYPE_Q6_K) {
             /* include/GGMLDequantize.hpp:503-527: y = d * sc * q, evaluated
              * left to right as (d*sc)*q with q = raw-32. */
@@ -330,6 +362,22 @@ static int32_t q6k_isum(const uint8_t *blk, const int8_t *xq) {
         int32_t s = 0;
         for (int i = 0; i < 16; ++i) s += (q6k_raw(blk, 16 * g + i) - 32) * xq[16 * g + i];
         tot += (int32_t)sc[g] * s;
+    }
+    return tot;
+}
+
+/* Q3_K block integer sum_g (sc[g]-32) * sum_16 q * q8 with q in -4..3: the
+ * exact integer behind matMulVecBatchQ3K_Q8K_AVX2's blockDot
+ * (src/cpp/core/SIMDMatMulVecAVX2.cpp:3480-3520: w' = q + 4 in the dots and
+ * -4 * sum (sc-32) * bsum folded back). */
+static int32_t q3k_isum(const uint8_t *blk, const int8_t *xq) {
+    int sc[16];
+    q3k_scales(blk, sc);
+    int32_t tot = 0;
+    for (int g = 0; g < 16; ++g) {
+        int32_t s = 0;
+        for (int i = 0; i < 16; ++i) s += q3k_value(blk, 16 * g + i) * xq[16 * g + i];
+        tot += sc[g] * s;
     }
     return tot;
 }
@@ -405,6 +453,7 @@ int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                 switch (type) {
                     case OC_TYPE_Q4_K: q4k_subsums(blk, xq, o); break;
                     case OC_TYPE_Q5_K: q5k_subsums(blk, xq, o); break;
+                    case OC_TYPE_Q3_K: o[0] = q3k_isum(blk, xq); break;
                     case OC_TYPE_Q6_K: o[0] = q6k_isum(blk, xq); break;
                     case OC_TYPE_IQ3_XXS: o[0] = iq3_isum(blk, xq); break;
                     default: o[0] = q80_isum(blk, xq); break;
@@ -559,6 +608,51 @@ static float row_q6k(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff
     return hsum8(racc);
 }
 
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:3220-3560 (matMulVecBatchQ3K_Q8K_AVX2):
+ * the same 8-lane structure as the Q6_K kernel. Per block, lane j starts at
+ * c0 * (s[2j]*bs[2j] + s[2j+1]*bs[2j+1]) with c0 = (-4*dq)*d8 and s = sc-32;
+ * per chunk, lane j adds fma(dq*d8, sumi_j) where sumi_j sums, over the 4
+ * sub-blocks idx of the chunk, s[2idx + (j>=4)] * sum_4 w'*q8 over elements
+ * 32idx + 4j.. (w' = q + 4, 0..7); lanes add into the row accumulator, then
+ * the 8 lanes are reduced as ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)). */
+static float row_q3k(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff,
+                     size_t boff) {
+    float racc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 110;
+        const float dq = h2f_at(blk + 108);
+        int sc[16];
+        q3k_scales(blk, sc);
+        const float d8 = a->d[doff + b];
+        const int8_t *xq = a->qs + qoff + (size_t)b * 256;
+        const int16_t *bsums = a->bsums + boff + (size_t)b * 16;
+        const float c0 = -4.0f * dq * d8;
+        const float dd8 = dq * d8;
+        float acc[8];
+        for (int j = 0; j < 8; ++j) {
+            const int32_t bp = (int32_t)sc[2 * j] * bsums[2 * j] + (int32_t)sc[2 * j + 1] * bsums[2 * j + 1];
+            acc[j] = c0 * (float)bp;
+        }
+        for (int chunk = 0; chunk < 2; ++chunk) {
+            int32_t sumi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int sub = 0; sub < 4; ++sub) {
+                const int idx = chunk * 4 + sub;
+                for (int j = 0; j < 8; ++j) {
+                    int32_t p = 0;
+                    for (int k = 0; k < 4; ++k) {
+                        const int e = 32 * idx + 4 * j + k;
+                        p += (q3k_value(blk, e) + 4) * xq[e];
+                    }
+                    sumi[j] += (int32_t)sc[2 * idx + (j >= 4)] * p;
+                }
+            }
+            for (int j = 0; j < 8; ++j) acc[j] = fmaf(dd8, (float)sumi[j], acc[j]);
+        }
+        for (int j = 0; j < 8; ++j) racc[j] = racc[j] + acc[j];
+    }
+    return hsum8(racc);
+}
+
 /* include/GGMLDequantize.hpp:2231-2269 (matMulVecBatchQ8K) with the IQ3_XXS
  * block dot :2064-2097 and the row scale 0.25 (:2148-2159). */
 static float row_iq3(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff) {
@@ -588,6 +682,7 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t r
             switch (type) {
                 case OC_TYPE_Q4_K: v = row_q4k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_Q5_K: v = row_q5k(rp, nb, &a, qoff, doff, boff); break;
+                case OC_TYPE_Q3_K: v = row_q3k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_Q6_K: v = row_q6k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_IQ3_XXS: v = row_iq3(rp, nb, &a, qoff, doff); break;
                 default: v = row_q80(rp, nb, &a, qoff, doff); break;
@@ -721,6 +816,57 @@ void oc_encode_q5k_block(const float *x, uint8_t *out) {
     }
 }
 
+/* Q3_K weight encoder (the reference ships none; this build defines it).
+ * Per 16-group: signed first-abs-max m, group scale m/-4 (m maps to -4).
+ * Block: signed first-abs-max of the group scales M, iscale = -32/M, 6-bit
+ * signed scales s = clamp(rne(iscale*scale), -32, 31) stored as s+32, d =
+ * 1/iscale as fp16 (RNE). Weights q = clamp(rne(x / (d_fp16*s)), -4, 3),
+ * stored as q+4: 2 low bits in qs, the third bit in hmask, laid out as the
+ * decoder include/GGMLDequantize.hpp:612-648 reads them. */
+void oc_encode_q3k_block(const float *x, uint8_t *out) {
+    float gs[16];
+    for (int g = 0; g < 16; ++g) {
+        float amax;
+        const float m = first_abs_max(x + 16 * g, 16, &amax);
+        gs[g] = amax == 0.0f ? 0.0f : m / -4.0f;
+    }
+    float amaxs;
+    const float M = first_abs_max(gs, 16, &amaxs);
+    memset(out, 0, 110);
+    int s6[16], L[256];
+    if (amaxs == 0.0f) {
+        for (int g = 0; g < 16; ++g) s6[g] = 32;
+        for (int e = 0; e < 256; ++e) L[e] = 4;
+    } else {
+        const float iscale = -32.0f / M;
+        for (int g = 0; g < 16; ++g) {
+            int v = (int)lrintf(iscale * gs[g]);
+            v = v < -32 ? -32 : (v > 31 ? 31 : v);
+            s6[g] = v + 32;
+        }
+        const uint16_t hd = f2h_rne(1.0f / iscale);
+        memcpy(out + 108, &hd, 2);
+        const float dh = oc_half_to_float(hd);
+        for (int e = 0; e < 256; ++e) {
+            const float dg = dh * (float)(s6[e >> 4] - 32);
+            int q = dg != 0.0f ? (int)lrintf(x[e] / dg) : 0;
+            q = q < -4 ? -4 : (q > 3 ? 3 : q);
+            L[e] = q + 4;
+        }
+    }
+    for (int i = 0; i < 4; ++i) {
+        out[96 + i] = (uint8_t)((s6[i] & 15) | ((s6[8 + i] & 15) << 4));
+        out[100 + i] = (uint8_t)((s6[4 + i] & 15) | ((s6[12 + i] & 15) << 4));
+        out[104 + i] = (uint8_t)((s6[i] >> 4) | ((s6[4 + i] >> 4) << 2) | ((s6[8 + i] >> 4) << 4) |
+                                 ((s6[12 + i] >> 4) << 6));
+    }
+    for (int e = 0; e < 256; ++e) {
+        const int n = e >> 7, j = (e >> 5) & 3, l = e & 31;
+        out[32 + 32 * n + l] |= (uint8_t)((L[e] & 3) << (2 * j));
+        out[l] |= (uint8_t)((L[e] >> 2) << (4 * n + j));
+    }
+}
+
 /* Q6_K weight encoder (the reference ships none; this build defines it).
  * Per 16-group: signed first-abs-max m, group scale m/-32. Block: signed
  * first-abs-max of the group scales M, iscale = -128/M, sc = min(127,
@@ -843,6 +989,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
             case OC_TYPE_Q8_0: oc_encode_q8_0_block(xb, o); break;
             case OC_TYPE_Q4_K: oc_encode_q4k_block(xb, o); break;
             case OC_TYPE_Q5_K: oc_encode_q5k_block(xb, o); break;
+            case OC_TYPE_Q3_K: oc_encode_q3k_block(xb, o); break;
             case OC_TYPE_Q6_K: oc_encode_q6k_block(xb, o); break;
             default: oc_encode_iq3xxs_block(xb, o); break;
         }

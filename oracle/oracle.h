@@ -18,11 +18,11 @@
  *   oc_dequant_row  pinned: golden vectors + closed forms on hand-built blocks.
  *   oc_block_isums  pinned: brute-force integer dot of dequantized integer
  *       weights x quantized activations (order-free integer identity).
- *   oc_matmul (Q8_0/Q4_K/Q5_K/Q6_K/IQ3_XXS)  pinned: bit-exact against
+ *   oc_matmul (Q8_0/Q3_K/Q4_K/Q5_K/Q6_K/IQ3_XXS)  pinned: bit-exact against
  *       golden outputs of the compiled reference AVX2 / scalar kernels.
  *   oc_encode_q4k_block  pinned: bit-exact against the compiled reference
  *       quantizeQ4KBlock (golden) + the reference's own round-trip test.
- *   oc_encode_q8_0_block / oc_encode_q5k_block / oc_encode_q6k_block /
+ *   oc_encode_q8_0_block / oc_encode_q3k_block / oc_encode_q5k_block / oc_encode_q6k_block /
  *   oc_encode_iq3xxs_block:
  *       the reference has no encoder for these formats (this build defines
  *       them); pinned by decode round-trip error bounds only.
@@ -40,6 +40,7 @@ extern "C" {
 
 enum {
     OC_TYPE_Q8_0 = 8,
+    OC_TYPE_Q3_K = 11,
     OC_TYPE_Q4_K = 12,
     OC_TYPE_Q5_K = 13,
     OC_TYPE_Q6_K = 14,
@@ -76,6 +77,7 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S,
 /* Weight encoders. */
 void oc_encode_q4k_block(const float *x, uint8_t *out);
 void oc_encode_q8_0_block(const float *x, uint8_t *out);
+void oc_encode_q3k_block(const float *x, uint8_t *out);
 void oc_encode_q5k_block(const float *x, uint8_t *out);
 void oc_encode_q6k_block(const float *x, uint8_t *out);
 void oc_encode_iq3xxs_block(const float *x, uint8_t *out);

@@ -70,6 +70,14 @@ def q5k_random_blocks(rng, nblk):
     return b.ravel()
 
 
+def q3k_random_blocks(rng, nblk):
+    """Random Q3_K bytes (every hmask, 2-bit and 6-bit scale pattern) with a
+    fixed normal fp16 d."""
+    b = rng.integers(0, 256, (nblk, 110), dtype=np.uint8)
+    b[:, 108:110] = np.frombuffer(np.float16(0.0027).tobytes(), np.uint8)
+    return b.ravel()
+
+
 def q80_random_blocks(rng, nblk):
     b = rng.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
     d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-10, -6, nblk)).astype(np.float16)
@@ -231,6 +239,21 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.Q5_K, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.Q5_K, w, X4, rows, cols)
+
+    # Q3_K, likewise: its dequant and matMulVecBatchQ3K_Q8K_AVX2
+    # (SIMDMatMulVecAVX2.cpp:3220) on random blocks and on this build's encoder
+    # output. Own generator.
+    r3 = np.random.default_rng(20261203)
+    g["deq_q3k_w"] = q3k_random_blocks(r3, 8)
+    g["deq_q3k_y"] = ref.dequant(O.Q3_K, g["deq_q3k_w"], 8, 256)
+    cases3 = {
+        "q3k_rand": q3k_random_blocks(r3, rows * nb),
+        "q3k_enc002": O.Oracle().encode(O.Q3_K, (r3.standard_normal((rows, cols)) * 0.02).astype(np.float32)),
+    }
+    for name, w in cases3.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.Q3_K, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.Q3_K, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")

@@ -104,7 +104,7 @@ def test_quantize_q8_0_act_pinned_by_reference_probe(oracle, golden):
 
 # ---- block decoders ---------------------------------------------------------------
 
-@pytest.mark.parametrize("name,qt", [("q4k", O.Q4_K), ("q5k", O.Q5_K), ("q6k", O.Q6_K), ("iq3", O.IQ3_XXS),
+@pytest.mark.parametrize("name,qt", [("q3k", O.Q3_K), ("q4k", O.Q4_K), ("q5k", O.Q5_K), ("q6k", O.Q6_K), ("iq3", O.IQ3_XXS),
                                      ("q80", O.Q8_0)])
 def test_dequant_matches_reference(oracle, golden, name, qt):
     w = golden[f"deq_{name}_w"]
@@ -160,7 +160,7 @@ def test_iq3_dequant_closed_form(oracle):
 
 # ---- per-block integer dots: brute-force identity ------------------------------------
 
-@pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS])
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS])
 def test_block_isums_identity(oracle, qt):
     """sum over blocks of the integer sums, scaled per block by the float block
     scales, reproduces dequant(W) . (d8 * xq) in exact rational arithmetic."""
@@ -177,6 +177,9 @@ def test_block_isums_identity(oracle, qt):
         w = gen(rng, rows * cols // 256)
     elif qt == O.Q6_K:
         from gen_golden import q6k_random_blocks as gen
+        w = gen(rng, rows * cols // 256)
+    elif qt == O.Q3_K:
+        from gen_golden import q3k_random_blocks as gen
         w = gen(rng, rows * cols // 256)
     else:
         from gen_golden import iq3_random_blocks as gen
@@ -215,14 +218,15 @@ def test_block_isums_identity(oracle, qt):
         expect = (q5 * qs.reshape(1, -1, 256)).reshape(rows, -1, 8, 32).sum(3)
         assert np.array_equal(expect, isums)
     else:
-        # Q6_K / IQ3_XXS: dequant = c_block * (per-group integer scale * int weight),
+        # Q3_K / Q6_K / IQ3_XXS: dequant = c_block * (per-group integer scale * int weight),
         # so the integer sum equals sum(deq * xq) / c_block exactly (powers of two
         # or exact small-integer products in double).
         qs, d8, _ = oracle.quantize_q8k(x[0])
         xq = qs.astype(np.float64).reshape(1, -1, 256)
-        if qt == O.Q6_K:
-            wb = w.reshape(rows, cols // 256, 210)
-            c = wb[:, :, 208:210].copy().view(np.float16).astype(np.float64)[:, :, 0]
+        if qt in (O.Q3_K, O.Q6_K):
+            tb, do = (110, 108) if qt == O.Q3_K else (210, 208)
+            wb = w.reshape(rows, cols // 256, tb)
+            c = wb[:, :, do:do + 2].copy().view(np.float16).astype(np.float64)[:, :, 0]
             lhs = (deq.reshape(rows, -1, 256) * xq).sum(2) / c
         else:
             wb = w.reshape(rows, cols // 256, 98)
@@ -235,7 +239,7 @@ def test_block_isums_identity(oracle, qt):
 # ---- mat-vec kernels -----------------------------------------------------------------
 
 MM = [("q4k_rand", O.Q4_K), ("q4k_enc1", O.Q4_K), ("q4k_enc002", O.Q4_K), ("q5k_rand", O.Q5_K),
-      ("q5k_enc1", O.Q5_K), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
+      ("q5k_enc1", O.Q5_K), ("q3k_rand", O.Q3_K), ("q3k_enc002", O.Q3_K), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
 
 
 @pytest.mark.parametrize("name,qt", MM)
@@ -253,7 +257,7 @@ def test_matmul_q80_cols96(oracle, golden):
     assert (bits(got) == bits(golden["mm_q80c96_y"])).all()
 
 
-@pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS])
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS])
 def test_matmul_close_to_float_dot(oracle, qt):
     """Independent of the reference: the quantized mat-vec approximates the
     float product of the dequantized weights with x (activation quantization
@@ -310,9 +314,10 @@ def test_q4k_encoder_reference_roundtrip_thresholds(oracle):
     assert rel.mean() < 0.09
 
 
-@pytest.mark.parametrize("qt,bound", [(O.Q8_0, 0.01), (O.Q5_K, 0.08), (O.Q6_K, 0.04), (O.IQ3_XXS, 0.25)])
+@pytest.mark.parametrize("qt,bound", [(O.Q8_0, 0.01), (O.Q3_K, 0.2), (O.Q5_K, 0.08), (O.Q6_K, 0.04),
+                                      (O.IQ3_XXS, 0.25)])
 def test_own_encoders_roundtrip(oracle, qt, bound):
-    """This build's Q8_0 / Q5_K / Q6_K / IQ3_XXS encoders (the reference has none):
+    """This build's Q8_0 / Q3_K / Q5_K / Q6_K / IQ3_XXS encoders (the reference has none):
     N(0, 0.02) rows round-trip within the format's expected relative RMS."""
     rng = np.random.default_rng(9)
     x = (rng.standard_normal((16, 1024)) * 0.02).astype(np.float32)
