@@ -196,7 +196,7 @@ def roof_probes(torch, tc, tc_hip, dev):
 
 def other_decode_bench(torch, tc, tc_hip, dev, reps):
     """BASELINE configs #1 and #3 (batch-1 decode mat-vecs of other formats), and
-    Q5_K at the 7B FFN shape:
+    Q5_K and Q3_K at the 7B FFN shape:
     weights N(0,0.02) through the GPU encoders, rotating copies so that every
     working set exceeds the 256 MB Infinity Cache."""
     gen = torch.Generator(device=dev).manual_seed(11)
@@ -206,7 +206,9 @@ def other_decode_bench(torch, tc, tc_hip, dev, reps):
              ("cfg3 Q6_K down 3584x18944", tc_hip.Q6_K, 3584, 18944, False, 6),
              ("cfg3 IQ3_XXS gate/up pair 18944x3584 (SwiGLU)", tc_hip.IQ3_XXS, 18944, 3584, True, 6),
              ("Q5_K gate/up pair 18944x3584 (SwiGLU; format beyond the BASELINE configs)", tc_hip.Q5_K, 18944,
-              3584, True, 6)]
+              3584, True, 6),
+             ("Q3_K gate/up pair 18944x3584 (SwiGLU; format beyond the BASELINE configs)", tc_hip.Q3_K, 18944,
+              3584, True, 8)]
     res = []
     for name, qt, rows, cols, dual, ncopy in cases:
         mats = 2 if dual else 1

@@ -63,7 +63,7 @@ struct LaunchArgs {
     uint32_t off_d, off_b, off_g, off_p;
 };
 
-__host__ __device__ constexpr bool uses_bsums(int type) { return type == kQ4_K || type == kQ5_K || type == kQ6_K; }
+__host__ __device__ constexpr bool uses_bsums(int type) { return type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ6_K; }
 // Passes of weight loads each lane keeps in flight (register ring), sized so
 // that the kernel stays within the 256 VGPRs of an 8-wave-per-CU launch.
 __host__ __device__ constexpr int ring_depth(int type, int S) {
@@ -983,6 +983,67 @@ struct TDot<kQ5_K, S> {
     }
 };
 
+// Q3_K, one unit (110 B, 2-byte aligned in LDS) per lane: w' = q + 4 (0..7)
+// from 2 bits of qs (at 2j) and bit 4n+j of hmask, one dword of each per 4
+// weights; isum = sum_g (sc_g - 32) * (sum_16 w'*x - 4*bsum_g) exactly (the
+// reference folds the -4 through the bsums the same way,
+// SIMDMatMulVecAVX2.cpp:3480-3520); value = (d*d8) * isum.
+template <int S>
+struct TDot<kQ3_K, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        const u32x4 h0 = lds128(u), h1 = lds128(u + 16);
+        const uint32_t hm[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        // 12 scale bytes, then d (bytes 108-109 of the unit) in the low half of .w
+        const u32x4 sv = lds128(u + 96);
+        const uint32_t km1 = 0x03030303u, km2 = 0x0F0F0F0Fu, tmp = sv.z;
+        const uint32_t scw[4] = {(sv.x & km2) | ((tmp & km1) << 4), (sv.y & km2) | (((tmp >> 2) & km1) << 4),
+                                 ((sv.x >> 4) & km2) | (((tmp >> 4) & km1) << 4),
+                                 ((sv.y >> 4) & km2) | (((tmp >> 6) & km1) << 4)};
+        const float d = h2f(sv.w & 0xFFFFu);
+        int tot[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) tot[s] = 0;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const u32x4 qa = lds128(u + 32 + 32 * n), qb = lds128(u + 48 + 32 * n);
+            const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int sb = 4 * n + j;  // sub-block of 32
+                uint32_t w[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    w[k] = ((q[k] >> (2 * j)) & km1) | (((hm[k] >> (4 * n + j)) & 0x01010101u) << 2);
+                const int sc0 = int(byte_of(scw[(2 * sb) >> 2], (2 * sb) & 3)) - 32;
+                const int sc1 = int(byte_of(scw[(2 * sb + 1) >> 2], (2 * sb + 1) & 3)) - 32;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const unsigned char *xr = xr0 + s * xtok;
+                    const u32x4 x0 = lds128(xr + 32 * sb), x1 = lds128(xr + 32 * sb + 16);
+                    int p0 = sdot4(int(w[0]), int(x0.x), 0);
+                    p0 = sdot4(int(w[1]), int(x0.y), p0);
+                    p0 = sdot4(int(w[2]), int(x0.z), p0);
+                    p0 = sdot4(int(w[3]), int(x0.w), p0);
+                    int p1 = sdot4(int(w[4]), int(x1.x), 0);
+                    p1 = sdot4(int(w[5]), int(x1.y), p1);
+                    p1 = sdot4(int(w[6]), int(x1.z), p1);
+                    p1 = sdot4(int(w[7]), int(x1.w), p1);
+                    const uint32_t bsp = *reinterpret_cast<const uint32_t *>(xr + XB_BS + 4 * sb);
+                    const int b0 = int(int16_t(bsp & 0xFFFFu)), b1 = int(int16_t(bsp >> 16));
+                    tot[s] += sc0 * (p0 - 4 * b0) + sc1 * (p1 - 4 * b1);
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (dbg) dbg[s * dbg_tok] = tot[s];
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = (d * d8) * float(tot[s]);
+        }
+    }
+};
+
 // Q8_0, one unit (8 blocks of 34 B) per lane: value = sum_blk (d_w*d8) * isum
 // (reference SIMDMatMulVecAVX2.cpp:4339-4366).
 template <int S>
@@ -1509,7 +1570,7 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     return o;
 }
 
-bool tiled_type(int type) { return type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -1570,10 +1631,10 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
         if (fit == 0) return hipErrorInvalidValue;
         rpw = std::min(rpw, fit);
-        // Q6_K / IQ3_XXS rows are not 16-byte multiples: 8-row groups keep
-        // every workgroup's first row 16-byte aligned (8*210 and 8*98 bytes
-        // per 256 columns are multiples of 16).
-        if ((type == kQ6_K || type == kIQ3_XXS) && rpw < g.rows) {
+        // Q3_K / Q6_K / IQ3_XXS rows are not 16-byte multiples: 8-row groups
+        // keep every workgroup's first row 16-byte aligned (8*110, 8*210 and
+        // 8*98 bytes per 256 columns are multiples of 16).
+        if ((type == kQ3_K || type == kQ6_K || type == kIQ3_XXS) && rpw < g.rows) {
             rpw = (rpw + 7) / 8 * 8;
             if (rpw > fit) rpw = fit / 8 * 8;
             if (rpw == 0) return hipErrorInvalidValue;
@@ -1589,6 +1650,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
     switch (type) {
         case kQ4_K: return launch_tiled<kQ4_K, C>(S, a, wg, lds, st);
         case kQ5_K: return launch_tiled<kQ5_K, C>(S, a, wg, lds, st);
+        case kQ3_K: return launch_tiled<kQ3_K, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:

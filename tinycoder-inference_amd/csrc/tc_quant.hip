@@ -237,6 +237,58 @@ __device__ void enc_q8_0(const float *x, uint8_t *out) {
     }
 }
 
+// Q3_K (this build's encoder; the reference ships none): per-16 group scale
+// m/-4 from the signed first-abs-max, block iscale = -32/M over the group
+// scales, 6-bit signed scales (stored +32), fp16 (RNE) d = 1/iscale, q =
+// clamp(rne(x/(d*s)), -4, 3) stored as q+4 (2 bits in qs, the third in
+// hmask), packed as the reference decoder reads them
+// (include/GGMLDequantize.hpp:612-648).
+__device__ void enc_q3k(const float *x, uint8_t *out) {
+    float gs[16];
+    for (int g = 0; g < 16; ++g) {
+        float amax;
+        const float m = first_abs_max(x + 16 * g, 16, &amax);
+        gs[g] = amax == 0.0f ? 0.0f : __fdiv_rn(m, -4.0f);
+    }
+    float amaxs;
+    const float M = first_abs_max(gs, 16, &amaxs);
+    for (int i = 0; i < 110; ++i) out[i] = 0;
+    int s6[16];
+    uint8_t L[256];
+    if (amaxs == 0.0f) {
+        for (int g = 0; g < 16; ++g) s6[g] = 32;
+        for (int e = 0; e < 256; ++e) L[e] = 4;
+    } else {
+        const float iscale = __fdiv_rn(-32.0f, M);
+        for (int g = 0; g < 16; ++g) {
+            int v = int(rintf(iscale * gs[g]));
+            v = v < -32 ? -32 : (v > 31 ? 31 : v);
+            s6[g] = v + 32;
+        }
+        const uint16_t hd = f2h_rne(__fdiv_rn(1.0f, iscale));
+        out[108] = uint8_t(hd);
+        out[109] = uint8_t(hd >> 8);
+        const float dh = h2f(hd);
+        for (int e = 0; e < 256; ++e) {
+            const float dg = dh * float(s6[e >> 4] - 32);
+            int q = dg != 0.0f ? int(rintf(__fdiv_rn(x[e], dg))) : 0;
+            q = q < -4 ? -4 : (q > 3 ? 3 : q);
+            L[e] = uint8_t(q + 4);
+        }
+    }
+    for (int i = 0; i < 4; ++i) {
+        out[96 + i] = uint8_t((s6[i] & 15) | ((s6[8 + i] & 15) << 4));
+        out[100 + i] = uint8_t((s6[4 + i] & 15) | ((s6[12 + i] & 15) << 4));
+        out[104 + i] =
+            uint8_t((s6[i] >> 4) | ((s6[4 + i] >> 4) << 2) | ((s6[8 + i] >> 4) << 4) | ((s6[12 + i] >> 4) << 6));
+    }
+    for (int e = 0; e < 256; ++e) {
+        const int n = e >> 7, j = (e >> 5) & 3, l = e & 31;
+        out[32 + 32 * n + l] |= uint8_t((L[e] & 3) << (2 * j));
+        out[l] |= uint8_t((L[e] >> 2) << (4 * n + j));
+    }
+}
+
 // Q6_K (this build's encoder; the reference ships none): per-16 group scale
 // m/-32 from the signed first-abs-max, block iscale = -128/M over the group
 // scales, int8 sub-scales, fp16 (RNE) d = 1/iscale, q = clamp(rne(x/(d*sc)),
@@ -356,6 +408,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
     switch (type) {
         case kQ4_K: enc_q4k(xu, o); break;
         case kQ8_0: enc_q8_0(xu, o); break;
+        case kQ3_K: enc_q3k(xu, o); break;
         case kQ5_K: enc_q5k(xu, o); break;
         case kQ6_K: enc_q6k(xu, o); break;
         default: enc_iq3xxs(xu, o); break;
