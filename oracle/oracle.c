@@ -15,6 +15,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+static const uint32_t k_iq3s_grid[512] = {
+#include "iq3s_grid.inc"
+};
 static const uint32_t k_iq3xxs_grid[256] = {
 #include "iq3xxs_grid.inc"
 };
@@ -29,6 +32,7 @@ uint32_t oc_type_size(int type) {
         case OC_TYPE_Q5_K: return 176;
         case OC_TYPE_Q6_K: return 210;
         case OC_TYPE_IQ3_XXS: return 98;
+        case OC_TYPE_IQ3_S: return 110;
         default: return 0;
     }
 }
@@ -259,6 +263,21 @@ static int iq3_signed(const uint8_t *blk, int e, int *ls_out) {
     return (signs >> j) & 1u ? -mag : mag;
 }
 
+/* IQ3_S (110 B: d, qs[64] at 2, qh[8] at 66, signs[32] at 74, scales[4] at
+ * 106) signed integer weight of element e = 32ib + 8l + j: grid entry
+ * qs[8ib + 2l + (j>=4)] with bit 8 from qh[ib] bit 2l (+1 for j>=4), byte
+ * j&3, negated by bit j of signs[4ib + l]; per-32 scale 2*ls+1 with ls the
+ * nibble ib&1 of scales[ib/2] (include/GGMLDequantize.hpp:1164-1212,
+ * :2102-2145). */
+static int iq3s_signed(const uint8_t *blk, int e, int *ls_out) {
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7, hi = j >> 2;
+    const uint8_t *qs = blk + 2, *qh = blk + 66, *signs = blk + 74, *scales = blk + 106;
+    const int idx = qs[8 * ib + 2 * l + hi] | ((qh[ib] << ((hi ? 7 : 8) - 2 * l)) & 256);
+    const int mag = (int)((k_iq3s_grid[idx] >> (8 * (j & 3))) & 0xFFu);
+    *ls_out = (scales[ib >> 1] >> (4 * (ib & 1))) & 15;
+    return (signs[4 * ib + l] >> j) & 1 ? -mag : mag;
+}
+
 int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type);
     if (bs == 0 || n % bs) return -1;
@@ -308,6 +327,17 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
             for (int e = 0; e < 256; ++e) {
                 const int q = q6k_raw(blk, e) - 32;
                 y[e] = d * (float)sc[e >> 4] * (float)q;
+            }
+        } else if (type == OC_TYPE_IQ3_S) {
+            /* include/GGMLDequantize.hpp:1164-1212: y = (db * grid) * sign,
+             * db = d * (1 + 2*ls). */
+            const float d = h2f_at(blk);
+            for (int e = 0; e < 256; ++e) {
+                int ls;
+                const int v = iq3s_signed(blk, e, &ls);
+                const float db = d * (1.0f + 2.0f * (float)ls);
+                const float mag = (float)(v < 0 ? -v : v);
+                y[e] = db * mag * (v < 0 ? -1.0f : 1.0f);
             }
         } else {
             /* include/GGMLDequantize.hpp:1135-1161:
@@ -395,6 +425,19 @@ static int32_t iq3_isum(const uint8_t *blk, const int8_t *xq) {
     return bsum;
 }
 
+/* IQ3_S block integer bsum = sum_ib32 (2*ls+1) * sum_32 grid*sign*q8:
+ * include/GGMLDequantize.hpp:2102-2145 (dotProductIQ3_S_Q8K). */
+static int32_t iq3s_isum(const uint8_t *blk, const int8_t *xq) {
+    int32_t bsum = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+        int32_t sumi = 0;
+        int ls = 0;
+        for (int r = 0; r < 32; ++r) sumi += iq3s_signed(blk, 32 * ib + r, &ls) * xq[32 * ib + r];
+        bsum += sumi * (2 * ls + 1);
+    }
+    return bsum;
+}
+
 /* Q8_0 block sum_32 w*q8, the true integer product (the reference kernel's
  * sum, src/cpp/core/SIMDMatMulVecAVX2.cpp:4346-4356, equals it whenever no
  * weight byte is -128). */
@@ -456,6 +499,7 @@ int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                     case OC_TYPE_Q3_K: o[0] = q3k_isum(blk, xq); break;
                     case OC_TYPE_Q6_K: o[0] = q6k_isum(blk, xq); break;
                     case OC_TYPE_IQ3_XXS: o[0] = iq3_isum(blk, xq); break;
+                    case OC_TYPE_IQ3_S: o[0] = iq3s_isum(blk, xq); break;
                     default: o[0] = q80_isum(blk, xq); break;
                 }
             }
@@ -666,6 +710,20 @@ static float row_iq3(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff
     return 0.25f * sumf;
 }
 
+/* include/GGMLDequantize.hpp:2231-2269 (matMulVecBatchQ8K) with the IQ3_S
+ * block dot :2102-2145 (d = d_w * d8, d * bsum) and the row scale 1
+ * (:2148-2159). */
+static float row_iq3s(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff) {
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 110;
+        const float d = h2f_at(blk) * a->d[doff + b];
+        const int32_t bsum = iq3s_isum(blk, a->qs + qoff + (size_t)b * 256);
+        sumf += d * (float)bsum;
+    }
+    return 1.0f * sumf;
+}
+
 int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t rows,
               uint32_t cols, float *out) {
     if (!shape_ok(type, cols)) return -1;
@@ -685,6 +743,7 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t r
                 case OC_TYPE_Q3_K: v = row_q3k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_Q6_K: v = row_q6k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_IQ3_XXS: v = row_iq3(rp, nb, &a, qoff, doff); break;
+                case OC_TYPE_IQ3_S: v = row_iq3s(rp, nb, &a, qoff, doff); break;
                 default: v = row_q80(rp, nb, &a, qoff, doff); break;
             }
             out[(size_t)s * rows + r] = v;
@@ -925,6 +984,57 @@ void oc_encode_q6k_block(const float *x, uint8_t *out) {
  * implies the 8th by even parity). Magnitudes per 4: the grid entry with the
  * least sum of squared differences to |x|/db (first on ties), sums formed in
  * index order without FMA. */
+/* IQ3_S weight encoder (the reference ships none; this build defines it).
+ * Per 32: s = max|x|/15; d = max s / 31 (fp16 RNE); ls = clamp(rne((s/d -
+ * 1)/2), 0, 15), db = d*(1+2ls); per weight the sign bit (x < 0); per 4 the
+ * grid entry (of 512) nearest |x|/db in squared error (first wins), its
+ * bit 8 in qh, as the decoder include/GGMLDequantize.hpp:1164-1212 reads. */
+void oc_encode_iq3s_block(const float *x, uint8_t *out) {
+    float sc[8], smax = 0.0f;
+    for (int c = 0; c < 8; ++c) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fabsf(x[32 * c + i]) > amax ? fabsf(x[32 * c + i]) : amax;
+        sc[c] = amax / 15.0f;
+        smax = sc[c] > smax ? sc[c] : smax;
+    }
+    memset(out, 0, 110);
+    const uint16_t hd = f2h_rne(smax / 31.0f);
+    const float d = oc_half_to_float(hd);
+    if (d == 0.0f) return;
+    memcpy(out, &hd, 2);
+    uint8_t *qs = out + 2, *qh = out + 66, *signs = out + 74, *scales = out + 106;
+    for (int c = 0; c < 8; ++c) {
+        int ls = (int)lrintf((sc[c] / d - 1.0f) / 2.0f);
+        ls = ls < 0 ? 0 : (ls > 15 ? 15 : ls);
+        scales[c >> 1] |= (uint8_t)(ls << (4 * (c & 1)));
+        const float db = d * (1.0f + 2.0f * (float)ls);
+        for (int l = 0; l < 4; ++l) {
+            const float *xv = x + 32 * c + 8 * l;
+            for (int j = 0; j < 8; ++j)
+                if (xv[j] < 0.0f) signs[4 * c + l] |= (uint8_t)(1u << j);
+            for (int h = 0; h < 2; ++h) {
+                float t[4];
+                for (int j = 0; j < 4; ++j) t[j] = fabsf(xv[4 * h + j]) / db;
+                int best = 0;
+                float berr = 0.0f;
+                for (int gi = 0; gi < 512; ++gi) {
+                    float err = 0.0f;
+                    for (int j = 0; j < 4; ++j) {
+                        const float diff = (float)((k_iq3s_grid[gi] >> (8 * j)) & 0xFFu) - t[j];
+                        err = err + diff * diff;
+                    }
+                    if (gi == 0 || err < berr) {
+                        berr = err;
+                        best = gi;
+                    }
+                }
+                qs[8 * c + 2 * l + h] = (uint8_t)(best & 255);
+                qh[c] |= (uint8_t)((best >> 8) << (2 * l + h));
+            }
+        }
+    }
+}
+
 void oc_encode_iq3xxs_block(const float *x, uint8_t *out) {
     float sc[8], smax = 0.0f;
     for (int c = 0; c < 8; ++c) {
@@ -991,6 +1101,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
             case OC_TYPE_Q5_K: oc_encode_q5k_block(xb, o); break;
             case OC_TYPE_Q3_K: oc_encode_q3k_block(xb, o); break;
             case OC_TYPE_Q6_K: oc_encode_q6k_block(xb, o); break;
+            case OC_TYPE_IQ3_S: oc_encode_iq3s_block(xb, o); break;
             default: oc_encode_iq3xxs_block(xb, o); break;
         }
     }

@@ -54,6 +54,7 @@ void ref_dequant_block(int type, const uint8_t *blk, float *out) {
         case 13: GGMLDequantize::dequantizeQ5_KBlock(blk, out); break;  // include/GGMLDequantize.hpp:346
         case 14: GGMLDequantize::dequantizeQ6_KBlock(blk, out); break;
         case 18: GGMLDequantize::dequantizeIQ3_XXSBlock(blk, out); break;
+        case 21: GGMLDequantize::dequantizeIQ3_SBlock(blk, out); break;  // include/GGMLDequantize.hpp:1164
         default: break;
     }
 }
@@ -90,9 +91,17 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
         case 18:
             GGMLDequantize::matMulVecBatchQ8K(GGML_TYPE_IQ3_XXS, W, X, seqLen, rows, cols, out);
             return 0;
+        // IQ3_S: the same scalar fused Q8_K path (include/GGMLDequantize.hpp:2102 block dot)
+        case 21:
+            GGMLDequantize::matMulVecBatchQ8K(GGML_TYPE_IQ3_S, W, X, seqLen, rows, cols, out);
+            return 0;
         default: return -1;
     }
 }
+
+// The IQ3_S codebook (include/GGMLDequantize.hpp:815, 512 words): format
+// data, exported to write this build's table file.
+void ref_iq3s_grid(uint32_t *out) { std::memcpy(out, GGMLDequantize::IQ3S_GRID, 512 * sizeof(uint32_t)); }
 
 // ---- GGUF reader (include/GGUFLoader.hpp:48) ---------------------------------
 // A loader handle; load() or loadMetadata() per `metadata_only`. NULL on failure.

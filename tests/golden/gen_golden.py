@@ -9,6 +9,7 @@ fixture is what the CPU tests pin the C restatement (oracle/oracle.c) against,
 and what the GPU tests compare the HIP library against, on the GPU box where
 the reference does not exist.
 """
+import ctypes
 import hashlib
 import os
 import sys
@@ -75,6 +76,14 @@ def q3k_random_blocks(rng, nblk):
     fixed normal fp16 d."""
     b = rng.integers(0, 256, (nblk, 110), dtype=np.uint8)
     b[:, 108:110] = np.frombuffer(np.float16(0.0027).tobytes(), np.uint8)
+    return b.ravel()
+
+
+def iq3s_random_blocks(rng, nblk):
+    """Random IQ3_S bytes (every grid index, qh bit, sign and scale nibble)
+    with a fixed normal fp16 d."""
+    b = rng.integers(0, 256, (nblk, 110), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(np.float16(0.0009).tobytes(), np.uint8)
     return b.ravel()
 
 
@@ -254,6 +263,23 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.Q3_K, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.Q3_K, w, X4, rows, cols)
+
+    # IQ3_S, likewise (scalar fused Q8_K path, GGMLDequantize.hpp:2102), and
+    # the digest of the reference codebook the committed table must match.
+    ri = np.random.default_rng(20261204)
+    grid = np.zeros(512, np.uint32)
+    ref.lib.ref_iq3s_grid(ctypes.c_void_p(grid.ctypes.data))
+    g["iq3s_grid_sha256"] = np.frombuffer(hashlib.sha256(grid.tobytes()).digest(), np.uint8)
+    g["deq_iq3s_w"] = iq3s_random_blocks(ri, 8)
+    g["deq_iq3s_y"] = ref.dequant(O.IQ3_S, g["deq_iq3s_w"], 8, 256)
+    casesi = {
+        "iq3s_rand": iq3s_random_blocks(ri, rows * nb),
+        "iq3s_enc002": O.Oracle().encode(O.IQ3_S, (ri.standard_normal((rows, cols)) * 0.02).astype(np.float32)),
+    }
+    for name, w in casesi.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.IQ3_S, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.IQ3_S, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")
