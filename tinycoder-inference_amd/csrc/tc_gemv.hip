@@ -38,6 +38,9 @@ namespace {
 __constant__ uint32_t c_grid[256] = {
 #include "iq3xxs_grid.inc"
 };
+__constant__ uint32_t c_grid_s[512] = {
+#include "iq3s_grid.inc"
+};
 
 constexpr int NT = 512;
 constexpr int kUnitsPerPass = NT / 4;
@@ -1201,6 +1204,64 @@ struct TDot<kIQ3_XXS, S> {
     }
 };
 
+// IQ3_S, one unit (110 B, 2-byte aligned in LDS) per lane: per 32-run ib,
+// 8 grid indices (qs bytes with bit 8 from qh[ib]; codebook of 512 words in
+// LDS), 8 sign bits per 8 weights (applied bytewise as a two's-complement
+// negation; magnitudes are at most 15, so no byte carries), scale 2*ls+1 from
+// the nibble of scales[ib/2]; isum = sum_ib (2ls+1) * sum_32 w*x; value =
+// (d*d8) * isum (include/GGMLDequantize.hpp:2102-2145).
+template <int S>
+struct TDot<kIQ3_S, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               const uint32_t *grid, float *val, int32_t *dbg, size_t dbg_tok) {
+        const uint16_t *u16 = reinterpret_cast<const uint16_t *>(u);
+        const uint32_t scw = uint32_t(u16[53]) | (uint32_t(u16[54]) << 16);
+        int tot[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) tot[s] = 0;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            const uint32_t g0 = uint32_t(u16[1 + 4 * ib]) | (uint32_t(u16[2 + 4 * ib]) << 16);
+            const uint32_t g1 = uint32_t(u16[3 + 4 * ib]) | (uint32_t(u16[4 + 4 * ib]) << 16);
+            const uint32_t sw = uint32_t(u16[37 + 2 * ib]) | (uint32_t(u16[38 + 2 * ib]) << 16);
+            const uint32_t qhb = (uint32_t(u16[33 + ib / 2]) >> (8 * (ib & 1))) & 0xFFu;
+            uint32_t w[8];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t gw = l < 2 ? g0 : g1;
+                const uint32_t i1 = byte_of(gw, 2 * (l & 1)) | ((qhb << (8 - 2 * l)) & 256u);
+                const uint32_t i2 = byte_of(gw, 2 * (l & 1) + 1) | ((qhb << (7 - 2 * l)) & 256u);
+                const uint32_t sb = byte_of(sw, l);
+                const uint32_t m1 = spread_sign4(sb & 15u), m2 = spread_sign4(sb >> 4);
+                w[2 * l] = (grid[i1] ^ m1) + (m1 & 0x01010101u);
+                w[2 * l + 1] = (grid[i2] ^ m2) + (m2 & 0x01010101u);
+            }
+            const int mult = 2 * int((scw >> (4 * ib)) & 15u) + 1;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const unsigned char *xr = xr0 + s * xtok + 32 * ib;
+                const u32x4 x0 = lds128(xr), x1 = lds128(xr + 16);
+                int p = sdot4(int(w[0]), int(x0.x), 0);
+                p = sdot4(int(w[1]), int(x0.y), p);
+                p = sdot4(int(w[2]), int(x0.z), p);
+                p = sdot4(int(w[3]), int(x0.w), p);
+                p = sdot4(int(w[4]), int(x1.x), p);
+                p = sdot4(int(w[5]), int(x1.y), p);
+                p = sdot4(int(w[6]), int(x1.z), p);
+                p = sdot4(int(w[7]), int(x1.w), p);
+                tot[s] += mult * p;
+            }
+        }
+        const float d = h2f(u16[0]);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (dbg) dbg[s * dbg_tok] = tot[s];
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = (d * d8) * float(tot[s]);
+        }
+    }
+};
+
 template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
@@ -1364,6 +1425,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
             });
         }
     }
+    if constexpr (TYPE == kIQ3_S) {
+        uint32_t *sg = reinterpret_cast<uint32_t *>(smem + L.off_g);
+        for (uint32_t i = tid; i < 512; i += TNT) sg[i] = c_grid_s[i];
+    }
     TC_TRACE_PT(4);
     tstage_finish<TYPE, S, TNT>(jb, xrs, xp, xr);
     TC_TRACE_PT(5);
@@ -1403,7 +1468,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
                     float val[S];
                     // rank-group mode: tile of rank m against that rank's activations (S == 1)
                     const unsigned char *xb = xr + (RG ? size_t(m) * xtok : 0) + size_t(b) * XB;
-                    if constexpr (TYPE == kIQ3_XXS)
+                    if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S)
                         TDot<TYPE, S>::run(tile + lane * UB, xb, xtok,
                                            reinterpret_cast<const uint32_t *>(smem + L.off_g), val, dbg, dbg_tok);
                     else
@@ -1564,13 +1629,14 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     uint32_t o = S * (cols / 256) * XB;
     a->off_g = o;
     if (type == kIQ3_XXS) o += 16384;  // signed grid, 256 x 16 words
+    if (type == kIQ3_S) o += 2048;     // IQ3_S codebook, 512 words
     a->off_t = o;
     o += (C::NT / 64) * tile_slot_bytes(type);
     a->off_p = o;
     return o;
 }
 
-bool tiled_type(int type) { return type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -1631,10 +1697,10 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
         if (fit == 0) return hipErrorInvalidValue;
         rpw = std::min(rpw, fit);
-        // Q3_K / Q6_K / IQ3_XXS rows are not 16-byte multiples: 8-row groups
-        // keep every workgroup's first row 16-byte aligned (8*110, 8*210 and
-        // 8*98 bytes per 256 columns are multiples of 16).
-        if ((type == kQ3_K || type == kQ6_K || type == kIQ3_XXS) && rpw < g.rows) {
+        // Q3_K / Q6_K / IQ3_XXS / IQ3_S rows are not 16-byte multiples: 8-row
+        // groups keep every workgroup's first row 16-byte aligned (8*110,
+        // 8*210 and 8*98 bytes per 256 columns are multiples of 16).
+        if ((type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S) && rpw < g.rows) {
             rpw = (rpw + 7) / 8 * 8;
             if (rpw > fit) rpw = fit / 8 * 8;
             if (rpw == 0) return hipErrorInvalidValue;
@@ -1651,6 +1717,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         case kQ4_K: return launch_tiled<kQ4_K, C>(S, a, wg, lds, st);
         case kQ5_K: return launch_tiled<kQ5_K, C>(S, a, wg, lds, st);
         case kQ3_K: return launch_tiled<kQ3_K, C>(S, a, wg, lds, st);
+        case kIQ3_S: return launch_tiled<kIQ3_S, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:

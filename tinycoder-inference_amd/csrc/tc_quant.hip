@@ -12,6 +12,9 @@ namespace tc {
 __constant__ uint32_t c_iq3xxs_grid[256] = {
 #include "iq3xxs_grid.inc"
 };
+__constant__ uint32_t c_iq3s_grid[512] = {
+#include "iq3s_grid.inc"
+};
 
 // ---- activation quantizers ---------------------------------------------------
 
@@ -399,6 +402,59 @@ __device__ void enc_iq3xxs(const float *x, uint8_t *out) {
     }
 }
 
+// IQ3_S (this build's encoder; the reference ships none): per-32 s =
+// max|x|/15, d = max s / 31 (fp16 RNE), ls = clamp(rne((s/d - 1)/2), 0, 15),
+// db = d*(1+2ls); a sign bit per weight; per 4 the codebook entry (of 512)
+// nearest |x|/db in squared error (first wins), its bit 8 in qh, as the
+// reference decoder reads them (include/GGMLDequantize.hpp:1164-1212).
+__device__ void enc_iq3s(const float *x, uint8_t *out) {
+    float sc[8], smax = 0.0f;
+    for (int c = 0; c < 8; ++c) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fabsf(x[32 * c + i]) > amax ? fabsf(x[32 * c + i]) : amax;
+        sc[c] = __fdiv_rn(amax, 15.0f);
+        smax = sc[c] > smax ? sc[c] : smax;
+    }
+    for (int i = 0; i < 110; ++i) out[i] = 0;
+    const uint16_t hd = f2h_rne(__fdiv_rn(smax, 31.0f));
+    const float d = h2f(hd);
+    if (d == 0.0f) return;
+    out[0] = uint8_t(hd);
+    out[1] = uint8_t(hd >> 8);
+    uint8_t *qs = out + 2, *qh = out + 66, *signs = out + 74, *scales = out + 106;
+    for (int c = 0; c < 8; ++c) {
+        int ls = int(rintf(__fdiv_rn(__fdiv_rn(sc[c], d) - 1.0f, 2.0f)));
+        ls = ls < 0 ? 0 : (ls > 15 ? 15 : ls);
+        scales[c >> 1] |= uint8_t(ls << (4 * (c & 1)));
+        const float db = d * (1.0f + 2.0f * float(ls));
+        for (int l = 0; l < 4; ++l) {
+            const float *xv = x + 32 * c + 8 * l;
+            for (int j = 0; j < 8; ++j)
+                if (xv[j] < 0.0f) signs[4 * c + l] |= uint8_t(1u << j);
+            for (int h = 0; h < 2; ++h) {
+                float t[4];
+                for (int j = 0; j < 4; ++j) t[j] = __fdiv_rn(fabsf(xv[4 * h + j]), db);
+                int best = 0;
+                float berr = 0.0f;
+                for (int gi = 0; gi < 512; ++gi) {
+                    const uint32_t gv = c_iq3s_grid[gi];
+                    float err = 0.0f;
+                    for (int j = 0; j < 4; ++j) {
+                        const float diff = float((gv >> (8 * j)) & 0xFFu) - t[j];
+                        err = err + diff * diff;
+                    }
+                    if (gi == 0 || err < berr) {
+                        berr = err;
+                        best = gi;
+                    }
+                }
+                qs[8 * c + 2 * l + h] = uint8_t(best & 255);
+                qh[c] |= uint8_t((best >> 8) << (2 * l + h));
+            }
+        }
+    }
+}
+
 __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict__ x, uint8_t *__restrict__ out,
                                                uint32_t nunits) {
     const uint32_t u = blockIdx.x * 64 + threadIdx.x;
@@ -411,6 +467,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
         case kQ3_K: enc_q3k(xu, o); break;
         case kQ5_K: enc_q5k(xu, o); break;
         case kQ6_K: enc_q6k(xu, o); break;
+        case kIQ3_S: enc_iq3s(xu, o); break;
         default: enc_iq3xxs(xu, o); break;
     }
 }
