@@ -15,6 +15,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+static const uint64_t k_iq2s_grid[1024] = {
+#include "iq2s_grid.inc"
+};
 static const uint32_t k_iq3s_grid[512] = {
 #include "iq3s_grid.inc"
 };
@@ -33,6 +36,7 @@ uint32_t oc_type_size(int type) {
         case OC_TYPE_Q6_K: return 210;
         case OC_TYPE_IQ3_XXS: return 98;
         case OC_TYPE_IQ3_S: return 110;
+        case OC_TYPE_IQ2_S: return 82;
         default: return 0;
     }
 }
@@ -278,6 +282,20 @@ static int iq3s_signed(const uint8_t *blk, int e, int *ls_out) {
     return (signs[4 * ib + l] >> j) & 1 ? -mag : mag;
 }
 
+/* IQ2_S (82 B: d, qs[32] at 2, signs[32] at 34, qh[8] at 66, scales[8] at
+ * 74) signed integer weight of element e = 32ib + 8l + j: byte j of codebook
+ * entry qs[4ib + l] | ((qh[ib] << (8 - 2l)) & 0x300), negated by bit j of
+ * signs[4ib + l]; scale nibble (l >= 2) of scales[ib]
+ * (include/GGMLDequantize.hpp:1215-1242, :2028-2057). */
+static int iq2s_signed(const uint8_t *blk, int e, int *ls_out) {
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+    const uint8_t *qs = blk + 2, *signs = blk + 34, *qh = blk + 66, *scales = blk + 74;
+    const int idx = qs[4 * ib + l] | ((qh[ib] << (8 - 2 * l)) & 0x300);
+    const int mag = (int)((k_iq2s_grid[idx] >> (8 * j)) & 0xFFu);
+    *ls_out = (scales[ib] >> (4 * (l >> 1))) & 15;
+    return (signs[4 * ib + l] >> j) & 1 ? -mag : mag;
+}
+
 int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type);
     if (bs == 0 || n % bs) return -1;
@@ -327,6 +345,17 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
             for (int e = 0; e < 256; ++e) {
                 const int q = q6k_raw(blk, e) - 32;
                 y[e] = d * (float)sc[e >> 4] * (float)q;
+            }
+        } else if (type == OC_TYPE_IQ2_S) {
+            /* include/GGMLDequantize.hpp:1215-1242: db = (d * (0.5 + ls)) *
+             * 0.25, y = (db * grid) * sign. */
+            const float d = h2f_at(blk);
+            for (int e = 0; e < 256; ++e) {
+                int ls;
+                const int v = iq2s_signed(blk, e, &ls);
+                const float db = d * (0.5f + (float)ls) * 0.25f;
+                const float mag = (float)(v < 0 ? -v : v);
+                y[e] = db * mag * (v < 0 ? -1.0f : 1.0f);
             }
         } else if (type == OC_TYPE_IQ3_S) {
             /* include/GGMLDequantize.hpp:1164-1212: y = (db * grid) * sign,
@@ -438,6 +467,20 @@ static int32_t iq3s_isum(const uint8_t *blk, const int8_t *xq) {
     return bsum;
 }
 
+/* IQ2_S block integer bsum = sum_ib32 (1+2*ls1) * sum_16 + (1+2*ls2) * sum_16
+ * of grid*sign*q8: include/GGMLDequantize.hpp:2028-2057 (dotProductIQ2_S_Q8K). */
+static int32_t iq2s_isum(const uint8_t *blk, const int8_t *xq) {
+    int32_t bsum = 0;
+    for (int ib = 0; ib < 8; ++ib)
+        for (int h = 0; h < 2; ++h) {
+            int32_t sumi = 0;
+            int ls = 0;
+            for (int r = 0; r < 16; ++r) sumi += iq2s_signed(blk, 32 * ib + 16 * h + r, &ls) * xq[32 * ib + 16 * h + r];
+            bsum += (1 + 2 * ls) * sumi;
+        }
+    return bsum;
+}
+
 /* Q8_0 block sum_32 w*q8, the true integer product (the reference kernel's
  * sum, src/cpp/core/SIMDMatMulVecAVX2.cpp:4346-4356, equals it whenever no
  * weight byte is -128). */
@@ -500,6 +543,7 @@ int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                     case OC_TYPE_Q6_K: o[0] = q6k_isum(blk, xq); break;
                     case OC_TYPE_IQ3_XXS: o[0] = iq3_isum(blk, xq); break;
                     case OC_TYPE_IQ3_S: o[0] = iq3s_isum(blk, xq); break;
+                    case OC_TYPE_IQ2_S: o[0] = iq2s_isum(blk, xq); break;
                     default: o[0] = q80_isum(blk, xq); break;
                 }
             }
@@ -724,6 +768,19 @@ static float row_iq3s(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qof
     return 1.0f * sumf;
 }
 
+/* The IQ2_S row: the same loop with the block dot :2028-2057 and the row
+ * scale 0.125 (:2148-2159). */
+static float row_iq2s(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff) {
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 82;
+        const float d = h2f_at(blk) * a->d[doff + b];
+        const int32_t bsum = iq2s_isum(blk, a->qs + qoff + (size_t)b * 256);
+        sumf += d * (float)bsum;
+    }
+    return 0.125f * sumf;
+}
+
 int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t rows,
               uint32_t cols, float *out) {
     if (!shape_ok(type, cols)) return -1;
@@ -744,6 +801,7 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t r
                 case OC_TYPE_Q6_K: v = row_q6k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_IQ3_XXS: v = row_iq3(rp, nb, &a, qoff, doff); break;
                 case OC_TYPE_IQ3_S: v = row_iq3s(rp, nb, &a, qoff, doff); break;
+                case OC_TYPE_IQ2_S: v = row_iq2s(rp, nb, &a, qoff, doff); break;
                 default: v = row_q80(rp, nb, &a, qoff, doff); break;
             }
             out[(size_t)s * rows + r] = v;
@@ -1035,6 +1093,59 @@ void oc_encode_iq3s_block(const float *x, uint8_t *out) {
     }
 }
 
+/* IQ2_S weight encoder (the reference ships none; this build defines it).
+ * Per 16 (half of a 32-run): s = max|x|/43; d = 8 * max s / 31 (fp16 RNE);
+ * ls = clamp(rne((8s/d - 1)/2), 0, 15), db = (d*(0.5+ls))*0.25; a sign bit
+ * per weight; per 8 the codebook entry (of 1024) nearest |x|/db in squared
+ * error (first wins), index bits 8-9 in qh, as the decoder
+ * include/GGMLDequantize.hpp:1215-1242 reads them. */
+void oc_encode_iq2s_block(const float *x, uint8_t *out) {
+    float sc[16], smax = 0.0f;
+    for (int c = 0; c < 16; ++c) {
+        float amax = 0.0f;
+        for (int i = 0; i < 16; ++i) amax = fabsf(x[16 * c + i]) > amax ? fabsf(x[16 * c + i]) : amax;
+        sc[c] = amax / 43.0f;
+        smax = sc[c] > smax ? sc[c] : smax;
+    }
+    memset(out, 0, 82);
+    const uint16_t hd = f2h_rne(8.0f * smax / 31.0f);
+    const float d = oc_half_to_float(hd);
+    if (d == 0.0f) return;
+    memcpy(out, &hd, 2);
+    uint8_t *qs = out + 2, *signs = out + 34, *qh = out + 66, *scales = out + 74;
+    for (int c = 0; c < 16; ++c) {
+        const int ib = c >> 1, h = c & 1;
+        int ls = (int)lrintf((8.0f * sc[c] / d - 1.0f) / 2.0f);
+        ls = ls < 0 ? 0 : (ls > 15 ? 15 : ls);
+        scales[ib] |= (uint8_t)(ls << (4 * h));
+        const float db = d * (0.5f + (float)ls) * 0.25f;
+        for (int q = 0; q < 2; ++q) {
+            const int l = 2 * h + q;
+            const float *xv = x + 32 * ib + 8 * l;
+            float t[8];
+            for (int j = 0; j < 8; ++j) {
+                if (xv[j] < 0.0f) signs[4 * ib + l] |= (uint8_t)(1u << j);
+                t[j] = fabsf(xv[j]) / db;
+            }
+            int best = 0;
+            float berr = 0.0f;
+            for (int gi = 0; gi < 1024; ++gi) {
+                float err = 0.0f;
+                for (int j = 0; j < 8; ++j) {
+                    const float diff = (float)((k_iq2s_grid[gi] >> (8 * j)) & 0xFFu) - t[j];
+                    err = err + diff * diff;
+                }
+                if (gi == 0 || err < berr) {
+                    berr = err;
+                    best = gi;
+                }
+            }
+            qs[4 * ib + l] = (uint8_t)(best & 255);
+            qh[ib] |= (uint8_t)((best >> 8) << (2 * l));
+        }
+    }
+}
+
 void oc_encode_iq3xxs_block(const float *x, uint8_t *out) {
     float sc[8], smax = 0.0f;
     for (int c = 0; c < 8; ++c) {
@@ -1102,6 +1213,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
             case OC_TYPE_Q3_K: oc_encode_q3k_block(xb, o); break;
             case OC_TYPE_Q6_K: oc_encode_q6k_block(xb, o); break;
             case OC_TYPE_IQ3_S: oc_encode_iq3s_block(xb, o); break;
+            case OC_TYPE_IQ2_S: oc_encode_iq2s_block(xb, o); break;
             default: oc_encode_iq3xxs_block(xb, o); break;
         }
     }

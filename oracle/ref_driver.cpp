@@ -55,6 +55,7 @@ void ref_dequant_block(int type, const uint8_t *blk, float *out) {
         case 14: GGMLDequantize::dequantizeQ6_KBlock(blk, out); break;
         case 18: GGMLDequantize::dequantizeIQ3_XXSBlock(blk, out); break;
         case 21: GGMLDequantize::dequantizeIQ3_SBlock(blk, out); break;  // include/GGMLDequantize.hpp:1164
+        case 22: GGMLDequantize::dequantizeIQ2_SBlock(blk, out); break;  // include/GGMLDequantize.hpp:1215
         default: break;
     }
 }
@@ -95,6 +96,10 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
         case 21:
             GGMLDequantize::matMulVecBatchQ8K(GGML_TYPE_IQ3_S, W, X, seqLen, rows, cols, out);
             return 0;
+        // IQ2_S: the same path (block dot include/GGMLDequantize.hpp:2028, row scale 0.125)
+        case 22:
+            GGMLDequantize::matMulVecBatchQ8K(GGML_TYPE_IQ2_S, W, X, seqLen, rows, cols, out);
+            return 0;
         default: return -1;
     }
 }
@@ -102,6 +107,8 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
 // The IQ3_S codebook (include/GGMLDequantize.hpp:815, 512 words): format
 // data, exported to write this build's table file.
 void ref_iq3s_grid(uint32_t *out) { std::memcpy(out, GGMLDequantize::IQ3S_GRID, 512 * sizeof(uint32_t)); }
+// The IQ2_S codebook (include/GGMLDequantize.hpp:807, 1024 x 8 bytes), likewise.
+void ref_iq2s_grid(uint64_t *out) { std::memcpy(out, GGMLDequantize::IQ2S_GRID, 1024 * sizeof(uint64_t)); }
 
 // ---- GGUF reader (include/GGUFLoader.hpp:48) ---------------------------------
 // A loader handle; load() or loadMetadata() per `metadata_only`. NULL on failure.

@@ -87,6 +87,14 @@ def iq3s_random_blocks(rng, nblk):
     return b.ravel()
 
 
+def iq2s_random_blocks(rng, nblk):
+    """Random IQ2_S bytes (every grid index, qh bits, sign and scale nibble)
+    with a fixed normal fp16 d."""
+    b = rng.integers(0, 256, (nblk, 82), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(np.float16(0.0011).tobytes(), np.uint8)
+    return b.ravel()
+
+
 def q80_random_blocks(rng, nblk):
     b = rng.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
     d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-10, -6, nblk)).astype(np.float16)
@@ -280,6 +288,22 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.IQ3_S, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.IQ3_S, w, X4, rows, cols)
+
+    # IQ2_S, likewise (row scale 0.125), and the codebook digest.
+    r2 = np.random.default_rng(20261205)
+    grid2 = np.zeros(1024, np.uint64)
+    ref.lib.ref_iq2s_grid(ctypes.c_void_p(grid2.ctypes.data))
+    g["iq2s_grid_sha256"] = np.frombuffer(hashlib.sha256(grid2.tobytes()).digest(), np.uint8)
+    g["deq_iq2s_w"] = iq2s_random_blocks(r2, 8)
+    g["deq_iq2s_y"] = ref.dequant(O.IQ2_S, g["deq_iq2s_w"], 8, 256)
+    cases2 = {
+        "iq2s_rand": iq2s_random_blocks(r2, rows * nb),
+        "iq2s_enc002": O.Oracle().encode(O.IQ2_S, (r2.standard_normal((rows, cols)) * 0.02).astype(np.float32)),
+    }
+    for name, w in cases2.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.IQ2_S, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.IQ2_S, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")

@@ -105,7 +105,7 @@ def test_quantize_q8_0_act_pinned_by_reference_probe(oracle, golden):
 # ---- block decoders ---------------------------------------------------------------
 
 @pytest.mark.parametrize("name,qt", [("q3k", O.Q3_K), ("q4k", O.Q4_K), ("q5k", O.Q5_K), ("q6k", O.Q6_K), ("iq3", O.IQ3_XXS),
-                                     ("iq3s", O.IQ3_S),
+                                     ("iq3s", O.IQ3_S), ("iq2s", O.IQ2_S),
                                      ("q80", O.Q8_0)])
 def test_dequant_matches_reference(oracle, golden, name, qt):
     w = golden[f"deq_{name}_w"]
@@ -161,7 +161,7 @@ def test_iq3_dequant_closed_form(oracle):
 
 # ---- per-block integer dots: brute-force identity ------------------------------------
 
-@pytest.mark.parametrize("qt", [O.Q8_0, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S])
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S])
 def test_block_isums_identity(oracle, qt):
     """sum over blocks of the integer sums, scaled per block by the float block
     scales, reproduces dequant(W) . (d8 * xq) in exact rational arithmetic."""
@@ -184,6 +184,9 @@ def test_block_isums_identity(oracle, qt):
         w = gen(rng, rows * cols // 256)
     elif qt == O.IQ3_S:
         from gen_golden import iq3s_random_blocks as gen
+        w = gen(rng, rows * cols // 256)
+    elif qt == O.IQ2_S:
+        from gen_golden import iq2s_random_blocks as gen
         w = gen(rng, rows * cols // 256)
     else:
         from gen_golden import iq3_random_blocks as gen
@@ -237,6 +240,11 @@ def test_block_isums_identity(oracle, qt):
             c = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
             # db = d*(1+2ls)
             lhs = (deq.reshape(rows, -1, 256) * xq).sum(2) / c
+        elif qt == O.IQ2_S:
+            wb = w.reshape(rows, cols // 256, 82)
+            c = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+            # db = d*(0.5+ls)*0.25 = d*(1+2ls)/8
+            lhs = (deq.reshape(rows, -1, 256) * xq).sum(2) / c * 8.0
         else:
             wb = w.reshape(rows, cols // 256, 98)
             c = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
@@ -249,7 +257,7 @@ def test_block_isums_identity(oracle, qt):
 
 MM = [("q4k_rand", O.Q4_K), ("q4k_enc1", O.Q4_K), ("q4k_enc002", O.Q4_K), ("q5k_rand", O.Q5_K),
       ("q5k_enc1", O.Q5_K), ("q3k_rand", O.Q3_K), ("q3k_enc002", O.Q3_K), ("iq3s_rand", O.IQ3_S),
-      ("iq3s_enc002", O.IQ3_S), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
+      ("iq3s_enc002", O.IQ3_S), ("iq2s_rand", O.IQ2_S), ("iq2s_enc002", O.IQ2_S), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
 
 
 @pytest.mark.parametrize("name,qt", MM)
@@ -267,7 +275,7 @@ def test_matmul_q80_cols96(oracle, golden):
     assert (bits(got) == bits(golden["mm_q80c96_y"])).all()
 
 
-@pytest.mark.parametrize("qt", [O.Q8_0, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S])
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S])
 def test_matmul_close_to_float_dot(oracle, qt):
     """Independent of the reference: the quantized mat-vec approximates the
     float product of the dequantized weights with x (activation quantization
@@ -325,9 +333,9 @@ def test_q4k_encoder_reference_roundtrip_thresholds(oracle):
 
 
 @pytest.mark.parametrize("qt,bound", [(O.Q8_0, 0.01), (O.Q3_K, 0.2), (O.Q5_K, 0.08), (O.Q6_K, 0.04),
-                                      (O.IQ3_XXS, 0.25), (O.IQ3_S, 0.2)])
+                                      (O.IQ3_XXS, 0.25), (O.IQ3_S, 0.2), (O.IQ2_S, 0.35)])
 def test_own_encoders_roundtrip(oracle, qt, bound):
-    """This build's Q8_0 / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S encoders (the reference has none):
+    """This build's Q8_0 / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S encoders (the reference has none):
     N(0, 0.02) rows round-trip within the format's expected relative RMS."""
     rng = np.random.default_rng(9)
     x = (rng.standard_normal((16, 1024)) * 0.02).astype(np.float32)
@@ -359,6 +367,19 @@ def test_iq3s_grid_tables_match_reference(golden):
         # format facts: odd magnitudes 1..15 in every byte
         b = np.array(vals, np.uint32).view(np.uint8)
         assert ((b % 2 == 1) & (b <= 15)).all()
+
+
+def test_iq2s_grid_tables_match_reference(golden):
+    """The committed IQ2_S codebook (oracle/ and the kernels' copy) is the
+    reference table; every byte is one of the format's magnitudes 8, 25, 43."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for path in ("oracle/iq2s_grid.inc", "tinycoder-inference_amd/csrc/iq2s_grid.inc"):
+        text = open(os.path.join(root, path)).read()
+        vals = [int(t, 16) for t in __import__("re").findall(r"0x([0-9a-f]{16})ull", text)]
+        assert len(vals) == 1024
+        arr = np.array(vals, np.uint64)
+        assert hashlib.sha256(arr.tobytes()).digest() == golden["iq2s_grid_sha256"].tobytes(), path
+        assert np.isin(arr.view(np.uint8), [8, 25, 43]).all()
 
 
 # ---- MoE ------------------------------------------------------------------------------
