@@ -41,6 +41,9 @@ __constant__ uint32_t c_grid[256] = {
 __constant__ uint32_t c_grid_s[512] = {
 #include "iq3s_grid.inc"
 };
+__constant__ uint64_t c_grid_2s[1024] = {
+#include "iq2s_grid.inc"
+};
 
 constexpr int NT = 512;
 constexpr int kUnitsPerPass = NT / 4;
@@ -1262,6 +1265,62 @@ struct TDot<kIQ3_S, S> {
     }
 };
 
+// IQ2_S, one unit (82 B, 2-byte aligned in LDS) per lane: per 8 weights one
+// codebook entry of 8 magnitudes (index qs byte | 2 bits of qh[ib], codebook
+// of 1024 x 8 bytes in LDS), 8 sign bits applied bytewise as a two's-
+// complement negation (magnitudes 8..43, no carries), scale 1+2*ls per 16
+// from the nibbles of scales[ib]; isum = sum_ib ls1*sum_16 + ls2*sum_16;
+// value = (d*d8) * isum, and the row is scaled by 0.125 at the end
+// (include/GGMLDequantize.hpp:2028-2057, :2148-2159).
+template <int S>
+struct TDot<kIQ2_S, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               const uint32_t *grid, float *val, int32_t *dbg, size_t dbg_tok) {
+        const uint16_t *u16 = reinterpret_cast<const uint16_t *>(u);
+        int tot[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) tot[s] = 0;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            const uint32_t gw = uint32_t(u16[1 + 2 * ib]) | (uint32_t(u16[2 + 2 * ib]) << 16);
+            const uint32_t sw = uint32_t(u16[17 + 2 * ib]) | (uint32_t(u16[18 + 2 * ib]) << 16);
+            const uint32_t qhb = (uint32_t(u16[33 + ib / 2]) >> (8 * (ib & 1))) & 0xFFu;
+            const uint32_t scb = (uint32_t(u16[37 + ib / 2]) >> (8 * (ib & 1))) & 0xFFu;
+            uint32_t w[8];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t idx = byte_of(gw, l) | ((qhb << (8 - 2 * l)) & 0x300u);
+                const uint32_t sb = byte_of(sw, l);
+                const uint32_t m1 = spread_sign4(sb & 15u), m2 = spread_sign4(sb >> 4);
+                w[2 * l] = (grid[2 * idx] ^ m1) + (m1 & 0x01010101u);
+                w[2 * l + 1] = (grid[2 * idx + 1] ^ m2) + (m2 & 0x01010101u);
+            }
+            const int ls1 = 1 + 2 * int(scb & 15u), ls2 = 1 + 2 * int(scb >> 4);
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const unsigned char *xr = xr0 + s * xtok + 32 * ib;
+                const u32x4 x0 = lds128(xr), x1 = lds128(xr + 16);
+                int p1 = sdot4(int(w[0]), int(x0.x), 0);
+                p1 = sdot4(int(w[1]), int(x0.y), p1);
+                p1 = sdot4(int(w[2]), int(x0.z), p1);
+                p1 = sdot4(int(w[3]), int(x0.w), p1);
+                int p2 = sdot4(int(w[4]), int(x1.x), 0);
+                p2 = sdot4(int(w[5]), int(x1.y), p2);
+                p2 = sdot4(int(w[6]), int(x1.z), p2);
+                p2 = sdot4(int(w[7]), int(x1.w), p2);
+                tot[s] += ls1 * p1 + ls2 * p2;
+            }
+        }
+        const float d = h2f(u16[0]);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (dbg) dbg[s * dbg_tok] = tot[s];
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = (d * d8) * float(tot[s]);
+        }
+    }
+};
+
 template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
@@ -1429,6 +1488,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         uint32_t *sg = reinterpret_cast<uint32_t *>(smem + L.off_g);
         for (uint32_t i = tid; i < 512; i += TNT) sg[i] = c_grid_s[i];
     }
+    if constexpr (TYPE == kIQ2_S) {
+        uint64_t *sg = reinterpret_cast<uint64_t *>(smem + L.off_g);
+        for (uint32_t i = tid; i < 1024; i += TNT) sg[i] = c_grid_2s[i];
+    }
     TC_TRACE_PT(4);
     tstage_finish<TYPE, S, TNT>(jb, xrs, xp, xr);
     TC_TRACE_PT(5);
@@ -1468,7 +1531,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
                     float val[S];
                     // rank-group mode: tile of rank m against that rank's activations (S == 1)
                     const unsigned char *xb = xr + (RG ? size_t(m) * xtok : 0) + size_t(b) * XB;
-                    if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S)
+                    if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S || TYPE == kIQ2_S)
                         TDot<TYPE, S>::run(tile + lane * UB, xb, xtok,
                                            reinterpret_cast<const uint32_t *>(smem + L.off_g), val, dbg, dbg_tok);
                     else
@@ -1497,6 +1560,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
                 for (uint32_t bb = q; bb < nu; bb += 4) g += pg[bb];
                 g = quad_sum(g);
                 if constexpr (TYPE == kIQ3_XXS) g = 0.25f * g;
+                if constexpr (TYPE == kIQ2_S) g = 0.125f * g;
                 const int32_t e = rank_expert(k);
                 if (e < 0 || uint32_t(e) >= jb.n_experts) g = 0.0f;
                 acc = fmaf(rwts[k], g, acc);
@@ -1522,6 +1586,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         if constexpr (TYPE == kIQ3_XXS) {
             g = 0.25f * g;
             u = 0.25f * u;
+        }
+        if constexpr (TYPE == kIQ2_S) {  // the row scale of the IQ2_S fused path (GGMLDequantize.hpp:2148-2159)
+            g = 0.125f * g;
+            u = 0.125f * u;
         }
         if (o < nout && q == 0) {
             if (pairs == 2) {
@@ -1630,13 +1698,14 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     a->off_g = o;
     if (type == kIQ3_XXS) o += 16384;  // signed grid, 256 x 16 words
     if (type == kIQ3_S) o += 2048;     // IQ3_S codebook, 512 words
+    if (type == kIQ2_S) o += 8192;     // IQ2_S codebook, 1024 x 8 bytes
     a->off_t = o;
     o += (C::NT / 64) * tile_slot_bytes(type);
     a->off_p = o;
     return o;
 }
 
-bool tiled_type(int type) { return type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -1697,10 +1766,11 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
         if (fit == 0) return hipErrorInvalidValue;
         rpw = std::min(rpw, fit);
-        // Q3_K / Q6_K / IQ3_XXS / IQ3_S rows are not 16-byte multiples: 8-row
-        // groups keep every workgroup's first row 16-byte aligned (8*110,
-        // 8*210 and 8*98 bytes per 256 columns are multiples of 16).
-        if ((type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S) && rpw < g.rows) {
+        // Q3_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S rows are not 16-byte
+        // multiples: 8-row groups keep every workgroup's first row 16-byte
+        // aligned (8*110, 8*210, 8*98 and 8*82 bytes per 256 columns are
+        // multiples of 16).
+        if ((type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S || type == kIQ2_S) && rpw < g.rows) {
             rpw = (rpw + 7) / 8 * 8;
             if (rpw > fit) rpw = fit / 8 * 8;
             if (rpw == 0) return hipErrorInvalidValue;
@@ -1718,6 +1788,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         case kQ5_K: return launch_tiled<kQ5_K, C>(S, a, wg, lds, st);
         case kQ3_K: return launch_tiled<kQ3_K, C>(S, a, wg, lds, st);
         case kIQ3_S: return launch_tiled<kIQ3_S, C>(S, a, wg, lds, st);
+        case kIQ2_S: return launch_tiled<kIQ2_S, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:

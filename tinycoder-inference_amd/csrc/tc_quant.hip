@@ -15,6 +15,9 @@ __constant__ uint32_t c_iq3xxs_grid[256] = {
 __constant__ uint32_t c_iq3s_grid[512] = {
 #include "iq3s_grid.inc"
 };
+__constant__ uint64_t c_iq2s_grid[1024] = {
+#include "iq2s_grid.inc"
+};
 
 // ---- activation quantizers ---------------------------------------------------
 
@@ -455,6 +458,61 @@ __device__ void enc_iq3s(const float *x, uint8_t *out) {
     }
 }
 
+// IQ2_S (this build's encoder; the reference ships none): per-16 s =
+// max|x|/43, d = 8 * max s / 31 (fp16 RNE), ls = clamp(rne((8s/d - 1)/2), 0,
+// 15), db = (d*(0.5+ls))*0.25; a sign bit per weight; per 8 the codebook
+// entry (of 1024) nearest |x|/db in squared error (first wins), index bits
+// 8-9 in qh, as the reference decoder reads them
+// (include/GGMLDequantize.hpp:1215-1242).
+__device__ void enc_iq2s(const float *x, uint8_t *out) {
+    float sc[16], smax = 0.0f;
+    for (int c = 0; c < 16; ++c) {
+        float amax = 0.0f;
+        for (int i = 0; i < 16; ++i) amax = fabsf(x[16 * c + i]) > amax ? fabsf(x[16 * c + i]) : amax;
+        sc[c] = __fdiv_rn(amax, 43.0f);
+        smax = sc[c] > smax ? sc[c] : smax;
+    }
+    for (int i = 0; i < 82; ++i) out[i] = 0;
+    const uint16_t hd = f2h_rne(__fdiv_rn(8.0f * smax, 31.0f));
+    const float d = h2f(hd);
+    if (d == 0.0f) return;
+    out[0] = uint8_t(hd);
+    out[1] = uint8_t(hd >> 8);
+    uint8_t *qs = out + 2, *signs = out + 34, *qh = out + 66, *scales = out + 74;
+    for (int c = 0; c < 16; ++c) {
+        const int ib = c >> 1, h = c & 1;
+        int ls = int(rintf(__fdiv_rn(__fdiv_rn(8.0f * sc[c], d) - 1.0f, 2.0f)));
+        ls = ls < 0 ? 0 : (ls > 15 ? 15 : ls);
+        scales[ib] |= uint8_t(ls << (4 * h));
+        const float db = d * (0.5f + float(ls)) * 0.25f;
+        for (int q = 0; q < 2; ++q) {
+            const int l = 2 * h + q;
+            const float *xv = x + 32 * ib + 8 * l;
+            float t[8];
+            for (int j = 0; j < 8; ++j) {
+                if (xv[j] < 0.0f) signs[4 * ib + l] |= uint8_t(1u << j);
+                t[j] = __fdiv_rn(fabsf(xv[j]), db);
+            }
+            int best = 0;
+            float berr = 0.0f;
+            for (int gi = 0; gi < 1024; ++gi) {
+                const uint64_t gv = c_iq2s_grid[gi];
+                float err = 0.0f;
+                for (int j = 0; j < 8; ++j) {
+                    const float diff = float(uint32_t(gv >> (8 * j)) & 0xFFu) - t[j];
+                    err = err + diff * diff;
+                }
+                if (gi == 0 || err < berr) {
+                    berr = err;
+                    best = gi;
+                }
+            }
+            qs[4 * ib + l] = uint8_t(best & 255);
+            qh[ib] |= uint8_t((best >> 8) << (2 * l));
+        }
+    }
+}
+
 __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict__ x, uint8_t *__restrict__ out,
                                                uint32_t nunits) {
     const uint32_t u = blockIdx.x * 64 + threadIdx.x;
@@ -468,6 +526,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
         case kQ5_K: enc_q5k(xu, o); break;
         case kQ6_K: enc_q6k(xu, o); break;
         case kIQ3_S: enc_iq3s(xu, o); break;
+        case kIQ2_S: enc_iq2s(xu, o); break;
         default: enc_iq3xxs(xu, o); break;
     }
 }
