@@ -30,6 +30,7 @@ uint32_t oc_type_size(int type) {
      * unit_tests/DequantizeTest.cpp:570 (Q4_K=144, IQ3_XXS=98). */
     switch (type) {
         case OC_TYPE_Q8_0: return 34;
+        case OC_TYPE_Q2_K: return 84;
         case OC_TYPE_Q3_K: return 110;
         case OC_TYPE_Q4_K: return 144;
         case OC_TYPE_Q5_K: return 176;
@@ -215,6 +216,15 @@ static int q5k_value(const uint8_t *blk, int g, int l) {
     return ((qs[32 * c + l] >> (4 * h)) & 0xF) | (((qh[l] >> (2 * c + h)) & 1) << 4);
 }
 
+/* Q2_K (84 B: scales[16] at 0 -- low nibble scale, high nibble min per 16
+ * weights --, qs[64] at 16, d at 80, dmin at 82): 2-bit value of element
+ * e = 128h + 32t + l, bits 2t of qs[32h + l] (include/GGMLDequantize.hpp:
+ * 550-590). */
+static int q2k_value(const uint8_t *blk, int e) {
+    const int h = e >> 7, t = (e >> 5) & 3, l = e & 31;
+    return (blk[16 + 32 * h + l] >> (2 * t)) & 3;
+}
+
 /* Q3_K (110 B: hmask[32] at 0, qs[64] at 32, 12 scale bytes at 96, d at
  * 108): the 16 6-bit scales as unpacked by include/GGMLDequantize.hpp:612-630
  * (kmask1/kmask2 on three little-endian words), returned minus 32. */
@@ -330,6 +340,15 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
                 const float d1 = d * (float)sc, m1 = dmin * (float)m;
                 for (int l = 0; l < 32; ++l) y[32 * g + l] = d1 * (float)q5k_value(blk, g, l) - m1;
             }
+        } else if (type == OC_TYPE_Q2_K) {
+            /* include/GGMLDequantize.hpp:550-590: dl = d * sc, ml = dmin * m per
+             * 16, y = dl * q - ml. */
+            const float d = h2f_at(blk + 80), dmin = h2f_at(blk + 82);
+            for (int e = 0; e < 256; ++e) {
+                const uint8_t sc = blk[e >> 4];
+                const float dl = d * (float)(sc & 0xF), ml = dmin * (float)(sc >> 4);
+                y[e] = dl * (float)q2k_value(blk, e) - ml;
+            }
         } else if (type == OC_TYPE_Q3_K) {
             /* include/GGMLDequantize.hpp:612-648: dl = d * (sc - 32) per 16,
              * y = dl * q with q = q2 - (hmask bit ? 0 : 4). */
@@ -423,6 +442,21 @@ static int32_t q6k_isum(const uint8_t *blk, const int8_t *xq) {
         tot += (int32_t)sc[g] * s;
     }
     return tot;
+}
+
+/* Q2_K block integers: out[0] = sum_g sc_g * sum_16 q*q8 (main), out[1] =
+ * sum_g m_g * bsum_g (min), the two exact sums of the compact kernel's
+ * blockDot (src/cpp/core/SIMDMatMulVecAVX2.cpp:4995-5020). */
+static void q2k_isums(const uint8_t *blk, const int8_t *xq, const int16_t *bsums, int32_t out[2]) {
+    int32_t mainI = 0, minI = 0;
+    for (int g = 0; g < 16; ++g) {
+        int32_t s = 0;
+        for (int i = 0; i < 16; ++i) s += q2k_value(blk, 16 * g + i) * xq[16 * g + i];
+        mainI += (blk[g] & 0xF) * s;
+        minI += (blk[g] >> 4) * bsums[g];
+    }
+    out[0] = mainI;
+    out[1] = minI;
 }
 
 /* Q3_K block integer sum_g (sc[g]-32) * sum_16 q * q8 with q in -4..3: the
@@ -529,7 +563,7 @@ int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
     act_t a;
     if (quantize_acts(type, X, S, cols, &a)) return -1;
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type), nb = cols / bs;
-    const uint32_t k = (type == OC_TYPE_Q4_K || type == OC_TYPE_Q5_K) ? 8 : 1;
+    const uint32_t k = (type == OC_TYPE_Q4_K || type == OC_TYPE_Q5_K) ? 8 : type == OC_TYPE_Q2_K ? 2 : 1;
     for (uint32_t s = 0; s < S; ++s)
         for (uint32_t r = 0; r < rows; ++r)
             for (uint32_t b = 0; b < nb; ++b) {
@@ -540,6 +574,9 @@ int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                     case OC_TYPE_Q4_K: q4k_subsums(blk, xq, o); break;
                     case OC_TYPE_Q5_K: q5k_subsums(blk, xq, o); break;
                     case OC_TYPE_Q3_K: o[0] = q3k_isum(blk, xq); break;
+                    case OC_TYPE_Q2_K:
+                        q2k_isums(blk, xq, a.bsums + (size_t)s * (cols / 16) + (size_t)b * 16, o);
+                        break;
                     case OC_TYPE_Q6_K: o[0] = q6k_isum(blk, xq); break;
                     case OC_TYPE_IQ3_XXS: o[0] = iq3_isum(blk, xq); break;
                     case OC_TYPE_IQ3_S: o[0] = iq3s_isum(blk, xq); break;
@@ -696,6 +733,49 @@ static float row_q6k(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff
     return hsum8(racc);
 }
 
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:4757-5050
+ * (matMulVecBatchQ2K_Compact_Q8K_AVX2): 8 lanes per block. Lane j: min term
+ * (-dmin*d8) * (m[2j]*bs[2j] + m[2j+1]*bs[2j+1]) (one rounding: an fma with
+ * 0); acc from 0 gets fma(dq*d8, sumi_j) per chunk, sumi_j summing over the
+ * chunk's 4 sub-blocks idx sc[2idx + (j>=4)] * sum_4 q*q8 over elements
+ * 32idx + 4j..; the block adds acc + minTerm lane-wise into the row
+ * accumulator; the 8 lanes reduce as ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)). */
+static float row_q2k(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff,
+                     size_t boff) {
+    float racc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 84;
+        const float dq = h2f_at(blk + 80), ndmin = -h2f_at(blk + 82);
+        const float d8 = a->d[doff + b];
+        const int8_t *xq = a->qs + qoff + (size_t)b * 256;
+        const int16_t *bsums = a->bsums + boff + (size_t)b * 16;
+        const float cm = ndmin * d8, dd8 = dq * d8;
+        float minT[8], acc[8];
+        for (int j = 0; j < 8; ++j) {
+            const int32_t prod = (int32_t)(blk[2 * j] >> 4) * bsums[2 * j] + (int32_t)(blk[2 * j + 1] >> 4) * bsums[2 * j + 1];
+            minT[j] = cm * (float)prod;
+            acc[j] = 0.0f;
+        }
+        for (int chunk = 0; chunk < 2; ++chunk) {
+            int32_t sumi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int sub = 0; sub < 4; ++sub) {
+                const int idx = chunk * 4 + sub;
+                for (int j = 0; j < 8; ++j) {
+                    int32_t p = 0;
+                    for (int k = 0; k < 4; ++k) {
+                        const int e = 32 * idx + 4 * j + k;
+                        p += q2k_value(blk, e) * xq[e];
+                    }
+                    sumi[j] += (int32_t)(blk[2 * idx + (j >= 4)] & 0xF) * p;
+                }
+            }
+            for (int j = 0; j < 8; ++j) acc[j] = fmaf(dd8, (float)sumi[j], acc[j]);
+        }
+        for (int j = 0; j < 8; ++j) racc[j] = racc[j] + (acc[j] + minT[j]);
+    }
+    return hsum8(racc);
+}
+
 /* src/cpp/core/SIMDMatMulVecAVX2.cpp:3220-3560 (matMulVecBatchQ3K_Q8K_AVX2):
  * the same 8-lane structure as the Q6_K kernel. Per block, lane j starts at
  * c0 * (s[2j]*bs[2j] + s[2j+1]*bs[2j+1]) with c0 = (-4*dq)*d8 and s = sc-32;
@@ -798,6 +878,7 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t r
                 case OC_TYPE_Q4_K: v = row_q4k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_Q5_K: v = row_q5k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_Q3_K: v = row_q3k(rp, nb, &a, qoff, doff, boff); break;
+                case OC_TYPE_Q2_K: v = row_q2k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_Q6_K: v = row_q6k(rp, nb, &a, qoff, doff, boff); break;
                 case OC_TYPE_IQ3_XXS: v = row_iq3(rp, nb, &a, qoff, doff); break;
                 case OC_TYPE_IQ3_S: v = row_iq3s(rp, nb, &a, qoff, doff); break;
@@ -929,6 +1010,48 @@ void oc_encode_q5k_block(const float *x, uint8_t *out) {
             v = v < 0 ? 0 : (v > 31 ? 31 : v);
             qs[32 * c + l] |= (uint8_t)((v & 15) << (4 * h));
             qh[l] |= (uint8_t)((v >> 4) << (2 * c + h));
+        }
+    }
+}
+
+/* Q2_K weight encoder (the reference ships none; this build defines it).
+ * Per 16: mn = min(0, min x), mx = max(0, max x), scale (mx-mn)/3, min -mn.
+ * Block: d = max scale / 15 and dmin = max min / 15 as fp16 (RNE); 4-bit
+ * sc = clamp(rne(scale/d), 0, 15), m = clamp(rne(min/dmin), 0, 15); weights
+ * q = clamp(rne((x + dmin_fp16*m) / (d_fp16*sc)), 0, 3), packed as the
+ * decoder include/GGMLDequantize.hpp:550-590 reads them. */
+void oc_encode_q2k_block(const float *x, uint8_t *out) {
+    float scale[16], minv[16], maxScale = 0.0f, maxMin = 0.0f;
+    for (int g = 0; g < 16; ++g) {
+        float mn = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 16; ++i) {
+            mn = x[16 * g + i] < mn ? x[16 * g + i] : mn;
+            mx = mx < x[16 * g + i] ? x[16 * g + i] : mx;
+        }
+        scale[g] = (mx - mn) / 3.0f;
+        minv[g] = -mn;
+        maxScale = maxScale < scale[g] ? scale[g] : maxScale;
+        maxMin = maxMin < minv[g] ? minv[g] : maxMin;
+    }
+    memset(out, 0, 84);
+    const uint16_t hd = maxScale > 0.0f ? f2h_rne(maxScale / 15.0f) : 0;
+    const uint16_t hm = maxMin > 0.0f ? f2h_rne(maxMin / 15.0f) : 0;
+    memcpy(out + 80, &hd, 2);
+    memcpy(out + 82, &hm, 2);
+    const float d = oc_half_to_float(hd), dm = oc_half_to_float(hm);
+    for (int g = 0; g < 16; ++g) {
+        int sv = d > 0.0f ? (int)lrintf(scale[g] / d) : 0;
+        int mv = dm > 0.0f ? (int)lrintf(minv[g] / dm) : 0;
+        sv = sv < 0 ? 0 : (sv > 15 ? 15 : sv);
+        mv = mv < 0 ? 0 : (mv > 15 ? 15 : mv);
+        out[g] = (uint8_t)(sv | (mv << 4));
+        const float es = d * (float)sv, em = dm * (float)mv;
+        for (int i = 0; i < 16; ++i) {
+            const int e = 16 * g + i;
+            int q = es > 0.0f ? (int)lrintf((x[e] + em) / es) : 0;
+            q = q < 0 ? 0 : (q > 3 ? 3 : q);
+            const int h = e >> 7, t = (e >> 5) & 3, l = e & 31;
+            out[16 + 32 * h + l] |= (uint8_t)(q << (2 * t));
         }
     }
 }
@@ -1211,6 +1334,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
             case OC_TYPE_Q4_K: oc_encode_q4k_block(xb, o); break;
             case OC_TYPE_Q5_K: oc_encode_q5k_block(xb, o); break;
             case OC_TYPE_Q3_K: oc_encode_q3k_block(xb, o); break;
+            case OC_TYPE_Q2_K: oc_encode_q2k_block(xb, o); break;
             case OC_TYPE_Q6_K: oc_encode_q6k_block(xb, o); break;
             case OC_TYPE_IQ3_S: oc_encode_iq3s_block(xb, o); break;
             case OC_TYPE_IQ2_S: oc_encode_iq2s_block(xb, o); break;

@@ -18,11 +18,11 @@
  *   oc_dequant_row  pinned: golden vectors + closed forms on hand-built blocks.
  *   oc_block_isums  pinned: brute-force integer dot of dequantized integer
  *       weights x quantized activations (order-free integer identity).
- *   oc_matmul (Q8_0/Q3_K/Q4_K/Q5_K/Q6_K/IQ3_XXS/IQ3_S/IQ2_S)  pinned: bit-exact against
+ *   oc_matmul (Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K/IQ3_XXS/IQ3_S/IQ2_S)  pinned: bit-exact against
  *       golden outputs of the compiled reference AVX2 / scalar kernels.
  *   oc_encode_q4k_block  pinned: bit-exact against the compiled reference
  *       quantizeQ4KBlock (golden) + the reference's own round-trip test.
- *   oc_encode_q8_0_block / oc_encode_q3k_block / oc_encode_q5k_block / oc_encode_q6k_block /
+ *   oc_encode_q8_0_block / oc_encode_q2k_block / oc_encode_q3k_block / oc_encode_q5k_block / oc_encode_q6k_block /
  *   oc_encode_iq3xxs_block / oc_encode_iq3s_block / oc_encode_iq2s_block:
  *       the reference has no encoder for these formats (this build defines
  *       them); pinned by decode round-trip error bounds only.
@@ -40,6 +40,7 @@ extern "C" {
 
 enum {
     OC_TYPE_Q8_0 = 8,
+    OC_TYPE_Q2_K = 10,
     OC_TYPE_Q3_K = 11,
     OC_TYPE_Q4_K = 12,
     OC_TYPE_Q5_K = 13,
@@ -67,7 +68,8 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out);
 
 /* Per-block integer dot sums of W[rows][cols] against the quantized activations
  * of X[S][cols]. Output layout [S][rows][nblk][k]: k = 8 sub-block sums for
- * Q4_K and Q5_K, k = 1 otherwise (Q8_0 blocks are the 32-wide ones). */
+ * Q4_K and Q5_K, k = 2 (main, min) for Q2_K, k = 1 otherwise (Q8_0 blocks
+ * are the 32-wide ones). */
 int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                    uint32_t rows, uint32_t cols, int32_t *isums);
 
@@ -79,6 +81,7 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S,
 /* Weight encoders. */
 void oc_encode_q4k_block(const float *x, uint8_t *out);
 void oc_encode_q8_0_block(const float *x, uint8_t *out);
+void oc_encode_q2k_block(const float *x, uint8_t *out);
 void oc_encode_q3k_block(const float *x, uint8_t *out);
 void oc_encode_q5k_block(const float *x, uint8_t *out);
 void oc_encode_q6k_block(const float *x, uint8_t *out);

@@ -49,6 +49,7 @@ void ref_quantize_q8k(const float *x, uint32_t n, int8_t *qs, float *d, int16_t 
 void ref_dequant_block(int type, const uint8_t *blk, float *out) {
     switch (type) {
         case 8: GGMLDequantize::dequantizeQ8_0Block(blk, out); break;
+        case 10: GGMLDequantize::dequantizeQ2_KBlock(blk, out); break;  // include/GGMLDequantize.hpp:550
         case 11: GGMLDequantize::dequantizeQ3_KBlock(blk, out); break;  // include/GGMLDequantize.hpp:612
         case 12: GGMLDequantize::dequantizeQ4_KBlock(blk, out); break;
         case 13: GGMLDequantize::dequantizeQ5_KBlock(blk, out); break;  // include/GGMLDequantize.hpp:346
@@ -83,6 +84,8 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
                uint32_t cols, float *out) {
     switch (type) {
         case 12: simd::matMulVecBatchQ4K_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
+        // src/cpp/core/SIMDMatMulVecAVX2.cpp:4757 (the compact-block Q2_K kernel)
+        case 10: simd::matMulVecBatchQ2K_Compact_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
         // src/cpp/core/SIMDMatMulVecAVX2.cpp:3220 (no residual)
         case 11: simd::matMulVecBatchQ3K_Q8K_AVX2(W, X, seqLen, rows, cols, out, nullptr); return 0;
         // src/cpp/core/SIMDMatMulVecAVX2.cpp:3842

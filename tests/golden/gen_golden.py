@@ -95,6 +95,15 @@ def iq2s_random_blocks(rng, nblk):
     return b.ravel()
 
 
+def q2k_random_blocks(rng, nblk):
+    """Random Q2_K bytes (every scale/min nibble and 2-bit pattern) with fixed
+    normal fp16 d and dmin."""
+    b = rng.integers(0, 256, (nblk, 84), dtype=np.uint8)
+    b[:, 80:82] = np.frombuffer(np.float16(0.0093).tobytes(), np.uint8)
+    b[:, 82:84] = np.frombuffer(np.float16(0.0051).tobytes(), np.uint8)
+    return b.ravel()
+
+
 def q80_random_blocks(rng, nblk):
     b = rng.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
     d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-10, -6, nblk)).astype(np.float16)
@@ -304,6 +313,20 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.IQ2_S, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.IQ2_S, w, X4, rows, cols)
+
+    # Q2_K, likewise: its dequant and the compact-block kernel
+    # matMulVecBatchQ2K_Compact_Q8K_AVX2 (SIMDMatMulVecAVX2.cpp:4757).
+    rq = np.random.default_rng(20261206)
+    g["deq_q2k_w"] = q2k_random_blocks(rq, 8)
+    g["deq_q2k_y"] = ref.dequant(O.Q2_K, g["deq_q2k_w"], 8, 256)
+    casesq = {
+        "q2k_rand": q2k_random_blocks(rq, rows * nb),
+        "q2k_enc002": O.Oracle().encode(O.Q2_K, (rq.standard_normal((rows, cols)) * 0.02).astype(np.float32)),
+    }
+    for name, w in casesq.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.Q2_K, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.Q2_K, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")

@@ -104,7 +104,7 @@ def test_quantize_q8_0_act_pinned_by_reference_probe(oracle, golden):
 
 # ---- block decoders ---------------------------------------------------------------
 
-@pytest.mark.parametrize("name,qt", [("q3k", O.Q3_K), ("q4k", O.Q4_K), ("q5k", O.Q5_K), ("q6k", O.Q6_K), ("iq3", O.IQ3_XXS),
+@pytest.mark.parametrize("name,qt", [("q2k", O.Q2_K), ("q3k", O.Q3_K), ("q4k", O.Q4_K), ("q5k", O.Q5_K), ("q6k", O.Q6_K), ("iq3", O.IQ3_XXS),
                                      ("iq3s", O.IQ3_S), ("iq2s", O.IQ2_S),
                                      ("q80", O.Q8_0)])
 def test_dequant_matches_reference(oracle, golden, name, qt):
@@ -161,7 +161,7 @@ def test_iq3_dequant_closed_form(oracle):
 
 # ---- per-block integer dots: brute-force identity ------------------------------------
 
-@pytest.mark.parametrize("qt", [O.Q8_0, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S])
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S])
 def test_block_isums_identity(oracle, qt):
     """sum over blocks of the integer sums, scaled per block by the float block
     scales, reproduces dequant(W) . (d8 * xq) in exact rational arithmetic."""
@@ -181,6 +181,9 @@ def test_block_isums_identity(oracle, qt):
         w = gen(rng, rows * cols // 256)
     elif qt == O.Q3_K:
         from gen_golden import q3k_random_blocks as gen
+        w = gen(rng, rows * cols // 256)
+    elif qt == O.Q2_K:
+        from gen_golden import q2k_random_blocks as gen
         w = gen(rng, rows * cols // 256)
     elif qt == O.IQ3_S:
         from gen_golden import iq3s_random_blocks as gen
@@ -211,6 +214,20 @@ def test_block_isums_identity(oracle, qt):
             nib[:, :, 32 * g:32 * g + 32] = (byt >> 4) if g % 2 else (byt & 15)
         expect = (nib * qs.reshape(1, -1, 256)).reshape(rows, -1, 8, 32).sum(3)
         assert np.array_equal(expect, isums)
+    elif qt == O.Q2_K:
+        # 2-bit values and 4-bit scale/min nibbles from the block bytes (layout
+        # pinned by the reference dequant golden): main = sum sc*sum q*x,
+        # min = sum m*bsum; and dequant = d*main-part - dmin*min-part exactly
+        qs, d8, bs = oracle.quantize_q8k(x[0])
+        wb = w.reshape(rows, cols // 256, 84).astype(np.int64)
+        q2 = np.zeros((rows, cols // 256, 256), np.int64)
+        for e in range(256):
+            h, t, l = e // 128, (e // 32) % 4, e % 32
+            q2[:, :, e] = (wb[:, :, 16 + 32 * h + l] >> (2 * t)) & 3
+        sc, mn = wb[:, :, :16] & 15, wb[:, :, :16] >> 4
+        grp = (q2 * qs.reshape(1, -1, 256)).reshape(rows, -1, 16, 16).sum(3)
+        assert np.array_equal((sc * grp).sum(2), isums[:, :, 0])
+        assert np.array_equal((mn * bs.reshape(1, -1, 16)).sum(2), isums[:, :, 1])
     elif qt == O.Q5_K:
         # 5-bit values from the block bytes (layout pinned by the reference
         # dequant golden): qs at 48, qh at 16, sub-block g = 2c + h
@@ -256,7 +273,8 @@ def test_block_isums_identity(oracle, qt):
 # ---- mat-vec kernels -----------------------------------------------------------------
 
 MM = [("q4k_rand", O.Q4_K), ("q4k_enc1", O.Q4_K), ("q4k_enc002", O.Q4_K), ("q5k_rand", O.Q5_K),
-      ("q5k_enc1", O.Q5_K), ("q3k_rand", O.Q3_K), ("q3k_enc002", O.Q3_K), ("iq3s_rand", O.IQ3_S),
+      ("q5k_enc1", O.Q5_K), ("q3k_rand", O.Q3_K), ("q3k_enc002", O.Q3_K), ("q2k_rand", O.Q2_K),
+      ("q2k_enc002", O.Q2_K), ("iq3s_rand", O.IQ3_S),
       ("iq3s_enc002", O.IQ3_S), ("iq2s_rand", O.IQ2_S), ("iq2s_enc002", O.IQ2_S), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
 
 
@@ -275,7 +293,7 @@ def test_matmul_q80_cols96(oracle, golden):
     assert (bits(got) == bits(golden["mm_q80c96_y"])).all()
 
 
-@pytest.mark.parametrize("qt", [O.Q8_0, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S])
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S])
 def test_matmul_close_to_float_dot(oracle, qt):
     """Independent of the reference: the quantized mat-vec approximates the
     float product of the dequantized weights with x (activation quantization
@@ -332,10 +350,10 @@ def test_q4k_encoder_reference_roundtrip_thresholds(oracle):
     assert rel.mean() < 0.09
 
 
-@pytest.mark.parametrize("qt,bound", [(O.Q8_0, 0.01), (O.Q3_K, 0.2), (O.Q5_K, 0.08), (O.Q6_K, 0.04),
+@pytest.mark.parametrize("qt,bound", [(O.Q8_0, 0.01), (O.Q2_K, 0.45), (O.Q3_K, 0.2), (O.Q5_K, 0.08), (O.Q6_K, 0.04),
                                       (O.IQ3_XXS, 0.25), (O.IQ3_S, 0.2), (O.IQ2_S, 0.35)])
 def test_own_encoders_roundtrip(oracle, qt, bound):
-    """This build's Q8_0 / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S encoders (the reference has none):
+    """This build's Q8_0 / Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S encoders (the reference has none):
     N(0, 0.02) rows round-trip within the format's expected relative RMS."""
     rng = np.random.default_rng(9)
     x = (rng.standard_normal((16, 1024)) * 0.02).astype(np.float32)
