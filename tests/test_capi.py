@@ -55,7 +55,8 @@ def test_row_bytes():
     assert lib.tc_row_bytes(14, 18944) == 74 * 210
     assert lib.tc_row_bytes(18, 3584) == 14 * 98
     assert lib.tc_row_bytes(11, 256) == 110
-    assert lib.tc_row_bytes(10, 256) == 0  # Q2_K: not a supported type
+    assert lib.tc_row_bytes(10, 256) == 84
+    assert lib.tc_row_bytes(9, 256) == 0  # Q8_1: not a weight type here
 
 
 def test_reference_interface_header_compiles_and_links(tmp_path):

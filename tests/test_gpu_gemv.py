@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from qdata import ALL, IQ2_S, IQ3_S, IQ3_XXS, NAMES, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
+from qdata import ALL, IQ2_S, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -77,7 +77,7 @@ def test_block_isums_bit_exact(tc, dev, oracle, qt, S, rows, cols):
 # ---- mat-vec outputs ----------------------------------------------------------------------
 
 MM = [("q4k_rand", Q4_K), ("q4k_enc1", Q4_K), ("q4k_enc002", Q4_K),
-      ("q5k_rand", Q5_K), ("q5k_enc1", Q5_K), ("q3k_rand", Q3_K), ("q3k_enc002", Q3_K), ("iq3s_rand", IQ3_S),
+      ("q5k_rand", Q5_K), ("q5k_enc1", Q5_K), ("q3k_rand", Q3_K), ("q3k_enc002", Q3_K), ("q2k_rand", Q2_K), ("q2k_enc002", Q2_K), ("iq3s_rand", IQ3_S),
       ("iq3s_enc002", IQ3_S), ("iq2s_rand", IQ2_S), ("iq2s_enc002", IQ2_S),
       ("q6k_rand", Q6_K), ("iq3_rand", IQ3_XXS), ("q80_rand", Q8_0)]
 
@@ -121,7 +121,7 @@ def test_gemv_vs_oracle(tc, dev, oracle, qt, S):
 
 @pytest.mark.parametrize("qt,rows,cols", [
     (Q4_K, 3584, 3584), (Q4_K, 512, 3584), (Q4_K, 18944, 3584), (Q4_K, 3584, 18944),
-    (Q8_0, 4096, 4096), (Q6_K, 3584, 18944), (IQ3_XXS, 18944, 3584), (Q5_K, 18944, 3584), (Q3_K, 3584, 18944), (IQ3_S, 18944, 3584), (IQ2_S, 3584, 18944),
+    (Q8_0, 4096, 4096), (Q6_K, 3584, 18944), (IQ3_XXS, 18944, 3584), (Q5_K, 18944, 3584), (Q3_K, 3584, 18944), (IQ3_S, 18944, 3584), (IQ2_S, 3584, 18944), (Q2_K, 18944, 3584),
 ])
 def test_gemv_full_shapes(tc, dev, oracle, qt, rows, cols):
     """BASELINE shapes at full size, weights from the GPU encoder on N(0,0.02)
@@ -160,7 +160,7 @@ def test_gemv_refuses_bad_shapes_without_writing(tc, dev):
     w = torch.zeros(144 * 4, dtype=torch.uint8, device=dev)
     x = torch.zeros((1, 512), device=dev)
     out = torch.full((1, 2), 7.0, device=dev)
-    for args in [(Q4_K, 2, 300), (Q4_K, 0, 512), (10, 2, 512)]:
+    for args in [(Q4_K, 2, 300), (Q4_K, 0, 512), (9, 2, 512)]:
         qt, rows, cols = args
         with pytest.raises(TCError) as e:
             tc.gemv(qt, w, x, rows, cols, out=out)
@@ -305,6 +305,8 @@ def test_debug_blocks_hook(tc, dev, oracle, qt):
                 wz[k, 208:210] = 0
             elif qt == Q3_K:
                 wz[k, 108:110] = 0
+            elif qt == Q2_K:
+                wz[k, 80:84] = 0
             else:
                 wz[k, :2] = 0
         ok, worst = close(blk[b], oracle.matmul(qt, wz.ravel(), x, 1, cols)[0, 0])

@@ -86,7 +86,7 @@ bool ensure(void *&p, size_t &cap, size_t need) {
 // touch: one 128-token tile of 256-byte rows.
 constexpr size_t kGemmActSlack = 128 * 256;
 
-bool type_ok(int t) { return t == TC_Q8_0 || t == TC_IQ2_S || t == TC_IQ3_S || t == TC_Q3_K || t == TC_Q4_K || t == TC_Q5_K || t == TC_Q6_K || t == TC_IQ3_XXS; }
+bool type_ok(int t) { return t == TC_Q8_0 || t == TC_Q2_K || t == TC_IQ2_S || t == TC_IQ3_S || t == TC_Q3_K || t == TC_Q4_K || t == TC_Q5_K || t == TC_Q6_K || t == TC_IQ3_XXS; }
 
 bool g_q8_gemm_enabled = true;
 
@@ -141,7 +141,7 @@ int run_gemv(Device *dev, int type, const void *w, const void *w2, const float *
     if (smax == 0) return fail(TC_E_UNSUPPORTED, "cols=%u too wide for the decode kernel", cols);
     const tc::ActLayout L = tc::act_layout(type, S, cols);
     const uint32_t nbr = type == TC_Q8_0 ? cols / 32 : cols / 256;
-    const size_t per = type == TC_Q4_K || type == TC_Q5_K ? 8 : 1;
+    const size_t per = type == TC_Q4_K || type == TC_Q5_K ? 8 : type == TC_Q2_K ? 2 : 1;
     for (uint32_t s0 = 0; s0 < S; s0 += smax) {
         const uint32_t n = std::min(smax, S - s0);
         tc::GemvJob job;
@@ -294,7 +294,7 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
     if (type == TC_Q8_0 && !g_q8_gemm_enabled) return fail(TC_E_UNSUPPORTED, "Q8_0 GEMM disabled");
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (type != TC_Q4_K && type != TC_Q8_0) {
-        // Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S: the exact batched path (the reference's launchQGemm,
+        // Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S: the exact batched path (the reference's launchQGemm,
         // GpuGemvIQInt8.hpp:771-847) -- the decode kernel over token groups.
         for (uint32_t s0 = 0; s0 < seq_len; s0 += 8) {
             const uint32_t S = std::min(8u, seq_len - s0);
@@ -542,11 +542,12 @@ struct DevBuf {
 };
 
 // Scale fields of one block zeroed: the block then contributes exactly 0 in
-// every kernel (Q3_K d, Q4_K / Q5_K d and dmin, IQ3_S / IQ2_S d, Q6_K d, IQ3_XXS d, Q8_0 d).
+// every kernel (Q2_K d and dmin, Q3_K d, Q4_K / Q5_K d and dmin, IQ3_S / IQ2_S d, Q6_K d, IQ3_XXS d, Q8_0 d).
 void zero_block_scales(int type, uint8_t *blk) {
     switch (type) {
         case TC_Q4_K:
         case TC_Q5_K: std::memset(blk, 0, 4); break;
+        case TC_Q2_K: std::memset(blk + 80, 0, 4); break;
         case TC_Q3_K: std::memset(blk + 108, 0, 2); break;
         case TC_Q6_K: std::memset(blk + 208, 0, 2); break;
         default: std::memset(blk, 0, 2); break;

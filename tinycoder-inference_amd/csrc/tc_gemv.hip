@@ -69,7 +69,7 @@ struct LaunchArgs {
     uint32_t off_d, off_b, off_g, off_p;
 };
 
-__host__ __device__ constexpr bool uses_bsums(int type) { return type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ6_K; }
+__host__ __device__ constexpr bool uses_bsums(int type) { return type == kQ2_K || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ6_K; }
 // Passes of weight loads each lane keeps in flight (register ring), sized so
 // that the kernel stays within the 256 VGPRs of an 8-wave-per-CU launch.
 __host__ __device__ constexpr int ring_depth(int type, int S) {
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(NT) void k_gemv(LaunchArgs L) {
     const uint32_t row_begin = (blockIdx.x - jb.wg_begin) * jb.rows_per_wg;
     const uint32_t row_end = min(jb.rows, row_begin + jb.rows_per_wg);
     const size_t nbr = TYPE == kQ8_0 ? jb.cols / 32 : jb.cols / 256;
-    const size_t per = TYPE == kQ4_K || TYPE == kQ5_K ? 8 : 1;
+    const size_t per = TYPE == kQ4_K || TYPE == kQ5_K ? 8 : TYPE == kQ2_K ? 2 : 1;
 
     XCtx c;
     c.sx = sx;
@@ -1050,6 +1050,73 @@ struct TDot<kQ3_K, S> {
     }
 };
 
+// Q2_K, one unit (84 B, 4-byte aligned in LDS) per lane: 2-bit values (bits
+// 2t of qs[32h + l] for sub-block 4h + t) straight into v_dot4 (0..3); per 16
+// the 4-bit scale (low nibble) and min (high nibble) of scales[g]; main =
+// sum sc*sum q*x and min = sum m*bsum exact in int32, value d8*(d*main -
+// dmin*min) (the two sums of the compact-block kernel,
+// SIMDMatMulVecAVX2.cpp:4995-5020; it rounds them per lane in fp32).
+template <int S>
+struct TDot<kQ2_K, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        const u32x4 sv = lds128(u);
+        const uint32_t scb[4] = {sv.x, sv.y, sv.z, sv.w};
+        const uint32_t dw = *reinterpret_cast<const uint32_t *>(u + 80);
+        const float d = h2f(dw & 0xFFFFu), dmin = h2f(dw >> 16);
+        int mainI[S], minI[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) mainI[s] = minI[s] = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x4 qa = lds128(u + 16 + 32 * h), qb = lds128(u + 32 + 32 * h);
+            const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int sb = 4 * h + t;
+                uint32_t w[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) w[k] = (q[k] >> (2 * t)) & 0x03030303u;
+                const int sc0 = int(byte_of(scb[(2 * sb) >> 2], (2 * sb) & 3) & 15u);
+                const int sc1 = int(byte_of(scb[(2 * sb + 1) >> 2], (2 * sb + 1) & 3) & 15u);
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const unsigned char *xr = xr0 + s * xtok + 32 * sb;
+                    const u32x4 x0 = lds128(xr), x1 = lds128(xr + 16);
+                    int p0 = sdot4(int(w[0]), int(x0.x), 0);
+                    p0 = sdot4(int(w[1]), int(x0.y), p0);
+                    p0 = sdot4(int(w[2]), int(x0.z), p0);
+                    p0 = sdot4(int(w[3]), int(x0.w), p0);
+                    int p1 = sdot4(int(w[4]), int(x1.x), 0);
+                    p1 = sdot4(int(w[5]), int(x1.y), p1);
+                    p1 = sdot4(int(w[6]), int(x1.z), p1);
+                    p1 = sdot4(int(w[7]), int(x1.w), p1);
+                    mainI[s] += sc0 * p0 + sc1 * p1;
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const uint32_t *bsp = reinterpret_cast<const uint32_t *>(xr0 + s * xtok + XB_BS);
+            int m = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t sc2 = (scb[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;  // scale bytes 2i, 2i+1
+                const uint32_t mp = ((sc2 >> 4) & 0xFu) | (((sc2 >> 12) & 0xFu) << 16);
+                const uint32_t bp = bsp[i];
+                m += int((mp & 0xFFFFu)) * int(int16_t(bp & 0xFFFFu)) + int(mp >> 16) * int(int16_t(bp >> 16));
+            }
+            minI[s] = m;
+            if (dbg) {
+                dbg[s * dbg_tok] = mainI[s];
+                dbg[s * dbg_tok + 1] = minI[s];
+            }
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = d8 * (d * float(mainI[s]) - dmin * float(minI[s]));
+        }
+    }
+};
+
 // Q8_0, one unit (8 blocks of 34 B) per lane: value = sum_blk (d_w*d8) * isum
 // (reference SIMDMatMulVecAVX2.cpp:4339-4366).
 template <int S>
@@ -1381,7 +1448,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     const uint32_t ntiles_mat = (per_mat + kTileUnits - 1) / kTileUnits;
     const uint32_t ntiles = ntiles_mat * pairs;
     const size_t nbr = TYPE == kQ8_0 ? jb.cols / 32 : jb.cols / 256;
-    const size_t per = TYPE == kQ4_K || TYPE == kQ5_K ? 8 : 1;
+    const size_t per = TYPE == kQ4_K || TYPE == kQ5_K ? 8 : TYPE == kQ2_K ? 2 : 1;
     const size_t dbg_tok = size_t(jb.rows) * nbr * per;
     const size_t xtok = size_t(nu) * XB;
     // Expert of rank m (rank-group mode; m is wave-uniform).
@@ -1705,7 +1772,7 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     return o;
 }
 
-bool tiled_type(int type) { return type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -1766,11 +1833,12 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
         if (fit == 0) return hipErrorInvalidValue;
         rpw = std::min(rpw, fit);
-        // Q3_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S rows are not 16-byte
+        // Q2_K / Q3_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S rows are not 16-byte
         // multiples: 8-row groups keep every workgroup's first row 16-byte
-        // aligned (8*110, 8*210, 8*98 and 8*82 bytes per 256 columns are
-        // multiples of 16).
-        if ((type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S || type == kIQ2_S) && rpw < g.rows) {
+        // aligned (8*84, 8*110, 8*210, 8*98 and 8*82 bytes per 256 columns
+        // are multiples of 16).
+        if ((type == kQ2_K || type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S || type == kIQ2_S) &&
+            rpw < g.rows) {
             rpw = (rpw + 7) / 8 * 8;
             if (rpw > fit) rpw = fit / 8 * 8;
             if (rpw == 0) return hipErrorInvalidValue;
@@ -1789,6 +1857,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         case kQ3_K: return launch_tiled<kQ3_K, C>(S, a, wg, lds, st);
         case kIQ3_S: return launch_tiled<kIQ3_S, C>(S, a, wg, lds, st);
         case kIQ2_S: return launch_tiled<kIQ2_S, C>(S, a, wg, lds, st);
+        case kQ2_K: return launch_tiled<kQ2_K, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:

@@ -243,6 +243,49 @@ __device__ void enc_q8_0(const float *x, uint8_t *out) {
     }
 }
 
+// Q2_K (this build's encoder; the reference ships none): per-16 affine
+// scale (max-min)/3 and min -min (0 included in the range), fp16 (RNE)
+// super-scales max/15, 4-bit scales and mins (low / high nibble of
+// scales[g]), q = clamp(rne((x + dmin*m)/(d*sc)), 0, 3), packed as the
+// reference decoder reads them (include/GGMLDequantize.hpp:550-590).
+__device__ void enc_q2k(const float *x, uint8_t *out) {
+    float scale[16], minv[16], maxScale = 0.0f, maxMin = 0.0f;
+    for (int g = 0; g < 16; ++g) {
+        float mn = 0.0f, mx = 0.0f;
+        for (int i = 0; i < 16; ++i) {
+            mn = x[16 * g + i] < mn ? x[16 * g + i] : mn;
+            mx = mx < x[16 * g + i] ? x[16 * g + i] : mx;
+        }
+        scale[g] = __fdiv_rn(mx - mn, 3.0f);
+        minv[g] = -mn;
+        maxScale = maxScale < scale[g] ? scale[g] : maxScale;
+        maxMin = maxMin < minv[g] ? minv[g] : maxMin;
+    }
+    for (int i = 0; i < 84; ++i) out[i] = 0;
+    const uint16_t hd = maxScale > 0.0f ? f2h_rne(__fdiv_rn(maxScale, 15.0f)) : 0;
+    const uint16_t hm = maxMin > 0.0f ? f2h_rne(__fdiv_rn(maxMin, 15.0f)) : 0;
+    out[80] = uint8_t(hd);
+    out[81] = uint8_t(hd >> 8);
+    out[82] = uint8_t(hm);
+    out[83] = uint8_t(hm >> 8);
+    const float d = h2f(hd), dm = h2f(hm);
+    for (int g = 0; g < 16; ++g) {
+        int sv = d > 0.0f ? int(rintf(__fdiv_rn(scale[g], d))) : 0;
+        int mv = dm > 0.0f ? int(rintf(__fdiv_rn(minv[g], dm))) : 0;
+        sv = sv < 0 ? 0 : (sv > 15 ? 15 : sv);
+        mv = mv < 0 ? 0 : (mv > 15 ? 15 : mv);
+        out[g] = uint8_t(sv | (mv << 4));
+        const float es = d * float(sv), em = dm * float(mv);
+        for (int i = 0; i < 16; ++i) {
+            const int e = 16 * g + i;
+            int q = es > 0.0f ? int(rintf(__fdiv_rn(x[e] + em, es))) : 0;
+            q = q < 0 ? 0 : (q > 3 ? 3 : q);
+            const int h = e >> 7, t = (e >> 5) & 3, l = e & 31;
+            out[16 + 32 * h + l] |= uint8_t(q << (2 * t));
+        }
+    }
+}
+
 // Q3_K (this build's encoder; the reference ships none): per-16 group scale
 // m/-4 from the signed first-abs-max, block iscale = -32/M over the group
 // scales, 6-bit signed scales (stored +32), fp16 (RNE) d = 1/iscale, q =
@@ -522,6 +565,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
     switch (type) {
         case kQ4_K: enc_q4k(xu, o); break;
         case kQ8_0: enc_q8_0(xu, o); break;
+        case kQ2_K: enc_q2k(xu, o); break;
         case kQ3_K: enc_q3k(xu, o); break;
         case kQ5_K: enc_q5k(xu, o); break;
         case kQ6_K: enc_q6k(xu, o); break;

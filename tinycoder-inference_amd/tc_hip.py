@@ -11,10 +11,10 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtc_hip.so")
 
-Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S = 8, 11, 12, 13, 14, 18, 21, 22
-TYPES = {"Q8_0": Q8_0, "Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "IQ3_XXS": IQ3_XXS, "IQ3_S": IQ3_S, "IQ2_S": IQ2_S}
-TYPE_SIZE = {Q8_0: 34, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82}
-BLOCK_SIZE = {Q8_0: 32, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256}
+Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S = 8, 10, 11, 12, 13, 14, 18, 21, 22
+TYPES = {"Q8_0": Q8_0, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "IQ3_XXS": IQ3_XXS, "IQ3_S": IQ3_S, "IQ2_S": IQ2_S}
+TYPE_SIZE = {Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82}
+BLOCK_SIZE = {Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256}
 
 TC_OK, TC_E_UNSUPPORTED, TC_E_LAUNCH, TC_E_ARG = 0, -1, -2, -3
 
@@ -190,7 +190,7 @@ class Library:
         import torch
         S = x.numel() // cols
         nb = cols // BLOCK_SIZE[qtype]
-        k = 8 if qtype in (Q4_K, Q5_K) else 1
+        k = 8 if qtype in (Q4_K, Q5_K) else 2 if qtype == Q2_K else 1
         out = torch.empty((S, rows, nb, k), dtype=torch.int32, device=x.device)
         self._check(self.lib.tc_block_isums(qtype, _ptr(w), _ptr(x), _ptr(out), S, rows, cols,
                                             self._stream()))
