@@ -15,6 +15,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+static const uint64_t k_iq2xs_grid[512] = {
+#include "iq2xs_grid.inc"
+};
 static const uint64_t k_iq2s_grid[1024] = {
 #include "iq2s_grid.inc"
 };
@@ -38,6 +41,7 @@ uint32_t oc_type_size(int type) {
         case OC_TYPE_IQ3_XXS: return 98;
         case OC_TYPE_IQ3_S: return 110;
         case OC_TYPE_IQ2_S: return 82;
+        case OC_TYPE_IQ2_XS: return 74;
         default: return 0;
     }
 }
@@ -306,6 +310,24 @@ static int iq2s_signed(const uint8_t *blk, int e, int *ls_out) {
     return (signs[4 * ib + l] >> j) & 1 ? -mag : mag;
 }
 
+/* IQ2_XS (74 B: d, qs16[32] at 2 -- bits 0-8 codebook index, bits 9-15 a
+ * 7-bit sign index whose 8th sign is its parity --, scales[8] at 66) float
+ * weight of element e = 32ib + 8l + j: dl * grid byte j * sign with dl =
+ * (d * (0.5 + ls)) * 0.25, ls the nibble (l >= 2) of scales[ib]
+ * (include/GGMLDequantize.hpp:1245-1271, the same arithmetic in the block
+ * dot :1901-1927). */
+static float iq2xs_weight(const uint8_t *blk, int e) {
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7;
+    uint16_t q;
+    memcpy(&q, blk + 2 + 2 * (4 * ib + l), 2);
+    const uint32_t si = q >> 9;
+    const uint32_t signs = si | ((uint32_t)__builtin_parity(si) << 7);
+    const int ls = (blk[66 + ib] >> (4 * (l >> 1))) & 15;
+    const float dl = h2f_at(blk) * (0.5f + (float)ls) * 0.25f;
+    const float g = (float)((k_iq2xs_grid[q & 511] >> (8 * j)) & 0xFFu);
+    return dl * g * ((signs >> j) & 1 ? -1.0f : 1.0f);
+}
+
 int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type);
     if (bs == 0 || n % bs) return -1;
@@ -365,6 +387,8 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
                 const int q = q6k_raw(blk, e) - 32;
                 y[e] = d * (float)sc[e >> 4] * (float)q;
             }
+        } else if (type == OC_TYPE_IQ2_XS) {
+            for (int e = 0; e < 256; ++e) y[e] = iq2xs_weight(blk, e);
         } else if (type == OC_TYPE_IQ2_S) {
             /* include/GGMLDequantize.hpp:1215-1242: db = (d * (0.5 + ls)) *
              * 0.25, y = (db * grid) * sign. */
@@ -559,7 +583,7 @@ static int shape_ok(int type, uint32_t cols) {
 
 int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                    uint32_t rows, uint32_t cols, int32_t *isums) {
-    if (!shape_ok(type, cols)) return -1;
+    if (!shape_ok(type, cols) || type == OC_TYPE_IQ2_XS) return -1;  /* float path: no integer sums */
     act_t a;
     if (quantize_acts(type, X, S, cols, &a)) return -1;
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type), nb = cols / bs;
@@ -861,9 +885,34 @@ static float row_iq2s(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qof
     return 0.125f * sumf;
 }
 
+/* IQ2_XS: no activation quantization. Block dot = float(sum_e double(x_e) *
+ * double(w_e)) (dotProductIQ2_XS, include/GGMLDequantize.hpp:1901-1927); row =
+ * float(sum_b double(block dot)) (matMulVecFused, :2449-2461). The double
+ * products of two floats are exact, so fused or not they round the same. */
+static void matmul_iq2xs(const uint8_t *W, const float *X, uint32_t S, uint32_t rows, uint32_t cols,
+                         float *out) {
+    const uint32_t nb = cols / 256;
+    for (uint32_t s = 0; s < S; ++s)
+        for (uint32_t r = 0; r < rows; ++r) {
+            double dot = 0.0;
+            for (uint32_t b = 0; b < nb; ++b) {
+                const uint8_t *blk = W + ((size_t)r * nb + b) * 74;
+                const float *x = X + (size_t)s * cols + (size_t)b * 256;
+                double bd = 0.0;
+                for (int e = 0; e < 256; ++e) bd += (double)x[e] * (double)iq2xs_weight(blk, e);
+                dot += (double)(float)bd;
+            }
+            out[(size_t)s * rows + r] = (float)dot;
+        }
+}
+
 int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t rows,
               uint32_t cols, float *out) {
     if (!shape_ok(type, cols)) return -1;
+    if (type == OC_TYPE_IQ2_XS) {
+        matmul_iq2xs(W, X, S, rows, cols, out);
+        return 0;
+    }
     act_t a;
     if (quantize_acts(type, X, S, cols, &a)) return -1;
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type), nb = cols / bs;
@@ -1269,6 +1318,63 @@ void oc_encode_iq2s_block(const float *x, uint8_t *out) {
     }
 }
 
+/* IQ2_XS weight encoder (the reference ships none; this build defines it).
+ * Scales as IQ2_S (per 16: s = max|x|/43, d = 8 max s / 31 fp16 RNE, ls =
+ * clamp(rne((8s/d - 1)/2), 0, 15)); per 8: the negative signs with the
+ * smallest-|x| one flipped on odd count (the format implies even parity) and
+ * the codebook entry (of 512) nearest |x|/db in squared error (first wins);
+ * qs16 = index | (signs & 127) << 9, as include/GGMLDequantize.hpp:1245-1271
+ * reads them. */
+void oc_encode_iq2xs_block(const float *x, uint8_t *out) {
+    float sc[16], smax = 0.0f;
+    for (int c = 0; c < 16; ++c) {
+        float amax = 0.0f;
+        for (int i = 0; i < 16; ++i) amax = fabsf(x[16 * c + i]) > amax ? fabsf(x[16 * c + i]) : amax;
+        sc[c] = amax / 43.0f;
+        smax = sc[c] > smax ? sc[c] : smax;
+    }
+    memset(out, 0, 74);
+    const uint16_t hd = f2h_rne(8.0f * smax / 31.0f);
+    const float d = oc_half_to_float(hd);
+    if (d == 0.0f) return;
+    memcpy(out, &hd, 2);
+    for (int c = 0; c < 16; ++c) {
+        const int ib = c >> 1, h = c & 1;
+        int ls = (int)lrintf((8.0f * sc[c] / d - 1.0f) / 2.0f);
+        ls = ls < 0 ? 0 : (ls > 15 ? 15 : ls);
+        out[66 + ib] |= (uint8_t)(ls << (4 * h));
+        const float db = d * (0.5f + (float)ls) * 0.25f;
+        for (int q = 0; q < 2; ++q) {
+            const int l = 2 * h + q;
+            const float *xv = x + 32 * ib + 8 * l;
+            uint32_t neg = 0;
+            int minj = 0;
+            float t[8];
+            for (int j = 0; j < 8; ++j) {
+                if (xv[j] < 0.0f) neg |= 1u << j;
+                if (fabsf(xv[j]) < fabsf(xv[minj])) minj = j;
+                t[j] = fabsf(xv[j]) / db;
+            }
+            if (__builtin_popcount(neg) & 1) neg ^= 1u << minj;
+            int best = 0;
+            float berr = 0.0f;
+            for (int gi = 0; gi < 512; ++gi) {
+                float err = 0.0f;
+                for (int j = 0; j < 8; ++j) {
+                    const float diff = (float)((k_iq2xs_grid[gi] >> (8 * j)) & 0xFFu) - t[j];
+                    err = err + diff * diff;
+                }
+                if (gi == 0 || err < berr) {
+                    berr = err;
+                    best = gi;
+                }
+            }
+            const uint16_t qv = (uint16_t)(best | ((neg & 127u) << 9));
+            memcpy(out + 2 + 2 * (4 * ib + l), &qv, 2);
+        }
+    }
+}
+
 void oc_encode_iq3xxs_block(const float *x, uint8_t *out) {
     float sc[8], smax = 0.0f;
     for (int c = 0; c < 8; ++c) {
@@ -1338,6 +1444,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
             case OC_TYPE_Q6_K: oc_encode_q6k_block(xb, o); break;
             case OC_TYPE_IQ3_S: oc_encode_iq3s_block(xb, o); break;
             case OC_TYPE_IQ2_S: oc_encode_iq2s_block(xb, o); break;
+            case OC_TYPE_IQ2_XS: oc_encode_iq2xs_block(xb, o); break;
             default: oc_encode_iq3xxs_block(xb, o); break;
         }
     }

@@ -18,12 +18,13 @@
  *   oc_dequant_row  pinned: golden vectors + closed forms on hand-built blocks.
  *   oc_block_isums  pinned: brute-force integer dot of dequantized integer
  *       weights x quantized activations (order-free integer identity).
- *   oc_matmul (Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K/IQ3_XXS/IQ3_S/IQ2_S)  pinned: bit-exact against
+ *   oc_matmul (Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K/IQ3_XXS/IQ3_S/IQ2_S/IQ2_XS)  pinned: bit-exact against
  *       golden outputs of the compiled reference AVX2 / scalar kernels.
  *   oc_encode_q4k_block  pinned: bit-exact against the compiled reference
  *       quantizeQ4KBlock (golden) + the reference's own round-trip test.
  *   oc_encode_q8_0_block / oc_encode_q2k_block / oc_encode_q3k_block / oc_encode_q5k_block / oc_encode_q6k_block /
- *   oc_encode_iq3xxs_block / oc_encode_iq3s_block / oc_encode_iq2s_block:
+ *   oc_encode_iq3xxs_block / oc_encode_iq3s_block / oc_encode_iq2s_block /
+ *   oc_encode_iq2xs_block:
  *       the reference has no encoder for these formats (this build defines
  *       them); pinned by decode round-trip error bounds only.
  *   oc_moe_ffn  pinned: composed of the pinned pieces; golden vectors from the
@@ -45,6 +46,7 @@ enum {
     OC_TYPE_Q4_K = 12,
     OC_TYPE_Q5_K = 13,
     OC_TYPE_Q6_K = 14,
+    OC_TYPE_IQ2_XS = 17,
     OC_TYPE_IQ3_XXS = 18,
     OC_TYPE_IQ3_S = 21,
     OC_TYPE_IQ2_S = 22,
@@ -69,7 +71,8 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out);
 /* Per-block integer dot sums of W[rows][cols] against the quantized activations
  * of X[S][cols]. Output layout [S][rows][nblk][k]: k = 8 sub-block sums for
  * Q4_K and Q5_K, k = 2 (main, min) for Q2_K, k = 1 otherwise (Q8_0 blocks
- * are the 32-wide ones). */
+ * are the 32-wide ones; IQ2_XS, whose CPU path does not quantize x, has none:
+ * -1). */
 int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                    uint32_t rows, uint32_t cols, int32_t *isums);
 
@@ -88,6 +91,7 @@ void oc_encode_q6k_block(const float *x, uint8_t *out);
 void oc_encode_iq3xxs_block(const float *x, uint8_t *out);
 void oc_encode_iq3s_block(const float *x, uint8_t *out);
 void oc_encode_iq2s_block(const float *x, uint8_t *out);
+void oc_encode_iq2xs_block(const float *x, uint8_t *out);
 int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8_t *out);
 
 /* MoE expert FFN (Q4_K experts), rank-order reduction.

@@ -57,6 +57,7 @@ void ref_dequant_block(int type, const uint8_t *blk, float *out) {
         case 18: GGMLDequantize::dequantizeIQ3_XXSBlock(blk, out); break;
         case 21: GGMLDequantize::dequantizeIQ3_SBlock(blk, out); break;  // include/GGMLDequantize.hpp:1164
         case 22: GGMLDequantize::dequantizeIQ2_SBlock(blk, out); break;  // include/GGMLDequantize.hpp:1215
+        case 17: GGMLDequantize::dequantizeIQ2_XSBlock(blk, out); break;  // include/GGMLDequantize.hpp:1245
         default: break;
     }
 }
@@ -103,6 +104,22 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
         case 22:
             GGMLDequantize::matMulVecBatchQ8K(GGML_TYPE_IQ2_S, W, X, seqLen, rows, cols, out);
             return 0;
+        // IQ2_XS has no Q8_K dot: the float fused path, whose row loop
+        // (include/GGMLDequantize.hpp:2449-2461: double sum of the per-block
+        // float dots, one float conversion per row) is composed here around
+        // the reference's own block dot dotProductIQ2_XS (:1901-1927).
+        // (matMulVecFused itself links a helper of SIMDMatMulVec.cpp, which
+        // does not build here; that helper serves partial blocks only.)
+        case 17:
+            for (uint32_t s = 0; s < seqLen; ++s)
+                for (uint32_t j = 0; j < rows; ++j) {
+                    double dot = 0.0;
+                    for (uint32_t b = 0; b < cols / 256; ++b)
+                        dot += static_cast<double>(GGMLDequantize::dotProductIQ2_XS(
+                            W + (size_t(j) * (cols / 256) + b) * 74, X + size_t(s) * cols + size_t(b) * 256));
+                    out[size_t(s) * rows + j] = static_cast<float>(dot);
+                }
+            return 0;
         default: return -1;
     }
 }
@@ -112,6 +129,8 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
 void ref_iq3s_grid(uint32_t *out) { std::memcpy(out, GGMLDequantize::IQ3S_GRID, 512 * sizeof(uint32_t)); }
 // The IQ2_S codebook (include/GGMLDequantize.hpp:807, 1024 x 8 bytes), likewise.
 void ref_iq2s_grid(uint64_t *out) { std::memcpy(out, GGMLDequantize::IQ2S_GRID, 1024 * sizeof(uint64_t)); }
+// The IQ2_XS codebook (include/GGMLDequantize.hpp:821, 512 x 8 bytes), likewise.
+void ref_iq2xs_grid(uint64_t *out) { std::memcpy(out, GGMLDequantize::iq2xs_grid, 512 * sizeof(uint64_t)); }
 
 // ---- GGUF reader (include/GGUFLoader.hpp:48) ---------------------------------
 // A loader handle; load() or loadMetadata() per `metadata_only`. NULL on failure.

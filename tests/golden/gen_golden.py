@@ -104,6 +104,14 @@ def q2k_random_blocks(rng, nblk):
     return b.ravel()
 
 
+def iq2xs_random_blocks(rng, nblk):
+    """Random IQ2_XS bytes (every codebook index, sign index and scale nibble)
+    with a fixed normal fp16 d."""
+    b = rng.integers(0, 256, (nblk, 74), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(np.float16(0.0011).tobytes(), np.uint8)
+    return b.ravel()
+
+
 def q80_random_blocks(rng, nblk):
     b = rng.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
     d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-10, -6, nblk)).astype(np.float16)
@@ -327,6 +335,23 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.Q2_K, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.Q2_K, w, X4, rows, cols)
+
+    # IQ2_XS, likewise (float path: unquantized x, double sums), and the
+    # codebook digest.
+    rx = np.random.default_rng(20261207)
+    gridx = np.zeros(512, np.uint64)
+    ref.lib.ref_iq2xs_grid(ctypes.c_void_p(gridx.ctypes.data))
+    g["iq2xs_grid_sha256"] = np.frombuffer(hashlib.sha256(gridx.tobytes()).digest(), np.uint8)
+    g["deq_iq2xs_w"] = iq2xs_random_blocks(rx, 8)
+    g["deq_iq2xs_y"] = ref.dequant(O.IQ2_XS, g["deq_iq2xs_w"], 8, 256)
+    casesx = {
+        "iq2xs_rand": iq2xs_random_blocks(rx, rows * nb),
+        "iq2xs_enc002": O.Oracle().encode(O.IQ2_XS, (rx.standard_normal((rows, cols)) * 0.02).astype(np.float32)),
+    }
+    for name, w in casesx.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.IQ2_XS, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.IQ2_XS, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")

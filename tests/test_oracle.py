@@ -105,7 +105,7 @@ def test_quantize_q8_0_act_pinned_by_reference_probe(oracle, golden):
 # ---- block decoders ---------------------------------------------------------------
 
 @pytest.mark.parametrize("name,qt", [("q2k", O.Q2_K), ("q3k", O.Q3_K), ("q4k", O.Q4_K), ("q5k", O.Q5_K), ("q6k", O.Q6_K), ("iq3", O.IQ3_XXS),
-                                     ("iq3s", O.IQ3_S), ("iq2s", O.IQ2_S),
+                                     ("iq3s", O.IQ3_S), ("iq2s", O.IQ2_S), ("iq2xs", O.IQ2_XS),
                                      ("q80", O.Q8_0)])
 def test_dequant_matches_reference(oracle, golden, name, qt):
     w = golden[f"deq_{name}_w"]
@@ -275,7 +275,8 @@ def test_block_isums_identity(oracle, qt):
 MM = [("q4k_rand", O.Q4_K), ("q4k_enc1", O.Q4_K), ("q4k_enc002", O.Q4_K), ("q5k_rand", O.Q5_K),
       ("q5k_enc1", O.Q5_K), ("q3k_rand", O.Q3_K), ("q3k_enc002", O.Q3_K), ("q2k_rand", O.Q2_K),
       ("q2k_enc002", O.Q2_K), ("iq3s_rand", O.IQ3_S),
-      ("iq3s_enc002", O.IQ3_S), ("iq2s_rand", O.IQ2_S), ("iq2s_enc002", O.IQ2_S), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
+      ("iq3s_enc002", O.IQ3_S), ("iq2s_rand", O.IQ2_S), ("iq2s_enc002", O.IQ2_S),
+      ("iq2xs_rand", O.IQ2_XS), ("iq2xs_enc002", O.IQ2_XS), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
 
 
 @pytest.mark.parametrize("name,qt", MM)
@@ -293,7 +294,8 @@ def test_matmul_q80_cols96(oracle, golden):
     assert (bits(got) == bits(golden["mm_q80c96_y"])).all()
 
 
-@pytest.mark.parametrize("qt", [O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S])
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S,
+                                O.IQ2_XS])
 def test_matmul_close_to_float_dot(oracle, qt):
     """Independent of the reference: the quantized mat-vec approximates the
     float product of the dequantized weights with x (activation quantization
@@ -351,9 +353,10 @@ def test_q4k_encoder_reference_roundtrip_thresholds(oracle):
 
 
 @pytest.mark.parametrize("qt,bound", [(O.Q8_0, 0.01), (O.Q2_K, 0.45), (O.Q3_K, 0.2), (O.Q5_K, 0.08), (O.Q6_K, 0.04),
-                                      (O.IQ3_XXS, 0.25), (O.IQ3_S, 0.2), (O.IQ2_S, 0.35)])
+                                      (O.IQ3_XXS, 0.25), (O.IQ3_S, 0.2), (O.IQ2_S, 0.35),
+                                      (O.IQ2_XS, 0.4)])
 def test_own_encoders_roundtrip(oracle, qt, bound):
-    """This build's Q8_0 / Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S encoders (the reference has none):
+    """This build's Q8_0 / Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS encoders (the reference has none):
     N(0, 0.02) rows round-trip within the format's expected relative RMS."""
     rng = np.random.default_rng(9)
     x = (rng.standard_normal((16, 1024)) * 0.02).astype(np.float32)
@@ -385,6 +388,25 @@ def test_iq3s_grid_tables_match_reference(golden):
         # format facts: odd magnitudes 1..15 in every byte
         b = np.array(vals, np.uint32).view(np.uint8)
         assert ((b % 2 == 1) & (b <= 15)).all()
+
+
+def test_iq2xs_float_path_and_grid(oracle, golden):
+    """IQ2_XS: no integer sums (the reference's CPU path dots unquantized x);
+    its codebook tables match the reference digest; every 8-group of an
+    encoded block has an even number of negative weights (format rule)."""
+    w = golden["mm_iq2xs_rand_w"]
+    with pytest.raises(AssertionError):
+        oracle.block_isums(O.IQ2_XS, w, golden["mm_x1"], len(w) // 74 // (golden["mm_x1"].shape[1] // 256),
+                           golden["mm_x1"].shape[1])
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for path in ("oracle/iq2xs_grid.inc", "tinycoder-inference_amd/csrc/iq2xs_grid.inc"):
+        text = open(os.path.join(root, path)).read()
+        arr = np.array([int(t, 16) for t in __import__("re").findall(r"0x([0-9a-f]{16})ull", text)], np.uint64)
+        assert len(arr) == 512
+        assert hashlib.sha256(arr.tobytes()).digest() == golden["iq2xs_grid_sha256"].tobytes(), path
+    x = np.random.default_rng(4).standard_normal((4, 256)).astype(np.float32)
+    y = oracle.dequant(O.IQ2_XS, oracle.encode(O.IQ2_XS, x), 4, 256)
+    assert ((y < 0).reshape(4, 32, 8).sum(2) % 2 == 0).all()
 
 
 def test_iq2s_grid_tables_match_reference(golden):
