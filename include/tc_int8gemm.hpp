@@ -31,7 +31,7 @@ inline bool ok(int rc) {
 inline bool int8GemmAvailable() { return tc_available() != 0; }
 
 /// out[seqLen][rows] = x[seqLen][cols] @ W[rows][cols]^T on the int8 matrix
-/// cores (Q4_K, Q8_0) or the exact batched mat-vec (Q2_K, Q3_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S)
+/// cores (Q4_K, Q8_0) or the exact batched mat-vec (Q2_K, Q3_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS)
 /// (reference int8Gemm, Int8Gemm.hpp:57-59).
 inline bool int8Gemm(int type, const void *w, const float *x, float *out, uint32_t seqLen, uint32_t rows,
                      uint32_t cols, uint32_t blocksPerRow, void *stream) {
@@ -70,11 +70,11 @@ inline bool int8GemvDualQ4K(const void *wg, const void *wu, const float *x, floa
     return detail::ok(tc_gemv_dual(TC_Q4_K, wg, wu, x, gout, uout, rows, cols, stream));
 }
 
-/// IQ2_XS is outside this library's formats: false, so the caller falls back
-/// (reference int8GemvDualIQ2XS, Int8Gemm.hpp:99).
-inline bool int8GemvDualIQ2XS(const void *, const void *, const float *, float *, float *, uint32_t, uint32_t,
-                              void *) {
-    return false;
+/// IQ2_XS gate/up pair (reference int8GemvDualIQ2XS, Int8Gemm.hpp:99), on
+/// fp32 activations as the reference CPU path for IQ2_XS computes it.
+inline bool int8GemvDualIQ2XS(const void *wg, const void *wu, const float *x, float *gout, float *uout,
+                              uint32_t rows, uint32_t cols, void *stream) {
+    return detail::ok(tc_gemv_dual(TC_IQ2_XS, wg, wu, x, gout, uout, rows, cols, stream));
 }
 
 }  // namespace tinycoder::gpu

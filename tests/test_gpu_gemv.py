@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from qdata import ALL, IQ2_S, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
+from qdata import ALL, INT8_ACT, IQ2_S, IQ2_XS, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -62,7 +62,7 @@ def test_quantize_act_probe_golden(tc, dev, golden):
 
 # ---- per-block integer sums ---------------------------------------------------------
 
-@pytest.mark.parametrize("qt", ALL)
+@pytest.mark.parametrize("qt", INT8_ACT)
 @pytest.mark.parametrize("S,rows,cols", [(1, 37, 512), (3, 130, 1024), (8, 9, 3584), (1, 5, 18944)])
 def test_block_isums_bit_exact(tc, dev, oracle, qt, S, rows, cols):
     rng = np.random.default_rng(rows * 31 + qt)
@@ -79,6 +79,7 @@ def test_block_isums_bit_exact(tc, dev, oracle, qt, S, rows, cols):
 MM = [("q4k_rand", Q4_K), ("q4k_enc1", Q4_K), ("q4k_enc002", Q4_K),
       ("q5k_rand", Q5_K), ("q5k_enc1", Q5_K), ("q3k_rand", Q3_K), ("q3k_enc002", Q3_K), ("q2k_rand", Q2_K), ("q2k_enc002", Q2_K), ("iq3s_rand", IQ3_S),
       ("iq3s_enc002", IQ3_S), ("iq2s_rand", IQ2_S), ("iq2s_enc002", IQ2_S),
+      ("iq2xs_rand", IQ2_XS), ("iq2xs_enc002", IQ2_XS),
       ("q6k_rand", Q6_K), ("iq3_rand", IQ3_XXS), ("q80_rand", Q8_0)]
 
 
@@ -121,7 +122,7 @@ def test_gemv_vs_oracle(tc, dev, oracle, qt, S):
 
 @pytest.mark.parametrize("qt,rows,cols", [
     (Q4_K, 3584, 3584), (Q4_K, 512, 3584), (Q4_K, 18944, 3584), (Q4_K, 3584, 18944),
-    (Q8_0, 4096, 4096), (Q6_K, 3584, 18944), (IQ3_XXS, 18944, 3584), (Q5_K, 18944, 3584), (Q3_K, 3584, 18944), (IQ3_S, 18944, 3584), (IQ2_S, 3584, 18944), (Q2_K, 18944, 3584),
+    (Q8_0, 4096, 4096), (Q6_K, 3584, 18944), (IQ3_XXS, 18944, 3584), (Q5_K, 18944, 3584), (Q3_K, 3584, 18944), (IQ3_S, 18944, 3584), (IQ2_S, 3584, 18944), (Q2_K, 18944, 3584), (IQ2_XS, 18944, 3584),
 ])
 def test_gemv_full_shapes(tc, dev, oracle, qt, rows, cols):
     """BASELINE shapes at full size, weights from the GPU encoder on N(0,0.02)
@@ -238,7 +239,7 @@ def test_gemv_dual_swiglu(tc, dev, oracle, qt):
     assert (err <= bound).all(), float((err / bound).max())
 
 
-@pytest.mark.parametrize("qt", ALL)
+@pytest.mark.parametrize("qt", INT8_ACT)
 def test_gemv_prequantized_equals_fused(tc, dev, qt):
     """tc_act_quantize + tc_gemv_q8 (the reference's launchQGemvQ81 shape)
     gives bit-identical results to tc_gemv, which quantizes in-kernel."""
@@ -256,7 +257,7 @@ def test_gemv_prequantized_equals_fused(tc, dev, qt):
 # ---- parity hooks (reference GPUModel::debugQ8KRow / debugQ8_0Row / debugQ8KBlocks /
 # debugQ8_0Blocks, include/GPUCompute.hpp:399-460) -----------------------------------------------
 
-@pytest.mark.parametrize("qt", ALL)
+@pytest.mark.parametrize("qt", INT8_ACT)
 def test_debug_row_hook(tc, dev, oracle, qt):
     rng = np.random.default_rng(400 + qt)
     cols = 2048
@@ -271,7 +272,7 @@ def test_debug_row_hook(tc, dev, oracle, qt):
         assert ok, worst
 
 
-@pytest.mark.parametrize("qt", ALL)
+@pytest.mark.parametrize("qt", INT8_ACT)
 def test_debug_blocks_hook(tc, dev, oracle, qt):
     rng = np.random.default_rng(500 + qt)
     cols = 1536
@@ -311,3 +312,23 @@ def test_debug_blocks_hook(tc, dev, oracle, qt):
                 wz[k, :2] = 0
         ok, worst = close(blk[b], oracle.matmul(qt, wz.ravel(), x, 1, cols)[0, 0])
         assert ok, (b, worst)
+
+
+def test_iq2xs_refuses_quantized_activation_entry_points(tc, dev):
+    """IQ2_XS dots fp32 x (as its reference CPU path): the entry points that
+    hand over quantized activations refuse it without writing."""
+    import ctypes
+    import torch
+    from tc_hip import TC_E_UNSUPPORTED, _ptr
+    w = torch.zeros(74 * 2, dtype=torch.uint8, device=dev)
+    x = torch.zeros((1, 256), device=dev)
+    buf = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    out = torch.full((1, 2), 7.0, device=dev)
+    assert tc.lib.tc_act_bytes(IQ2_XS, 1, 256) == 0
+    assert tc.lib.tc_act_quantize(IQ2_XS, _ptr(x), 1, 256, _ptr(buf), None) == TC_E_UNSUPPORTED
+    assert tc.lib.tc_gemv_q8(IQ2_XS, _ptr(w), _ptr(buf), _ptr(out), 1, 2, 256, None) == TC_E_UNSUPPORTED
+    isums = torch.zeros(16, dtype=torch.int32, device=dev)
+    assert tc.lib.tc_block_isums(IQ2_XS, _ptr(w), _ptr(x), _ptr(isums), 1, 2, 256, None) == TC_E_UNSUPPORTED
+    torch.cuda.synchronize()
+    assert (out.cpu() == 7.0).all()
+    del ctypes

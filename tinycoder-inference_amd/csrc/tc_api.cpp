@@ -86,7 +86,11 @@ bool ensure(void *&p, size_t &cap, size_t need) {
 // touch: one 128-token tile of 256-byte rows.
 constexpr size_t kGemmActSlack = 128 * 256;
 
-bool type_ok(int t) { return t == TC_Q8_0 || t == TC_Q2_K || t == TC_IQ2_S || t == TC_IQ3_S || t == TC_Q3_K || t == TC_Q4_K || t == TC_Q5_K || t == TC_Q6_K || t == TC_IQ3_XXS; }
+// IQ2_XS takes fp32 activations (its reference CPU path does not quantize x):
+// the entry points that hand over quantized activations refuse it.
+bool int8_act_type(int t) { return t != TC_IQ2_XS; }
+
+bool type_ok(int t) { return t == TC_Q8_0 || t == TC_IQ2_XS || t == TC_Q2_K || t == TC_IQ2_S || t == TC_IQ3_S || t == TC_Q3_K || t == TC_Q4_K || t == TC_Q5_K || t == TC_Q6_K || t == TC_IQ3_XXS; }
 
 bool g_q8_gemm_enabled = true;
 
@@ -235,7 +239,7 @@ int tc_gemv_multi(int type, uint32_t n, const void *const *w, const float *const
 }
 
 size_t tc_act_bytes(int type, uint32_t seq_len, uint32_t cols) {
-    if (!type_ok(type) || cols % 256) return 0;
+    if (!type_ok(type) || !int8_act_type(type) || cols % 256) return 0;
     return tc::act_layout(type, seq_len, cols).bytes;
 }
 
@@ -243,6 +247,7 @@ int tc_act_quantize(int type, const float *x, uint32_t seq_len, uint32_t cols, v
     if (!device()) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
     int rc = check_common(type, act, x, act, seq_len, 1, cols);
     if (rc) return rc;
+    if (!int8_act_type(type)) return fail(TC_E_UNSUPPORTED, "type %d takes fp32 activations", type);
     if (reinterpret_cast<uintptr_t>(act) & 255) return fail(TC_E_ARG, "act must be 256-byte aligned");
     const tc::ActLayout L = tc::act_layout(type, seq_len, cols);
     hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, act, static_cast<hipStream_t>(stream));
@@ -257,6 +262,7 @@ int tc_gemv_q8(int type, const void *w, const void *act, float *out, uint32_t se
     int rc = check_common(type, w, act, out, seq_len, rows, cols);
     if (rc) return rc;
     if (seq_len > 8) return fail(TC_E_UNSUPPORTED, "seq_len=%u > 8 (use tc_gemm)", seq_len);
+    if (!int8_act_type(type)) return fail(TC_E_UNSUPPORTED, "type %d takes fp32 activations", type);
     if (reinterpret_cast<uintptr_t>(act) & 255) return fail(TC_E_ARG, "act must be 256-byte aligned");
     return run_gemv(dev, type, w, nullptr, nullptr, act, out, nullptr, 0, nullptr, seq_len, rows, cols,
                     static_cast<hipStream_t>(stream));
@@ -334,6 +340,7 @@ int tc_quantize_act(int type, const float *x, uint32_t seq_len, uint32_t cols, i
     Device *dev = device();
     if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
     if (!type_ok(type)) return fail(TC_E_UNSUPPORTED, "unsupported type %d", type);
+    if (!int8_act_type(type)) return fail(TC_E_UNSUPPORTED, "type %d takes fp32 activations", type);
     if (!x || !qs || !d || (type != TC_Q8_0 && !bsums)) return fail(TC_E_ARG, "null pointer");
     const uint32_t blk = type == TC_Q8_0 ? 32 : 256;
     if (seq_len == 0 || cols == 0 || cols % blk) return fail(TC_E_UNSUPPORTED, "cols=%u", cols);
@@ -358,6 +365,7 @@ int tc_block_isums(int type, const void *w, const float *x, int32_t *isums, uint
     if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
     int rc = check_common(type, w, x, isums, seq_len, rows, cols);
     if (rc) return rc;
+    if (!int8_act_type(type)) return fail(TC_E_UNSUPPORTED, "type %d has no integer block sums (fp32 path)", type);
     hipStream_t st = static_cast<hipStream_t>(stream);
     // The decode kernel writes the integer sums as a side output; its fp32
     // results land in a scratch row buffer.
@@ -624,7 +632,8 @@ int debug_quant(int type, const float *x_host, uint32_t cols, uint8_t *out_quant
 
 int tc_debug_q8k_row(int type, const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
                      float *result) {
-    if (type == TC_Q8_0 || !type_ok(type)) return fail(TC_E_UNSUPPORTED, "type %d is not a Q8_K-activation type", type);
+    if (type == TC_Q8_0 || !type_ok(type) || !int8_act_type(type))
+        return fail(TC_E_UNSUPPORTED, "type %d is not a Q8_K-activation type", type);
     if (!w_row || !x || !result) return fail(TC_E_ARG, "null pointer");
     if (cols % 256 || blocks_per_row != cols / 256) return fail(TC_E_ARG, "blocks_per_row/cols mismatch");
     return debug_rows(type, w_row, 1, x, cols, result);

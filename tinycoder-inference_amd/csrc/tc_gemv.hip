@@ -44,6 +44,9 @@ __constant__ uint32_t c_grid_s[512] = {
 __constant__ uint64_t c_grid_2s[1024] = {
 #include "iq2s_grid.inc"
 };
+__constant__ uint64_t c_grid_2xs[512] = {
+#include "iq2xs_grid.inc"
+};
 
 constexpr int NT = 512;
 constexpr int kUnitsPerPass = NT / 4;
@@ -556,6 +559,12 @@ struct CfgSmall {
 constexpr int kTileUnits = 64;
 constexpr uint32_t XB = 304;                // LDS bytes per 256-element activation block
 constexpr uint32_t XB_BS = 256, XB_D = 288;  // bsums and d offsets inside a record
+// LDS bytes per 256-element activation block: the Q8_K / Q8_0 record, or the
+// unquantized fp32 values for IQ2_XS (whose reference CPU path dots fp32 x),
+// padded to 1072 bytes: the lanes of a wave read the records of consecutive
+// blocks, and a 1024-byte stride would put them all in the same LDS banks
+// (1072 = 48 mod 256, the residue of the conflict-free 304-byte record).
+__host__ __device__ constexpr uint32_t xrec_bytes(int type) { return type == kIQ2_XS ? 1072u : XB; }
 
 // 16-byte loads per lane per tile (the last one partial for Q6_K / IQ3_XXS,
 // whose 64-unit tiles are 13440 / 6272 bytes) and the LDS bytes of one tile.
@@ -806,6 +815,27 @@ template <int TYPE, int S, int TNT>
 __device__ __forceinline__ void tstage_finish(const TJobDev &jb, const XRsrc &rs, const XPre &p, unsigned char *xr) {
     const uint32_t tid = threadIdx.x;
     const uint32_t nblk = jb.nx * (jb.cols / 256);
+    if constexpr (TYPE == kIQ2_XS) {
+        // fp32 x as it is: 64-byte chunk c (16 floats) of block c/16 into that
+        // block's record
+        const uint32_t nchunk = nblk * 16;
+        auto dst = [&](uint32_t c) __attribute__((always_inline)) {
+            return xr + size_t(c / 16) * xrec_bytes(TYPE) + 64 * (c & 15);
+        };
+        static_for<0, kXPre>([&](auto i) __attribute__((always_inline)) {
+            const uint32_t c = tid + i.value * TNT;
+            if (c < nchunk)
+                static_for<0, 4>([&](auto q) __attribute__((always_inline)) {
+                    *reinterpret_cast<u32x4 *>(dst(c) + 16 * decltype(q)::value) = reg<4 * i.value + decltype(q)::value>(p.r);
+                });
+        });
+        for (uint32_t c = tid + kXPre * TNT; c < nchunk; c += TNT)
+            static_for<0, 4>([&](auto q) __attribute__((always_inline)) {
+                *reinterpret_cast<u32x4 *>(dst(c) + 16 * decltype(q)::value) =
+                    __builtin_amdgcn_raw_buffer_load_b128(rs.a, c * 64u + 16u * decltype(q)::value, 0, 0);
+            });
+        return;
+    }
     if (jb.x != nullptr) {
         const uint32_t nchunk = nblk * 16;
         static_for<0, kXPre>([&](auto i) __attribute__((always_inline)) {
@@ -1388,6 +1418,66 @@ struct TDot<kIQ2_S, S> {
     }
 };
 
+// IQ2_XS, one unit (74 B, 2-byte aligned in LDS) per lane, on fp32 x (the
+// reference's CPU path for this type, dotProductIQ2_XS, dots unquantized x;
+// include/GGMLDequantize.hpp:1901-1927): per 8 weights one 16-bit entry --
+// codebook index (bits 0-8, 512 x 8 bytes in LDS) and a 7-bit sign index whose
+// 8th sign is its parity --, weight = ((d*(0.5+ls))*0.25) * magnitude with the
+// sign applied to the float's sign bit; the scale is applied once per 8
+// weights (value = sum of dl * sum_8 x * signed magnitude), which rounds
+// differently from the reference's per-weight products only in fp32 order.
+template <int S>
+struct TDot<kIQ2_XS, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               const uint32_t *grid, float *val, int32_t *dbg, size_t dbg_tok) {
+        (void)dbg;
+        (void)dbg_tok;
+        const uint16_t *u16 = reinterpret_cast<const uint16_t *>(u);
+        const float d = h2f(u16[0]);
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[s] = 0.0f;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            const uint32_t scb = (uint32_t(u16[33 + ib / 2]) >> (8 * (ib & 1))) & 0xFFu;
+            const float dl0 = d * (0.5f + float(scb & 15u)) * 0.25f;
+            const float dl1 = d * (0.5f + float(scb >> 4)) * 0.25f;
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t q = u16[1 + 4 * ib + l];
+                const uint32_t si = q >> 9;
+                const uint32_t sg = si | ((__builtin_popcount(si) & 1u) << 7);
+                const uint32_t g0 = grid[2 * (q & 511u)], g1 = grid[2 * (q & 511u) + 1];
+                const float dl = l < 2 ? dl0 : dl1;
+                // signed magnitudes (the scale dl is applied once per 8 weights)
+                float w[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t gb = ((j < 4 ? g0 : g1) >> (8 * (j & 3))) & 0xFFu;
+                    w[j] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, float(gb)) ^ (((sg >> j) & 1u) << 31));
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const float *xp = reinterpret_cast<const float *>(xr0 + s * xtok) + 32 * ib + 8 * l;
+                    const float4 xa = *reinterpret_cast<const float4 *>(xp);
+                    const float4 xb = *reinterpret_cast<const float4 *>(xp + 4);
+                    float p = xa.x * w[0];
+                    p = fmaf(xa.y, w[1], p);
+                    p = fmaf(xa.z, w[2], p);
+                    p = fmaf(xa.w, w[3], p);
+                    p = fmaf(xb.x, w[4], p);
+                    p = fmaf(xb.y, w[5], p);
+                    p = fmaf(xb.z, w[6], p);
+                    p = fmaf(xb.w, w[7], p);
+                    acc[s] = fmaf(dl, p, acc[s]);
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) val[s] = acc[s];
+    }
+};
+
 template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
@@ -1450,7 +1540,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     const size_t nbr = TYPE == kQ8_0 ? jb.cols / 32 : jb.cols / 256;
     const size_t per = TYPE == kQ4_K || TYPE == kQ5_K ? 8 : TYPE == kQ2_K ? 2 : 1;
     const size_t dbg_tok = size_t(jb.rows) * nbr * per;
-    const size_t xtok = size_t(nu) * XB;
+    const size_t xtok = size_t(nu) * xrec_bytes(TYPE);
     // Expert of rank m (rank-group mode; m is wave-uniform).
     auto rank_expert = [&](uint32_t m) __attribute__((always_inline)) {
         int32_t e = reid[0];
@@ -1559,6 +1649,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         uint64_t *sg = reinterpret_cast<uint64_t *>(smem + L.off_g);
         for (uint32_t i = tid; i < 1024; i += TNT) sg[i] = c_grid_2s[i];
     }
+    if constexpr (TYPE == kIQ2_XS) {
+        uint64_t *sg = reinterpret_cast<uint64_t *>(smem + L.off_g);
+        for (uint32_t i = tid; i < 512; i += TNT) sg[i] = c_grid_2xs[i];
+    }
     TC_TRACE_PT(4);
     tstage_finish<TYPE, S, TNT>(jb, xrs, xp, xr);
     TC_TRACE_PT(5);
@@ -1597,8 +1691,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
                         dbg = jb.dbg + (size_t(r0 + rl) * nbr + (TYPE == kQ8_0 ? size_t(b) * 8 : b)) * per;
                     float val[S];
                     // rank-group mode: tile of rank m against that rank's activations (S == 1)
-                    const unsigned char *xb = xr + (RG ? size_t(m) * xtok : 0) + size_t(b) * XB;
-                    if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S || TYPE == kIQ2_S)
+                    const unsigned char *xb = xr + (RG ? size_t(m) * xtok : 0) + size_t(b) * xrec_bytes(TYPE);
+                    if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S || TYPE == kIQ2_S || TYPE == kIQ2_XS)
                         TDot<TYPE, S>::run(tile + lane * UB, xb, xtok,
                                            reinterpret_cast<const uint32_t *>(smem + L.off_g), val, dbg, dbg_tok);
                     else
@@ -1761,18 +1855,19 @@ constexpr uint64_t kBigBytes = 24ull << 20;
 
 template <class C>
 uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
-    uint32_t o = S * (cols / 256) * XB;
+    uint32_t o = S * (cols / 256) * xrec_bytes(type);
     a->off_g = o;
     if (type == kIQ3_XXS) o += 16384;  // signed grid, 256 x 16 words
     if (type == kIQ3_S) o += 2048;     // IQ3_S codebook, 512 words
     if (type == kIQ2_S) o += 8192;     // IQ2_S codebook, 1024 x 8 bytes
+    if (type == kIQ2_XS) o += 4096;    // IQ2_XS codebook, 512 x 8 bytes
     a->off_t = o;
     o += (C::NT / 64) * tile_slot_bytes(type);
     a->off_p = o;
     return o;
 }
 
-bool tiled_type(int type) { return type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kIQ2_XS || type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -1836,8 +1931,9 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         // Q2_K / Q3_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S rows are not 16-byte
         // multiples: 8-row groups keep every workgroup's first row 16-byte
         // aligned (8*84, 8*110, 8*210, 8*98 and 8*82 bytes per 256 columns
-        // are multiples of 16).
-        if ((type == kQ2_K || type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S || type == kIQ2_S) &&
+        // are multiples of 16; IQ2_XS: 8*74).
+        if ((type == kQ2_K || type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S || type == kIQ2_S ||
+             type == kIQ2_XS) &&
             rpw < g.rows) {
             rpw = (rpw + 7) / 8 * 8;
             if (rpw > fit) rpw = fit / 8 * 8;
@@ -1858,6 +1954,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         case kIQ3_S: return launch_tiled<kIQ3_S, C>(S, a, wg, lds, st);
         case kIQ2_S: return launch_tiled<kIQ2_S, C>(S, a, wg, lds, st);
         case kQ2_K: return launch_tiled<kQ2_K, C>(S, a, wg, lds, st);
+        case kIQ2_XS: return launch_tiled<kIQ2_XS, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:
@@ -1889,7 +1986,7 @@ hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t
 
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes) {
     // S*cols up to which the tiled kernels preload all of x ahead of the weights
-    if (!tiled_type(type)) return 0xFFFFFFFFu;
+    if (!tiled_type(type) || type == kIQ2_XS) return 0xFFFFFFFFu;  // IQ2_XS: fp32 x, never pre-quantized
     return uint32_t(kXPre) * (use_big(type, weight_bytes) ? CfgBig::NT : CfgSmall::NT) * 16u;
 }
 

@@ -18,6 +18,9 @@ __constant__ uint32_t c_iq3s_grid[512] = {
 __constant__ uint64_t c_iq2s_grid[1024] = {
 #include "iq2s_grid.inc"
 };
+__constant__ uint64_t c_iq2xs_grid[512] = {
+#include "iq2xs_grid.inc"
+};
 
 // ---- activation quantizers ---------------------------------------------------
 
@@ -556,6 +559,64 @@ __device__ void enc_iq2s(const float *x, uint8_t *out) {
     }
 }
 
+// IQ2_XS (this build's encoder; the reference ships none): scales as IQ2_S;
+// per 8 the negative signs with the smallest-|x| one flipped on odd count (the
+// format implies even parity) and the codebook entry (of 512) nearest |x|/db
+// (first wins); entry = index | (signs & 127) << 9, as the reference decoder
+// reads it (include/GGMLDequantize.hpp:1245-1271).
+__device__ void enc_iq2xs(const float *x, uint8_t *out) {
+    float sc[16], smax = 0.0f;
+    for (int c = 0; c < 16; ++c) {
+        float amax = 0.0f;
+        for (int i = 0; i < 16; ++i) amax = fabsf(x[16 * c + i]) > amax ? fabsf(x[16 * c + i]) : amax;
+        sc[c] = __fdiv_rn(amax, 43.0f);
+        smax = sc[c] > smax ? sc[c] : smax;
+    }
+    for (int i = 0; i < 74; ++i) out[i] = 0;
+    const uint16_t hd = f2h_rne(__fdiv_rn(8.0f * smax, 31.0f));
+    const float d = h2f(hd);
+    if (d == 0.0f) return;
+    out[0] = uint8_t(hd);
+    out[1] = uint8_t(hd >> 8);
+    for (int c = 0; c < 16; ++c) {
+        const int ib = c >> 1, h = c & 1;
+        int ls = int(rintf(__fdiv_rn(__fdiv_rn(8.0f * sc[c], d) - 1.0f, 2.0f)));
+        ls = ls < 0 ? 0 : (ls > 15 ? 15 : ls);
+        out[66 + ib] |= uint8_t(ls << (4 * h));
+        const float db = d * (0.5f + float(ls)) * 0.25f;
+        for (int q = 0; q < 2; ++q) {
+            const int l = 2 * h + q;
+            const float *xv = x + 32 * ib + 8 * l;
+            uint32_t neg = 0;
+            int minj = 0;
+            float t[8];
+            for (int j = 0; j < 8; ++j) {
+                if (xv[j] < 0.0f) neg |= 1u << j;
+                if (fabsf(xv[j]) < fabsf(xv[minj])) minj = j;
+                t[j] = __fdiv_rn(fabsf(xv[j]), db);
+            }
+            if (__builtin_popcount(neg) & 1) neg ^= 1u << minj;
+            int best = 0;
+            float berr = 0.0f;
+            for (int gi = 0; gi < 512; ++gi) {
+                const uint64_t gv = c_iq2xs_grid[gi];
+                float err = 0.0f;
+                for (int j = 0; j < 8; ++j) {
+                    const float diff = float(uint32_t(gv >> (8 * j)) & 0xFFu) - t[j];
+                    err = err + diff * diff;
+                }
+                if (gi == 0 || err < berr) {
+                    berr = err;
+                    best = gi;
+                }
+            }
+            const uint32_t qv = uint32_t(best) | ((neg & 127u) << 9);
+            out[2 + 2 * (4 * ib + l)] = uint8_t(qv);
+            out[3 + 2 * (4 * ib + l)] = uint8_t(qv >> 8);
+        }
+    }
+}
+
 __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict__ x, uint8_t *__restrict__ out,
                                                uint32_t nunits) {
     const uint32_t u = blockIdx.x * 64 + threadIdx.x;
@@ -571,6 +632,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
         case kQ6_K: enc_q6k(xu, o); break;
         case kIQ3_S: enc_iq3s(xu, o); break;
         case kIQ2_S: enc_iq2s(xu, o); break;
+        case kIQ2_XS: enc_iq2xs(xu, o); break;
         default: enc_iq3xxs(xu, o); break;
     }
 }
