@@ -42,6 +42,7 @@ uint32_t oc_type_size(int type) {
         case OC_TYPE_IQ3_S: return 110;
         case OC_TYPE_IQ2_S: return 82;
         case OC_TYPE_IQ2_XS: return 74;
+        case OC_TYPE_IQ4_XS: return 136;
         default: return 0;
     }
 }
@@ -310,6 +311,23 @@ static int iq2s_signed(const uint8_t *blk, int e, int *ls_out) {
     return (signs[4 * ib + l] >> j) & 1 ? -mag : mag;
 }
 
+/* IQ4_XS (136 B: d at 0, scales_h (16 bits) at 2, scales_l[4] at 4, qs[128]
+ * at 8): element 32ib + j is kvalues_iq4nl[nibble] with the low nibble of
+ * qs[16ib + j] for j < 16 and the high nibble of qs[16ib + j - 16] above;
+ * sub-block scale ls - 32 with ls = scales_l nibble ib | scales_h bits 2ib
+ * << 4 (include/GGMLDequantize.hpp:1044-1080, table :55-57). */
+static const int8_t k_kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                           1, 13, 25, 38, 53, 69, 89, 113};
+static int iq4xs_value(const uint8_t *blk, int e) {
+    const int ib = e >> 5, j = e & 31;
+    const uint8_t q = blk[8 + 16 * ib + (j & 15)];
+    return k_kvalues_iq4nl[j < 16 ? (q & 0xF) : (q >> 4)];
+}
+static int iq4xs_scale(const uint8_t *blk, int ib) {
+    const int sh = blk[2] | (blk[3] << 8);
+    return (((blk[4 + ib / 2] >> (4 * (ib % 2))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4)) - 32;
+}
+
 /* IQ2_XS (74 B: d, qs16[32] at 2 -- bits 0-8 codebook index, bits 9-15 a
  * 7-bit sign index whose 8th sign is its parity --, scales[8] at 66) float
  * weight of element e = 32ib + 8l + j: dl * grid byte j * sign with dl =
@@ -389,6 +407,10 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
             }
         } else if (type == OC_TYPE_IQ2_XS) {
             for (int e = 0; e < 256; ++e) y[e] = iq2xs_weight(blk, e);
+        } else if (type == OC_TYPE_IQ4_XS) {
+            /* dl = d * (ls - 32) per 32, y = dl * kvalues (:1044-1080) */
+            const float d = h2f_at(blk);
+            for (int e = 0; e < 256; ++e) y[e] = d * (float)iq4xs_scale(blk, e >> 5) * (float)iq4xs_value(blk, e);
         } else if (type == OC_TYPE_IQ2_S) {
             /* include/GGMLDequantize.hpp:1215-1242: db = (d * (0.5 + ls)) *
              * 0.25, y = (db * grid) * sign. */
@@ -539,6 +561,25 @@ static int32_t iq2s_isum(const uint8_t *blk, const int8_t *xq) {
     return bsum;
 }
 
+/* IQ4_XS per-32 integer sums s[ib] = sum_32 kvalues*q8, the exact int32 of
+ * the reference's maddubs/madd reduction (|w|, |x| <= 127: no int16
+ * saturation; SIMDMatMulVecAVX2.cpp:4090-4101). */
+static void iq4xs_subsums(const uint8_t *blk, const int8_t *xq, int32_t s[8]) {
+    for (int ib = 0; ib < 8; ++ib) {
+        int32_t t = 0;
+        for (int j = 0; j < 32; ++j) t += iq4xs_value(blk, 32 * ib + j) * xq[32 * ib + j];
+        s[ib] = t;
+    }
+}
+
+/* IQ4_XS block integer sum_ib (ls_ib - 32) * s[ib] (the GPU test hook's value). */
+static int32_t iq4xs_isum(const uint8_t *blk, const int8_t *xq) {
+    int32_t s[8], tot = 0;
+    iq4xs_subsums(blk, xq, s);
+    for (int ib = 0; ib < 8; ++ib) tot += iq4xs_scale(blk, ib) * s[ib];
+    return tot;
+}
+
 /* Q8_0 block sum_32 w*q8, the true integer product (the reference kernel's
  * sum, src/cpp/core/SIMDMatMulVecAVX2.cpp:4346-4356, equals it whenever no
  * weight byte is -128). */
@@ -605,6 +646,7 @@ int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                     case OC_TYPE_IQ3_XXS: o[0] = iq3_isum(blk, xq); break;
                     case OC_TYPE_IQ3_S: o[0] = iq3s_isum(blk, xq); break;
                     case OC_TYPE_IQ2_S: o[0] = iq2s_isum(blk, xq); break;
+                    case OC_TYPE_IQ4_XS: o[0] = iq4xs_isum(blk, xq); break;
                     default: o[0] = q80_isum(blk, xq); break;
                 }
             }
@@ -885,6 +927,25 @@ static float row_iq2s(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qof
     return 0.125f * sumf;
 }
 
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:3988-4119 (matMulVecBatchIQ4XS_Q8K_AVX2):
+ * per block dl[ib] = d * (float)(ls - 32); mainS from 0 accumulates dl[ib] *
+ * (float)s[ib] over ib; acc += d8 * mainS over blocks in order. Both
+ * accumulations contract to fused multiply-adds (g++ -ffp-contract=fast with
+ * -mfma, as the Q4_K kernel). */
+static float row_iq4xs(const uint8_t *rp, uint32_t nb, const act_t *a, size_t qoff, size_t doff) {
+    float acc = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = rp + (size_t)b * 136;
+        const float d = h2f_at(blk);
+        int32_t s[8];
+        iq4xs_subsums(blk, a->qs + qoff + (size_t)b * 256, s);
+        float mainS = 0.0f;
+        for (int ib = 0; ib < 8; ++ib) mainS = fmaf(d * (float)iq4xs_scale(blk, ib), (float)s[ib], mainS);
+        acc = fmaf(a->d[doff + b], mainS, acc);
+    }
+    return acc;
+}
+
 /* IQ2_XS: no activation quantization. Block dot = float(sum_e double(x_e) *
  * double(w_e)) (dotProductIQ2_XS, include/GGMLDequantize.hpp:1901-1927); row =
  * float(sum_b double(block dot)) (matMulVecFused, :2449-2461). The double
@@ -932,6 +993,7 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t r
                 case OC_TYPE_IQ3_XXS: v = row_iq3(rp, nb, &a, qoff, doff); break;
                 case OC_TYPE_IQ3_S: v = row_iq3s(rp, nb, &a, qoff, doff); break;
                 case OC_TYPE_IQ2_S: v = row_iq2s(rp, nb, &a, qoff, doff); break;
+                case OC_TYPE_IQ4_XS: v = row_iq4xs(rp, nb, &a, qoff, doff); break;
                 default: v = row_q80(rp, nb, &a, qoff, doff); break;
             }
             out[(size_t)s * rows + r] = v;
@@ -1318,6 +1380,50 @@ void oc_encode_iq2s_block(const float *x, uint8_t *out) {
     }
 }
 
+/* IQ4_XS weight encoder (the reference ships none; this build defines it).
+ * Per 32: s = m / -127 with m the first element of largest |x| (it maps to
+ * kvalues[0]). Block: d = M / -32 (fp16 RNE) with M the first s of largest
+ * |s|; ls - 32 = clamp(rne(s / d), -32, 31); dl = d * (ls - 32); per weight
+ * the table entry n minimising (dl * kvalues[n] - x)^2 (first wins), packed
+ * as the decoder include/GGMLDequantize.hpp:1044-1080 reads it. */
+void oc_encode_iq4xs_block(const float *x, uint8_t *out) {
+    float sc[8], smax = 0.0f;
+    for (int c = 0; c < 8; ++c) {
+        float m = 0.0f;
+        for (int i = 0; i < 32; ++i) m = fabsf(x[32 * c + i]) > fabsf(m) ? x[32 * c + i] : m;
+        sc[c] = m / -127.0f;
+        smax = fabsf(sc[c]) > fabsf(smax) ? sc[c] : smax;
+    }
+    memset(out, 0, 136);
+    const uint16_t hd = f2h_rne(smax / -32.0f);
+    const float d = oc_half_to_float(hd);
+    if (d == 0.0f || d != d) return;
+    memcpy(out, &hd, 2);
+    uint16_t sh = 0;
+    for (int c = 0; c < 8; ++c) {
+        int l = (int)rintf(sc[c] / d);
+        l = l < -32 ? -32 : (l > 31 ? 31 : l);
+        const int ls = l + 32;
+        out[4 + c / 2] |= (uint8_t)((ls & 15) << (4 * (c % 2)));
+        sh |= (uint16_t)((ls >> 4) << (2 * c));
+        const float dl = d * (float)l;
+        for (int j = 0; j < 32; ++j) {
+            int best = 0;
+            float berr = 0.0f;
+            for (int n = 0; n < 16; ++n) {
+                const float diff = dl * (float)k_kvalues_iq4nl[n] - x[32 * c + j];
+                const float err = diff * diff;
+                if (n == 0 || err < berr) {
+                    berr = err;
+                    best = n;
+                }
+            }
+            out[8 + 16 * c + (j & 15)] |= (uint8_t)(j < 16 ? best : best << 4);
+        }
+    }
+    memcpy(out + 2, &sh, 2);
+}
+
 /* IQ2_XS weight encoder (the reference ships none; this build defines it).
  * Scales as IQ2_S (per 16: s = max|x|/43, d = 8 max s / 31 fp16 RNE, ls =
  * clamp(rne((8s/d - 1)/2), 0, 15)); per 8: the negative signs with the
@@ -1445,6 +1551,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
             case OC_TYPE_IQ3_S: oc_encode_iq3s_block(xb, o); break;
             case OC_TYPE_IQ2_S: oc_encode_iq2s_block(xb, o); break;
             case OC_TYPE_IQ2_XS: oc_encode_iq2xs_block(xb, o); break;
+            case OC_TYPE_IQ4_XS: oc_encode_iq4xs_block(xb, o); break;
             default: oc_encode_iq3xxs_block(xb, o); break;
         }
     }

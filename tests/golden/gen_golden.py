@@ -112,6 +112,15 @@ def iq2xs_random_blocks(rng, nblk):
     return b.ravel()
 
 
+def iq4xs_random_blocks(rng, nblk):
+    """Random IQ4_XS bytes (every nibble, 6-bit scale and scales_h pattern)
+    with normal fp16 d of varied exponent."""
+    b = rng.integers(0, 256, (nblk, 136), dtype=np.uint8)
+    d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-14, -8, nblk)).astype(np.float16)
+    b[:, 0:2] = d.view(np.uint8).reshape(nblk, 2)
+    return b.ravel()
+
+
 def q80_random_blocks(rng, nblk):
     b = rng.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
     d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-10, -6, nblk)).astype(np.float16)
@@ -352,6 +361,20 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.IQ2_XS, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.IQ2_XS, w, X4, rows, cols)
+
+    # IQ4_XS, likewise: its dequant and the Q8_K kernel
+    # matMulVecBatchIQ4XS_Q8K_AVX2 (SIMDMatMulVecAVX2.cpp:3988).
+    r4 = np.random.default_rng(20261208)
+    g["deq_iq4xs_w"] = iq4xs_random_blocks(r4, 8)
+    g["deq_iq4xs_y"] = ref.dequant(O.IQ4_XS, g["deq_iq4xs_w"], 8, 256)
+    cases4 = {
+        "iq4xs_rand": iq4xs_random_blocks(r4, rows * nb),
+        "iq4xs_enc002": O.Oracle().encode(O.IQ4_XS, (r4.standard_normal((rows, cols)) * 0.02).astype(np.float32)),
+    }
+    for name, w in cases4.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.IQ4_XS, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.IQ4_XS, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")

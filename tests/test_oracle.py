@@ -105,7 +105,7 @@ def test_quantize_q8_0_act_pinned_by_reference_probe(oracle, golden):
 # ---- block decoders ---------------------------------------------------------------
 
 @pytest.mark.parametrize("name,qt", [("q2k", O.Q2_K), ("q3k", O.Q3_K), ("q4k", O.Q4_K), ("q5k", O.Q5_K), ("q6k", O.Q6_K), ("iq3", O.IQ3_XXS),
-                                     ("iq3s", O.IQ3_S), ("iq2s", O.IQ2_S), ("iq2xs", O.IQ2_XS),
+                                     ("iq3s", O.IQ3_S), ("iq2s", O.IQ2_S), ("iq2xs", O.IQ2_XS), ("iq4xs", O.IQ4_XS),
                                      ("q80", O.Q8_0)])
 def test_dequant_matches_reference(oracle, golden, name, qt):
     w = golden[f"deq_{name}_w"]
@@ -161,7 +161,8 @@ def test_iq3_dequant_closed_form(oracle):
 
 # ---- per-block integer dots: brute-force identity ------------------------------------
 
-@pytest.mark.parametrize("qt", [O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S])
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S,
+                                O.IQ4_XS])
 def test_block_isums_identity(oracle, qt):
     """sum over blocks of the integer sums, scaled per block by the float block
     scales, reproduces dequant(W) . (d8 * xq) in exact rational arithmetic."""
@@ -190,6 +191,9 @@ def test_block_isums_identity(oracle, qt):
         w = gen(rng, rows * cols // 256)
     elif qt == O.IQ2_S:
         from gen_golden import iq2s_random_blocks as gen
+        w = gen(rng, rows * cols // 256)
+    elif qt == O.IQ4_XS:
+        from gen_golden import iq4xs_random_blocks as gen
         w = gen(rng, rows * cols // 256)
     else:
         from gen_golden import iq3_random_blocks as gen
@@ -257,6 +261,12 @@ def test_block_isums_identity(oracle, qt):
             c = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
             # db = d*(1+2ls)
             lhs = (deq.reshape(rows, -1, 256) * xq).sum(2) / c
+        elif qt == O.IQ4_XS:
+            # dequant = d * (ls-32) * kvalue (11 + 6 + 7 significant bits: exact
+            # in fp32), so sum(deq * xq) / d is the integer sum exactly
+            wb = w.reshape(rows, cols // 256, 136)
+            c = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+            lhs = (deq.reshape(rows, -1, 256) * xq).sum(2) / c
         elif qt == O.IQ2_S:
             wb = w.reshape(rows, cols // 256, 82)
             c = wb[:, :, 0:2].copy().view(np.float16).astype(np.float64)[:, :, 0]
@@ -276,7 +286,8 @@ MM = [("q4k_rand", O.Q4_K), ("q4k_enc1", O.Q4_K), ("q4k_enc002", O.Q4_K), ("q5k_
       ("q5k_enc1", O.Q5_K), ("q3k_rand", O.Q3_K), ("q3k_enc002", O.Q3_K), ("q2k_rand", O.Q2_K),
       ("q2k_enc002", O.Q2_K), ("iq3s_rand", O.IQ3_S),
       ("iq3s_enc002", O.IQ3_S), ("iq2s_rand", O.IQ2_S), ("iq2s_enc002", O.IQ2_S),
-      ("iq2xs_rand", O.IQ2_XS), ("iq2xs_enc002", O.IQ2_XS), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
+      ("iq2xs_rand", O.IQ2_XS), ("iq2xs_enc002", O.IQ2_XS), ("iq4xs_rand", O.IQ4_XS),
+      ("iq4xs_enc002", O.IQ4_XS), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
 
 
 @pytest.mark.parametrize("name,qt", MM)
@@ -295,7 +306,7 @@ def test_matmul_q80_cols96(oracle, golden):
 
 
 @pytest.mark.parametrize("qt", [O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S,
-                                O.IQ2_XS])
+                                O.IQ2_XS, O.IQ4_XS])
 def test_matmul_close_to_float_dot(oracle, qt):
     """Independent of the reference: the quantized mat-vec approximates the
     float product of the dequantized weights with x (activation quantization
@@ -354,9 +365,9 @@ def test_q4k_encoder_reference_roundtrip_thresholds(oracle):
 
 @pytest.mark.parametrize("qt,bound", [(O.Q8_0, 0.01), (O.Q2_K, 0.45), (O.Q3_K, 0.2), (O.Q5_K, 0.08), (O.Q6_K, 0.04),
                                       (O.IQ3_XXS, 0.25), (O.IQ3_S, 0.2), (O.IQ2_S, 0.35),
-                                      (O.IQ2_XS, 0.4)])
+                                      (O.IQ2_XS, 0.4), (O.IQ4_XS, 0.1)])
 def test_own_encoders_roundtrip(oracle, qt, bound):
-    """This build's Q8_0 / Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS encoders (the reference has none):
+    """This build's Q8_0 / Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS encoders (the reference has none):
     N(0, 0.02) rows round-trip within the format's expected relative RMS."""
     rng = np.random.default_rng(9)
     x = (rng.standard_normal((16, 1024)) * 0.02).astype(np.float32)
