@@ -1418,6 +1418,67 @@ struct TDot<kIQ2_S, S> {
     }
 };
 
+// IQ4_XS, one unit (136 B, 8-byte aligned in LDS) per lane: d at 0, 16 bits
+// of scale high parts at 2, scale low nibbles at 4, 128 nibble bytes at 8.
+// Sub-block ib (32 weights): ls = low nibble ib | high bits 2ib << 4, scale
+// ls - 32; weight j < 16 is kvalues[low nibble of byte 16ib + j], j >= 16
+// kvalues[high nibble of byte 16ib + j - 16] (include/GGMLDequantize.hpp:
+// 1044-1080). Four nibbles become four table bytes with three v_perm_b32:
+// the entries 0-7 and 8-15 by the nibble's low 3 bits, then a per-byte pick
+// by bit 3. value = d*d8*sum_ib (ls-32)*sum_32 w*q8, exact in int32 (the
+// reference kernel, SIMDMatMulVecAVX2.cpp:3988-4119, rounds per 32 in fp32).
+__device__ __forceinline__ uint32_t iq4nl_lut(uint32_t n) {
+    // kvalues_iq4nl (include/GGMLDequantize.hpp:55-57) as four words of bytes
+    constexpr uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
+    const uint32_t lo3 = n & 0x07070707u;
+    const uint32_t a = __builtin_amdgcn_perm(T1, T0, lo3), b = __builtin_amdgcn_perm(T3, T2, lo3);
+    return __builtin_amdgcn_perm(b, a, ((n >> 1) & 0x04040404u) | 0x03020100u);
+}
+
+template <int S>
+struct TDot<kIQ4_XS, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        const uint32_t *u32 = reinterpret_cast<const uint32_t *>(u);
+        const uint32_t h0 = u32[0], sl = u32[1];
+        int tot[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) tot[s] = 0;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            uint32_t w[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = u32[2 + 4 * ib + k];
+                w[k] = iq4nl_lut(q & 0x0F0F0F0Fu);
+                w[4 + k] = iq4nl_lut((q >> 4) & 0x0F0F0F0Fu);
+            }
+            const int ls = int(((sl >> (4 * ib)) & 15u) | (((h0 >> (16 + 2 * ib)) & 3u) << 4)) - 32;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const unsigned char *xr = xr0 + s * xtok + 32 * ib;
+                const u32x4 x0 = lds128(xr), x1 = lds128(xr + 16);
+                int p = sdot4(int(w[0]), int(x0.x), 0);
+                p = sdot4(int(w[1]), int(x0.y), p);
+                p = sdot4(int(w[2]), int(x0.z), p);
+                p = sdot4(int(w[3]), int(x0.w), p);
+                p = sdot4(int(w[4]), int(x1.x), p);
+                p = sdot4(int(w[5]), int(x1.y), p);
+                p = sdot4(int(w[6]), int(x1.z), p);
+                p = sdot4(int(w[7]), int(x1.w), p);
+                tot[s] += ls * p;
+            }
+        }
+        const float d = h2f(h0 & 0xFFFFu);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if (dbg) dbg[s * dbg_tok] = tot[s];
+            const float d8 = *reinterpret_cast<const float *>(xr0 + s * xtok + XB_D);
+            val[s] = (d * d8) * float(tot[s]);
+        }
+    }
+};
+
 // IQ2_XS, one unit (74 B, 2-byte aligned in LDS) per lane, on fp32 x (the
 // reference's CPU path for this type, dotProductIQ2_XS, dots unquantized x;
 // include/GGMLDequantize.hpp:1901-1927): per 8 weights one 16-bit entry --
@@ -1867,7 +1928,7 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     return o;
 }
 
-bool tiled_type(int type) { return type == kIQ2_XS || type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kIQ4_XS || type == kIQ2_XS || type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -1931,9 +1992,9 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         // Q2_K / Q3_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S rows are not 16-byte
         // multiples: 8-row groups keep every workgroup's first row 16-byte
         // aligned (8*84, 8*110, 8*210, 8*98 and 8*82 bytes per 256 columns
-        // are multiples of 16; IQ2_XS: 8*74).
+        // are multiples of 16; IQ2_XS: 8*74, IQ4_XS: 8*136).
         if ((type == kQ2_K || type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S || type == kIQ2_S ||
-             type == kIQ2_XS) &&
+             type == kIQ2_XS || type == kIQ4_XS) &&
             rpw < g.rows) {
             rpw = (rpw + 7) / 8 * 8;
             if (rpw > fit) rpw = fit / 8 * 8;
@@ -1955,6 +2016,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         case kIQ2_S: return launch_tiled<kIQ2_S, C>(S, a, wg, lds, st);
         case kQ2_K: return launch_tiled<kQ2_K, C>(S, a, wg, lds, st);
         case kIQ2_XS: return launch_tiled<kIQ2_XS, C>(S, a, wg, lds, st);
+        case kIQ4_XS: return launch_tiled<kIQ4_XS, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:

@@ -559,6 +559,54 @@ __device__ void enc_iq2s(const float *x, uint8_t *out) {
     }
 }
 
+// IQ4_XS (this build's encoder; the reference ships none): per 32, s = m /
+// -127 with m the first element of largest |x|; d = M / -32 (fp16 RNE) with M
+// the first s of largest |s|; ls - 32 = clamp(rne(s / d), -32, 31); per
+// weight the table entry nearest x / (d * (ls - 32)) in squared error (first
+// wins), packed as the reference decoder reads it
+// (include/GGMLDequantize.hpp:1044-1080).
+__constant__ int8_t c_kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+__device__ void enc_iq4xs(const float *x, uint8_t *out) {
+    float sc[8], smax = 0.0f;
+    for (int c = 0; c < 8; ++c) {
+        float m = 0.0f;
+        for (int i = 0; i < 32; ++i) m = fabsf(x[32 * c + i]) > fabsf(m) ? x[32 * c + i] : m;
+        sc[c] = __fdiv_rn(m, -127.0f);
+        smax = fabsf(sc[c]) > fabsf(smax) ? sc[c] : smax;
+    }
+    for (int i = 0; i < 136; ++i) out[i] = 0;
+    const uint16_t hd = f2h_rne(__fdiv_rn(smax, -32.0f));
+    const float d = h2f(hd);
+    if (d == 0.0f || d != d) return;
+    out[0] = uint8_t(hd);
+    out[1] = uint8_t(hd >> 8);
+    uint32_t sh = 0;
+    for (int c = 0; c < 8; ++c) {
+        int l = int(rintf(__fdiv_rn(sc[c], d)));
+        l = l < -32 ? -32 : (l > 31 ? 31 : l);
+        const int ls = l + 32;
+        out[4 + c / 2] |= uint8_t((ls & 15) << (4 * (c % 2)));
+        sh |= uint32_t(ls >> 4) << (2 * c);
+        const float dl = d * float(l);
+        for (int j = 0; j < 32; ++j) {
+            int best = 0;
+            float berr = 0.0f;
+            for (int n = 0; n < 16; ++n) {
+                const float diff = dl * float(c_kvalues_iq4nl[n]) - x[32 * c + j];
+                const float err = diff * diff;
+                if (n == 0 || err < berr) {
+                    berr = err;
+                    best = n;
+                }
+            }
+            out[8 + 16 * c + (j & 15)] |= uint8_t(j < 16 ? best : best << 4);
+        }
+    }
+    out[2] = uint8_t(sh);
+    out[3] = uint8_t(sh >> 8);
+}
+
 // IQ2_XS (this build's encoder; the reference ships none): scales as IQ2_S;
 // per 8 the negative signs with the smallest-|x| one flipped on odd count (the
 // format implies even parity) and the codebook entry (of 512) nearest |x|/db
@@ -633,6 +681,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
         case kIQ3_S: enc_iq3s(xu, o); break;
         case kIQ2_S: enc_iq2s(xu, o); break;
         case kIQ2_XS: enc_iq2xs(xu, o); break;
+        case kIQ4_XS: enc_iq4xs(xu, o); break;
         default: enc_iq3xxs(xu, o); break;
     }
 }
