@@ -43,12 +43,13 @@ uint32_t oc_type_size(int type) {
         case OC_TYPE_IQ2_S: return 82;
         case OC_TYPE_IQ2_XS: return 74;
         case OC_TYPE_IQ4_XS: return 136;
+        case OC_TYPE_IQ4_NL: return 18;
         default: return 0;
     }
 }
 
 uint32_t oc_block_size(int type) {
-    return type == OC_TYPE_Q8_0 ? 32u : (oc_type_size(type) ? 256u : 0u);
+    return type == OC_TYPE_Q8_0 || type == OC_TYPE_IQ4_NL ? 32u : (oc_type_size(type) ? 256u : 0u);
 }
 
 /* ---- fp16 <-> fp32 -------------------------------------------------------- */
@@ -352,7 +353,15 @@ int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
     for (uint32_t b = 0; b < n / bs; ++b) {
         const uint8_t *blk = w + (size_t)b * ts;
         float *y = out + (size_t)b * bs;
-        if (type == OC_TYPE_Q8_0) {
+        if (type == OC_TYPE_IQ4_NL) {
+            /* include/GGMLDequantize.hpp:1304-1312: y[j] = d * kvalues[low
+             * nibble of qs[j]], y[j+16] = d * kvalues[high nibble] */
+            const float d = h2f_at(blk);
+            for (int j = 0; j < 16; ++j) {
+                y[j] = d * (float)k_kvalues_iq4nl[blk[2 + j] & 0xF];
+                y[j + 16] = d * (float)k_kvalues_iq4nl[blk[2 + j] >> 4];
+            }
+        } else if (type == OC_TYPE_Q8_0) {
             /* include/GGMLDequantize.hpp:243-250 */
             const float d = h2f_at(blk);
             for (int i = 0; i < 32; ++i) y[i] = (float)(int8_t)blk[2 + i] * d;
@@ -624,7 +633,7 @@ static int shape_ok(int type, uint32_t cols) {
 
 int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                    uint32_t rows, uint32_t cols, int32_t *isums) {
-    if (!shape_ok(type, cols) || type == OC_TYPE_IQ2_XS) return -1;  /* float path: no integer sums */
+    if (!shape_ok(type, cols) || type == OC_TYPE_IQ2_XS || type == OC_TYPE_IQ4_NL) return -1;  /* float paths: no integer sums */
     act_t a;
     if (quantize_acts(type, X, S, cols, &a)) return -1;
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type), nb = cols / bs;
@@ -967,11 +976,48 @@ static void matmul_iq2xs(const uint8_t *W, const float *X, uint32_t S, uint32_t 
         }
 }
 
+/* IQ4_NL: no activation quantization (src/cpp/core/SIMDMatMulVecAVX2.cpp:
+ * 4126-4200, matMulVecBatchIQ4NL_Q8K_AVX2, dots fp32 x). Per 32-block, lane l
+ * of 8 forms fma(w3, x[24+l], fma(w2, x[16+l], fma(w1, x[8+l], w0 * x[l])))
+ * with w_k = kvalues of element 8k + l; the lanes reduce as ((v0+v4) +
+ * (v1+v5)) + ((v2+v6) + (v3+v7)) (lo+hi, then two hadd); the row accumulator
+ * from 0 takes fma(d, sum, acc) block by block (contracted `acc += d * sum`). */
+static void matmul_iq4nl(const uint8_t *W, const float *X, uint32_t S, uint32_t rows, uint32_t cols,
+                         float *out) {
+    const uint32_t nb = cols / 32;
+    for (uint32_t s = 0; s < S; ++s)
+        for (uint32_t r = 0; r < rows; ++r) {
+            float acc = 0.0f;
+            for (uint32_t b = 0; b < nb; ++b) {
+                const uint8_t *blk = W + ((size_t)r * nb + b) * 18;
+                const float *x = X + (size_t)s * cols + (size_t)b * 32;
+                float w[32], v[8];
+                for (int j = 0; j < 16; ++j) {
+                    w[j] = (float)k_kvalues_iq4nl[blk[2 + j] & 0xF];
+                    w[j + 16] = (float)k_kvalues_iq4nl[blk[2 + j] >> 4];
+                }
+                for (int l = 0; l < 8; ++l) {
+                    float t = w[l] * x[l];
+                    t = fmaf(w[8 + l], x[8 + l], t);
+                    t = fmaf(w[16 + l], x[16 + l], t);
+                    v[l] = fmaf(w[24 + l], x[24 + l], t);
+                }
+                const float sum = hsum8(v);
+                acc = fmaf(h2f_at(blk), sum, acc);
+            }
+            out[(size_t)s * rows + r] = acc;
+        }
+}
+
 int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t rows,
               uint32_t cols, float *out) {
     if (!shape_ok(type, cols)) return -1;
     if (type == OC_TYPE_IQ2_XS) {
         matmul_iq2xs(W, X, S, rows, cols, out);
+        return 0;
+    }
+    if (type == OC_TYPE_IQ4_NL) {
+        matmul_iq4nl(W, X, S, rows, cols, out);
         return 0;
     }
     act_t a;
@@ -1424,6 +1470,33 @@ void oc_encode_iq4xs_block(const float *x, uint8_t *out) {
     memcpy(out + 2, &sh, 2);
 }
 
+/* IQ4_NL weight encoder (the reference ships none; this build defines it):
+ * d = m / -127 (fp16 RNE) with m the first element of largest |x|; per weight
+ * the table entry minimising (d * kvalues[n] - x)^2 (first wins), packed as
+ * the decoder include/GGMLDequantize.hpp:1304-1312 reads it. */
+void oc_encode_iq4nl_block(const float *x, uint8_t *out) {
+    float m = 0.0f;
+    for (int i = 0; i < 32; ++i) m = fabsf(x[i]) > fabsf(m) ? x[i] : m;
+    memset(out, 0, 18);
+    const uint16_t hd = f2h_rne(m / -127.0f);
+    const float d = oc_half_to_float(hd);
+    if (d == 0.0f || d != d) return;
+    memcpy(out, &hd, 2);
+    for (int j = 0; j < 32; ++j) {
+        int best = 0;
+        float berr = 0.0f;
+        for (int n = 0; n < 16; ++n) {
+            const float diff = d * (float)k_kvalues_iq4nl[n] - x[j];
+            const float err = diff * diff;
+            if (n == 0 || err < berr) {
+                berr = err;
+                best = n;
+            }
+        }
+        out[2 + (j & 15)] |= (uint8_t)(j < 16 ? best : best << 4);
+    }
+}
+
 /* IQ2_XS weight encoder (the reference ships none; this build defines it).
  * Scales as IQ2_S (per 16: s = max|x|/43, d = 8 max s / 31 fp16 RNE, ls =
  * clamp(rne((8s/d - 1)/2), 0, 15)); per 8: the negative signs with the
@@ -1552,6 +1625,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
             case OC_TYPE_IQ2_S: oc_encode_iq2s_block(xb, o); break;
             case OC_TYPE_IQ2_XS: oc_encode_iq2xs_block(xb, o); break;
             case OC_TYPE_IQ4_XS: oc_encode_iq4xs_block(xb, o); break;
+            case OC_TYPE_IQ4_NL: oc_encode_iq4nl_block(xb, o); break;
             default: oc_encode_iq3xxs_block(xb, o); break;
         }
     }

@@ -59,6 +59,7 @@ void ref_dequant_block(int type, const uint8_t *blk, float *out) {
         case 22: GGMLDequantize::dequantizeIQ2_SBlock(blk, out); break;  // include/GGMLDequantize.hpp:1215
         case 17: GGMLDequantize::dequantizeIQ2_XSBlock(blk, out); break;  // include/GGMLDequantize.hpp:1245
         case 23: GGMLDequantize::dequantizeIQ4_XSBlock(blk, out); break;  // include/GGMLDequantize.hpp:1319
+        case 20: GGMLDequantize::dequantizeIQ4_NLBlock(blk, out); break;  // include/GGMLDequantize.hpp:1304
         default: break;
     }
 }
@@ -88,6 +89,8 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
         case 12: simd::matMulVecBatchQ4K_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
         // src/cpp/core/SIMDMatMulVecAVX2.cpp:3988 (the IQ4_XS Q8_K kernel)
         case 23: simd::matMulVecBatchIQ4XS_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
+        // src/cpp/core/SIMDMatMulVecAVX2.cpp:4126 (IQ4_NL: fp32 x despite the name)
+        case 20: simd::matMulVecBatchIQ4NL_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
         // src/cpp/core/SIMDMatMulVecAVX2.cpp:4757 (the compact-block Q2_K kernel)
         case 10: simd::matMulVecBatchQ2K_Compact_Q8K_AVX2(W, X, seqLen, rows, cols, out); return 0;
         // src/cpp/core/SIMDMatMulVecAVX2.cpp:3220 (no residual)

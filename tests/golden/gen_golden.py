@@ -121,6 +121,14 @@ def iq4xs_random_blocks(rng, nblk):
     return b.ravel()
 
 
+def iq4nl_random_blocks(rng, nblk):
+    """Random IQ4_NL bytes (every nibble) with normal fp16 d of varied exponent."""
+    b = rng.integers(0, 256, (nblk, 18), dtype=np.uint8)
+    d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-14, -6, nblk)).astype(np.float16)
+    b[:, 0:2] = d.view(np.uint8).reshape(nblk, 2)
+    return b.ravel()
+
+
 def q80_random_blocks(rng, nblk):
     b = rng.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
     d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-10, -6, nblk)).astype(np.float16)
@@ -375,6 +383,20 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.IQ4_XS, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.IQ4_XS, w, X4, rows, cols)
+
+    # IQ4_NL, likewise: its dequant and the fp32-x kernel
+    # matMulVecBatchIQ4NL_Q8K_AVX2 (SIMDMatMulVecAVX2.cpp:4126).
+    rn = np.random.default_rng(20261209)
+    g["deq_iq4nl_w"] = iq4nl_random_blocks(rn, 16)
+    g["deq_iq4nl_y"] = ref.dequant(O.IQ4_NL, g["deq_iq4nl_w"], 2, 256)
+    casesn = {
+        "iq4nl_rand": iq4nl_random_blocks(rn, rows * cols // 32),
+        "iq4nl_enc002": O.Oracle().encode(O.IQ4_NL, (rn.standard_normal((rows, cols)) * 0.02).astype(np.float32)),
+    }
+    for name, w in casesn.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.IQ4_NL, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.IQ4_NL, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")
