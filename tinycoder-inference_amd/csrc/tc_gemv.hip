@@ -564,7 +564,7 @@ constexpr uint32_t XB_BS = 256, XB_D = 288;  // bsums and d offsets inside a rec
 // padded to 1072 bytes: the lanes of a wave read the records of consecutive
 // blocks, and a 1024-byte stride would put them all in the same LDS banks
 // (1072 = 48 mod 256, the residue of the conflict-free 304-byte record).
-__host__ __device__ constexpr uint32_t xrec_bytes(int type) { return type == kIQ2_XS ? 1072u : XB; }
+__host__ __device__ constexpr uint32_t xrec_bytes(int type) { return type == kIQ2_XS || type == kIQ4_NL ? 1072u : XB; }
 
 // 16-byte loads per lane per tile (the last one partial for Q6_K / IQ3_XXS,
 // whose 64-unit tiles are 13440 / 6272 bytes) and the LDS bytes of one tile.
@@ -815,7 +815,7 @@ template <int TYPE, int S, int TNT>
 __device__ __forceinline__ void tstage_finish(const TJobDev &jb, const XRsrc &rs, const XPre &p, unsigned char *xr) {
     const uint32_t tid = threadIdx.x;
     const uint32_t nblk = jb.nx * (jb.cols / 256);
-    if constexpr (TYPE == kIQ2_XS) {
+    if constexpr (TYPE == kIQ2_XS || TYPE == kIQ4_NL) {
         // fp32 x as it is: 64-byte chunk c (16 floats) of block c/16 into that
         // block's record
         const uint32_t nchunk = nblk * 16;
@@ -1479,6 +1479,75 @@ struct TDot<kIQ4_XS, S> {
     }
 };
 
+// IQ4_NL, one unit (8 blocks of 18 B: d, then 16 nibble bytes; 144 B, so
+// 16-byte aligned in LDS) per lane, on fp32 x (the reference's CPU kernel for
+// this type, matMulVecBatchIQ4NL_Q8K_AVX2, SIMDMatMulVecAVX2.cpp:4126-4200,
+// dots unquantized x). Table bytes as in IQ4_XS; per block the reference's
+// order: 8 lanes of a 4-deep fma chain over elements l, 8+l, 16+l, 24+l,
+// reduced ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)), then fma(d, sum, acc). The
+// unit's value chains its 8 blocks from 0, so a row differs from the
+// reference's one chain over all blocks by fp32 summation order only.
+template <int S>
+struct TDot<kIQ4_NL, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        (void)dbg;
+        (void)dbg_tok;
+        const uint32_t *u32 = reinterpret_cast<const uint32_t *>(u);
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[s] = 0.0f;
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {  // block pairs: 36 B = 9 dwords
+            uint32_t wd[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) wd[k] = u32[9 * pr + k];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int blk = 2 * pr + h;
+                uint32_t q[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) q[k] = h == 0 ? align2(wd[k + 1], wd[k], 2) : wd[5 + k];
+                const float d = h2f(h == 0 ? (wd[0] & 0xFFFFu) : (wd[4] >> 16));
+                uint32_t wt[8];  // table bytes of elements 4k.. (k < 4: low nibbles) and 16 + 4(k-4).. (high)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    wt[k] = iq4nl_lut(q[k] & 0x0F0F0F0Fu);
+                    wt[4 + k] = iq4nl_lut((q[k] >> 4) & 0x0F0F0F0Fu);
+                }
+                float w[32];
+#pragma unroll
+                for (int e = 0; e < 32; ++e) w[e] = float(int8_t(uint8_t(wt[e >> 2] >> (8 * (e & 3)))));
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const float4 *xp = reinterpret_cast<const float4 *>(xr0 + s * xtok) + 8 * blk;
+                    float x[32];
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const float4 v = xp[c];
+                        x[4 * c] = v.x;
+                        x[4 * c + 1] = v.y;
+                        x[4 * c + 2] = v.z;
+                        x[4 * c + 3] = v.w;
+                    }
+                    float v[8];
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) {
+                        float t = w[l] * x[l];
+                        t = fmaf(w[8 + l], x[8 + l], t);
+                        t = fmaf(w[16 + l], x[16 + l], t);
+                        v[l] = fmaf(w[24 + l], x[24 + l], t);
+                    }
+                    const float sum = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+                    acc[s] = fmaf(d, sum, acc[s]);
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) val[s] = acc[s];
+    }
+};
+
 // IQ2_XS, one unit (74 B, 2-byte aligned in LDS) per lane, on fp32 x (the
 // reference's CPU path for this type, dotProductIQ2_XS, dots unquantized x;
 // include/GGMLDequantize.hpp:1901-1927): per 8 weights one 16-bit entry --
@@ -1928,7 +1997,7 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     return o;
 }
 
-bool tiled_type(int type) { return type == kIQ4_XS || type == kIQ2_XS || type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kIQ4_NL || type == kIQ4_XS || type == kIQ2_XS || type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -2017,6 +2086,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         case kQ2_K: return launch_tiled<kQ2_K, C>(S, a, wg, lds, st);
         case kIQ2_XS: return launch_tiled<kIQ2_XS, C>(S, a, wg, lds, st);
         case kIQ4_XS: return launch_tiled<kIQ4_XS, C>(S, a, wg, lds, st);
+        case kIQ4_NL: return launch_tiled<kIQ4_NL, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:
@@ -2048,7 +2118,7 @@ hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t
 
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes) {
     // S*cols up to which the tiled kernels preload all of x ahead of the weights
-    if (!tiled_type(type) || type == kIQ2_XS) return 0xFFFFFFFFu;  // IQ2_XS: fp32 x, never pre-quantized
+    if (!tiled_type(type) || type == kIQ2_XS || type == kIQ4_NL) return 0xFFFFFFFFu;  // fp32 x, never pre-quantized
     return uint32_t(kXPre) * (use_big(type, weight_bytes) ? CfgBig::NT : CfgSmall::NT) * 16u;
 }
 

@@ -567,6 +567,39 @@ __device__ void enc_iq2s(const float *x, uint8_t *out) {
 // (include/GGMLDequantize.hpp:1044-1080).
 __constant__ int8_t c_kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
 
+// IQ4_NL (this build's encoder; the reference ships none): per 32-block d =
+// m / -127 (fp16 RNE) with m the first element of largest |x|; per weight the
+// table entry nearest x in squared error of d * kvalue (first wins), packed as
+// the reference decoder reads it (include/GGMLDequantize.hpp:1304-1312). One
+// unit is 8 consecutive blocks (144 bytes).
+__device__ void enc_iq4nl(const float *x, uint8_t *out) {
+    for (int b = 0; b < 8; ++b) {
+        const float *xb = x + 32 * b;
+        uint8_t *o = out + 18 * b;
+        float m = 0.0f;
+        for (int i = 0; i < 32; ++i) m = fabsf(xb[i]) > fabsf(m) ? xb[i] : m;
+        for (int i = 0; i < 18; ++i) o[i] = 0;
+        const uint16_t hd = f2h_rne(__fdiv_rn(m, -127.0f));
+        const float d = h2f(hd);
+        if (d == 0.0f || d != d) continue;
+        o[0] = uint8_t(hd);
+        o[1] = uint8_t(hd >> 8);
+        for (int j = 0; j < 32; ++j) {
+            int best = 0;
+            float berr = 0.0f;
+            for (int n = 0; n < 16; ++n) {
+                const float diff = d * float(c_kvalues_iq4nl[n]) - xb[j];
+                const float err = diff * diff;
+                if (n == 0 || err < berr) {
+                    berr = err;
+                    best = n;
+                }
+            }
+            o[2 + (j & 15)] |= uint8_t(j < 16 ? best : best << 4);
+        }
+    }
+}
+
 __device__ void enc_iq4xs(const float *x, uint8_t *out) {
     float sc[8], smax = 0.0f;
     for (int c = 0; c < 8; ++c) {
@@ -682,6 +715,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
         case kIQ2_S: enc_iq2s(xu, o); break;
         case kIQ2_XS: enc_iq2xs(xu, o); break;
         case kIQ4_XS: enc_iq4xs(xu, o); break;
+        case kIQ4_NL: enc_iq4nl(xu, o); break;
         default: enc_iq3xxs(xu, o); break;
     }
 }
