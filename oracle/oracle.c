@@ -44,12 +44,13 @@ uint32_t oc_type_size(int type) {
         case OC_TYPE_IQ2_XS: return 74;
         case OC_TYPE_IQ4_XS: return 136;
         case OC_TYPE_IQ4_NL: return 18;
+        case OC_TYPE_Q5_0: return 22;
         default: return 0;
     }
 }
 
 uint32_t oc_block_size(int type) {
-    return type == OC_TYPE_Q8_0 || type == OC_TYPE_IQ4_NL ? 32u : (oc_type_size(type) ? 256u : 0u);
+    return type == OC_TYPE_Q8_0 || type == OC_TYPE_IQ4_NL || type == OC_TYPE_Q5_0 ? 32u : (oc_type_size(type) ? 256u : 0u);
 }
 
 /* ---- fp16 <-> fp32 -------------------------------------------------------- */
@@ -347,13 +348,26 @@ static float iq2xs_weight(const uint8_t *blk, int e) {
     return dl * g * ((signs >> j) & 1 ? -1.0f : 1.0f);
 }
 
+/* Q5_0 (22 B: d, qh (32 bits) at 2, qs[16] at 6): element j < 16 is the low
+ * nibble of qs[j] with bit j of qh as bit 4, element j + 16 the high nibble
+ * with bit j + 16; value q - 16 (include/GGMLDequantize.hpp:163-185). */
+static int q50_value(const uint8_t *blk, int e) {
+    const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+    const uint8_t q = blk[6 + (e & 15)];
+    return (int)(((e < 16 ? q & 0xF : q >> 4) | (((qh >> e) & 1u) << 4))) - 16;
+}
+
 int oc_dequant_row(int type, const uint8_t *w, uint32_t n, float *out) {
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type);
     if (bs == 0 || n % bs) return -1;
     for (uint32_t b = 0; b < n / bs; ++b) {
         const uint8_t *blk = w + (size_t)b * ts;
         float *y = out + (size_t)b * bs;
-        if (type == OC_TYPE_IQ4_NL) {
+        if (type == OC_TYPE_Q5_0) {
+            /* include/GGMLDequantize.hpp:163-185: y = d * (q5 - 16) */
+            const float d = h2f_at(blk);
+            for (int e = 0; e < 32; ++e) y[e] = d * (float)q50_value(blk, e);
+        } else if (type == OC_TYPE_IQ4_NL) {
             /* include/GGMLDequantize.hpp:1304-1312: y[j] = d * kvalues[low
              * nibble of qs[j]], y[j+16] = d * kvalues[high nibble] */
             const float d = h2f_at(blk);
@@ -633,7 +647,7 @@ static int shape_ok(int type, uint32_t cols) {
 
 int oc_block_isums(int type, const uint8_t *W, const float *X, uint32_t S,
                    uint32_t rows, uint32_t cols, int32_t *isums) {
-    if (!shape_ok(type, cols) || type == OC_TYPE_IQ2_XS || type == OC_TYPE_IQ4_NL) return -1;  /* float paths: no integer sums */
+    if (!shape_ok(type, cols) || type == OC_TYPE_IQ2_XS || type == OC_TYPE_IQ4_NL || type == OC_TYPE_Q5_0) return -1;  /* float paths: no integer sums */
     act_t a;
     if (quantize_acts(type, X, S, cols, &a)) return -1;
     const uint32_t bs = oc_block_size(type), ts = oc_type_size(type), nb = cols / bs;
@@ -976,6 +990,29 @@ static void matmul_iq2xs(const uint8_t *W, const float *X, uint32_t S, uint32_t 
         }
 }
 
+/* Q5_0: no activation quantization. Block dot = (float)(sum over j < 16 of
+ * double(x_j) * v_j then double(x_{j+16}) * v_{j+16}, in that order) * d
+ * (dotProductQ5_0, include/GGMLDequantize.hpp:1820-1836); row = float(sum_b
+ * double(block dot)) (matMulVecFused, :2449-2461). */
+static void matmul_q50(const uint8_t *W, const float *X, uint32_t S, uint32_t rows, uint32_t cols, float *out) {
+    const uint32_t nb = cols / 32;
+    for (uint32_t s = 0; s < S; ++s)
+        for (uint32_t r = 0; r < rows; ++r) {
+            double dot = 0.0;
+            for (uint32_t b = 0; b < nb; ++b) {
+                const uint8_t *blk = W + ((size_t)r * nb + b) * 22;
+                const float *x = X + (size_t)s * cols + (size_t)b * 32;
+                double bd = 0.0;
+                for (int j = 0; j < 16; ++j) {
+                    bd += (double)x[j] * q50_value(blk, j);
+                    bd += (double)x[j + 16] * q50_value(blk, j + 16);
+                }
+                dot += (double)((float)bd * h2f_at(blk));
+            }
+            out[(size_t)s * rows + r] = (float)dot;
+        }
+}
+
 /* IQ4_NL: no activation quantization (src/cpp/core/SIMDMatMulVecAVX2.cpp:
  * 4126-4200, matMulVecBatchIQ4NL_Q8K_AVX2, dots fp32 x). Per 32-block, lane l
  * of 8 forms fma(w3, x[24+l], fma(w2, x[16+l], fma(w1, x[8+l], w0 * x[l])))
@@ -1018,6 +1055,10 @@ int oc_matmul(int type, const uint8_t *W, const float *X, uint32_t S, uint32_t r
     }
     if (type == OC_TYPE_IQ4_NL) {
         matmul_iq4nl(W, X, S, rows, cols, out);
+        return 0;
+    }
+    if (type == OC_TYPE_Q5_0) {
+        matmul_q50(W, X, S, rows, cols, out);
         return 0;
     }
     act_t a;
@@ -1470,6 +1511,28 @@ void oc_encode_iq4xs_block(const float *x, uint8_t *out) {
     memcpy(out + 2, &sh, 2);
 }
 
+/* Q5_0 weight encoder (the reference ships none; this build defines it): d =
+ * m / -16 (fp16 RNE) with m the first element of largest |x|; q =
+ * clamp(rne(x / d) + 16, 0, 31), packed as the decoder
+ * include/GGMLDequantize.hpp:163-185 reads it. */
+void oc_encode_q50_block(const float *x, uint8_t *out) {
+    float m = 0.0f;
+    for (int i = 0; i < 32; ++i) m = fabsf(x[i]) > fabsf(m) ? x[i] : m;
+    memset(out, 0, 22);
+    const uint16_t hd = f2h_rne(m / -16.0f);
+    const float d = oc_half_to_float(hd);
+    if (d == 0.0f || d != d) return;
+    memcpy(out, &hd, 2);
+    uint32_t qh = 0;
+    for (int j = 0; j < 32; ++j) {
+        int q = (int)rintf(x[j] / d) + 16;
+        q = q < 0 ? 0 : (q > 31 ? 31 : q);
+        out[6 + (j & 15)] |= (uint8_t)(j < 16 ? (q & 15) : (q & 15) << 4);
+        qh |= (uint32_t)(q >> 4) << j;
+    }
+    memcpy(out + 2, &qh, 4);
+}
+
 /* IQ4_NL weight encoder (the reference ships none; this build defines it):
  * d = m / -127 (fp16 RNE) with m the first element of largest |x|; per weight
  * the table entry minimising (d * kvalues[n] - x)^2 (first wins), packed as
@@ -1626,6 +1689,7 @@ int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8
             case OC_TYPE_IQ2_XS: oc_encode_iq2xs_block(xb, o); break;
             case OC_TYPE_IQ4_XS: oc_encode_iq4xs_block(xb, o); break;
             case OC_TYPE_IQ4_NL: oc_encode_iq4nl_block(xb, o); break;
+            case OC_TYPE_Q5_0: oc_encode_q50_block(xb, o); break;
             default: oc_encode_iq3xxs_block(xb, o); break;
         }
     }

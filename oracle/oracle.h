@@ -18,13 +18,14 @@
  *   oc_dequant_row  pinned: golden vectors + closed forms on hand-built blocks.
  *   oc_block_isums  pinned: brute-force integer dot of dequantized integer
  *       weights x quantized activations (order-free integer identity).
- *   oc_matmul (Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K/IQ3_XXS/IQ3_S/IQ2_S/IQ2_XS/IQ4_XS/IQ4_NL)  pinned: bit-exact against
+ *   oc_matmul (Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K/IQ3_XXS/IQ3_S/IQ2_S/IQ2_XS/IQ4_XS/IQ4_NL/Q5_0)  pinned: bit-exact against
  *       golden outputs of the compiled reference AVX2 / scalar kernels.
  *   oc_encode_q4k_block  pinned: bit-exact against the compiled reference
  *       quantizeQ4KBlock (golden) + the reference's own round-trip test.
  *   oc_encode_q8_0_block / oc_encode_q2k_block / oc_encode_q3k_block / oc_encode_q5k_block / oc_encode_q6k_block /
  *   oc_encode_iq3xxs_block / oc_encode_iq3s_block / oc_encode_iq2s_block /
- *   oc_encode_iq2xs_block / oc_encode_iq4xs_block / oc_encode_iq4nl_block:
+ *   oc_encode_iq2xs_block / oc_encode_iq4xs_block / oc_encode_iq4nl_block /
+ *   oc_encode_q50_block:
  *       the reference has no encoder for these formats (this build defines
  *       them); pinned by decode round-trip error bounds only.
  *   oc_moe_ffn  pinned: composed of the pinned pieces; golden vectors from the
@@ -40,6 +41,7 @@ extern "C" {
 #endif
 
 enum {
+    OC_TYPE_Q5_0 = 6,
     OC_TYPE_Q8_0 = 8,
     OC_TYPE_Q2_K = 10,
     OC_TYPE_Q3_K = 11,
@@ -96,6 +98,7 @@ void oc_encode_iq2s_block(const float *x, uint8_t *out);
 void oc_encode_iq2xs_block(const float *x, uint8_t *out);
 void oc_encode_iq4xs_block(const float *x, uint8_t *out);
 void oc_encode_iq4nl_block(const float *x, uint8_t *out);
+void oc_encode_q50_block(const float *x, uint8_t *out);
 int oc_encode_rows(int type, const float *x, uint32_t rows, uint32_t cols, uint8_t *out);
 
 /* MoE expert FFN (Q4_K experts), rank-order reduction.

@@ -60,6 +60,7 @@ void ref_dequant_block(int type, const uint8_t *blk, float *out) {
         case 17: GGMLDequantize::dequantizeIQ2_XSBlock(blk, out); break;  // include/GGMLDequantize.hpp:1245
         case 23: GGMLDequantize::dequantizeIQ4_XSBlock(blk, out); break;  // include/GGMLDequantize.hpp:1319
         case 20: GGMLDequantize::dequantizeIQ4_NLBlock(blk, out); break;  // include/GGMLDequantize.hpp:1304
+        case 6: GGMLDequantize::dequantizeQ5_0Block(blk, out); break;  // include/GGMLDequantize.hpp:163
         default: break;
     }
 }
@@ -123,6 +124,18 @@ int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint
                     for (uint32_t b = 0; b < cols / 256; ++b)
                         dot += static_cast<double>(GGMLDequantize::dotProductIQ2_XS(
                             W + (size_t(j) * (cols / 256) + b) * 74, X + size_t(s) * cols + size_t(b) * 256));
+                    out[size_t(s) * rows + j] = static_cast<float>(dot);
+                }
+            return 0;
+        // Q5_0: the same float fused row loop around the reference's own block
+        // dot dotProductQ5_0 (include/GGMLDequantize.hpp:1820), 32-wide blocks.
+        case 6:
+            for (uint32_t s = 0; s < seqLen; ++s)
+                for (uint32_t j = 0; j < rows; ++j) {
+                    double dot = 0.0;
+                    for (uint32_t b = 0; b < cols / 32; ++b)
+                        dot += static_cast<double>(GGMLDequantize::dotProductQ5_0(
+                            W + (size_t(j) * (cols / 32) + b) * 22, X + size_t(s) * cols + size_t(b) * 32));
                     out[size_t(s) * rows + j] = static_cast<float>(dot);
                 }
             return 0;

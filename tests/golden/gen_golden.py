@@ -129,6 +129,15 @@ def iq4nl_random_blocks(rng, nblk):
     return b.ravel()
 
 
+def q50_random_blocks(rng, nblk):
+    """Random Q5_0 bytes (every nibble and high-bit pattern) with normal fp16 d
+    of varied exponent."""
+    b = rng.integers(0, 256, (nblk, 22), dtype=np.uint8)
+    d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-14, -6, nblk)).astype(np.float16)
+    b[:, 0:2] = d.view(np.uint8).reshape(nblk, 2)
+    return b.ravel()
+
+
 def q80_random_blocks(rng, nblk):
     b = rng.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
     d = (rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-10, -6, nblk)).astype(np.float16)
@@ -397,6 +406,20 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.IQ4_NL, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.IQ4_NL, w, X4, rows, cols)
+
+    # Q5_0, likewise: its dequant and the float fused path around the
+    # reference's block dot dotProductQ5_0 (GGMLDequantize.hpp:1820).
+    r5 = np.random.default_rng(20261210)
+    g["deq_q50_w"] = q50_random_blocks(r5, 16)
+    g["deq_q50_y"] = ref.dequant(O.Q5_0, g["deq_q50_w"], 2, 256)
+    cases5 = {
+        "q50_rand": q50_random_blocks(r5, rows * cols // 32),
+        "q50_enc002": O.Oracle().encode(O.Q5_0, (r5.standard_normal((rows, cols)) * 0.02).astype(np.float32)),
+    }
+    for name, w in cases5.items():
+        g[f"mm_{name}_w"] = w
+        g[f"mm_{name}_y1"] = ref.matmul(O.Q5_0, w, X1, rows, cols)
+        g[f"mm_{name}_y4"] = ref.matmul(O.Q5_0, w, X4, rows, cols)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")

@@ -1,13 +1,13 @@
 """Seeded synthetic weight/activation generators shared by the tests."""
 import numpy as np
 
-Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS, IQ4_NL = 8, 10, 11, 12, 13, 14, 17, 18, 21, 22, 23, 20
-TYPE_SIZE = {Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ2_XS: 74, IQ4_XS: 136, IQ4_NL: 18}
-BLOCK_SIZE = {Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256, IQ2_XS: 256, IQ4_XS: 256, IQ4_NL: 32}
-ALL = (Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL)
-# types whose activations are quantized (Q8_K / Q8_0-32); IQ2_XS and IQ4_NL dot fp32 x
-INT8_ACT = tuple(t for t in ALL if t not in (IQ2_XS, IQ4_NL))
-NAMES = {Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ3_XXS: "IQ3_XXS", IQ3_S: "IQ3_S", IQ2_S: "IQ2_S", IQ2_XS: "IQ2_XS", IQ4_XS: "IQ4_XS", IQ4_NL: "IQ4_NL"}
+Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS, IQ4_NL, Q5_0 = 8, 10, 11, 12, 13, 14, 17, 18, 21, 22, 23, 20, 6
+TYPE_SIZE = {Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ2_XS: 74, IQ4_XS: 136, IQ4_NL: 18, Q5_0: 22}
+BLOCK_SIZE = {Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256, IQ2_XS: 256, IQ4_XS: 256, IQ4_NL: 32, Q5_0: 32}
+ALL = (Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0)
+# types whose activations are quantized (Q8_K / Q8_0-32); IQ2_XS, IQ4_NL and Q5_0 dot fp32 x
+INT8_ACT = tuple(t for t in ALL if t not in (IQ2_XS, IQ4_NL, Q5_0))
+NAMES = {Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ3_XXS: "IQ3_XXS", IQ3_S: "IQ3_S", IQ2_S: "IQ2_S", IQ2_XS: "IQ2_XS", IQ4_XS: "IQ4_XS", IQ4_NL: "IQ4_NL", Q5_0: "Q5_0"}
 
 
 def row_bytes(qt, cols):
@@ -35,7 +35,7 @@ def random_blocks(qt, rng, rows, cols):
     elif qt == Q2_K:
         b[:, 80:82] = _fp16_bytes(mag)
         b[:, 82:84] = _fp16_bytes(rng.uniform(1.0, 2.0, nblk) * 2.0 ** rng.integers(-12, -5, nblk))
-    elif qt in (IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL):
+    elif qt in (IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0):
         b[:, 0:2] = _fp16_bytes(mag)
     else:
         b[:, 0:2] = _fp16_bytes(mag)

@@ -105,7 +105,7 @@ def test_quantize_q8_0_act_pinned_by_reference_probe(oracle, golden):
 # ---- block decoders ---------------------------------------------------------------
 
 @pytest.mark.parametrize("name,qt", [("q2k", O.Q2_K), ("q3k", O.Q3_K), ("q4k", O.Q4_K), ("q5k", O.Q5_K), ("q6k", O.Q6_K), ("iq3", O.IQ3_XXS),
-                                     ("iq3s", O.IQ3_S), ("iq2s", O.IQ2_S), ("iq2xs", O.IQ2_XS), ("iq4xs", O.IQ4_XS), ("iq4nl", O.IQ4_NL),
+                                     ("iq3s", O.IQ3_S), ("iq2s", O.IQ2_S), ("iq2xs", O.IQ2_XS), ("iq4xs", O.IQ4_XS), ("iq4nl", O.IQ4_NL), ("q50", O.Q5_0),
                                      ("q80", O.Q8_0)])
 def test_dequant_matches_reference(oracle, golden, name, qt):
     w = golden[f"deq_{name}_w"]
@@ -287,7 +287,8 @@ MM = [("q4k_rand", O.Q4_K), ("q4k_enc1", O.Q4_K), ("q4k_enc002", O.Q4_K), ("q5k_
       ("q2k_enc002", O.Q2_K), ("iq3s_rand", O.IQ3_S),
       ("iq3s_enc002", O.IQ3_S), ("iq2s_rand", O.IQ2_S), ("iq2s_enc002", O.IQ2_S),
       ("iq2xs_rand", O.IQ2_XS), ("iq2xs_enc002", O.IQ2_XS), ("iq4xs_rand", O.IQ4_XS),
-      ("iq4xs_enc002", O.IQ4_XS), ("iq4nl_rand", O.IQ4_NL), ("iq4nl_enc002", O.IQ4_NL), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
+      ("iq4xs_enc002", O.IQ4_XS), ("iq4nl_rand", O.IQ4_NL), ("iq4nl_enc002", O.IQ4_NL),
+      ("q50_rand", O.Q5_0), ("q50_enc002", O.Q5_0), ("q6k_rand", O.Q6_K), ("iq3_rand", O.IQ3_XXS), ("q80_rand", O.Q8_0)]
 
 
 @pytest.mark.parametrize("name,qt", MM)
@@ -306,7 +307,7 @@ def test_matmul_q80_cols96(oracle, golden):
 
 
 @pytest.mark.parametrize("qt", [O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ3_XXS, O.IQ3_S, O.IQ2_S,
-                                O.IQ2_XS, O.IQ4_XS, O.IQ4_NL])
+                                O.IQ2_XS, O.IQ4_XS, O.IQ4_NL, O.Q5_0])
 def test_matmul_close_to_float_dot(oracle, qt):
     """Independent of the reference: the quantized mat-vec approximates the
     float product of the dequantized weights with x (activation quantization
@@ -365,9 +366,9 @@ def test_q4k_encoder_reference_roundtrip_thresholds(oracle):
 
 @pytest.mark.parametrize("qt,bound", [(O.Q8_0, 0.01), (O.Q2_K, 0.45), (O.Q3_K, 0.2), (O.Q5_K, 0.08), (O.Q6_K, 0.04),
                                       (O.IQ3_XXS, 0.25), (O.IQ3_S, 0.2), (O.IQ2_S, 0.35),
-                                      (O.IQ2_XS, 0.4), (O.IQ4_XS, 0.1), (O.IQ4_NL, 0.1)])
+                                      (O.IQ2_XS, 0.4), (O.IQ4_XS, 0.1), (O.IQ4_NL, 0.1), (O.Q5_0, 0.06)])
 def test_own_encoders_roundtrip(oracle, qt, bound):
-    """This build's Q8_0 / Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS / IQ4_NL encoders (the reference has none):
+    """This build's Q8_0 / Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS / IQ4_NL / Q5_0 encoders (the reference has none):
     N(0, 0.02) rows round-trip within the format's expected relative RMS."""
     rng = np.random.default_rng(9)
     x = (rng.standard_normal((16, 1024)) * 0.02).astype(np.float32)
@@ -445,14 +446,15 @@ def test_moe_matches_reference_composition(oracle, golden):
     assert np.allclose(got, ref, rtol=1e-3, atol=1e-4)
 
 
-def test_iq4nl_float_path(oracle, golden):
-    """IQ4_NL: no integer sums (the reference's CPU path dots fp32 x); the
-    mat-vec is linear in x (exact for x scaled by a power of two)."""
-    w = golden["mm_iq4nl_rand_w"]
+@pytest.mark.parametrize("name,qt,tb", [("iq4nl", O.IQ4_NL, 18), ("q50", O.Q5_0, 22)])
+def test_float_path_types(oracle, golden, name, qt, tb):
+    """IQ4_NL and Q5_0: no integer sums (the reference's CPU paths dot fp32
+    x); the mat-vec is linear in x (exact for x scaled by a power of two)."""
+    w = golden[f"mm_{name}_rand_w"]
     x = golden["mm_x1"]
     cols = x.shape[1]
-    rows = len(w) // 18 // (cols // 32)
+    rows = len(w) // tb // (cols // 32)
     with pytest.raises(AssertionError):
-        oracle.block_isums(O.IQ4_NL, w, x, rows, cols)
-    y = oracle.matmul(O.IQ4_NL, w, x, rows, cols)
-    assert (bits(oracle.matmul(O.IQ4_NL, w, 4.0 * x, rows, cols)) == bits(4.0 * y)).all()
+        oracle.block_isums(qt, w, x, rows, cols)
+    y = oracle.matmul(qt, w, x, rows, cols)
+    assert (bits(oracle.matmul(qt, w, 4.0 * x, rows, cols)) == bits(4.0 * y)).all()
