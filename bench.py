@@ -196,7 +196,7 @@ def roof_probes(torch, tc, tc_hip, dev):
 
 def other_decode_bench(torch, tc, tc_hip, dev, reps):
     """BASELINE configs #1 and #3 (batch-1 decode mat-vecs of other formats), and
-    Q5_K, Q3_K, Q2_K, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS and IQ4_NL at the 7B FFN shape:
+    Q5_K, Q3_K, Q2_K, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL and Q5_0 at the 7B FFN shape:
     weights N(0,0.02) through the GPU encoders, rotating copies so that every
     working set exceeds the 256 MB Infinity Cache."""
     gen = torch.Generator(device=dev).manual_seed(11)
@@ -220,6 +220,8 @@ def other_decode_bench(torch, tc, tc_hip, dev, reps):
              ("IQ4_XS gate/up pair 18944x3584 (SwiGLU; format beyond the BASELINE configs)", tc_hip.IQ4_XS, 18944,
               3584, True, 6),
              ("IQ4_NL gate/up pair 18944x3584 (SwiGLU, fp32 x; format beyond the BASELINE configs)", tc_hip.IQ4_NL,
+              18944, 3584, True, 6),
+             ("Q5_0 gate/up pair 18944x3584 (SwiGLU, fp32 x; format beyond the BASELINE configs)", tc_hip.Q5_0,
               18944, 3584, True, 6)]
     res = []
     for name, qt, rows, cols, dual, ncopy in cases:

@@ -9,7 +9,7 @@
  *     the layouts of the reference's int8Gemm/int8Gemv (include/Int8Gemm.hpp:42-107).
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *   - Weight type ids are GGML's: TC_Q8_0 = 8, TC_Q2_K = 10, TC_Q3_K = 11, TC_Q4_K = 12, TC_Q5_K = 13,
- *     TC_Q6_K = 14, TC_IQ2_XS = 17, TC_IQ3_XXS = 18, TC_IQ4_NL = 20, TC_IQ3_S = 21, TC_IQ2_S = 22, TC_IQ4_XS = 23 (reference include/IModelLoader.hpp:51-62).
+ *     TC_Q6_K = 14, TC_IQ2_XS = 17, TC_IQ3_XXS = 18, TC_IQ4_NL = 20, TC_IQ3_S = 21, TC_IQ2_S = 22, TC_IQ4_XS = 23, TC_Q5_0 = 6 (reference include/IModelLoader.hpp:51-62).
  *   - Return value: TC_OK (0) on success, a negative TC_E_* code otherwise;
  *     nothing is written to outputs when a shape or type is refused.
  *     tc_last_error() gives a message for the calling thread's last failure.
@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-enum { TC_Q8_0 = 8, TC_Q2_K = 10, TC_Q3_K = 11, TC_Q4_K = 12, TC_Q5_K = 13, TC_Q6_K = 14, TC_IQ2_XS = 17, TC_IQ3_XXS = 18, TC_IQ4_NL = 20, TC_IQ3_S = 21, TC_IQ2_S = 22, TC_IQ4_XS = 23 };
+enum { TC_Q5_0 = 6, TC_Q8_0 = 8, TC_Q2_K = 10, TC_Q3_K = 11, TC_Q4_K = 12, TC_Q5_K = 13, TC_Q6_K = 14, TC_IQ2_XS = 17, TC_IQ3_XXS = 18, TC_IQ4_NL = 20, TC_IQ3_S = 21, TC_IQ2_S = 22, TC_IQ4_XS = 23 };
 
 enum {
     TC_OK = 0,

@@ -1,5 +1,5 @@
 """GPU parity tests for the prefill GEMM (tc_gemm, int8 MFMA for Q4_K / Q8_0,
-the exact batched mat-vec path (IQ2_XS on fp32 x) for Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ4_XS / IQ4_NL), through the C-ABI.
+the exact batched mat-vec path (IQ2_XS on fp32 x) for Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ4_XS / IQ4_NL / Q5_0), through the C-ABI.
 
 Bar: fp32 outputs within 1e-3 relative / 1e-4 absolute of the oracle (the C
 restatement of the reference CPU kernels, itself bit-exact with the compiled
@@ -9,7 +9,7 @@ the one whose bytes are checked bit-exact in test_gpu_gemv.py.
 import numpy as np
 import pytest
 
-from qdata import ALL, IQ2_S, IQ2_XS, IQ4_NL, IQ4_XS, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
+from qdata import ALL, IQ2_S, IQ2_XS, IQ4_NL, IQ4_XS, Q5_0, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -59,7 +59,7 @@ def test_gemm_random_blocks(tc, dev, oracle, qt):
     assert ok, worst
 
 
-@pytest.mark.parametrize("qt", [Q2_K, Q3_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL])
+@pytest.mark.parametrize("qt", [Q2_K, Q3_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0])
 def test_gemm_exact_batched_types(tc, dev, oracle, qt):
     rng = np.random.default_rng(5 + qt)
     M, N, K = 21, 80, 512

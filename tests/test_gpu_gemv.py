@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from qdata import ALL, INT8_ACT, IQ2_S, IQ2_XS, IQ4_NL, IQ4_XS, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
+from qdata import ALL, INT8_ACT, IQ2_S, IQ2_XS, IQ4_NL, IQ4_XS, Q5_0, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -80,7 +80,7 @@ MM = [("q4k_rand", Q4_K), ("q4k_enc1", Q4_K), ("q4k_enc002", Q4_K),
       ("q5k_rand", Q5_K), ("q5k_enc1", Q5_K), ("q3k_rand", Q3_K), ("q3k_enc002", Q3_K), ("q2k_rand", Q2_K), ("q2k_enc002", Q2_K), ("iq3s_rand", IQ3_S),
       ("iq3s_enc002", IQ3_S), ("iq2s_rand", IQ2_S), ("iq2s_enc002", IQ2_S),
       ("iq2xs_rand", IQ2_XS), ("iq2xs_enc002", IQ2_XS), ("iq4xs_rand", IQ4_XS), ("iq4xs_enc002", IQ4_XS),
-      ("iq4nl_rand", IQ4_NL), ("iq4nl_enc002", IQ4_NL),
+      ("iq4nl_rand", IQ4_NL), ("iq4nl_enc002", IQ4_NL), ("q50_rand", Q5_0), ("q50_enc002", Q5_0),
       ("q6k_rand", Q6_K), ("iq3_rand", IQ3_XXS), ("q80_rand", Q8_0)]
 
 
@@ -123,7 +123,7 @@ def test_gemv_vs_oracle(tc, dev, oracle, qt, S):
 
 @pytest.mark.parametrize("qt,rows,cols", [
     (Q4_K, 3584, 3584), (Q4_K, 512, 3584), (Q4_K, 18944, 3584), (Q4_K, 3584, 18944),
-    (Q8_0, 4096, 4096), (Q6_K, 3584, 18944), (IQ3_XXS, 18944, 3584), (Q5_K, 18944, 3584), (Q3_K, 3584, 18944), (IQ3_S, 18944, 3584), (IQ2_S, 3584, 18944), (Q2_K, 18944, 3584), (IQ2_XS, 18944, 3584), (IQ4_XS, 3584, 18944), (IQ4_NL, 18944, 3584),
+    (Q8_0, 4096, 4096), (Q6_K, 3584, 18944), (IQ3_XXS, 18944, 3584), (Q5_K, 18944, 3584), (Q3_K, 3584, 18944), (IQ3_S, 18944, 3584), (IQ2_S, 3584, 18944), (Q2_K, 18944, 3584), (IQ2_XS, 18944, 3584), (IQ4_XS, 3584, 18944), (IQ4_NL, 18944, 3584), (Q5_0, 3584, 18944), (IQ2_XS, 3584, 18944),
 ])
 def test_gemv_full_shapes(tc, dev, oracle, qt, rows, cols):
     """BASELINE shapes at full size, weights from the GPU encoder on N(0,0.02)
@@ -315,9 +315,9 @@ def test_debug_blocks_hook(tc, dev, oracle, qt):
         assert ok, (b, worst)
 
 
-@pytest.mark.parametrize("qt", [IQ2_XS, IQ4_NL])
+@pytest.mark.parametrize("qt", [IQ2_XS, IQ4_NL, Q5_0])
 def test_float_types_refuse_quantized_activation_entry_points(tc, dev, qt):
-    """IQ2_XS and IQ4_NL dot fp32 x (as their reference CPU paths): the entry
+    """IQ2_XS, IQ4_NL and Q5_0 dot fp32 x (as their reference CPU paths): the entry
     points that hand over quantized activations refuse them without writing."""
     import ctypes
     import torch

@@ -86,11 +86,11 @@ bool ensure(void *&p, size_t &cap, size_t need) {
 // touch: one 128-token tile of 256-byte rows.
 constexpr size_t kGemmActSlack = 128 * 256;
 
-// IQ2_XS and IQ4_NL take fp32 activations (their reference CPU paths do not quantize x):
+// IQ2_XS, IQ4_NL and Q5_0 take fp32 activations (their reference CPU paths do not quantize x):
 // the entry points that hand over quantized activations refuse it.
-bool int8_act_type(int t) { return t != TC_IQ2_XS && t != TC_IQ4_NL; }
+bool int8_act_type(int t) { return t != TC_IQ2_XS && t != TC_IQ4_NL && t != TC_Q5_0; }
 
-bool type_ok(int t) { return t == TC_Q8_0 || t == TC_IQ4_NL || t == TC_IQ4_XS || t == TC_IQ2_XS || t == TC_Q2_K || t == TC_IQ2_S || t == TC_IQ3_S || t == TC_Q3_K || t == TC_Q4_K || t == TC_Q5_K || t == TC_Q6_K || t == TC_IQ3_XXS; }
+bool type_ok(int t) { return t == TC_Q8_0 || t == TC_Q5_0 || t == TC_IQ4_NL || t == TC_IQ4_XS || t == TC_IQ2_XS || t == TC_Q2_K || t == TC_IQ2_S || t == TC_IQ3_S || t == TC_Q3_K || t == TC_Q4_K || t == TC_Q5_K || t == TC_Q6_K || t == TC_IQ3_XXS; }
 
 bool g_q8_gemm_enabled = true;
 
@@ -300,7 +300,7 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
     if (type == TC_Q8_0 && !g_q8_gemm_enabled) return fail(TC_E_UNSUPPORTED, "Q8_0 GEMM disabled");
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (type != TC_Q4_K && type != TC_Q8_0) {
-        // Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS / IQ4_NL: the exact batched path (the reference's launchQGemm,
+        // Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS / IQ4_NL / Q5_0: the exact batched path (the reference's launchQGemm,
         // GpuGemvIQInt8.hpp:771-847) -- the decode kernel over token groups.
         for (uint32_t s0 = 0; s0 < seq_len; s0 += 8) {
             const uint32_t S = std::min(8u, seq_len - s0);

@@ -9,18 +9,18 @@
 namespace tc {
 
 // GGML type ids (reference include/IModelLoader.hpp:51-62).
-enum : int { kQ8_0 = 8, kQ2_K = 10, kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kIQ2_XS = 17, kIQ3_XXS = 18, kIQ3_S = 21, kIQ4_NL = 20, kIQ2_S = 22, kIQ4_XS = 23 };
+enum : int { kQ5_0 = 6, kQ8_0 = 8, kQ2_K = 10, kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kIQ2_XS = 17, kIQ3_XXS = 18, kIQ3_S = 21, kIQ4_NL = 20, kIQ2_S = 22, kIQ4_XS = 23 };
 
 // Every format is handled in "units" of 256 weights. For the K-quants and
 // IQ3_XXS a unit is one GGUF block; for Q8_0 it is 8 consecutive 34-byte
 // blocks (272 bytes, which keeps every unit 16-byte aligned).
 __host__ __device__ constexpr int unit_bytes(int type) {
-    return type == kQ2_K ? 84 : type == kQ3_K ? 110 : type == kQ4_K ? 144 : type == kQ5_K ? 176 : type == kQ6_K ? 210 : type == kIQ3_XXS ? 98 : type == kIQ3_S ? 110 : type == kIQ2_S ? 82 : type == kIQ2_XS ? 74 : type == kIQ4_XS ? 136 : type == kIQ4_NL ? 144 : type == kQ8_0 ? 272 : 0;
+    return type == kQ2_K ? 84 : type == kQ3_K ? 110 : type == kQ4_K ? 144 : type == kQ5_K ? 176 : type == kQ6_K ? 210 : type == kIQ3_XXS ? 98 : type == kIQ3_S ? 110 : type == kIQ2_S ? 82 : type == kIQ2_XS ? 74 : type == kIQ4_XS ? 136 : type == kIQ4_NL ? 144 : type == kQ5_0 ? 176 : type == kQ8_0 ? 272 : 0;
 }
 __host__ __device__ constexpr int block_bytes(int type) {
-    return type == kQ8_0 ? 34 : type == kIQ4_NL ? 18 : unit_bytes(type);
+    return type == kQ8_0 ? 34 : type == kIQ4_NL ? 18 : type == kQ5_0 ? 22 : unit_bytes(type);
 }
-__host__ __device__ constexpr int block_elems(int type) { return type == kQ8_0 || type == kIQ4_NL ? 32 : 256; }
+__host__ __device__ constexpr int block_elems(int type) { return type == kQ8_0 || type == kIQ4_NL || type == kQ5_0 ? 32 : 256; }
 
 // Activations quantized for one call live in one device buffer, per token s:
 //   qs    int8  [S][cols]            (the quantized values)

@@ -564,7 +564,7 @@ constexpr uint32_t XB_BS = 256, XB_D = 288;  // bsums and d offsets inside a rec
 // padded to 1072 bytes: the lanes of a wave read the records of consecutive
 // blocks, and a 1024-byte stride would put them all in the same LDS banks
 // (1072 = 48 mod 256, the residue of the conflict-free 304-byte record).
-__host__ __device__ constexpr uint32_t xrec_bytes(int type) { return type == kIQ2_XS || type == kIQ4_NL ? 1072u : XB; }
+__host__ __device__ constexpr uint32_t xrec_bytes(int type) { return type == kIQ2_XS || type == kIQ4_NL || type == kQ5_0 ? 1072u : XB; }
 
 // 16-byte loads per lane per tile (the last one partial for Q6_K / IQ3_XXS,
 // whose 64-unit tiles are 13440 / 6272 bytes) and the LDS bytes of one tile.
@@ -815,7 +815,7 @@ template <int TYPE, int S, int TNT>
 __device__ __forceinline__ void tstage_finish(const TJobDev &jb, const XRsrc &rs, const XPre &p, unsigned char *xr) {
     const uint32_t tid = threadIdx.x;
     const uint32_t nblk = jb.nx * (jb.cols / 256);
-    if constexpr (TYPE == kIQ2_XS || TYPE == kIQ4_NL) {
+    if constexpr (TYPE == kIQ2_XS || TYPE == kIQ4_NL || TYPE == kQ5_0) {
         // fp32 x as it is: 64-byte chunk c (16 floats) of block c/16 into that
         // block's record
         const uint32_t nchunk = nblk * 16;
@@ -1548,6 +1548,72 @@ struct TDot<kIQ4_NL, S> {
     }
 };
 
+// Q5_0, one unit (8 blocks of 22 B: d, 32 high bits, 16 nibble bytes; 176 B,
+// so 16-byte aligned in LDS) per lane, on fp32 x (the reference's CPU path
+// for this type, dotProductQ5_0, include/GGMLDequantize.hpp:1820-1836, dots
+// unquantized x). Weight j < 16 is the low nibble of byte j with bit j of the
+// high bits as bit 4, weight 16 + j the high nibble with bit 16 + j; value
+// q - 16. Per block d * sum(x * (q - 16)) in fp32 (the reference sums in
+// double), the unit's 8 blocks added in order.
+template <int S>
+struct TDot<kQ5_0, S> {
+    __device__ __forceinline__ static void run(const unsigned char *u, const unsigned char *xr0, size_t xtok,
+                                               float *val, int32_t *dbg, size_t dbg_tok) {
+        (void)dbg;
+        (void)dbg_tok;
+        const uint32_t *u32 = reinterpret_cast<const uint32_t *>(u);
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[s] = 0.0f;
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {  // block pairs: 44 B = 11 dwords
+            uint32_t wd[11];
+#pragma unroll
+            for (int k = 0; k < 11; ++k) wd[k] = u32[11 * pr + k];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int blk = 2 * pr + h;
+                uint32_t q[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) q[k] = h == 0 ? align2(wd[k + 2], wd[k + 1], 2) : wd[7 + k];
+                const uint32_t qh = h == 0 ? align2(wd[1], wd[0], 2) : wd[6];
+                const float d = h2f(h == 0 ? (wd[0] & 0xFFFFu) : (wd[5] >> 16));
+                // bytes 0..31 of the block's weights: w[k] elements 4k.., w[4+k] 16+4k..
+                uint32_t wb[8];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t lo = (qh >> (4 * k)) & 15u, hi = (qh >> (16 + 4 * k)) & 15u;
+                    wb[k] = (q[k] & 0x0F0F0F0Fu) | (((lo * 0x00204081u) & 0x01010101u) << 4);
+                    wb[4 + k] = ((q[k] >> 4) & 0x0F0F0F0Fu) | (((hi * 0x00204081u) & 0x01010101u) << 4);
+                }
+                float w[32];
+#pragma unroll
+                for (int e = 0; e < 32; ++e) w[e] = float(int((wb[e >> 2] >> (8 * (e & 3))) & 0xFFu) - 16);
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const float4 *xp = reinterpret_cast<const float4 *>(xr0 + s * xtok) + 8 * blk;
+                    float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const float4 a = xp[c], b = xp[4 + c];
+                        p0 = fmaf(a.x, w[4 * c], p0);
+                        p0 = fmaf(a.y, w[4 * c + 1], p0);
+                        p0 = fmaf(a.z, w[4 * c + 2], p0);
+                        p0 = fmaf(a.w, w[4 * c + 3], p0);
+                        p1 = fmaf(b.x, w[16 + 4 * c], p1);
+                        p1 = fmaf(b.y, w[16 + 4 * c + 1], p1);
+                        p1 = fmaf(b.z, w[16 + 4 * c + 2], p1);
+                        p1 = fmaf(b.w, w[16 + 4 * c + 3], p1);
+                    }
+                    acc[s] = fmaf(d, p0 + p1, acc[s]);
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) val[s] = acc[s];
+    }
+};
+
 // IQ2_XS, one unit (74 B, 2-byte aligned in LDS) per lane, on fp32 x (the
 // reference's CPU path for this type, dotProductIQ2_XS, dots unquantized x;
 // include/GGMLDequantize.hpp:1901-1927): per 8 weights one 16-bit entry --
@@ -1997,7 +2063,7 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
     return o;
 }
 
-bool tiled_type(int type) { return type == kIQ4_NL || type == kIQ4_XS || type == kIQ2_XS || type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
+bool tiled_type(int type) { return type == kQ5_0 || type == kIQ4_NL || type == kIQ4_XS || type == kIQ2_XS || type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
 // Matrices one workgroup streams per row range: 2 for a gate/up pair, rk in
 // rank-group mode, else 1.
@@ -2087,6 +2153,7 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         case kIQ2_XS: return launch_tiled<kIQ2_XS, C>(S, a, wg, lds, st);
         case kIQ4_XS: return launch_tiled<kIQ4_XS, C>(S, a, wg, lds, st);
         case kIQ4_NL: return launch_tiled<kIQ4_NL, C>(S, a, wg, lds, st);
+        case kQ5_0: return launch_tiled<kQ5_0, C>(S, a, wg, lds, st);
         case kQ6_K: return launch_tiled<kQ6_K, C>(S, a, wg, lds, st);
         case kIQ3_XXS: return launch_tiled<kIQ3_XXS, C>(S, a, wg, lds, st);
         case kQ8_0:
@@ -2107,9 +2174,23 @@ uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs) {
 
 namespace {
 
+// Types whose activations are staged as fp32 (1072 bytes per 256): at wide
+// inputs (the 18944-column down projection) only the 256-thread shape, with
+// half the wave tile slots, fits its records in LDS.
+bool fp32_act_type(int type) { return type == kIQ2_XS || type == kIQ4_NL || type == kQ5_0; }
+
+template <class C>
+bool tiled_fits(int type, uint32_t S, uint32_t cols) {
+    TLaunchArgs a;
+    return tlds_layout<C>(type, S, cols, &a) + 2 * 8 * S * (cols / 256) * 4 <= kTLdsBudget;
+}
+
 hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t njobs, int num_cu,
                              hipStream_t st) {
-    return use_big(type, jobs_weight_bytes(type, jobs, njobs))
+    bool big_fits = true;
+    if (fp32_act_type(type))
+        for (uint32_t i = 0; i < njobs; ++i) big_fits = big_fits && tiled_fits<CfgBig>(type, S, jobs[i].cols);
+    return big_fits && use_big(type, jobs_weight_bytes(type, jobs, njobs))
                ? launch_gemv_tiled_c<CfgBig>(type, S, jobs, njobs, num_cu, st)
                : launch_gemv_tiled_c<CfgSmall>(type, S, jobs, njobs, num_cu, st);
 }
@@ -2118,7 +2199,7 @@ hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t
 
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes) {
     // S*cols up to which the tiled kernels preload all of x ahead of the weights
-    if (!tiled_type(type) || type == kIQ2_XS || type == kIQ4_NL) return 0xFFFFFFFFu;  // fp32 x, never pre-quantized
+    if (!tiled_type(type) || type == kIQ2_XS || type == kIQ4_NL || type == kQ5_0) return 0xFFFFFFFFu;  // fp32 x, never pre-quantized
     return uint32_t(kXPre) * (use_big(type, weight_bytes) ? CfgBig::NT : CfgSmall::NT) * 16u;
 }
 
@@ -2128,7 +2209,10 @@ uint32_t gemv_max_tokens(int type, uint32_t cols) {
         for (uint32_t S = 1; S <= 8; ++S) {
             TLaunchArgs a;
             const uint32_t f = std::max(tlds_layout<CfgBig>(type, S, cols, &a), tlds_layout<CfgSmall>(type, S, cols, &a));
-            if ((type != kQ8_0 ? f : tlds_layout<CfgSmall>(type, S, cols, &a)) + 2 * 8 * S * (cols / 256) * 4 <=
+            // Q8_0 and (when the 512-thread shape does not fit) the fp32
+            // activation types launch the 256-thread shape only
+            const bool small_only = type == kQ8_0 || fp32_act_type(type);
+            if ((small_only ? tlds_layout<CfgSmall>(type, S, cols, &a) : f) + 2 * 8 * S * (cols / 256) * 4 <=
                 kTLdsBudget)
                 best = S;
         }

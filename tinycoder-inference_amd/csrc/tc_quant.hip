@@ -600,6 +600,33 @@ __device__ void enc_iq4nl(const float *x, uint8_t *out) {
     }
 }
 
+// Q5_0 (this build's encoder; the reference ships none): per 32-block d =
+// m / -16 (fp16 RNE) with m the first element of largest |x|; q =
+// clamp(rne(x / d) + 16, 0, 31), packed as the reference decoder reads it
+// (include/GGMLDequantize.hpp:163-185). One unit is 8 blocks (176 bytes).
+__device__ void enc_q50(const float *x, uint8_t *out) {
+    for (int b = 0; b < 8; ++b) {
+        const float *xb = x + 32 * b;
+        uint8_t *o = out + 22 * b;
+        float m = 0.0f;
+        for (int i = 0; i < 32; ++i) m = fabsf(xb[i]) > fabsf(m) ? xb[i] : m;
+        for (int i = 0; i < 22; ++i) o[i] = 0;
+        const uint16_t hd = f2h_rne(__fdiv_rn(m, -16.0f));
+        const float d = h2f(hd);
+        if (d == 0.0f || d != d) continue;
+        o[0] = uint8_t(hd);
+        o[1] = uint8_t(hd >> 8);
+        uint32_t qh = 0;
+        for (int j = 0; j < 32; ++j) {
+            int q = int(rintf(__fdiv_rn(xb[j], d))) + 16;
+            q = q < 0 ? 0 : (q > 31 ? 31 : q);
+            o[6 + (j & 15)] |= uint8_t(j < 16 ? (q & 15) : (q & 15) << 4);
+            qh |= uint32_t(q >> 4) << j;
+        }
+        for (int i = 0; i < 4; ++i) o[2 + i] = uint8_t(qh >> (8 * i));
+    }
+}
+
 __device__ void enc_iq4xs(const float *x, uint8_t *out) {
     float sc[8], smax = 0.0f;
     for (int c = 0; c < 8; ++c) {
@@ -716,6 +743,7 @@ __global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict
         case kIQ2_XS: enc_iq2xs(xu, o); break;
         case kIQ4_XS: enc_iq4xs(xu, o); break;
         case kIQ4_NL: enc_iq4nl(xu, o); break;
+        case kQ5_0: enc_q50(xu, o); break;
         default: enc_iq3xxs(xu, o); break;
     }
 }

@@ -11,10 +11,10 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtc_hip.so")
 
-Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS, IQ4_NL = 8, 10, 11, 12, 13, 14, 17, 18, 21, 22, 23, 20
-TYPES = {"Q8_0": Q8_0, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "IQ3_XXS": IQ3_XXS, "IQ3_S": IQ3_S, "IQ2_S": IQ2_S, "IQ2_XS": IQ2_XS, "IQ4_XS": IQ4_XS, "IQ4_NL": IQ4_NL}
-TYPE_SIZE = {Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ2_XS: 74, IQ4_XS: 136, IQ4_NL: 18}
-BLOCK_SIZE = {Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256, IQ2_XS: 256, IQ4_XS: 256, IQ4_NL: 32}
+Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ4_XS, IQ4_NL, Q5_0 = 8, 10, 11, 12, 13, 14, 17, 18, 21, 22, 23, 20, 6
+TYPES = {"Q8_0": Q8_0, "Q2_K": Q2_K, "Q3_K": Q3_K, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K, "IQ3_XXS": IQ3_XXS, "IQ3_S": IQ3_S, "IQ2_S": IQ2_S, "IQ2_XS": IQ2_XS, "IQ4_XS": IQ4_XS, "IQ4_NL": IQ4_NL, "Q5_0": Q5_0}
+TYPE_SIZE = {Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ2_XS: 74, IQ4_XS: 136, IQ4_NL: 18, Q5_0: 22}
+BLOCK_SIZE = {Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256, IQ2_XS: 256, IQ4_XS: 256, IQ4_NL: 32, Q5_0: 32}
 
 TC_OK, TC_E_UNSUPPORTED, TC_E_LAUNCH, TC_E_ARG = 0, -1, -2, -3
 
