@@ -59,6 +59,27 @@ def test_row_bytes():
     assert lib.tc_row_bytes(9, 256) == 0  # Q8_1: not a weight type here
 
 
+def test_type_ids_and_block_geometry():
+    """The header's TC_* type ids are the binding's, and each type's row size
+    is its GGUF block geometry as the GGUF reader's own table gives it (that
+    table is checked against the reference loader in test_gguf.py). IQ2_XXS
+    (16) and the reference's own formats are not weight types here."""
+    import tc_hip
+    lib = tc_hip.load_library()
+    text = open(os.path.join(ROOT, "include", "tc_qmatmul.h")).read()
+    enum = dict((m.group(1), int(m.group(2))) for m in re.finditer(r"\bTC_([A-Z0-9_]+) = (\d+)", text)
+                if not m.group(1).startswith("E_") and m.group(1) != "OK")
+    assert {k: v for k, v in enum.items() if k in tc_hip.TYPES} == tc_hip.TYPES
+    assert set(tc_hip.TYPES) <= set(enum)
+    for name, t in tc_hip.TYPES.items():
+        bs, ts = lib.tc_gguf_block_size(t), lib.tc_gguf_type_size(t)
+        assert (bs, ts) == (tc_hip.BLOCK_SIZE[t], tc_hip.TYPE_SIZE[t]), name
+        assert lib.tc_row_bytes(t, 18944) == 18944 // bs * ts, name
+        assert lib.tc_row_bytes(t, 3584) == 3584 // bs * ts, name
+    for t in (0, 1, 16, 142, 143, 200):
+        assert lib.tc_row_bytes(t, 256) == 0, t
+
+
 def test_reference_interface_header_compiles_and_links(tmp_path):
     """include/tc_int8gemm.hpp (the reference's tinycoder::gpu interface over
     the C ABI) compiles as C++17, links against the library, and reports no
