@@ -15,10 +15,11 @@
  *     tc_last_error() gives a message for the calling thread's last failure.
  *   - Numerics: activations are quantized with the reference CPU rule for the
  *     weight type (Q8_K, 256-wide, for Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ4_XS;
- *     IQ2_XS takes fp32 activations unquantized, as its reference CPU path
- *     (dotProductIQ2_XS) does, so the quantized-activation entry points
+ *     IQ2_XS, IQ4_NL and Q5_0 take fp32 activations unquantized, as their
+ *     reference CPU paths (dotProductIQ2_XS, matMulVecBatchIQ4NL_Q8K_AVX2,
+ *     dotProductQ5_0) do, so the quantized-activation entry points
  *     (tc_act_quantize, tc_gemv_q8, tc_quantize_act, tc_block_isums,
- *     tc_debug_q8k_blocks) refuse it; 32-wide with an
+ *     tc_debug_q8k_blocks) refuse them; 32-wide with an
  *     fp32 scale for Q8_0), bit-identical to the CPU; per-block integer sums are
  *     exact; fp32 outputs agree with the CPU reference within 1e-3 relative /
  *     1e-4 absolute.
