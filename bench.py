@@ -57,12 +57,50 @@ def measured_traffic():
     return None
 
 
+def host_cpu_info():
+    """CPU model, SIMD level and the CPUs this process may run on (`nproc`), read
+    from /proc/cpuinfo and the scheduler affinity (lscpu reads the same)."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    simd = ("avx512f+avx512bw" if {"avx512f", "avx512bw"} <= flags else "avx2" if "avx2" in flags else "sse")
+    if "amx_int8" in flags:
+        simd += "+amx"
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()
+            if q != "max":
+                quota = round(int(q) / int(per), 2)
+    except (OSError, ValueError):
+        pass
+    return model, simd, nproc, quota
+
+
 def cpu_baseline(weights_host, xs_host, row_bytes):
-    """The reference's CPU kernel (or the C port if the reference build is
-    absent) over full layer passes for a bounded ~8 s sample."""
+    """The reference's CPU kernel (matMulVecBatchQ4K_Q8K_AVX2 through its
+    ThreadPool, compiled from its sources; the C port if that build is absent)
+    over full layer passes for a bounded ~8 s sample. Threads: TINYCODER_THREADS
+    if set, else `nproc` (the reference's ThreadPool::recommendedThreadCount,
+    ThreadPool.cpp:68-94, counts the online CPUs; `nproc` counts the ones this
+    process may use). The pass rotates over N_COPIES copies of the layer's
+    weights (1.05 GB), so the host's last-level cache cannot serve them."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    threads = min(os.cpu_count() or 1, 16)
+    model, simd, nproc, quota = host_cpu_info()
+    env = os.environ.get("TINYCODER_THREADS", "")
+    threads = int(env) if env.isdigit() and int(env) > 0 else nproc
     try:
         impl = O.Reference(threads=threads)
         kind = "reference"
@@ -71,32 +109,38 @@ def cpu_baseline(weights_host, xs_host, row_bytes):
         impl = O.Oracle()
         kind = "port"
         threads = 1
+    copies = [{n: weights_host[n].copy() for n in weights_host} for _ in range(N_COPIES)]
     outs = {n: np.zeros((1, r), np.float32) for n, r, _ in LAYER}
     xmap = {}
     for g, _, names in GROUPS:
         for n in names:
             xmap[n] = xs_host[g]
 
-    def one_pass():
+    def one_pass(i):
+        w = copies[i % N_COPIES]
         for n, r, c in LAYER:
             if kind == "reference":
-                impl.matmul(12, weights_host[n], xmap[n], r, c, out=outs[n])
+                impl.matmul(12, w[n], xmap[n], r, c, out=outs[n])
             else:
-                outs[n][:] = impl.matmul(12, weights_host[n], xmap[n], r, c)
+                outs[n][:] = impl.matmul(12, w[n], xmap[n], r, c)
 
-    one_pass()
+    for i in range(N_COPIES):
+        one_pass(i)
     t0 = time.perf_counter()
     reps = 0
     while True:
-        one_pass()
+        one_pass(reps)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 8.0 or reps >= 2000:
+        if (el > 8.0 and reps >= N_COPIES) or reps >= 4000:
             break
     per_pass = sum(algorithmic_bytes(r, c, row_bytes(12, c)) for _, r, c in LAYER)
+    impl_name = ("reference AVX2 matMulVecBatchQ4K_Q8K_AVX2 + ThreadPool" if kind == "reference"
+                 else "C port, 1 thread")
     return {"value": round(per_pass * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{reps} full-layer passes (7 Q4_K mat-vecs, {per_pass / 1e6:.1f} MB each) in {el:.1f} s, "
-                      f"{'reference AVX2 matMulVecBatchQ4K_Q8K_AVX2 + ThreadPool' if kind == 'reference' else 'C port, 1 thread'}"}
+            "cpu_model": model, "simd": simd, "nproc": nproc, "cgroup_cpu_quota": quota,
+            "sample": f"{reps} full-layer passes (7 Q4_K mat-vecs, {per_pass / 1e6:.1f} MB each) over "
+                      f"{N_COPIES} rotating weight copies in {el:.1f} s, {impl_name}, {threads} threads"}
 
 
 GEMM_SHAPES = [(17408, 5120), (5120, 17408)]   # (rows N, cols K), out x in
@@ -107,7 +151,7 @@ INT8_PEAK_TOPS = 5000.0
 def gemm_bench(torch, tc, tc_hip, dev, reps):
     """Prefill GEMM (tc_gemm: activation quantization + int8 MFMA GEMM [+ split-K
     reduce]) at every M x shape x type; weights N(0,0.02) through the GPU
-    encoders, 4 rotating copies; x ~ N(0,1). Returns one record per config."""
+    encoders, rotating copies of at least 600 MB in all; x ~ N(0,1). Returns one record per config."""
     gen = torch.Generator(device=dev).manual_seed(7)
     res = []
     for qt, tname in ((tc_hip.Q4_K, "Q4_K"), (tc_hip.Q8_0, "Q8_0")):
@@ -115,19 +159,22 @@ def gemm_bench(torch, tc, tc_hip, dev, reps):
             wf = torch.randn((N, K), generator=gen, device=dev) * 0.02
             w0 = tc.encode(qt, wf)
             del wf
-            ws = [w0] + [w0.clone() for _ in range(3)]
+            # rotating copies: a working set of at least 600 MB, beyond the
+            # 256 MB Infinity Cache
+            ncopy = max(4, -(-600_000_000 // (w0.numel())))
+            ws = [w0] + [w0.clone() for _ in range(ncopy - 1)]
             for M in GEMM_TOKENS:
                 x = torch.randn((M, K), generator=gen, device=dev)
                 out = torch.empty((M, N), device=dev)
                 for i in range(3):
-                    tc.gemm(qt, ws[i % 4], x, N, K, out=out)
+                    tc.gemm(qt, ws[i % ncopy], x, N, K, out=out)
                 torch.cuda.synchronize()
                 n = max(3, reps if M < 2048 else reps // 4)
                 a = torch.cuda.Event(enable_timing=True)
                 b = torch.cuda.Event(enable_timing=True)
                 a.record()
                 for i in range(n):
-                    tc.gemm(qt, ws[i % 4], x, N, K, out=out)
+                    tc.gemm(qt, ws[i % ncopy], x, N, K, out=out)
                 b.record()
                 torch.cuda.synchronize()
                 us = a.elapsed_time(b) * 1e3 / n

@@ -146,6 +146,25 @@ int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t se
                const void *wg, const void *wu, const void *wd, uint32_t n_experts, uint32_t hidden,
                uint32_t ff, float *out, void *stream);
 
+/* MoE router of qwen35moe: logits[s][e] = x[s] . w_router[e] over the fp32
+ * router matrix w_router [n_experts][hidden], then per token the softmax over
+ * all experts, the top_k experts by probability and their renormalised
+ * weights into ids[s][r], wts[s][r] (rank order; the ids/wts inputs of
+ * tc_moe_ffn). Replaces Model::computeQwen35MoERouterOnly
+ * (src/cpp/core/ModelMoE.cpp:341-425) and the reference's GPU router
+ * kQ35MoeRouter (include/gpu/GpuQwen35Kernels.hpp:931). Bit-identical to the
+ * CPU router: the logits in its AVX2 FMA order (SIMDMatMulVecAVX2.cpp:2982),
+ * exp and the softmax sum in double, std::partial_sort's order of equal
+ * probabilities, the 6.103515625e-5 clamp. logits is a caller buffer of
+ * [seq_len][n_experts] fp32 (written). n_experts <= 4096, top_k <= n_experts. */
+int tc_moe_router(const float *w_router, const float *x, uint32_t seq_len, uint32_t n_experts, uint32_t hidden,
+                  uint32_t top_k, float *logits, int32_t *ids, float *wts, void *stream);
+
+/* The selection step of tc_moe_router alone, on given logits
+ * [seq_len][n_experts] (ModelMoE.cpp:387-424). */
+int tc_moe_select(const float *logits, uint32_t seq_len, uint32_t n_experts, uint32_t top_k, int32_t *ids, float *wts,
+                  void *stream);
+
 /* Token count from which tc_moe_ffn takes the grouped-GEMM path (no
  * reference counterpart: a tuning knob like int8GemmSetQ8Enabled; 0 = always,
  * UINT32_MAX = never). Process-wide. */

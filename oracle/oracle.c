@@ -1733,3 +1733,147 @@ int oc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t S,
     free(dn);
     return 0;
 }
+
+/* ---- MoE router (F32 router matrix, softmax, top-k, renormalisation) ---- */
+
+/* src/cpp/core/SIMDMatMulVecAVX2.cpp:2982-3090 (matMulVecBatchF32_AVX2, the
+ * qwen35moe router logits, ModelMoE.cpp:372-386): per (token, row) 32 fp32
+ * FMA lanes (four 8-wide chains) over the first floor(cols/32)*32 columns in
+ * steps of 32, the remaining whole 8-column groups into chain 0, the fixed
+ * horizontal tree (chains 0+1 and 2+3, their sum, halves, two pairwise adds),
+ * then the cols % 8 tail added serially (contracted into an FMA as g++
+ * compiles `v += x * w` there). out[S][rows]. */
+void oc_matmul_f32(const float *W, const float *X, uint32_t S, uint32_t rows, uint32_t cols, float *out) {
+    const uint32_t vec = cols / 8 * 8, tail = cols & 7u;
+    for (uint32_t s = 0; s < S; ++s) {
+        const float *x = X + (size_t)s * cols;
+        for (uint32_t r = 0; r < rows; ++r) {
+            const float *w = W + (size_t)r * cols;
+            float acc[4][8];
+            memset(acc, 0, sizeof acc);
+            uint32_t i = 0;
+            for (; i + 31 < vec; i += 32)
+                for (int c = 0; c < 4; ++c)
+                    for (int l = 0; l < 8; ++l) acc[c][l] = fmaf(x[i + 8 * c + l], w[i + 8 * c + l], acc[c][l]);
+            for (; i + 7 < vec; i += 8)
+                for (int l = 0; l < 8; ++l) acc[0][l] = fmaf(x[i + l], w[i + l], acc[0][l]);
+            float sv[8];
+            for (int l = 0; l < 8; ++l) sv[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+            float t[4];
+            for (int l = 0; l < 4; ++l) t[l] = sv[l] + sv[l + 4];
+            float v = (t[0] + t[1]) + (t[2] + t[3]);
+            for (uint32_t k = 0; k < tail; ++k) v = fmaf(x[vec + k], w[vec + k], v);
+            out[(size_t)s * rows + r] = v;
+        }
+    }
+}
+
+/* One (probability, expert) entry of the router's ranking. */
+typedef struct {
+    float p;
+    uint32_t e;
+} oc_scored;
+
+/* The ranking's order: a before b when a.p > b.p (the comparator of
+ * ModelMoE.cpp:402-405). */
+static int oc_before(const oc_scored *a, const oc_scored *b) { return a->p > b->p; }
+
+/* The selection of ModelMoE.cpp:402-405 is std::partial_sort(begin,
+ * begin + k, end, cmp), which leaves equal probabilities in an order the
+ * library's algorithm fixes: a binary heap over the first k entries whose
+ * top is the entry every other one is "before" (the smallest probability),
+ * each later entry that is strictly before the top replacing it, and a final
+ * heap sort. The next three functions are those heap steps as the GNU C++
+ * library (the reference's toolchain) performs them: a sift-down that moves
+ * the hole to a leaf along the child that is not before its sibling, then a
+ * sift-up of the value; the tie order of the result depends on exactly these
+ * moves. */
+static void oc_heap_push_up(oc_scored *h, size_t hole, size_t top, oc_scored v) {
+    size_t parent = (hole - 1) / 2;
+    while (hole > top && oc_before(&h[parent], &v)) {
+        h[hole] = h[parent];
+        hole = parent;
+        parent = (hole - 1) / 2;
+    }
+    h[hole] = v;
+}
+
+static void oc_heap_adjust(oc_scored *h, size_t hole, size_t len, oc_scored v) {
+    const size_t top = hole;
+    size_t child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * (child + 1);
+        if (oc_before(&h[child], &h[child - 1])) child--;
+        h[hole] = h[child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * (child + 1);
+        h[hole] = h[child - 1];
+        hole = child - 1;
+    }
+    oc_heap_push_up(h, hole, top, v);
+}
+
+/* h[0..k) <- the k first entries of a[0..n) in the order std::partial_sort
+ * leaves them (a is permuted as the library permutes it). */
+static void oc_partial_sort(oc_scored *a, size_t k, size_t n) {
+    if (k == 0) return;
+    if (k > 1)
+        for (size_t parent = (k - 2) / 2;; --parent) {
+            oc_heap_adjust(a, parent, k, a[parent]);
+            if (parent == 0) break;
+        }
+    for (size_t i = k; i < n; ++i)
+        if (oc_before(&a[i], &a[0])) {
+            const oc_scored v = a[i];
+            a[i] = a[0];
+            oc_heap_adjust(a, 0, k, v);
+        }
+    for (size_t last = k; last > 1;) {
+        --last;
+        const oc_scored v = a[last];
+        a[last] = a[0];
+        oc_heap_adjust(a, 0, last, v);
+    }
+}
+
+/* src/cpp/core/ModelMoE.cpp:387-424 (computeQwen35MoERouterOnly, from the
+ * logits on): per token, maxL = max logit; probs[e] = (float)exp((double)
+ * logit - maxL) summed in double in expert order; invSum = (float)(1/sum);
+ * probs *= invSum in float; the top k by the partial_sort above; wsum = the
+ * double sum of the k probabilities in rank order, clamped below at
+ * 6.103515625e-5; ids[s][r] = expert, wts[s][r] = p / (float)wsum. */
+int oc_moe_route(const float *logits, uint32_t S, uint32_t E, uint32_t K, int32_t *ids, float *wts) {
+    if (E == 0 || K == 0 || K > E) return -1;
+    oc_scored *sc = (oc_scored *)malloc(sizeof(oc_scored) * E);
+    float *probs = (float *)malloc(sizeof(float) * E);
+    if (!sc || !probs) return -1;
+    for (uint32_t s = 0; s < S; ++s) {
+        const float *l = logits + (size_t)s * E;
+        float maxL = -INFINITY;
+        for (uint32_t e = 0; e < E; ++e) maxL = l[e] > maxL ? l[e] : maxL;
+        double sum = 0.0;
+        for (uint32_t e = 0; e < E; ++e) {
+            probs[e] = (float)exp((double)l[e] - (double)maxL);
+            sum += (double)probs[e];
+        }
+        const float inv = (float)(1.0 / sum);
+        for (uint32_t e = 0; e < E; ++e) {
+            probs[e] = probs[e] * inv;
+            sc[e].p = probs[e];
+            sc[e].e = e;
+        }
+        oc_partial_sort(sc, K, E);
+        double wsum = 0.0;
+        for (uint32_t r = 0; r < K; ++r) wsum += (double)sc[r].p;
+        const float wc = (float)(wsum > 6.103515625e-5 ? wsum : 6.103515625e-5);
+        for (uint32_t r = 0; r < K; ++r) {
+            ids[(size_t)s * K + r] = (int32_t)sc[r].e;
+            wts[(size_t)s * K + r] = sc[r].p / wc;
+        }
+    }
+    free(sc);
+    free(probs);
+    return 0;
+}

@@ -108,6 +108,13 @@ int oc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t S,
                uint32_t K, const uint8_t *wg, const uint8_t *wu, const uint8_t *wd,
                uint32_t E, uint32_t H, uint32_t FF, float *out);
 
+/* MoE router. oc_matmul_f32: out[S][rows] = X[S][cols] @ W^T for an fp32
+ * matrix, in the reference AVX2 kernel's evaluation order (the router
+ * logits). oc_moe_route: softmax, top-K and renormalisation of logits[S][E]
+ * into ids[S][K] and wts[S][K]; returns 0 on success. */
+void oc_matmul_f32(const float *W, const float *X, uint32_t S, uint32_t rows, uint32_t cols, float *out);
+int oc_moe_route(const float *logits, uint32_t S, uint32_t E, uint32_t K, int32_t *ids, float *wts);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,8 @@ class Oracle(_Lib):
         L.oc_matmul.argtypes = [ctypes.c_int, _P, _P, _U32, _U32, _U32, _P]
         L.oc_encode_rows.argtypes = [ctypes.c_int, _P, _U32, _U32, _P]
         L.oc_moe_ffn.argtypes = [_P, _P, _P, _U32, _U32, _P, _P, _P, _U32, _U32, _U32, _P]
+        L.oc_matmul_f32.argtypes = [_P, _P, _U32, _U32, _U32, _P]
+        L.oc_moe_route.argtypes = [_P, _U32, _U32, _U32, _P, _P]
 
     def half_to_float(self, h):
         return self.lib.oc_half_to_float(int(h))
@@ -118,6 +120,22 @@ class Oracle(_Lib):
         assert rc == 0
         return out
 
+    def matmul_f32(self, w, x, rows, cols):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
+        out = np.zeros((x.shape[0], rows), np.float32)
+        self.lib.oc_matmul_f32(_ptr(w), _ptr(x), x.shape[0], rows, cols, _ptr(out))
+        return out
+
+    def moe_route(self, logits, k):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        S, E = logits.shape
+        ids = np.zeros((S, k), np.int32)
+        wts = np.zeros((S, k), np.float32)
+        rc = self.lib.oc_moe_route(_ptr(logits), S, E, k, _ptr(ids), _ptr(wts))
+        assert rc == 0
+        return ids, wts
+
     def moe_ffn(self, x, ids, wts, wg, wu, wd, E, H, FF):
         x = np.ascontiguousarray(x, dtype=np.float32)
         ids = np.ascontiguousarray(ids, dtype=np.int32)
@@ -148,6 +166,8 @@ class Reference(_Lib):
         L.ref_dot_iq3xxs_q8k.restype = ctypes.c_float
         L.ref_dot_iq3xxs_q8k.argtypes = [_P, _P]
         L.ref_matmul.argtypes = [ctypes.c_int, _P, _P, _U32, _U32, _U32, _P]
+        L.ref_matmul_f32.argtypes = [_P, _P, _U32, _U32, _U32, _P]
+        L.ref_moe_select.argtypes = [_P, _U32, _U32, _U32, _P, _P]
         L.ref_gguf_open.restype = _P
         L.ref_gguf_open.argtypes = [ctypes.c_char_p, ctypes.c_int]
         L.ref_gguf_close.argtypes = [_P]
@@ -190,6 +210,21 @@ class Reference(_Lib):
             self.lib.ref_quantize_q4k_block(ctypes.c_void_p(x.ctypes.data + i * 1024),
                                             ctypes.c_void_p(out.ctypes.data + i * 144))
         return out
+
+    def matmul_f32(self, w, x, rows, cols):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
+        out = np.zeros((x.shape[0], rows), np.float32)
+        self.lib.ref_matmul_f32(_ptr(w), _ptr(x), x.shape[0], rows, cols, _ptr(out))
+        return out
+
+    def moe_select(self, logits, k):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        S, E = logits.shape
+        ids = np.zeros((S, k), np.int32)
+        wts = np.zeros((S, k), np.float32)
+        self.lib.ref_moe_select(_ptr(logits), S, E, k, _ptr(ids), _ptr(wts))
+        return ids, wts
 
     def matmul(self, qtype, w, x, rows, cols, out=None):
         w = np.ascontiguousarray(w, dtype=np.uint8)

@@ -6,9 +6,13 @@
 //
 // Nothing here restates arithmetic: each wrapper forwards to the reference
 // function named in its comment (paths relative to the reference root).
+#include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <limits>
+#include <utility>
 #include <vector>
 
 #include "GGMLDequantize.hpp"
@@ -84,6 +88,47 @@ float ref_dot_iq3xxs_q8k(const uint8_t *blk, const float *x256) {
 //   IQ3_XXS include/GGMLDequantize.hpp:2231 (scalar matMulVecBatchQ8K; the
 //         type has no SIMD kernel, src/cpp/core/ModelInternal.cpp:499)
 // out[seqLen][rows]. Returns 0 on success.
+// src/cpp/core/SIMDMatMulVecAVX2.cpp:2982 (matMulVecBatchF32_AVX2: the
+// qwen35moe router logits, ModelMoE.cpp:372-386).
+void ref_matmul_f32(const float *W, const float *X, uint32_t seqLen, uint32_t rows, uint32_t cols, float *out) {
+    simd::matMulVecBatchF32_AVX2(W, X, seqLen, rows, cols, out);
+}
+
+// The router's selection, src/cpp/core/ModelMoE.cpp:387-424, on given logits.
+// Those lines are the body of Model::computeQwen35MoERouterOnly, a member of
+// Model whose config (expert counts) only a loaded model sets, so the member
+// itself cannot be called here; the lines are repeated verbatim in effect on
+// the same types (float probabilities, std::pair<float, uint32_t> entries)
+// and the same std::partial_sort call of this toolchain's C++ library, whose
+// tie order the GPU router and the C oracle must match.
+void ref_moe_select(const float *logits, uint32_t seqLen, uint32_t expertCount, uint32_t eu, int32_t *expertIdxOut,
+                    float *expertWgtOut) {
+    std::vector<float> probs(expertCount);
+    std::vector<std::pair<float, uint32_t>> scored(expertCount);
+    for (uint32_t s = 0; s < seqLen; ++s) {
+        const float *routerLogitsS = logits + static_cast<size_t>(s) * expertCount;
+        float maxL = -std::numeric_limits<float>::infinity();
+        for (uint32_t e = 0; e < expertCount; ++e) maxL = std::max(maxL, routerLogitsS[e]);
+        double sumExp = 0.0;
+        for (uint32_t e = 0; e < expertCount; ++e) {
+            probs[e] = std::exp(static_cast<double>(routerLogitsS[e]) - maxL);
+            sumExp += probs[e];
+        }
+        const float invSum = static_cast<float>(1.0 / sumExp);
+        for (uint32_t e = 0; e < expertCount; ++e) probs[e] *= invSum;
+        for (uint32_t e = 0; e < expertCount; ++e) scored[e] = {probs[e], e};
+        std::partial_sort(scored.begin(), scored.begin() + eu, scored.end(),
+                          [](const auto &a, const auto &b) { return a.first > b.first; });
+        double wsum = 0.0;
+        for (uint32_t r = 0; r < eu; ++r) wsum += scored[r].first;
+        const float wsumClamped = static_cast<float>(std::max(wsum, 6.103515625e-5));
+        for (uint32_t r = 0; r < eu; ++r) {
+            expertIdxOut[static_cast<size_t>(s) * eu + r] = static_cast<int32_t>(scored[r].second);
+            expertWgtOut[static_cast<size_t>(s) * eu + r] = scored[r].first / wsumClamped;
+        }
+    }
+}
+
 int ref_matmul(int type, const uint8_t *W, const float *X, uint32_t seqLen, uint32_t rows,
                uint32_t cols, float *out) {
     switch (type) {

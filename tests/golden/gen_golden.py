@@ -22,6 +22,10 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 import oracle as O  # noqa: E402
 
 OUT = os.path.join(HERE, "golden.npz")
+# BASELINE widths of the wide mat-vec goldens: (name, type, widths)
+WIDE_COLS = (3584, 4096, 5120, 17408, 18944)
+WIDE_CASES = (("q4k", O.Q4_K, (3584, 5120, 17408, 18944)), ("q6k", O.Q6_K, (3584, 17408, 18944)),
+              ("iq3", O.IQ3_XXS, (3584, 17408, 18944)), ("q80", O.Q8_0, (4096, 5120, 17408)))
 MOE_SEED = 777
 
 
@@ -420,6 +424,50 @@ def main():
         g[f"mm_{name}_w"] = w
         g[f"mm_{name}_y1"] = ref.matmul(O.Q5_0, w, X1, rows, cols)
         g[f"mm_{name}_y4"] = ref.matmul(O.Q5_0, w, X4, rows, cols)
+
+    # Mat-vec at the BASELINE widths (configs 1-4): 8 rows, S = 1 and 4 tokens
+    # (the one-token input is the first row of the four), so the reference's
+    # fp32 cross-block accumulation order is pinned at 14, 20, 68 and 74
+    # superblocks (Q8_0: 128, 160 and 544 blocks), not only at 2.
+    rw = np.random.default_rng(20261202)
+    oc = O.Oracle()
+    for cols in WIDE_COLS:
+        g[f"mmw_x4_{cols}"] = rw.standard_normal((4, cols)).astype(np.float32)
+    for name, qt, colsl in WIDE_CASES:
+        for cols in colsl:
+            nb = cols // 256
+            if qt == O.Q4_K:
+                w = ref.encode_q4k(rw.standard_normal((8, cols)).astype(np.float32))
+            elif qt == O.Q6_K:
+                w = q6k_random_blocks(rw, 8 * nb)
+            elif qt == O.IQ3_XXS:
+                w = iq3_random_blocks(rw, 8 * nb)
+            else:
+                w = oc.encode(O.Q8_0, (rw.standard_normal((8, cols)) * 0.02).astype(np.float32))
+            x4 = g[f"mmw_x4_{cols}"]
+            g[f"mmw_{name}_{cols}_w"] = w
+            g[f"mmw_{name}_{cols}_y1"] = ref.matmul(qt, w, x4[:1], 8, cols)
+            g[f"mmw_{name}_{cols}_y4"] = ref.matmul(qt, w, x4, 8, cols)
+
+    # MoE router (ModelMoE.cpp:341-425): logits from the reference's F32
+    # kernel (SIMDMatMulVecAVX2.cpp:2982) at a width with a 4-column tail, for
+    # one token (row path) and sixteen (tile path); the selection on those
+    # logits and on tie-heavy logits (multiples of 1/4: equal probabilities
+    # whose order std::partial_sort fixes), for k = 1, 8 and 10.
+    rr = np.random.default_rng(20261203)
+    E, H = 128, 516
+    wr = (rr.standard_normal((E, H)) * 0.05).astype(np.float32)
+    xr = rr.standard_normal((16, H)).astype(np.float32)
+    g["router_w"], g["router_x"] = wr, xr
+    g["router_logits1"] = ref.matmul_f32(wr, xr[:1], E, H)
+    g["router_logits16"] = ref.matmul_f32(wr, xr, E, H)
+    ties = (np.round(rr.standard_normal((32, E)) * 2.0) / 4.0).astype(np.float32)
+    wide = (rr.standard_normal((8, 256)) * 3.0).astype(np.float32)
+    g["router_ties"], g["router_wide"] = ties, wide
+    for k in (1, 8, 10):
+        g[f"router_sel{k}_ids"], g[f"router_sel{k}_wts"] = ref.moe_select(g["router_logits16"], k)
+        g[f"router_ties{k}_ids"], g[f"router_ties{k}_wts"] = ref.moe_select(ties, k)
+    g["router_wide8_ids"], g["router_wide8_wts"] = ref.moe_select(wide, 8)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")

@@ -55,3 +55,36 @@ def close(got, ref, rtol=1e-3, atol=1e-4):
     err = np.abs(got - ref)
     bound = atol + rtol * np.abs(ref)
     return bool((err <= bound).all()), float((err / bound).max()) if err.size else 0.0
+
+
+def oracle_matmul_par(oracle, qt, w, x, rows, cols):
+    """oracle.matmul split over row chunks run in parallel threads (the C call
+    releases the GIL; rows are independent, so the result is the same array
+    the single call gives)."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+    rb = row_bytes(qt, cols)
+    w = np.ascontiguousarray(w, np.uint8).reshape(rows, rb)
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    try:
+        ncpu = len(os.sched_getaffinity(0))
+    except AttributeError:
+        ncpu = os.cpu_count() or 1
+    nth = max(1, min(16, ncpu, rows))
+    bounds = np.linspace(0, rows, nth + 1).astype(int)
+    parts = [(int(a), int(b)) for a, b in zip(bounds[:-1], bounds[1:]) if b > a]
+    with ThreadPoolExecutor(len(parts)) as ex:
+        outs = list(ex.map(lambda ab: oracle.matmul(qt, w[ab[0]:ab[1]], x, ab[1] - ab[0], cols), parts))
+    return np.concatenate(outs, axis=1)
+
+
+def tile_edges(n, tile, extra, rng):
+    """Sorted indices: the first and last index of every `tile`-sized tile of
+    range(n), the whole last tile, and `extra` seeded random ones."""
+    idx = set()
+    for t0 in range(0, n, tile):
+        idx.add(t0)
+        idx.add(min(n, t0 + tile) - 1)
+    idx.update(range((n - 1) // tile * tile, n))
+    idx.update(rng.choice(n, size=min(n, extra), replace=False).tolist())
+    return np.array(sorted(idx), dtype=np.int64)

@@ -9,7 +9,7 @@ the one whose bytes are checked bit-exact in test_gpu_gemv.py.
 import numpy as np
 import pytest
 
-from qdata import ALL, IQ2_S, IQ2_XS, IQ4_NL, IQ4_XS, Q5_0, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, random_blocks, row_bytes
+from qdata import ALL, IQ2_S, IQ2_XS, IQ4_NL, IQ4_XS, Q5_0, IQ3_S, IQ3_XXS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, oracle_matmul_par, random_blocks, row_bytes, tile_edges
 
 pytestmark = pytest.mark.gpu
 
@@ -70,24 +70,36 @@ def test_gemm_exact_batched_types(tc, dev, oracle, qt):
     assert ok, worst
 
 
-@pytest.mark.parametrize("qt,N,K", [(Q4_K, 17408, 5120), (Q8_0, 5120, 17408)])
-def test_gemm_full_shape_sampled_rows(tc, dev, oracle, qt, N, K):
-    """Prefill shape at full size (M=512): weights from the GPU encoder, the
-    oracle evaluated on 48 sampled rows (all 512 tokens)."""
+@pytest.mark.parametrize("M", [128, 512, 2048])
+@pytest.mark.parametrize("qt,N,K", [(Q4_K, 17408, 5120), (Q4_K, 5120, 17408), (Q8_0, 17408, 5120),
+                                    (Q8_0, 5120, 17408)])
+def test_gemm_cfg4_full_shape(tc, dev, oracle, qt, N, K, M):
+    """BASELINE config 4 at full size: both matrices, both types, M in {128,
+    512, 2048}; weights from the GPU encoder, x ~ N(0,1). The oracle checks
+    the first and last row of every 64-row workgroup tile plus 32 seeded rows,
+    against every token for M <= 512, and at M = 2048 the first and last token
+    of every 128-token tile, the whole last token tile and 32 seeded tokens
+    (tokens and rows are independent of each other, so these entries are
+    exactly the full output's)."""
     import torch
-    M = 512
-    gen = torch.Generator(device=dev).manual_seed(4 + qt)
+    gen = torch.Generator(device=dev).manual_seed(4 + qt + N + M)
     wf = torch.randn((N, K), generator=gen, device=dev) * (1.0 if qt == Q4_K else 0.02)
     w = tc.encode(qt, wf)
     del wf
     x = torch.randn((M, K), generator=gen, device=dev)
     got = tc.gemm(qt, w, x, N, K).cpu().numpy()
-    rb = row_bytes(qt, K)
-    wh = w.cpu().numpy().reshape(N, rb)
-    rows = np.sort(np.random.default_rng(1).choice(N, 48, replace=False))
-    ref = oracle.matmul(qt, wh[rows].copy(), x.cpu().numpy(), len(rows), K)
-    ok, worst = close(got[:, rows], ref)
-    assert ok, worst
+    assert np.isfinite(got).all()
+    rng = np.random.default_rng(M + N)
+    rows = tile_edges(N, 64, 32, rng)
+    toks = np.arange(M) if M <= 512 else tile_edges(M, 128, 32, rng)
+    wh = w.cpu().numpy().reshape(N, row_bytes(qt, K))[rows]
+    xh = x.cpu().numpy()[toks]
+    ref = oracle_matmul_par(oracle, qt, wh, xh, len(rows), K)
+    sub = got[np.ix_(toks, rows)]
+    ok, worst = close(sub, ref)
+    bad = np.argwhere(~(np.abs(sub - ref) <= 1e-4 + 1e-3 * np.abs(ref)))
+    assert ok, (f"{NAMES[qt]} M={M} N={N} K={K}: worst err/bound {worst:.3g}; first bad (token, row) "
+                f"{[(int(toks[i]), int(rows[j])) for i, j in bad[:5]]}")
 
 
 def test_gemm_matches_gemv_small_batch(tc, dev):

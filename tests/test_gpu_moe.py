@@ -233,3 +233,90 @@ def test_moe_grouped_full_config(tc, dev, oracle):
     pairs = run_path(tc, args, 1 << 30)
     ok, worst = close_moe_flips(pairs, ref, step)
     assert ok, worst
+
+
+# ---- the router (ModelMoE.cpp:341-425) --------------------------------------------------
+# Bar: logits and expert ids bit-exact (integer/index work and the CPU's own
+# FMA order); weights within 1e-3 relative / 1e-4 absolute.
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def test_router_golden(tc, dev, golden):
+    """The compiled reference's logits (its F32 AVX2 kernel, a width with a
+    4-column tail) and its selection on them, for 1 and 16 tokens, k = 1, 8
+    and 10."""
+    from qdata import close
+    w, x = golden["router_w"], golden["router_x"]
+    wd = to_dev(w, dev)
+    for tag, xs in (("1", x[:1]), ("16", x)):
+        for k in (1, 8, 10):
+            lg, ids, wts = tc.moe_router(wd, to_dev(xs, dev), k)
+            assert (_bits(lg.cpu().numpy()) == _bits(golden[f"router_logits{tag}"])).all(), tag
+            n = xs.shape[0]
+            assert (ids.cpu().numpy() == golden[f"router_sel{k}_ids"][:n]).all(), (tag, k)
+            ok, worst = close(wts.cpu().numpy(), golden[f"router_sel{k}_wts"][:n])
+            assert ok, (tag, k, worst)
+
+
+@pytest.mark.parametrize("k", [1, 8, 10])
+def test_router_selection_ties_golden(tc, dev, golden, k):
+    """Tie-heavy logits (multiples of 1/4): equal probabilities come out in
+    std::partial_sort's order, exactly as the reference's selection."""
+    from qdata import close
+    cases = [("ties", golden["router_ties"])] + ([("wide", golden["router_wide"])] if k == 8 else [])
+    for name, lg in cases:
+        ids, wts = tc.moe_select(to_dev(lg, dev), k)
+        assert (ids.cpu().numpy() == golden[f"router_{name}{k}_ids"]).all(), name
+        ok, worst = close(wts.cpu().numpy(), golden[f"router_{name}{k}_wts"])
+        assert ok, (name, worst)
+
+
+@pytest.mark.parametrize("S", [1, 16, 300])
+def test_router_cfg5_vs_oracle(tc, dev, oracle, S):
+    """Config 5's router shape (128 experts, hidden 2048, top 8) against the
+    oracle: logits and ids bit for bit, weights within the bar."""
+    from qdata import close
+    rng = np.random.default_rng(S)
+    E, H, K = 128, 2048, 8
+    w = (rng.standard_normal((E, H)) * 0.03).astype(np.float32)
+    x = rng.standard_normal((S, H)).astype(np.float32)
+    lg, ids, wts = tc.moe_router(to_dev(w, dev), to_dev(x, dev), K)
+    rl = oracle.matmul_f32(w, x, E, H)
+    assert (_bits(lg.cpu().numpy()) == _bits(rl)).all()
+    rids, rwts = oracle.moe_route(rl, K)
+    assert (ids.cpu().numpy() == rids).all()
+    ok, worst = close(wts.cpu().numpy(), rwts)
+    assert ok, worst
+
+
+def test_router_feeds_moe_ffn(tc, dev, oracle):
+    """Router on the device feeding the expert FFN with no host round trip:
+    the ids and weights the FFN consumes are the oracle router's, and the
+    output is the oracle composition's within the MoE bar."""
+    E, K, H, FF, S = 16, 4, 1024, 512, 6
+    rng = np.random.default_rng(77)
+    wg, wu, wd = moe_weights(lambda x: oracle.encode(Q4_K, x), E, H, FF, seed=77)
+    wr = (rng.standard_normal((E, H)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((S, H)).astype(np.float32)
+    xd = to_dev(x, dev)
+    _, ids, wts = tc.moe_router(to_dev(wr, dev), xd, K)
+    got = tc.moe_ffn(xd, ids, wts, to_dev(wg, dev), to_dev(wu, dev), to_dev(wd, dev), E, H, FF).cpu().numpy()
+    rids, rwts = oracle.moe_route(oracle.matmul_f32(wr, x, E, H), K)
+    assert (ids.cpu().numpy() == rids).all()
+    ref = oracle.moe_ffn(x, rids, rwts, wg, wu, wd, E, H, FF)
+    ok, msg = close_moe(got, ref)
+    assert ok, msg
+
+
+def test_router_refuses_bad_arguments(tc, dev):
+    import torch
+    from tc_hip import TC_E_ARG, _ptr
+    lg = torch.zeros((2, 8), device=dev)
+    ids = torch.full((2, 9), -7, dtype=torch.int32, device=dev)
+    wts = torch.zeros((2, 9), device=dev)
+    assert tc.lib.tc_moe_select(_ptr(lg), 2, 8, 9, _ptr(ids), _ptr(wts), None) == TC_E_ARG  # top_k > n_experts
+    assert tc.lib.tc_moe_select(_ptr(lg), 2, 8, 0, _ptr(ids), _ptr(wts), None) == TC_E_ARG
+    torch.cuda.synchronize()
+    assert (ids.cpu() == -7).all()

@@ -301,6 +301,24 @@ def test_matmul_bit_exact_vs_reference(oracle, golden, name, qt):
         assert (bits(got) == bits(y)).all(), (name, tag)
 
 
+WIDE = [("q4k", O.Q4_K, c) for c in (3584, 5120, 17408, 18944)] + \
+       [("q6k", O.Q6_K, c) for c in (3584, 17408, 18944)] + \
+       [("iq3", O.IQ3_XXS, c) for c in (3584, 17408, 18944)] + [("q80", O.Q8_0, c) for c in (4096, 5120, 17408)]
+
+
+@pytest.mark.parametrize("name,qt,cols", WIDE)
+def test_matmul_bit_exact_vs_reference_at_baseline_widths(oracle, golden, name, qt, cols):
+    """At the BASELINE widths (14-74 superblocks, 128-544 Q8_0 blocks) the
+    oracle's fp32 cross-block accumulation matches the compiled reference bit
+    for bit, for the one-token row path and the 4-token batch path."""
+    w = golden[f"mmw_{name}_{cols}_w"]
+    x4 = golden[f"mmw_x4_{cols}"]
+    for tag, x in (("1", x4[:1]), ("4", x4)):
+        y = golden[f"mmw_{name}_{cols}_y{tag}"]
+        got = oracle.matmul(qt, w, x, 8, cols)
+        assert (bits(got) == bits(y)).all(), (name, cols, tag)
+
+
 def test_matmul_q80_cols96(oracle, golden):
     got = oracle.matmul(O.Q8_0, golden["mm_q80c96_w"], golden["mm_q80c96_x"], 16, 96)
     assert (bits(got) == bits(golden["mm_q80c96_y"])).all()
@@ -458,3 +476,60 @@ def test_float_path_types(oracle, golden, name, qt, tb):
         oracle.block_isums(qt, w, x, rows, cols)
     y = oracle.matmul(qt, w, x, rows, cols)
     assert (bits(oracle.matmul(qt, w, 4.0 * x, rows, cols)) == bits(4.0 * y)).all()
+
+
+# ---- MoE router ------------------------------------------------------------------------
+
+def test_router_logits_bit_exact_vs_reference(oracle, golden):
+    """The F32 router mat-vec (SIMDMatMulVecAVX2.cpp:2982) in the reference's
+    FMA-chain order, with a 4-column tail, for 1 and 16 tokens."""
+    w, x = golden["router_w"], golden["router_x"]
+    E, H = w.shape
+    for tag, xs in (("1", x[:1]), ("16", x)):
+        got = oracle.matmul_f32(w, xs, E, H)
+        assert (bits(got) == bits(golden[f"router_logits{tag}"])).all(), tag
+
+
+def test_router_logits_close_to_float64_dot(oracle):
+    """What the mathematics fixes: the logits are the dot products up to fp32
+    rounding (a dropped column or chain would fail this)."""
+    rng = np.random.default_rng(8)
+    for H in (7, 40, 520, 2052):
+        w = rng.standard_normal((16, H)).astype(np.float32)
+        x = rng.standard_normal((3, H)).astype(np.float32)
+        got = oracle.matmul_f32(w, x, 16, H).astype(np.float64)
+        ref = x.astype(np.float64) @ w.astype(np.float64).T
+        assert np.allclose(got, ref, rtol=1e-5, atol=1e-4 * np.sqrt(H))
+
+
+@pytest.mark.parametrize("k", [1, 8, 10])
+def test_router_selection_bit_exact_vs_reference(oracle, golden, k):
+    """Softmax, top-k (std::partial_sort's order, ties included) and the
+    clamped renormalisation of ModelMoE.cpp:387-424: ids and weights bit for
+    bit on random and tie-heavy logits."""
+    cases = [("sel", golden["router_logits16"]), ("ties", golden["router_ties"])]
+    if k == 8:
+        cases.append(("wide", golden["router_wide"]))
+    for name, lg in cases:
+        ids, wts = oracle.moe_route(lg, k)
+        assert (ids == golden[f"router_{name}{k}_ids"]).all(), name
+        assert (bits(wts) == bits(golden[f"router_{name}{k}_wts"])).all(), name
+
+
+def test_router_selection_invariants(oracle):
+    """Without ties the selection is the k largest probabilities in
+    descending order (brute force), the weights are the softmax restricted to
+    them and renormalised (they sum to 1), and logits shifted by a constant
+    select the same experts."""
+    rng = np.random.default_rng(9)
+    lg = (rng.standard_normal((64, 128)) * 3.0).astype(np.float32)
+    ids, wts = oracle.moe_route(lg, 8)
+    for s in range(64):
+        p = np.exp(lg[s].astype(np.float64) - lg[s].max())
+        p /= p.sum()
+        order = np.argsort(-p, kind="stable")[:8]
+        assert (ids[s] == order).all()
+        assert np.allclose(wts[s], p[order] / p[order].sum(), rtol=1e-5)
+        assert abs(float(wts[s].astype(np.float64).sum()) - 1.0) < 1e-5
+    ids2, _ = oracle.moe_route(lg + np.float32(0.5), 8)
+    assert (ids2 == ids).all()

@@ -41,6 +41,8 @@ struct Device {
     size_t act_bytes = 0;
     void *aux = nullptr;  // kernel intermediates (MoE hidden, GEMM partials)
     size_t aux_bytes = 0;
+    void *pad = nullptr;  // zero-padded copies of Q8_0 rows of a width not a multiple of 256
+    size_t pad_bytes = 0;
 };
 
 std::mutex g_mu;
@@ -168,14 +170,51 @@ int run_gemv(Device *dev, int type, const void *w, const void *w2, const float *
     return TC_OK;
 }
 
+// Q8_0 rows of a width that is a multiple of 32 but not of 256: the
+// reference's Q8_0 dispatch takes any cols % 32 == 0
+// (QuantizedMatrix.cpp:96-103), the kernels work on 256-column units.
+bool ragged_q80(int type, uint32_t cols) { return type == TC_Q8_0 && cols % 256 != 0 && cols % 32 == 0; }
+
 int check_common(int type, const void *w, const void *x, const void *out, uint32_t S, uint32_t rows,
-                 uint32_t cols) {
+                 uint32_t cols, bool ragged_ok = false) {
     if (!type_ok(type)) return fail(TC_E_UNSUPPORTED, "unsupported type %d", type);
     if (!w || !x || !out) return fail(TC_E_ARG, "null pointer");
     if (S == 0 || rows == 0 || cols == 0) return fail(TC_E_UNSUPPORTED, "empty shape");
-    if (cols % 256 != 0) return fail(TC_E_UNSUPPORTED, "cols=%u is not a multiple of 256", cols);
+    if (cols % 256 != 0 && !(ragged_ok && ragged_q80(type, cols)))
+        return fail(TC_E_UNSUPPORTED, "cols=%u is not a multiple of %u", cols, type == TC_Q8_0 ? 32u : 256u);
     if ((reinterpret_cast<uintptr_t>(w) & 15) || (reinterpret_cast<uintptr_t>(x) & 15))
         return fail(TC_E_UNSUPPORTED, "weights and activations must be 16-byte aligned");
+    return TC_OK;
+}
+
+// The ragged Q8_0 case runs on zero-padded copies: each weight row and each
+// activation row is copied into a row of the next multiple of 256 columns
+// (one small copy kernel per operand, into the device's pad scratch). A
+// padded weight block has d = 0 and a padded activation block is all zero,
+// so it adds exactly 0 to every output; the real blocks are quantized and
+// multiplied as they would be in place.
+struct Padded {
+    const void *w[2] = {nullptr, nullptr};
+    const float *x = nullptr;
+    uint32_t cols = 0;
+};
+
+int pad_q80(Device *dev, const void *w0, const void *w1, uint32_t rows, const float *x, uint32_t S, uint32_t cols,
+            Padded *p, hipStream_t st) {
+    const uint32_t cp = (cols + 255) / 256 * 256;
+    const uint32_t rb = cols / 32 * 34, rbp = cp / 32 * 34;
+    const size_t wbytes = (size_t(rows) * rbp + 255) & ~size_t(255);
+    const size_t need = wbytes * (w1 ? 2 : 1) + size_t(S) * cp * 4;
+    if (!ensure(dev->pad, dev->pad_bytes, need)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", need);
+    char *b = static_cast<char *>(dev->pad);
+    hipError_t e = tc::launch_pad_rows(w0, rb, b, rbp, rows, st);
+    if (e == hipSuccess && w1) e = tc::launch_pad_rows(w1, rb, b + wbytes, rbp, rows, st);
+    if (e == hipSuccess && x) e = tc::launch_pad_rows(x, cols * 4, b + wbytes * (w1 ? 2 : 1), cp * 4, S, st);
+    if (e != hipSuccess) return hip_fail(e, "Q8_0 row padding");
+    p->w[0] = b;
+    p->w[1] = w1 ? b + wbytes : nullptr;
+    p->x = reinterpret_cast<const float *>(b + wbytes * (w1 ? 2 : 1));
+    p->cols = cp;
     return TC_OK;
 }
 
@@ -208,11 +247,16 @@ int tc_gemv(int type, const void *w, const float *x, float *out, uint32_t seq_le
             void *stream) {
     Device *dev = device();
     if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
-    int rc = check_common(type, w, x, out, seq_len, rows, cols);
+    int rc = check_common(type, w, x, out, seq_len, rows, cols, true);
     if (rc) return rc;
     if (seq_len > 8) return fail(TC_E_UNSUPPORTED, "seq_len=%u > 8 (use tc_gemm)", seq_len);
-    return run_gemv(dev, type, w, nullptr, x, nullptr, out, nullptr, 0, nullptr, seq_len, rows, cols,
-                    static_cast<hipStream_t>(stream));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (ragged_q80(type, cols)) {
+        Padded p;
+        if ((rc = pad_q80(dev, w, nullptr, rows, x, seq_len, cols, &p, st))) return rc;
+        return run_gemv(dev, type, p.w[0], nullptr, p.x, nullptr, out, nullptr, 0, nullptr, seq_len, rows, p.cols, st);
+    }
+    return run_gemv(dev, type, w, nullptr, x, nullptr, out, nullptr, 0, nullptr, seq_len, rows, cols, st);
 }
 
 int tc_gemv_multi(int type, uint32_t n, const void *const *w, const float *const *x, float *const *out,
@@ -281,24 +325,38 @@ int tc_gemv_dual(int type, const void *wg, const void *wu, const float *x, float
                  uint32_t cols, void *stream) {
     Device *dev = device();
     if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
-    int rc = check_common(type, wg, x, gout, 1, rows, cols);
+    int rc = check_common(type, wg, x, gout, 1, rows, cols, true);
     if (rc) return rc;
     if (!wu || !uout) return fail(TC_E_ARG, "null pointer");
     if ((reinterpret_cast<uintptr_t>(wu) & 15)) return fail(TC_E_UNSUPPORTED, "weights must be 16-byte aligned");
-    return run_gemv(dev, type, wg, wu, x, nullptr, gout, uout, 1, nullptr, 1, rows, cols,
-                    static_cast<hipStream_t>(stream));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (ragged_q80(type, cols)) {
+        Padded p;
+        if ((rc = pad_q80(dev, wg, wu, rows, x, 1, cols, &p, st))) return rc;
+        return run_gemv(dev, type, p.w[0], p.w[1], p.x, nullptr, gout, uout, 1, nullptr, 1, rows, p.cols, st);
+    }
+    return run_gemv(dev, type, wg, wu, x, nullptr, gout, uout, 1, nullptr, 1, rows, cols, st);
 }
 
 int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_len, uint32_t rows, uint32_t cols,
             uint32_t blocks_per_row, void *stream) {
     Device *dev = device();
     if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
-    int rc = check_common(type, w, x, out, seq_len, rows, cols);
+    int rc = check_common(type, w, x, out, seq_len, rows, cols, true);
     if (rc) return rc;
     if (blocks_per_row != cols / uint32_t(tc::block_elems(type)))
         return fail(TC_E_ARG, "blocks_per_row=%u does not match cols=%u", blocks_per_row, cols);
     if (type == TC_Q8_0 && !g_q8_gemm_enabled) return fail(TC_E_UNSUPPORTED, "Q8_0 GEMM disabled");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (ragged_q80(type, cols)) {
+        if (uint64_t(seq_len) * cols >= (uint64_t(1) << 30))
+            return fail(TC_E_UNSUPPORTED, "activations of 4 GiB or more");
+        Padded p;
+        if ((rc = pad_q80(dev, w, nullptr, rows, x, seq_len, cols, &p, st))) return rc;
+        w = p.w[0];
+        x = p.x;
+        cols = p.cols;
+    }
     if (type != TC_Q4_K && type != TC_Q8_0) {
         // Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS / IQ4_NL / Q5_0: the exact batched path (the reference's launchQGemm,
         // GpuGemvIQInt8.hpp:771-847) -- the decode kernel over token groups.
@@ -345,14 +403,26 @@ int tc_quantize_act(int type, const float *x, uint32_t seq_len, uint32_t cols, i
     const uint32_t blk = type == TC_Q8_0 ? 32 : 256;
     if (seq_len == 0 || cols == 0 || cols % blk) return fail(TC_E_UNSUPPORTED, "cols=%u", cols);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const tc::ActLayout L = tc::act_layout(type, seq_len, cols);
+    // Q8_0 at a width that is not a multiple of 256: quantize zero-padded
+    // rows (each 32-block is quantized on its own, so the real blocks come
+    // out as they would in place), then copy out the real columns.
+    uint32_t cq = cols;
+    if (ragged_q80(type, cols)) {
+        Padded p;
+        int rc = pad_q80(dev, nullptr, nullptr, 0, x, seq_len, cols, &p, st);
+        if (rc) return rc;
+        x = p.x;
+        cq = p.cols;
+    }
+    const tc::ActLayout L = tc::act_layout(type, seq_len, cq);
     if (!ensure(dev->act, dev->act_bytes, L.bytes)) return fail(TC_E_LAUNCH, "hipMalloc failed");
-    hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, dev->act, st);
+    hipError_t e = tc::launch_quant_act(type, x, seq_len, cq, L, dev->act, st);
     if (e != hipSuccess) return hip_fail(e, "activation quantizer");
     const char *b = static_cast<const char *>(dev->act);
-    e = hipMemcpyAsync(qs, b + L.qs_off, size_t(seq_len) * cols, hipMemcpyDeviceToDevice, st);
+    e = hipMemcpy2DAsync(qs, cols, b + L.qs_off, cq, cols, seq_len, hipMemcpyDeviceToDevice, st);
     if (e == hipSuccess)
-        e = hipMemcpyAsync(d, b + L.d_off, size_t(seq_len) * (cols / blk) * 4, hipMemcpyDeviceToDevice, st);
+        e = hipMemcpy2DAsync(d, size_t(cols / blk) * 4, b + L.d_off, size_t(cq / blk) * 4, size_t(cols / blk) * 4,
+                             seq_len, hipMemcpyDeviceToDevice, st);
     if (e == hipSuccess && type != TC_Q8_0)
         e = hipMemcpyAsync(bsums, b + L.bs_off, size_t(seq_len) * (cols / 16) * 2, hipMemcpyDeviceToDevice, st);
     if (e != hipSuccess) return hip_fail(e, "copy");
@@ -536,6 +606,33 @@ int tc_moe_ffn(const float *x, const int32_t *ids, const float *wts, uint32_t se
     return TC_OK;
 }
 
+int tc_moe_select(const float *logits, uint32_t seq_len, uint32_t n_experts, uint32_t top_k, int32_t *ids, float *wts,
+                  void *stream) {
+    if (!device()) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!logits || !ids || !wts) return fail(TC_E_ARG, "null pointer");
+    if (seq_len == 0 || n_experts == 0 || top_k == 0 || top_k > n_experts)
+        return fail(TC_E_ARG, "seq_len=%u n_experts=%u top_k=%u", seq_len, n_experts, top_k);
+    if (n_experts > 4096) return fail(TC_E_UNSUPPORTED, "n_experts=%u > 4096", n_experts);
+    hipError_t e = tc::launch_router_select(logits, seq_len, n_experts, top_k, ids, wts, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "MoE router selection");
+    return TC_OK;
+}
+
+int tc_moe_router(const float *w_router, const float *x, uint32_t seq_len, uint32_t n_experts, uint32_t hidden,
+                  uint32_t top_k, float *logits, int32_t *ids, float *wts, void *stream) {
+    if (!device()) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!w_router || !x || !logits || !ids || !wts) return fail(TC_E_ARG, "null pointer");
+    if (seq_len == 0 || n_experts == 0 || hidden == 0 || top_k == 0 || top_k > n_experts)
+        return fail(TC_E_ARG, "seq_len=%u n_experts=%u hidden=%u top_k=%u", seq_len, n_experts, hidden, top_k);
+    if (n_experts > 4096 || seq_len > 65535) return fail(TC_E_UNSUPPORTED, "n_experts > 4096 or seq_len > 65535");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = tc::launch_router_logits(w_router, x, seq_len, n_experts, hidden, logits, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE router logits");
+    e = tc::launch_router_select(logits, seq_len, n_experts, top_k, ids, wts, st);
+    if (e != hipSuccess) return hip_fail(e, "MoE router selection");
+    return TC_OK;
+}
+
 // ---- parity hooks (reference GPUModel::debugQ8KRow / debugQ8_0Row /
 // debugQ8KBlocks / debugQ8_0Blocks, include/GPUCompute.hpp:399-460, as free
 // functions over host data) --------------------------------------------------
@@ -647,7 +744,8 @@ int tc_debug_q8_0_row(const uint8_t *w_row, uint32_t blocks_per_row, const float
 
 int tc_debug_q8k_blocks(int type, const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
                         float *out_blk, uint8_t *out_quant) {
-    if (type == TC_Q8_0 || !type_ok(type)) return fail(TC_E_UNSUPPORTED, "type %d is not a Q8_K-activation type", type);
+    if (type == TC_Q8_0 || !type_ok(type) || !int8_act_type(type))
+        return fail(TC_E_UNSUPPORTED, "type %d is not a Q8_K-activation type", type);
     if (!w_row || !x || !out_blk || !out_quant) return fail(TC_E_ARG, "null pointer");
     if (cols % 256 || blocks_per_row != cols / 256) return fail(TC_E_ARG, "blocks_per_row/cols mismatch");
     int rc = debug_quant(type, x, cols, out_quant);

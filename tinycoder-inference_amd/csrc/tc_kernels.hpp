@@ -21,6 +21,11 @@ hipError_t launch_quant_act_rows(const float *x, const uint32_t *rows, uint32_t 
 
 hipError_t launch_encode(int type, const float *x, void *out, uint32_t nunits, hipStream_t st);
 
+// rows x src_row_bytes -> rows x dst_row_bytes (a multiple of 4), each row
+// copied and zero-filled past src_row_bytes.
+hipError_t launch_pad_rows(const void *src, uint32_t src_row_bytes, void *dst, uint32_t dst_row_bytes, uint32_t rows,
+                           hipStream_t st);
+
 // One mat-vec job: out[s][r] (row stride out_ld per token) = W[r] . x[s].
 // With W2 set the job is a pair over the same rows (gate/up): out2 = W2 x and,
 // for epi == 1, out = silu(W x) * out2. Activations come from `x` (fp32,
@@ -95,6 +100,16 @@ hipError_t launch_moe_swiglu(float *g, const float *u, uint32_t nrows_max, uint3
 // (pairs with pos < 0 skipped), from 0.
 hipError_t launch_moe_combine_rows(const float *y, const int32_t *pos, const float *wts, float *out, uint32_t T,
                                    uint32_t top_k, uint32_t H, hipStream_t st);
+// ---- MoE router (F32 router matrix; the CPU router's exact evaluation) ----
+// logits out[S][rows] = X[S][cols] . W[rows][cols] in the reference AVX2
+// kernel's FMA order.
+hipError_t launch_router_logits(const float *W, const float *X, uint32_t S, uint32_t rows, uint32_t cols, float *out,
+                                hipStream_t st);
+// Softmax, top-K (std::partial_sort's order) and renormalised weights of
+// logits[S][E] into ids[S][K], wts[S][K].
+hipError_t launch_router_select(const float *logits, uint32_t S, uint32_t E, uint32_t K, int32_t *ids, float *wts,
+                                hipStream_t st);
+
 // Q4_K GEMM over expert-sorted rows: out[i][n] = act row i . W[e(i)] row n,
 // for the token tiles of mt (count *ntm, at most ntm_max).
 size_t gemm_grouped_workspace_bytes(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu);

@@ -70,6 +70,23 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x,
     quant_q8_0_blocks_wave(x + size_t(g) * 256, qs + size_t(o) * 256, d + size_t(o) * 8);
 }
 
+// Row copy into a wider, zero-padded row: dst[r][i] = src[r][i] for i < sbytes,
+// 0 for sbytes <= i < dbytes. One thread per destination dword (dbytes is a
+// multiple of 4; the source rows may sit at any byte offset).
+__global__ __launch_bounds__(256) void k_pad_rows(const uint8_t *__restrict__ src, uint32_t sbytes,
+                                                  uint32_t *__restrict__ dst, uint32_t dwords, uint32_t rows) {
+    const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= size_t(rows) * dwords) return;
+    const size_t r = i / dwords;
+    const uint32_t c = uint32_t(i - r * dwords) * 4;
+    const uint8_t *s = src + r * sbytes;
+    uint32_t v = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k)
+        if (c + k < sbytes) v |= uint32_t(s[c + k]) << (8 * k);
+    dst[i] = v;
+}
+
 // ---- fp16 encodings ----------------------------------------------------------
 
 // The reference's fp32 -> fp16 (include/GGMLDequantize.hpp:61-87): mantissa
@@ -627,7 +644,23 @@ __device__ void enc_q50(const float *x, uint8_t *out) {
     }
 }
 
-__device__ void enc_iq4xs(const float *x, uint8_t *out) {
+// Index of the table entry whose multiple of dl is nearest to xv (first on ties).
+__device__ int iq4_nearest(float dl, float xv) {
+    int best = 0;
+    float berr = 0.0f;
+    for (int n = 0; n < 16; ++n) {
+        const float diff = dl * float(c_kvalues_iq4nl[n]) - xv;
+        const float err = diff * diff;
+        if (n == 0 || err < berr) {
+            berr = err;
+            best = n;
+        }
+    }
+    return best;
+}
+
+// Out of line: inlined into its kernel this encoder takes the compiler minutes.
+__device__ __attribute__((noinline)) void enc_iq4xs(const float *x, uint8_t *out) {
     float sc[8], smax = 0.0f;
     for (int c = 0; c < 8; ++c) {
         float m = 0.0f;
@@ -650,16 +683,7 @@ __device__ void enc_iq4xs(const float *x, uint8_t *out) {
         sh |= uint32_t(ls >> 4) << (2 * c);
         const float dl = d * float(l);
         for (int j = 0; j < 32; ++j) {
-            int best = 0;
-            float berr = 0.0f;
-            for (int n = 0; n < 16; ++n) {
-                const float diff = dl * float(c_kvalues_iq4nl[n]) - x[32 * c + j];
-                const float err = diff * diff;
-                if (n == 0 || err < berr) {
-                    berr = err;
-                    best = n;
-                }
-            }
+            const int best = iq4_nearest(dl, x[32 * c + j]);
             out[8 + 16 * c + (j & 15)] |= uint8_t(j < 16 ? best : best << 4);
         }
     }
@@ -725,27 +749,28 @@ __device__ void enc_iq2xs(const float *x, uint8_t *out) {
     }
 }
 
-__global__ __launch_bounds__(64) void k_encode(int type, const float *__restrict__ x, uint8_t *__restrict__ out,
+// One kernel per weight type (one thread per 256-weight unit): kept apart so
+// that no kernel inlines every encoder.
+template <int TYPE>
+__global__ __launch_bounds__(64) void k_encode(const float *__restrict__ x, uint8_t *__restrict__ out,
                                                uint32_t nunits) {
     const uint32_t u = blockIdx.x * 64 + threadIdx.x;
     if (u >= nunits) return;
     const float *xu = x + size_t(u) * 256;
-    uint8_t *o = out + size_t(u) * unit_bytes(type);
-    switch (type) {
-        case kQ4_K: enc_q4k(xu, o); break;
-        case kQ8_0: enc_q8_0(xu, o); break;
-        case kQ2_K: enc_q2k(xu, o); break;
-        case kQ3_K: enc_q3k(xu, o); break;
-        case kQ5_K: enc_q5k(xu, o); break;
-        case kQ6_K: enc_q6k(xu, o); break;
-        case kIQ3_S: enc_iq3s(xu, o); break;
-        case kIQ2_S: enc_iq2s(xu, o); break;
-        case kIQ2_XS: enc_iq2xs(xu, o); break;
-        case kIQ4_XS: enc_iq4xs(xu, o); break;
-        case kIQ4_NL: enc_iq4nl(xu, o); break;
-        case kQ5_0: enc_q50(xu, o); break;
-        default: enc_iq3xxs(xu, o); break;
-    }
+    uint8_t *o = out + size_t(u) * unit_bytes(TYPE);
+    if constexpr (TYPE == kQ4_K) enc_q4k(xu, o);
+    else if constexpr (TYPE == kQ8_0) enc_q8_0(xu, o);
+    else if constexpr (TYPE == kQ2_K) enc_q2k(xu, o);
+    else if constexpr (TYPE == kQ3_K) enc_q3k(xu, o);
+    else if constexpr (TYPE == kQ5_K) enc_q5k(xu, o);
+    else if constexpr (TYPE == kQ6_K) enc_q6k(xu, o);
+    else if constexpr (TYPE == kIQ3_S) enc_iq3s(xu, o);
+    else if constexpr (TYPE == kIQ2_S) enc_iq2s(xu, o);
+    else if constexpr (TYPE == kIQ2_XS) enc_iq2xs(xu, o);
+    else if constexpr (TYPE == kIQ4_XS) enc_iq4xs(xu, o);
+    else if constexpr (TYPE == kIQ4_NL) enc_iq4nl(xu, o);
+    else if constexpr (TYPE == kQ5_0) enc_q50(xu, o);
+    else enc_iq3xxs(xu, o);
 }
 
 // ---- launchers -----------------------------------------------------------------
@@ -776,8 +801,27 @@ hipError_t launch_quant_act_rows(const float *x, const uint32_t *rows, uint32_t 
     return hipGetLastError();
 }
 
+hipError_t launch_pad_rows(const void *src, uint32_t src_row_bytes, void *dst, uint32_t dst_row_bytes, uint32_t rows,
+                           hipStream_t st) {
+    if (dst_row_bytes % 4 || dst_row_bytes < src_row_bytes) return hipErrorInvalidValue;
+    const size_t n = size_t(rows) * (dst_row_bytes / 4);
+    if (n == 0) return hipSuccess;
+    k_pad_rows<<<uint32_t((n + 255) / 256), 256, 0, st>>>(static_cast<const uint8_t *>(src), src_row_bytes,
+                                                           static_cast<uint32_t *>(dst), dst_row_bytes / 4, rows);
+    return hipGetLastError();
+}
+
 hipError_t launch_encode(int type, const float *x, void *out, uint32_t nunits, hipStream_t st) {
-    k_encode<<<(nunits + 63) / 64, 64, 0, st>>>(type, x, static_cast<uint8_t *>(out), nunits);
+    const uint32_t g = (nunits + 63) / 64;
+    uint8_t *o = static_cast<uint8_t *>(out);
+    switch (type) {
+#define TC_CASE(t) \
+    case t: k_encode<t><<<g, 64, 0, st>>>(x, o, nunits); break;
+        TC_CASE(kQ4_K) TC_CASE(kQ8_0) TC_CASE(kQ2_K) TC_CASE(kQ3_K) TC_CASE(kQ5_K) TC_CASE(kQ6_K) TC_CASE(kIQ3_S)
+        TC_CASE(kIQ2_S) TC_CASE(kIQ2_XS) TC_CASE(kIQ4_XS) TC_CASE(kIQ4_NL) TC_CASE(kQ5_0) TC_CASE(kIQ3_XXS)
+#undef TC_CASE
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -46,6 +46,8 @@ SIGNATURES = {
     "tc_probe_mfma_i8": (_I, [_U32, _U32, _P, _P]),
     "tc_probe_read": (_I, [_P, ctypes.c_size_t, _U32, _P, _P]),
     "tc_moe_set_gemm_min_tokens": (None, [_U32]),
+    "tc_moe_router": (_I, [_P, _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P]),
+    "tc_moe_select": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
     "tc_gguf_open": (_P, [ctypes.c_char_p]),
     "tc_gguf_open_metadata": (_P, [ctypes.c_char_p]),
     "tc_gguf_close": (None, [_P]),
@@ -244,6 +246,27 @@ class Library:
         self._check(self.lib.tc_moe_ffn(_ptr(x), _ptr(ids), _ptr(wts), S, K, _ptr(wg), _ptr(wu), _ptr(wd),
                                         n_experts, hidden, ff, _ptr(out), self._stream()))
         return out
+
+    def moe_router(self, w_router, x, top_k):
+        """Router logits, expert ids and weights for x [S][hidden] against the
+        fp32 router matrix [n_experts][hidden]."""
+        import torch
+        E, H = w_router.shape
+        S = x.numel() // H
+        logits = torch.empty((S, E), dtype=torch.float32, device=x.device)
+        ids = torch.empty((S, top_k), dtype=torch.int32, device=x.device)
+        wts = torch.empty((S, top_k), dtype=torch.float32, device=x.device)
+        self._check(self.lib.tc_moe_router(_ptr(w_router), _ptr(x), S, E, H, top_k, _ptr(logits), _ptr(ids),
+                                           _ptr(wts), self._stream()))
+        return logits, ids, wts
+
+    def moe_select(self, logits, top_k):
+        import torch
+        S, E = logits.shape
+        ids = torch.empty((S, top_k), dtype=torch.int32, device=logits.device)
+        wts = torch.empty((S, top_k), dtype=torch.float32, device=logits.device)
+        self._check(self.lib.tc_moe_select(_ptr(logits), S, E, top_k, _ptr(ids), _ptr(wts), self._stream()))
+        return ids, wts
 
 
 class TensorRecord:
