@@ -189,6 +189,26 @@ int tc_debug_q8k_blocks(int type, const uint8_t *w_row, uint32_t blocks_per_row,
 int tc_debug_q8_0_blocks(const uint8_t *w_row, uint32_t blocks_per_row, const float *x, uint32_t cols,
                          float *out_blk, uint8_t *out_quant);
 
+/* Host-pointer products: the boundary of the reference's CPU entry points
+ * matMulVecBatch{Q4K,Q3K,Q6K,Q5K,IQ4XS,IQ4NL,Q8_0}_SIMD
+ * (include/SIMDMatMulVec.hpp:448-584; include/tc_simd_matmul.hpp restates
+ * them over this call). W (raw GGUF rows), X [seq_len][cols], out
+ * [seq_len][rows] and residual (optional, [seq_len][rows]: out = W.x +
+ * residual, the Q3_K entry point's residual-fused store) are HOST pointers.
+ * The call copies X to the device, runs tc_gemv (seq_len <= 8) or tc_gemm,
+ * and copies out back; it returns when out is written. W is read from a
+ * registered device copy when it lies inside a range given to
+ * tc_host_weights_register, else it is copied to the device on every call.
+ * Calls are serialized by the library. */
+int tc_host_matmul(int type, const uint8_t *W, const float *X, uint32_t seq_len, uint32_t rows, uint32_t cols,
+                   float *out, const float *residual);
+/* Keep a device copy of the host range [host, host + bytes) (weights that
+ * later tc_host_matmul calls read); the copy is taken now, so later writes to
+ * the host range are not seen until it is registered again. No counterpart
+ * in the reference (its CPU kernels read host memory in place). */
+int tc_host_weights_register(const void *host, size_t bytes);
+int tc_host_weights_unregister(const void *host);
+
 /* Message for the calling thread's last failed call ("" if none). */
 const char *tc_last_error(void);
 

@@ -111,3 +111,24 @@ def test_reference_interface_header_compiles_and_links(tmp_path):
                     "-Wl,-rpath," + os.path.dirname(so), "-o", str(exe)], check=True)
     r = subprocess.run([str(exe)], capture_output=True, timeout=60)
     assert r.returncode == 0, (r.returncode, r.stderr)
+
+
+def test_cpp_interface_driver_without_gpu():
+    """The C++ interface driver (tests/cpp, built from include/tc_int8gemm.hpp
+    and include/tc_simd_matmul.hpp against the library) loads, and without a
+    GPU every call reports false and writes nothing."""
+    import numpy as np
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    import iface
+    d = iface.load()
+    assert d.drv_int8GemmAvailable() == 0
+    assert d.drv_int8Gemv(12, None, None, None, 1, 1, 256, None) == 0
+    assert d.drv_int8Gemm(12, None, None, None, 16, 1, 256, 1, None) == 0
+    w = np.zeros(144, np.uint8)
+    x = np.zeros(256, np.float32)
+    out = np.full(1, 7.0, np.float32)
+    for t in (12, 11, 14, 13, 23, 20, 8):
+        assert d.drv_matMulVecBatch_SIMD(t, w.ctypes.data, x.ctypes.data, 1, 1, 256, out.ctypes.data, None) == 0
+    assert out[0] == 7.0

@@ -223,6 +223,56 @@ int pad_q80(Device *dev, const void *w0, const void *w1, uint32_t rows, const fl
 namespace tc {
 // Error text for the calling thread's tc_last_error() (used by tc_gguf.cpp).
 void set_error(const std::string &msg) { g_err = msg; }
+
+// Compute units of the current device, 0 when it is not a gfx950.
+int device_cu_count() {
+    Device *d = device();
+    return d ? d->num_cu : 0;
+}
+
+// Shape limits of the MFMA prefill GEMM (Q4_K, Q8_0; cols % 256 == 0).
+int gemm_mfma_check(int type, uint32_t S, uint32_t rows, uint32_t cols) {
+    if (type != TC_Q4_K && type != TC_Q8_0) return fail(TC_E_UNSUPPORTED, "type %d has no MFMA GEMM", type);
+    if (cols % 256) return fail(TC_E_UNSUPPORTED, "cols=%u is not a multiple of 256", cols);
+    // 32-bit buffer offsets in the MFMA kernels
+    if (uint64_t(S) * cols >= (uint64_t(1) << 32) || uint64_t(rows) * tc_row_bytes(type, cols) >= (uint64_t(1) << 32))
+        return fail(TC_E_UNSUPPORTED, "activations or weights of 4 GiB or more");
+    return TC_OK;
+}
+
+// Device scratch of one MFMA GEMM call: *act_bytes for the block-major
+// quantized activations, the return value for the split / stream-K partials.
+size_t gemm_mfma_scratch(int type, uint32_t S, uint32_t rows, uint32_t cols, int num_cu, size_t *act_bytes) {
+    // + kGemmActSlack: the MFMA kernel's loads for token rows past M in the
+    // last superblock run up to one token tile past the buffer (values never
+    // stored; the buffer range check covers only the per-lane offset).
+    *act_bytes = tc::act_layout(type, S, cols).bytes + kGemmActSlack;
+    return tc::gemm_workspace_bytes(type, S, rows, cols, num_cu);
+}
+
+// Quantize all tokens once (block-major, into act), then the MFMA kernel
+// (partials in ws when the split needs them). No allocation.
+int gemm_mfma_into(int type, const void *w, const float *x, float *out, uint32_t S, uint32_t rows, uint32_t cols,
+                   int num_cu, void *act, void *ws, hipStream_t st) {
+    const tc::ActLayout L = tc::act_layout(type, S, cols);
+    hipError_t e = tc::launch_quant_act(type, x, S, cols, L, act, st, true);
+    if (e != hipSuccess) return hip_fail(e, "activation quantizer");
+    e = tc::launch_gemm(type, w, act_view(act, L, 0, type, cols), out, S, rows, cols, num_cu, ws, st);
+    if (e != hipSuccess) return hip_fail(e, "int8 MFMA GEMM");
+    return TC_OK;
+}
+
+int gemm_entry_check(int type, const void *w, const float *x, const float *out, uint32_t S, uint32_t rows,
+                     uint32_t cols, uint32_t blocks_per_row) {
+    int rc = check_common(type, w, x, out, S, rows, cols);
+    if (rc) return rc;
+    if (blocks_per_row != cols / uint32_t(tc::block_elems(type)))
+        return fail(TC_E_ARG, "blocks_per_row=%u does not match cols=%u", blocks_per_row, cols);
+    if (type == TC_Q8_0 && !g_q8_gemm_enabled) return fail(TC_E_UNSUPPORTED, "Q8_0 GEMM disabled");
+    return TC_OK;
+}
+
+int fail_code(int code, const char *msg) { return fail(code, "%s", msg); }
 }  // namespace tc
 
 extern "C" {
@@ -368,25 +418,12 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
         }
         return TC_OK;
     }
-    // 32-bit buffer offsets in the MFMA kernels
-    if (uint64_t(seq_len) * cols >= (uint64_t(1) << 32) ||
-        uint64_t(rows) * tc_row_bytes(type, cols) >= (uint64_t(1) << 32))
-        return fail(TC_E_UNSUPPORTED, "activations or weights of 4 GiB or more");
-    // Quantize all tokens once, then the MFMA kernel.
-    const tc::ActLayout L = tc::act_layout(type, seq_len, cols);
-    const size_t ws = tc::gemm_workspace_bytes(type, seq_len, rows, cols, dev->num_cu);
-    // + kGemmActSlack: the MFMA kernel's loads for token rows past M in the
-    // last superblock run up to one token tile past the buffer (values never
-    // stored; the buffer range check covers only the per-lane offset).
-    if (!ensure(dev->act, dev->act_bytes, L.bytes + kGemmActSlack))
-        return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", L.bytes + kGemmActSlack);
+    if ((rc = tc::gemm_mfma_check(type, seq_len, rows, cols))) return rc;
+    size_t act_bytes = 0;
+    const size_t ws = tc::gemm_mfma_scratch(type, seq_len, rows, cols, dev->num_cu, &act_bytes);
+    if (!ensure(dev->act, dev->act_bytes, act_bytes)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", act_bytes);
     if (ws && !ensure(dev->aux, dev->aux_bytes, ws)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", ws);
-    hipError_t e = tc::launch_quant_act(type, x, seq_len, cols, L, dev->act, st, true);
-    if (e != hipSuccess) return hip_fail(e, "activation quantizer");
-    e = tc::launch_gemm(type, w, act_view(dev->act, L, 0, type, cols), out, seq_len, rows, cols, dev->num_cu,
-                        ws ? dev->aux : nullptr, st);
-    if (e != hipSuccess) return hip_fail(e, "int8 MFMA GEMM");
-    return TC_OK;
+    return tc::gemm_mfma_into(type, w, x, out, seq_len, rows, cols, dev->num_cu, dev->act, ws ? dev->aux : nullptr, st);
 }
 
 int tc_gemm_preferred(uint32_t type, uint32_t, uint32_t) { return type_ok(int(type)) ? 1 : 0; }
@@ -758,6 +795,99 @@ int tc_debug_q8_0_blocks(const uint8_t *w_row, uint32_t blocks_per_row, const fl
     if (cols % 256 || blocks_per_row != cols / 32) return fail(TC_E_ARG, "blocks_per_row/cols mismatch");
     int rc = debug_quant(TC_Q8_0, x, cols, out_quant);
     return rc ? rc : debug_blocks(TC_Q8_0, w_row, blocks_per_row, x, cols, out_blk);
+}
+
+// ---- host-pointer products (the reference CPU entry points' boundary,
+// include/SIMDMatMulVec.hpp:448-584) ------------------------------------------
+
+namespace {
+
+struct HostRange {
+    const uint8_t *host;
+    size_t bytes;
+    void *dev;
+};
+
+std::mutex g_host_mu;
+std::vector<HostRange> g_host_ranges;  // registered host weight ranges and their device copies
+
+// Device address of [p, p + bytes) when it lies inside a registered range.
+const void *registered_copy(const void *p, size_t bytes) {
+    const uint8_t *q = static_cast<const uint8_t *>(p);
+    for (const HostRange &r : g_host_ranges)
+        if (q >= r.host && q + bytes <= r.host + r.bytes) return static_cast<const uint8_t *>(r.dev) + (q - r.host);
+    return nullptr;
+}
+
+struct HostScratch {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+HostScratch g_hw, g_hx, g_ho;  // weights / activations / outputs staged for host-pointer calls
+
+}  // namespace
+
+int tc_host_weights_register(const void *host, size_t bytes) {
+    if (!device()) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!host || bytes == 0) return fail(TC_E_ARG, "null or empty range");
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    for (const HostRange &r : g_host_ranges)
+        if (r.host == host) return fail(TC_E_ARG, "range already registered");
+    void *d = nullptr;
+    if (hipMalloc(&d, bytes) != hipSuccess) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", bytes);
+    if (hipMemcpy(d, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        return fail(TC_E_LAUNCH, "copy to device failed");
+    }
+    g_host_ranges.push_back({static_cast<const uint8_t *>(host), bytes, d});
+    return TC_OK;
+}
+
+int tc_host_weights_unregister(const void *host) {
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    for (size_t i = 0; i < g_host_ranges.size(); ++i)
+        if (g_host_ranges[i].host == host) {
+            (void)hipDeviceSynchronize();
+            (void)hipFree(g_host_ranges[i].dev);
+            g_host_ranges.erase(g_host_ranges.begin() + long(i));
+            return TC_OK;
+        }
+    return fail(TC_E_ARG, "range not registered");
+}
+
+int tc_host_matmul(int type, const uint8_t *W, const float *X, uint32_t seq_len, uint32_t rows, uint32_t cols,
+                   float *out, const float *residual) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!type_ok(type)) return fail(TC_E_UNSUPPORTED, "unsupported type %d", type);
+    if (!W || !X || !out) return fail(TC_E_ARG, "null pointer");
+    if (seq_len == 0 || rows == 0 || cols == 0) return fail(TC_E_UNSUPPORTED, "empty shape");
+    const size_t rb = tc_row_bytes(type, cols);
+    if (rb == 0) return fail(TC_E_UNSUPPORTED, "cols=%u", cols);
+    const size_t wbytes = rb * rows, xbytes = size_t(seq_len) * cols * 4, obytes = size_t(seq_len) * rows * 4;
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    const void *wd = registered_copy(W, wbytes);
+    if (!wd) {
+        if (!ensure(g_hw.p, g_hw.cap, wbytes)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", wbytes);
+        if (hipMemcpy(g_hw.p, W, wbytes, hipMemcpyHostToDevice) != hipSuccess)
+            return fail(TC_E_LAUNCH, "weight copy to device failed");
+        wd = g_hw.p;
+    }
+    if (!ensure(g_hx.p, g_hx.cap, xbytes) || !ensure(g_ho.p, g_ho.cap, obytes))
+        return fail(TC_E_LAUNCH, "hipMalloc failed");
+    if (hipMemcpy(g_hx.p, X, xbytes, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(TC_E_LAUNCH, "activation copy to device failed");
+    float *od = static_cast<float *>(g_ho.p);
+    const float *xd = static_cast<const float *>(g_hx.p);
+    const int rc = seq_len <= 8 ? tc_gemv(type, wd, xd, od, seq_len, rows, cols, nullptr)
+                                : tc_gemm(type, wd, xd, od, seq_len, rows, cols, cols / uint32_t(tc::block_elems(type)),
+                                          nullptr);
+    if (rc) return rc;
+    if (hipMemcpy(out, od, obytes, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(TC_E_LAUNCH, "output copy to host failed");
+    if (residual)  // out = dot + residual, as the reference's residual-fused store
+        for (size_t i = 0; i < size_t(seq_len) * rows; ++i) out[i] = out[i] + residual[i];
+    return TC_OK;
 }
 
 const char *tc_last_error(void) { return g_err.c_str(); }

@@ -117,4 +117,14 @@ hipError_t launch_gemm_grouped(const void *W, uint64_t wstride, const ActView &a
                                uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm, uint32_t ntm_max,
                                int num_cu, void *workspace, hipStream_t st);
 
+// ---- host-side helpers shared by the entry-point files (tc_api.cpp) ----
+int device_cu_count();
+int gemm_mfma_check(int type, uint32_t S, uint32_t rows, uint32_t cols);
+size_t gemm_mfma_scratch(int type, uint32_t S, uint32_t rows, uint32_t cols, int num_cu, size_t *act_bytes);
+int gemm_mfma_into(int type, const void *w, const float *x, float *out, uint32_t S, uint32_t rows, uint32_t cols,
+                   int num_cu, void *act, void *ws, hipStream_t st);
+int gemm_entry_check(int type, const void *w, const float *x, const float *out, uint32_t S, uint32_t rows,
+                     uint32_t cols, uint32_t blocks_per_row);
+int fail_code(int code, const char *msg);
+
 }  // namespace tc

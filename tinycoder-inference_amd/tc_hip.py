@@ -48,6 +48,9 @@ SIGNATURES = {
     "tc_moe_set_gemm_min_tokens": (None, [_U32]),
     "tc_moe_router": (_I, [_P, _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P]),
     "tc_moe_select": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
+    "tc_host_matmul": (_I, [_I, _P, _P, _U32, _U32, _U32, _P, _P]),
+    "tc_host_weights_register": (_I, [_P, ctypes.c_size_t]),
+    "tc_host_weights_unregister": (_I, [_P]),
     "tc_gguf_open": (_P, [ctypes.c_char_p]),
     "tc_gguf_open_metadata": (_P, [ctypes.c_char_p]),
     "tc_gguf_close": (None, [_P]),
