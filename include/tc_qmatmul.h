@@ -96,6 +96,20 @@ int tc_gemv_dual(int type, const void *wg, const void *wu, const float *x, float
 int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_len, uint32_t rows,
             uint32_t cols, uint32_t blocks_per_row, void *stream);
 
+/* Prefill GEMM that allocates nothing: the same kernels and results as
+ * tc_gemm for Q4_K and Q8_0 (cols % 256 == 0), with its scratch (quantized
+ * activations, split / stream-K partials) in a fixed per-device array of
+ * tc_gemm_noalloc_scratch_bytes() (32 MiB) instead of the library's buffers.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Shapes whose scratch exceeds the array are refused
+ * (TC_E_UNSUPPORTED, nothing written). Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU race; calls ordered on a stream
+ * do not. */
+int tc_gemm_noalloc(int type, const void *w, const float *x, float *out, uint32_t seq_len, uint32_t rows,
+                    uint32_t cols, uint32_t blocks_per_row, void *stream);
+size_t tc_gemm_noalloc_scratch_bytes(void);
+
 /* Shape-based preference of the int8 path over an fp16 twin. The fp16-twin
  * path does not exist in this build, so it answers 1 for every supported type.
  * Replaces tinycoder::gpu::int8GemmPreferred (include/Int8Gemm.hpp:73). */
