@@ -6,7 +6,9 @@ gate/up 18944x3584, down 3584x18944 -- with weights drawn from N(0, 0.02)
 and quantized by the reference's own Q4_K quantizer (bit-exact GPU port),
 activations N(0, 1). A step is one pass over the layer in decode order, as 4
 launches: q/k/v in one launch on the shared input, o, gate/up as a pair with
-the SwiGLU epilogue, down (each launch quantizes its input in-kernel). The weights of 8 identical layer copies are rotated step by
+the SwiGLU epilogue, down (each launch quantizes its input in-kernel), issued
+as one HIP graph replay per step (the eager 4-launch sequence is timed
+beside it). The weights of 8 identical layer copies are rotated step by
 step (1.05 GB working set) so that the 256 MB Infinity Cache cannot serve them.
 
 Prints one JSON line. `value` is whole-step weight+activation bytes per
@@ -461,6 +463,26 @@ def main():
         print(json.dumps({"pmc_probe": True, "copy_bytes": 2 * src.numel() * 4, "steps": args.steps}), flush=True)
         return
 
+    # ---- the step as a HIP graph ------------------------------------------------------
+    # One graph per weight copy, each holding one step's 4 launches, captured
+    # after the warm-up (which sized every scratch buffer, so nothing
+    # allocates under capture); a step is one replay. This is how a serving
+    # loop issues a decode step; the eager launch sequence is timed beside it.
+    graphs = []
+    cap_stream = torch.cuda.Stream()
+    cap_stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap_stream):
+        for c in range(N_COPIES):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cap_stream):
+                step(c)
+            graphs.append(g)
+    torch.cuda.current_stream().wait_stream(cap_stream)
+    torch.cuda.synchronize()
+    for i in range(N_COPIES):
+        graphs[i].replay()
+    torch.cuda.synchronize()
+
     # ---- timed region: K steps ------------------------------------------------------
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
@@ -468,10 +490,21 @@ def main():
     head_start(torch)
     t_start.record()
     for i in range(args.steps):
-        step(i)
+        graphs[i % N_COPIES].replay()
     t_end.record()
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
+
+    # the same K steps issued eagerly (4 launches each from the host)
+    e_start = torch.cuda.Event(enable_timing=True)
+    e_end = torch.cuda.Event(enable_timing=True)
+    head_start(torch)
+    e_start.record()
+    for i in range(args.steps):
+        step(i)
+    e_end.record()
+    torch.cuda.synchronize()
+    eager_ms_per_step = e_start.elapsed_time(e_end) / args.steps
 
     # the same layer as one launch (7 independent mat-vecs, one kernel)
     t1s = torch.cuda.Event(enable_timing=True)
@@ -524,6 +557,9 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "k_gemv_t<Q4_K,1,CfgBig> gate/up pair 2x18944x3584 with SwiGLU epilogue "
                                "(the step's largest launch); bytes = weights + x + both outputs per launch"},
+        "step_issue": {"timed": "one HIP graph replay per step (4 launches)",
+                       "eager_ms_per_step": round(eager_ms_per_step, 4),
+                       "eager_GB/s": round(step_bytes / (eager_ms_per_step * 1e-3) / 1e9, 1)},
         "per_launch": per_launch,
         "layer_one_launch": {"us": round(one_launch_ms * 1e3, 2), "GB/s": round(one_launch_gbs, 1),
                              "frac": round(one_launch_gbs / HBM_PEAK_GBS, 4)},

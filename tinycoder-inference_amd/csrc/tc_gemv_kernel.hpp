@@ -1169,7 +1169,9 @@ struct TDot<kIQ2_XS, S> {
     }
 };
 
-template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false>
+// ONE: a single-job launch, whose descriptor is read without the job-table
+// lookup (one round of kernel-argument loads instead of two).
+template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false, bool ONE = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1185,9 +1187,11 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     float *spart = reinterpret_cast<float *>(smem + L.off_p);
 
     uint32_t j = 0;
+    if constexpr (!ONE) {
 #pragma unroll
-    for (int k = 1; k < kMaxJobs; ++k)
-        if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
+        for (int k = 1; k < kMaxJobs; ++k)
+            if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
+    }
     TJobDev jb = L.jobs[j];
     uint32_t lw = blockIdx.x - jb.wg_begin;
     bool no_expert = false;
@@ -1433,14 +1437,14 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     }
 }
 
-template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false>
+template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false, bool ONE = false>
 hipError_t launch_tiled_sd(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_t st) {
     // Dynamic LDS above 64 KB needs the per-kernel opt-in, once per process.
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG, C, RG, KEEP>), hipFuncAttributeMaxDynamicSharedMemorySize,
-        160 * 1024);
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG, C, RG, KEEP, ONE>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    k_gemv_t<TYPE, S, DBG, C, RG, KEEP><<<g, C::NT, lds, st>>>(a);
+    k_gemv_t<TYPE, S, DBG, C, RG, KEEP, ONE><<<g, C::NT, lds, st>>>(a);
     return hipSuccess;
 }
 
@@ -1459,13 +1463,21 @@ hipError_t launch_tiled_s(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_
     if (rg) {
         if constexpr (TYPE == kQ4_K && S == 1) {
             if (dbg || a.njobs != 1) return hipErrorInvalidValue;
-            return launch_tiled_sd<TYPE, S, false, C, true, true>(a, g, lds, st);
+            return launch_tiled_sd<TYPE, S, false, C, true, true, true>(a, g, lds, st);
         }
         return hipErrorInvalidValue;
     }
     if constexpr (TYPE == kQ4_K && S == 1)
-        if (experts && !dbg) return launch_tiled_sd<TYPE, S, false, C, false, true>(a, g, lds, st);
-    return dbg ? launch_tiled_sd<TYPE, S, true, C>(a, g, lds, st) : launch_tiled_sd<TYPE, S, false, C>(a, g, lds, st);
+        if (experts && !dbg) {
+            if (a.njobs != 1) return hipErrorInvalidValue;
+            return launch_tiled_sd<TYPE, S, false, C, false, true, true>(a, g, lds, st);
+        }
+    if (dbg) return launch_tiled_sd<TYPE, S, true, C>(a, g, lds, st);
+    // one-token single-job launches (most decode launches): the descriptor
+    // without the job-table lookup
+    if constexpr (S == 1)
+        if (a.njobs == 1) return launch_tiled_sd<TYPE, S, false, C, false, false, true>(a, g, lds, st);
+    return launch_tiled_sd<TYPE, S, false, C>(a, g, lds, st);
 }
 
 template <int TYPE, class C>
