@@ -7,7 +7,7 @@ and quantized by the reference's own Q4_K quantizer (bit-exact GPU port),
 activations N(0, 1). A step is one pass over the layer in decode order, as 4
 launches: q/k/v in one launch on the shared input, o, gate/up as a pair with
 the SwiGLU epilogue, down (each launch quantizes its input in-kernel), issued
-as one HIP graph replay per step (the eager 4-launch sequence is timed
+as HIP graph replays of 8 steps (the eager 4-launch sequence is timed
 beside it). The weights of 8 identical layer copies are rotated step by
 step (1.05 GB working set) so that the 256 MB Infinity Cache cannot serve them.
 
@@ -147,6 +147,7 @@ def cpu_baseline(weights_host, xs_host, row_bytes):
 
 GEMM_SHAPES = [(17408, 5120), (5120, 17408)]   # (rows N, cols K), out x in
 GEMM_TOKENS = [128, 512, 2048]
+GEMM_7B_SHAPES = [(18944, 3584), (3584, 18944)]   # qwen2.5-7b FFN up and down
 INT8_PEAK_TOPS = 5000.0
 
 
@@ -156,8 +157,10 @@ def gemm_bench(torch, tc, tc_hip, dev, reps):
     encoders, rotating copies of at least 600 MB in all; x ~ N(0,1). Returns one record per config."""
     gen = torch.Generator(device=dev).manual_seed(7)
     res = []
-    for qt, tname in ((tc_hip.Q4_K, "Q4_K"), (tc_hip.Q8_0, "Q8_0")):
-        for N, K in GEMM_SHAPES:
+    legs = [(tc_hip.Q4_K, "Q4_K", GEMM_SHAPES), (tc_hip.Q8_0, "Q8_0", GEMM_SHAPES),
+            (tc_hip.Q6_K, "Q6_K", GEMM_7B_SHAPES), (tc_hip.IQ3_XXS, "IQ3_XXS", GEMM_7B_SHAPES)]
+    for qt, tname, shapes in legs:
+        for N, K in shapes:
             wf = torch.randn((N, K), generator=gen, device=dev) * 0.02
             w0 = tc.encode(qt, wf)
             del wf
@@ -463,25 +466,38 @@ def main():
         print(json.dumps({"pmc_probe": True, "copy_bytes": 2 * src.numel() * 4, "steps": args.steps}), flush=True)
         return
 
-    # ---- the step as a HIP graph ------------------------------------------------------
-    # One graph per weight copy, each holding one step's 4 launches, captured
-    # after the warm-up (which sized every scratch buffer, so nothing
-    # allocates under capture); a step is one replay. This is how a serving
-    # loop issues a decode step; the eager launch sequence is timed beside it.
-    graphs = []
+    # ---- the steps as HIP graphs -----------------------------------------------------
+    # One graph holds N_COPIES consecutive steps (one per weight copy, 4
+    # launches each), captured after the warm-up (which sized every scratch
+    # buffer, so nothing allocates under capture); K steps are K // N_COPIES
+    # replays of it plus single-step graphs for the remainder. This is how a
+    # serving loop issues decode steps; the eager launch sequence is timed
+    # beside it.
     cap_stream = torch.cuda.Stream()
     cap_stream.wait_stream(torch.cuda.current_stream())
+    one = []
     with torch.cuda.stream(cap_stream):
+        block = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(block, stream=cap_stream):
+            for c in range(N_COPIES):
+                step(c)
         for c in range(N_COPIES):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=cap_stream):
                 step(c)
-            graphs.append(g)
+            one.append(g)
     torch.cuda.current_stream().wait_stream(cap_stream)
     torch.cuda.synchronize()
-    for i in range(N_COPIES):
-        graphs[i].replay()
+    block.replay()
+    for g in one:
+        g.replay()
     torch.cuda.synchronize()
+
+    def graph_steps(k):
+        for _ in range(k // N_COPIES):
+            block.replay()
+        for c in range(k % N_COPIES):
+            one[c].replay()
 
     # ---- timed region: K steps ------------------------------------------------------
     t_start = torch.cuda.Event(enable_timing=True)
@@ -489,8 +505,7 @@ def main():
     torch.cuda.synchronize()
     head_start(torch)
     t_start.record()
-    for i in range(args.steps):
-        graphs[i % N_COPIES].replay()
+    graph_steps(args.steps)
     t_end.record()
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
@@ -557,7 +572,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "k_gemv_t<Q4_K,1,CfgBig> gate/up pair 2x18944x3584 with SwiGLU epilogue "
                                "(the step's largest launch); bytes = weights + x + both outputs per launch"},
-        "step_issue": {"timed": "one HIP graph replay per step (4 launches)",
+        "step_issue": {"timed": f"HIP graph replays of {N_COPIES} steps (4 launches each), remainder as 1-step graphs",
                        "eager_ms_per_step": round(eager_ms_per_step, 4),
                        "eager_GB/s": round(step_bytes / (eager_ms_per_step * 1e-3) / 1e9, 1)},
         "per_launch": per_launch,

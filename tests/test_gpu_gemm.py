@@ -1,5 +1,6 @@
-"""GPU parity tests for the prefill GEMM (tc_gemm, int8 MFMA for Q4_K / Q8_0,
-the exact batched mat-vec path (IQ2_XS on fp32 x) for Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ4_XS / IQ4_NL / Q5_0), through the C-ABI.
+"""GPU parity tests for the prefill GEMM (tc_gemm, int8 MFMA for Q4_K / Q6_K /
+IQ3_XXS / Q8_0, the exact batched mat-vec path (IQ2_XS on fp32 x) for Q2_K /
+Q3_K / Q5_K / IQ3_S / IQ2_S / IQ4_XS / IQ4_NL / Q5_0), through the C-ABI.
 
 Bar: fp32 outputs within 1e-3 relative / 1e-4 absolute of the oracle (the C
 restatement of the reference CPU kernels, itself bit-exact with the compiled
@@ -34,8 +35,11 @@ SHAPES = [(1, 64, 256), (37, 200, 1024), (128, 256, 5120), (130, 136, 2048), (30
           (200, 1000, 4096)]
 
 
+MFMA_TYPES = [Q4_K, Q6_K, IQ3_XXS, Q8_0]
+
+
 @pytest.mark.parametrize("M,N,K", SHAPES)
-@pytest.mark.parametrize("qt", [Q4_K, Q8_0])
+@pytest.mark.parametrize("qt", MFMA_TYPES)
 def test_gemm_vs_oracle(tc, dev, oracle, qt, M, N, K):
     rng = np.random.default_rng(M * 7 + N + K + qt)
     w = enc_weights(oracle, qt, rng, N, K)
@@ -46,7 +50,7 @@ def test_gemm_vs_oracle(tc, dev, oracle, qt, M, N, K):
     assert ok, f"{NAMES[qt]} M={M} N={N} K={K}: worst err/bound {worst:.3g}"
 
 
-@pytest.mark.parametrize("qt", [Q4_K, Q8_0])
+@pytest.mark.parametrize("qt", MFMA_TYPES)
 def test_gemm_random_blocks(tc, dev, oracle, qt):
     """Arbitrary block bytes (all scale/min codes, subnormal fp16 scales)."""
     rng = np.random.default_rng(99 + qt)
@@ -59,7 +63,7 @@ def test_gemm_random_blocks(tc, dev, oracle, qt):
     assert ok, worst
 
 
-@pytest.mark.parametrize("qt", [Q2_K, Q3_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0])
+@pytest.mark.parametrize("qt", [Q2_K, Q3_K, Q5_K, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0])
 def test_gemm_exact_batched_types(tc, dev, oracle, qt):
     rng = np.random.default_rng(5 + qt)
     M, N, K = 21, 80, 512
@@ -75,7 +79,21 @@ def test_gemm_exact_batched_types(tc, dev, oracle, qt):
                                     (Q8_0, 5120, 17408)])
 def test_gemm_cfg4_full_shape(tc, dev, oracle, qt, N, K, M):
     """BASELINE config 4 at full size: both matrices, both types, M in {128,
-    512, 2048}; weights from the GPU encoder, x ~ N(0,1). The oracle checks
+    512, 2048}."""
+    full_shape_check(tc, dev, oracle, qt, N, K, M)
+
+
+@pytest.mark.parametrize("M", [128, 512])
+@pytest.mark.parametrize("qt,N,K", [(Q6_K, 18944, 3584), (Q6_K, 3584, 18944), (IQ3_XXS, 18944, 3584),
+                                    (IQ3_XXS, 3584, 18944)])
+def test_gemm_q6k_iq3_full_shape(tc, dev, oracle, qt, N, K, M):
+    """The 7B FFN shapes (18944 x 3584 up, 3584 x 18944 down) for the two
+    other MFMA types at prefill batch sizes 128 and 512."""
+    full_shape_check(tc, dev, oracle, qt, N, K, M)
+
+
+def full_shape_check(tc, dev, oracle, qt, N, K, M):
+    """Weights from the GPU encoder, x ~ N(0,1). The oracle checks
     the first and last row of every 64-row workgroup tile plus 32 seeded rows,
     against every token for M <= 512, and at M = 2048 the first and last token
     of every 128-token tile, the whole last token tile and 32 seeded tokens

@@ -8,7 +8,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from qdata import Q4_K, Q8_0, gaussian
+from qdata import IQ3_XXS, Q4_K, Q6_K, Q8_0, gaussian
 
 pytestmark = pytest.mark.gpu
 
@@ -17,7 +17,7 @@ def P(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-@pytest.mark.parametrize("qt", [Q4_K, Q8_0])
+@pytest.mark.parametrize("qt", [Q4_K, Q6_K, IQ3_XXS, Q8_0])
 def test_gemm_noalloc_matches_gemm(tc, dev, oracle, qt):
     import torch
     from tc_hip import TC_OK

@@ -96,6 +96,10 @@ bool type_ok(int t) { return t == TC_Q8_0 || t == TC_Q5_0 || t == TC_IQ4_NL || t
 
 bool g_q8_gemm_enabled = true;
 
+// Weight types of the int8 MFMA prefill GEMM (the others run the decode
+// kernel over groups of 8 tokens).
+bool mfma_gemm_type(int t) { return t == TC_Q4_K || t == TC_Q6_K || t == TC_IQ3_XXS || t == TC_Q8_0; }
+
 tc::ActView act_view(void *buf, const tc::ActLayout &L, size_t tok, int type, uint32_t cols) {
     const uint32_t blk = type == TC_Q8_0 ? 32u : 256u;
     char *b = static_cast<char *>(buf);
@@ -232,7 +236,7 @@ int device_cu_count() {
 
 // Shape limits of the MFMA prefill GEMM (Q4_K, Q8_0; cols % 256 == 0).
 int gemm_mfma_check(int type, uint32_t S, uint32_t rows, uint32_t cols) {
-    if (type != TC_Q4_K && type != TC_Q8_0) return fail(TC_E_UNSUPPORTED, "type %d has no MFMA GEMM", type);
+    if (!mfma_gemm_type(type)) return fail(TC_E_UNSUPPORTED, "type %d has no MFMA GEMM", type);
     if (cols % 256) return fail(TC_E_UNSUPPORTED, "cols=%u is not a multiple of 256", cols);
     // 32-bit buffer offsets in the MFMA kernels
     if (uint64_t(S) * cols >= (uint64_t(1) << 32) || uint64_t(rows) * tc_row_bytes(type, cols) >= (uint64_t(1) << 32))
@@ -407,8 +411,8 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
         x = p.x;
         cols = p.cols;
     }
-    if (type != TC_Q4_K && type != TC_Q8_0) {
-        // Q2_K / Q3_K / Q5_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS / IQ4_NL / Q5_0: the exact batched path (the reference's launchQGemm,
+    if (!mfma_gemm_type(type)) {
+        // Q2_K / Q3_K / Q5_K / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS / IQ4_NL / Q5_0: the exact batched path (the reference's launchQGemm,
         // GpuGemvIQInt8.hpp:771-847) -- the decode kernel over token groups.
         for (uint32_t s0 = 0; s0 < seq_len; s0 += 8) {
             const uint32_t S = std::min(8u, seq_len - s0);

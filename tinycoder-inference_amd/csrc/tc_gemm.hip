@@ -53,21 +53,27 @@ constexpr int PL = 272;       // LDS plane row stride (256 + 16: conflict-free b
 // LDS layout (bytes); at most 80 KB for either weight type, so that two
 // workgroups fit a CU and one's conversion / epilogue overlaps the other's
 // MFMA work.
+// Weight types whose products run on int8 digit planes: every weight of a
+// superblock becomes an exact integer e (Q4_K sc*q, Q6_K sc*(q-32), IQ3_XXS
+// (2ls+1)*signed grid value) written as two int8 planes, 128*hi + lo.
+__host__ __device__ constexpr bool dig_type(int t) { return t == kQ4_K || t == kQ6_K || t == kIQ3_XXS; }
+
 template <int TYPE>
 struct GLds {
-    static constexpr bool K = TYPE == kQ4_K;
+    static constexpr bool K = dig_type(TYPE);
+    static constexpr bool M4 = TYPE == kQ4_K;  // the Q4_K min term
     static constexpr uint32_t A0 = 0;                                 // Q4_K hi plane / Q8_0 weights [GN][PL]
     static constexpr uint32_t A1 = A0 + GN * PL;                      // Q4_K lo plane [GN][PL]
     static constexpr uint32_t AM = A1 + (K ? GN * PL : 0);            // Q4_K mins, 8 bytes + 24 zero [GN][32]
-    static constexpr uint32_t AS = AM + (K ? GN * 32 : 0);            // Q4_K d [GN] | Q8_0 dw [GN][8]
+    static constexpr uint32_t AS = AM + (M4 ? GN * 32 : 0);           // row d [GN] (IQ3_XXS: d/4) | Q8_0 dw [GN][8]
     static constexpr uint32_t AD = AS + (K ? GN * 4 : GN * 32);       // Q4_K dmin [GN]
     // activation int8 [GM][BP]; Q4_K: 256-byte rows, 16-byte chunk j of
     // token t at slot j ^ (t & 15) (written by direct-to-LDS loads)
     static constexpr uint32_t BP = K ? 256 : PL;
-    static constexpr uint32_t B = AD + (K ? GN * 4 : 0);
+    static constexpr uint32_t B = AD + (M4 ? GN * 4 : 0);
     static constexpr uint32_t BL = B + GM * BP;                       // Q4_K pair-sum low digits, 8 + 24 zero [GM][32]
-    static constexpr uint32_t BH = BL + (K ? GM * 32 : 0);            // Q4_K pair-sum high digits [GM][32]
-    static constexpr uint32_t BD = BH + (K ? GM * 32 : 0);            // Q8_K d [GM] | Q8_0 d [GM][8]
+    static constexpr uint32_t BH = BL + (M4 ? GM * 32 : 0);           // Q4_K pair-sum high digits [GM][32]
+    static constexpr uint32_t BD = BH + (M4 ? GM * 32 : 0);           // Q8_K d [GM] | Q8_0 d [GM][8]
     static constexpr uint32_t RAW = BD + (K ? GM * 4 : GM * 32);      // Q8_0 raw weight tile [GN][272]
     static constexpr uint32_t bytes = RAW + (K ? 0 : GN * 272);
 };
@@ -123,9 +129,16 @@ __device__ __forceinline__ void digits4(uint32_t q, uint32_t sc, uint32_t &hi, u
 template <int TYPE>
 struct GPrefetch {
     // Q4_K: the 16-byte header and the 32 quant bytes this thread converts
-    // (row tid/4, quarter tid%4); Q8_0: raw 16-byte chunks of the tile.
-    static constexpr int RAWC = TYPE == kQ4_K ? 3 : (GN * 272 / 16 + GT - 1) / GT;
+    // (row tid/4, quarter tid%4); Q6_K: its 16-byte runs of ql (two) and qh,
+    // read from 4-byte-aligned addresses (blocks are 2-byte aligned) with
+    // their fifth dwords in ex, then the scale bytes and d; IQ3_XXS: its 16
+    // grid-index bytes (+1 dword), its 8 scale/sign bytes and d. Q8_0: raw
+    // 16-byte chunks of the tile.
+    static constexpr int RAWC = TYPE == kQ4_K || TYPE == kQ6_K ? 3 : TYPE == kIQ3_XXS ? 1 : (GN * 272 / 16 + GT - 1) / GT;
+    static constexpr int EXC = TYPE == kQ6_K ? 7 : TYPE == kIQ3_XXS ? 5 : 1;
     u4 raw[RAWC];
+    uint32_t ex[EXC];
+    uint32_t sh;           // Q6_K / IQ3_XXS: the block's byte offset mod 4
     static constexpr int ACTC = TYPE == kQ8_0 ? GM * 16 / GT : 0;
     u4 act[ACTC > 0 ? ACTC : 1];  // 16-byte activation chunks (Q8_0; Q4_K loads them straight into LDS)
     u4 side;               // Q8_K bsums (256 chunks) or Q8_0 d (256 chunks)
@@ -138,6 +151,7 @@ struct GPrefetch {
 struct GSrc {
     __amdgpu_buffer_rsrc_t w, q, d, bs;
     uint32_t vw, vw2, vq, vd, vbs;  // per-lane offsets (vw2: Q4_K quant bytes / unused)
+    uint32_t vo[4];                 // Q6_K / IQ3_XXS: this thread's byte offsets inside a block
     uint32_t vr[5];                 // Q8_0 raw chunks
 };
 
@@ -155,6 +169,22 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
     g.bs = grsrc(a.bsums, TYPE == kQ8_0 ? 0 : uint64_t(a.M) * (a.K / 16) * 2);
     g.vw = (n0 + tid / 4) * a.row_bytes;
     g.vw2 = g.vw + 16 + 32 * (tid & 3);
+    if constexpr (TYPE == kQ6_K) {
+        // thread (row tid/4, half n = bit 1, part p = bit 0): ql[64n + 16p ..],
+        // ql[64n + 32 + 16p ..], qh[32n + 16p ..] (16 bytes each), scales 8n..8n+7
+        const uint32_t n = (tid >> 1) & 1, pp = tid & 1;
+        g.vo[0] = 64 * n + 16 * pp;
+        g.vo[1] = 64 * n + 32 + 16 * pp;
+        g.vo[2] = 128 + 32 * n + 16 * pp;
+        g.vo[3] = 192 + 8 * n;
+    } else if constexpr (TYPE == kIQ3_XXS) {
+        // thread (row tid/4, quarter qq): grid indices qs[16qq ..] at 2 + 16qq,
+        // the two scale/sign words at 66 + 8qq
+        const uint32_t qq = tid & 3;
+        g.vo[0] = 2 + 16 * qq;
+        g.vo[1] = 66 + 8 * qq;
+        g.vo[2] = g.vo[3] = 0;
+    }
     // Activations are block-major: 256-column block b of token m at b * M + m.
     g.vq = (m0 + tid / 16) * 256 + 16 * (tid & 15);
     const uint32_t ms = m0 + (tid & 255) / 2;
@@ -175,6 +205,27 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
         p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw, b * UB, 0);
         p.raw[1] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2, b * UB, 0);
         p.raw[2] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2 + 16, b * UB, 0);
+    } else if constexpr (TYPE == kQ6_K) {
+        const uint32_t blk = g.vw + b * UB;  // block start (2-byte aligned)
+        p.sh = blk & 3;
+        const uint32_t al = blk & ~3u;  // every vo is a multiple of 4
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            p.raw[i] = __builtin_amdgcn_raw_buffer_load_b128(g.w, al + g.vo[i], 0, 0);
+            p.ex[i] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + g.vo[i] + 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i) p.ex[3 + i] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + g.vo[3] + 4 * i, 0, 0);
+        p.ex[6] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + 208, 0, 0);  // d (bytes 208, 209)
+    } else if constexpr (TYPE == kIQ3_XXS) {
+        const uint32_t blk = g.vw + b * UB;
+        p.sh = blk & 3;
+        const uint32_t al = blk & ~3u, alq = (blk + 2) & ~3u;  // d at 0; qs and signs at 2 mod 4 from it
+        p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, alq + g.vo[0] - 2, 0, 0);
+        p.ex[0] = __builtin_amdgcn_raw_buffer_load_b32(g.w, alq + g.vo[0] - 2 + 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) p.ex[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(g.w, alq + g.vo[1] - 2 + 4 * i, 0, 0);
+        p.ex[4] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al, 0, 0);
     } else {
 #pragma unroll
         for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i)
@@ -185,9 +236,10 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
         p.act[i] = __builtin_amdgcn_raw_buffer_load_b128(g.q, g.vq, b * a.M * 256 + i * 16 * 256, 0);
     if constexpr (TYPE == kQ8_0)
         p.side = __builtin_amdgcn_raw_buffer_load_b128(g.d, g.vbs, b * a.M * 32, 0);
-    else
+    else if constexpr (TYPE == kQ4_K)
         p.side = __builtin_amdgcn_raw_buffer_load_b128(g.bs, g.vbs, b * a.M * 32, 0);
-    if constexpr (TYPE == kQ4_K) p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * a.M * 4, 0));
+    if constexpr (dig_type(TYPE))
+        p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * a.M * 4, 0));
 }
 
 // Q4_K weights of this thread (row tid/4: header + qs[32qq .. 32qq+31]) ->
@@ -231,14 +283,137 @@ __device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u
     reinterpret_cast<float *>(lds + L::AD)[r] = h2f(hdr.x >> 16);
 }
 
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// Signed byte digits of e = k * v for four values packed in a word (16-bit
+// lanes: v at bytes 0 and 2 of `even`, bytes 1 and 3 of the original at bytes 0
+// and 2 of `odd`), |e| <= 4096: hi = e >> 7 (arithmetic) and lo = e & 127 as
+// bytes in the original order, so that e = 128*hi + lo exactly.
+__device__ __forceinline__ void digits_s16(s16x2 ve, s16x2 vo, short k, uint32_t &hi, uint32_t &lo) {
+    const s16x2 kk = {k, k};
+    const s16x2 ee = ve * kk, eo = vo * kk;
+    const s16x2 he = ee >> s16x2{7, 7}, ho = eo >> s16x2{7, 7};
+    const uint32_t le = __builtin_bit_cast(uint32_t, ee) & 0x007F007Fu, lo_ = __builtin_bit_cast(uint32_t, eo) & 0x007F007Fu;
+    lo = __builtin_amdgcn_perm(lo_, le, 0x06020400u);
+    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he), 0x06020400u);
+}
+
+// Four unsigned 6-bit values per word (Q6_K q) -> digits of sc * (q - 32).
+__device__ __forceinline__ void digits_q6(uint32_t q, int sc, uint32_t &hi, uint32_t &lo) {
+    const s16x2 ve = __builtin_bit_cast(s16x2, q & 0x00FF00FFu) - s16x2{32, 32};
+    const s16x2 vo = __builtin_bit_cast(s16x2, (q >> 8) & 0x00FF00FFu) - s16x2{32, 32};
+    digits_s16(ve, vo, short(sc), hi, lo);
+}
+
+// Four signed bytes per word (IQ3_XXS signed grid values) -> digits of k * v.
+__device__ __forceinline__ void digits_i8(uint32_t v, int k, uint32_t &hi, uint32_t &lo) {
+    // sign extension per 16-bit lane: (b ^ 0x80) - 0x80
+    const s16x2 ve = __builtin_bit_cast(s16x2, (v & 0x00FF00FFu) ^ 0x00800080u) - s16x2{128, 128};
+    const s16x2 vo = __builtin_bit_cast(s16x2, ((v >> 8) & 0x00FF00FFu) ^ 0x00800080u) - s16x2{128, 128};
+    digits_s16(ve, vo, short(k), hi, lo);
+}
+
+__device__ __forceinline__ uint32_t realign(uint32_t hi, uint32_t lo, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+
+// Q6_K weights of this thread (row tid/4, half n, part p: positions
+// 128n + 32c + 16p + j of the four families c) -> the digit planes and d.
+// q = ql nibble | (qh 2-bit field) << 4 (reference dequantizeQ6_KBlock,
+// include/GGMLDequantize.hpp:503-527), e = sc[8n + 2c + p] * (q - 32).
+__device__ __forceinline__ void q6k_convert(const GPrefetch<kQ6_K> &p, unsigned char *lds, uint32_t tid) {
+    using L = GLds<kQ6_K>;
+    const uint32_t r = tid / 4, n = (tid >> 1) & 1, pp = tid & 1;
+    uint32_t w[3][4];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const uint32_t v[5] = {p.raw[i].x, p.raw[i].y, p.raw[i].z, p.raw[i].w, p.ex[i]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[i][j] = realign(v[j + 1], v[j], p.sh);
+    }
+    const uint32_t s0 = realign(p.ex[4], p.ex[3], p.sh), s1 = realign(p.ex[5], p.ex[4], p.sh);  // scales 8n..8n+7
+    const uint32_t dh = p.sh ? (p.ex[6] >> 16) : (p.ex[6] & 0xFFFFu);
+    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t sb = 2 * c + pp;  // scale byte index within the 8
+        const int sc = int(int8_t(((sb < 4 ? s0 : s1) >> (8 * (sb & 3))) & 0xFFu));
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t la = w[0][j], lb = w[1][j], qh = w[2][j];
+            uint32_t q;
+            if (c == 0) q = (la & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
+            else if (c == 1) q = (lb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
+            else if (c == 2) q = ((la >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
+            else q = ((lb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+            digits_q6(q, sc, hi[j], lo[j]);
+        }
+        const uint32_t k0 = 128 * n + 32 * c + 16 * pp;
+        *reinterpret_cast<u4 *>(a0 + k0) = u4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u4 *>(a1 + k0) = u4{lo[0], lo[1], lo[2], lo[3]};
+    }
+    reinterpret_cast<float *>(lds + L::AS)[r] = h2f(dh);
+}
+
+// IQ3_XXS weights of this thread (row tid/4, 32-chunks 2qq, 2qq+1) -> the
+// digit planes and d/4 (the 0.25 row scale of the reference's fused path,
+// include/GGMLDequantize.hpp:2148, is a power of two: exact on d). Per 4
+// weights one codebook word (grid in LDS) with the chunk's sign bits applied
+// bytewise (sign byte = 7-bit index | parity << 7), times 2ls+1
+// (GGMLDequantize.hpp:1135-1161).
+__device__ __forceinline__ void iq3_convert(const GPrefetch<kIQ3_XXS> &p, unsigned char *lds, const uint32_t *grid,
+                                            uint32_t tid) {
+    using L = GLds<kIQ3_XXS>;
+    const uint32_t r = tid / 4, qq = tid & 3;
+    const uint32_t shq = p.sh ^ 2u;  // qs and signs sit 2 bytes off the block start's alignment
+    const uint32_t v[5] = {p.raw[0].x, p.raw[0].y, p.raw[0].z, p.raw[0].w, p.ex[0]};
+    uint32_t gi[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gi[j] = realign(v[j + 1], v[j], shq);
+    const uint32_t aux[2] = {realign(p.ex[2], p.ex[1], shq), realign(p.ex[3], p.ex[2], shq)};
+    const uint32_t dh = p.sh ? (p.ex[4] >> 16) : (p.ex[4] & 0xFFFFu);
+    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+        const int k = 2 * int(aux[ch] >> 28) + 1;
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t idx7 = (aux[ch] >> (7 * l)) & 127u;
+            const uint32_t s8 = idx7 | ((__builtin_popcount(idx7) & 1u) << 7);
+            const uint32_t gw = gi[2 * ch + (l >> 1)];
+            const uint32_t g1 = grid[(gw >> (16 * (l & 1))) & 0xFFu], g2 = grid[(gw >> (16 * (l & 1) + 8)) & 0xFFu];
+            const uint32_t m1 = spread_sign4(s8 & 15u), m2 = spread_sign4(s8 >> 4);
+            digits_i8((g1 ^ m1) + (m1 & 0x01010101u), k, hi[2 * l], lo[2 * l]);
+            digits_i8((g2 ^ m2) + (m2 & 0x01010101u), k, hi[2 * l + 1], lo[2 * l + 1]);
+        }
+        const uint32_t k0 = 64 * qq + 32 * ch;
+        *reinterpret_cast<u4 *>(a0 + k0) = u4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u4 *>(a0 + k0 + 16) = u4{hi[4], hi[5], hi[6], hi[7]};
+        *reinterpret_cast<u4 *>(a1 + k0) = u4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u4 *>(a1 + k0 + 16) = u4{lo[4], lo[5], lo[6], lo[7]};
+    }
+    reinterpret_cast<float *>(lds + L::AS)[r] = 0.25f * h2f(dh);
+}
+
+__constant__ uint32_t c_iq3_grid[256] = {
+#include "iq3xxs_grid.inc"
+};
+
 // Staged registers -> LDS: the activation plane and its side data; Q4_K
 // weights converted to the digit planes straight from registers, Q8_0 raw
 // rows to a staging area (converted after the barrier).
 template <int TYPE>
-__device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned char *lds, uint32_t tid) {
+__device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned char *lds, uint32_t tid,
+                                           const uint32_t *grid = nullptr) {
     using L = GLds<TYPE>;
     if constexpr (TYPE == kQ4_K) {
         q4k_convert(p.raw[0], p.raw[1], p.raw[2], lds, tid);
+    } else if constexpr (TYPE == kQ6_K) {
+        q6k_convert(p, lds, tid);
+    } else if constexpr (TYPE == kIQ3_XXS) {
+        iq3_convert(p, lds, grid, tid);
     } else {
 #pragma unroll
         for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
@@ -251,7 +426,7 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
         const uint32_t c = tid + i * GT;
         *reinterpret_cast<u4 *>(lds + L::B + (c / 16) * PL + 16 * (c & 15)) = p.act[i];
     }
-    {
+    if constexpr (TYPE == kQ8_0 || TYPE == kQ4_K) {
         const uint32_t m = (tid & 255) / 2, h = tid & 1;
         if constexpr (TYPE == kQ8_0) {
             *reinterpret_cast<u4 *>(lds + L::BD + m * 32 + 16 * h) = p.side;
@@ -279,7 +454,7 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
             }
         }
     }
-    if constexpr (TYPE == kQ4_K) {
+    if constexpr (dig_type(TYPE)) {
         reinterpret_cast<float *>(lds + L::BD)[tid & (GM - 1)] = p.d8;  // threads tid and tid+128 hold the same d
     }
 }
@@ -314,10 +489,10 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
 // wave instruction fills 1 KB = 4 token rows; lane l writes slot l%16 of
 // token 4k + l/16 and so reads chunk (l%16) ^ (t%16) of its 256 bytes. Tokens past M read the next
 // superblock's bytes (their outputs are never stored); past the buffer, zeros.
-template <int CW>
-__device__ __forceinline__ void q4k_act_to_lds(const GemmArgs &a, uint32_t m0, uint32_t b, unsigned char *ldsb,
+template <int TYPE, int CW>
+__device__ __forceinline__ void dig_act_to_lds(const GemmArgs &a, uint32_t m0, uint32_t b, unsigned char *ldsb,
                                                uint32_t w, uint32_t lane) {
-    using L = GLds<kQ4_K>;
+    using L = GLds<TYPE>;
     typedef int v4i32 __attribute__((ext_vector_type(4)));
     const uint64_t base = reinterpret_cast<uint64_t>(a.qs);
     const v4i32 rs = {int(uint32_t(base)), int(uint32_t(base >> 32) & 0xFFFF), int(a.M * a.K), 0x00020000};
@@ -346,10 +521,11 @@ __device__ __forceinline__ void q4k_act_to_lds(const GemmArgs &a, uint32_t m0, u
 // One superblock of a consumer wave's 32-row x (32 NTT)-token Q4_K tile from
 // the LDS planes at `lds` (MFMA chains and the fp32 combination into acc).
 // tok0: the wave's first token row in the tile.
-template <int NTT>
-__device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t wn, uint32_t tok0, uint32_t li,
+template <int TYPE, int NTT>
+__device__ __forceinline__ void dig_consume(const unsigned char *lds, uint32_t wn, uint32_t tok0, uint32_t li,
                                             uint32_t lg, float (&acc)[NTT][16]) {
-    using L = GLds<kQ4_K>;
+    using L = GLds<TYPE>;
+    constexpr bool MIN = L::M4;
     const unsigned char *arow = lds + (32 * wn + li) * PL + 16 * lg;
     // token rows tok0 + 32t + li (all with t % 16 = li % 16)
     auto brow = [&](int t) __attribute__((always_inline)) { return lds + L::B + (tok0 + 32 * t + li) * L::BP; };
@@ -365,15 +541,13 @@ __device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t w
     }
 #pragma unroll
     for (int s = 0; s < 8; ++s) al[s] = as_v4i(lds4(arow + L::A1 + 32 * s));
-    const v4i am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
+    v4i am = v4i{0, 0, 0, 0};
+    if constexpr (MIN) am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
     __builtin_amdgcn_sched_barrier(0);
     // One accumulator per token tile: the hi-digit chain, then C = hi << 7
     // and the lo-digit chain on top (= 128*hi + lo exactly); the min term over
     // the 8 useful k slots (k-group 0, bytes 0..7) folded the same way.
     auto chain = [&](int t, v16i &c, v16i &m) __attribute__((always_inline)) {
-        const uint32_t tb = tok0 + 32 * t + li;
-        const v4i bh = as_v4i(lds4(lds + L::BH + tb * 32 + 16 * lg));
-        const v4i bl = as_v4i(lds4(lds + L::BL + tb * 32 + 16 * lg));
         c = v16i{};
 #pragma unroll
         for (int s = 0; s < 8; ++s) c = mfma(ah[s], x[s], c);
@@ -381,10 +555,15 @@ __device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t w
         for (int r = 0; r < 16; ++r) c[r] <<= 7;
 #pragma unroll
         for (int s = 0; s < 8; ++s) c = mfma(al[s], x[s], c);
-        m = mfma(am, bh, v16i{});
+        if constexpr (MIN) {
+            const uint32_t tb = tok0 + 32 * t + li;
+            const v4i bh = as_v4i(lds4(lds + L::BH + tb * 32 + 16 * lg));
+            const v4i bl = as_v4i(lds4(lds + L::BL + tb * 32 + 16 * lg));
+            m = mfma(am, bh, v16i{});
 #pragma unroll
-        for (int r = 0; r < 16; ++r) m[r] <<= 7;
-        m = mfma(am, bl, m);
+            for (int r = 0; r < 16; ++r) m[r] <<= 7;
+            m = mfma(am, bl, m);
+        }
     };
     auto combine = [&](int t, const v16i &c, const v16i &m) __attribute__((always_inline)) {
         const float d8 = reinterpret_cast<const float *>(lds + L::BD)[tok0 + 32 * t + li];
@@ -392,12 +571,21 @@ __device__ __forceinline__ void q4k_consume(const unsigned char *lds, uint32_t w
         for (int q = 0; q < 4; ++q) {
             const uint32_t rr = 32 * wn + 8 * q + 4 * lg;
             const float4 dv = *reinterpret_cast<const float4 *>(lds + L::AS + 4 * rr);
-            const float4 mv = *reinterpret_cast<const float4 *>(lds + L::AD + 4 * rr);
-            const float dd[4] = {dv.x, dv.y, dv.z, dv.w}, dm[4] = {mv.x, mv.y, mv.z, mv.w};
+            const float dd[4] = {dv.x, dv.y, dv.z, dv.w};
+            if constexpr (MIN) {
+                const float4 mv = *reinterpret_cast<const float4 *>(lds + L::AD + 4 * rr);
+                const float dm[4] = {mv.x, mv.y, mv.z, mv.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 4 * q + e;
-                acc[t][r] = fmaf(d8, dd[e] * float(c[r]) - dm[e] * float(m[r]), acc[t][r]);
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * q + e;
+                    acc[t][r] = fmaf(d8, dd[e] * float(c[r]) - dm[e] * float(m[r]), acc[t][r]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * q + e;
+                    acc[t][r] = fmaf(d8, dd[e] * float(c[r]), acc[t][r]);
+                }
             }
         }
     };
@@ -452,8 +640,8 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const unsigned char *arow = lds + (32 * wn + li) * PL + 16 * lg;
         const unsigned char *brow0 = lds + L::B + (64 * wm + li) * PL + 16 * lg;
         const unsigned char *brow1 = brow0 + 32 * PL;
-        if constexpr (TYPE == kQ4_K) {
-            static_assert(TYPE != kQ4_K, "Q4_K runs k_gemm_q4k_ws");
+        if constexpr (dig_type(TYPE)) {
+            static_assert(!dig_type(TYPE), "the digit-plane types run k_gemm_dig");
         } else {
             const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
 #pragma unroll 2
@@ -552,11 +740,11 @@ __host__ __device__ inline uint32_t sk_begin(uint32_t units, uint32_t grid, uint
     return uint32_t(uint64_t(units) * w / grid);
 }
 
-template <int CW, bool GRP>
-__global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 + CW / 4, 1 + CW / 4))) void k_gemm_q4k_ws(
+template <int TYPE, int CW, bool GRP>
+__global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 + CW / 4, 1 + CW / 4))) void k_gemm_dig(
     GemmArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
-    using L = GLds<kQ4_K>;
+    using L = GLds<TYPE>;
     constexpr int NTT = 8 / CW;  // 32-token tiles per consumer wave
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -566,6 +754,12 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
     const uint32_t li = lane & 31, lg = lane >> 5;
     const uint32_t ptid = tid - 64 * CW;  // producer thread index 0..255
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
+    // IQ3_XXS codebook in LDS, past the two buffers (read by the producers' conversion)
+    uint32_t *grid = reinterpret_cast<uint32_t *>(lds + 2 * L::bytes);
+    if constexpr (TYPE == kIQ3_XXS) {
+        for (uint32_t i = tid; i < 256; i += blockDim.x) grid[i] = c_iq3_grid[i];
+        __syncthreads();
+    }
 
     const uint32_t ntm = sk_ntm<GRP>(a);
     const uint32_t units = (GRP ? ntm * a.ntn : a.ntiles) * a.nblk;
@@ -587,19 +781,19 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
         if (producer) {
             // Two superblocks of loads in flight per producer thread: global
             // latency under load exceeds one superblock's compute time.
-            const GSrc gs = gemm_src<kQ4_K>(a, n0, m0, ptid, tg.W);
-            GPrefetch<kQ4_K> pa, pb;
-            gemm_prefetch<kQ4_K>(a, gs, b0, pa);
-            gemm_stage<kQ4_K>(pa, buf(b0), ptid);
-            gemm_prefetch<kQ4_K>(a, gs, min(b0 + 1, b1 - 1), pa);
-            gemm_prefetch<kQ4_K>(a, gs, min(b0 + 2, b1 - 1), pb);
+            const GSrc gs = gemm_src<TYPE>(a, n0, m0, ptid, tg.W);
+            GPrefetch<TYPE> pa, pb;
+            gemm_prefetch<TYPE>(a, gs, b0, pa);
+            gemm_stage<TYPE>(pa, buf(b0), ptid, grid);
+            gemm_prefetch<TYPE>(a, gs, min(b0 + 1, b1 - 1), pa);
+            gemm_prefetch<TYPE>(a, gs, min(b0 + 2, b1 - 1), pb);
             __syncthreads();
             // Straight-line steps (past the end they stage into the idle buffer
             // and reload the last superblock), so the compiler's wait counts
             // stay exact.
-            auto step = [&](GPrefetch<kQ4_K> &pf, uint32_t b) __attribute__((always_inline)) {
-                gemm_stage<kQ4_K>(pf, buf(b + 1), ptid);
-                gemm_prefetch<kQ4_K>(a, gs, min(b + 3, b1 - 1), pf);
+            auto step = [&](GPrefetch<TYPE> &pf, uint32_t b) __attribute__((always_inline)) {
+                gemm_stage<TYPE>(pf, buf(b + 1), ptid, grid);
+                gemm_prefetch<TYPE>(a, gs, min(b + 3, b1 - 1), pf);
                 __syncthreads();
             };
             for (uint32_t b = b0; b < bend; b += 2) {
@@ -616,12 +810,12 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
         // Consumers fill the activation planes: superblock b+1 goes into the
         // other buffer while b is multiplied (their only memory loads, so the
         // wait before each barrier waits for nothing else).
-        q4k_act_to_lds<CW>(a, m0, b0, buf(b0), wave, lane);
+        dig_act_to_lds<TYPE, CW>(a, m0, b0, buf(b0), wave, lane);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
         for (uint32_t b = b0; b < bend; ++b) {
-            q4k_act_to_lds<CW>(a, m0, min(b + 1, b1 - 1), buf(b + 1), wave, lane);
-            if (b < b1) q4k_consume<NTT>(buf(b), wn, tok0, li, lg, acc);
+            dig_act_to_lds<TYPE, CW>(a, m0, min(b + 1, b1 - 1), buf(b + 1), wave, lane);
+            if (b < b1) dig_consume<TYPE, NTT>(buf(b), wn, tok0, li, lg, acc);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this superblock's plane is in LDS
             __syncthreads();
         }
@@ -700,12 +894,13 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
 
 template <int TYPE, bool GRP = false>
 hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
-    if constexpr (TYPE == kQ4_K) {
+    if constexpr (dig_type(TYPE)) {
         constexpr int CW = 8;  // consumer waves (4 measured 10-15% slower)
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_q4k_ws<CW, GRP>),
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_dig<TYPE, CW, GRP>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (attr != hipSuccess) return attr;
-        k_gemm_q4k_ws<CW, GRP><<<grid, GT + 64 * CW, 2 * GLds<TYPE>::bytes, st>>>(a);
+        const uint32_t lds = 2 * GLds<TYPE>::bytes + (TYPE == kIQ3_XXS ? 1024 : 0);
+        k_gemm_dig<TYPE, CW, GRP><<<grid, GT + 64 * CW, lds, st>>>(a);
     } else {
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<TYPE>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -724,7 +919,7 @@ uint32_t sk_grid(uint32_t M, uint32_t N, uint32_t K, int num_cu) {
 }
 
 uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
-    if (type == kQ4_K) return 1;  // stream-K instead
+    if (dig_type(type)) return 1;  // stream-K instead
     const uint32_t tiles = ((M + GM - 1) / GM) * ((N + GN - 1) / GN);
     const uint32_t nblk = K / 256;
     uint32_t s = 1;
@@ -735,7 +930,7 @@ uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
 }
 
 size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
-    if (type == kQ4_K) return size_t(sk_grid(M, N, K, num_cu)) * 2 * GM * GN * 4;
+    if (dig_type(type)) return size_t(sk_grid(M, N, K, num_cu)) * 2 * GM * GN * 4;
     const uint32_t s = gemm_splits(type, M, N, K, num_cu);
     return s > 1 ? size_t(s) * M * N * 4 : 0;
 }
@@ -793,9 +988,9 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
     // weight matrix must each stay below 4 GiB.
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
-    if (type != kQ4_K && type != kQ8_0) return hipErrorInvalidValue;
+    if (!dig_type(type) && type != kQ8_0) return hipErrorInvalidValue;
     const uint32_t nsplit = gemm_splits(type, M, N, K, num_cu);
-    if ((nsplit > 1 || type == kQ4_K) && workspace == nullptr) return hipErrorInvalidValue;
+    if ((nsplit > 1 || dig_type(type)) && workspace == nullptr) return hipErrorInvalidValue;
     GemmArgs a{};
     a.W = static_cast<const uint8_t *>(W);
     a.qs = act.qs;
@@ -809,12 +1004,14 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
     a.ntm = (M + GM - 1) / GM;
     a.split_blk = (a.nblk + nsplit - 1) / nsplit;
     a.ntiles = a.ntm * ((N + GN - 1) / GN);
-    if (type == kQ4_K) {
+    if (dig_type(type)) {
         const uint32_t G = sk_grid(M, N, K, num_cu);
         a.out = out;
         a.ws = static_cast<float *>(workspace);
         a.skg = G;
-        hipError_t e = launch_gemm_t<kQ4_K>(a, dim3{G, 1u, 1u}, st);
+        hipError_t e = type == kQ4_K   ? launch_gemm_t<kQ4_K>(a, dim3{G, 1u, 1u}, st)
+                       : type == kQ6_K ? launch_gemm_t<kQ6_K>(a, dim3{G, 1u, 1u}, st)
+                                       : launch_gemm_t<kIQ3_XXS>(a, dim3{G, 1u, 1u}, st);
         if (e != hipSuccess) return e;
         // Any tile split over workgroups? (a range boundary inside a tile)
         bool split = false;
