@@ -158,7 +158,9 @@ def gemm_bench(torch, tc, tc_hip, dev, reps):
     gen = torch.Generator(device=dev).manual_seed(7)
     res = []
     legs = [(tc_hip.Q4_K, "Q4_K", GEMM_SHAPES), (tc_hip.Q8_0, "Q8_0", GEMM_SHAPES),
-            (tc_hip.Q6_K, "Q6_K", GEMM_7B_SHAPES), (tc_hip.IQ3_XXS, "IQ3_XXS", GEMM_7B_SHAPES)]
+            (tc_hip.Q5_K, "Q5_K", GEMM_7B_SHAPES), (tc_hip.Q6_K, "Q6_K", GEMM_7B_SHAPES),
+            (tc_hip.IQ3_XXS, "IQ3_XXS", GEMM_7B_SHAPES), (tc_hip.IQ3_S, "IQ3_S", GEMM_7B_SHAPES),
+            (tc_hip.IQ2_S, "IQ2_S", GEMM_7B_SHAPES)]
     for qt, tname, shapes in legs:
         for N, K in shapes:
             wf = torch.randn((N, K), generator=gen, device=dev) * 0.02

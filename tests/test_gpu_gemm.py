@@ -1,6 +1,7 @@
-"""GPU parity tests for the prefill GEMM (tc_gemm, int8 MFMA for Q4_K / Q6_K /
-IQ3_XXS / Q8_0, the exact batched mat-vec path (IQ2_XS on fp32 x) for Q2_K /
-Q3_K / Q5_K / IQ3_S / IQ2_S / IQ4_XS / IQ4_NL / Q5_0), through the C-ABI.
+"""GPU parity tests for the prefill GEMM (tc_gemm, int8 MFMA for Q4_K / Q5_K /
+Q6_K / IQ3_XXS / IQ3_S / IQ2_S / Q8_0, the exact batched mat-vec path (IQ2_XS
+on fp32 x) for Q2_K / Q3_K / IQ4_XS / IQ4_NL / Q5_0 / IQ2_XS), through the
+C-ABI.
 
 Bar: fp32 outputs within 1e-3 relative / 1e-4 absolute of the oracle (the C
 restatement of the reference CPU kernels, itself bit-exact with the compiled
@@ -23,7 +24,7 @@ def to_dev(a, dev):
 def enc_weights(oracle, qt, rng, rows, cols):
     # Q4_K from N(0,1): at N(0,0.02) the reference quantizer stores most
     # scales as 0 (its fp16 conversion flushes values below 2^-13).
-    return oracle.encode(qt, gaussian(rng, (rows, cols), 1.0 if qt == Q4_K else 0.02))
+    return oracle.encode(qt, gaussian(rng, (rows, cols), 1.0 if qt in (Q4_K, Q5_K) else 0.02))
 
 
 # (M tokens, N rows, K cols): ragged tiles, a K-split case (few output tiles),
@@ -35,7 +36,7 @@ SHAPES = [(1, 64, 256), (37, 200, 1024), (128, 256, 5120), (130, 136, 2048), (30
           (200, 1000, 4096)]
 
 
-MFMA_TYPES = [Q4_K, Q6_K, IQ3_XXS, Q8_0]
+MFMA_TYPES = [Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, Q8_0]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -63,7 +64,7 @@ def test_gemm_random_blocks(tc, dev, oracle, qt):
     assert ok, worst
 
 
-@pytest.mark.parametrize("qt", [Q2_K, Q3_K, Q5_K, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0])
+@pytest.mark.parametrize("qt", [Q2_K, Q3_K, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0])
 def test_gemm_exact_batched_types(tc, dev, oracle, qt):
     rng = np.random.default_rng(5 + qt)
     M, N, K = 21, 80, 512
@@ -84,11 +85,11 @@ def test_gemm_cfg4_full_shape(tc, dev, oracle, qt, N, K, M):
 
 
 @pytest.mark.parametrize("M", [128, 512])
-@pytest.mark.parametrize("qt,N,K", [(Q6_K, 18944, 3584), (Q6_K, 3584, 18944), (IQ3_XXS, 18944, 3584),
-                                    (IQ3_XXS, 3584, 18944)])
-def test_gemm_q6k_iq3_full_shape(tc, dev, oracle, qt, N, K, M):
-    """The 7B FFN shapes (18944 x 3584 up, 3584 x 18944 down) for the two
-    other MFMA types at prefill batch sizes 128 and 512."""
+@pytest.mark.parametrize("qt,N,K", [(qt, N, K) for qt in (Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S)
+                                    for N, K in ((18944, 3584), (3584, 18944))])
+def test_gemm_7b_ffn_full_shape(tc, dev, oracle, qt, N, K, M):
+    """The 7B FFN shapes (18944 x 3584 up, 3584 x 18944 down) for the other
+    MFMA types at prefill batch sizes 128 and 512."""
     full_shape_check(tc, dev, oracle, qt, N, K, M)
 
 
@@ -101,7 +102,7 @@ def full_shape_check(tc, dev, oracle, qt, N, K, M):
     exactly the full output's)."""
     import torch
     gen = torch.Generator(device=dev).manual_seed(4 + qt + N + M)
-    wf = torch.randn((N, K), generator=gen, device=dev) * (1.0 if qt == Q4_K else 0.02)
+    wf = torch.randn((N, K), generator=gen, device=dev) * (1.0 if qt in (Q4_K, Q5_K) else 0.02)
     w = tc.encode(qt, wf)
     del wf
     x = torch.randn((M, K), generator=gen, device=dev)

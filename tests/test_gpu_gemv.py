@@ -428,3 +428,32 @@ def test_float_types_refuse_quantized_activation_entry_points(tc, dev, qt):
     torch.cuda.synchronize()
     assert (out.cpu() == 7.0).all()
     del ctypes
+
+
+@pytest.mark.parametrize("qt", [IQ2_XS, IQ4_NL, Q5_0])
+def test_float_types_wide_multi_token(tc, dev, oracle, qt):
+    """fp32-activation types at cols=18944 with 8 tokens: tc_gemv and tc_gemm
+    (which split the tokens over launches when x does not fit one workgroup's
+    LDS) match the oracle, and tc_gemv_multi, which must run all tokens in one
+    launch, either matches it too or refuses without writing."""
+    import torch
+    import tc_hip
+    rng = np.random.default_rng(77 + qt)
+    S, rows, cols = 8, 256, 18944
+    w = random_blocks(qt, rng, rows, cols)
+    x = gaussian(rng, (S, cols))
+    ref = oracle_matmul_par(oracle, qt, w, x, rows, cols)
+    wd, xd = torch.from_numpy(w).to(dev), torch.from_numpy(x).to(dev)
+    for fn in (tc.gemv, tc.gemm):
+        ok, worst = close(fn(qt, wd, xd, rows, cols).cpu().numpy(), ref)
+        assert ok, (fn.__name__, worst)
+    out = torch.full((S, rows), 7.0, device=dev)
+    try:
+        tc.gemv_multi(qt, [wd], [xd], [rows], [cols], outs=[out])
+    except tc_hip.TCError as e:
+        assert e.code == tc_hip.TC_E_UNSUPPORTED
+        torch.cuda.synchronize()
+        assert (out.cpu() == 7.0).all()
+    else:
+        ok, worst = close(out.cpu().numpy(), ref)
+        assert ok, worst

@@ -8,7 +8,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from qdata import IQ3_XXS, Q4_K, Q6_K, Q8_0, gaussian
+from qdata import IQ2_S, IQ3_S, IQ3_XXS, Q4_K, Q5_K, Q6_K, Q8_0, gaussian
 
 pytestmark = pytest.mark.gpu
 
@@ -17,7 +17,7 @@ def P(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-@pytest.mark.parametrize("qt", [Q4_K, Q6_K, IQ3_XXS, Q8_0])
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, Q8_0])
 def test_gemm_noalloc_matches_gemm(tc, dev, oracle, qt):
     import torch
     from tc_hip import TC_OK
@@ -27,7 +27,7 @@ def test_gemm_noalloc_matches_gemm(tc, dev, oracle, qt):
     rng = np.random.default_rng(qt)
     bdiv = 32 if qt == Q8_0 else 256
     for M, N, K in ((300, 1000, 4096), (40, 136, 2048)):  # second call: smaller input
-        w = oracle.encode(qt, gaussian(rng, (N, K), 1.0 if qt == Q4_K else 0.02))
+        w = oracle.encode(qt, gaussian(rng, (N, K), 1.0 if qt in (Q4_K, Q5_K) else 0.02))
         x = gaussian(rng, (M, K))
         wd, xd = torch.from_numpy(w).to(dev), torch.from_numpy(x).to(dev)
         ref = tc.gemm(qt, wd, xd, N, K)

@@ -98,7 +98,9 @@ bool g_q8_gemm_enabled = true;
 
 // Weight types of the int8 MFMA prefill GEMM (the others run the decode
 // kernel over groups of 8 tokens).
-bool mfma_gemm_type(int t) { return t == TC_Q4_K || t == TC_Q6_K || t == TC_IQ3_XXS || t == TC_Q8_0; }
+bool mfma_gemm_type(int t) {
+    return t == TC_Q4_K || t == TC_Q5_K || t == TC_Q6_K || t == TC_IQ3_XXS || t == TC_IQ3_S || t == TC_IQ2_S || t == TC_Q8_0;
+}
 
 tc::ActView act_view(void *buf, const tc::ActLayout &L, size_t tok, int type, uint32_t cols) {
     const uint32_t blk = type == TC_Q8_0 ? 32u : 256u;
@@ -234,7 +236,8 @@ int device_cu_count() {
     return d ? d->num_cu : 0;
 }
 
-// Shape limits of the MFMA prefill GEMM (Q4_K, Q8_0; cols % 256 == 0).
+// Shape limits of the MFMA prefill GEMM (the int8-activation K-quant and IQ
+// types and Q8_0; cols % 256 == 0).
 int gemm_mfma_check(int type, uint32_t S, uint32_t rows, uint32_t cols) {
     if (!mfma_gemm_type(type)) return fail(TC_E_UNSUPPORTED, "type %d has no MFMA GEMM", type);
     if (cols % 256) return fail(TC_E_UNSUPPORTED, "cols=%u is not a multiple of 256", cols);

@@ -56,12 +56,21 @@ constexpr int PL = 272;       // LDS plane row stride (256 + 16: conflict-free b
 // Weight types whose products run on int8 digit planes: every weight of a
 // superblock becomes an exact integer e (Q4_K sc*q, Q6_K sc*(q-32), IQ3_XXS
 // (2ls+1)*signed grid value) written as two int8 planes, 128*hi + lo.
-__host__ __device__ constexpr bool dig_type(int t) { return t == kQ4_K || t == kQ6_K || t == kIQ3_XXS; }
+__host__ __device__ constexpr bool dig_type(int t) {
+    return t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ3_XXS || t == kIQ3_S || t == kIQ2_S;
+}
+// K-quants with a per-sub-block min (w = d*sc*q - dmin*m): the min term runs
+// on one more MFMA pair against the activation pair sums.
+__host__ __device__ constexpr bool min_type(int t) { return t == kQ4_K || t == kQ5_K; }
+// Codebook bytes the converter reads from LDS (past the two stage buffers).
+__host__ __device__ constexpr uint32_t grid_bytes(int t) {
+    return t == kIQ3_XXS ? 256 * 4 : t == kIQ3_S ? 512 * 4 : t == kIQ2_S ? 1024 * 8 : 0;
+}
 
 template <int TYPE>
 struct GLds {
     static constexpr bool K = dig_type(TYPE);
-    static constexpr bool M4 = TYPE == kQ4_K;  // the Q4_K min term
+    static constexpr bool M4 = min_type(TYPE);  // the K-quant min term
     static constexpr uint32_t A0 = 0;                                 // Q4_K hi plane / Q8_0 weights [GN][PL]
     static constexpr uint32_t A1 = A0 + GN * PL;                      // Q4_K lo plane [GN][PL]
     static constexpr uint32_t AM = A1 + (K ? GN * PL : 0);            // Q4_K mins, 8 bytes + 24 zero [GN][32]
@@ -117,26 +126,33 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t *q, int j, uint32_t 
     }
 }
 
-// sc * (4 nibbles packed one per byte) -> (hi, lo) digit bytes: byte b of the
-// result pair holds (sc*q_b) >> 7 and (sc*q_b) & 127.
+// sc * (4 values of up to 5 bits packed one per byte) -> (hi, lo) digit
+// bytes: byte b of the result pair holds (sc*q_b) >> 7 and (sc*q_b) & 127
+// (sc*q_b <= 63*31 < 2048).
 __device__ __forceinline__ void digits4(uint32_t q, uint32_t sc, uint32_t &hi, uint32_t &lo) {
-    const uint32_t e = (q & 0x000F000Fu) * sc;          // bytes 0, 2 as 16-bit lanes
-    const uint32_t o = ((q >> 8) & 0x000F000Fu) * sc;   // bytes 1, 3
+    const uint32_t e = (q & 0x001F001Fu) * sc;          // bytes 0, 2 as 16-bit lanes
+    const uint32_t o = ((q >> 8) & 0x001F001Fu) * sc;   // bytes 1, 3
     lo = (e & 0x007F007Fu) | ((o & 0x007F007Fu) << 8);
-    hi = ((e >> 7) & 0x00070007u) | (((o >> 7) & 0x00070007u) << 8);
+    hi = ((e >> 7) & 0x000F000Fu) | (((o >> 7) & 0x000F000Fu) << 8);
 }
 
 template <int TYPE>
 struct GPrefetch {
     // Q4_K: the 16-byte header and the 32 quant bytes this thread converts
-    // (row tid/4, quarter tid%4); Q6_K: its 16-byte runs of ql (two) and qh,
+    // (row tid/4, quarter tid%4); Q5_K: the same and the 32 qh bytes; IQ3_S
+    // and IQ2_S: the bytes of the two 32-chunks 2qq, 2qq+1 (4-byte-aligned
+    // words, realigned on conversion); Q6_K: its 16-byte runs of ql (two) and qh,
     // read from 4-byte-aligned addresses (blocks are 2-byte aligned) with
     // their fifth dwords in ex, then the scale bytes and d; IQ3_XXS: its 16
     // grid-index bytes (+1 dword), its 8 scale/sign bytes and d. Q8_0: raw
     // 16-byte chunks of the tile.
-    static constexpr int RAWC = TYPE == kQ4_K || TYPE == kQ6_K ? 3 : TYPE == kIQ3_XXS ? 1 : (GN * 272 / 16 + GT - 1) / GT;
-    static constexpr int EXC = TYPE == kQ6_K ? 7 : TYPE == kIQ3_XXS ? 5 : 1;
-    u4 raw[RAWC];
+    static constexpr int RAWC = TYPE == kQ4_K || TYPE == kQ6_K       ? 3
+                                : TYPE == kQ5_K                       ? 5
+                                : TYPE == kIQ3_XXS || TYPE == kIQ3_S  ? 1
+                                : TYPE == kIQ2_S                      ? 0
+                                                                      : (GN * 272 / 16 + GT - 1) / GT;
+    static constexpr int EXC = TYPE == kQ6_K || TYPE == kIQ3_S ? 7 : TYPE == kIQ3_XXS ? 5 : TYPE == kIQ2_S ? 9 : 1;
+    u4 raw[RAWC > 0 ? RAWC : 1];
     uint32_t ex[EXC];
     uint32_t sh;           // Q6_K / IQ3_XXS: the block's byte offset mod 4
     static constexpr int ACTC = TYPE == kQ8_0 ? GM * 16 / GT : 0;
@@ -168,7 +184,7 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
     g.d = grsrc(a.d8, uint64_t(a.M) * (a.K / (TYPE == kQ8_0 ? 32 : 256)) * 4);
     g.bs = grsrc(a.bsums, TYPE == kQ8_0 ? 0 : uint64_t(a.M) * (a.K / 16) * 2);
     g.vw = (n0 + tid / 4) * a.row_bytes;
-    g.vw2 = g.vw + 16 + 32 * (tid & 3);
+    g.vw2 = g.vw + (TYPE == kQ5_K ? 48 : 16) + 32 * (tid & 3);
     if constexpr (TYPE == kQ6_K) {
         // thread (row tid/4, half n = bit 1, part p = bit 0): ql[64n + 16p ..],
         // ql[64n + 32 + 16p ..], qh[32n + 16p ..] (16 bytes each), scales 8n..8n+7
@@ -184,6 +200,9 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
         g.vo[0] = 2 + 16 * qq;
         g.vo[1] = 66 + 8 * qq;
         g.vo[2] = g.vo[3] = 0;
+    } else {
+        g.vo[0] = g.vo[1] = g.vo[2] = 0;
+        g.vo[3] = tid & 3;  // IQ3_S / IQ2_S: the thread's quarter
     }
     // Activations are block-major: 256-column block b of token m at b * M + m.
     g.vq = (m0 + tid / 16) * 256 + 16 * (tid & 15);
@@ -205,6 +224,42 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
         p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw, b * UB, 0);
         p.raw[1] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2, b * UB, 0);
         p.raw[2] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2 + 16, b * UB, 0);
+    } else if constexpr (TYPE == kQ5_K) {
+        // 176-byte blocks: every piece 16-byte aligned
+        p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw, b * UB, 0);
+        p.raw[1] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw + 16, b * UB, 0);
+        p.raw[2] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw + 32, b * UB, 0);
+        p.raw[3] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2, b * UB, 0);
+        p.raw[4] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2 + 16, b * UB, 0);
+    } else if constexpr (TYPE == kIQ3_S || TYPE == kIQ2_S) {
+        // 2-byte-aligned blocks; each piece from its 4-byte-aligned address
+        // down, the block start's offset mod 4 in sh
+        const uint32_t blk = g.vw + b * UB;
+        p.sh = blk & 3;
+        const uint32_t al = blk & ~3u;
+        auto w32 = [&](uint32_t off) __attribute__((always_inline)) {
+            return __builtin_amdgcn_raw_buffer_load_b32(g.w, (blk + off) & ~3u, 0, 0);
+        };
+        const uint32_t qq = g.vo[3];
+        if constexpr (TYPE == kIQ3_S) {
+            p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, (blk + 2 + 16 * qq) & ~3u, 0, 0);  // qs
+            p.ex[0] = w32(2 + 16 * qq + 16);
+            p.ex[1] = w32(66 + 2 * qq);       // qh bytes 2qq, 2qq+1 (never straddle a word)
+            p.ex[2] = w32(74 + 8 * qq);       // signs
+            p.ex[3] = w32(74 + 8 * qq + 4);
+            p.ex[4] = w32(74 + 8 * qq + 8);
+            p.ex[5] = w32(106 + qq);          // scale byte
+        } else {
+            p.ex[0] = w32(2 + 8 * qq);        // qs (grid low bytes)
+            p.ex[1] = w32(2 + 8 * qq + 4);
+            p.ex[2] = w32(2 + 8 * qq + 8);
+            p.ex[3] = w32(34 + 8 * qq);       // signs
+            p.ex[4] = w32(34 + 8 * qq + 4);
+            p.ex[5] = w32(34 + 8 * qq + 8);
+            p.ex[7] = w32(66 + 2 * qq);       // qh bytes 2qq, 2qq+1
+            p.ex[8] = w32(74 + 2 * qq);       // scale bytes 2qq, 2qq+1
+        }
+        p.ex[6] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al, 0, 0);  // d
     } else if constexpr (TYPE == kQ6_K) {
         const uint32_t blk = g.vw + b * UB;  // block start (2-byte aligned)
         p.sh = blk & 3;
@@ -236,17 +291,22 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
         p.act[i] = __builtin_amdgcn_raw_buffer_load_b128(g.q, g.vq, b * a.M * 256 + i * 16 * 256, 0);
     if constexpr (TYPE == kQ8_0)
         p.side = __builtin_amdgcn_raw_buffer_load_b128(g.d, g.vbs, b * a.M * 32, 0);
-    else if constexpr (TYPE == kQ4_K)
+    else if constexpr (min_type(TYPE))
         p.side = __builtin_amdgcn_raw_buffer_load_b128(g.bs, g.vbs, b * a.M * 32, 0);
     if constexpr (dig_type(TYPE))
         p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * a.M * 4, 0));
 }
 
-// Q4_K weights of this thread (row tid/4: header + qs[32qq .. 32qq+31]) ->
-// the two digit planes, the mins and the row scales.
+// Q4_K / Q5_K weights of this thread (row tid/4: header + qs[32qq .. 32qq+31],
+// Q5_K also bits 2qq, 2qq+1 of the 32 qh bytes) -> the two digit planes, the
+// mins and the row scales. Q5_K (reference dequantizeQ5_KBlock,
+// include/GGMLDequantize.hpp:392-402) shares Q4_K's header and scale
+// packing; its fifth bit of weight l of sub-block 2qq + h is bit 2qq + h of
+// qh[l].
+template <int TYPE>
 __device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u4 &qb, unsigned char *lds,
-                                            uint32_t tid) {
-    using L = GLds<kQ4_K>;
+                                            uint32_t tid, const u4 &qh0 = u4{}, const u4 &qh1 = u4{}) {
+    using L = GLds<TYPE>;
     const uint32_t r = tid / 4, qq = tid & 3;
     // the 8 6-bit scales / mins as bytes (reference get_scale_min_k4,
     // GGMLDequantize.hpp:436-447): sub-blocks 0-3 from the low words, 4-7 from
@@ -258,11 +318,17 @@ __device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u
     const uint32_t scw = (qq < 2 ? scl : sch) >> sh, mnw = (qq < 2 ? mnl : mnh) >> sh;
     const uint32_t sc0 = scw & 0xFF, sc1 = (scw >> 8) & 0xFF, mn0 = mnw & 0xFF, mn1 = (mnw >> 8) & 0xFF;
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const uint32_t qh[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
     uint32_t hl[8], ll[8], hh[8], lh[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        digits4(q[k] & 0x0F0F0F0Fu, sc0, hl[k], ll[k]);
-        digits4((q[k] >> 4) & 0x0F0F0F0Fu, sc1, hh[k], lh[k]);
+        uint32_t vl = q[k] & 0x0F0F0F0Fu, vh = (q[k] >> 4) & 0x0F0F0F0Fu;
+        if constexpr (TYPE == kQ5_K) {
+            vl |= ((qh[k] >> (2 * qq)) & 0x01010101u) << 4;
+            vh |= ((qh[k] >> (2 * qq + 1)) & 0x01010101u) << 4;
+        }
+        digits4(vl, sc0, hl[k], ll[k]);
+        digits4(vh, sc1, hh[k], lh[k]);
     }
     unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
     const uint32_t s0 = 64 * qq, s1 = 64 * qq + 32;  // k offsets of sub-blocks 2qq, 2qq+1
@@ -397,8 +463,98 @@ __device__ __forceinline__ void iq3_convert(const GPrefetch<kIQ3_XXS> &p, unsign
     reinterpret_cast<float *>(lds + L::AS)[r] = 0.25f * h2f(dh);
 }
 
+// IQ3_S weights of this thread (row tid/4, 32-chunks ib = 2qq + c) -> the
+// digit planes and d. Group l (8 weights) of chunk ib: codebook entries
+// qs[8ib + 2l] and qs[8ib + 2l + 1] with bit 8 from bits 2l and 2l+1 of
+// qh[ib], negated by the bits of signs[4ib + l], times 2ls+1 with ls nibble
+// ib&1 of scales[ib/2] (reference include/GGMLDequantize.hpp:1164-1212 and
+// the integer block dot :2102-2145).
+__device__ __forceinline__ void iq3s_convert(const GPrefetch<kIQ3_S> &p, unsigned char *lds, const uint32_t *grid,
+                                             uint32_t tid) {
+    using L = GLds<kIQ3_S>;
+    const uint32_t r = tid / 4, qq = tid & 3;
+    const uint32_t s_qs = (p.sh + 2) & 3, s_sg = (p.sh + 2) & 3;  // qs at 2 + 16qq, signs at 74 + 8qq
+    const uint32_t v[5] = {p.raw[0].x, p.raw[0].y, p.raw[0].z, p.raw[0].w, p.ex[0]};
+    uint32_t qs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qs[j] = realign(v[j + 1], v[j], s_qs);
+    const uint32_t sg[2] = {realign(p.ex[3], p.ex[2], s_sg), realign(p.ex[4], p.ex[3], s_sg)};
+    const uint32_t qh2 = p.ex[1] >> (8 * ((p.sh + 66 + 2 * qq) & 3));      // qh[2qq] | qh[2qq+1] << 8
+    const uint32_t scb = (p.ex[5] >> (8 * ((p.sh + 106 + qq) & 3))) & 0xFFu;  // scales[qq]
+    const uint32_t dh = p.sh ? (p.ex[6] >> 16) : (p.ex[6] & 0xFFFFu);
+    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int k = 2 * int((scb >> (4 * c)) & 15u) + 1;
+        const uint32_t qh = (qh2 >> (8 * c)) & 0xFFu;
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t qw = qs[2 * c + (l >> 1)], sh8 = 16 * (l & 1);
+            const uint32_t i1 = ((qw >> sh8) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
+            const uint32_t i2 = ((qw >> (sh8 + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
+            const uint32_t s8 = (sg[c] >> (8 * l)) & 0xFFu;
+            const uint32_t m1 = spread_sign4(s8 & 15u), m2 = spread_sign4(s8 >> 4);
+            digits_i8((grid[i1] ^ m1) + (m1 & 0x01010101u), k, hi[2 * l], lo[2 * l]);
+            digits_i8((grid[i2] ^ m2) + (m2 & 0x01010101u), k, hi[2 * l + 1], lo[2 * l + 1]);
+        }
+        const uint32_t k0 = 64 * qq + 32 * c;
+        *reinterpret_cast<u4 *>(a0 + k0) = u4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u4 *>(a0 + k0 + 16) = u4{hi[4], hi[5], hi[6], hi[7]};
+        *reinterpret_cast<u4 *>(a1 + k0) = u4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u4 *>(a1 + k0 + 16) = u4{lo[4], lo[5], lo[6], lo[7]};
+    }
+    reinterpret_cast<float *>(lds + L::AS)[r] = h2f(dh);
+}
+
+// IQ2_S weights of this thread (row tid/4, 32-chunks ib = 2qq + c) -> the
+// digit planes and d/8 (the row scale 0.125 of the reference's fused path,
+// include/GGMLDequantize.hpp:2148-2159, is a power of two: exact on d). Group
+// l (8 weights) of chunk ib: the 8 magnitudes of codebook entry qs[4ib + l]
+// with bits 8-9 from bits 2l, 2l+1 of qh[ib], negated by the bits of
+// signs[4ib + l], times 2ls+1 with ls nibble l/2 of scales[ib]
+// (GGMLDequantize.hpp:1215-1242, :2028-2057).
+__device__ __forceinline__ void iq2s_convert(const GPrefetch<kIQ2_S> &p, unsigned char *lds, const uint32_t *grid,
+                                             uint32_t tid) {
+    using L = GLds<kIQ2_S>;
+    const uint32_t r = tid / 4, qq = tid & 3;
+    const uint32_t s8b = (p.sh + 2) & 3;  // qs at 2 + 8qq and signs at 34 + 8qq: the same offset mod 4
+    const uint32_t qs[2] = {realign(p.ex[1], p.ex[0], s8b), realign(p.ex[2], p.ex[1], s8b)};
+    const uint32_t sg[2] = {realign(p.ex[4], p.ex[3], s8b), realign(p.ex[5], p.ex[4], s8b)};
+    const uint32_t qh2 = p.ex[7] >> (8 * ((p.sh + 66 + 2 * qq) & 3));
+    const uint32_t sc2 = p.ex[8] >> (8 * ((p.sh + 74 + 2 * qq) & 3));
+    const uint32_t dh = p.sh ? (p.ex[6] >> 16) : (p.ex[6] & 0xFFFFu);
+    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const uint32_t qh = (qh2 >> (8 * c)) & 0xFFu, scb = (sc2 >> (8 * c)) & 0xFFu;
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const int k = 2 * int((scb >> (4 * (l >> 1))) & 15u) + 1;
+            const uint32_t idx = ((qs[c] >> (8 * l)) & 0xFFu) | (((qh >> (2 * l)) & 3u) << 8);
+            const uint32_t s8 = (sg[c] >> (8 * l)) & 0xFFu;
+            const uint32_t m1 = spread_sign4(s8 & 15u), m2 = spread_sign4(s8 >> 4);
+            digits_i8((grid[2 * idx] ^ m1) + (m1 & 0x01010101u), k, hi[2 * l], lo[2 * l]);
+            digits_i8((grid[2 * idx + 1] ^ m2) + (m2 & 0x01010101u), k, hi[2 * l + 1], lo[2 * l + 1]);
+        }
+        const uint32_t k0 = 64 * qq + 32 * c;
+        *reinterpret_cast<u4 *>(a0 + k0) = u4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u4 *>(a0 + k0 + 16) = u4{hi[4], hi[5], hi[6], hi[7]};
+        *reinterpret_cast<u4 *>(a1 + k0) = u4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u4 *>(a1 + k0 + 16) = u4{lo[4], lo[5], lo[6], lo[7]};
+    }
+    reinterpret_cast<float *>(lds + L::AS)[r] = 0.125f * h2f(dh);
+}
+
 __constant__ uint32_t c_iq3_grid[256] = {
 #include "iq3xxs_grid.inc"
+};
+__constant__ uint32_t c_iq3s_grid[512] = {
+#include "iq3s_grid.inc"
+};
+__constant__ uint64_t c_iq2s_grid[1024] = {
+#include "iq2s_grid.inc"
 };
 
 // Staged registers -> LDS: the activation plane and its side data; Q4_K
@@ -409,7 +565,13 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
                                            const uint32_t *grid = nullptr) {
     using L = GLds<TYPE>;
     if constexpr (TYPE == kQ4_K) {
-        q4k_convert(p.raw[0], p.raw[1], p.raw[2], lds, tid);
+        q4k_convert<kQ4_K>(p.raw[0], p.raw[1], p.raw[2], lds, tid);
+    } else if constexpr (TYPE == kQ5_K) {
+        q4k_convert<kQ5_K>(p.raw[0], p.raw[3], p.raw[4], lds, tid, p.raw[1], p.raw[2]);
+    } else if constexpr (TYPE == kIQ3_S) {
+        iq3s_convert(p, lds, grid, tid);
+    } else if constexpr (TYPE == kIQ2_S) {
+        iq2s_convert(p, lds, grid, tid);
     } else if constexpr (TYPE == kQ6_K) {
         q6k_convert(p, lds, tid);
     } else if constexpr (TYPE == kIQ3_XXS) {
@@ -426,7 +588,7 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
         const uint32_t c = tid + i * GT;
         *reinterpret_cast<u4 *>(lds + L::B + (c / 16) * PL + 16 * (c & 15)) = p.act[i];
     }
-    if constexpr (TYPE == kQ8_0 || TYPE == kQ4_K) {
+    if constexpr (TYPE == kQ8_0 || min_type(TYPE)) {
         const uint32_t m = (tid & 255) / 2, h = tid & 1;
         if constexpr (TYPE == kQ8_0) {
             *reinterpret_cast<u4 *>(lds + L::BD + m * 32 + 16 * h) = p.side;
@@ -754,10 +916,13 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
     const uint32_t li = lane & 31, lg = lane >> 5;
     const uint32_t ptid = tid - 64 * CW;  // producer thread index 0..255
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
-    // IQ3_XXS codebook in LDS, past the two buffers (read by the producers' conversion)
+    // IQ3_XXS / IQ3_S / IQ2_S codebook in LDS, past the two buffers (read by the producers' conversion)
     uint32_t *grid = reinterpret_cast<uint32_t *>(lds + 2 * L::bytes);
-    if constexpr (TYPE == kIQ3_XXS) {
-        for (uint32_t i = tid; i < 256; i += blockDim.x) grid[i] = c_iq3_grid[i];
+    if constexpr (grid_bytes(TYPE) != 0) {
+        const uint32_t *src = TYPE == kIQ3_XXS ? c_iq3_grid
+                              : TYPE == kIQ3_S ? c_iq3s_grid
+                                               : reinterpret_cast<const uint32_t *>(c_iq2s_grid);
+        for (uint32_t i = tid; i < grid_bytes(TYPE) / 4; i += blockDim.x) grid[i] = src[i];
         __syncthreads();
     }
 
@@ -899,7 +1064,7 @@ hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_dig<TYPE, CW, GRP>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (attr != hipSuccess) return attr;
-        const uint32_t lds = 2 * GLds<TYPE>::bytes + (TYPE == kIQ3_XXS ? 1024 : 0);
+        const uint32_t lds = 2 * GLds<TYPE>::bytes + grid_bytes(TYPE);
         k_gemm_dig<TYPE, CW, GRP><<<grid, GT + 64 * CW, lds, st>>>(a);
     } else {
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<TYPE>),
@@ -1009,9 +1174,13 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
         a.out = out;
         a.ws = static_cast<float *>(workspace);
         a.skg = G;
-        hipError_t e = type == kQ4_K   ? launch_gemm_t<kQ4_K>(a, dim3{G, 1u, 1u}, st)
-                       : type == kQ6_K ? launch_gemm_t<kQ6_K>(a, dim3{G, 1u, 1u}, st)
-                                       : launch_gemm_t<kIQ3_XXS>(a, dim3{G, 1u, 1u}, st);
+        const dim3 g{G, 1u, 1u};
+        hipError_t e = type == kQ4_K     ? launch_gemm_t<kQ4_K>(a, g, st)
+                       : type == kQ5_K   ? launch_gemm_t<kQ5_K>(a, g, st)
+                       : type == kQ6_K   ? launch_gemm_t<kQ6_K>(a, g, st)
+                       : type == kIQ3_S  ? launch_gemm_t<kIQ3_S>(a, g, st)
+                       : type == kIQ2_S  ? launch_gemm_t<kIQ2_S>(a, g, st)
+                                         : launch_gemm_t<kIQ3_XXS>(a, g, st);
         if (e != hipSuccess) return e;
         // Any tile split over workgroups? (a range boundary inside a tile)
         bool split = false;
