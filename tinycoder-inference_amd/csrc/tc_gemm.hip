@@ -1011,12 +1011,24 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
 }
 
 // Tiles split over several stream-K workgroups: out = the partial segments
-// summed in workgroup order (one workgroup per tile; whole tiles exit).
+// summed in workgroup order, kFixSlices workgroups per tile (each a quarter of
+// its entries). Plain mode: workgroup group j takes the tile that holds
+// range boundary j+1, when the boundary splits it and is the first to do so;
+// grouped mode (tile count on the device): one group per possible tile,
+// whole tiles exit.
+constexpr uint32_t kFixSlices = 4;
 template <bool GRP>
 __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
     const uint32_t ntm = sk_ntm<GRP>(a);
     const uint32_t ntiles = GRP ? ntm * a.ntn : a.ntiles;
-    const uint32_t tile = blockIdx.x, units = ntiles * a.nblk, G = a.skg;
+    const uint32_t units = ntiles * a.nblk, G = a.skg;
+    const uint32_t slice = blockIdx.x % kFixSlices;
+    uint32_t tile = blockIdx.x / kFixSlices;
+    if constexpr (!GRP) {
+        const uint32_t wb = tile + 1, u = sk_begin(units, G, wb);
+        tile = u / a.nblk;
+        if (u % a.nblk == 0 || sk_begin(units, G, wb - 1) > tile * a.nblk) return;
+    }
     if (tile >= ntiles) return;  // grouped mode: the grid covers the largest possible tile count
     const uint32_t t0 = tile * a.nblk, t1 = t0 + a.nblk;
     // first workgroup whose range holds unit t0
@@ -1026,7 +1038,8 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
     if (sk_begin(units, G, w) <= t0 && sk_begin(units, G, w + 1) >= t1) return;  // one workgroup: stored directly
     const TileGeom tg = sk_tile<GRP>(a, ntm, tile);
     const uint32_t m0 = tg.m0, n0 = tg.n0;
-    for (uint32_t i = threadIdx.x; i < GM * GN / 4; i += 256) {
+    constexpr uint32_t per = GM * GN / 4 / kFixSlices;  // float4 entries per slice
+    for (uint32_t i = slice * per + threadIdx.x; i < (slice + 1) * per; i += 256) {
         const uint32_t ml = (4 * i) / GN, nl = (4 * i) % GN;
         float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
         for (uint32_t v = w; v < G && sk_begin(units, G, v) < t1; ++v) {
@@ -1142,7 +1155,7 @@ hipError_t launch_gemm_grouped(const void *W, uint64_t wstride, const ActView &a
     if (e != hipSuccess) return e;
     // The split tiles are known on the device only: one fixup workgroup per
     // possible tile (those past the count, or stored whole, exit at once).
-    k_gemm_fixup<true><<<dim3{ntm_max * ntn, 1u, 1u}, 256, 0, st>>>(a);
+    k_gemm_fixup<true><<<dim3{ntm_max * ntn * kFixSlices, 1u, 1u}, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -1186,7 +1199,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
         bool split = false;
         for (uint32_t w = 1; w < G && !split; ++w) split = sk_begin(a.ntiles * a.nblk, G, w) % a.nblk != 0;
         if (!split) return hipSuccess;
-        k_gemm_fixup<false><<<dim3{a.ntiles, 1u, 1u}, 256, 0, st>>>(a);
+        k_gemm_fixup<false><<<dim3{(G - 1) * kFixSlices, 1u, 1u}, 256, 0, st>>>(a);
         return hipGetLastError();
     }
     a.out = nsplit > 1 ? static_cast<float *>(workspace) : out;
