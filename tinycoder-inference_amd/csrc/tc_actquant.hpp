@@ -4,82 +4,79 @@
 //
 // Both rules are bit-identical to the reference CPU: the first element with
 // the largest |x| (lowest index on ties) gives max, iscale = -127/max (IEEE
-// division), q = min(127, rne(iscale*x)), d = 1/iscale (IEEE). Only products
-// feed the rounding, so FP contraction cannot change any result.
+// division), q = min(127, rne(iscale*x)), d = 1/iscale (IEEE). The one sum
+// (the rounding trick in q8_bits) is kept apart from its product.
 #pragma once
 
 #include "tc_common.hpp"
 
 namespace tc {
 
-struct AbsMax {
-    float amax, maxv;
-    int idx;
-};
-
-__device__ __forceinline__ AbsMax absmax_combine(AbsMax a, AbsMax b) {
-    const bool take = (b.amax > a.amax) || (b.amax == a.amax && b.idx < a.idx);
-    return take ? b : a;
-}
-
-template <int WIDTH>
-__device__ __forceinline__ AbsMax absmax_reduce(AbsMax v) {
+// The block's signed max (its first element of largest |x|) when the block
+// is spread over WIDTH lanes, lane values e[0..N) at block indices base ..
+// base+N-1: the lane's largest |x| and the key 2i + sign of its first element
+// reaching it; across the lanes the largest |x|, then the smallest key among
+// the lanes holding it (lowest index). +-0 for an all-zero block.
+template <int WIDTH, int N>
+__device__ __forceinline__ float first_absmax(const float (&e)[N], int base) {
+    float am = 0.0f;
 #pragma unroll
-    for (int m = 1; m < WIDTH; m <<= 1) {
-        AbsMax o;
-        o.amax = __shfl_xor(v.amax, m);
-        o.maxv = __shfl_xor(v.maxv, m);
-        o.idx = __shfl_xor(v.idx, m);
-        v = absmax_combine(v, o);
-    }
-    return v;
-}
-
-__device__ __forceinline__ AbsMax absmax4(float4 v, int base) {
-    AbsMax r{0.0f, 0.0f, 1 << 20};
-    const float e[4] = {v.x, v.y, v.z, v.w};
+    for (int i = 0; i < N; ++i) am = fmaxf(am, fabsf(e[i]));
+    uint32_t key = 0xFFFFFFFFu;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float a = fabsf(e[k]);
-        if (a > r.amax) {
-            r.amax = a;
-            r.maxv = e[k];
-            r.idx = base + k;
-        }
-    }
-    return r;
-}
-
-__device__ __forceinline__ uint32_t quant4(float4 v, float iscale) {
-    const float e[4] = {v.x, v.y, v.z, v.w};
-    uint32_t packed = 0;
+    for (int i = N - 1; i >= 0; --i)
+        if (fabsf(e[i]) == am) key = uint32_t(2 * (base + i)) | (__builtin_bit_cast(uint32_t, e[i]) >> 31);
+    float gm = am;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        int q = int(rintf(iscale * e[k]));
-        q = q < 127 ? q : 127;
-        packed |= uint32_t(uint8_t(int8_t(q))) << (8 * k);
-    }
-    return packed;
+    for (int m = 1; m < WIDTH; m <<= 1) gm = fmaxf(gm, __shfl_xor(gm, m));
+    uint32_t kk = am == gm ? key : 0xFFFFFFFFu;
+#pragma unroll
+    for (int m = 1; m < WIDTH; m <<= 1) kk = min(kk, uint32_t(__shfl_xor(int(kk), m)));
+    return (kk & 1u) ? -gm : gm;
 }
 
-__device__ __forceinline__ int bytesum4(uint32_t p) {
-    return int(int8_t(p)) + int(int8_t(p >> 8)) + int(int8_t(p >> 16)) + int(int8_t(p >> 24));
+// rne(iscale * x) (the product rounded once, then to the nearest integer,
+// ties to even) as the low byte of the float bits of the product + 1.5*2^23:
+// |product| <= 127.00002, so the sum lies in [2^23, 2^24), where the float
+// spacing is 1, and its bits are 0x4B400000 + rne(product). No clamp is
+// needed: |iscale| <= 127/|max| (1 + 2^-24), so the product never rounds
+// above 127 (the reference's min(127, .) never applies).
+constexpr uint32_t kQ8Magic = 0x4B400000u;
+__device__ __forceinline__ uint32_t q8_bits(float iscale, float x) {
+#pragma clang fp contract(off)
+    const float p = iscale * x;
+    return __builtin_bit_cast(uint32_t, p + 12582912.0f);
+}
+
+// Low bytes of four q8_bits values packed in order.
+__device__ __forceinline__ uint32_t q8_pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_amdgcn_perm(b, a, 0x0c0c0400u) | __builtin_amdgcn_perm(d, c, 0x04000c0cu);
+}
+
+// Four values of one block quantized with iscale: the packed bytes, and
+// their sum in *sum.
+__device__ __forceinline__ uint32_t quant4_sum(float4 v, float iscale, int *sum) {
+    const uint32_t a = q8_bits(iscale, v.x), b = q8_bits(iscale, v.y), c = q8_bits(iscale, v.z), d = q8_bits(iscale, v.w);
+    *sum = int(a + b + c + d - 4u * kQ8Magic);
+    return q8_pack4(a, b, c, d);
 }
 
 // One 256-element Q8_K block by one full wave, lane values already loaded
 // (lane l holds elements 4l..4l+3). Writes qs[0..255], *d and bsums[0..15].
 __device__ __forceinline__ void quant_q8k_block_wave_v(float4 v, int8_t *qs, float *d, int16_t *bsums) {
     const uint32_t lane = threadIdx.x & 63;
-    const AbsMax m = absmax_reduce<64>(absmax4(v, 4 * lane));
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    const float maxv = first_absmax<64>(e, 4 * int(lane));
     uint32_t packed = 0;
+    int sum = 0;
     float dv = 0.0f;
-    if (m.amax != 0.0f) {
-        const float iscale = __fdiv_rn(-127.0f, m.maxv);
-        packed = quant4(v, iscale);
+    if (maxv != 0.0f) {
+        const float iscale = __fdiv_rn(-127.0f, maxv);
+        packed = quant4_sum(v, iscale, &sum);
         dv = __fdiv_rn(1.0f, iscale);
     }
     reinterpret_cast<uint32_t *>(qs)[lane] = packed;
-    const int s16 = quad_sum(bytesum4(packed));
+    const int s16 = quad_sum(sum);
     if ((lane & 3) == 0) bsums[lane >> 2] = int16_t(s16);
     if (lane == 0) *d = dv;
 }
@@ -93,12 +90,14 @@ __device__ __forceinline__ void quant_q8k_block_wave(const float *x, int8_t *qs,
 __device__ __forceinline__ void quant_q8_0_blocks_wave_v(float4 v, int8_t *qs, float *d) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t sub = lane & 7;
-    const AbsMax m = absmax_reduce<8>(absmax4(v, 4 * sub));
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    const float maxv = first_absmax<8>(e, 4 * int(sub));
     uint32_t packed = 0;
     float dv = 0.0f;
-    if (m.amax != 0.0f) {
-        const float iscale = __fdiv_rn(-127.0f, m.maxv);
-        packed = quant4(v, iscale);
+    if (maxv != 0.0f) {
+        const float iscale = __fdiv_rn(-127.0f, maxv);
+        int sum;
+        packed = quant4_sum(v, iscale, &sum);
         dv = __fdiv_rn(1.0f, iscale);
     }
     reinterpret_cast<uint32_t *>(qs)[lane] = packed;

@@ -249,31 +249,23 @@ __device__ __forceinline__ XPre tstage_preload(const TJobDev &jb, const XRsrc &r
 }
 
 template <int TYPE>
-__device__ __forceinline__ void tquant_chunk(const float *e, uint32_t g, uint32_t k, bool ok, unsigned char *xr) {
+__device__ __forceinline__ void tquant_chunk(const float (&e)[16], uint32_t g, uint32_t k, bool ok, unsigned char *xr) {
     constexpr int WIDTH = TYPE == kQ8_0 ? 2 : 16;  // lanes per activation block
-    AbsMax m{0.0f, 0.0f, 1 << 20};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float a = fabsf(e[i]);
-        if (a > m.amax) {
-            m.amax = a;
-            m.maxv = e[i];
-            m.idx = int(16 * (k % WIDTH)) + i;
-        }
-    }
-    m = absmax_reduce<WIDTH>(m);
+    const float maxv = first_absmax<WIDTH>(e, int(16 * (k % WIDTH)));
     uint32_t w[4] = {0, 0, 0, 0};
     int bsum = 0;
     float dv = 0.0f;
-    if (m.amax != 0.0f) {
-        const float iscale = __fdiv_rn(-127.0f, m.maxv);
+    if (maxv != 0.0f) {
+        const float iscale = __fdiv_rn(-127.0f, maxv);
+        uint32_t qb[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            int qv = int(rintf(iscale * e[i]));
-            qv = qv < 127 ? qv : 127;
-            bsum += qv;
-            w[i >> 2] |= uint32_t(uint8_t(int8_t(qv))) << (8 * (i & 3));
-        }
+        for (int i = 0; i < 16; ++i) qb[i] = q8_bits(iscale, e[i]);
+        uint32_t tot = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tot += qb[i];
+        bsum = int(tot - 16u * kQ8Magic);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = q8_pack4(qb[4 * j], qb[4 * j + 1], qb[4 * j + 2], qb[4 * j + 3]);
         dv = __fdiv_rn(1.0f, iscale);
     }
     if (ok) {
