@@ -31,7 +31,8 @@ inline bool ok(int rc) {
 inline bool int8GemmAvailable() { return tc_available() != 0; }
 
 /// out[seqLen][rows] = x[seqLen][cols] @ W[rows][cols]^T on the int8 matrix
-/// cores (Q4_K, Q8_0) or the exact batched mat-vec (Q2_K, Q3_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0)
+/// cores (Q4_K, Q5_K, Q6_K, Q8_0, IQ3_XXS, IQ3_S, IQ2_S) or the exact batched
+/// mat-vec (Q2_K, Q3_K, IQ2_XS, IQ4_XS, IQ4_NL, Q5_0)
 /// (reference int8Gemm, Int8Gemm.hpp:57-59).
 inline bool int8Gemm(int type, const void *w, const float *x, float *out, uint32_t seqLen, uint32_t rows,
                      uint32_t cols, uint32_t blocksPerRow, void *stream) {

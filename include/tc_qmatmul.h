@@ -89,15 +89,17 @@ int tc_gemv_reserve(uint32_t cols, uint32_t seq_len);
 int tc_gemv_dual(int type, const void *wg, const void *wu, const float *x, float *gout, float *uout,
                  uint32_t rows, uint32_t cols, void *stream);
 
-/* Prefill GEMM, seq_len >= 1: out[seq_len][rows] = x[seq_len][cols] @ W^T with
- * the int8 MFMA kernel. Replaces tinycoder::gpu::int8Gemm
- * (include/Int8Gemm.hpp:57-59, GemmDispatch.cu:595). blocks_per_row must
- * equal cols / block_elems. */
+/* Prefill GEMM, seq_len >= 1: out[seq_len][rows] = x[seq_len][cols] @ W^T.
+ * Replaces tinycoder::gpu::int8Gemm (include/Int8Gemm.hpp:57-59,
+ * GemmDispatch.cu:595). Int8 MFMA for the types the reference's GEMM takes
+ * (Q4_K, Q5_K, Q6_K, Q8_0, IQ3_XXS, IQ3_S, IQ2_S; GemmDispatch.cu:600-602);
+ * the other types run the decode kernel over groups of 8 tokens.
+ * blocks_per_row must equal cols / block_elems. */
 int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_len, uint32_t rows,
             uint32_t cols, uint32_t blocks_per_row, void *stream);
 
 /* Prefill GEMM that allocates nothing: the same kernels and results as
- * tc_gemm for Q4_K and Q8_0 (cols % 256 == 0), with its scratch (quantized
+ * tc_gemm for its MFMA types (cols % 256 == 0), with its scratch (quantized
  * activations, split / stream-K partials) in a fixed per-device array of
  * tc_gemm_noalloc_scratch_bytes() (32 MiB) instead of the library's buffers.
  * No counterpart in the reference: for callers that cannot allocate device

@@ -112,10 +112,12 @@ tc::ActView act_view(void *buf, const tc::ActLayout &L, size_t tok, int type, ui
     return v;
 }
 
-// Activations wider than 16 Q8_K blocks (per launch) are quantized once by a
-// small kernel into the device scratch instead of in every workgroup of the
-// mat-vec (whose prologue would repeat the work hundreds of times). The
-// tiled kernels (Q4_K, Q8_0) take that path; the others quantize in-kernel.
+// Activations wider than the mat-vec prologue preloads (S*cols beyond 3
+// 16-value chunks per thread: 24576 values for the 512-thread shape, 12288
+// for the 256-thread one) are quantized once by a small kernel into the
+// device scratch instead of in every workgroup of the mat-vec (whose
+// prologue would repeat the work hundreds of times). The fp32-activation
+// types (IQ2_XS, IQ4_NL, Q5_0) always stage x in-kernel.
 bool prequantize_wide(int type, uint32_t S, uint32_t cols, uint64_t weight_bytes) {
     return size_t(S) * cols > tc::gemv_fused_quant_limit(type, weight_bytes);
 }
@@ -415,7 +417,8 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
         cols = p.cols;
     }
     if (!mfma_gemm_type(type)) {
-        // Q2_K / Q3_K / Q5_K / IQ3_S / IQ2_S / IQ2_XS / IQ4_XS / IQ4_NL / Q5_0: the exact batched path (the reference's launchQGemm,
+        // Q2_K / Q3_K / IQ4_XS and the fp32-activation IQ2_XS / IQ4_NL / Q5_0:
+        // the exact batched path (the reference's launchQGemm,
         // GpuGemvIQInt8.hpp:771-847) -- the decode kernel over token groups.
         for (uint32_t s0 = 0; s0 < seq_len; s0 += 8) {
             const uint32_t S = std::min(8u, seq_len - s0);

@@ -1,22 +1,23 @@
 // tc_gemm.hip -- prefill GEMM: out[m][n] = W[n] . x[m] for M tokens against raw
-// GGUF Q4_K / Q8_0 weight rows, on the int8 matrix cores (v_mfma_i32_32x32x32_i8).
+// GGUF weight rows (Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, Q8_0), on the
+// int8 matrix cores (v_mfma_i32_32x32x32_i8).
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698) with
 // the CPU reference's numerics: the activations are quantized by the same
-// bit-exact quantizers as the mat-vec path (Q8_K for Q4_K weights, 32-wide
-// Q8_0-style for Q8_0 weights), every integer dot product of a weight block
+// bit-exact quantizers as the mat-vec path (Q8_K for the K-quant and IQ
+// weights, 32-wide Q8_0-style for Q8_0 weights), every integer dot product of a weight block
 // with an activation block is exact, and only the final per-block scale
 // combination runs in fp32.
 //
 // Decomposition. One workgroup owns a tile of 64 weight rows x 128 tokens and
-// walks K one 256-element superblock at a time. Q4_K spreads the (tile,
-// superblock) units evenly over one workgroup per CU (stream-K, partial tiles
-// summed by k_gemm_fixup); Q8_0 runs one workgroup per tile (split-K when the
+// walks K one 256-element superblock at a time. The digit-plane types spread
+// the (tile, superblock) units evenly over one workgroup per CU (stream-K,
+// partial tiles summed by k_gemm_fixup); Q8_0 runs one workgroup per tile (split-K when the
 // tiles do not fill the chip). The activations arrive block-major
 // (256-column block b of token m at b*M + m), so one superblock of a token
 // tile is one contiguous 32 KB run. Per superblock the raw weight rows, the
-// quantized activations and their scales are staged through LDS. Q4_K runs 12
-// waves: 4 producers (weight loads two superblocks ahead, conversion into one
+// quantized activations and their scales are staged through LDS. The
+// digit-plane kernel runs 12 waves: 4 producers (weight loads two superblocks ahead, conversion into one
 // half of a double-buffered LDS) and 8 consumers (the activation plane loaded
 // straight into LDS, MFMAs on the other half); Q8_0 runs 4 waves that do both,
 // two workgroups per CU.
@@ -28,7 +29,10 @@
 //    128*acc(hi) + acc(lo). The min term sum_s m_s * (x-sum of sub-block s) is
 //    one more pair of MFMAs over 8 useful k-slots, with the activation pair
 //    sums split into int8 digits the same way. Per superblock and output:
-//    acc += d8 * (d*main - dmin*min).
+//    acc += d8 * (d*main - dmin*min). Q5_K is the same with 5-bit q (sc*q
+//    <= 1953); Q6_K, IQ3_XXS, IQ3_S and IQ2_S write their signed integer
+//    weights (sc*(q-32), (2ls+1)*(+-grid value)) as signed digits and have no
+//    min term.
 //  * Q8_0: the int8 weights are the A operand directly; each 32-block gives
 //    one MFMA and acc += (dw*d8) * isum.
 //

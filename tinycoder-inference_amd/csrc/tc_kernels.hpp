@@ -72,7 +72,7 @@ uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs);
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes);
 uint32_t gemv_max_tokens(int type, uint32_t cols);
 
-// Prefill GEMM (int8 MFMA) for Q4_K / Q8_0 weights: out[M][N] = W x^T with
+// Prefill GEMM (int8 MFMA) for the digit-plane types and Q8_0: out[M][N] = W x^T with
 // activations already quantized (launch_quant_act over M tokens). Splits K
 // across workgroups when the output tiles do not fill the chip; the partial
 // sums then need gemm_workspace_bytes() of device scratch.
