@@ -220,8 +220,10 @@ int tc_host_matmul(int type, const uint8_t *W, const float *X, uint32_t seq_len,
                    float *out, const float *residual);
 /* Keep a device copy of the host range [host, host + bytes) (weights that
  * later tc_host_matmul calls read); the copy is taken now, so later writes to
- * the host range are not seen until it is registered again. No counterpart
- * in the reference (its CPU kernels read host memory in place). */
+ * the host range are not seen until it is registered again. A copy belongs
+ * to the device current at registration and serves calls made on that
+ * device. No counterpart in the reference (its CPU kernels read host memory
+ * in place). */
 int tc_host_weights_register(const void *host, size_t bytes);
 int tc_host_weights_unregister(const void *host);
 

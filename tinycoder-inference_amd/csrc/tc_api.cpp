@@ -816,16 +816,25 @@ struct HostRange {
     const uint8_t *host;
     size_t bytes;
     void *dev;
+    int device;  // the HIP device holding the copy
 };
 
 std::mutex g_host_mu;
 std::vector<HostRange> g_host_ranges;  // registered host weight ranges and their device copies
 
-// Device address of [p, p + bytes) when it lies inside a registered range.
+int current_device() {
+    int id = -1;
+    return hipGetDevice(&id) == hipSuccess ? id : -1;
+}
+
+// Device address of [p, p + bytes) when it lies inside a range registered on
+// the current device.
 const void *registered_copy(const void *p, size_t bytes) {
     const uint8_t *q = static_cast<const uint8_t *>(p);
+    const int id = current_device();
     for (const HostRange &r : g_host_ranges)
-        if (q >= r.host && q + bytes <= r.host + r.bytes) return static_cast<const uint8_t *>(r.dev) + (q - r.host);
+        if (r.device == id && q >= r.host && q + bytes <= r.host + r.bytes)
+            return static_cast<const uint8_t *>(r.dev) + (q - r.host);
     return nullptr;
 }
 
@@ -841,22 +850,24 @@ int tc_host_weights_register(const void *host, size_t bytes) {
     if (!device()) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
     if (!host || bytes == 0) return fail(TC_E_ARG, "null or empty range");
     std::lock_guard<std::mutex> lk(g_host_mu);
+    const int id = current_device();
     for (const HostRange &r : g_host_ranges)
-        if (r.host == host) return fail(TC_E_ARG, "range already registered");
+        if (r.host == host && r.device == id) return fail(TC_E_ARG, "range already registered");
     void *d = nullptr;
     if (hipMalloc(&d, bytes) != hipSuccess) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", bytes);
     if (hipMemcpy(d, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
         (void)hipFree(d);
         return fail(TC_E_LAUNCH, "copy to device failed");
     }
-    g_host_ranges.push_back({static_cast<const uint8_t *>(host), bytes, d});
+    g_host_ranges.push_back({static_cast<const uint8_t *>(host), bytes, d, id});
     return TC_OK;
 }
 
 int tc_host_weights_unregister(const void *host) {
     std::lock_guard<std::mutex> lk(g_host_mu);
+    const int id = current_device();
     for (size_t i = 0; i < g_host_ranges.size(); ++i)
-        if (g_host_ranges[i].host == host) {
+        if (g_host_ranges[i].host == host && g_host_ranges[i].device == id) {
             (void)hipDeviceSynchronize();
             (void)hipFree(g_host_ranges[i].dev);
             g_host_ranges.erase(g_host_ranges.begin() + long(i));
