@@ -73,15 +73,17 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
         if (fit == 0) return hipErrorInvalidValue;
         rpw = std::min(rpw, fit);
-        // Q2_K / Q3_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S rows are not 16-byte
-        // multiples: 8-row groups keep every workgroup's first row 16-byte
-        // aligned (8*84, 8*110, 8*210, 8*98 and 8*82 bytes per 256 columns
-        // are multiples of 16; IQ2_XS: 8*74, IQ4_XS: 8*136).
-        if ((type == kQ2_K || type == kQ3_K || type == kQ6_K || type == kIQ3_XXS || type == kIQ3_S || type == kIQ2_S ||
-             type == kIQ2_XS || type == kIQ4_XS) &&
-            rpw < g.rows) {
-            rpw = (rpw + 7) / 8 * 8;
-            if (rpw > fit) rpw = fit / 8 * 8;
+        // Rows of Q2_K / Q3_K / Q6_K / IQ3_XXS / IQ3_S / IQ2_S / IQ2_XS /
+        // IQ4_XS are not always 16-byte multiples: every workgroup's first row
+        // stays 16-byte aligned with row groups of the fewest rows whose bytes
+        // are a multiple of 16 (at most 8: 8*84, 8*110, 8*210, 8*98, 8*82,
+        // 8*74 and 8*136 bytes per 256 columns are).
+        if (rpw < g.rows) {
+            const uint64_t row_bytes = uint64_t(d.nu) * unit_bytes(type);
+            uint32_t grp = 1;
+            while (grp < 8 && (grp * row_bytes) % 16 != 0) grp *= 2;
+            rpw = (rpw + grp - 1) / grp * grp;
+            if (rpw > fit) rpw = fit / grp * grp;
             if (rpw == 0) return hipErrorInvalidValue;
         }
         d.rows_per_wg = rpw;
