@@ -1043,24 +1043,45 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
     const TileGeom tg = sk_tile<GRP>(a, ntm, tile);
     const uint32_t m0 = tg.m0, n0 = tg.n0;
     constexpr uint32_t per = GM * GN / 4 / kFixSlices;  // float4 entries per slice
-    for (uint32_t i = slice * per + threadIdx.x; i < (slice + 1) * per; i += 256) {
-        const uint32_t ml = (4 * i) / GN, nl = (4 * i) % GN;
-        float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (uint32_t v = w; v < G && sk_begin(units, G, v) < t1; ++v) {
-            if (sk_begin(units, G, v + 1) <= t0 || sk_begin(units, G, v + 1) == sk_begin(units, G, v)) continue;
-            const uint32_t slot = sk_begin(units, G, v) >= t0 ? 0u : 1u;
-            const float4 p = *reinterpret_cast<const float4 *>(a.ws + (size_t(v) * 2 + slot) * (GM * GN) + ml * GN + nl);
-            s.x += p.x;
-            s.y += p.y;
-            s.z += p.z;
-            s.w += p.w;
+    constexpr uint32_t NI = per / 256;                   // per thread
+    static_assert(per % 256 == 0, "a fixup slice is a whole number of 256-thread rounds");
+    float4 s[NI];
+#pragma unroll
+    for (uint32_t k = 0; k < NI; ++k) s[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    // The contributing workgroups in order (range boundaries computed once
+    // per workgroup, not per entry); slot 1 for the one whose range starts
+    // before the tile.
+    uint32_t bv = sk_begin(units, G, w);
+    for (uint32_t v = w; v < G && bv < t1; ++v) {
+        const uint32_t bn = sk_begin(units, G, v + 1);
+        if (bn > t0 && bn != bv) {
+            const float *src = a.ws + (size_t(v) * 2 + (bv >= t0 ? 0u : 1u)) * (GM * GN);
+#pragma unroll
+            for (uint32_t k = 0; k < NI; ++k) {
+                const float4 p = reinterpret_cast<const float4 *>(src)[slice * per + k * 256 + threadIdx.x];
+                s[k].x += p.x;
+                s[k].y += p.y;
+                s[k].z += p.z;
+                s[k].w += p.w;
+            }
         }
+        bv = bn;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < NI; ++k) {
+        const uint32_t i = slice * per + k * 256 + threadIdx.x;
+        const uint32_t ml = (4 * i) / GN, nl = (4 * i) % GN;
         const uint32_t m = m0 + ml, n = n0 + nl;
         if (m >= tg.mend) continue;
-        const float sv[4] = {s.x, s.y, s.z, s.w};
+        float *o = a.out + size_t(m) * a.N + n;
+        if (n + 3 < a.N && (a.N & 3) == 0) {
+            *reinterpret_cast<float4 *>(o) = s[k];
+        } else {
+            const float sv[4] = {s[k].x, s[k].y, s[k].z, s[k].w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (n + e < a.N) a.out[size_t(m) * a.N + n + e] = sv[e];
+            for (int e = 0; e < 4; ++e)
+                if (n + e < a.N) o[e] = sv[e];
+        }
     }
 }
 
