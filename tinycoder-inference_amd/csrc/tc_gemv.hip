@@ -2,6 +2,7 @@
 // (k_gemv_t in tc_gemv_kernel.hpp): job layout, row split over the CUs,
 // launch-shape choice and the per-type launch.
 #include <algorithm>
+#include <cmath>
 
 #include "tc_gemv_kernel.hpp"
 
@@ -38,6 +39,42 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
     // One workgroup per CU, each with at least 2 tiles of work.
     const uint64_t want = std::max<uint64_t>(
         1, std::min<uint64_t>(uint64_t(num_cu), (total_units + 2 * kTileUnits - 1) / (2 * kTileUnits)));
+    // Workgroups per job. A workgroup first stages its job's activations
+    // (nu records per token; wide inputs cost several times more than narrow
+    // ones) and then streams its units, so in a launch of plain jobs with
+    // different widths the shares are chosen so that every workgroup's
+    // staging + units come out equal: g_j = units_j / (T - stage_j), with the
+    // smallest T for which the counts fit on the chip.
+    uint64_t gplan[kMaxJobs] = {};
+    bool plan = njobs > 1;
+    for (uint32_t j = 0; j < njobs; ++j) plan = plan && jobs[j].npairs == 1 && jobs[j].ids == nullptr;
+    if (plan) {
+        // staging one activation record costs about as much time as
+        // streaming 10 weight units (measured on the 7-matrix Q4_K layer)
+        constexpr double kStage = 10.0;
+        double st[kMaxJobs], smax = 0.0;
+        for (uint32_t j = 0; j < njobs; ++j) {
+            st[j] = kStage * (jobs[j].cols / 256) * S;
+            smax = std::max(smax, st[j]);
+        }
+        auto count = [&](double T, uint64_t *g) {
+            uint64_t tot = 0;
+            for (uint32_t j = 0; j < njobs; ++j) {
+                const double u = double(jobs[j].rows) * (jobs[j].cols / 256) * job_mats(jobs[j]);
+                g[j] = std::min<uint64_t>(jobs[j].rows, std::max<uint64_t>(1, uint64_t(std::ceil(u / (T - st[j])))));
+                tot += g[j];
+            }
+            return tot;
+        };
+        double lo = smax, hi = smax + double(total_units) + 1.0;  // count(hi) == njobs
+        for (int it = 0; it < 60; ++it) {
+            const double mid = 0.5 * (lo + hi);
+            uint64_t g[kMaxJobs];
+            if (count(mid, g) > want) lo = mid;
+            else hi = mid;
+        }
+        count(hi, gplan);
+    }
     uint32_t wg = 0, max_part = 0;
     for (uint32_t j = 0; j < njobs; ++j) {
         const GemvJob &g = jobs[j];
@@ -67,7 +104,9 @@ hipError_t launch_gemv_tiled_c(int type, uint32_t S, const GemvJob *jobs, uint32
         d.nx = g.rk ? g.rk : S;
         const uint64_t units = uint64_t(g.rows) * d.nu * pairs * g.npairs;
         // workgroups per mat-vec (per expert pair in expert-pair mode)
-        uint64_t gj = std::max<uint64_t>(1, (want * units + total_units / 2) / total_units / g.npairs);
+        // (rounded down: one workgroup more than the CUs would run as a
+        // second round)
+        uint64_t gj = plan ? gplan[j] : std::max<uint64_t>(1, want * units / total_units / g.npairs);
         gj = std::min<uint64_t>(gj, g.rows);
         uint32_t rpw = uint32_t((g.rows + gj - 1) / gj);
         const uint32_t fit = part_avail / (pairs * S * d.nu * 4);
