@@ -296,6 +296,34 @@ def test_gemv_multi_matches_single(tc, dev, oracle):
         assert ok, (i, worst)
 
 
+@pytest.mark.parametrize("S", [1, 2])
+def test_gemv_multi_full_layer(tc, dev, oracle, S):
+    """The 7 matrices of a Qwen2.5-7B layer (q, k, v, o, gate, up, down;
+    inputs of 3584 and 18944 columns) in ONE launch, as the benchmark's
+    one-launch layer: the workgroup shares differ from the single launches
+    (per-job staging cost), so every output is checked against its own
+    single-matrix launch bit for bit and against the oracle on every row."""
+    import torch
+    H, F = 3584, 18944
+    shapes = [(H, H), (512, H), (512, H), (H, H), (F, H), (F, H), (H, F)]
+    g = torch.Generator(device=dev).manual_seed(90 + S)
+    rng = np.random.default_rng(90 + S)
+    ws, xs = [], []
+    for r, c in shapes:
+        ws.append(tc.encode(Q4_K, torch.randn((r, c), generator=g, device=dev)))
+    x_attn = gaussian(rng, (S, H))
+    xs = [x_attn, x_attn, x_attn, gaussian(rng, (S, H)), *(2 * [gaussian(rng, (S, H))]), gaussian(rng, (S, F))]
+    xd = [to_dev(x, dev) for x in xs]
+    outs = tc.gemv_multi(Q4_K, ws, xd, [r for r, _ in shapes], [c for _, c in shapes])
+    for i, (r, c) in enumerate(shapes):
+        got = outs[i].cpu().numpy()
+        single = tc.gemv(Q4_K, ws[i], xd[i], r, c).cpu().numpy()
+        assert np.array_equal(got, single), (i, r, c)
+        ref = oracle_matmul_par(oracle, Q4_K, ws[i].cpu().numpy(), xs[i], r, c)
+        ok, worst = close(got, ref)
+        assert ok, (i, r, c, worst)
+
+
 @pytest.mark.parametrize("qt", ALL)
 def test_gemv_dual_swiglu(tc, dev, oracle, qt):
     """gate/up pair in one launch: uout = up row sums, gout = silu(gate) * up.
