@@ -34,8 +34,10 @@ def test_quantize_q8k_golden(tc, dev, golden):
 
 
 @pytest.mark.parametrize("qt", [Q4_K, Q8_0])
-@pytest.mark.parametrize("S,cols", [(1, 256), (3, 3584), (8, 18944), (2, 5120)])
+@pytest.mark.parametrize("S,cols", [(1, 256), (3, 3584), (8, 18944), (2, 5120), (7, 599296)])
 def test_quantize_act_bit_exact(tc, dev, oracle, qt, S, cols):
+    """Bit-exact against the oracle. 7 x 599296 is 16387 blocks: the
+    large-batch quantizer (4 blocks per wave) with a partial last wave."""
     rng = np.random.default_rng(cols + S)
     x = gaussian(rng, (S, cols))
     x[0, :64] = 0.0

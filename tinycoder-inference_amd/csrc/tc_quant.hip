@@ -33,16 +33,30 @@ __device__ __forceinline__ uint32_t act_dst_block(uint32_t g, uint32_t nbk, uint
     return (g - t * nbk) * S + t;
 }
 
-// Q8_K (reference include/GGMLDequantize.hpp:2769-2807): one wave per
-// 256-element block. nblk_total = S * cols / 256 (token rows are contiguous,
-// so block g covers x[256g, 256g+256)).
+// Q8_K (reference include/GGMLDequantize.hpp:2769-2807): one wave per BPW
+// consecutive 256-element blocks, all of their loads issued before the first
+// block is quantized (large batches: a wave per block would keep too few bytes
+// in flight). nblk_total = S * cols / 256 (token rows are contiguous, so block
+// g covers x[256g, 256g+256)).
+template <int BPW>
 __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int8_t *__restrict__ qs,
                                                    float *__restrict__ d, int16_t *__restrict__ bsums,
                                                    uint32_t nblk_total, uint32_t nbk, uint32_t bm_S) {
-    const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (g >= nblk_total) return;
-    const uint32_t o = act_dst_block(g, nbk, bm_S);
-    quant_q8k_block_wave(x + size_t(g) * 256, qs + size_t(o) * 256, d + o, bsums + size_t(o) * 16);
+    const uint32_t g0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW;
+    if (g0 >= nblk_total) return;
+    const uint32_t lane = threadIdx.x & 63;
+    float4 v[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i)
+        v[i] = g0 + i < nblk_total ? reinterpret_cast<const float4 *>(x + size_t(g0 + i) * 256)[lane]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const uint32_t g = g0 + i;
+        if (g >= nblk_total) break;  // wave-uniform
+        const uint32_t o = act_dst_block(g, nbk, bm_S);
+        quant_q8k_block_wave_v(v[i], qs + size_t(o) * 256, d + o, bsums + size_t(o) * 16);
+    }
 }
 
 // The same with a row gather: output row s quantizes x row rows[s] (MoE
@@ -60,14 +74,27 @@ __global__ __launch_bounds__(256) void k_quant_q8k_rows(const float *__restrict_
 }
 
 // 32-wide rule used for Q8_0 weights (reference
-// src/cpp/core/SIMDMatMulVecAVX2.cpp:4296-4326): one wave per 8 blocks.
+// src/cpp/core/SIMDMatMulVecAVX2.cpp:4296-4326): one wave per BPW groups of 8
+// blocks, loads first as in k_quant_q8k.
+template <int BPW>
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int8_t *__restrict__ qs,
                                                     float *__restrict__ d, uint32_t ngroups, uint32_t nbk,
                                                     uint32_t bm_S) {
-    const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (g >= ngroups) return;
-    const uint32_t o = act_dst_block(g, nbk, bm_S);
-    quant_q8_0_blocks_wave(x + size_t(g) * 256, qs + size_t(o) * 256, d + size_t(o) * 8);
+    const uint32_t g0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW;
+    if (g0 >= ngroups) return;
+    const uint32_t lane = threadIdx.x & 63;
+    float4 v[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i)
+        v[i] = g0 + i < ngroups ? reinterpret_cast<const float4 *>(x + size_t(g0 + i) * 256)[lane]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const uint32_t g = g0 + i;
+        if (g >= ngroups) break;  // wave-uniform
+        const uint32_t o = act_dst_block(g, nbk, bm_S);
+        quant_q8_0_blocks_wave_v(v[i], qs + size_t(o) * 256, d + size_t(o) * 8);
+    }
 }
 
 // Row copy into a wider, zero-padded row: dst[r][i] = src[r][i] for i < sbytes,
@@ -782,11 +809,15 @@ hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols
     float *d = reinterpret_cast<float *>(static_cast<char *>(buf) + L.d_off);
     if (wtype == kQ8_0) {
         const uint32_t ng = S * (cols / 256);
-        k_quant_q8_0<<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
+        if (ng >= 16384) k_quant_q8_0<4><<<(ng + 15) / 16, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
+        else k_quant_q8_0<1><<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
     } else {
         int16_t *bs = reinterpret_cast<int16_t *>(static_cast<char *>(buf) + L.bs_off);
         const uint32_t nb = S * (cols / 256);
-        k_quant_q8k<<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, nb, nbk, bm_S);
+        // 4 blocks per wave once there are enough blocks to fill the chip
+        // with waves anyway
+        if (nb >= 16384) k_quant_q8k<4><<<(nb + 15) / 16, 256, 0, st>>>(x, qs, d, bs, nb, nbk, bm_S);
+        else k_quant_q8k<1><<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, nb, nbk, bm_S);
     }
     return hipGetLastError();
 }
