@@ -151,10 +151,39 @@ GEMM_7B_SHAPES = [(18944, 3584), (3584, 18944)]   # qwen2.5-7b FFN up and down
 INT8_PEAK_TOPS = 5000.0
 
 
+def gemm_time(torch, tc, qt, N, K, Ms, gen, dev, reps):
+    """Per-call time in us of tc_gemm (activation quantization + int8 MFMA GEMM
+    [+ split-K reduce]) for each M in Ms: weights N(0,0.02) through the GPU
+    encoder, rotating copies of at least 600 MB in all (beyond the 256 MB
+    Infinity Cache); x ~ N(0,1)."""
+    wf = torch.randn((N, K), generator=gen, device=dev) * 0.02
+    w0 = tc.encode(qt, wf)
+    del wf
+    ncopy = max(4, -(-600_000_000 // (w0.numel())))
+    ws = [w0] + [w0.clone() for _ in range(ncopy - 1)]
+    times = []
+    for M in Ms:
+        x = torch.randn((M, K), generator=gen, device=dev)
+        out = torch.empty((M, N), device=dev)
+        for i in range(3):
+            tc.gemm(qt, ws[i % ncopy], x, N, K, out=out)
+        torch.cuda.synchronize()
+        n = max(3, reps if M < 2048 else reps // 4)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(n):
+            tc.gemm(qt, ws[i % ncopy], x, N, K, out=out)
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) * 1e3 / n)
+    del ws, w0
+    torch.cuda.empty_cache()
+    return times
+
+
 def gemm_bench(torch, tc, tc_hip, dev, reps):
-    """Prefill GEMM (tc_gemm: activation quantization + int8 MFMA GEMM [+ split-K
-    reduce]) at every M x shape x type; weights N(0,0.02) through the GPU
-    encoders, rotating copies of at least 600 MB in all; x ~ N(0,1). Returns one record per config."""
+    """Prefill GEMM at every M x shape x type. Returns one record per config."""
     gen = torch.Generator(device=dev).manual_seed(7)
     res = []
     legs = [(tc_hip.Q4_K, "Q4_K", GEMM_SHAPES), (tc_hip.Q8_0, "Q8_0", GEMM_SHAPES),
@@ -163,34 +192,30 @@ def gemm_bench(torch, tc, tc_hip, dev, reps):
             (tc_hip.IQ2_S, "IQ2_S", GEMM_7B_SHAPES)]
     for qt, tname, shapes in legs:
         for N, K in shapes:
-            wf = torch.randn((N, K), generator=gen, device=dev) * 0.02
-            w0 = tc.encode(qt, wf)
-            del wf
-            # rotating copies: a working set of at least 600 MB, beyond the
-            # 256 MB Infinity Cache
-            ncopy = max(4, -(-600_000_000 // (w0.numel())))
-            ws = [w0] + [w0.clone() for _ in range(ncopy - 1)]
-            for M in GEMM_TOKENS:
-                x = torch.randn((M, K), generator=gen, device=dev)
-                out = torch.empty((M, N), device=dev)
-                for i in range(3):
-                    tc.gemm(qt, ws[i % ncopy], x, N, K, out=out)
-                torch.cuda.synchronize()
-                n = max(3, reps if M < 2048 else reps // 4)
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record()
-                for i in range(n):
-                    tc.gemm(qt, ws[i % ncopy], x, N, K, out=out)
-                b.record()
-                torch.cuda.synchronize()
-                us = a.elapsed_time(b) * 1e3 / n
+            for M, us in zip(GEMM_TOKENS, gemm_time(torch, tc, qt, N, K, GEMM_TOKENS, gen, dev, reps)):
                 tops = 2.0 * M * N * K / us / 1e6
                 res.append({"type": tname, "N": N, "K": K, "M": M, "us": round(us, 1), "TOPS": round(tops, 1),
                             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
-            del ws, w0
-            torch.cuda.empty_cache()
     return res
+
+
+# The only per-shape GEMM times the reference publishes (source comments,
+# RTX 2080 Ti, seq 512): GemmDispatch.cu:522 (IQ3_XXS) and :533-536 (Q4_K).
+REF_GEMM_POINTS = [("Q4_K", 18944, 3584, 1389.0), ("Q4_K", 3584, 18944, 1604.0), ("Q4_K", 3584, 3584, 341.0),
+                   ("Q4_K", 512, 3584, 102.0), ("IQ3_XXS", 18944, 3584, 1724.0)]
+
+
+def gemm_reference_points(torch, tc, tc_hip, dev, reps):
+    """The reference's published int8 GEMM shapes at seq 512, timed here the
+    same way, beside the reference's own figures (other hardware: a side
+    comparison, not the headline vs_baseline)."""
+    gen = torch.Generator(device=dev).manual_seed(11)
+    out = []
+    for tname, N, K, ref_us in REF_GEMM_POINTS:
+        us = gemm_time(torch, tc, getattr(tc_hip, tname), N, K, [512], gen, dev, reps)[0]
+        out.append({"type": tname, "N": N, "K": K, "M": 512, "us": round(us, 1),
+                    "reference_us_rtx2080ti": ref_us, "speedup": round(ref_us / us, 1)})
+    return out
 
 
 def head_start(torch):
@@ -588,10 +613,12 @@ def main():
     if not args.no_gemm:
         del copies
         torch.cuda.empty_cache()
-        g = gemm_bench(torch, tc, tc_hip, dev, max(10, args.steps // 4))
+        greps = max(10, args.steps // 4)
+        g = gemm_bench(torch, tc, tc_hip, dev, greps)
         best = max(g, key=lambda r: r["TOPS"])
         line["prefill_gemm"] = {"unit": "TOPS (2*M*N*K / time, int8 MFMA; includes the activation quantizer)",
-                                "peak_TOPS": INT8_PEAK_TOPS, "best": best, "configs": g}
+                                "peak_TOPS": INT8_PEAK_TOPS, "best": best, "configs": g,
+                                "reference_shapes_seq512": gemm_reference_points(torch, tc, tc_hip, dev, greps)}
     line["roof_probes"] = roof_probes(torch, tc, tc_hip, dev)
     if not args.no_cpu:
         wh = {n: base[n].cpu().numpy() for n in base}
