@@ -1164,7 +1164,14 @@ struct TDot<kIQ2_XS, S> {
 // ONE: a single-job launch, whose descriptor is read without the job-table
 // lookup (one round of kernel-argument loads instead of two).
 template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false, bool ONE = false>
-__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(TLaunchArgs L) {
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(
+    // Job 0's first-needed fields again, as leading scalar arguments: built
+    // with kernarg preloading, these arrive in SGPRs at wave start, so the
+    // one-job launches issue their activation and weight loads without
+    // waiting for a kernel-argument fetch (the rest of the descriptor loads
+    // meanwhile). Other launches ignore them.
+    const float *p_x, const uint8_t *p_W, const uint8_t *p_W2, uint32_t p_cols, uint32_t p_nx, uint32_t p_rows,
+    uint32_t p_rpw, uint32_t p_nu, TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char *xr = smem;
@@ -1185,6 +1192,18 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
             if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
     }
     TJobDev jb = L.jobs[j];
+    if constexpr (ONE && !KEEP && !RG) {
+        jb.x = p_x;
+        jb.W = p_W;
+        jb.W2 = p_W2;
+        jb.cols = p_cols;
+        jb.nx = p_nx;
+        jb.rows = p_rows;
+        jb.rows_per_wg = p_rpw;
+        jb.nu = p_nu;
+        jb.wg_begin = 0;
+        jb.act = ActView{};  // fp32 x: no pre-quantized activations (the host picks this variant only then)
+    }
     uint32_t lw = blockIdx.x - jb.wg_begin;
     bool no_expert = false;
     // Expert ids are loaded here and first used after the activation loads
@@ -1193,7 +1212,8 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
     i32x8 reid = {-1, -1, -1, -1, -1, -1, -1, -1};  // rank-group mode: this token's experts (-1 past rk)
     const float *rwts = nullptr;
-    if (jb.ids != nullptr) {
+    // (the plain one-job launches have no expert ids)
+    if (!(ONE && !KEEP && !RG) && jb.ids != nullptr) {
         const uint32_t p = lw / jb.wg_per_pair;
         lw -= p * jb.wg_per_pair;
         if constexpr (!RG) {
@@ -1260,7 +1280,7 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
     // for the loads).
     __builtin_amdgcn_s_barrier();
     if constexpr (!RG) {
-        if (jb.ids != nullptr) {
+        if (!(ONE && !KEEP && !RG) && jb.ids != nullptr) {
             no_expert = eid < 0 || uint32_t(eid) >= jb.n_experts;
             const uint64_t off = no_expert ? 0 : uint64_t(eid) * jb.wstride;
             jb.W += off;
@@ -1436,7 +1456,9 @@ hipError_t launch_tiled_sd(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream
         hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_t<TYPE, S, DBG, C, RG, KEEP, ONE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    k_gemv_t<TYPE, S, DBG, C, RG, KEEP, ONE><<<g, C::NT, lds, st>>>(a);
+    const TJobDev &j0 = a.jobs[0];
+    k_gemv_t<TYPE, S, DBG, C, RG, KEEP, ONE><<<g, C::NT, lds, st>>>(j0.x, j0.W, j0.W2, j0.cols, j0.nx, j0.rows,
+                                                                    j0.rows_per_wg, j0.nu, a);
     return hipSuccess;
 }
 
@@ -1465,10 +1487,11 @@ hipError_t launch_tiled_s(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream_
             return launch_tiled_sd<TYPE, S, false, C, false, true, true>(a, g, lds, st);
         }
     if (dbg) return launch_tiled_sd<TYPE, S, true, C>(a, g, lds, st);
-    // one-token single-job launches (most decode launches): the descriptor
-    // without the job-table lookup
+    // one-token single-job launches on fp32 x (most decode launches): the
+    // descriptor without the job-table lookup, its first fields preloaded
     if constexpr (S == 1)
-        if (a.njobs == 1) return launch_tiled_sd<TYPE, S, false, C, false, false, true>(a, g, lds, st);
+        if (a.njobs == 1 && a.jobs[0].x != nullptr && a.jobs[0].ids == nullptr)
+            return launch_tiled_sd<TYPE, S, false, C, false, false, true>(a, g, lds, st);
     return launch_tiled_sd<TYPE, S, false, C>(a, g, lds, st);
 }
 
