@@ -1415,20 +1415,45 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
         }
         return;
     }
-    for (uint32_t o0 = 0; o0 < nout; o0 += TNT / 4) {
-        const uint32_t o = o0 + tid / 4, q = tid & 3;
+    // A row's sum is a fixed tree that depends only on the row's unit count,
+    // never on the launch shape, so every launch of a matrix gives the same
+    // bits. Up to 16 units: 4 strided partials (units q, q+4, ... in order)
+    // and their quad sum, 4 lanes per row. More: 16 strided partials, then
+    // quads, then pairs of quads, on 16 lanes per row when the workgroup has
+    // few rows (the down projection's 74 units per row then take 5 adds per
+    // lane instead of 19), else on 4 lanes with 4 partials each.
+    const bool p16 = nu > 16;
+    const bool wide = p16 && nout * 16 <= uint32_t(TNT);
+    const uint32_t lpr = wide ? 16u : 4u;
+    for (uint32_t o0 = 0; o0 < nout; o0 += TNT / lpr) {
+        const uint32_t o = o0 + tid / lpr, q = tid & (lpr - 1);
         const uint32_t oc = o < nout ? o : nout - 1;
         const uint32_t s = oc / nr, rl = oc - s * nr;
-        const float *pg = spart + (size_t(s) * nr + rl) * nu;
-        float g = 0.0f;
-        for (uint32_t bb = q; bb < nu; bb += 4) g += pg[bb];
-        g = quad_sum(g);
+        auto row_sum = [&](const float *pr) __attribute__((always_inline)) {
+            if (!p16) {
+                float v = 0.0f;
+                for (uint32_t bb = q; bb < nu; bb += 4) v += pr[bb];
+                return quad_sum(v);
+            }
+            if (wide) {
+                float v = 0.0f;
+                for (uint32_t bb = q; bb < nu; bb += 16) v += pr[bb];
+                v = quad_sum(v);
+                v += __shfl_xor(v, 4);
+                return v + __shfl_xor(v, 8);
+            }
+            float pj[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                float v = 0.0f;
+                for (uint32_t bb = q + 4 * j; bb < nu; bb += 16) v += pr[bb];
+                pj[j] = quad_sum(v);
+            }
+            return (pj[0] + pj[1]) + (pj[2] + pj[3]);
+        };
+        float g = row_sum(spart + (size_t(s) * nr + rl) * nu);
         float u = 0.0f;
-        if (pairs == 2) {
-            const float *pu = spart + ((size_t(S) + s) * nr + rl) * nu;
-            for (uint32_t bb = q; bb < nu; bb += 4) u += pu[bb];
-            u = quad_sum(u);
-        }
+        if (pairs == 2) u = row_sum(spart + ((size_t(S) + s) * nr + rl) * nu);
         if constexpr (TYPE == kIQ3_XXS) {
             g = 0.25f * g;
             u = 0.25f * u;
