@@ -809,14 +809,14 @@ hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols
     float *d = reinterpret_cast<float *>(static_cast<char *>(buf) + L.d_off);
     if (wtype == kQ8_0) {
         const uint32_t ng = S * (cols / 256);
-        if (ng >= 16384) k_quant_q8_0<4><<<(ng + 15) / 16, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
+        if (ng >= 131072) k_quant_q8_0<4><<<(ng + 15) / 16, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
         else k_quant_q8_0<1><<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
     } else {
         int16_t *bs = reinterpret_cast<int16_t *>(static_cast<char *>(buf) + L.bs_off);
         const uint32_t nb = S * (cols / 256);
-        // 4 blocks per wave once there are enough blocks to fill the chip
-        // with waves anyway
-        if (nb >= 16384) k_quant_q8k<4><<<(nb + 15) / 16, 256, 0, st>>>(x, qs, d, bs, nb, nbk, bm_S);
+        // 4 blocks per wave from 131072 blocks on (measured: slower than a
+        // wave per block at 29k-41k blocks, faster at 139k and more)
+        if (nb >= 131072) k_quant_q8k<4><<<(nb + 15) / 16, 256, 0, st>>>(x, qs, d, bs, nb, nbk, bm_S);
         else k_quant_q8k<1><<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, nb, nbk, bm_S);
     }
     return hipGetLastError();
