@@ -1161,17 +1161,20 @@ struct TDot<kIQ2_XS, S> {
     }
 };
 
-// ONE: a single-job launch, whose descriptor is read without the job-table
-// lookup (one round of kernel-argument loads instead of two).
+// ONE: a single-job launch (on fp32 x, without expert ids in the plain
+// form), whose first-needed descriptor fields arrive as preloaded arguments.
 template <int TYPE, int S, bool DBG, class C, bool RG = false, bool KEEP = false, bool ONE = false>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemv_t(
-    // Job 0's first-needed fields again, as leading scalar arguments: built
-    // with kernarg preloading, these arrive in SGPRs at wave start, so the
-    // one-job launches issue their activation and weight loads without
-    // waiting for a kernel-argument fetch (the rest of the descriptor loads
-    // meanwhile). Other launches ignore them.
-    const float *p_x, const uint8_t *p_W, const uint8_t *p_W2, uint32_t p_cols, uint32_t p_nx, uint32_t p_rows,
-    uint32_t p_rpw, uint32_t p_nu, TLaunchArgs L) {
+    // Leading scalar arguments, built with kernarg preloading so that they
+    // arrive in SGPRs at wave start. One-job launches (ONE): job 0's
+    // first-needed fields (x, W, W2 as bits, cols, tokens, rows, rows per
+    // workgroup, units per row), so the activation and weight loads issue
+    // without waiting for a kernel-argument fetch. Other launches: the first
+    // workgroup of jobs 1..5 in p_a..p_e and of jobs 6, 7 in the two halves of
+    // p_w2 (~0u past the last job), so a workgroup finds its job without a
+    // fetch and loads only that job's descriptor.
+    const float *p_x, const uint8_t *p_W, uint64_t p_w2, uint32_t p_a, uint32_t p_b, uint32_t p_c, uint32_t p_d,
+    uint32_t p_e, TLaunchArgs L) {
     constexpr int TNT = C::NT, TNW = TNT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
     unsigned char *xr = smem;
@@ -1187,20 +1190,22 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
 
     uint32_t j = 0;
     if constexpr (!ONE) {
+        static_assert(kMaxJobs == 8, "job starts in the leading arguments");
+        const uint32_t wgb[7] = {p_a, p_b, p_c, p_d, p_e, uint32_t(p_w2), uint32_t(p_w2 >> 32)};
 #pragma unroll
         for (int k = 1; k < kMaxJobs; ++k)
-            if (uint32_t(k) < L.njobs && blockIdx.x >= L.jobs[k].wg_begin) j = k;
+            if (blockIdx.x >= wgb[k - 1]) j = k;
     }
     TJobDev jb = L.jobs[j];
     if constexpr (ONE && !KEEP && !RG) {
         jb.x = p_x;
         jb.W = p_W;
-        jb.W2 = p_W2;
-        jb.cols = p_cols;
-        jb.nx = p_nx;
-        jb.rows = p_rows;
-        jb.rows_per_wg = p_rpw;
-        jb.nu = p_nu;
+        jb.W2 = reinterpret_cast<const uint8_t *>(p_w2);
+        jb.cols = p_a;
+        jb.nx = p_b;
+        jb.rows = p_c;
+        jb.rows_per_wg = p_d;
+        jb.nu = p_e;
         jb.wg_begin = 0;
         jb.act = ActView{};  // fp32 x: no pre-quantized activations (the host picks this variant only then)
     }
@@ -1482,8 +1487,15 @@ hipError_t launch_tiled_sd(const TLaunchArgs &a, dim3 g, uint32_t lds, hipStream
                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
     const TJobDev &j0 = a.jobs[0];
-    k_gemv_t<TYPE, S, DBG, C, RG, KEEP, ONE><<<g, C::NT, lds, st>>>(j0.x, j0.W, j0.W2, j0.cols, j0.nx, j0.rows,
-                                                                    j0.rows_per_wg, j0.nu, a);
+    if constexpr (ONE) {
+        k_gemv_t<TYPE, S, DBG, C, RG, KEEP, ONE><<<g, C::NT, lds, st>>>(
+            j0.x, j0.W, uint64_t(reinterpret_cast<uintptr_t>(j0.W2)), j0.cols, j0.nx, j0.rows, j0.rows_per_wg, j0.nu, a);
+    } else {
+        uint32_t w[7];
+        for (uint32_t k = 1; k < uint32_t(kMaxJobs); ++k) w[k - 1] = k < a.njobs ? a.jobs[k].wg_begin : ~0u;
+        k_gemv_t<TYPE, S, DBG, C, RG, KEEP, ONE><<<g, C::NT, lds, st>>>(
+            nullptr, nullptr, uint64_t(w[5]) | (uint64_t(w[6]) << 32), w[0], w[1], w[2], w[3], w[4], a);
+    }
     return hipSuccess;
 }
 
