@@ -298,6 +298,23 @@ def test_gemv_multi_matches_single(tc, dev, oracle):
         assert ok, (i, worst)
 
 
+def test_gemv_multi_eight_jobs(tc, dev, oracle):
+    """The largest job list (8 matrices of different heights and widths): every
+    workgroup must find its job, the last one included."""
+    rng = np.random.default_rng(78)
+    shapes = [(96, 512), (200, 1024), (33, 256), (512, 768), (64, 2048), (7, 512), (150, 1280), (301, 512)]
+    ws = [random_blocks(Q4_K, rng, r, c) for r, c in shapes]
+    xs = [gaussian(rng, (1, c)) for _, c in shapes]
+    wd = [to_dev(w, dev) for w in ws]
+    xd = [to_dev(x, dev) for x in xs]
+    outs = tc.gemv_multi(Q4_K, wd, xd, [r for r, _ in shapes], [c for _, c in shapes])
+    for i, (r, c) in enumerate(shapes):
+        got = outs[i].cpu().numpy()
+        assert np.array_equal(got, tc.gemv(Q4_K, wd[i], xd[i], r, c).cpu().numpy()), i
+        ok, worst = close(got, oracle.matmul(Q4_K, ws[i], xs[i], r, c))
+        assert ok, (i, worst)
+
+
 @pytest.mark.parametrize("S", [1, 2])
 def test_gemv_multi_full_layer(tc, dev, oracle, S):
     """The 7 matrices of a Qwen2.5-7B layer (q, k, v, o, gate, up, down;
