@@ -1015,19 +1015,22 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
 }
 
 // Tiles split over several stream-K workgroups: out = the partial segments
-// summed in workgroup order, kFixSlices workgroups per tile (each a quarter of
-// its entries). Plain mode: workgroup group j takes the tile that holds
-// range boundary j+1, when the boundary splits it and is the first to do so;
-// grouped mode (tile count on the device): one group per possible tile,
-// whole tiles exit.
+// summed in workgroup order. Plain mode: kFixSlices workgroups per tile
+// (each a quarter of its entries), workgroup group j taking the tile that
+// holds range boundary j+1, when the boundary splits it and is the first to do
+// so; grouped mode (tile count on the device): one workgroup per possible
+// tile, whole tiles exit.
 constexpr uint32_t kFixSlices = 4;
 template <bool GRP>
 __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
     const uint32_t ntm = sk_ntm<GRP>(a);
     const uint32_t ntiles = GRP ? ntm * a.ntn : a.ntiles;
     const uint32_t units = ntiles * a.nblk, G = a.skg;
-    const uint32_t slice = blockIdx.x % kFixSlices;
-    uint32_t tile = blockIdx.x / kFixSlices;
+    // grouped mode: one workgroup per possible tile (most of them exit; four
+    // per tile made the exits cost more than the sums)
+    constexpr uint32_t SL = GRP ? 1u : kFixSlices;
+    const uint32_t slice = blockIdx.x % SL;
+    uint32_t tile = blockIdx.x / SL;
     if constexpr (!GRP) {
         const uint32_t wb = tile + 1, u = sk_begin(units, G, wb);
         tile = u / a.nblk;
@@ -1042,7 +1045,7 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
     if (sk_begin(units, G, w) <= t0 && sk_begin(units, G, w + 1) >= t1) return;  // one workgroup: stored directly
     const TileGeom tg = sk_tile<GRP>(a, ntm, tile);
     const uint32_t m0 = tg.m0, n0 = tg.n0;
-    constexpr uint32_t per = GM * GN / 4 / kFixSlices;  // float4 entries per slice
+    constexpr uint32_t per = GM * GN / 4 / SL;  // float4 entries per slice
     constexpr uint32_t NI = per / 256;                   // per thread
     static_assert(per % 256 == 0, "a fixup slice is a whole number of 256-thread rounds");
     float4 s[NI];
@@ -1180,7 +1183,7 @@ hipError_t launch_gemm_grouped(const void *W, uint64_t wstride, const ActView &a
     if (e != hipSuccess) return e;
     // The split tiles are known on the device only: one fixup workgroup per
     // possible tile (those past the count, or stored whole, exit at once).
-    k_gemm_fixup<true><<<dim3{ntm_max * ntn * kFixSlices, 1u, 1u}, 256, 0, st>>>(a);
+    k_gemm_fixup<true><<<dim3{ntm_max * ntn, 1u, 1u}, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
