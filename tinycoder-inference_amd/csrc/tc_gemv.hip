@@ -12,6 +12,10 @@ namespace {
 using namespace gv;
 // Streams of at least this many weight bytes use the 512-thread shape.
 constexpr uint64_t kBigBytes = 24ull << 20;
+// MoE expert launches (expert ids on the device) from 4 MB: their weight
+// loads wait for the ids, and more waves per CU hide that (batch 1: 14.4
+// against 15.1 us; plain 7 MB launches were slower on the 512-thread shape).
+constexpr uint64_t kBigBytesExperts = 4ull << 20;
 
 bool tiled_type(int type) { return type == kQ5_0 || type == kIQ4_NL || type == kIQ4_XS || type == kIQ2_XS || type == kQ2_K || type == kIQ2_S || type == kIQ3_S || type == kQ3_K || type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kQ6_K || type == kIQ3_XXS; }
 
@@ -172,7 +176,10 @@ hipError_t launch_gemv_tiled(int type, uint32_t S, const GemvJob *jobs, uint32_t
     bool big_fits = true;
     if (fp32_act_type(type))
         for (uint32_t i = 0; i < njobs; ++i) big_fits = big_fits && tiled_fits<CfgBig>(type, S, jobs[i].cols);
-    return big_fits && use_big(type, jobs_weight_bytes(type, jobs, njobs))
+    bool experts = false;
+    for (uint32_t i = 0; i < njobs; ++i) experts = experts || jobs[i].ids != nullptr;
+    const uint64_t wb = jobs_weight_bytes(type, jobs, njobs);
+    return big_fits && (use_big(type, wb) || (experts && type != kQ8_0 && wb >= kBigBytesExperts))
                ? launch_gemv_tiled_c<CfgBig>(type, S, jobs, njobs, num_cu, st)
                : launch_gemv_tiled_c<CfgSmall>(type, S, jobs, njobs, num_cu, st);
 }
