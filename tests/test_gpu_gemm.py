@@ -51,6 +51,20 @@ def test_gemm_vs_oracle(tc, dev, oracle, qt, M, N, K):
     assert ok, f"{NAMES[qt]} M={M} N={N} K={K}: worst err/bound {worst:.3g}"
 
 
+@pytest.mark.parametrize("M", [8, 40, 64, 100])
+@pytest.mark.parametrize("qt", MFMA_TYPES)
+def test_gemm_token_tiles(tc, dev, oracle, qt, M):
+    """Token counts around the token-tile widths the GEMM picks from M (32,
+    64, 128 tokens), with a ragged last row block."""
+    rng = np.random.default_rng(M * 3 + qt)
+    N, K = 300, 2048
+    w = enc_weights(oracle, qt, rng, N, K)
+    x = gaussian(rng, (M, K))
+    got = tc.gemm(qt, to_dev(w, dev), to_dev(x, dev), N, K).cpu().numpy()
+    ok, worst = close(got, oracle.matmul(qt, w, x, N, K))
+    assert ok, f"{NAMES[qt]} M={M}: worst err/bound {worst:.3g}"
+
+
 @pytest.mark.parametrize("qt", MFMA_TYPES)
 def test_gemm_random_blocks(tc, dev, oracle, qt):
     """Arbitrary block bytes (all scale/min codes, subnormal fp16 scales)."""

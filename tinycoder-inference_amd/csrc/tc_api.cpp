@@ -109,6 +109,7 @@ tc::ActView act_view(void *buf, const tc::ActLayout &L, size_t tok, int type, ui
     v.qs = reinterpret_cast<const int8_t *>(b + L.qs_off) + tok * cols;
     v.d = reinterpret_cast<const float *>(b + L.d_off) + tok * (cols / blk);
     v.bsums = reinterpret_cast<const int16_t *>(b + L.bs_off) + tok * (cols / 16);
+    v.dg = type == TC_Q8_0 ? nullptr : reinterpret_cast<const int8_t *>(b + L.dg_off) + tok * (cols / 256) * 16;
     return v;
 }
 
@@ -256,6 +257,7 @@ size_t gemm_mfma_scratch(int type, uint32_t S, uint32_t rows, uint32_t cols, int
     // last superblock run up to one token tile past the buffer (values never
     // stored; the buffer range check covers only the per-lane offset).
     *act_bytes = tc::act_layout(type, S, cols).bytes + kGemmActSlack;
+    if (tc::prefill_type(type)) return tc::prefill_workspace_bytes(type, S, rows, cols, num_cu);
     return tc::gemm_workspace_bytes(type, S, rows, cols, num_cu);
 }
 
@@ -266,7 +268,10 @@ int gemm_mfma_into(int type, const void *w, const float *x, float *out, uint32_t
     const tc::ActLayout L = tc::act_layout(type, S, cols);
     hipError_t e = tc::launch_quant_act(type, x, S, cols, L, act, st, true);
     if (e != hipSuccess) return hip_fail(e, "activation quantizer");
-    e = tc::launch_gemm(type, w, act_view(act, L, 0, type, cols), out, S, rows, cols, num_cu, ws, st);
+    if (tc::prefill_type(type))
+        e = tc::launch_prefill(type, w, act_view(act, L, 0, type, cols), out, S, rows, cols, num_cu, ws, st);
+    else
+        e = tc::launch_gemm(type, w, act_view(act, L, 0, type, cols), out, S, rows, cols, num_cu, ws, st);
     if (e != hipSuccess) return hip_fail(e, "int8 MFMA GEMM");
     return TC_OK;
 }

@@ -26,14 +26,18 @@ __host__ __device__ constexpr int block_elems(int type) { return type == kQ8_0 |
 //   qs    int8  [S][cols]            (the quantized values)
 //   d     fp32  [S][cols / blk]      (blk = 256 for Q8_K, 32 for Q8_0-style)
 //   bsums int16 [S][cols / 16]       (Q8_K only: sums of 16 consecutive qs)
+//   dg    int8  [S][cols / 256][16]  (Q8_K only: the 8 sums of 32 consecutive
+//                                     qs as two int8 digits, bytes 0-7 the
+//                                     high digits s >> 7, 8-15 the low s & 127)
 struct ActView {
     const int8_t *qs;
     const float *d;
     const int16_t *bsums;
+    const int8_t *dg = nullptr;
 };
 
 struct ActLayout {
-    size_t qs_off, d_off, bs_off, bytes;
+    size_t qs_off, d_off, bs_off, dg_off, bytes;
 };
 
 __host__ inline ActLayout act_layout(int wtype, uint32_t S, uint32_t cols) {
@@ -43,7 +47,8 @@ __host__ inline ActLayout act_layout(int wtype, uint32_t S, uint32_t cols) {
     L.qs_off = 0;
     L.d_off = up(size_t(S) * cols);
     L.bs_off = L.d_off + up(size_t(S) * (cols / blk) * 4);
-    L.bytes = L.bs_off + up(size_t(S) * (cols / 16) * 2);
+    L.dg_off = L.bs_off + up(size_t(S) * (cols / 16) * 2);
+    L.bytes = L.dg_off + (wtype == kQ8_0 ? 0 : up(size_t(S) * (cols / 256) * 16));
     return L;
 }
 

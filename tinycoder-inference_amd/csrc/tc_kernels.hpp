@@ -81,6 +81,14 @@ size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int nu
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
                        int num_cu, void *workspace, hipStream_t st);
 
+// Prefill GEMM with the weights converted in the MFMA lanes' registers, once
+// per token tile of up to 256 tokens (tc_prefill.hip; Q4_K). Needs the
+// activations' digit sums (act.dg) and prefill_workspace_bytes() of scratch.
+bool prefill_type(int type);
+size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
+hipError_t launch_prefill(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N,
+                          uint32_t K, int num_cu, void *workspace, hipStream_t st);
+
 // ---- MoE prefill over expert-sorted rows ----
 // Device-side router: pairs p = t*top_k + r (ids[p] in [0, E), others
 // skipped) sorted by expert; each expert's segment starts at a multiple of
