@@ -40,6 +40,8 @@
 // 8 XCDs) hold one contiguous range, so they share one token tile's
 // activations in their L2. A tile split over several workgroups is summed by
 // k_pf_fixup in workgroup order (deterministic).
+#include <type_traits>
+
 #include "tc_kernels.hpp"
 
 namespace tc {
@@ -59,7 +61,8 @@ struct PLds {
     static constexpr uint32_t QS = 0;                       // [TT][256], 16-byte chunk c of token t at slot c ^ (t & 15)
     static constexpr uint32_t DG = TT * 256;                // [TT][16] digit sums
     static constexpr uint32_t D8 = DG + TT * 16;            // [max(TT, 64)] Q8_K d
-    static constexpr uint32_t bytes = D8 + (TT < 64 ? 64 : TT) * 4;  // one buffer
+    static constexpr uint32_t W = D8 + (TT < 64 ? 64 : TT) * 4;  // [PR][144] the tile's weight blocks
+    static constexpr uint32_t bytes = W + 256 * 144;        // one buffer
 };
 
 struct PfArgs {
@@ -73,6 +76,9 @@ struct PfArgs {
     uint32_t row_bytes, nblk;
     uint32_t ntm, ntn, ntiles;  // token tiles, row blocks, tiles
     uint32_t G;                 // workgroups
+#ifdef TC_PF_TRACE
+    unsigned long long *trace;
+#endif
 };
 
 __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
@@ -102,19 +108,19 @@ struct Q4Raw {
     u4 h, q[4];
 };
 
-// blk: the block's byte offset; g: the lane's k-half.
-__device__ __forceinline__ void q4_load(Q4Raw &r, __amdgpu_buffer_rsrc_t w, uint32_t blk, uint32_t g) {
-    r.h = __builtin_amdgcn_raw_buffer_load_b128(w, blk, 0, 0);
+// From the tile's weight blocks in LDS (row stride 144 bytes: the 16-byte
+// reads of 16 consecutive rows fall on distinct banks).
+__device__ __forceinline__ void q4_read(Q4Raw &r, const unsigned char *blk, uint32_t g) {
+    r.h = lds4(blk);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) r.q[p] = __builtin_amdgcn_raw_buffer_load_b128(w, blk + 16 + 32 * p + 16 * g, 0, 0);
+    for (int p = 0; p < 4; ++p) r.q[p] = lds4(blk + 16 + 32 * p + 16 * g);
 }
 
 // B operands of one superblock: digit planes of sc*q per sub-block, the mins
-// (bytes 0-7 for the high-digit MFMA, 8-15 for the low one; zero in k-half 1),
 // and the row scales.
 struct Q4Frag {
     v4i bh[8], bl[8];
-    v4i mh, ml;
+    v4i m;  // bytes 0-7: the 8 mins (k-half 0; zero in k-half 1)
     float d, dm;
 };
 
@@ -146,8 +152,7 @@ __device__ __forceinline__ void q4_convert(const Q4Raw &r, uint32_t g, Q4Frag &f
     }
     const int z = 0;
     const int a = g == 0 ? int(mnl) : z, b = g == 0 ? int(mnh) : z;
-    f.mh = v4i{a, b, 0, 0};
-    f.ml = v4i{0, 0, a, b};
+    f.m = v4i{a, b, 0, 0};
 }
 
 // Direct-to-LDS buffer loads (no registers, no LDS stores): lane l's 16 (or
@@ -212,6 +217,28 @@ __device__ __forceinline__ void act_to_lds(const PfArgs &a, uint32_t m0, uint32_
     }
 }
 
+// Superblock b of the tile's weight rows into LDS, [row][144] (9 16-byte
+// chunks per row; a wave instruction covers 64 consecutive chunks, so its
+// loads fall on 7-8 consecutive rows: whole cache lines). Rows past N lie
+// outside the descriptor and load zeros.
+template <int NT>
+__device__ __forceinline__ void w_to_lds(const v4i wrs, uint32_t row_bytes,
+                                         uint32_t n0, uint32_t b, unsigned char *buf, uint32_t w, uint32_t lane) {
+    using L = PLds<NT>;
+    constexpr uint32_t NC = PR * 9 / 64;  // wave instructions per superblock
+    const uint32_t base = lds_addr(buf) + L::W;
+    uint32_t ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (uint32_t i = 0; i < (NC + PW - 1) / PW; ++i) {
+        const uint32_t k = w + PW * i;
+        if (NC % PW == 0 || k < NC) {
+            const uint32_t c = 64 * k + ln, r = c / 9, p = c - 9 * r;
+            lds_load16(base + 1024 * k, wrs, (n0 + r) * row_bytes + b * 144 + 16 * p);
+        }
+    }
+}
+
 // One 32-token block t of the tile against this wave's converted weights.
 // The hi and lo chains run interleaved as two independent accumulators (no
 // MFMA waits on the previous one's result), C = 8*hi + lo after both; the
@@ -223,7 +250,8 @@ __device__ __forceinline__ void q4_block(const unsigned char *buf, const Q4Frag 
     using L = PLds<NT>;
     const unsigned char *arow = buf + L::QS + (32 * t + j) * 256;
     const v4i dgv = as_v4i(lds4(buf + L::DG + (32 * t + j) * 16));
-    v16i mn = mfma(dgv, f.mh, v16i{});
+    // high digits in bytes 0-7 against the mins; then the low digits moved there
+    v16i mn = mfma(dgv, f.m, v16i{});
     v16i ch = {}, cl = {};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -233,7 +261,7 @@ __device__ __forceinline__ void q4_block(const unsigned char *buf, const Q4Frag 
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) mn[r] <<= 7;
-    mn = mfma(dgv, f.ml, mn);
+    mn = mfma(v4i{dgv.z, dgv.w, dgv.z, dgv.w}, f.m, mn);
 #pragma unroll
     for (int r = 0; r < 16; ++r) ch[r] = (ch[r] << 3) + cl[r];
     const float *d8 = reinterpret_cast<const float *>(buf + L::D8) + 32 * t + 4 * g;
@@ -266,9 +294,12 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
-    const __amdgpu_buffer_rsrc_t wr = rsrc(a.W, uint64_t(a.N) * a.row_bytes);
+    const v4i wrs = rs4(a.W, a.N * a.row_bytes);
 
     const uint32_t v = sk_logical(blockIdx.x, a.G);
+#ifdef TC_PF_TRACE
+    unsigned long long twait = 0, tconv = 0, tblk = 0, tgap = 0, ts3p = 0, tstore = 0, tstart = __builtin_readcyclecounter();
+#endif
     const uint32_t units = a.ntiles * a.nblk;
     const uint32_t ub = sk_begin(units, a.G, v), ue = sk_begin(units, a.G, v + 1);
     for (uint32_t u = ub; u < ue;) {
@@ -286,7 +317,6 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const uint32_t j = ln & 31, g = ln >> 5;
         const uint32_t tn = tile % a.ntn, tm = tile / a.ntn;
         const uint32_t n0 = tn * PR, m0 = tm * TT;
-        const uint32_t vrow = (n0 + 32 * w + j) * a.row_bytes;  // rows past N: outside the descriptor (zeros)
 
         float acc[NT][16];
 #pragma unroll
@@ -296,32 +326,55 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 
         // Previous segment's readers of both buffers are done.
         __syncthreads();
-        Q4Raw rr;
+        Q4Frag f;
         act_to_lds<NT>(a, m0, b0, buf(b0), w, lane);
-        q4_load(rr, wr, vrow + b0 * 144, g);
-        // Per superblock: its activations and weights are waited for, the
-        // weights converted, the next superblock's loads issued (into the
-        // other LDS buffer and the freed weight registers), then the MFMAs.
+        w_to_lds<NT>(wrs, a.row_bytes, n0, b0, buf(b0), w, lane);
+        // Per superblock: its activations and weight blocks are waited for,
+        // the next superblock's loads issued into the other LDS buffer, this
+        // lane's weights converted, then the MFMAs.
         for (uint32_t b = b0; b < b1; ++b) {
+#ifdef TC_PF_TRACE
+            const unsigned long long ts0 = __builtin_readcyclecounter();
+            if (b > b0) tgap += ts0 - ts3p;
+#endif
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             __syncthreads();
-            Q4Frag f;
-            q4_convert(rr, g, f);
+#ifdef TC_PF_TRACE
+            const unsigned long long ts1 = __builtin_readcyclecounter();
+#endif
             act_to_lds<NT>(a, m0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
-            q4_load(rr, wr, vrow + min(b + 1, b1 - 1) * 144, g);
+            w_to_lds<NT>(wrs, a.row_bytes, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
             {
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    // one token block at a time in the scheduler's window (it
-                    // would otherwise hoist every block's operand reads)
-                    __builtin_amdgcn_sched_barrier(0);
-                    q4_block<NT>(buf(b), f, t, j, g, acc[t]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
+                Q4Raw rr;
+                q4_read(rr, buf(b) + L::W + (32 * w + j) * 144, g);
+                q4_convert(rr, g, f);
             }
+#ifdef TC_PF_TRACE
+            const unsigned long long ts2 = __builtin_readcyclecounter();
+#endif
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                // one token block at a time in the scheduler's window (it
+                // would otherwise hoist every block's operand reads)
+                __builtin_amdgcn_sched_barrier(0);
+                q4_block<NT>(buf(b), f, t, j, g, acc[t]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#ifdef TC_PF_TRACE
+            {
+                const unsigned long long ts3 = __builtin_readcyclecounter();
+                twait += ts1 - ts0;
+                tconv += ts2 - ts1;
+                tblk += ts3 - ts2;
+                ts3p = ts3;
+            }
+#endif
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // nothing of this segment left in flight
 
+#ifdef TC_PF_TRACE
+        const unsigned long long tsst = __builtin_readcyclecounter();
+#endif
         // lane: row n0 + 32w + j, tokens m0 + 32t + 8q + 4g + e
         const uint32_t nl = 32 * w + j, n = n0 + nl;
 #pragma unroll
@@ -339,7 +392,17 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 }
             }
         }
+#ifdef TC_PF_TRACE
+        tstore += __builtin_readcyclecounter() - tsst;
+#endif
     }
+#ifdef TC_PF_TRACE
+    if (lane == 0) {
+        unsigned long long *tr = a.trace + (size_t(blockIdx.x) * PW + w) * 8;
+        tr[0] = twait; tr[1] = tconv; tr[2] = tblk; tr[3] = tgap; tr[4] = tstore;
+        tr[5] = __builtin_readcyclecounter() - tstart;
+    }
+#endif
 }
 
 // Tiles split over several workgroups: out = the partial segments summed in
@@ -441,6 +504,10 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
 
 }  // namespace
 
+#ifdef TC_PF_TRACE
+void *tc_pf_trace_buf = nullptr;
+extern "C" void tc_pf_set_trace(void *p) { tc_pf_trace_buf = p; }
+#endif
 bool prefill_type(int type) { return type == kQ4_K; }
 
 size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
@@ -472,6 +539,9 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
     a.ntn = g.ntn;
     a.ntiles = g.ntiles;
     a.G = g.G;
+#ifdef TC_PF_TRACE
+    a.trace = static_cast<unsigned long long *>(tc_pf_trace_buf);
+#endif
     switch (g.nt) {
         case 1: return pf_launch<1>(a, st);
         case 2: return pf_launch<2>(a, st);
