@@ -97,8 +97,10 @@ __device__ __forceinline__ void quant_q8k_block_wave(const float *x, int8_t *qs,
 }
 
 // Eight 32-element blocks by one full wave (8 lanes per block), lane values
-// already loaded.
-__device__ __forceinline__ void quant_q8_0_blocks_wave_v(float4 v, int8_t *qs, float *d) {
+// already loaded. With dp, also each block's d as three bf16 pieces that sum
+// to it exactly (top 8 significant bits, the next 8, the rest), plus a zero:
+// dp[4b .. 4b+3] (the prefill GEMM forms dw*d from them on the matrix cores).
+__device__ __forceinline__ void quant_q8_0_blocks_wave_v(float4 v, int8_t *qs, float *d, uint16_t *dp = nullptr) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t sub = lane & 7;
     const float e[4] = {v.x, v.y, v.z, v.w};
@@ -113,6 +115,18 @@ __device__ __forceinline__ void quant_q8_0_blocks_wave_v(float4 v, int8_t *qs, f
     }
     reinterpret_cast<uint32_t *>(qs)[lane] = packed;
     if (sub == 0) d[lane >> 3] = dv;
+    if (dp != nullptr && sub == 0) {
+#pragma clang fp contract(off)
+        const uint32_t hb = __builtin_bit_cast(uint32_t, dv) & 0xFFFF0000u;
+        const float r = dv - __builtin_bit_cast(float, hb);
+        const uint32_t mb = __builtin_bit_cast(uint32_t, r) & 0xFFFF0000u;
+        const float l = r - __builtin_bit_cast(float, mb);
+        const uint32_t lb = __builtin_bit_cast(uint32_t, l);
+        uint2 pk;
+        pk.x = (hb >> 16) | mb;
+        pk.y = lb >> 16;
+        reinterpret_cast<uint2 *>(dp)[lane >> 3] = pk;
+    }
 }
 
 __device__ __forceinline__ void quant_q8_0_blocks_wave(const float *x, int8_t *qs, float *d) {

@@ -1,45 +1,55 @@
-// tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K weights on
-// the int8 matrix cores (v_mfma_i32_32x32x32_i8), each weight converted once
-// per token tile of up to 256 tokens, in the registers of the lane that feeds
-// it to the MFMA.
+// tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K and Q8_0
+// weights on the int8 matrix cores (v_mfma_i32_32x32x32_i8). The weights of a
+// tile are converted once per token tile of up to 128 tokens, in the
+// registers of the lanes that feed them to the MFMA.
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698 and
 // its stream-K kernel GemmKernels.cuh:3707-4030) with the CPU reference's
-// numerics: the activations are quantized by the bit-exact Q8_K quantizer,
-// every integer dot product of a weight sub-block with an activation
-// sub-block is exact, and only the per-superblock scale combination runs in
-// fp32.
+// numerics: the activations are quantized by the bit-exact quantizers (Q8_K
+// for Q4_K, the 32-wide Q8_0 rule for Q8_0), every integer dot product of a
+// weight block with an activation block is exact, and only the scale
+// combination runs in fp32.
 //
-// Decomposition. A workgroup has 4 waves; wave w owns 32 weight rows
-// (n0 + 32w + lane % 32) and all TT = 32 NT tokens of the tile, so no weight
-// is converted twice for one tile. The activations of the tile (TT tokens x
-// one 256-wide superblock: int8 values, scale and the digit sums below) are
-// loaded straight into LDS, double-buffered, and read by all 4 waves as the
-// MFMA A operand; the weights never pass through LDS: each lane loads the
-// 80 bytes of its row and k-half it needs (header + 64 quant bytes), two
-// superblocks ahead, and converts them into its B-operand registers.
+// Decomposition. A workgroup has 8 waves (two per SIMD). Per 256-wide
+// superblock of K, the tile's activations (int8 values and their scale data)
+// and raw weight blocks are loaded straight into LDS (no registers, whole
+// cache lines per wave instruction), double-buffered. Each lane then reads
+// the bytes of its weight row and k-half, converts them into its MFMA B
+// operand, and runs the MFMAs against activation fragments read from LDS.
+//  * Q4_K: wave w owns 32 weight rows and every token of the tile (256 rows
+//    per workgroup), so no weight is converted twice for one tile.
+//  * Q8_0: 128 rows per workgroup, waves w and w + 4 share rows and take one
+//    half of the tile's tokens each (the Q8_0 weight blocks take 272 bytes of
+//    LDS per row and superblock).
 //
 // Q4_K (reference dequantizeQ4_KBlock, GGMLDequantize.hpp:436-477): a weight
 // of sub-block s is w = d*sc_s*q - dmin*m_s with q in 0..15 and sc_s, m_s in
 // 0..63. With sc_s = 8*h_s + l_s (h_s, l_s in 0..7) the products h_s*q and
-// l_s*q fit int8, so the hi chain (8 MFMAs) and the lo chain (8 more, on the
-// hi result shifted left by 3) give C = sum_s sc_s * (q . x)_s exactly. The
-// min term sum_s m_s * S_s (S_s the sum of the 32 activations of sub-block s,
-// from the quantizer as int8 digits S_s = 128*hi + lo) is one MFMA pair over 8
-// k slots. Per superblock and output, in fp32: acc += d8 * (d*C - dmin*Mn).
+// l_s*q fit int8, so the hi chain (8 MFMAs) and the lo chain (8 more) give
+// C = sum_s sc_s * (q . x)_s exactly as 8*hi + lo. The min term sum_s m_s *
+// S_s (S_s the sum of the 32 activations of sub-block s, from the quantizer
+// as int8 digits S_s = 128*hi + lo) is one MFMA pair over 8 k slots. Per
+// superblock and output, in fp32: acc += d8 * (d*C - dmin*Mn).
 //
-// MFMA operands: lane l feeds row (l & 31) and the 16 bytes of k-group
-// (l >> 5) of A and of B (any fixed pairing of k positions works, as both
-// operands use it). A = activations (row = token), B = weights (column =
-// weight row), so a lane's 16 results share one weight row (its scales are
-// lane constants) and cover tokens 8*(r/4) + 4*(l >> 5) + (r % 4).
+// Q8_0 (reference matMulVecBatchQ8_0_Q8K_AVX2, SIMDMatMulVecAVX2.cpp:4239-4383):
+// one MFMA per 32-block gives the exact integer I; the scale dw * d8 of every
+// output of the block comes from one bf16 MFMA as an outer product of their
+// exact bf16 pieces (dw = h + l, d8 = h + m + l, 6 exact products summed in
+// fp32), so the fp32 combination acc += I * (dw*d8) is two VALU operations
+// per output (a convert and an fma) instead of three.
+//
+// MFMA operands: lane l feeds row (l & 31) and k-group (l >> 5) of A and of B
+// (any fixed pairing of k positions works, as both operands use it). A =
+// activations (row = token), B = weights (column = weight row), so a lane's
+// 16 results share one weight row (its scales are lane constants) and cover
+// tokens 8*(r/4) + 4*(l >> 5) + (r % 4).
 //
 // Work split: the (tile, superblock) units, tiles ordered row block fastest,
-// are divided evenly over the workgroups (stream-K); workgroup ranges are
-// numbered so that the workgroups of one XCD (dispatched round robin over the
-// 8 XCDs) hold one contiguous range, so they share one token tile's
-// activations in their L2. A tile split over several workgroups is summed by
-// k_pf_fixup in workgroup order (deterministic).
+// are divided evenly over one workgroup per CU (stream-K); workgroup ranges
+// are numbered so that the workgroups of one XCD (dispatched round robin over
+// the 8 XCDs) hold one contiguous range and share one token tile's activations
+// in their L2. A tile split over several workgroups is summed by k_pf_fixup
+// in workgroup order (deterministic).
 #include <type_traits>
 
 #include "tc_kernels.hpp"
@@ -49,47 +59,65 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
-constexpr uint32_t PW = 8;          // waves per workgroup (two per SIMD)
-constexpr uint32_t PR = 32 * PW;    // weight rows per workgroup tile
+constexpr uint32_t PW = 8;  // waves per workgroup (two per SIMD)
 
-template <int NT>
+// Per weight type: rows per workgroup tile, waves per row group (waves that
+// share rows and split the tokens), unit bytes, and the activation scale
+// data per token and superblock (Q4_K: 16 digit bytes + the fp32 d; Q8_0: 8
+// blocks x 4 bf16 pieces).
+template <int TYPE>
+struct PfType;
+template <>
+struct PfType<kQ4_K> {
+    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 144, XB = 16;
+};
+template <>
+struct PfType<kQ8_0> {
+    static constexpr uint32_t PR = 128, TSPLIT = 2, UB = 272, XB = 64;
+};
+
+// One LDS buffer: [TT][256] activation values (16-byte chunk c of token t at
+// slot c ^ (t & 15)), [TT][XB] scale data, Q4_K's [max(TT, 64)] fp32 d,
+// [PR][UB] raw weight blocks.
+template <int TYPE, int NT>
 struct PLds {
-    static constexpr uint32_t TT = 32 * NT;                 // tokens per tile
-    static constexpr uint32_t QS = 0;                       // [TT][256], 16-byte chunk c of token t at slot c ^ (t & 15)
-    static constexpr uint32_t DG = TT * 256;                // [TT][16] digit sums
-    static constexpr uint32_t D8 = DG + TT * 16;            // [max(TT, 64)] Q8_K d
-    static constexpr uint32_t W = D8 + (TT < 64 ? 64 : TT) * 4;  // [PR][144] the tile's weight blocks
-    static constexpr uint32_t bytes = W + 256 * 144;        // one buffer
+    using T = PfType<TYPE>;
+    static constexpr uint32_t TT = 32 * NT;
+    static constexpr uint32_t QS = 0;
+    static constexpr uint32_t XS = TT * 256;
+    static constexpr uint32_t D8 = XS + TT * T::XB;
+    static constexpr uint32_t W = D8 + (TYPE == kQ4_K ? (TT < 64 ? 64 : TT) * 4 : 0);
+    static constexpr uint32_t bytes = W + T::PR * T::UB;
 };
 
 struct PfArgs {
     const uint8_t *W;
     const int8_t *qs;   // block-major [nblk][M][256]
-    const float *d8;    // [nblk][M]
-    const int8_t *dg;   // [nblk][M][16]
+    const float *d8;    // Q4_K: [nblk][M]
+    const int8_t *xs;   // Q4_K digit sums [nblk][M][16]; Q8_0 d pieces [nblk][M][64 B]
     float *out;         // [M][N]
     float *ws;          // partial tiles [G][2][TT][PR]
     uint32_t M, N, K;
     uint32_t row_bytes, nblk;
     uint32_t ntm, ntn, ntiles;  // token tiles, row blocks, tiles
     uint32_t G;                 // workgroups
-#ifdef TC_PF_TRACE
-    unsigned long long *trace;
-#endif
 };
 
 __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ u4 lds4(const unsigned char *p) { return *reinterpret_cast<const u4 *>(p); }
-__device__ __forceinline__ v4i as_v4i(u4 v) { return __builtin_bit_cast(v4i, v); }
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, uint64_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), short(0), int(uint32_t(bytes)), 0x00020000);
+__device__ __forceinline__ v16f mfma_bf16(v4i a, v4i b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0,
+                                                  0, 0);
 }
+__device__ __forceinline__ u4 lds4(const unsigned char *p) { return *reinterpret_cast<const u4 *>(p); }
+__device__ __forceinline__ uint32_t lds1(const unsigned char *p) { return *reinterpret_cast<const uint32_t *>(p); }
+__device__ __forceinline__ v4i as_v4i(u4 v) { return __builtin_bit_cast(v4i, v); }
 
 // Bytewise products of four values (each <= 15) with one multiplier <= 7
 // held in both 16-bit halves of m: no product exceeds a byte, so the 16-bit
@@ -102,22 +130,22 @@ __device__ __forceinline__ uint32_t bcast16(uint32_t w, uint32_t k) {
     return __builtin_amdgcn_perm(0u, w, 0x0c000c00u | (k << 16) | k);
 }
 
-// Raw bytes of one superblock of this lane's weight row: the 16-byte header
-// and, for k-half g, bytes 16g..16g+15 of each 32-byte quant group.
+// ---- Q4_K: B operands of one superblock ------------------------------------
+
+// The 16-byte header and, for k-half g, bytes 16g..16g+15 of each 32-byte
+// quant group of this lane's weight row, from the tile's blocks in LDS (row
+// stride 144 bytes: the 16-byte reads of 16 consecutive rows fall on
+// distinct banks).
 struct Q4Raw {
     u4 h, q[4];
 };
-
-// From the tile's weight blocks in LDS (row stride 144 bytes: the 16-byte
-// reads of 16 consecutive rows fall on distinct banks).
 __device__ __forceinline__ void q4_read(Q4Raw &r, const unsigned char *blk, uint32_t g) {
     r.h = lds4(blk);
 #pragma unroll
     for (int p = 0; p < 4; ++p) r.q[p] = lds4(blk + 16 + 32 * p + 16 * g);
 }
 
-// B operands of one superblock: digit planes of sc*q per sub-block, the mins
-// and the row scales.
+// Digit planes of sc*q per sub-block, the mins and the row scales.
 struct Q4Frag {
     v4i bh[8], bl[8];
     v4i m;  // bytes 0-7: the 8 mins (k-half 0; zero in k-half 1)
@@ -150,10 +178,96 @@ __device__ __forceinline__ void q4_convert(const Q4Raw &r, uint32_t g, Q4Frag &f
             f.bl[s1][k] = pkmul(hi, ml1);
         }
     }
-    const int z = 0;
-    const int a = g == 0 ? int(mnl) : z, b = g == 0 ? int(mnh) : z;
+    const int a = g == 0 ? int(mnl) : 0, b = g == 0 ? int(mnh) : 0;
     f.m = v4i{a, b, 0, 0};
 }
+
+// One 32-token block (activation row arow, digit sums at dgp, scales at d8)
+// against this wave's converted weights. The hi and lo chains run
+// interleaved as two independent accumulators (no MFMA waits on the previous
+// one's result); the min term's high-digit MFMA is issued first so that its
+// shift overlaps the chains.
+__device__ __forceinline__ void q4_block(const unsigned char *arow, const unsigned char *dgp, const float *d8,
+                                         const Q4Frag &f, uint32_t j, uint32_t g, float (&acc)[16]) {
+    const v4i dgv = as_v4i(lds4(dgp));
+    // high digits in bytes 0-7 against the mins; then the low digits moved there
+    v16i mn = mfma(dgv, f.m, v16i{});
+    v16i ch = {}, cl = {};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const v4i af = as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
+        ch = mfma(af, f.bh[s], ch);
+        cl = mfma(af, f.bl[s], cl);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mn[r] <<= 7;
+    mn = mfma(v4i{dgv.z, dgv.w, dgv.z, dgv.w}, f.m, mn);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ch[r] = (ch[r] << 3) + cl[r];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 dv = *reinterpret_cast<const float4 *>(d8 + 8 * q);
+        const float dd[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = 4 * q + e;
+            acc[r] = fmaf(dd[e], fmaf(f.d, float(ch[r]), -f.dm * float(mn[r])), acc[r]);
+        }
+    }
+}
+
+// ---- Q8_0: B operands of one superblock ------------------------------------
+
+// The 8 blocks of this lane's row (34-byte blocks, so 2-byte aligned): the
+// 16 values of k-half g of each block as one B operand, and each block's
+// scale as bf16 pieces dw = h + l (l exact: dw has 11 significant bits) laid
+// out against the activation pieces [h8 m8 l8 0 h8 m8 l8 0]: slots 0-3 times
+// h, 4-7 times l (zero in k-half 1, which the activation side leaves free).
+struct Q8Frag {
+    v4i bw[8], bp[8];
+};
+
+__device__ __forceinline__ void q8_convert(const unsigned char *row, uint32_t g, Q8Frag &f) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t off = 34 * k + 2 + 16 * g;  // the 16 values (k even: 2 mod 4; odd: 0 mod 4)
+        if ((k & 1) == 0) {
+            uint32_t dw[5];
+#pragma unroll
+            for (int i = 0; i < 5; ++i) dw[i] = lds1(row + off - 2 + 4 * i);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) f.bw[k][i] = int(__builtin_amdgcn_alignbyte(dw[i + 1], dw[i], 2));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) f.bw[k][i] = int(lds1(row + off + 4 * i));
+        }
+        const uint32_t dword = lds1(row + ((34 * k) & ~3u));
+        const uint32_t dbits = (k & 1) ? dword >> 16 : dword & 0xFFFFu;
+        const float d = h2f(dbits);
+        const uint32_t hb = __builtin_bit_cast(uint32_t, d) & 0xFFFF0000u;
+        const uint32_t lb = __builtin_bit_cast(uint32_t, d - __builtin_bit_cast(float, hb));
+        const uint32_t h16 = hb >> 16, l16 = lb >> 16;
+        f.bp[k] = g == 0 ? v4i{int(h16 | hb), int(h16), int(l16 | (l16 << 16)), int(l16)} : v4i{0, 0, 0, 0};
+    }
+}
+
+// One 32-token block: per 32-wide weight block k, the exact integer product
+// I (int8 MFMA) and the scales dw*d8 of its 32x32 outputs (bf16 MFMA), then
+// acc += I * scale.
+__device__ __forceinline__ void q8_block(const unsigned char *arow, const unsigned char *prow, const Q8Frag &f,
+                                         uint32_t j, uint32_t g, float (&acc)[16]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const v4i af = as_v4i(lds4(arow + 16 * ((2 * k + g) ^ (j & 15))));
+        const uint2 pp = *reinterpret_cast<const uint2 *>(prow + 8 * k);
+        const v16i I = mfma(af, f.bw[k], v16i{});
+        const v16f S = mfma_bf16(v4i{int(pp.x), int(pp.y), int(pp.x), int(pp.y)}, f.bp[k], v16f{});
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = fmaf(float(I[r]), S[r], acc[r]);
+    }
+}
+
+// ---- loads into LDS ---------------------------------------------------------
 
 // Direct-to-LDS buffer loads (no registers, no LDS stores): lane l's 16 (or
 // 4) bytes land at lds_dst + 16 l (4 l). Inline, so that the compiler, which
@@ -183,98 +297,54 @@ __device__ __forceinline__ uint32_t lds_addr(const unsigned char *p) {
     return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(p)));
 }
 
-// Superblock b of token tile m0 into one LDS buffer: values (1 KB per wave
-// instruction = 4 tokens, XOR-swizzled chunks), digit sums and scales. Tokens
-// past M read other tokens' bytes or zeros (their outputs are never stored).
-template <int NT>
-__device__ __forceinline__ void act_to_lds(const PfArgs &a, uint32_t m0, uint32_t b, unsigned char *buf, uint32_t w,
-                                           uint32_t lane) {
-    using L = PLds<NT>;
+// Wave instruction k of N (k = w, w + PW, ...) -- the loads of one stage are
+// spread over the waves.
+template <uint32_t N, typename F>
+__device__ __forceinline__ void each_inst(uint32_t w, F &&f) {
+#pragma unroll
+    for (uint32_t i = 0; i < (N + PW - 1) / PW; ++i) {
+        const uint32_t k = w + PW * i;
+        if (N % PW == 0 || k < N) f(k);
+    }
+}
+
+// Superblock b of the tile into one LDS buffer: activation values (1 KB per
+// wave instruction = 4 tokens, XOR-swizzled chunks), their scale data, and the
+// weight blocks of rows n0 .. n0 + PR - 1 ([row][UB]; a wave instruction
+// covers 64 consecutive 16-byte chunks, so its loads fall on consecutive
+// rows: whole cache lines). Tokens past M read other tokens' bytes or zeros
+// and rows past N lie outside the descriptor (zeros); neither is stored.
+template <int TYPE, int NT>
+__device__ __forceinline__ void stage(const PfArgs &a, uint32_t m0, uint32_t n0, uint32_t b, unsigned char *buf,
+                                      uint32_t w, uint32_t lane) {
+    using L = PLds<TYPE, NT>;
+    using T = PfType<TYPE>;
     constexpr uint32_t TT = L::TT;
-    const v4i rq = rs4(a.qs, a.M * a.K), rg = rs4(a.dg, a.M * a.nblk * 16), rd = rs4(a.d8, a.M * a.nblk * 4);
     const uint32_t base = lds_addr(buf);
     const uint32_t tb = b * a.M + m0;  // first token record of the tile in this superblock
     uint32_t ln = lane;
     asm volatile("" : "+v"(ln));  // per-call lane arithmetic (not hoisted into held registers)
-    // values: instruction k (of TT/4 1-KB rows) fills tokens 4k..4k+3
-    constexpr uint32_t NQ = TT / 4, NG = TT / 16, ND = (TT + 63) / 64;
-#pragma unroll
-    for (uint32_t i = 0; i < (NQ + PW - 1) / PW; ++i) {
-        const uint32_t k = w + PW * i, t = 4 * k + ln / 16;
-        if (NQ % PW == 0 || k < NQ)
-            lds_load16(base + L::QS + 1024 * k, rq, (tb + t) * 256 + 16 * ((ln & 15) ^ (t & 15)));
+    const v4i rq = rs4(a.qs, a.M * a.K);
+    each_inst<TT / 4>(w, [&](uint32_t k) {
+        const uint32_t t = 4 * k + ln / 16;
+        lds_load16(base + L::QS + 1024 * k, rq, (tb + t) * 256 + 16 * ((ln & 15) ^ (t & 15)));
+    });
+    const v4i rx = rs4(a.xs, a.M * a.nblk * T::XB);
+    if constexpr (TYPE == kQ4_K) {
+        each_inst<TT / 16>(w, [&](uint32_t k) { lds_load4(base + L::XS + 256 * k, rx, (tb + 16 * k) * 16 + 4 * ln); });
+        const v4i rd = rs4(a.d8, a.M * a.nblk * 4);
+        each_inst<(TT + 63) / 64>(w, [&](uint32_t k) { lds_load4(base + L::D8 + 256 * k, rd, (tb + 64 * k + ln) * 4); });
+    } else {
+        each_inst<TT * T::XB / 1024>(w, [&](uint32_t k) {
+            lds_load16(base + L::XS + 1024 * k, rx, tb * T::XB + 1024 * k + 16 * ln);
+        });
     }
-    // digit sums: 256 bytes (16 tokens) per instruction; scales: 64 tokens
-#pragma unroll
-    for (uint32_t i = 0; i < (NG + PW - 1) / PW; ++i) {
-        const uint32_t k = w + PW * i;
-        if (NG % PW == 0 || k < NG) lds_load4(base + L::DG + 256 * k, rg, (tb + 16 * k) * 16 + 4 * ln);
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < (ND + PW - 1) / PW; ++i) {
-        const uint32_t k = w + PW * i;
-        if (ND % PW == 0 || k < ND) lds_load4(base + L::D8 + 256 * k, rd, (tb + 64 * k + ln) * 4);
-    }
-}
-
-// Superblock b of the tile's weight rows into LDS, [row][144] (9 16-byte
-// chunks per row; a wave instruction covers 64 consecutive chunks, so its
-// loads fall on 7-8 consecutive rows: whole cache lines). Rows past N lie
-// outside the descriptor and load zeros.
-template <int NT>
-__device__ __forceinline__ void w_to_lds(const v4i wrs, uint32_t row_bytes,
-                                         uint32_t n0, uint32_t b, unsigned char *buf, uint32_t w, uint32_t lane) {
-    using L = PLds<NT>;
-    constexpr uint32_t NC = PR * 9 / 64;  // wave instructions per superblock
-    const uint32_t base = lds_addr(buf) + L::W;
-    uint32_t ln = lane;
-    asm volatile("" : "+v"(ln));
-#pragma unroll
-    for (uint32_t i = 0; i < (NC + PW - 1) / PW; ++i) {
-        const uint32_t k = w + PW * i;
-        if (NC % PW == 0 || k < NC) {
-            const uint32_t c = 64 * k + ln, r = c / 9, p = c - 9 * r;
-            lds_load16(base + 1024 * k, wrs, (n0 + r) * row_bytes + b * 144 + 16 * p);
-        }
-    }
-}
-
-// One 32-token block t of the tile against this wave's converted weights.
-// The hi and lo chains run interleaved as two independent accumulators (no
-// MFMA waits on the previous one's result), C = 8*hi + lo after both; the
-// min term's high-digit MFMA is issued first so that its shift overlaps the
-// chains.
-template <int NT>
-__device__ __forceinline__ void q4_block(const unsigned char *buf, const Q4Frag &f, uint32_t t, uint32_t j,
-                                         uint32_t g, float (&acc)[16]) {
-    using L = PLds<NT>;
-    const unsigned char *arow = buf + L::QS + (32 * t + j) * 256;
-    const v4i dgv = as_v4i(lds4(buf + L::DG + (32 * t + j) * 16));
-    // high digits in bytes 0-7 against the mins; then the low digits moved there
-    v16i mn = mfma(dgv, f.m, v16i{});
-    v16i ch = {}, cl = {};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const v4i af = as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-        ch = mfma(af, f.bh[s], ch);
-        cl = mfma(af, f.bl[s], cl);
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mn[r] <<= 7;
-    mn = mfma(v4i{dgv.z, dgv.w, dgv.z, dgv.w}, f.m, mn);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) ch[r] = (ch[r] << 3) + cl[r];
-    const float *d8 = reinterpret_cast<const float *>(buf + L::D8) + 32 * t + 4 * g;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float4 dv = *reinterpret_cast<const float4 *>(d8 + 8 * q);
-        const float dd[4] = {dv.x, dv.y, dv.z, dv.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 4 * q + e;
-            acc[r] = fmaf(dd[e], fmaf(f.d, float(ch[r]), -f.dm * float(mn[r])), acc[r]);
-        }
-    }
+    constexpr uint32_t CPR = T::UB / 16;  // 16-byte chunks per row
+    const v4i rw = rs4(a.W, a.N * a.row_bytes);
+    each_inst<T::PR * CPR / 64>(w, [&](uint32_t k) {
+        const uint32_t c = 64 * k + ln, r = c / CPR, p = c - CPR * r;
+        lds_load16(base + L::W + 1024 * k, rw, (n0 + r) * a.row_bytes + b * T::UB + 16 * p);
+    });
 }
 
 __host__ __device__ inline uint32_t sk_begin(uint32_t units, uint32_t grid, uint32_t v) {
@@ -286,20 +356,21 @@ __device__ __forceinline__ uint32_t sk_logical(uint32_t bid, uint32_t G) {
     return (G & 7) ? bid : (bid & 7) * (G >> 3) + (bid >> 3);
 }
 
-template <int NT>
-__global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_q4k(PfArgs a) {
+template <int TYPE, int NT>
+__global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_prefill(PfArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
-    using L = PLds<NT>;
-    constexpr uint32_t TT = L::TT;
+    using L = PLds<TYPE, NT>;
+    using T = PfType<TYPE>;
+    constexpr uint32_t TT = L::TT, PR = T::PR;
+    constexpr uint32_t RG = PW / T::TSPLIT;       // row groups of 32
+    constexpr int NB = NT / int(T::TSPLIT);       // 32-token blocks per wave
+    static_assert(NB >= 1, "at least one token block per wave");
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t rg = w % RG, tg = w / RG;      // row group, token group
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
-    const v4i wrs = rs4(a.W, a.N * a.row_bytes);
 
     const uint32_t v = sk_logical(blockIdx.x, a.G);
-#ifdef TC_PF_TRACE
-    unsigned long long twait = 0, tconv = 0, tblk = 0, tgap = 0, ts3p = 0, tstore = 0, tstart = __builtin_readcyclecounter();
-#endif
     const uint32_t units = a.ntiles * a.nblk;
     const uint32_t ub = sk_begin(units, a.G, v), ue = sk_begin(units, a.G, v + 1);
     for (uint32_t u = ub; u < ue;) {
@@ -317,102 +388,85 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const uint32_t j = ln & 31, g = ln >> 5;
         const uint32_t tn = tile % a.ntn, tm = tile / a.ntn;
         const uint32_t n0 = tn * PR, m0 = tm * TT;
+        const uint32_t rl = 32 * rg + j;  // the lane's row in the tile
 
-        float acc[NT][16];
+        float acc[NB][16];
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+        for (int t = 0; t < NB; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
         // Previous segment's readers of both buffers are done.
         __syncthreads();
-        Q4Frag f;
-        act_to_lds<NT>(a, m0, b0, buf(b0), w, lane);
-        w_to_lds<NT>(wrs, a.row_bytes, n0, b0, buf(b0), w, lane);
-        // Per superblock: its activations and weight blocks are waited for,
-        // the next superblock's loads issued into the other LDS buffer, this
-        // lane's weights converted, then the MFMAs.
+        stage<TYPE, NT>(a, m0, n0, b0, buf(b0), w, lane);
+        // Per superblock: its loads are waited for, the next superblock's
+        // issued into the other LDS buffer, this lane's weights converted,
+        // then the MFMAs.
         for (uint32_t b = b0; b < b1; ++b) {
-#ifdef TC_PF_TRACE
-            const unsigned long long ts0 = __builtin_readcyclecounter();
-            if (b > b0) tgap += ts0 - ts3p;
-#endif
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             __syncthreads();
-#ifdef TC_PF_TRACE
-            const unsigned long long ts1 = __builtin_readcyclecounter();
-#endif
-            act_to_lds<NT>(a, m0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
-            w_to_lds<NT>(wrs, a.row_bytes, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
-            {
-                Q4Raw rr;
-                q4_read(rr, buf(b) + L::W + (32 * w + j) * 144, g);
-                q4_convert(rr, g, f);
-            }
-#ifdef TC_PF_TRACE
-            const unsigned long long ts2 = __builtin_readcyclecounter();
-#endif
+            stage<TYPE, NT>(a, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
+            const unsigned char *bb = buf(b);
+            if constexpr (TYPE == kQ4_K) {
+                Q4Frag f;
+                {
+                    Q4Raw rr;
+                    q4_read(rr, bb + L::W + rl * T::UB, g);
+                    q4_convert(rr, g, f);
+                }
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                // one token block at a time in the scheduler's window (it
-                // would otherwise hoist every block's operand reads)
-                __builtin_amdgcn_sched_barrier(0);
-                q4_block<NT>(buf(b), f, t, j, g, acc[t]);
+                for (int t = 0; t < NB; ++t) {
+                    // one token block at a time in the scheduler's window (it
+                    // would otherwise hoist every block's operand reads)
+                    __builtin_amdgcn_sched_barrier(0);
+                    const uint32_t tok = 32 * (tg * NB + t) + j;
+                    q4_block(bb + L::QS + tok * 256, bb + L::XS + tok * 16,
+                             reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g, f, j, g,
+                             acc[t]);
+                }
+            } else {
+                Q8Frag f;
+                q8_convert(bb + L::W + rl * T::UB, g, f);
+#pragma unroll
+                for (int t = 0; t < NB; ++t) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    const uint32_t tok = 32 * (tg * NB + t) + j;
+                    q8_block(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB, f, j, g, acc[t]);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
-#ifdef TC_PF_TRACE
-            {
-                const unsigned long long ts3 = __builtin_readcyclecounter();
-                twait += ts1 - ts0;
-                tconv += ts2 - ts1;
-                tblk += ts3 - ts2;
-                ts3p = ts3;
-            }
-#endif
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // nothing of this segment left in flight
 
-#ifdef TC_PF_TRACE
-        const unsigned long long tsst = __builtin_readcyclecounter();
-#endif
-        // lane: row n0 + 32w + j, tokens m0 + 32t + 8q + 4g + e
-        const uint32_t nl = 32 * w + j, n = n0 + nl;
+        // lane: row n0 + rl, tokens m0 + 32 (tg NB + t) + 8q + 4g + e
+        const uint32_t n = n0 + rl;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
+        for (int t = 0; t < NB; ++t) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t ml = 32 * t + 8 * q + 4 * g + e, m = m0 + ml;
+                    const uint32_t ml = 32 * (tg * NB + t) + 8 * q + 4 * g + e, m = m0 + ml;
                     const float val = acc[t][4 * q + e];
                     if (part != nullptr)
-                        part[ml * PR + nl] = val;
+                        part[ml * PR + rl] = val;
                     else if (m < a.M && n < a.N)
                         a.out[size_t(m) * a.N + n] = val;
                 }
             }
         }
-#ifdef TC_PF_TRACE
-        tstore += __builtin_readcyclecounter() - tsst;
-#endif
     }
-#ifdef TC_PF_TRACE
-    if (lane == 0) {
-        unsigned long long *tr = a.trace + (size_t(blockIdx.x) * PW + w) * 8;
-        tr[0] = twait; tr[1] = tconv; tr[2] = tblk; tr[3] = tgap; tr[4] = tstore;
-        tr[5] = __builtin_readcyclecounter() - tstart;
-    }
-#endif
 }
 
 // Tiles split over several workgroups: out = the partial segments summed in
 // workgroup (range) order. kFix workgroups per split tile, each a slice of
 // it; group j takes the tile holding range boundary j + 1 when that boundary
-// splits it and is the first to do so.
+// splits it and is the first to do so. (Summing inside the main kernel, by
+// the last contributor to arrive, measured slower: its device-scope release
+// and acquire around the partial tiles cost more than this launch.)
 constexpr uint32_t kFix = 4;
-template <int NT>
+template <uint32_t TT, uint32_t PR>
 __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
-    constexpr uint32_t TT = PLds<NT>::TT;
     const uint32_t units = a.ntiles * a.nblk, G = a.G;
     const uint32_t slice = blockIdx.x % kFix;
     const uint32_t wb = blockIdx.x / kFix + 1, ubd = sk_begin(units, G, wb);
@@ -465,20 +519,26 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
     }
 }
 
-// Token-tile width from M (reference GemmDispatch.cu:634-643 picks its tile
-// from seqLen too): the smallest of 32, 64, 128 tokens that holds M, else 256.
-int pf_nt(uint32_t M) { return M <= 32 ? 1 : M <= 64 ? 2 : 4; }
+// Token-tile width from M (the reference picks its tile from seqLen too,
+// GemmDispatch.cu:634-643): the smallest of 32, 64, 128 tokens that holds M,
+// else 128 (Q8_0: 64 or 128, as its waves split the tile's tokens in two).
+int pf_nt(int type, uint32_t M) {
+    const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
+    return type == kQ8_0 ? std::max(nt, 2) : nt;
+}
+uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }
 
 struct PfGeom {
     int nt;
-    uint32_t tt, ntm, ntn, ntiles, G;
+    uint32_t tt, pr, ntm, ntn, ntiles, G;
 };
-PfGeom pf_geom(uint32_t M, uint32_t N, uint32_t K, int num_cu) {
+PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     PfGeom g;
-    g.nt = pf_nt(M);
+    g.nt = pf_nt(type, M);
     g.tt = 32u * g.nt;
+    g.pr = pf_rows(type);
     g.ntm = (M + g.tt - 1) / g.tt;
-    g.ntn = (N + PR - 1) / PR;
+    g.ntn = (N + g.pr - 1) / g.pr;
     g.ntiles = g.ntm * g.ntn;
     const uint64_t units = uint64_t(g.ntiles) * (K / 256);
     // one workgroup per CU, each with at least 2 superblocks of work
@@ -486,34 +546,31 @@ PfGeom pf_geom(uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     return g;
 }
 
-template <int NT>
+template <int TYPE, int NT>
 hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_pf_q4k<NT>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    using L = PLds<TYPE, NT>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_prefill<TYPE, NT>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 2 * L::bytes);
     if (attr != hipSuccess) return attr;
-    k_pf_q4k<NT><<<dim3{a.G, 1u, 1u}, 64 * PW, 2 * PLds<NT>::bytes, st>>>(a);
+    k_prefill<TYPE, NT><<<dim3{a.G, 1u, 1u}, 64 * PW, 2 * L::bytes, st>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t units = a.ntiles * a.nblk;
     bool split = false;
     for (uint32_t v = 1; v < a.G && !split; ++v) split = sk_begin(units, a.G, v) % a.nblk != 0;
     if (!split) return hipSuccess;
-    k_pf_fixup<NT><<<dim3{(a.G - 1) * kFix, 1u, 1u}, 256, 0, st>>>(a);
+    k_pf_fixup<L::TT, PfType<TYPE>::PR><<<dim3{(a.G - 1) * kFix, 1u, 1u}, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
 }  // namespace
 
-#ifdef TC_PF_TRACE
-void *tc_pf_trace_buf = nullptr;
-extern "C" void tc_pf_set_trace(void *p) { tc_pf_trace_buf = p; }
-#endif
-bool prefill_type(int type) { return type == kQ4_K; }
+bool prefill_type(int type) { return type == kQ4_K || type == kQ8_0; }
 
 size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     if (!prefill_type(type)) return 0;
-    const PfGeom g = pf_geom(M, N, K, num_cu);
-    return size_t(g.G) * 2 * g.tt * PR * 4;
+    const PfGeom g = pf_geom(type, M, N, K, num_cu);
+    return size_t(g.G) * 2 * g.tt * g.pr * 4;
 }
 
 hipError_t launch_prefill(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N,
@@ -522,12 +579,12 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
         return hipErrorInvalidValue;
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
-    const PfGeom g = pf_geom(M, N, K, num_cu);
+    const PfGeom g = pf_geom(type, M, N, K, num_cu);
     PfArgs a{};
     a.W = static_cast<const uint8_t *>(W);
     a.qs = act.qs;
     a.d8 = act.d;
-    a.dg = act.dg;
+    a.xs = act.dg;
     a.out = out;
     a.ws = static_cast<float *>(workspace);
     a.M = M;
@@ -539,13 +596,11 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
     a.ntn = g.ntn;
     a.ntiles = g.ntiles;
     a.G = g.G;
-#ifdef TC_PF_TRACE
-    a.trace = static_cast<unsigned long long *>(tc_pf_trace_buf);
-#endif
+    if (type == kQ8_0) return g.nt == 2 ? pf_launch<kQ8_0, 2>(a, st) : pf_launch<kQ8_0, 4>(a, st);
     switch (g.nt) {
-        case 1: return pf_launch<1>(a, st);
-        case 2: return pf_launch<2>(a, st);
-        default: return pf_launch<4>(a, st);
+        case 1: return pf_launch<kQ4_K, 1>(a, st);
+        case 2: return pf_launch<kQ4_K, 2>(a, st);
+        default: return pf_launch<kQ4_K, 4>(a, st);
     }
 }
 

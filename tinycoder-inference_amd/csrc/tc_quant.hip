@@ -80,8 +80,8 @@ __global__ __launch_bounds__(256) void k_quant_q8k_rows(const float *__restrict_
 // blocks, loads first as in k_quant_q8k.
 template <int BPW>
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int8_t *__restrict__ qs,
-                                                    float *__restrict__ d, uint32_t ngroups, uint32_t nbk,
-                                                    uint32_t bm_S) {
+                                                    float *__restrict__ d, uint16_t *__restrict__ dp,
+                                                    uint32_t ngroups, uint32_t nbk, uint32_t bm_S) {
     const uint32_t g0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW;
     if (g0 >= ngroups) return;
     const uint32_t lane = threadIdx.x & 63;
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x,
         const uint32_t g = g0 + i;
         if (g >= ngroups) break;  // wave-uniform
         const uint32_t o = act_dst_block(g, nbk, bm_S);
-        quant_q8_0_blocks_wave_v(v[i], qs + size_t(o) * 256, d + size_t(o) * 8);
+        quant_q8_0_blocks_wave_v(v[i], qs + size_t(o) * 256, d + size_t(o) * 8, dp + size_t(o) * 32);
     }
 }
 
@@ -810,9 +810,10 @@ hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols
     int8_t *qs = reinterpret_cast<int8_t *>(static_cast<char *>(buf) + L.qs_off);
     float *d = reinterpret_cast<float *>(static_cast<char *>(buf) + L.d_off);
     if (wtype == kQ8_0) {
+        uint16_t *dp = reinterpret_cast<uint16_t *>(static_cast<char *>(buf) + L.dg_off);
         const uint32_t ng = S * (cols / 256);
-        if (ng >= 131072) k_quant_q8_0<4><<<(ng + 15) / 16, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
-        else k_quant_q8_0<1><<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, ng, nbk, bm_S);
+        if (ng >= 131072) k_quant_q8_0<4><<<(ng + 15) / 16, 256, 0, st>>>(x, qs, d, dp, ng, nbk, bm_S);
+        else k_quant_q8_0<1><<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, dp, ng, nbk, bm_S);
     } else {
         int16_t *bs = reinterpret_cast<int16_t *>(static_cast<char *>(buf) + L.bs_off);
         int8_t *dg = reinterpret_cast<int8_t *>(static_cast<char *>(buf) + L.dg_off);
