@@ -377,7 +377,7 @@ def moe_prefill_bench(torch, tc, tc_hip, dev, reps):
     at the config-5 expert shapes: T tokens x top-8, routed on the device,
     each matrix one grouped int8 MFMA GEMM over all experts ("gemm"); beside
     it the per-(token, rank) mat-vec path ("pairs") on the same inputs (the
-    library takes the GEMM from 160 tokens). TOPS = 2 * T * 8 *
+    library takes the GEMM from 40 tokens). TOPS = 2 * T * 8 *
     3 * 768 * 2048 int8 ops / time (the whole FFN, router and combine
     included)."""
     E, K, H, FF = 128, 8, 2048, 768
@@ -402,7 +402,7 @@ def moe_prefill_bench(torch, tc, tc_hip, dev, reps):
             tc.lib.tc_moe_set_gemm_min_tokens(thr)
             us = timed(torch, lambda i: tc.moe_ffn(x, idd, wd_, wg, wu, wd, E, H, FF, out=out), reps)
             row[name] = {"us": round(us, 1), "TOPS": round(ops / us / 1e6, 1)}
-        tc.lib.tc_moe_set_gemm_min_tokens(160)
+        tc.lib.tc_moe_set_gemm_min_tokens(40)
         res.append(row)
     del wg, wu, wd
     torch.cuda.empty_cache()

@@ -155,7 +155,7 @@ def test_moe_full_config(tc, dev, oracle, S):
 
 # ---- grouped path: device-side routing + one grouped MFMA GEMM per matrix ----------
 
-GEMM_MIN = 160  # the library's default
+GEMM_MIN = 40  # the library's default
 
 
 @pytest.fixture

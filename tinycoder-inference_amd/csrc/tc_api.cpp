@@ -514,11 +514,11 @@ int tc_encode(int type, const float *x, void *out, uint32_t rows, uint32_t cols,
 namespace {
 
 // Token count from which tc_moe_ffn runs the grouped GEMM. Below it the
-// per-pair mat-vecs win: at these sizes every expert sits in the Infinity
-// Cache and the mat-vec work, not HBM, sets the time, while the GEMM pays
-// for whole 128-row token tiles per expert (measured crossover 128-256
-// tokens for 128 experts x top-8).
-uint32_t g_moe_gemm_min_tokens = 160;
+// per-pair mat-vecs win: the GEMM path's eight launches cost more than the
+// mat-vecs' work at a few (token, rank) pairs per expert. Measured for 128
+// experts x top-8 (2048 x 768 experts): 16 tokens 106 us grouped vs 49 us
+// pairs, 64 tokens 151 vs 187 us.
+uint32_t g_moe_gemm_min_tokens = 40;
 
 // MoE prefill over expert-sorted rows: device-side routing, the grouped Q4_K
 // MFMA GEMM for gate and up (one launch each over all experts), SwiGLU, the
@@ -527,11 +527,12 @@ int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wt
                 const void *wg, const void *wu, const void *wd, uint32_t E, uint32_t H, uint32_t FF, float *out,
                 hipStream_t st) {
     const uint32_t P = T * top_k;
-    const uint32_t ntm_max = tc::moe_max_tiles(P, E, 128);
+    const uint32_t tile = tc::prefill_grouped_tile(P, E);
+    const uint32_t ntm_max = tc::moe_max_tiles(P, E, tile);
     auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
     const tc::ActLayout LX = tc::act_layout(TC_Q4_K, P, H), LH = tc::act_layout(TC_Q4_K, P, FF);
-    const size_t ws = std::max(tc::gemm_grouped_workspace_bytes(ntm_max, FF, H, dev->num_cu),
-                               tc::gemm_grouped_workspace_bytes(ntm_max, H, FF, dev->num_cu));
+    const size_t ws = std::max(tc::prefill_grouped_workspace_bytes(tile, ntm_max, FF, H, dev->num_cu),
+                               tc::prefill_grouped_workspace_bytes(tile, ntm_max, H, FF, dev->num_cu));
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -551,20 +552,21 @@ int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wt
     float *y = reinterpret_cast<float *>(b + o_y);
     const uint64_t gstride = uint64_t(FF) * (H / 256) * 144, dstride = uint64_t(H) * (FF / 256) * 144;
 
-    hipError_t e = tc::launch_moe_route(ids, P, top_k, E, 1, 128, pos, tok, mt, ntm, st);
+    hipError_t e = tc::launch_moe_route(ids, P, top_k, E, 1, tile, pos, tok, mt, ntm, st);
     if (e != hipSuccess) return hip_fail(e, "MoE router");
     e = tc::launch_quant_act_rows(x, tok, P, H, LX, b + o_ax, st);
     if (e != hipSuccess) return hip_fail(e, "MoE activation gather");
     const tc::ActView ax = act_view(b + o_ax, LX, 0, TC_Q4_K, H);
-    e = tc::launch_gemm_grouped(wg, gstride, ax, g, P, FF, H, mt, ntm, ntm_max, dev->num_cu, b + o_ws, st);
+    e = tc::launch_prefill_grouped(wg, gstride, ax, g, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, b + o_ws, st);
     if (e == hipSuccess)
-        e = tc::launch_gemm_grouped(wu, gstride, ax, u, P, FF, H, mt, ntm, ntm_max, dev->num_cu, b + o_ws, st);
+        e = tc::launch_prefill_grouped(wu, gstride, ax, u, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, b + o_ws,
+                                       st);
     if (e != hipSuccess) return hip_fail(e, "MoE gate/up GEMM");
     e = tc::launch_moe_swiglu(g, u, P, FF, st);
     if (e == hipSuccess) e = tc::launch_quant_act(TC_Q4_K, g, P, FF, LH, b + o_ah, st, true);
     if (e != hipSuccess) return hip_fail(e, "MoE SwiGLU");
     const tc::ActView ah = act_view(b + o_ah, LH, 0, TC_Q4_K, FF);
-    e = tc::launch_gemm_grouped(wd, dstride, ah, y, P, H, FF, mt, ntm, ntm_max, dev->num_cu, b + o_ws, st);
+    e = tc::launch_prefill_grouped(wd, dstride, ah, y, P, H, FF, mt, ntm, ntm_max, tile, dev->num_cu, b + o_ws, st);
     if (e != hipSuccess) return hip_fail(e, "MoE down GEMM");
     e = tc::launch_moe_combine_rows(y, pos, wts, out, T, top_k, H, st);
     if (e != hipSuccess) return hip_fail(e, "MoE combine");

@@ -89,6 +89,15 @@ size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int
 hipError_t launch_prefill(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N,
                           uint32_t K, int num_cu, void *workspace, hipStream_t st);
 
+// Grouped (MoE) form over expert-sorted rows: out[i][n] = act row i . W[e(i)]
+// row n for the token tiles of mt (count *ntm, at most ntm_max; tiles of at
+// most `tile` rows, tile from prefill_grouped_tile).
+uint32_t prefill_grouped_tile(uint32_t rows_total, uint32_t n_experts);
+size_t prefill_grouped_workspace_bytes(uint32_t tile, uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu);
+hipError_t launch_prefill_grouped(const void *W, uint64_t wstride, const ActView &act, float *out,
+                                  uint32_t rows_total, uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm,
+                                  uint32_t ntm_max, uint32_t tile, int num_cu, void *workspace, hipStream_t st);
+
 // ---- MoE prefill over expert-sorted rows ----
 // Device-side router: pairs p = t*top_k + r (ids[p] in [0, E), others
 // skipped) sorted by expert; each expert's segment starts at a multiple of

@@ -106,7 +106,43 @@ struct PfArgs {
     uint32_t row_bytes, nblk;
     uint32_t ntm, ntn, ntiles;  // token tiles, row blocks, tiles
     uint32_t G;                 // workgroups
+    // Grouped (MoE) mode: token tile i covers rows [mt[3i], mt[3i+1]) of the
+    // expert-sorted activations and uses expert mt[3i+2]'s matrix at W +
+    // expert * wstride; the tile count is read from *ntm_dev (written on the
+    // device by the router).
+    const uint32_t *mt;
+    const uint32_t *ntm_dev;
+    uint64_t wstride;
 };
+
+// A tile's token rows [m0, mend) and weight matrix.
+struct PfTile {
+    uint32_t m0, mend, n0;
+    const uint8_t *W;
+};
+template <bool GRP>
+__device__ __forceinline__ PfTile pf_tile(const PfArgs &a, uint32_t tile, uint32_t TT, uint32_t PR) {
+    const uint32_t tn = tile % a.ntn, tm = tile / a.ntn;
+    PfTile t;
+    t.n0 = tn * PR;
+    if constexpr (GRP) {
+        t.m0 = a.mt[3 * tm];
+        t.mend = a.mt[3 * tm + 1];
+        t.W = a.W + uint64_t(a.mt[3 * tm + 2]) * a.wstride;
+    } else {
+        t.m0 = tm * TT;
+        t.mend = a.M;
+        t.W = a.W;
+    }
+    return t;
+}
+template <bool GRP>
+__device__ __forceinline__ uint32_t pf_ntiles(const PfArgs &a) {
+    if constexpr (GRP)
+        return *a.ntm_dev * a.ntn;
+    else
+        return a.ntiles;
+}
 
 __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
@@ -315,8 +351,8 @@ __device__ __forceinline__ void each_inst(uint32_t w, F &&f) {
 // rows: whole cache lines). Tokens past M read other tokens' bytes or zeros
 // and rows past N lie outside the descriptor (zeros); neither is stored.
 template <int TYPE, int NT>
-__device__ __forceinline__ void stage(const PfArgs &a, uint32_t m0, uint32_t n0, uint32_t b, unsigned char *buf,
-                                      uint32_t w, uint32_t lane) {
+__device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_t m0, uint32_t n0, uint32_t b,
+                                      unsigned char *buf, uint32_t w, uint32_t lane) {
     using L = PLds<TYPE, NT>;
     using T = PfType<TYPE>;
     constexpr uint32_t TT = L::TT;
@@ -340,7 +376,7 @@ __device__ __forceinline__ void stage(const PfArgs &a, uint32_t m0, uint32_t n0,
         });
     }
     constexpr uint32_t CPR = T::UB / 16;  // 16-byte chunks per row
-    const v4i rw = rs4(a.W, a.N * a.row_bytes);
+    const v4i rw = rs4(W, a.N * a.row_bytes);
     each_inst<T::PR * CPR / 64>(w, [&](uint32_t k) {
         const uint32_t c = 64 * k + ln, r = c / CPR, p = c - CPR * r;
         lds_load16(base + L::W + 1024 * k, rw, (n0 + r) * a.row_bytes + b * T::UB + 16 * p);
@@ -356,7 +392,7 @@ __device__ __forceinline__ uint32_t sk_logical(uint32_t bid, uint32_t G) {
     return (G & 7) ? bid : (bid & 7) * (G >> 3) + (bid >> 3);
 }
 
-template <int TYPE, int NT>
+template <int TYPE, int NT, bool GRP>
 __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_prefill(PfArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
     using L = PLds<TYPE, NT>;
@@ -371,7 +407,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
 
     const uint32_t v = sk_logical(blockIdx.x, a.G);
-    const uint32_t units = a.ntiles * a.nblk;
+    const uint32_t units = pf_ntiles<GRP>(a) * a.nblk;
     const uint32_t ub = sk_begin(units, a.G, v), ue = sk_begin(units, a.G, v + 1);
     for (uint32_t u = ub; u < ue;) {
         const uint32_t tile = u / a.nblk;
@@ -386,8 +422,8 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         uint32_t ln = lane;
         asm volatile("" : "+v"(ln));
         const uint32_t j = ln & 31, g = ln >> 5;
-        const uint32_t tn = tile % a.ntn, tm = tile / a.ntn;
-        const uint32_t n0 = tn * PR, m0 = tm * TT;
+        const PfTile tg_ = pf_tile<GRP>(a, tile, TT, PR);
+        const uint32_t n0 = tg_.n0, m0 = tg_.m0;
         const uint32_t rl = 32 * rg + j;  // the lane's row in the tile
 
         float acc[NB][16];
@@ -398,14 +434,14 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 
         // Previous segment's readers of both buffers are done.
         __syncthreads();
-        stage<TYPE, NT>(a, m0, n0, b0, buf(b0), w, lane);
+        stage<TYPE, NT>(a, tg_.W, m0, n0, b0, buf(b0), w, lane);
         // Per superblock: its loads are waited for, the next superblock's
         // issued into the other LDS buffer, this lane's weights converted,
         // then the MFMAs.
         for (uint32_t b = b0; b < b1; ++b) {
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             __syncthreads();
-            stage<TYPE, NT>(a, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
+            stage<TYPE, NT>(a, tg_.W, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
             const unsigned char *bb = buf(b);
             if constexpr (TYPE == kQ4_K) {
                 Q4Frag f;
@@ -450,7 +486,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     const float val = acc[t][4 * q + e];
                     if (part != nullptr)
                         part[ml * PR + rl] = val;
-                    else if (m < a.M && n < a.N)
+                    else if (m < tg_.mend && n < a.N)
                         a.out[size_t(m) * a.N + n] = val;
                 }
             }
@@ -465,20 +501,21 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 // the last contributor to arrive, measured slower: its device-scope release
 // and acquire around the partial tiles cost more than this launch.)
 constexpr uint32_t kFix = 4;
-template <uint32_t TT, uint32_t PR>
+template <uint32_t TT, uint32_t PR, bool GRP>
 __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
-    const uint32_t units = a.ntiles * a.nblk, G = a.G;
+    const uint32_t ntiles = pf_ntiles<GRP>(a);
+    const uint32_t units = ntiles * a.nblk, G = a.G;
     const uint32_t slice = blockIdx.x % kFix;
     const uint32_t wb = blockIdx.x / kFix + 1, ubd = sk_begin(units, G, wb);
     const uint32_t tile = ubd / a.nblk;
     if (ubd % a.nblk == 0 || sk_begin(units, G, wb - 1) > tile * a.nblk) return;
-    if (tile >= a.ntiles) return;
+    if (tile >= ntiles) return;
     const uint32_t t0 = tile * a.nblk, t1 = t0 + a.nblk;
     uint32_t v = uint32_t(uint64_t(t0) * G / units);
     while (v + 1 < G && sk_begin(units, G, v + 1) <= t0) ++v;
     while (v > 0 && sk_begin(units, G, v) > t0) --v;
-    const uint32_t tn = tile % a.ntn, tm = tile / a.ntn;
-    const uint32_t n0 = tn * PR, m0 = tm * TT;
+    const PfTile tg_ = pf_tile<GRP>(a, tile, TT, PR);
+    const uint32_t n0 = tg_.n0, m0 = tg_.m0;
     constexpr uint32_t per = TT * PR / 4 / kFix;  // float4 entries per slice
     constexpr uint32_t NI = per / 256;
     static_assert(per % 256 == 0, "a fixup slice is a whole number of 256-thread rounds");
@@ -506,7 +543,7 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
         const uint32_t i = slice * per + k * 256 + threadIdx.x;
         const uint32_t ml = (4 * i) / PR, nl = (4 * i) % PR;
         const uint32_t m = m0 + ml, n = n0 + nl;
-        if (m >= a.M) continue;
+        if (m >= tg_.mend) continue;
         float *o = a.out + size_t(m) * a.N + n;
         const float sv[4] = {s[k].x, s[k].y, s[k].z, s[k].w};
         if (n + 3 < a.N && (a.N & 3) == 0) {
@@ -546,20 +583,22 @@ PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     return g;
 }
 
-template <int TYPE, int NT>
+template <int TYPE, int NT, bool GRP = false>
 hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
     using L = PLds<TYPE, NT>;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_prefill<TYPE, NT>),
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_prefill<TYPE, NT, GRP>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 2 * L::bytes);
     if (attr != hipSuccess) return attr;
-    k_prefill<TYPE, NT><<<dim3{a.G, 1u, 1u}, 64 * PW, 2 * L::bytes, st>>>(a);
+    k_prefill<TYPE, NT, GRP><<<dim3{a.G, 1u, 1u}, 64 * PW, 2 * L::bytes, st>>>(a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const uint32_t units = a.ntiles * a.nblk;
-    bool split = false;
-    for (uint32_t v = 1; v < a.G && !split; ++v) split = sk_begin(units, a.G, v) % a.nblk != 0;
-    if (!split) return hipSuccess;
-    k_pf_fixup<L::TT, PfType<TYPE>::PR><<<dim3{(a.G - 1) * kFix, 1u, 1u}, 256, 0, st>>>(a);
+    if (e != hipSuccess || a.G == 1) return e;
+    if (!GRP) {  // the split tiles are known on the host; grouped: only on the device
+        const uint32_t units = a.ntiles * a.nblk;
+        bool split = false;
+        for (uint32_t v = 1; v < a.G && !split; ++v) split = sk_begin(units, a.G, v) % a.nblk != 0;
+        if (!split) return hipSuccess;
+    }
+    k_pf_fixup<L::TT, PfType<TYPE>::PR, GRP><<<dim3{(a.G - 1) * kFix, 1u, 1u}, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -601,6 +640,58 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
         case 1: return pf_launch<kQ4_K, 1>(a, st);
         case 2: return pf_launch<kQ4_K, 2>(a, st);
         default: return pf_launch<kQ4_K, 4>(a, st);
+    }
+}
+
+// Grouped (MoE) mode: token-tile width from the average rows per expert.
+int pf_grouped_nt(uint32_t rows_total, uint32_t n_experts) {
+    const uint32_t avg = (rows_total + n_experts - 1) / n_experts;
+    return avg <= 32 ? 1 : avg <= 64 ? 2 : 4;
+}
+uint32_t prefill_grouped_tile(uint32_t rows_total, uint32_t n_experts) {
+    return 32u * pf_grouped_nt(rows_total, n_experts);
+}
+namespace {
+uint32_t pf_grouped_grid(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
+    const uint64_t units = uint64_t(ntm_max) * ((N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR) * (K / 256);
+    return uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(uint64_t(num_cu), units / 2)));
+}
+}  // namespace
+size_t prefill_grouped_workspace_bytes(uint32_t tile, uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
+    return size_t(pf_grouped_grid(ntm_max, N, K, num_cu)) * 2 * tile * PfType<kQ4_K>::PR * 4;
+}
+
+hipError_t launch_prefill_grouped(const void *W, uint64_t wstride, const ActView &act, float *out,
+                                  uint32_t rows_total, uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm,
+                                  uint32_t ntm_max, uint32_t tile, int num_cu, void *workspace, hipStream_t st) {
+    if (rows_total == 0 || N == 0 || K == 0 || K % 256 || ntm_max == 0 || workspace == nullptr || act.dg == nullptr)
+        return hipErrorInvalidValue;
+    const uint32_t ntn = (N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR;
+    if (uint64_t(rows_total) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * 144 >= (uint64_t(1) << 32) ||
+        uint64_t(ntm_max) * ntn * (K / 256) >= (uint64_t(1) << 32))
+        return hipErrorInvalidValue;
+    PfArgs a{};
+    a.W = static_cast<const uint8_t *>(W);
+    a.qs = act.qs;
+    a.d8 = act.d;
+    a.xs = act.dg;
+    a.out = out;
+    a.ws = static_cast<float *>(workspace);
+    a.M = rows_total;
+    a.N = N;
+    a.K = K;
+    a.nblk = K / 256;
+    a.row_bytes = a.nblk * 144;
+    a.ntn = ntn;
+    a.mt = mt;
+    a.ntm_dev = ntm;
+    a.wstride = wstride;
+    a.G = pf_grouped_grid(ntm_max, N, K, num_cu);
+    switch (tile) {
+        case 32: return pf_launch<kQ4_K, 1, true>(a, st);
+        case 64: return pf_launch<kQ4_K, 2, true>(a, st);
+        case 128: return pf_launch<kQ4_K, 4, true>(a, st);
+        default: return hipErrorInvalidValue;
     }
 }
 
