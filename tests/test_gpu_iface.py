@@ -148,15 +148,25 @@ def test_matMulVecBatchQ3K_residual_and_registered_weights(drv, tc, oracle):
     assert drv.drv_matMulVecBatch_SIMD(Q3_K, H(w), H(x), S, rows, cols, H(out), H(res)) == 1
     ok, worst = close(out, ref)
     assert ok, worst
+    # out and residual the same buffer (the reference's attnO in-place residual,
+    # SIMDMatMulVec.hpp:472-476): W.x + residual, the residual read before the
+    # output overwrites it
+    inplace = res.copy()
+    assert drv.drv_matMulVecBatch_SIMD(Q3_K, H(w), H(x), S, rows, cols, H(inplace), H(inplace)) == 1
+    ok, worst = close(inplace, ref)
+    assert ok, worst
     assert tc.lib.tc_host_weights_register(H(w), w.nbytes) == 0
     try:
-        # a sub-range of the registered matrix: rows 100..199
         rb = row_bytes(Q3_K, cols)
-        wsub = w[100 * rb:200 * rb]
-        out3 = np.zeros((S, 100), np.float32)
-        assert drv.drv_matMulVecBatch_SIMD(Q3_K, H(wsub), H(x), S, 100, cols, H(out3), None) == 1
-        ok, worst = close(out3, (ref - res)[:, 100:200])
-        assert ok, worst
+        # sub-ranges of the registered matrix: rows 100..199 (a 16-byte-aligned
+        # start) and rows 1..100 (1540-byte rows: the device copy's address is
+        # not 16-byte aligned, so the call stages the range instead)
+        for r0, nr in ((100, 100), (1, 100)):
+            wsub = w[r0 * rb:(r0 + nr) * rb]
+            out3 = np.zeros((S, nr), np.float32)
+            assert drv.drv_matMulVecBatch_SIMD(Q3_K, H(wsub), H(x), S, nr, cols, H(out3), None) == 1
+            ok, worst = close(out3, (ref - res)[:, r0:r0 + nr])
+            assert ok, (r0, worst)
         out2 = np.zeros((S, rows), np.float32)
         assert drv.drv_matMulVecBatch_SIMD(Q3_K, H(w), H(x), S, rows, cols, H(out2), None) == 1
         ok, worst = close(out2, ref - res)

@@ -840,8 +840,12 @@ const void *registered_copy(const void *p, size_t bytes) {
     const uint8_t *q = static_cast<const uint8_t *>(p);
     const int id = current_device();
     for (const HostRange &r : g_host_ranges)
-        if (r.device == id && q >= r.host && q + bytes <= r.host + r.bytes)
-            return static_cast<const uint8_t *>(r.dev) + (q - r.host);
+        if (r.device == id && q >= r.host && q + bytes <= r.host + r.bytes) {
+            const uint8_t *d = static_cast<const uint8_t *>(r.dev) + (q - r.host);
+            // The kernels take 16-byte-aligned weights; a sub-range starting
+            // elsewhere (e.g. row 1 of 1540-byte Q3_K rows) is staged instead.
+            return (reinterpret_cast<uintptr_t>(d) & 15) == 0 ? d : nullptr;
+        }
     return nullptr;
 }
 
@@ -911,10 +915,19 @@ int tc_host_matmul(int type, const uint8_t *W, const float *X, uint32_t seq_len,
                                 : tc_gemm(type, wd, xd, od, seq_len, rows, cols, cols / uint32_t(tc::block_elems(type)),
                                           nullptr);
     if (rc) return rc;
-    if (hipMemcpy(out, od, obytes, hipMemcpyDeviceToHost) != hipSuccess)
+    if (!residual) {
+        if (hipMemcpy(out, od, obytes, hipMemcpyDeviceToHost) != hipSuccess)
+            return fail(TC_E_LAUNCH, "output copy to host failed");
+        return TC_OK;
+    }
+    // out = dot + residual, as the reference's residual-fused store; out may
+    // be the residual buffer itself (the attnO in-place residual,
+    // SIMDMatMulVec.hpp:472-476), so the products land in a host buffer first
+    // and every residual value is read before its output is written.
+    std::vector<float> dot(size_t(seq_len) * rows);
+    if (hipMemcpy(dot.data(), od, obytes, hipMemcpyDeviceToHost) != hipSuccess)
         return fail(TC_E_LAUNCH, "output copy to host failed");
-    if (residual)  // out = dot + residual, as the reference's residual-fused store
-        for (size_t i = 0; i < size_t(seq_len) * rows; ++i) out[i] = out[i] + residual[i];
+    for (size_t i = 0; i < dot.size(); ++i) out[i] = dot[i] + residual[i];
     return TC_OK;
 }
 

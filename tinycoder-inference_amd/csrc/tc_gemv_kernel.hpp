@@ -1569,6 +1569,25 @@ uint32_t tlds_layout(int type, uint32_t S, uint32_t cols, TLaunchArgs *a) {
 // tc_gemv_inst.hip): the 512-thread shape when big, else the 256-thread one.
 template <int TYPE>
 hipError_t launch_type(bool big, uint32_t S, const TLaunchArgs &a, uint32_t grid, uint32_t lds, hipStream_t st);
+// The explicit specializations, one per type the Makefile builds
+// (GEMV_TYPES): declared here, so that every caller sees them before use.
+#define TC_GV_DECLARE(T) \
+    template <>          \
+    hipError_t launch_type<T>(bool big, uint32_t S, const TLaunchArgs &a, uint32_t grid, uint32_t lds, hipStream_t st);
+TC_GV_DECLARE(kQ5_0)
+TC_GV_DECLARE(kQ8_0)
+TC_GV_DECLARE(kQ2_K)
+TC_GV_DECLARE(kQ3_K)
+TC_GV_DECLARE(kQ4_K)
+TC_GV_DECLARE(kQ5_K)
+TC_GV_DECLARE(kQ6_K)
+TC_GV_DECLARE(kIQ2_XS)
+TC_GV_DECLARE(kIQ3_XXS)
+TC_GV_DECLARE(kIQ4_NL)
+TC_GV_DECLARE(kIQ3_S)
+TC_GV_DECLARE(kIQ2_S)
+TC_GV_DECLARE(kIQ4_XS)
+#undef TC_GV_DECLARE
 
 }  // namespace gv
 }  // namespace tc
