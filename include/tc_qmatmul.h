@@ -218,6 +218,14 @@ int tc_debug_q8_0_blocks(const uint8_t *w_row, uint32_t blocks_per_row, const fl
  * Calls are serialized by the library. */
 int tc_host_matmul(int type, const uint8_t *W, const float *X, uint32_t seq_len, uint32_t rows, uint32_t cols,
                    float *out, const float *residual);
+/* fp32 weights: out[s][j] = W[j] . X[s] over host pointers (W [rows][cols],
+ * X [seq_len][cols], out [seq_len][rows]), the boundary of the reference's
+ * matMulVecBatchF32_SIMD (include/SIMDMatMulVec.hpp:426; its one caller is
+ * the qwen35moe router). Each output is formed in the reference AVX2
+ * kernel's FMA order (SIMDMatMulVecAVX2.cpp:2982), so the results are its
+ * bits, as tc_moe_router's logits. W is read from a registered device copy
+ * as for tc_host_matmul. seq_len <= 65535. */
+int tc_host_matmul_f32(const float *W, const float *X, uint32_t seq_len, uint32_t rows, uint32_t cols, float *out);
 /* Keep a device copy of the host range [host, host + bytes) (weights that
  * later tc_host_matmul calls read); the copy is taken now, so later writes to
  * the host range are not seen until it is registered again. A copy belongs

@@ -1,5 +1,5 @@
 // tc_simd_matmul.hpp -- the reference's CPU mat-vec entry points
-// (namespace tinycoder, include/SIMDMatMulVec.hpp:448-584 of the reference)
+// (namespace tinycoder, include/SIMDMatMulVec.hpp:426-606 of the reference)
 // with the same names, arguments and bool result, backed by the gfx950
 // kernels of libtc_hip.so through tc_host_matmul (include/tc_qmatmul.h).
 //
@@ -20,6 +20,13 @@
 #include "tc_qmatmul.h"
 
 namespace tinycoder {
+
+/// fp32 weights, the router's F32 matrix (reference SIMDMatMulVec.hpp:426):
+/// the outputs carry the reference AVX2 kernel's bits (same FMA order).
+inline bool matMulVecBatchF32_SIMD(const float *W_f32, const float *X, uint32_t seqLen, uint32_t rows,
+                                   uint32_t cols, float *out) {
+    return tc_host_matmul_f32(W_f32, X, seqLen, rows, cols, out) == TC_OK;
+}
 
 /// Q4_K (reference SIMDMatMulVec.hpp:448).
 inline bool matMulVecBatchQ4K_SIMD(const uint8_t *W_q4k, const float *X, uint32_t seqLen, uint32_t rows,
@@ -62,6 +69,13 @@ inline bool matMulVecBatchIQ4NL_SIMD(const uint8_t *W_iq4nl, const float *X, uin
 inline bool matMulVecBatchQ8_0_SIMD(const uint8_t *W_q8_0, const float *X, uint32_t seqLen, uint32_t rows,
                                     uint32_t cols, float *out) {
     return tc_host_matmul(TC_Q8_0, W_q8_0, X, seqLen, rows, cols, out, nullptr) == TC_OK;
+}
+
+/// Compact Q2_K, i.e. raw 84-byte GGUF Q2_K blocks (reference
+/// SIMDMatMulVec.hpp:606, the re-quantized LM head).
+inline bool matMulVecBatchQ2K_Compact_SIMD(const uint8_t *W_q2k, const float *X, uint32_t seqLen, uint32_t rows,
+                                           uint32_t cols, float *out) {
+    return tc_host_matmul(TC_Q2_K, W_q2k, X, seqLen, rows, cols, out, nullptr) == TC_OK;
 }
 
 }  // namespace tinycoder

@@ -45,8 +45,14 @@ int drv_matMulVecBatch_SIMD(int type, const uint8_t *W, const float *X, uint32_t
         case TC_IQ4_XS: return tinycoder::matMulVecBatchIQ4XS_SIMD(W, X, seqLen, rows, cols, out);
         case TC_IQ4_NL: return tinycoder::matMulVecBatchIQ4NL_SIMD(W, X, seqLen, rows, cols, out);
         case TC_Q8_0: return tinycoder::matMulVecBatchQ8_0_SIMD(W, X, seqLen, rows, cols, out);
+        case TC_Q2_K: return tinycoder::matMulVecBatchQ2K_Compact_SIMD(W, X, seqLen, rows, cols, out);
         default: return 0;
     }
+}
+
+int drv_matMulVecBatchF32_SIMD(const float *W, const float *X, uint32_t seqLen, uint32_t rows, uint32_t cols,
+                               float *out) {
+    return tinycoder::matMulVecBatchF32_SIMD(W, X, seqLen, rows, cols, out);
 }
 
 }  // extern "C"

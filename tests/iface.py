@@ -16,6 +16,7 @@ SIGS = {
     "drv_int8Gemm": (_I, [_I, _P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "drv_int8GemvDual": (_I, [_I, _P, _P, _P, _P, _P, _U32, _U32, _P]),
     "drv_matMulVecBatch_SIMD": (_I, [_I, _P, _P, _U32, _U32, _U32, _P, _P]),
+    "drv_matMulVecBatchF32_SIMD": (_I, [_P, _P, _U32, _U32, _U32, _P]),
 }
 
 

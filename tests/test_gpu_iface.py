@@ -13,7 +13,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from qdata import IQ3_XXS, IQ4_NL, IQ4_XS, NAMES, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, row_bytes
+from qdata import IQ3_XXS, IQ4_NL, IQ4_XS, NAMES, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, close, gaussian, row_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -116,7 +116,7 @@ def test_int8GemvDual(drv, tc, dev, oracle, which, qt):
     assert ok, worst
 
 
-SIMD_TYPES = [Q4_K, Q3_K, Q6_K, Q5_K, IQ4_XS, IQ4_NL, Q8_0]
+SIMD_TYPES = [Q4_K, Q3_K, Q6_K, Q5_K, IQ4_XS, IQ4_NL, Q8_0, Q2_K]  # Q2_K: matMulVecBatchQ2K_Compact_SIMD
 
 
 @pytest.mark.parametrize("qt", SIMD_TYPES)
@@ -132,6 +132,20 @@ def test_matMulVecBatch_SIMD_host_pointers(drv, tc, oracle, qt, S):
     assert drv.drv_matMulVecBatch_SIMD(qt, H(w), H(x), S, rows, cols, H(out), None) == 1
     ok, worst = close(out, oracle.matmul(qt, w, x, rows, cols))
     assert ok, f"{NAMES[qt]} S={S}: {worst:.3g}"
+
+
+@pytest.mark.parametrize("S", [1, 16])
+def test_matMulVecBatchF32_SIMD_bits(drv, tc, oracle, S):
+    """The router's F32 entry point on host buffers: the reference AVX2
+    kernel's FMA order, so the oracle's bits (a width with a 4-column tail)."""
+    rng = np.random.default_rng(50 + S)
+    rows, cols = 128, 2052
+    w = (rng.standard_normal((rows, cols)) * 0.03).astype(np.float32)
+    x = rng.standard_normal((S, cols)).astype(np.float32)
+    out = np.full((S, rows), 7.0, np.float32)
+    assert drv.drv_matMulVecBatchF32_SIMD(H(w), H(x), S, rows, cols, H(out)) == 1
+    ref = oracle.matmul_f32(w, x, rows, cols)
+    assert (out.view(np.uint32) == np.ascontiguousarray(ref, np.float32).view(np.uint32)).all()
 
 
 def test_matMulVecBatchQ3K_residual_and_registered_weights(drv, tc, oracle):

@@ -931,6 +931,34 @@ int tc_host_matmul(int type, const uint8_t *W, const float *X, uint32_t seq_len,
     return TC_OK;
 }
 
+int tc_host_matmul_f32(const float *W, const float *X, uint32_t seq_len, uint32_t rows, uint32_t cols, float *out) {
+    Device *dev = device();
+    if (!dev) return fail(TC_E_UNSUPPORTED, "no gfx950 device");
+    if (!W || !X || !out) return fail(TC_E_ARG, "null pointer");
+    if (seq_len == 0 || rows == 0 || cols == 0) return fail(TC_E_UNSUPPORTED, "empty shape");
+    if (seq_len > 65535) return fail(TC_E_UNSUPPORTED, "seq_len=%u > 65535", seq_len);
+    const size_t wbytes = size_t(rows) * cols * 4, xbytes = size_t(seq_len) * cols * 4,
+                 obytes = size_t(seq_len) * rows * 4;
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    const void *wd = registered_copy(W, wbytes);
+    if (!wd) {
+        if (!ensure(g_hw.p, g_hw.cap, wbytes)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", wbytes);
+        if (hipMemcpy(g_hw.p, W, wbytes, hipMemcpyHostToDevice) != hipSuccess)
+            return fail(TC_E_LAUNCH, "weight copy to device failed");
+        wd = g_hw.p;
+    }
+    if (!ensure(g_hx.p, g_hx.cap, xbytes) || !ensure(g_ho.p, g_ho.cap, obytes))
+        return fail(TC_E_LAUNCH, "hipMalloc failed");
+    if (hipMemcpy(g_hx.p, X, xbytes, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(TC_E_LAUNCH, "activation copy to device failed");
+    hipError_t e = tc::launch_router_logits(static_cast<const float *>(wd), static_cast<const float *>(g_hx.p), seq_len,
+                                            rows, cols, static_cast<float *>(g_ho.p), nullptr);
+    if (e != hipSuccess) return hip_fail(e, "fp32 mat-vec");
+    if (hipMemcpy(out, g_ho.p, obytes, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(TC_E_LAUNCH, "output copy to host failed");
+    return TC_OK;
+}
+
 const char *tc_last_error(void) { return g_err.c_str(); }
 
 }  // extern "C"

@@ -49,6 +49,7 @@ SIGNATURES = {
     "tc_moe_router": (_I, [_P, _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P]),
     "tc_moe_select": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
     "tc_host_matmul": (_I, [_I, _P, _P, _U32, _U32, _U32, _P, _P]),
+    "tc_host_matmul_f32": (_I, [_P, _P, _U32, _U32, _U32, _P]),
     "tc_gemm_noalloc": (_I, [_I, _P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "tc_gemm_noalloc_scratch_bytes": (ctypes.c_size_t, []),
     "tc_host_weights_register": (_I, [_P, ctypes.c_size_t]),
