@@ -154,3 +154,34 @@ def test_gemm_refuses_bad_shapes(tc, dev):
     x = to_dev(np.zeros((3, 500), np.float32), dev)
     with pytest.raises(tc_hip.TCError):
         tc.gemm(Q4_K, w, x, 4, 500)
+
+
+def test_q80_minus128_true_product(tc, dev, oracle):
+    """Q8_0 weight bytes of -128 (never written by a quantizer: q =
+    round(w/d) with d = amax/127 stays in [-127, 127]): the GPU paths compute
+    the true product -128 * x. The reference AVX2 kernel's sign trick
+    (SIMDMatMulVecAVX2.cpp:4239-4383) cannot negate -128 and gives -128 * |x|
+    instead; the oracle mirrors that, so on such rows the two differ. Pins the
+    GPU's behaviour (mat-vec, the MFMA GEMM and the host entry point) against
+    the exact product from the reference's own activation quantization."""
+    rng = np.random.default_rng(128)
+    rows, cols = 96, 1024
+    w = random_blocks(Q8_0, rng, rows, cols)
+    blk = w.reshape(rows, cols // 32, 34)
+    q = blk[:, :, 2:].view(np.int8)
+    q[rng.random(q.shape) < 0.05] = -128  # some -128 bytes in most blocks
+    blk[:, :, :2] = (rng.uniform(0.5, 2.0, (rows, cols // 32, 1)) * 1e-3).astype(np.float16).view(np.uint8)
+    dw = blk[:, :, :2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+    for S in (1, 4, 40):
+        x = gaussian(rng, (S, cols))
+        exact = np.zeros((S, rows))
+        for s in range(S):
+            xq, d8 = oracle.quantize_q8_0_act(x[s])
+            isum = (q.astype(np.int64) * xq.reshape(cols // 32, 32).astype(np.int64)[None]).sum(axis=2)
+            exact[s] = (isum * dw * d8.astype(np.float64)[None]).sum(axis=1)
+        xd, wd = to_dev(x, dev), to_dev(w, dev)
+        got = tc.gemv(Q8_0, wd, xd, rows, cols) if S <= 8 else tc.gemm(Q8_0, wd, xd, rows, cols)
+        ok, worst = close(got.cpu().numpy(), exact.astype(np.float32))
+        assert ok, f"S={S}: worst err/bound {worst:.3g}"
+        ref = oracle.matmul(Q8_0, w, x, rows, cols)
+        assert not close(ref, exact.astype(np.float32))[0], "the reference quirk should show on these rows"
