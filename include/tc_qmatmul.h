@@ -101,7 +101,7 @@ int tc_gemm(int type, const void *w, const float *x, float *out, uint32_t seq_le
 /* Prefill GEMM that allocates nothing: the same kernels and results as
  * tc_gemm for its MFMA types (cols % 256 == 0), with its scratch (quantized
  * activations, split / stream-K partials) in a fixed per-device array of
- * tc_gemm_noalloc_scratch_bytes() (32 MiB) instead of the library's buffers.
+ * tc_gemm_noalloc_scratch_bytes() (128 MiB) instead of the library's buffers.
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). Shapes whose scratch exceeds the array are refused

@@ -46,7 +46,7 @@ def test_gemm_noalloc_refuses_beyond_scratch(tc, dev):
     lib.tc_gemm_noalloc.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 3 + [ctypes.c_uint32] * 4 + [ctypes.c_void_p]
     lib.tc_gemm_noalloc_scratch_bytes.restype = ctypes.c_size_t
     cap = lib.tc_gemm_noalloc_scratch_bytes()
-    M, K, N = 4096, 17408, 64  # ~81 MB of quantized activations
+    M, K, N = 8192, 17408, 64  # ~143 MB of quantized activations
     assert M * K > cap
     w = torch.zeros(N * K // 256 * 144, dtype=torch.uint8, device=dev)
     x = torch.zeros((M, K), device=dev)

@@ -20,7 +20,7 @@
 
 namespace {
 
-constexpr size_t kScratchBytes = size_t(32) << 20;  // TC_GEMM_NOALLOC_SCRATCH_BYTES
+constexpr size_t kScratchBytes = size_t(128) << 20;  // TC_GEMM_NOALLOC_SCRATCH_BYTES
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -62,7 +62,7 @@ int tc_gemm_noalloc(int type, const void *w, const float *x, float *out, uint32_
     const size_t ws_bytes = tc::gemm_mfma_scratch(type, seq_len, rows, cols, num_cu, &act_bytes);
     const size_t act_room = (act_bytes + 255) & ~size_t(255);
     if (act_room + ws_bytes > kScratchBytes)
-        return tc::fail_code(TC_E_UNSUPPORTED, "shape needs more than the 32 MiB no-alloc scratch (use tc_gemm)");
+        return tc::fail_code(TC_E_UNSUPPORTED, "shape needs more than the 128 MiB no-alloc scratch (use tc_gemm)");
     void *base = nullptr;
     if ((rc = scratch_on_device(&base))) return rc;
     unsigned char *b = static_cast<unsigned char *>(base);
