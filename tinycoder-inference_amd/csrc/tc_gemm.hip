@@ -1,40 +1,34 @@
 // tc_gemm.hip -- prefill GEMM: out[m][n] = W[n] . x[m] for M tokens against raw
-// GGUF weight rows (Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, Q8_0), on the
-// int8 matrix cores (v_mfma_i32_32x32x32_i8).
+// GGUF weight rows of Q5_K, Q6_K, IQ3_XXS, IQ3_S and IQ2_S, on the int8
+// matrix cores (v_mfma_i32_32x32x32_i8). (Q4_K and Q8_0, the config-4 types,
+// run the register-conversion kernel of tc_prefill.hip.)
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698) with
 // the CPU reference's numerics: the activations are quantized by the same
-// bit-exact quantizers as the mat-vec path (Q8_K for the K-quant and IQ
-// weights, 32-wide Q8_0-style for Q8_0 weights), every integer dot product of a weight block
-// with an activation block is exact, and only the final per-block scale
-// combination runs in fp32.
+// bit-exact Q8_K quantizer as the mat-vec path, every integer dot product of
+// a weight block with an activation block is exact, and only the final
+// per-block scale combination runs in fp32.
 //
 // Decomposition. One workgroup owns a tile of 64 weight rows x 128 tokens and
-// walks K one 256-element superblock at a time. The digit-plane types spread
-// the (tile, superblock) units evenly over one workgroup per CU (stream-K,
-// partial tiles summed by k_gemm_fixup); Q8_0 runs one workgroup per tile (split-K when the
-// tiles do not fill the chip). The activations arrive block-major
-// (256-column block b of token m at b*M + m), so one superblock of a token
-// tile is one contiguous 32 KB run. Per superblock the raw weight rows, the
-// quantized activations and their scales are staged through LDS. The
-// digit-plane kernel runs 12 waves: 4 producers (weight loads two superblocks ahead, conversion into one
-// half of a double-buffered LDS) and 8 consumers (the activation plane loaded
-// straight into LDS, MFMAs on the other half); Q8_0 runs 4 waves that do both,
-// two workgroups per CU.
+// walks K one 256-element superblock at a time; the (tile, superblock) units
+// are spread evenly over one workgroup per CU (stream-K, partial tiles summed
+// by k_gemm_fixup). The activations arrive block-major (256-column block b of
+// token m at b*M + m), so one superblock of a token tile is one contiguous
+// 32 KB run. The kernel runs 12 waves: 4 producers (weight loads two
+// superblocks ahead, conversion into one half of a double-buffered LDS) and 8
+// consumers (the activation plane loaded straight into LDS, MFMAs on the
+// other half).
 //
-//  * Q4_K: a weight of sub-block s is w = d*sc_s*q - dmin*m_s (q in 0..15,
-//    sc_s, m_s in 0..63). The product sc_s*q (<= 945) is written to two int8
-//    planes, hi = (sc_s*q) >> 7 and lo = (sc_s*q) & 127, so that one chain of
-//    MFMAs over the 8 sub-blocks gives main = sum_s sc_s * (q . x)_s exactly as
-//    128*acc(hi) + acc(lo). The min term sum_s m_s * (x-sum of sub-block s) is
-//    one more pair of MFMAs over 8 useful k-slots, with the activation pair
-//    sums split into int8 digits the same way. Per superblock and output:
-//    acc += d8 * (d*main - dmin*min). Q5_K is the same with 5-bit q (sc*q
-//    <= 1953); Q6_K, IQ3_XXS, IQ3_S and IQ2_S write their signed integer
-//    weights (sc*(q-32), (2ls+1)*(+-grid value)) as signed digits and have no
-//    min term.
-//  * Q8_0: the int8 weights are the A operand directly; each 32-block gives
-//    one MFMA and acc += (dw*d8) * isum.
+// Every weight of a superblock becomes an exact integer e written to two int8
+// planes, e = 128*hi + lo, so that one MFMA chain over the hi plane, a shift
+// by 7 and the lo chain on top give sum_s e . x exactly:
+//  * Q5_K: a weight of sub-block s is w = d*sc_s*q - dmin*m_s with q 5-bit
+//    (sc_s*q <= 1953); the min term sum_s m_s * (x-sum of sub-block s) is one
+//    more pair of MFMAs over 8 useful k-slots, with the activation pair sums
+//    split into int8 digits the same way. Per superblock and output: acc +=
+//    d8 * (d*main - dmin*min). (The Q4_K producer code is shared with it.)
+//  * Q6_K, IQ3_XXS, IQ3_S and IQ2_S write their signed integer weights
+//    (sc*(q-32), (2ls+1)*(+-grid value)) as signed digits and have no min term.
 //
 // MFMA operands: lane l feeds row (l & 31) and the 16 bytes of k-group
 // (l >> 5) of both A (weights) and B (activations), so each product pairs the
@@ -625,27 +619,6 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
     }
 }
 
-// Q8_0 raw rows in LDS -> the weight plane and the per-block scales.
-__device__ __forceinline__ void q80_convert(unsigned char *lds) {
-    using L = GLds<kQ8_0>;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t r = tid / 4, qq = tid & 3;
-    // 8 blocks of 34 bytes per row (2-byte aligned); thread qq: blocks 2qq, 2qq+1.
-    const unsigned char *raw = lds + L::RAW + r * 272;
-    unsigned char *a0 = lds + L::A0 + r * PL;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint32_t blk = 2 * qq + j;
-        const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + 34 * blk);
-        uint32_t w[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) w[k] = uint32_t(src[1 + 2 * k]) | (uint32_t(src[2 + 2 * k]) << 16);
-        *reinterpret_cast<u4 *>(a0 + 32 * blk) = u4{w[0], w[1], w[2], w[3]};
-        *reinterpret_cast<u4 *>(a0 + 32 * blk + 16) = u4{w[4], w[5], w[6], w[7]};
-        reinterpret_cast<float *>(lds + L::AS + r * 32)[blk] = h2f(src[0]);
-    }
-}
-
 __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
@@ -766,95 +739,6 @@ __device__ __forceinline__ void dig_consume(const unsigned char *lds, uint32_t w
         combine(1, c1, m1);
     } else {
         combine(0, c0, m0);
-    }
-}
-
-template <int TYPE>
-__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(GemmArgs a) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t wn = wave & 1, wm = wave >> 1;  // 32-row group, 64-token group
-    using L = GLds<TYPE>;
-    const uint32_t li = lane & 31, lg = lane >> 5;
-
-    const uint32_t tile = blockIdx.x;
-    const uint32_t split = blockIdx.y;
-    const uint32_t tm = tile % a.ntm, tn = tile / a.ntm;
-    const uint32_t n0 = tn * GN, m0 = tm * GM;
-    const uint32_t b0 = split * a.split_blk;
-    const uint32_t b1 = min(b0 + a.split_blk, a.nblk);
-
-    float acc[2][16];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
-
-    const GSrc gs = gemm_src<TYPE>(a, n0, m0, tid);
-    GPrefetch<TYPE> pf;
-    if (b0 < b1) gemm_prefetch<TYPE>(a, gs, b0, pf);
-    for (uint32_t b = b0; b < b1; ++b) {
-        gemm_stage<TYPE>(pf, lds, tid);
-        if (b + 1 < b1) gemm_prefetch<TYPE>(a, gs, b + 1, pf);
-        __syncthreads();
-        if constexpr (TYPE == kQ8_0) {
-            q80_convert(lds);
-            __syncthreads();
-        }
-
-        const unsigned char *arow = lds + (32 * wn + li) * PL + 16 * lg;
-        const unsigned char *brow0 = lds + L::B + (64 * wm + li) * PL + 16 * lg;
-        const unsigned char *brow1 = brow0 + 32 * PL;
-        if constexpr (dig_type(TYPE)) {
-            static_assert(!dig_type(TYPE), "the digit-plane types run k_gemm_dig");
-        } else {
-            const uint32_t tb0 = 64 * wm + li, tb1 = tb0 + 32;
-#pragma unroll 2
-            for (int s = 0; s < 8; ++s) {
-                const v4i aw = as_v4i(lds4(arow + L::A0 + 32 * s));
-                const v4i x0 = as_v4i(lds4(brow0 + 32 * s));
-                const v4i x1 = as_v4i(lds4(brow1 + 32 * s));
-                const v16i z16 = {};
-                const v16i c0 = mfma(aw, x0, z16), c1 = mfma(aw, x1, z16);
-                const float d80 = reinterpret_cast<const float *>(lds + L::BD + tb0 * 32)[s];
-                const float d81 = reinterpret_cast<const float *>(lds + L::BD + tb1 * 32)[s];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int r = 4 * q + e;
-                        const float dw = reinterpret_cast<const float *>(
-                            lds + L::AS + (32 * wn + 8 * q + 4 * lg + e) * 32)[s];
-                        acc[0][r] = fmaf(dw * d80, float(c0[r]), acc[0][r]);
-                        acc[1][r] = fmaf(dw * d81, float(c1[r]), acc[1][r]);
-                    }
-                }
-            }
-        }
-        __syncthreads();
-    }
-
-    // Store: this lane holds tokens m0 + 64wm + 32t + li, rows n0 + 32wn +
-    // 8q + 4lg + e. Rows of a register quad are consecutive.
-    float *out = a.out + size_t(split) * a.M * a.N;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const uint32_t m = m0 + 64 * wm + 32 * t + li;
-        if (m >= a.M) continue;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t n = n0 + 32 * wn + 8 * q + 4 * lg;
-            float *o = out + size_t(m) * a.N + n;
-            if (n + 3 < a.N && (a.N & 3) == 0) {
-                *reinterpret_cast<float4 *>(o) = make_float4(acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2],
-                                                             acc[t][4 * q + 3]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (n + e < a.N) o[e] = acc[t][4 * q + e];
-            }
-        }
     }
 }
 
@@ -1107,11 +991,6 @@ hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
         if (attr != hipSuccess) return attr;
         const uint32_t lds = 2 * GLds<TYPE>::bytes + grid_bytes(TYPE);
         k_gemm_dig<TYPE, CW, GRP><<<grid, GT + 64 * CW, lds, st>>>(a);
-    } else {
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm<TYPE>),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (attr != hipSuccess) return attr;
-        k_gemm<TYPE><<<grid, GT, GLds<TYPE>::bytes, st>>>(a);
     }
     return hipGetLastError();
 }
@@ -1141,52 +1020,6 @@ size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int nu
     return s > 1 ? size_t(s) * M * N * 4 : 0;
 }
 
-namespace {
-uint32_t grouped_grid(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
-    const uint64_t units = uint64_t(ntm_max) * ((N + GN - 1) / GN) * (K / 256);
-    return uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(uint64_t(num_cu), units / 4)));
-}
-}  // namespace
-
-size_t gemm_grouped_workspace_bytes(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
-    return size_t(grouped_grid(ntm_max, N, K, num_cu)) * 2 * GM * GN * 4;
-}
-
-hipError_t launch_gemm_grouped(const void *W, uint64_t wstride, const ActView &act, float *out, uint32_t rows_total,
-                               uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm, uint32_t ntm_max,
-                               int num_cu, void *workspace, hipStream_t st) {
-    if (rows_total == 0 || N == 0 || K == 0 || K % 256 || ntm_max == 0 || workspace == nullptr)
-        return hipErrorInvalidValue;
-    const uint32_t ntn = (N + GN - 1) / GN;
-    // 32-bit buffer offsets and unit counts
-    if (uint64_t(rows_total) * K >= (uint64_t(1) << 32) || wstride >= (uint64_t(1) << 32) ||
-        uint64_t(ntm_max) * ntn * (K / 256) >= (uint64_t(1) << 32))
-        return hipErrorInvalidValue;
-    GemmArgs a{};
-    a.W = static_cast<const uint8_t *>(W);
-    a.qs = act.qs;
-    a.d8 = act.d;
-    a.bsums = act.bsums;
-    a.M = rows_total;
-    a.N = N;
-    a.K = K;
-    a.nblk = K / 256;
-    a.row_bytes = a.nblk * unit_bytes(kQ4_K);
-    a.mt = mt;
-    a.ntm_dev = ntm;
-    a.wstride = wstride;
-    a.ntn = ntn;
-    a.out = out;
-    a.ws = static_cast<float *>(workspace);
-    a.skg = grouped_grid(ntm_max, N, K, num_cu);
-    hipError_t e = launch_gemm_t<kQ4_K, true>(a, dim3{a.skg, 1u, 1u}, st);
-    if (e != hipSuccess) return e;
-    // The split tiles are known on the device only: one fixup workgroup per
-    // possible tile (those past the count, or stored whole, exit at once).
-    k_gemm_fixup<true><<<dim3{ntm_max * ntn, 1u, 1u}, 256, 0, st>>>(a);
-    return hipGetLastError();
-}
-
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
                        int num_cu, void *workspace, hipStream_t st) {
     if (M == 0 || N == 0 || K == 0 || K % 256) return hipErrorInvalidValue;
@@ -1194,7 +1027,8 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
     // weight matrix must each stay below 4 GiB.
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
-    if (!dig_type(type) && type != kQ8_0) return hipErrorInvalidValue;
+    // Q4_K and Q8_0 run k_prefill (tc_prefill.hip); the other MFMA types here.
+    if (!dig_type(type) || type == kQ4_K) return hipErrorInvalidValue;
     const uint32_t nsplit = gemm_splits(type, M, N, K, num_cu);
     if ((nsplit > 1 || dig_type(type)) && workspace == nullptr) return hipErrorInvalidValue;
     GemmArgs a{};
@@ -1216,8 +1050,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
         a.ws = static_cast<float *>(workspace);
         a.skg = G;
         const dim3 g{G, 1u, 1u};
-        hipError_t e = type == kQ4_K     ? launch_gemm_t<kQ4_K>(a, g, st)
-                       : type == kQ5_K   ? launch_gemm_t<kQ5_K>(a, g, st)
+        hipError_t e = type == kQ5_K     ? launch_gemm_t<kQ5_K>(a, g, st)
                        : type == kQ6_K   ? launch_gemm_t<kQ6_K>(a, g, st)
                        : type == kIQ3_S  ? launch_gemm_t<kIQ3_S>(a, g, st)
                        : type == kIQ2_S  ? launch_gemm_t<kIQ2_S>(a, g, st)
@@ -1230,14 +1063,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
         k_gemm_fixup<false><<<dim3{(G - 1) * kFixSlices, 1u, 1u}, 256, 0, st>>>(a);
         return hipGetLastError();
     }
-    a.out = nsplit > 1 ? static_cast<float *>(workspace) : out;
-    const dim3 grid{a.ntiles, nsplit, 1u};
-    hipError_t e = launch_gemm_t<kQ8_0>(a, grid, st);
-    if (e != hipSuccess || nsplit == 1) return e;
-    const size_t mn = size_t(M) * N;
-    k_gemm_reduce<<<dim3{uint32_t((mn + 255) / 256), 1u, 1u}, 256, 0, st>>>(static_cast<const float *>(workspace),
-                                                                           out, mn, nsplit);
-    return hipGetLastError();
+    return hipErrorInvalidValue;
 }
 
 }  // namespace tc

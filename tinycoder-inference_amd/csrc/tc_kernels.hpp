@@ -72,10 +72,10 @@ uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs);
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes);
 uint32_t gemv_max_tokens(int type, uint32_t cols);
 
-// Prefill GEMM (int8 MFMA) for the digit-plane types and Q8_0: out[M][N] = W x^T with
-// activations already quantized (launch_quant_act over M tokens). Splits K
-// across workgroups when the output tiles do not fill the chip; the partial
-// sums then need gemm_workspace_bytes() of device scratch.
+// Prefill GEMM (int8 MFMA) for Q5_K, Q6_K, IQ3_XXS, IQ3_S and IQ2_S (Q4_K and
+// Q8_0: launch_prefill): out[M][N] = W x^T with activations already
+// quantized (launch_quant_act over M tokens, block-major). Stream-K over one
+// workgroup per CU; the partial tiles need gemm_workspace_bytes() of scratch.
 uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
 size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
@@ -127,12 +127,7 @@ hipError_t launch_router_logits(const float *W, const float *X, uint32_t S, uint
 hipError_t launch_router_select(const float *logits, uint32_t S, uint32_t E, uint32_t K, int32_t *ids, float *wts,
                                 hipStream_t st);
 
-// Q4_K GEMM over expert-sorted rows: out[i][n] = act row i . W[e(i)] row n,
-// for the token tiles of mt (count *ntm, at most ntm_max).
-size_t gemm_grouped_workspace_bytes(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu);
-hipError_t launch_gemm_grouped(const void *W, uint64_t wstride, const ActView &act, float *out, uint32_t rows_total,
-                               uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm, uint32_t ntm_max,
-                               int num_cu, void *workspace, hipStream_t st);
+
 
 // ---- host-side helpers shared by the entry-point files (tc_api.cpp) ----
 int device_cu_count();
