@@ -63,10 +63,10 @@ __device__ __forceinline__ uint32_t quant4_sum(float4 v, float iscale, int *sum)
 
 // One 256-element Q8_K block by one full wave, lane values already loaded
 // (lane l holds elements 4l..4l+3). Writes qs[0..255], *d and bsums[0..15],
-// and with dg the 32-wide sums as digits (dg[p] = s_p >> 7, dg[8 + p] =
-// s_p & 127, s_p = bsums[2p] + bsums[2p + 1]).
+// and with dg the 32-wide sums s_p = bsums[2p] + bsums[2p + 1] as two exact
+// bf16 pieces: dg[p] = 128 * (s_p >> 7), dg[8 + p] = s_p & 127.
 __device__ __forceinline__ void quant_q8k_block_wave_v(float4 v, int8_t *qs, float *d, int16_t *bsums,
-                                                       int8_t *dg = nullptr) {
+                                                       uint16_t *dg = nullptr) {
     const uint32_t lane = threadIdx.x & 63;
     const float e[4] = {v.x, v.y, v.z, v.w};
     const float maxv = first_absmax<64>(e, 4 * int(lane));
@@ -85,14 +85,16 @@ __device__ __forceinline__ void quant_q8k_block_wave_v(float4 v, int8_t *qs, flo
     if (dg != nullptr) {
         const int s32 = s16 + __shfl_xor(s16, 4);  // lanes 8p: bsums 2p and 2p+1
         if ((lane & 7) == 0) {
-            dg[lane >> 3] = int8_t(s32 >> 7);
-            dg[8 + (lane >> 3)] = int8_t(s32 & 127);
+            // |s| <= 4064: 128 * (s >> 7) has at most 6 significant bits and
+            // s & 127 at most 7, so both are exact in bf16
+            dg[lane >> 3] = uint16_t(__builtin_bit_cast(uint32_t, float((s32 >> 7) * 128)) >> 16);
+            dg[8 + (lane >> 3)] = uint16_t(__builtin_bit_cast(uint32_t, float(s32 & 127)) >> 16);
         }
     }
 }
 
 __device__ __forceinline__ void quant_q8k_block_wave(const float *x, int8_t *qs, float *d, int16_t *bsums,
-                                                     int8_t *dg = nullptr) {
+                                                     uint16_t *dg = nullptr) {
     quant_q8k_block_wave_v(reinterpret_cast<const float4 *>(x)[threadIdx.x & 63], qs, d, bsums, dg);
 }
 

@@ -109,7 +109,7 @@ tc::ActView act_view(void *buf, const tc::ActLayout &L, size_t tok, int type, ui
     v.qs = reinterpret_cast<const int8_t *>(b + L.qs_off) + tok * cols;
     v.d = reinterpret_cast<const float *>(b + L.d_off) + tok * (cols / blk);
     v.bsums = reinterpret_cast<const int16_t *>(b + L.bs_off) + tok * (cols / 16);
-    v.dg = reinterpret_cast<const int8_t *>(b + L.dg_off) + tok * (cols / 256) * (type == TC_Q8_0 ? 64 : 16);
+    v.dg = reinterpret_cast<const int8_t *>(b + L.dg_off) + tok * (cols / 256) * tc::dg_bytes(type);
     return v;
 }
 

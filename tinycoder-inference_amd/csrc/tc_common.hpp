@@ -26,11 +26,14 @@ __host__ __device__ constexpr int block_elems(int type) { return type == kQ8_0 |
 //   qs    int8  [S][cols]            (the quantized values)
 //   d     fp32  [S][cols / blk]      (blk = 256 for Q8_K, 32 for Q8_0-style)
 //   bsums int16 [S][cols / 16]       (Q8_K only: sums of 16 consecutive qs)
-//   dg    int8  [S][cols / 256][16]  (Q8_K: the 8 sums of 32 consecutive qs as
-//                                     two int8 digits, bytes 0-7 the high
-//                                     digits s >> 7, 8-15 the low s & 127)
+//   dg    bf16  [S][cols / 256][16]  (Q8_K: the 8 sums s of 32 consecutive qs
+//                                     as two exact bf16 pieces, 0-7 the high
+//                                     128 * (s >> 7), 8-15 the low s & 127)
 //         bf16  [S][cols / 32][4]    (Q8_0: each block's d as 3 bf16 pieces
 //                                     summing to it exactly, and a zero)
+// Bytes of dg per token and 256 columns.
+__host__ __device__ constexpr uint32_t dg_bytes(int wtype) { return wtype == kQ8_0 ? 64u : 32u; }
+
 struct ActView {
     const int8_t *qs;
     const float *d;
@@ -50,7 +53,7 @@ __host__ inline ActLayout act_layout(int wtype, uint32_t S, uint32_t cols) {
     L.d_off = up(size_t(S) * cols);
     L.bs_off = L.d_off + up(size_t(S) * (cols / blk) * 4);
     L.dg_off = L.bs_off + up(size_t(S) * (cols / 16) * 2);
-    L.bytes = L.dg_off + up(size_t(S) * (cols / 256) * (wtype == kQ8_0 ? 64 : 16));
+    L.bytes = L.dg_off + up(size_t(S) * (cols / 256) * dg_bytes(wtype));
     return L;
 }
 

@@ -26,10 +26,12 @@
 // of sub-block s is w = d*sc_s*q - dmin*m_s with q in 0..15 and sc_s, m_s in
 // 0..63. With sc_s = 8*h_s + l_s (h_s, l_s in 0..7) the products h_s*q and
 // l_s*q fit int8, so the hi chain (8 MFMAs) and the lo chain (8 more) give
-// C = sum_s sc_s * (q . x)_s exactly as 8*hi + lo. The min term sum_s m_s *
-// S_s (S_s the sum of the 32 activations of sub-block s, from the quantizer
-// as int8 digits S_s = 128*hi + lo) is one MFMA pair over 8 k slots. Per
-// superblock and output, in fp32: acc += d8 * (d*C - dmin*Mn).
+// C = sum_s sc_s * (q . x)_s exactly as 8*hi + lo. The min term Mn = sum_s
+// m_s * S_s (S_s the sum of the 32 activations of sub-block s) is one bf16
+// MFMA: the quantizer writes S_s as two exact bf16 pieces 128*(S_s >> 7) and
+// S_s & 127, the weights give m_s (6 bits) against each, and every product
+// and partial sum is an integer below 2^24, so the fp32 result is Mn exactly.
+// Per superblock and output, in fp32: acc += d8 * (d*C - dmin*Mn).
 //
 // Q8_0 (reference matMulVecBatchQ8_0_Q8K_AVX2, SIMDMatMulVecAVX2.cpp:4239-4383):
 // one MFMA per 32-block gives the exact integer I; the scale dw * d8 of every
@@ -68,13 +70,13 @@ constexpr uint32_t PW = 8;  // waves per workgroup (two per SIMD)
 
 // Per weight type: rows per workgroup tile, waves per row group (waves that
 // share rows and split the tokens), unit bytes, and the activation scale
-// data per token and superblock (Q4_K: 16 digit bytes + the fp32 d; Q8_0: 8
-// blocks x 4 bf16 pieces).
+// data per token and superblock (Q4_K: 16 bf16 pieces of the 32-wide sums +
+// the fp32 d; Q8_0: 8 blocks x 4 bf16 pieces).
 template <int TYPE>
 struct PfType;
 template <>
 struct PfType<kQ4_K> {
-    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 144, XB = 16;
+    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 144, XB = 32;
 };
 template <>
 struct PfType<kQ8_0> {
@@ -99,7 +101,7 @@ struct PfArgs {
     const uint8_t *W;
     const int8_t *qs;   // block-major [nblk][M][256]
     const float *d8;    // Q4_K: [nblk][M]
-    const int8_t *xs;   // Q4_K digit sums [nblk][M][16]; Q8_0 d pieces [nblk][M][64 B]
+    const int8_t *xs;   // Q4_K sum pieces [nblk][M][32 B]; Q8_0 d pieces [nblk][M][64 B]
     float *out;         // [M][N]
     float *ws;          // partial tiles [G][2][TT][PR]
     uint32_t M, N, K;
@@ -184,9 +186,15 @@ __device__ __forceinline__ void q4_read(Q4Raw &r, const unsigned char *blk, uint
 // Digit planes of sc*q per sub-block, the mins and the row scales.
 struct Q4Frag {
     v4i bh[8], bl[8];
-    v4i m;  // bytes 0-7: the 8 mins (k-half 0; zero in k-half 1)
+    v4i mb;  // the 8 mins as bf16 (both k-halves: against the high and the low pieces)
     float d, dm;
 };
+
+// bf16 of the small integers in bytes 2i and 2i + 1 of w (exact: <= 8 bits).
+__device__ __forceinline__ int bf16_pair(uint32_t w, int i) {
+    const float f0 = float((w >> (16 * i)) & 0xFFu), f1 = float((w >> (16 * i + 8)) & 0xFFu);
+    return int(__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u));
+}
 
 __device__ __forceinline__ void q4_convert(const Q4Raw &r, uint32_t g, Q4Frag &f) {
     const u4 h = r.h;
@@ -214,40 +222,51 @@ __device__ __forceinline__ void q4_convert(const Q4Raw &r, uint32_t g, Q4Frag &f
             f.bl[s1][k] = pkmul(hi, ml1);
         }
     }
-    const int a = g == 0 ? int(mnl) : 0, b = g == 0 ? int(mnh) : 0;
-    f.m = v4i{a, b, 0, 0};
+    f.mb = v4i{bf16_pair(mnl, 0), bf16_pair(mnl, 1), bf16_pair(mnh, 0), bf16_pair(mnh, 1)};
 }
 
-// One 32-token block (activation row arow, digit sums at dgp, scales at d8)
-// against this wave's converted weights. The hi and lo chains run
-// interleaved as two independent accumulators (no MFMA waits on the previous
-// one's result); the min term's high-digit MFMA is issued first so that its
-// shift overlaps the chains.
+// One 32-token block (activation row arow, this k-half's sum pieces at dgp,
+// scales at d8) against this wave's converted weights. The hi and lo chains
+// run interleaved as two independent accumulators (no MFMA waits on the
+// previous one's result); the min term's MFMA is issued first.
 __device__ __forceinline__ void q4_block(const unsigned char *arow, const unsigned char *dgp, const float *d8,
                                          const Q4Frag &f, uint32_t j, uint32_t g, float (&acc)[16]) {
+    // LDS reads issued ahead of their use (the scheduler otherwise places each
+    // right before its consumer): activation fragments two sub-blocks ahead,
+    // the sum pieces before the chains, the token scales mid-chain; the min
+    // MFMA mid-chain so that its result is ready for the epilogue.
+    auto aread = [&](int s) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
+    };
     const v4i dgv = as_v4i(lds4(dgp));
-    // high digits in bytes 0-7 against the mins; then the low digits moved there
-    v16i mn = mfma(dgv, f.m, v16i{});
+    v4i af[3];
+    af[0] = aread(0);
+    af[1] = aread(1);
+    __builtin_amdgcn_sched_barrier(0);
     v16i ch = {}, cl = {};
+    v16f mn;
+    float4 dv[4];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        const v4i af = as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-        ch = mfma(af, f.bh[s], ch);
-        cl = mfma(af, f.bl[s], cl);
-    }
+        if (s + 2 < 8) af[(s + 2) % 3] = aread(s + 2);
+        if (s == 2) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mn[r] <<= 7;
-    mn = mfma(v4i{dgv.z, dgv.w, dgv.z, dgv.w}, f.m, mn);
+            for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
+        }
+        ch = mfma(af[s % 3], f.bh[s], ch);
+        cl = mfma(af[s % 3], f.bl[s], cl);
+        if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
+        __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) ch[r] = (ch[r] << 3) + cl[r];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const float4 dv = *reinterpret_cast<const float4 *>(d8 + 8 * q);
-        const float dd[4] = {dv.x, dv.y, dv.z, dv.w};
+        const float dd[4] = {dv[q].x, dv[q].y, dv[q].z, dv[q].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int r = 4 * q + e;
-            acc[r] = fmaf(dd[e], fmaf(f.d, float(ch[r]), -f.dm * float(mn[r])), acc[r]);
+            acc[r] = fmaf(dd[e], fmaf(f.d, float(ch[r]), -f.dm * mn[r]), acc[r]);
         }
     }
 }
@@ -373,7 +392,9 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
     });
     const v4i rx = rs4(a.xs, a.M * a.nblk * T::XB);
     if constexpr (TYPE == kQ4_K) {
-        each_inst<TT / 16>(w, [&](uint32_t k) { lds_load4(base + L::XS + 256 * k, rx, (tb + 16 * k) * 16 + 4 * ln); });
+        each_inst<TT / 32>(w, [&](uint32_t k) {
+            lds_load16(base + L::XS + 1024 * k, rx, (tb + 32 * k) * T::XB + 16 * ln);
+        });
         const v4i rd = rs4(a.d8, a.M * a.nblk * 4);
         each_inst<(TT + 63) / 64>(w, [&](uint32_t k) { lds_load4(base + L::D8 + 256 * k, rd, (tb + 64 * k + ln) * 4); });
     } else {
@@ -462,7 +483,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     // would otherwise hoist every block's operand reads)
                     __builtin_amdgcn_sched_barrier(0);
                     const uint32_t tok = 32 * (tg * NB + t) + j;
-                    q4_block(bb + L::QS + tok * 256, bb + L::XS + tok * 16,
+                    q4_block(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g,
                              reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g, f, j, g,
                              acc[t]);
                 }
@@ -501,52 +522,73 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 }
 
 // Tiles split over several workgroups: out = the partial segments summed in
-// workgroup (range) order. kFix workgroups per split tile, each a slice of
-// it; group j takes the tile holding range boundary j + 1 when that boundary
-// splits it and is the first to do so. (Summing inside the main kernel, by
-// the last contributor to arrive, measured slower: its device-scope release
-// and acquire around the partial tiles cost more than this launch.)
-constexpr uint32_t kFix = 4;
+// workgroup (range) order. A split tile is summed by kFixSlices(TT, PR)
+// workgroups, each a slice of kFixNI float4 per thread; group j takes the
+// tile holding range boundary j + 1 when that boundary splits it and is the
+// first to do so. A thread issues the loads of up to 4 contributors before
+// adding them (in order), so that a CU has many partial lines in flight.
+// (Summing inside the main kernel, by the last contributor to arrive,
+// measured slower: its device-scope release and acquire around the partial
+// tiles cost more than this launch.)
+constexpr uint32_t kFixNI = 2;
+__host__ __device__ constexpr uint32_t kFixSlices(uint32_t TT, uint32_t PR) { return TT * PR / 4 / (256 * kFixNI); }
 template <uint32_t TT, uint32_t PR, bool GRP>
 __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
+    constexpr uint32_t NS = kFixSlices(TT, PR);
+    static_assert(NS * 256 * kFixNI * 4 == TT * PR, "a fixup slice is a whole number of 256-thread rounds");
     const uint32_t ntiles = pf_ntiles<GRP>(a);
     const uint32_t units = ntiles * a.nblk, G = a.G;
-    const uint32_t slice = blockIdx.x % kFix;
-    const uint32_t wb = blockIdx.x / kFix + 1, ubd = sk_begin(units, G, wb);
+    const uint32_t slice = blockIdx.x % NS;
+    const uint32_t wb = blockIdx.x / NS + 1, ubd = sk_begin(units, G, wb);
     const uint32_t tile = ubd / a.nblk;
     if (ubd % a.nblk == 0 || sk_begin(units, G, wb - 1) > tile * a.nblk) return;
     if (tile >= ntiles) return;
     const uint32_t t0 = tile * a.nblk, t1 = t0 + a.nblk;
-    uint32_t v = uint32_t(uint64_t(t0) * G / units);
-    while (v + 1 < G && sk_begin(units, G, v + 1) <= t0) ++v;
-    while (v > 0 && sk_begin(units, G, v) > t0) --v;
+    // contributors: the nonempty ranges from vf (the one holding t0) to vl
+    // (the one holding t1 - 1); grouped launches size the grid for the
+    // largest tile count, so some ranges may be empty there
+    uint32_t vf = uint32_t(uint64_t(t0) * G / units);
+    while (vf + 1 < G && sk_begin(units, G, vf + 1) <= t0) ++vf;
+    while (vf > 0 && sk_begin(units, G, vf) > t0) --vf;
+    uint32_t vl = vf;
+    while (vl + 1 < G && sk_begin(units, G, vl + 1) < t1) ++vl;
+    const uint32_t first_slot = sk_begin(units, G, vf) < t0 ? 1u : 0u;  // vf's second segment
     const PfTile tg_ = pf_tile<GRP>(a, tile, TT, PR);
     const uint32_t n0 = tg_.n0, m0 = tg_.m0;
-    constexpr uint32_t per = TT * PR / 4 / kFix;  // float4 entries per slice
-    constexpr uint32_t NI = per / 256;
-    static_assert(per % 256 == 0, "a fixup slice is a whole number of 256-thread rounds");
-    float4 s[NI];
+    const uint32_t e0 = slice * (256 * kFixNI) + threadIdx.x;  // float4 index of item k: e0 + 256 k
+    float4 s[kFixNI];
 #pragma unroll
-    for (uint32_t k = 0; k < NI; ++k) s[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    uint32_t bv = sk_begin(units, G, v);
-    for (; v < G && bv < t1; ++v) {
-        const uint32_t bn = sk_begin(units, G, v + 1);
-        if (bn > t0 && bn != bv) {
-            const float *src = a.ws + (size_t(v) * 2 + (bv >= t0 ? 0u : 1u)) * (TT * PR);
+    for (uint32_t k = 0; k < kFixNI; ++k) s[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t v = vf; v <= vl; v += 4) {
+        float4 p[4][kFixNI];
+        bool live[4];
 #pragma unroll
-            for (uint32_t k = 0; k < NI; ++k) {
-                const float4 p = reinterpret_cast<const float4 *>(src)[slice * per + k * 256 + threadIdx.x];
-                s[k].x += p.x;
-                s[k].y += p.y;
-                s[k].z += p.z;
-                s[k].w += p.w;
+        for (uint32_t c = 0; c < 4; ++c) {
+            const uint32_t vc = v + c;
+            live[c] = vc <= vl && (!GRP || sk_begin(units, G, vc) != sk_begin(units, G, vc + 1));
+            if (live[c]) {
+                const float4 *src = reinterpret_cast<const float4 *>(
+                    a.ws + (size_t(vc) * 2 + (vc == vf ? first_slot : 0u)) * (TT * PR));
+#pragma unroll
+                for (uint32_t k = 0; k < kFixNI; ++k) p[c][k] = src[e0 + 256 * k];
             }
         }
-        bv = bn;
+#pragma unroll
+        for (uint32_t c = 0; c < 4; ++c) {
+            if (live[c]) {
+#pragma unroll
+                for (uint32_t k = 0; k < kFixNI; ++k) {
+                    s[k].x += p[c][k].x;
+                    s[k].y += p[c][k].y;
+                    s[k].z += p[c][k].z;
+                    s[k].w += p[c][k].w;
+                }
+            }
+        }
     }
 #pragma unroll
-    for (uint32_t k = 0; k < NI; ++k) {
-        const uint32_t i = slice * per + k * 256 + threadIdx.x;
+    for (uint32_t k = 0; k < kFixNI; ++k) {
+        const uint32_t i = e0 + 256 * k;
         const uint32_t ml = (4 * i) / PR, nl = (4 * i) % PR;
         const uint32_t m = m0 + ml, n = n0 + nl;
         if (m >= tg_.mend) continue;
@@ -604,7 +646,8 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
         for (uint32_t v = 1; v < a.G && !split; ++v) split = sk_begin(units, a.G, v) % a.nblk != 0;
         if (!split) return hipSuccess;
     }
-    k_pf_fixup<L::TT, PfType<TYPE>::PR, GRP><<<dim3{(a.G - 1) * kFix, 1u, 1u}, 256, 0, st>>>(a);
+    k_pf_fixup<L::TT, PfType<TYPE>::PR, GRP>
+        <<<dim3{(a.G - 1) * kFixSlices(L::TT, PfType<TYPE>::PR), 1u, 1u}, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 

@@ -41,7 +41,7 @@ __device__ __forceinline__ uint32_t act_dst_block(uint32_t g, uint32_t nbk, uint
 template <int BPW>
 __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int8_t *__restrict__ qs,
                                                    float *__restrict__ d, int16_t *__restrict__ bsums,
-                                                   int8_t *__restrict__ dg, uint32_t nblk_total, uint32_t nbk,
+                                                   uint16_t *__restrict__ dg, uint32_t nblk_total, uint32_t nbk,
                                                    uint32_t bm_S) {
     const uint32_t g0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW;
     if (g0 >= nblk_total) return;
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, 
 // activations in expert-sorted order).
 __global__ __launch_bounds__(256) void k_quant_q8k_rows(const float *__restrict__ x, const uint32_t *__restrict__ rows,
                                                         int8_t *__restrict__ qs, float *__restrict__ d,
-                                                        int16_t *__restrict__ bsums, int8_t *__restrict__ dg,
+                                                        int16_t *__restrict__ bsums, uint16_t *__restrict__ dg,
                                                         uint32_t nblk_total, uint32_t nbk, uint32_t bm_S) {
     const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (g >= nblk_total) return;
@@ -816,7 +816,7 @@ hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols
         else k_quant_q8_0<1><<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, dp, ng, nbk, bm_S);
     } else {
         int16_t *bs = reinterpret_cast<int16_t *>(static_cast<char *>(buf) + L.bs_off);
-        int8_t *dg = reinterpret_cast<int8_t *>(static_cast<char *>(buf) + L.dg_off);
+        uint16_t *dg = reinterpret_cast<uint16_t *>(static_cast<char *>(buf) + L.dg_off);
         const uint32_t nb = S * (cols / 256);
         // 4 blocks per wave from 131072 blocks on (measured: slower than a
         // wave per block at 29k-41k blocks, faster at 139k and more)
@@ -833,7 +833,7 @@ hipError_t launch_quant_act_rows(const float *x, const uint32_t *rows, uint32_t 
     k_quant_q8k_rows<<<(nb + 3) / 4, 256, 0, st>>>(x, rows, reinterpret_cast<int8_t *>(b + L.qs_off),
                                                    reinterpret_cast<float *>(b + L.d_off),
                                                    reinterpret_cast<int16_t *>(b + L.bs_off),
-                                                   reinterpret_cast<int8_t *>(b + L.dg_off), nb, nbk, S);
+                                                   reinterpret_cast<uint16_t *>(b + L.dg_off), nb, nbk, S);
     return hipGetLastError();
 }
 
