@@ -266,7 +266,10 @@ size_t gemm_mfma_scratch(int type, uint32_t S, uint32_t rows, uint32_t cols, int
 int gemm_mfma_into(int type, const void *w, const float *x, float *out, uint32_t S, uint32_t rows, uint32_t cols,
                    int num_cu, void *act, void *ws, hipStream_t st) {
     const tc::ActLayout L = tc::act_layout(type, S, cols);
-    hipError_t e = tc::launch_quant_act(type, x, S, cols, L, act, st, true);
+    // the quantizer also zeroes the prefill GEMM's arrival counters (the
+    // head of ws)
+    const uint32_t nctr = ws ? tc::prefill_counter_words(type, S, rows, cols, num_cu) : 0;
+    hipError_t e = tc::launch_quant_act(type, x, S, cols, L, act, st, true, static_cast<uint32_t *>(ws), nctr);
     if (e != hipSuccess) return hip_fail(e, "activation quantizer");
     if (tc::prefill_type(type))
         e = tc::launch_prefill(type, w, act_view(act, L, 0, type, cols), out, S, rows, cols, num_cu, ws, st);
@@ -543,6 +546,11 @@ int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wt
                  o_ntm = take(4), o_g = take(size_t(P) * FF * 4), o_u = take(size_t(P) * FF * 4),
                  o_y = take(size_t(P) * H * 4), o_ax = take(LX.bytes + kGemmActSlack),
                  o_ah = take(LH.bytes + kGemmActSlack), o_ws = take(ws);
+    // the GEMMs' arrival counters (zeroed by the gather below; each GEMM
+    // launch leaves them zero for the next)
+    const uint32_t nctr =
+        std::max(tc::prefill_grouped_counter_words(ntm_max, FF), tc::prefill_grouped_counter_words(ntm_max, H));
+    const size_t o_ctr = take(size_t(nctr) * 4);
     if (!ensure(dev->aux, dev->aux_bytes, off)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", off);
     char *b = static_cast<char *>(dev->aux);
     int32_t *pos = reinterpret_cast<int32_t *>(b + o_pos);
@@ -554,19 +562,22 @@ int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wt
 
     hipError_t e = tc::launch_moe_route(ids, P, top_k, E, 1, tile, pos, tok, mt, ntm, st);
     if (e != hipSuccess) return hip_fail(e, "MoE router");
-    e = tc::launch_quant_act_rows(x, tok, P, H, LX, b + o_ax, st);
+    uint32_t *ctr = reinterpret_cast<uint32_t *>(b + o_ctr);
+    e = tc::launch_quant_act_rows(x, tok, P, H, LX, b + o_ax, st, ctr, nctr);
     if (e != hipSuccess) return hip_fail(e, "MoE activation gather");
     const tc::ActView ax = act_view(b + o_ax, LX, 0, TC_Q4_K, H);
-    e = tc::launch_prefill_grouped(wg, gstride, ax, g, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, b + o_ws, st);
+    e = tc::launch_prefill_grouped(wg, gstride, ax, g, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, ctr, b + o_ws,
+                                   st);
     if (e == hipSuccess)
-        e = tc::launch_prefill_grouped(wu, gstride, ax, u, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, b + o_ws,
-                                       st);
+        e = tc::launch_prefill_grouped(wu, gstride, ax, u, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, ctr,
+                                       b + o_ws, st);
     if (e != hipSuccess) return hip_fail(e, "MoE gate/up GEMM");
     e = tc::launch_moe_swiglu(g, u, P, FF, st);
     if (e == hipSuccess) e = tc::launch_quant_act(TC_Q4_K, g, P, FF, LH, b + o_ah, st, true);
     if (e != hipSuccess) return hip_fail(e, "MoE SwiGLU");
     const tc::ActView ah = act_view(b + o_ah, LH, 0, TC_Q4_K, FF);
-    e = tc::launch_prefill_grouped(wd, dstride, ah, y, P, H, FF, mt, ntm, ntm_max, tile, dev->num_cu, b + o_ws, st);
+    e = tc::launch_prefill_grouped(wd, dstride, ah, y, P, H, FF, mt, ntm, ntm_max, tile, dev->num_cu, ctr, b + o_ws,
+                                   st);
     if (e != hipSuccess) return hip_fail(e, "MoE down GEMM");
     e = tc::launch_moe_combine_rows(y, pos, wts, out, T, top_k, H, st);
     if (e != hipSuccess) return hip_fail(e, "MoE combine");

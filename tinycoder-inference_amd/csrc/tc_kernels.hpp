@@ -11,13 +11,16 @@ namespace tc {
 // act_layout(wtype, S, cols).
 // With block_major the blocks are stored block-major (block j of token t at
 // j * S + t), the layout launch_gemm reads.
+// The launch also zeroes zero[0 .. nzero) (the prefill GEMM's arrival
+// counters, which must be zero when the GEMM that follows starts).
 hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols, const ActLayout &L,
-                            void *buf, hipStream_t st, bool block_major = false);
+                            void *buf, hipStream_t st, bool block_major = false, uint32_t *zero = nullptr,
+                            uint32_t nzero = 0);
 
 // Weight encoder: x[nunits][256] fp32 -> nunits units of `type`.
 // Q8_K block-major quantization of the gathered rows x[rows[s]], s < S.
 hipError_t launch_quant_act_rows(const float *x, const uint32_t *rows, uint32_t S, uint32_t cols, const ActLayout &L,
-                                 void *buf, hipStream_t st);
+                                 void *buf, hipStream_t st, uint32_t *zero = nullptr, uint32_t nzero = 0);
 
 hipError_t launch_encode(int type, const float *x, void *out, uint32_t nunits, hipStream_t st);
 
@@ -82,21 +85,29 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
                        int num_cu, void *workspace, hipStream_t st);
 
 // Prefill GEMM with the weights converted in the MFMA lanes' registers, once
-// per token tile of up to 256 tokens (tc_prefill.hip; Q4_K). Needs the
-// activations' digit sums (act.dg) and prefill_workspace_bytes() of scratch.
+// per token tile of up to 128 tokens (tc_prefill.hip; Q4_K, Q8_0). Needs the
+// activations' scale data (act.dg) and prefill_workspace_bytes() of scratch
+// whose first prefill_counter_words() 32-bit words are zero when the launch
+// starts (every launch leaves them zero again).
 bool prefill_type(int type);
+uint32_t prefill_counter_words(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
 size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
 hipError_t launch_prefill(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N,
                           uint32_t K, int num_cu, void *workspace, hipStream_t st);
 
 // Grouped (MoE) form over expert-sorted rows: out[i][n] = act row i . W[e(i)]
 // row n for the token tiles of mt (count *ntm, at most ntm_max; tiles of at
-// most `tile` rows, tile from prefill_grouped_tile).
+// most `tile` rows, tile from prefill_grouped_tile). ctr: the arrival
+// counters, prefill_grouped_counter_words() of them, zero when the launch
+// starts (every launch leaves them zero again); workspace:
+// prefill_grouped_workspace_bytes() for the partial tiles.
 uint32_t prefill_grouped_tile(uint32_t rows_total, uint32_t n_experts);
+uint32_t prefill_grouped_counter_words(uint32_t ntm_max, uint32_t N);
 size_t prefill_grouped_workspace_bytes(uint32_t tile, uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu);
 hipError_t launch_prefill_grouped(const void *W, uint64_t wstride, const ActView &act, float *out,
                                   uint32_t rows_total, uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm,
-                                  uint32_t ntm_max, uint32_t tile, int num_cu, void *workspace, hipStream_t st);
+                                  uint32_t ntm_max, uint32_t tile, int num_cu, uint32_t *ctr, void *workspace,
+                                  hipStream_t st);
 
 // ---- MoE prefill over expert-sorted rows ----
 // Device-side router: pairs p = t*top_k + r (ids[p] in [0, E), others

@@ -50,8 +50,11 @@
 // are divided evenly over one workgroup per CU (stream-K); workgroup ranges
 // are numbered so that the workgroups of one XCD (dispatched round robin over
 // the 8 XCDs) hold one contiguous range and share one token tile's activations
-// in their L2. A tile split over several workgroups is summed by k_pf_fixup
-// in workgroup order (deterministic).
+// in their L2. A tile split over a few workgroups is summed by the last of
+// them to finish its part, in workgroup order (deterministic); the others
+// leave their partial tiles in memory (system-scope stores) and count their
+// arrival on the tile's counter. Tiles split over more workgroups are summed
+// by k_pf_fixup, a second launch, in the same order.
 #include <type_traits>
 
 #include "tc_kernels.hpp"
@@ -104,6 +107,8 @@ struct PfArgs {
     const int8_t *xs;   // Q4_K sum pieces [nblk][M][32 B]; Q8_0 d pieces [nblk][M][64 B]
     float *out;         // [M][N]
     float *ws;          // partial tiles [G][2][TT][PR]
+    uint32_t *ctr;      // per tile: contributors arrived (zero before the launch, zero after it)
+    uint32_t fused;     // split tiles summed by their last contributor (else by k_pf_fixup)
     uint32_t M, N, K;
     uint32_t row_bytes, nblk;
     uint32_t ntm, ntn, ntiles;  // token tiles, row blocks, tiles
@@ -503,33 +508,105 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 
         // lane: row n0 + rl, tokens m0 + 32 (tg NB + t) + 8q + 4g + e
         const uint32_t n = n0 + rl;
+        if (part == nullptr) {
 #pragma unroll
-        for (int t = 0; t < NB; ++t) {
+            for (int t = 0; t < NB; ++t)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t ml = 32 * (tg * NB + t) + 8 * q + 4 * g + e, m = m0 + ml;
+                        if (m < tg_.mend && n < a.N) a.out[size_t(m) * a.N + n] = acc[t][4 * q + e];
+                    }
+            continue;
+        }
+        if (!a.fused) {
+#pragma unroll
+            for (int t = 0; t < NB; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        part[(32 * (tg * NB + t) + 8 * q + 4 * g + e) * PR + rl] = acc[t][4 * q + e];
+            continue;
+        }
+        // A split tile: publish this segment's partial (system-scope stores
+        // go through to memory, where other XCDs' loads find them), then
+        // count the arrival. The last of the tile's contributors to arrive
+        // sums the partials in range order (its own from registers) and
+        // writes the tile; nobody waits for anybody.
+#pragma unroll
+        for (int t = 0; t < NB; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t ml = 32 * (tg * NB + t) + 8 * q + 4 * g + e;
+                    __hip_atomic_store(part + ml * PR + rl, acc[t][4 * q + e], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // this thread's partial is in memory
+        __syncthreads();
+        // contributors: the nonempty ranges from vf (holding the tile's first
+        // unit) to vl (its last); grouped launches size the grid for the
+        // largest tile count, so some ranges may be empty there
+        const uint32_t t0 = tile * a.nblk, t1 = t0 + a.nblk;
+        uint32_t vf = v;
+        while (vf > 0 && sk_begin(units, a.G, vf) > t0) --vf;
+        uint32_t vl = v;
+        while (vl + 1 < a.G && sk_begin(units, a.G, vl + 1) < t1) ++vl;
+        auto live = [&](uint32_t c) __attribute__((always_inline)) {
+            return !GRP || sk_begin(units, a.G, c) != sk_begin(units, a.G, c + 1);
+        };
+        uint32_t ncontrib = 0;
+        for (uint32_t c = vf; c <= vl; ++c) ncontrib += live(c) ? 1u : 0u;
+        uint32_t *const flag = reinterpret_cast<uint32_t *>(lds);  // no LDS reader left (barrier above)
+        if (tid == 0)
+            *flag = __builtin_amdgcn_atomic_inc32(a.ctr + tile, ncontrib - 1, __ATOMIC_RELAXED, "");
+        __syncthreads();
+        const bool last = *flag == ncontrib - 1;  // the counter wrapped back to 0
+        if (!last) continue;
+        const uint32_t first_slot = sk_begin(units, a.G, vf) < t0 ? 1u : 0u;  // vf's second segment
+        // every contributor's partial from memory (this workgroup's too: it
+        // is there already, and acc's registers then hold the sum)
+        for (uint32_t c = vf; c <= vl; ++c) {
+            if (!live(c)) continue;
+            const float *src = a.ws + (size_t(c) * 2 + (c == vf ? first_slot : 0u)) * (TT * PR);
+            uint32_t lo = 4 * g * PR + rl;  // this lane's offset, recomputed per contributor
+            asm volatile("" : "+v"(lo));
+            float p[NB][16];
+#pragma unroll
+            for (int t = 0; t < NB; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        p[t][4 * q + e] = __hip_atomic_load(src + (32 * (tg * NB + t) + 8 * q + e) * PR + lo,
+                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+            for (int t = 0; t < NB; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[t][r] = c == vf ? p[t][r] : acc[t][r] + p[t][r];
+        }
+#pragma unroll
+        for (int t = 0; t < NB; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t ml = 32 * (tg * NB + t) + 8 * q + 4 * g + e, m = m0 + ml;
-                    const float val = acc[t][4 * q + e];
-                    if (part != nullptr)
-                        part[ml * PR + rl] = val;
-                    else if (m < tg_.mend && n < a.N)
-                        a.out[size_t(m) * a.N + n] = val;
+                    if (m < tg_.mend && n < a.N) a.out[size_t(m) * a.N + n] = acc[t][4 * q + e];
                 }
-            }
-        }
     }
 }
 
-// Tiles split over several workgroups: out = the partial segments summed in
-// workgroup (range) order. A split tile is summed by kFixSlices(TT, PR)
+// Tiles split over many workgroups (launches with more than kFusedMax
+// contributors per tile): out = the partial segments summed in workgroup
+// (range) order. A split tile is summed by kFixSlices(TT, PR)
 // workgroups, each a slice of kFixNI float4 per thread; group j takes the
 // tile holding range boundary j + 1 when that boundary splits it and is the
 // first to do so. A thread issues the loads of up to 4 contributors before
 // adding them (in order), so that a CU has many partial lines in flight.
-// (Summing inside the main kernel, by the last contributor to arrive,
-// measured slower: its device-scope release and acquire around the partial
-// tiles cost more than this launch.)
 constexpr uint32_t kFixNI = 2;
 __host__ __device__ constexpr uint32_t kFixSlices(uint32_t TT, uint32_t PR) { return TT * PR / 4 / (256 * kFixNI); }
 template <uint32_t TT, uint32_t PR, bool GRP>
@@ -613,6 +690,19 @@ int pf_nt(int type, uint32_t M) {
 }
 uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }
 
+// Split tiles are summed inside the main kernel, by their last contributor,
+// when no tile has more than kFusedMax contributors: that workgroup reads the
+// others' partial tiles alone (one CU's bandwidth, at the end of the launch),
+// which beats a fixup launch for 2-3 partials and loses to it for more
+// (measured: Q4_K 17408x5120, M=512 (2 per tile) 120 -> 115 us; M=128 (5
+// per tile) 47 -> 56 us).
+constexpr uint32_t kFusedMax = 3;
+bool pf_fused(uint64_t units, uint32_t G, uint32_t nblk) {
+    const uint64_t len = units / G;  // shortest range
+    if (len == 0) return false;
+    return (nblk - 1 + len - 1) / len + 1 <= kFusedMax;
+}
+
 struct PfGeom {
     int nt;
     uint32_t tt, pr, ntm, ntn, ntiles, G;
@@ -639,13 +729,11 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
     if (attr != hipSuccess) return attr;
     k_prefill<TYPE, NT, GRP><<<dim3{a.G, 1u, 1u}, 64 * PW, 2 * L::bytes, st>>>(a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.G == 1) return e;
-    if (!GRP) {  // the split tiles are known on the host; grouped: only on the device
-        const uint32_t units = a.ntiles * a.nblk;
-        bool split = false;
-        for (uint32_t v = 1; v < a.G && !split; ++v) split = sk_begin(units, a.G, v) % a.nblk != 0;
-        if (!split) return hipSuccess;
-    }
+    if (e != hipSuccess || a.fused || a.G == 1) return e;
+    const uint32_t units = a.ntiles * a.nblk;
+    bool split = false;
+    for (uint32_t v = 1; v < a.G && !split; ++v) split = sk_begin(units, a.G, v) % a.nblk != 0;
+    if (!split) return hipSuccess;
     k_pf_fixup<L::TT, PfType<TYPE>::PR, GRP>
         <<<dim3{(a.G - 1) * kFixSlices(L::TT, PfType<TYPE>::PR), 1u, 1u}, 256, 0, st>>>(a);
     return hipGetLastError();
@@ -655,10 +743,18 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
 
 bool prefill_type(int type) { return type == kQ4_K || type == kQ8_0; }
 
+// Workspace: the per-tile arrival counters (256-byte rounded), then the
+// partial tiles, two per workgroup.
+namespace {
+size_t ctr_bytes(uint64_t ntiles) { return (ntiles * 4 + 255) & ~uint64_t(255); }
+}  // namespace
+uint32_t prefill_counter_words(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
+    return prefill_type(type) ? pf_geom(type, M, N, K, num_cu).ntiles : 0;
+}
 size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     if (!prefill_type(type)) return 0;
     const PfGeom g = pf_geom(type, M, N, K, num_cu);
-    return size_t(g.G) * 2 * g.tt * g.pr * 4;
+    return ctr_bytes(g.ntiles) + size_t(g.G) * 2 * g.tt * g.pr * 4;
 }
 
 hipError_t launch_prefill(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N,
@@ -674,7 +770,8 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
     a.d8 = act.d;
     a.xs = act.dg;
     a.out = out;
-    a.ws = static_cast<float *>(workspace);
+    a.ctr = static_cast<uint32_t *>(workspace);
+    a.ws = reinterpret_cast<float *>(static_cast<char *>(workspace) + ctr_bytes(g.ntiles));
     a.M = M;
     a.N = N;
     a.K = K;
@@ -684,6 +781,7 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
     a.ntn = g.ntn;
     a.ntiles = g.ntiles;
     a.G = g.G;
+    a.fused = pf_fused(a.ntiles * a.nblk, a.G, a.nblk) ? 1u : 0u;
     if (type == kQ8_0) return g.nt == 2 ? pf_launch<kQ8_0, 2>(a, st) : pf_launch<kQ8_0, 4>(a, st);
     switch (g.nt) {
         case 1: return pf_launch<kQ4_K, 1>(a, st);
@@ -706,14 +804,19 @@ uint32_t pf_grouped_grid(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
     return uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(uint64_t(num_cu), units / 2)));
 }
 }  // namespace
+uint32_t prefill_grouped_counter_words(uint32_t ntm_max, uint32_t N) {
+    return ntm_max * ((N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR);
+}
 size_t prefill_grouped_workspace_bytes(uint32_t tile, uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
     return size_t(pf_grouped_grid(ntm_max, N, K, num_cu)) * 2 * tile * PfType<kQ4_K>::PR * 4;
 }
 
 hipError_t launch_prefill_grouped(const void *W, uint64_t wstride, const ActView &act, float *out,
                                   uint32_t rows_total, uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm,
-                                  uint32_t ntm_max, uint32_t tile, int num_cu, void *workspace, hipStream_t st) {
-    if (rows_total == 0 || N == 0 || K == 0 || K % 256 || ntm_max == 0 || workspace == nullptr || act.dg == nullptr)
+                                  uint32_t ntm_max, uint32_t tile, int num_cu, uint32_t *ctr, void *workspace,
+                                  hipStream_t st) {
+    if (rows_total == 0 || N == 0 || K == 0 || K % 256 || ntm_max == 0 || workspace == nullptr || ctr == nullptr ||
+        act.dg == nullptr)
         return hipErrorInvalidValue;
     const uint32_t ntn = (N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR;
     if (uint64_t(rows_total) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * 144 >= (uint64_t(1) << 32) ||
@@ -725,6 +828,8 @@ hipError_t launch_prefill_grouped(const void *W, uint64_t wstride, const ActView
     a.d8 = act.d;
     a.xs = act.dg;
     a.out = out;
+    a.ctr = ctr;
+    a.fused = 1;  // the tile count is known on the device only
     a.ws = static_cast<float *>(workspace);
     a.M = rows_total;
     a.N = N;

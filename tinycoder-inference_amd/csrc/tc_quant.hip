@@ -42,7 +42,10 @@ template <int BPW>
 __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int8_t *__restrict__ qs,
                                                    float *__restrict__ d, int16_t *__restrict__ bsums,
                                                    uint16_t *__restrict__ dg, uint32_t nblk_total, uint32_t nbk,
-                                                   uint32_t bm_S) {
+                                                   uint32_t bm_S, uint32_t *zero, uint32_t nzero) {
+    if (blockIdx.x == 0)
+        for (uint32_t i = threadIdx.x; i < nzero; i += 256)
+            __hip_atomic_store(zero + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const uint32_t g0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW;
     if (g0 >= nblk_total) return;
     const uint32_t lane = threadIdx.x & 63;
@@ -65,7 +68,11 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, 
 __global__ __launch_bounds__(256) void k_quant_q8k_rows(const float *__restrict__ x, const uint32_t *__restrict__ rows,
                                                         int8_t *__restrict__ qs, float *__restrict__ d,
                                                         int16_t *__restrict__ bsums, uint16_t *__restrict__ dg,
-                                                        uint32_t nblk_total, uint32_t nbk, uint32_t bm_S) {
+                                                        uint32_t nblk_total, uint32_t nbk, uint32_t bm_S,
+                                                        uint32_t *zero, uint32_t nzero) {
+    if (blockIdx.x == 0)
+        for (uint32_t i = threadIdx.x; i < nzero; i += 256)
+            __hip_atomic_store(zero + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (g >= nblk_total) return;
     const uint32_t s = g / nbk, j = g - s * nbk;
@@ -81,7 +88,11 @@ __global__ __launch_bounds__(256) void k_quant_q8k_rows(const float *__restrict_
 template <int BPW>
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int8_t *__restrict__ qs,
                                                     float *__restrict__ d, uint16_t *__restrict__ dp,
-                                                    uint32_t ngroups, uint32_t nbk, uint32_t bm_S) {
+                                                    uint32_t ngroups, uint32_t nbk, uint32_t bm_S, uint32_t *zero,
+                                                    uint32_t nzero) {
+    if (blockIdx.x == 0)
+        for (uint32_t i = threadIdx.x; i < nzero; i += 256)
+            __hip_atomic_store(zero + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const uint32_t g0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW;
     if (g0 >= ngroups) return;
     const uint32_t lane = threadIdx.x & 63;
@@ -805,35 +816,35 @@ __global__ __launch_bounds__(64) void k_encode(const float *__restrict__ x, uint
 // ---- launchers -----------------------------------------------------------------
 
 hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols, const ActLayout &L,
-                            void *buf, hipStream_t st, bool block_major) {
+                            void *buf, hipStream_t st, bool block_major, uint32_t *zero, uint32_t nzero) {
     const uint32_t nbk = cols / 256, bm_S = block_major ? S : 0;
     int8_t *qs = reinterpret_cast<int8_t *>(static_cast<char *>(buf) + L.qs_off);
     float *d = reinterpret_cast<float *>(static_cast<char *>(buf) + L.d_off);
     if (wtype == kQ8_0) {
         uint16_t *dp = reinterpret_cast<uint16_t *>(static_cast<char *>(buf) + L.dg_off);
         const uint32_t ng = S * (cols / 256);
-        if (ng >= 131072) k_quant_q8_0<4><<<(ng + 15) / 16, 256, 0, st>>>(x, qs, d, dp, ng, nbk, bm_S);
-        else k_quant_q8_0<1><<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, dp, ng, nbk, bm_S);
+        if (ng >= 131072) k_quant_q8_0<4><<<(ng + 15) / 16, 256, 0, st>>>(x, qs, d, dp, ng, nbk, bm_S, zero, nzero);
+        else k_quant_q8_0<1><<<(ng + 3) / 4, 256, 0, st>>>(x, qs, d, dp, ng, nbk, bm_S, zero, nzero);
     } else {
         int16_t *bs = reinterpret_cast<int16_t *>(static_cast<char *>(buf) + L.bs_off);
         uint16_t *dg = reinterpret_cast<uint16_t *>(static_cast<char *>(buf) + L.dg_off);
         const uint32_t nb = S * (cols / 256);
         // 4 blocks per wave from 131072 blocks on (measured: slower than a
         // wave per block at 29k-41k blocks, faster at 139k and more)
-        if (nb >= 131072) k_quant_q8k<4><<<(nb + 15) / 16, 256, 0, st>>>(x, qs, d, bs, dg, nb, nbk, bm_S);
-        else k_quant_q8k<1><<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, dg, nb, nbk, bm_S);
+        if (nb >= 131072) k_quant_q8k<4><<<(nb + 15) / 16, 256, 0, st>>>(x, qs, d, bs, dg, nb, nbk, bm_S, zero, nzero);
+        else k_quant_q8k<1><<<(nb + 3) / 4, 256, 0, st>>>(x, qs, d, bs, dg, nb, nbk, bm_S, zero, nzero);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_quant_act_rows(const float *x, const uint32_t *rows, uint32_t S, uint32_t cols, const ActLayout &L,
-                                 void *buf, hipStream_t st) {
+                                 void *buf, hipStream_t st, uint32_t *zero, uint32_t nzero) {
     const uint32_t nbk = cols / 256, nb = S * nbk;
     char *b = static_cast<char *>(buf);
     k_quant_q8k_rows<<<(nb + 3) / 4, 256, 0, st>>>(x, rows, reinterpret_cast<int8_t *>(b + L.qs_off),
                                                    reinterpret_cast<float *>(b + L.d_off),
                                                    reinterpret_cast<int16_t *>(b + L.bs_off),
-                                                   reinterpret_cast<uint16_t *>(b + L.dg_off), nb, nbk, S);
+                                                   reinterpret_cast<uint16_t *>(b + L.dg_off), nb, nbk, S, zero, nzero);
     return hipGetLastError();
 }
 
