@@ -12,6 +12,22 @@
 
 namespace tc {
 
+// Lane-group reductions with DPP lane moves (no LDS crossbar): xor 1 and
+// xor 2 inside quads, then the mirror of each 8- and 16-lane row segment.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t x) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), CTRL, 0xF, 0xF, false));
+}
+template <int WIDTH, typename Op>
+__device__ __forceinline__ uint32_t group_reduce(uint32_t x, Op op) {
+    static_assert(WIDTH == 2 || WIDTH == 4 || WIDTH == 8 || WIDTH == 16, "groups of 2 to 16 lanes");
+    x = op(x, dpp_move<0xB1>(x));                          // quad_perm [1,0,3,2]
+    if constexpr (WIDTH >= 4) x = op(x, dpp_move<0x4E>(x));   // quad_perm [2,3,0,1]
+    if constexpr (WIDTH >= 8) x = op(x, dpp_move<0x141>(x));  // row_half_mirror
+    if constexpr (WIDTH >= 16) x = op(x, dpp_move<0x140>(x)); // row_mirror
+    return x;
+}
+
 // The block's signed max (its first element of largest |x|) when the block
 // is spread over WIDTH lanes, lane values e[0..N) at block indices base ..
 // base+N-1: the lane's largest |x| and the key 2i + sign of its first element
@@ -26,13 +42,28 @@ __device__ __forceinline__ float first_absmax(const float (&e)[N], int base) {
 #pragma unroll
     for (int i = N - 1; i >= 0; --i)
         if (fabsf(e[i]) == am) key = uint32_t(2 * (base + i)) | (__builtin_bit_cast(uint32_t, e[i]) >> 31);
-    float gm = am;
-#pragma unroll
-    for (int m = 1; m < WIDTH; m <<= 1) gm = fmaxf(gm, __shfl_xor(gm, m));
-    uint32_t kk = am == gm ? key : 0xFFFFFFFFu;
-#pragma unroll
-    for (int m = 1; m < WIDTH; m <<= 1) kk = min(kk, uint32_t(__shfl_xor(int(kk), m)));
-    return (kk & 1u) ? -gm : gm;
+    // the |x| are non-negative floats (never NaN: fmaxf drops NaN), whose
+    // bits order as unsigned integers
+    auto umax = [](uint32_t p, uint32_t q) { return p > q ? p : q; };
+    auto umin = [](uint32_t p, uint32_t q) { return p < q ? p : q; };
+    const uint32_t ab = __builtin_bit_cast(uint32_t, am);
+    if constexpr (WIDTH == 64) {
+        // the whole wave is one block: the 16-lane rows' maxima, then the
+        // lowest lane holding the max (lanes hold increasing indices, so it
+        // holds the smallest key)
+        const uint32_t r = group_reduce<16>(ab, umax);
+        const uint32_t gb = umax(umax(__builtin_amdgcn_readlane(r, 0), __builtin_amdgcn_readlane(r, 16)),
+                                 umax(__builtin_amdgcn_readlane(r, 32), __builtin_amdgcn_readlane(r, 48)));
+        const float gm = __builtin_bit_cast(float, gb);
+        const uint64_t hit = __ballot(ab == gb);
+        const uint32_t k0 = __builtin_amdgcn_readlane(key, __builtin_ctzll(hit));
+        return (k0 & 1u) ? -gm : gm;
+    } else {
+        const uint32_t gb = group_reduce<WIDTH>(ab, umax);
+        const uint32_t kk = group_reduce<WIDTH>(ab == gb ? key : 0xFFFFFFFFu, umin);
+        const float gm = __builtin_bit_cast(float, gb);
+        return (kk & 1u) ? -gm : gm;
+    }
 }
 
 // rne(iscale * x) (the product rounded once, then to the nearest integer,

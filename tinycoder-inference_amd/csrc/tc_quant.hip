@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, 
     if (blockIdx.x == 0)
         for (uint32_t i = threadIdx.x; i < nzero; i += 256)
             __hip_atomic_store(zero + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    const uint32_t g0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW;
+    const uint32_t g0 = (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * BPW;
     if (g0 >= nblk_total) return;
     const uint32_t lane = threadIdx.x & 63;
     float4 v[BPW];
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(256) void k_quant_q8k_rows(const float *__restrict_
     if (blockIdx.x == 0)
         for (uint32_t i = threadIdx.x; i < nzero; i += 256)
             __hip_atomic_store(zero + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t g = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (g >= nblk_total) return;
     const uint32_t s = g / nbk, j = g - s * nbk;
     const uint32_t o = act_dst_block(g, nbk, bm_S);
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x,
     if (blockIdx.x == 0)
         for (uint32_t i = threadIdx.x; i < nzero; i += 256)
             __hip_atomic_store(zero + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    const uint32_t g0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW;
+    const uint32_t g0 = (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * BPW;
     if (g0 >= ngroups) return;
     const uint32_t lane = threadIdx.x & 63;
     float4 v[BPW];
