@@ -311,15 +311,16 @@ __device__ __forceinline__ void q8_convert(const unsigned char *row, uint32_t g,
     }
 }
 
-// One 32-token block: per 32-wide weight block k, the exact integer product
-// I (int8 MFMA) and the scales dw*d8 of its 32x32 outputs (bf16 MFMA), then
-// acc += I * scale.
+// One 32-token block (the token's activation pieces at prow, those of block
+// k at prow + 256 (k / 2) + 8 (k % 2)): per 32-wide weight block k, the
+// exact integer product I (int8 MFMA) and the scales dw*d8 of its 32x32
+// outputs (bf16 MFMA), then acc += I * scale.
 __device__ __forceinline__ void q8_block(const unsigned char *arow, const unsigned char *prow, const Q8Frag &f,
                                          uint32_t j, uint32_t g, float (&acc)[16]) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const v4i af = as_v4i(lds4(arow + 16 * ((2 * k + g) ^ (j & 15))));
-        const uint2 pp = *reinterpret_cast<const uint2 *>(prow + 8 * k);
+        const uint2 pp = *reinterpret_cast<const uint2 *>(prow + 256 * (k >> 1) + 8 * (k & 1));
         const v16i I = mfma(af, f.bw[k], v16i{});
         const v16f S = mfma_bf16(v4i{int(pp.x), int(pp.y), int(pp.x), int(pp.y)}, f.bp[k], v16f{});
 #pragma unroll
@@ -403,8 +404,11 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
         const v4i rd = rs4(a.d8, a.M * a.nblk * 4);
         each_inst<(TT + 63) / 64>(w, [&](uint32_t k) { lds_load4(base + L::D8 + 256 * k, rd, (tb + 64 * k + ln) * 4); });
     } else {
+        // chunk-major per 16 tokens: slot 16c + t of group k holds chunk c
+        // (blocks 2c, 2c + 1) of token 16k + t, so that the 32 tokens' reads
+        // of one block fall on distinct banks
         each_inst<TT * T::XB / 1024>(w, [&](uint32_t k) {
-            lds_load16(base + L::XS + 1024 * k, rx, tb * T::XB + 1024 * k + 16 * ln);
+            lds_load16(base + L::XS + 1024 * k, rx, (tb + 16 * k + (ln & 15)) * T::XB + 16 * (ln >> 4));
         });
     }
     constexpr uint32_t CPR = T::UB / 16;  // 16-byte chunks per row
@@ -499,7 +503,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 for (int t = 0; t < NB; ++t) {
                     __builtin_amdgcn_sched_barrier(0);
                     const uint32_t tok = 32 * (tg * NB + t) + j;
-                    q8_block(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB, f, j, g, acc[t]);
+                    q8_block(bb + L::QS + tok * 256, bb + L::XS + 1024 * (tok >> 4) + 16 * (tok & 15), f, j, g, acc[t]);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
