@@ -278,8 +278,9 @@ __device__ __forceinline__ void q4_block(const unsigned char *arow, const unsign
 
 // ---- Q8_0: B operands of one superblock ------------------------------------
 
-// The 8 blocks of this lane's row (34-byte blocks, so 2-byte aligned): the
-// 16 values of k-half g of each block as one B operand, and each block's
+// The 8 blocks of this lane's row (34-byte blocks, so 2-byte aligned; read
+// as the 16-byte chunks that hold them, conflict-free at the 272-byte row
+// stride): the 16 values of k-half g of each block as one B operand, and each block's
 // scale as bf16 pieces dw = h + l (l exact: dw has 11 significant bits) laid
 // out against the activation pieces [h8 m8 l8 0 h8 m8 l8 0]: slots 0-3 times
 // h, 4-7 times l (zero in k-half 1, which the activation side leaves free).
@@ -290,17 +291,21 @@ struct Q8Frag {
 __device__ __forceinline__ void q8_convert(const unsigned char *row, uint32_t g, Q8Frag &f) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const uint32_t off = 34 * k + 2 + 16 * g;  // the 16 values (k even: 2 mod 4; odd: 0 mod 4)
-        if ((k & 1) == 0) {
-            uint32_t dw[5];
-#pragma unroll
-            for (int i = 0; i < 5; ++i) dw[i] = lds1(row + off - 2 + 4 * i);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) f.bw[k][i] = int(__builtin_amdgcn_alignbyte(dw[i + 1], dw[i], 2));
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) f.bw[k][i] = int(lds1(row + off + 4 * i));
+        // the 16 values start at byte 34k + 2 + 16g: in the 16-byte chunks
+        // cs + g and cs + g + 1 (cs = (34k + 2) / 16) at shift sh
+        const int sb = 34 * k + 2, cs = sb / 16, sh = sb % 16;  // constants once unrolled
+        const unsigned char *cp = row + 16 * (cs + g);
+        uint32_t v[8] = {};
+        const u4 lo = lds4(cp);
+        v[0] = lo.x, v[1] = lo.y, v[2] = lo.z, v[3] = lo.w;
+        if (sh != 0) {
+            const u4 hi = lds4(cp + 16);
+            v[4] = hi.x, v[5] = hi.y, v[6] = hi.z, v[7] = hi.w;
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            f.bw[k][i] = sh % 4 == 0 ? int(v[sh / 4 + i])
+                                     : int(__builtin_amdgcn_alignbyte(v[sh / 4 + i + 1], v[sh / 4 + i], sh % 4));
         const uint32_t dword = lds1(row + ((34 * k) & ~3u));
         const uint32_t dbits = (k & 1) ? dword >> 16 : dword & 0xFFFFu;
         const float d = h2f(dbits);
