@@ -1,7 +1,7 @@
 // tc_gemm.hip -- prefill GEMM: out[m][n] = W[n] . x[m] for M tokens against raw
-// GGUF weight rows of Q5_K, Q6_K, IQ3_XXS, IQ3_S and IQ2_S, on the int8
-// matrix cores (v_mfma_i32_32x32x32_i8). (Q4_K and Q8_0, the config-4 types,
-// run the register-conversion kernel of tc_prefill.hip.)
+// GGUF weight rows of Q5_K, Q6_K, IQ3_S and IQ2_S, on the int8 matrix cores
+// (v_mfma_i32_32x32x32_i8). (Q4_K, Q8_0 and IQ3_XXS run the
+// register-conversion kernel of tc_prefill.hip.)
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698) with
 // the CPU reference's numerics: the activations are quantized by the same
@@ -27,8 +27,8 @@
 //    more pair of MFMAs over 8 useful k-slots, with the activation pair sums
 //    split into int8 digits the same way. Per superblock and output: acc +=
 //    d8 * (d*main - dmin*min). (The Q4_K producer code is shared with it.)
-//  * Q6_K, IQ3_XXS, IQ3_S and IQ2_S write their signed integer weights
-//    (sc*(q-32), (2ls+1)*(+-grid value)) as signed digits and have no min term.
+//  * Q6_K, IQ3_S and IQ2_S write their signed integer weights (sc*(q-32),
+//    (2ls+1)*(+-grid value)) as signed digits and have no min term.
 //
 // MFMA operands: lane l feeds row (l & 31) and the 16 bytes of k-group
 // (l >> 5) of both A (weights) and B (activations), so each product pairs the
@@ -52,17 +52,17 @@ constexpr int PL = 272;       // LDS plane row stride (256 + 16: conflict-free b
 // workgroups fit a CU and one's conversion / epilogue overlaps the other's
 // MFMA work.
 // Weight types whose products run on int8 digit planes: every weight of a
-// superblock becomes an exact integer e (Q4_K sc*q, Q6_K sc*(q-32), IQ3_XXS
-// (2ls+1)*signed grid value) written as two int8 planes, 128*hi + lo.
+// superblock becomes an exact integer e (Q4_K sc*q, Q6_K sc*(q-32), IQ3_S
+// and IQ2_S (2ls+1)*signed grid value) written as two int8 planes, 128*hi + lo.
 __host__ __device__ constexpr bool dig_type(int t) {
-    return t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ3_XXS || t == kIQ3_S || t == kIQ2_S;
+    return t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ3_S || t == kIQ2_S;
 }
 // K-quants with a per-sub-block min (w = d*sc*q - dmin*m): the min term runs
 // on one more MFMA pair against the activation pair sums.
 __host__ __device__ constexpr bool min_type(int t) { return t == kQ4_K || t == kQ5_K; }
 // Codebook bytes the converter reads from LDS (past the two stage buffers).
 __host__ __device__ constexpr uint32_t grid_bytes(int t) {
-    return t == kIQ3_XXS ? 256 * 4 : t == kIQ3_S ? 512 * 4 : t == kIQ2_S ? 1024 * 8 : 0;
+    return t == kIQ3_S ? 512 * 4 : t == kIQ2_S ? 1024 * 8 : 0;
 }
 
 template <int TYPE>
@@ -72,7 +72,7 @@ struct GLds {
     static constexpr uint32_t A0 = 0;                                 // Q4_K hi plane / Q8_0 weights [GN][PL]
     static constexpr uint32_t A1 = A0 + GN * PL;                      // Q4_K lo plane [GN][PL]
     static constexpr uint32_t AM = A1 + (K ? GN * PL : 0);            // Q4_K mins, 8 bytes + 24 zero [GN][32]
-    static constexpr uint32_t AS = AM + (M4 ? GN * 32 : 0);           // row d [GN] (IQ3_XXS: d/4) | Q8_0 dw [GN][8]
+    static constexpr uint32_t AS = AM + (M4 ? GN * 32 : 0);           // row d [GN] (IQ2_S: d/8) | Q8_0 dw [GN][8]
     static constexpr uint32_t AD = AS + (K ? GN * 4 : GN * 32);       // Q4_K dmin [GN]
     // activation int8 [GM][BP]; Q4_K: 256-byte rows, 16-byte chunk j of
     // token t at slot j ^ (t & 15) (written by direct-to-LDS loads)
@@ -141,18 +141,17 @@ struct GPrefetch {
     // and IQ2_S: the bytes of the two 32-chunks 2qq, 2qq+1 (4-byte-aligned
     // words, realigned on conversion); Q6_K: its 16-byte runs of ql (two) and qh,
     // read from 4-byte-aligned addresses (blocks are 2-byte aligned) with
-    // their fifth dwords in ex, then the scale bytes and d; IQ3_XXS: its 16
-    // grid-index bytes (+1 dword), its 8 scale/sign bytes and d. Q8_0: raw
-    // 16-byte chunks of the tile.
+    // their fifth dwords in ex, then the scale bytes and d. Q8_0: raw 16-byte
+    // chunks of the tile.
     static constexpr int RAWC = TYPE == kQ4_K || TYPE == kQ6_K       ? 3
                                 : TYPE == kQ5_K                       ? 5
-                                : TYPE == kIQ3_XXS || TYPE == kIQ3_S  ? 1
+                                : TYPE == kIQ3_S                      ? 1
                                 : TYPE == kIQ2_S                      ? 0
                                                                       : (GN * 272 / 16 + GT - 1) / GT;
-    static constexpr int EXC = TYPE == kQ6_K || TYPE == kIQ3_S ? 7 : TYPE == kIQ3_XXS ? 5 : TYPE == kIQ2_S ? 9 : 1;
+    static constexpr int EXC = TYPE == kQ6_K || TYPE == kIQ3_S ? 7 : TYPE == kIQ2_S ? 9 : 1;
     u4 raw[RAWC > 0 ? RAWC : 1];
     uint32_t ex[EXC];
-    uint32_t sh;           // Q6_K / IQ3_XXS: the block's byte offset mod 4
+    uint32_t sh;           // Q6_K, IQ3_S, IQ2_S: the block's byte offset mod 4
     static constexpr int ACTC = TYPE == kQ8_0 ? GM * 16 / GT : 0;
     u4 act[ACTC > 0 ? ACTC : 1];  // 16-byte activation chunks (Q8_0; Q4_K loads them straight into LDS)
     u4 side;               // Q8_K bsums (256 chunks) or Q8_0 d (256 chunks)
@@ -165,7 +164,7 @@ struct GPrefetch {
 struct GSrc {
     __amdgpu_buffer_rsrc_t w, q, d, bs;
     uint32_t vw, vw2, vq, vd, vbs;  // per-lane offsets (vw2: Q4_K quant bytes / unused)
-    uint32_t vo[4];                 // Q6_K / IQ3_XXS: this thread's byte offsets inside a block
+    uint32_t vo[4];                 // Q6_K: this thread's byte offsets inside a block; IQ types: vo[3] the quarter
     uint32_t vr[5];                 // Q8_0 raw chunks
 };
 
@@ -191,13 +190,6 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
         g.vo[1] = 64 * n + 32 + 16 * pp;
         g.vo[2] = 128 + 32 * n + 16 * pp;
         g.vo[3] = 192 + 8 * n;
-    } else if constexpr (TYPE == kIQ3_XXS) {
-        // thread (row tid/4, quarter qq): grid indices qs[16qq ..] at 2 + 16qq,
-        // the two scale/sign words at 66 + 8qq
-        const uint32_t qq = tid & 3;
-        g.vo[0] = 2 + 16 * qq;
-        g.vo[1] = 66 + 8 * qq;
-        g.vo[2] = g.vo[3] = 0;
     } else {
         g.vo[0] = g.vo[1] = g.vo[2] = 0;
         g.vo[3] = tid & 3;  // IQ3_S / IQ2_S: the thread's quarter
@@ -270,15 +262,6 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
 #pragma unroll
         for (int i = 0; i < 3; ++i) p.ex[3 + i] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + g.vo[3] + 4 * i, 0, 0);
         p.ex[6] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + 208, 0, 0);  // d (bytes 208, 209)
-    } else if constexpr (TYPE == kIQ3_XXS) {
-        const uint32_t blk = g.vw + b * UB;
-        p.sh = blk & 3;
-        const uint32_t al = blk & ~3u, alq = (blk + 2) & ~3u;  // d at 0; qs and signs at 2 mod 4 from it
-        p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, alq + g.vo[0] - 2, 0, 0);
-        p.ex[0] = __builtin_amdgcn_raw_buffer_load_b32(g.w, alq + g.vo[0] - 2 + 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 3; ++i) p.ex[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(g.w, alq + g.vo[1] - 2 + 4 * i, 0, 0);
-        p.ex[4] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al, 0, 0);
     } else {
 #pragma unroll
         for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i)
@@ -369,7 +352,7 @@ __device__ __forceinline__ void digits_q6(uint32_t q, int sc, uint32_t &hi, uint
     digits_s16(ve, vo, short(sc), hi, lo);
 }
 
-// Four signed bytes per word (IQ3_XXS signed grid values) -> digits of k * v.
+// Four signed bytes per word (signed grid values) -> digits of k * v.
 __device__ __forceinline__ void digits_i8(uint32_t v, int k, uint32_t &hi, uint32_t &lo) {
     // sign extension per 16-bit lane: (b ^ 0x80) - 0x80
     const s16x2 ve = __builtin_bit_cast(s16x2, (v & 0x00FF00FFu) ^ 0x00800080u) - s16x2{128, 128};
@@ -418,47 +401,6 @@ __device__ __forceinline__ void q6k_convert(const GPrefetch<kQ6_K> &p, unsigned 
         *reinterpret_cast<u4 *>(a1 + k0) = u4{lo[0], lo[1], lo[2], lo[3]};
     }
     reinterpret_cast<float *>(lds + L::AS)[r] = h2f(dh);
-}
-
-// IQ3_XXS weights of this thread (row tid/4, 32-chunks 2qq, 2qq+1) -> the
-// digit planes and d/4 (the 0.25 row scale of the reference's fused path,
-// include/GGMLDequantize.hpp:2148, is a power of two: exact on d). Per 4
-// weights one codebook word (grid in LDS) with the chunk's sign bits applied
-// bytewise (sign byte = 7-bit index | parity << 7), times 2ls+1
-// (GGMLDequantize.hpp:1135-1161).
-__device__ __forceinline__ void iq3_convert(const GPrefetch<kIQ3_XXS> &p, unsigned char *lds, const uint32_t *grid,
-                                            uint32_t tid) {
-    using L = GLds<kIQ3_XXS>;
-    const uint32_t r = tid / 4, qq = tid & 3;
-    const uint32_t shq = p.sh ^ 2u;  // qs and signs sit 2 bytes off the block start's alignment
-    const uint32_t v[5] = {p.raw[0].x, p.raw[0].y, p.raw[0].z, p.raw[0].w, p.ex[0]};
-    uint32_t gi[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) gi[j] = realign(v[j + 1], v[j], shq);
-    const uint32_t aux[2] = {realign(p.ex[2], p.ex[1], shq), realign(p.ex[3], p.ex[2], shq)};
-    const uint32_t dh = p.sh ? (p.ex[4] >> 16) : (p.ex[4] & 0xFFFFu);
-    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-        const int k = 2 * int(aux[ch] >> 28) + 1;
-        uint32_t hi[8], lo[8];
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const uint32_t idx7 = (aux[ch] >> (7 * l)) & 127u;
-            const uint32_t s8 = idx7 | ((__builtin_popcount(idx7) & 1u) << 7);
-            const uint32_t gw = gi[2 * ch + (l >> 1)];
-            const uint32_t g1 = grid[(gw >> (16 * (l & 1))) & 0xFFu], g2 = grid[(gw >> (16 * (l & 1) + 8)) & 0xFFu];
-            const uint32_t m1 = spread_sign4(s8 & 15u), m2 = spread_sign4(s8 >> 4);
-            digits_i8((g1 ^ m1) + (m1 & 0x01010101u), k, hi[2 * l], lo[2 * l]);
-            digits_i8((g2 ^ m2) + (m2 & 0x01010101u), k, hi[2 * l + 1], lo[2 * l + 1]);
-        }
-        const uint32_t k0 = 64 * qq + 32 * ch;
-        *reinterpret_cast<u4 *>(a0 + k0) = u4{hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<u4 *>(a0 + k0 + 16) = u4{hi[4], hi[5], hi[6], hi[7]};
-        *reinterpret_cast<u4 *>(a1 + k0) = u4{lo[0], lo[1], lo[2], lo[3]};
-        *reinterpret_cast<u4 *>(a1 + k0 + 16) = u4{lo[4], lo[5], lo[6], lo[7]};
-    }
-    reinterpret_cast<float *>(lds + L::AS)[r] = 0.25f * h2f(dh);
 }
 
 // IQ3_S weights of this thread (row tid/4, 32-chunks ib = 2qq + c) -> the
@@ -545,9 +487,6 @@ __device__ __forceinline__ void iq2s_convert(const GPrefetch<kIQ2_S> &p, unsigne
     reinterpret_cast<float *>(lds + L::AS)[r] = 0.125f * h2f(dh);
 }
 
-__constant__ uint32_t c_iq3_grid[256] = {
-#include "iq3xxs_grid.inc"
-};
 __constant__ uint32_t c_iq3s_grid[512] = {
 #include "iq3s_grid.inc"
 };
@@ -572,8 +511,6 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
         iq2s_convert(p, lds, grid, tid);
     } else if constexpr (TYPE == kQ6_K) {
         q6k_convert(p, lds, tid);
-    } else if constexpr (TYPE == kIQ3_XXS) {
-        iq3_convert(p, lds, grid, tid);
     } else {
 #pragma unroll
         for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
@@ -804,12 +741,10 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
     const uint32_t li = lane & 31, lg = lane >> 5;
     const uint32_t ptid = tid - 64 * CW;  // producer thread index 0..255
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
-    // IQ3_XXS / IQ3_S / IQ2_S codebook in LDS, past the two buffers (read by the producers' conversion)
+    // IQ3_S / IQ2_S codebook in LDS, past the two buffers (read by the producers' conversion)
     uint32_t *grid = reinterpret_cast<uint32_t *>(lds + 2 * L::bytes);
     if constexpr (grid_bytes(TYPE) != 0) {
-        const uint32_t *src = TYPE == kIQ3_XXS ? c_iq3_grid
-                              : TYPE == kIQ3_S ? c_iq3s_grid
-                                               : reinterpret_cast<const uint32_t *>(c_iq2s_grid);
+        const uint32_t *src = TYPE == kIQ3_S ? c_iq3s_grid : reinterpret_cast<const uint32_t *>(c_iq2s_grid);
         for (uint32_t i = tid; i < grid_bytes(TYPE) / 4; i += blockDim.x) grid[i] = src[i];
         __syncthreads();
     }
@@ -1027,7 +962,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
     // weight matrix must each stay below 4 GiB.
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
-    // Q4_K and Q8_0 run k_prefill (tc_prefill.hip); the other MFMA types here.
+    // Q4_K, Q8_0 and IQ3_XXS run k_prefill (tc_prefill.hip); the other MFMA types here.
     if (!dig_type(type) || type == kQ4_K) return hipErrorInvalidValue;
     const uint32_t nsplit = gemm_splits(type, M, N, K, num_cu);
     if ((nsplit > 1 || dig_type(type)) && workspace == nullptr) return hipErrorInvalidValue;
@@ -1053,8 +988,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
         hipError_t e = type == kQ5_K     ? launch_gemm_t<kQ5_K>(a, g, st)
                        : type == kQ6_K   ? launch_gemm_t<kQ6_K>(a, g, st)
                        : type == kIQ3_S  ? launch_gemm_t<kIQ3_S>(a, g, st)
-                       : type == kIQ2_S  ? launch_gemm_t<kIQ2_S>(a, g, st)
-                                         : launch_gemm_t<kIQ3_XXS>(a, g, st);
+                                         : launch_gemm_t<kIQ2_S>(a, g, st);
         if (e != hipSuccess) return e;
         // Any tile split over workgroups? (a range boundary inside a tile)
         bool split = false;

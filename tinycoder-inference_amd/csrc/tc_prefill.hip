@@ -1,14 +1,14 @@
-// tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K and Q8_0
-// weights on the int8 matrix cores (v_mfma_i32_32x32x32_i8). The weights of a
-// tile are converted once per token tile of up to 128 tokens, in the
-// registers of the lanes that feed them to the MFMA.
+// tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K, Q8_0 and
+// IQ3_XXS weights on the int8 matrix cores (v_mfma_i32_32x32x32_i8). The
+// weights of a tile are converted once per token tile of up to 128 tokens,
+// in the registers of the lanes that feed them to the MFMA.
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698 and
 // its stream-K kernel GemmKernels.cuh:3707-4030) with the CPU reference's
 // numerics: the activations are quantized by the bit-exact quantizers (Q8_K
-// for Q4_K, the 32-wide Q8_0 rule for Q8_0), every integer dot product of a
-// weight block with an activation block is exact, and only the scale
-// combination runs in fp32.
+// for Q4_K and IQ3_XXS, the 32-wide Q8_0 rule for Q8_0), every integer dot
+// product of a weight block with an activation block is exact, and only the
+// scale combination runs in fp32.
 //
 // Decomposition. A workgroup has 8 waves (two per SIMD). Per 256-wide
 // superblock of K, the tile's activations (int8 values and their scale data)
@@ -21,6 +21,8 @@
 //  * Q8_0: 128 rows per workgroup, waves w and w + 4 share rows and take one
 //    half of the tile's tokens each (the Q8_0 weight blocks take 272 bytes of
 //    LDS per row and superblock).
+//  * IQ3_XXS: as Q4_K (256 rows); the sign-applied codebook is built in LDS
+//    once per workgroup.
 //
 // Q4_K (reference dequantizeQ4_KBlock, GGMLDequantize.hpp:436-477): a weight
 // of sub-block s is w = d*sc_s*q - dmin*m_s with q in 0..15 and sc_s, m_s in
@@ -85,19 +87,32 @@ template <>
 struct PfType<kQ8_0> {
     static constexpr uint32_t PR = 128, TSPLIT = 2, UB = 272, XB = 64;
 };
+// IQ3_XXS: a row's 98-byte unit is 2-byte aligned; LDS holds the 100-byte
+// window from its 4-byte-aligned start down: 6 chunks at a 112-byte row
+// stride (conflict-free 16-byte reads) and the last dword in TAIL.
+template <>
+struct PfType<kIQ3_XXS> {
+    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 112, XB = 0;
+};
 
 // One LDS buffer: [TT][256] activation values (16-byte chunk c of token t at
-// slot c ^ (t & 15)), [TT][XB] scale data, Q4_K's [max(TT, 64)] fp32 d,
-// [PR][UB] raw weight blocks.
+// slot c ^ (t & 15)), [TT][XB] scale data, the Q8_K types' [max(TT, 64)]
+// fp32 d, [PR][UB] raw weight blocks. IQ3_XXS's signed grid (256 x 16
+// words, one copy per workgroup, at offset 0 so that a lookup's address is
+// its index times 4), then the two buffers.
 template <int TYPE, int NT>
 struct PLds {
     using T = PfType<TYPE>;
     static constexpr uint32_t TT = 32 * NT;
+    static constexpr uint32_t GRID = 0;  // IQ3_XXS's signed grid (before the two buffers)
+    static constexpr uint32_t BUF0 = TYPE == kIQ3_XXS ? 256 * 16 * 4 : 0;
     static constexpr uint32_t QS = 0;
     static constexpr uint32_t XS = TT * 256;
     static constexpr uint32_t D8 = XS + TT * T::XB;
-    static constexpr uint32_t W = D8 + (TYPE == kQ4_K ? (TT < 64 ? 64 : TT) * 4 : 0);
-    static constexpr uint32_t bytes = W + T::PR * T::UB;
+    static constexpr uint32_t W = D8 + (TYPE != kQ8_0 ? (TT < 64 ? 64 : TT) * 4 : 0);
+    static constexpr uint32_t TAIL = W + T::PR * T::UB;
+    static constexpr uint32_t bytes = TAIL + (TYPE == kIQ3_XXS ? T::PR * 4 : 0);
+    static constexpr uint32_t total = BUF0 + 2 * bytes;
 };
 
 struct PfArgs {
@@ -333,6 +348,119 @@ __device__ __forceinline__ void q8_block(const unsigned char *arow, const unsign
     }
 }
 
+
+// ---- IQ3_XXS: B operands of one superblock ---------------------------------
+// Reference dequantizeIQ3_XXSBlock (GGMLDequantize.hpp:1135-1161) and the
+// fused dot (:2064-2097): per 32-block ib, 8 grid indices (qs, 4 weights
+// each), and aux = 4 7-bit sign indices (sign byte = idx | parity(idx) << 7)
+// and the scale ls in bits 28-31; a weight is d * (0.5 + ls) * 0.5 * grid
+// byte * sign, i.e. (d / 4) * (2 ls + 1) * signed grid byte. The signed
+// grid bytes (|w| <= 62) are the int8 B operand as they are, so one MFMA per
+// 32-block gives the exact integer I_ib; isum = sum_ib (2 ls + 1) I_ib by
+// 24-bit integer multiply-adds (|I| < 2^18), then acc += (d / 4) * d8 * isum.
+
+__constant__ uint32_t c_pf_iq3_grid[256] = {
+#include "iq3xxs_grid.inc"
+};
+
+struct I3Frag {
+    v4i bw[8];  // the signed grid bytes of k-half g of each 32-block
+    int sc[8];  // 2 ls + 1
+    float d;    // d / 4
+};
+
+// This lane's row: the 100-byte window (its unit at byte sh of it) in the
+// row's LDS chunks, its bytes 96-99 in tail. Fields are read as 2-byte
+// halves (the unit is 2-byte aligned). sgrid: the signed grid in LDS, entry
+// 16 i + n = grid word i with the signs of nibble n applied bytewise.
+__device__ __forceinline__ void i3_convert(const unsigned char *row, const unsigned char *tail, uint32_t sh,
+                                           const uint32_t *sgrid, uint32_t g, I3Frag &f) {
+    auto h16 = [&](uint32_t x) __attribute__((always_inline)) {  // window bytes x, x + 1 (x even, < 96)
+        return uint32_t(*reinterpret_cast<const uint16_t *>(row + x));
+    };
+    f.d = 0.25f * h2f(h16(sh));
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        const uint32_t qo = sh + 2 + 8 * ib + 4 * g, ao = sh + 66 + 4 * ib;
+        const uint32_t qsw = h16(qo) | (h16(qo + 2) << 16);
+        uint32_t aux;
+        if (ib < 7) {
+            aux = h16(ao) | (h16(ao + 2) << 16);
+        } else {  // window bytes sh + 94 .. sh + 97: the last ones in tail
+            const uint32_t t = *reinterpret_cast<const uint32_t *>(tail);
+            aux = sh ? t : __builtin_amdgcn_alignbyte(t, h16(94) << 16, 2);
+        }
+        f.sc[ib] = 2 * int(aux >> 28) + 1;
+        uint32_t e[4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {  // sign group l = 2g + u: 8 weights, grid indices bytes 2u, 2u + 1 of qsw
+            const uint32_t s7 = __builtin_amdgcn_ubfe(aux, 14 * g + 7 * u, 7);
+            const uint32_t s8 = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+            e[2 * u] = sgrid[(__builtin_amdgcn_ubfe(qsw, 16 * u, 8) << 4) | (s8 & 15u)];
+            e[2 * u + 1] = sgrid[(__builtin_amdgcn_ubfe(qsw, 16 * u + 8, 8) << 4) | (s8 >> 4)];
+        }
+        f.bw[ib] = v4i{int(e[0]), int(e[1]), int(e[2]), int(e[3])};
+    }
+}
+
+// P (1 or 2) 32-token blocks (activation rows arow[t], token scales d8[t]):
+// per 32-block the MFMAs of all P token blocks first, then their integer
+// multiply-adds (so that no multiply-add waits for the MFMA issued just
+// before it).
+template <int P>
+__device__ __forceinline__ void i3_blocks(const unsigned char *const (&arow)[P], const float *const (&d8)[P],
+                                          const I3Frag &f, uint32_t j, uint32_t g, float (&acc)[P][16]) {
+    int is[P][16];
+#pragma unroll
+    for (int t = 0; t < P; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) is[t][r] = 0;
+    auto aread = [&](int ib, int t) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow[t] + 16 * ((2 * ib + g) ^ (j & 15))));
+    };
+    // activation fragments one 32-block ahead; the scheduling barriers keep
+    // that order (the scheduler otherwise reads each right before its MFMA
+    // and runs each block's multiply-adds right after its own MFMA)
+    v4i af[2][P];
+#pragma unroll
+    for (int t = 0; t < P; ++t) af[0][t] = aread(0, t);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        if (ib + 1 < 8)
+#pragma unroll
+            for (int t = 0; t < P; ++t) af[(ib + 1) & 1][t] = aread(ib + 1, t);
+        v16i I[P];
+#pragma unroll
+        for (int t = 0; t < P; ++t) I[t] = mfma(af[ib & 1][t], f.bw[ib], v16i{});
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < P; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                is[t][r] = __mul24(f.sc[ib], I[t][r]) + is[t][r];  // v_mad_i32_i24
+                // kept as one multiply-add per 32-block: the compiler would
+                // otherwise reassociate the chain into multiplies and 3-way adds
+                asm("" : "+v"(is[t][r]));
+            }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    float4 dv[P][4];
+#pragma unroll
+    for (int t = 0; t < P; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dv[t][q] = *reinterpret_cast<const float4 *>(d8[t] + 8 * q);
+#pragma unroll
+    for (int t = 0; t < P; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float dd[4] = {dv[t][q].x, dv[t][q].y, dv[t][q].z, dv[t][q].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc[t][4 * q + e] = fmaf(dd[e] * f.d, float(is[t][4 * q + e]), acc[t][4 * q + e]);
+        }
+}
+
 // ---- loads into LDS ---------------------------------------------------------
 
 // Direct-to-LDS buffer loads (no registers, no LDS stores): lane l's 16 (or
@@ -402,10 +530,11 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
         lds_load16(base + L::QS + 1024 * k, rq, (tb + t) * 256 + 16 * ((ln & 15) ^ (t & 15)));
     });
     const v4i rx = rs4(a.xs, a.M * a.nblk * T::XB);
-    if constexpr (TYPE == kQ4_K) {
-        each_inst<TT / 32>(w, [&](uint32_t k) {
-            lds_load16(base + L::XS + 1024 * k, rx, (tb + 32 * k) * T::XB + 16 * ln);
-        });
+    if constexpr (TYPE != kQ8_0) {
+        if constexpr (T::XB != 0)
+            each_inst<TT / 32>(w, [&](uint32_t k) {
+                lds_load16(base + L::XS + 1024 * k, rx, (tb + 32 * k) * T::XB + 16 * ln);
+            });
         const v4i rd = rs4(a.d8, a.M * a.nblk * 4);
         each_inst<(TT + 63) / 64>(w, [&](uint32_t k) { lds_load4(base + L::D8 + 256 * k, rd, (tb + 64 * k + ln) * 4); });
     } else {
@@ -420,8 +549,15 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
     const v4i rw = rs4(W, a.N * a.row_bytes);
     each_inst<T::PR * CPR / 64>(w, [&](uint32_t k) {
         const uint32_t c = 64 * k + ln, r = c / CPR, p = c - CPR * r;
-        lds_load16(base + L::W + 1024 * k, rw, (n0 + r) * a.row_bytes + b * T::UB + 16 * p);
+        if constexpr (TYPE == kIQ3_XXS)  // the window from the unit's 4-byte-aligned start (slot 6: unused)
+            lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 98) & ~3u) + 16 * min(p, 5u));
+        else
+            lds_load16(base + L::W + 1024 * k, rw, (n0 + r) * a.row_bytes + b * T::UB + 16 * p);
     });
+    if constexpr (TYPE == kIQ3_XXS)  // the window's 25th dword (ends at most 2 bytes past the unit)
+        each_inst<T::PR / 64>(w, [&](uint32_t k) {
+            lds_load4(base + L::TAIL + 256 * k, rw, (((n0 + 64 * k + ln) * a.row_bytes + b * 98) & ~3u) + 96);
+        });
 }
 
 __host__ __device__ inline uint32_t sk_begin(uint32_t units, uint32_t grid, uint32_t v) {
@@ -445,8 +581,18 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t rg = w % RG, tg = w / RG;      // row group, token group
-    auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
+    auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + L::BUF0 + (b & 1) * L::bytes; };
 
+    if constexpr (TYPE == kIQ3_XXS) {
+        // the signed grid: entry 16 i + n = grid word i with the signs of
+        // nibble n applied bytewise (grid bytes are nonzero: no carries)
+        uint32_t *sg = reinterpret_cast<uint32_t *>(lds + L::GRID);
+        for (uint32_t e = tid; e < 256 * 16; e += 64 * PW) {
+            const uint32_t m = spread_sign4(e & 15u), gw = c_pf_iq3_grid[e >> 4];
+            sg[e] = (gw ^ m) + (m & 0x01010101u);
+        }
+        // first read after the superblock loop's barrier
+    }
     const uint32_t v = sk_logical(blockIdx.x, a.G);
     const uint32_t units = pf_ntiles<GRP>(a) * a.nblk;
     const uint32_t ub = sk_begin(units, a.G, v), ue = sk_begin(units, a.G, v + 1);
@@ -500,6 +646,24 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     q4_block(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g,
                              reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g, f, j, g,
                              acc[t]);
+                }
+            } else if constexpr (TYPE == kIQ3_XXS) {
+                I3Frag f;
+                i3_convert(bb + L::W + rl * T::UB, bb + L::TAIL + 4 * rl, ((n0 + rl) * a.row_bytes + b * 98) & 3u,
+                           reinterpret_cast<const uint32_t *>(lds + L::GRID), g, f);
+                constexpr int P = NB >= 2 ? 2 : 1;
+                static_assert(NB % P == 0, "token blocks in pairs");
+#pragma unroll
+                for (int t = 0; t < NB; t += P) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    const unsigned char *ar[P];
+                    const float *dp[P];
+#pragma unroll
+                    for (int i = 0; i < P; ++i) {
+                        ar[i] = bb + L::QS + (32 * (tg * NB + t + i) + j) * 256;
+                        dp[i] = reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t + i) + 4 * g;
+                    }
+                    i3_blocks<P>(ar, dp, f, j, g, reinterpret_cast<float(&)[P][16]>(acc[t]));
                 }
             } else {
                 Q8Frag f;
@@ -569,7 +733,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         };
         uint32_t ncontrib = 0;
         for (uint32_t c = vf; c <= vl; ++c) ncontrib += live(c) ? 1u : 0u;
-        uint32_t *const flag = reinterpret_cast<uint32_t *>(lds);  // no LDS reader left (barrier above)
+        uint32_t *const flag = reinterpret_cast<uint32_t *>(lds + L::BUF0);  // no reader of the buffers left (barrier above)
         if (tid == 0)
             *flag = __builtin_amdgcn_atomic_inc32(a.ctr + tile, ncontrib - 1, __ATOMIC_RELAXED, "");
         __syncthreads();
@@ -694,10 +858,13 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
 // GemmDispatch.cu:634-643): the smallest of 32, 64, 128 tokens that holds M,
 // else 128 (Q8_0: 64 or 128, as its waves split the tile's tokens in two).
 int pf_nt(int type, uint32_t M) {
+    static_assert(PLds<kIQ3_XXS, 4>::total <= 160 * 1024 && PLds<kQ4_K, 4>::total <= 160 * 1024 &&
+                      PLds<kQ8_0, 4>::total <= 160 * 1024,
+                  "LDS of one workgroup");
     const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
     return type == kQ8_0 ? std::max(nt, 2) : nt;
 }
-uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }
+uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // IQ3_XXS: 256 too
 
 // Split tiles are summed inside the main kernel, by their last contributor,
 // when no tile has more than kFusedMax contributors: that workgroup reads the
@@ -734,9 +901,9 @@ template <int TYPE, int NT, bool GRP = false>
 hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
     using L = PLds<TYPE, NT>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_prefill<TYPE, NT, GRP>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 2 * L::bytes);
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, L::total);
     if (attr != hipSuccess) return attr;
-    k_prefill<TYPE, NT, GRP><<<dim3{a.G, 1u, 1u}, 64 * PW, 2 * L::bytes, st>>>(a);
+    k_prefill<TYPE, NT, GRP><<<dim3{a.G, 1u, 1u}, 64 * PW, L::total, st>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.fused || a.G == 1) return e;
     const uint32_t units = a.ntiles * a.nblk;
@@ -750,7 +917,7 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
 
 }  // namespace
 
-bool prefill_type(int type) { return type == kQ4_K || type == kQ8_0; }
+bool prefill_type(int type) { return type == kQ4_K || type == kQ8_0 || type == kIQ3_XXS; }
 
 // Workspace: the per-tile arrival counters (256-byte rounded), then the
 // partial tiles, two per workgroup.
@@ -768,7 +935,8 @@ size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int
 
 hipError_t launch_prefill(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N,
                           uint32_t K, int num_cu, void *workspace, hipStream_t st) {
-    if (!prefill_type(type) || M == 0 || N == 0 || K == 0 || K % 256 || workspace == nullptr || act.dg == nullptr)
+    if (!prefill_type(type) || M == 0 || N == 0 || K == 0 || K % 256 || workspace == nullptr ||
+        (type != kIQ3_XXS && act.dg == nullptr))
         return hipErrorInvalidValue;
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
@@ -792,6 +960,13 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
     a.G = g.G;
     a.fused = pf_fused(a.ntiles * a.nblk, a.G, a.nblk) ? 1u : 0u;
     if (type == kQ8_0) return g.nt == 2 ? pf_launch<kQ8_0, 2>(a, st) : pf_launch<kQ8_0, 4>(a, st);
+    if (type == kIQ3_XXS) {
+        switch (g.nt) {
+            case 1: return pf_launch<kIQ3_XXS, 1>(a, st);
+            case 2: return pf_launch<kIQ3_XXS, 2>(a, st);
+            default: return pf_launch<kIQ3_XXS, 4>(a, st);
+        }
+    }
     switch (g.nt) {
         case 1: return pf_launch<kQ4_K, 1>(a, st);
         case 2: return pf_launch<kQ4_K, 2>(a, st);
