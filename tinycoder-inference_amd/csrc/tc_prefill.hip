@@ -883,9 +883,9 @@ struct PfGeom {
     int nt;
     uint32_t tt, pr, ntm, ntn, ntiles, G;
 };
-PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
+PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     PfGeom g;
-    g.nt = pf_nt(type, M);
+    g.nt = nt;
     g.tt = 32u * g.nt;
     g.pr = pf_rows(type);
     g.ntm = (M + g.tt - 1) / g.tt;
@@ -895,6 +895,17 @@ PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     // one workgroup per CU, each with at least 2 superblocks of work
     g.G = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(uint64_t(num_cu), units / 2)));
     return g;
+}
+// 64-token tiles instead of 128 where that lets the split tiles be summed
+// inside the kernel (at most kFusedMax contributors) and 128 would not: the
+// weights are converted twice as often, but the fixup launch goes (Q4_K
+// 17408x5120, M = 128: 52.2 -> 49.7 us; where neither or both fuse, 128-token
+// tiles measured as fast or faster).
+PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
+    const PfGeom g = pf_geom_nt(type, pf_nt(type, M), M, N, K, num_cu);
+    if (g.nt != 4 || type == kQ8_0 || pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256)) return g;
+    const PfGeom h = pf_geom_nt(type, 2, M, N, K, num_cu);
+    return pf_fused(uint64_t(h.ntiles) * (K / 256), h.G, K / 256) ? h : g;
 }
 
 template <int TYPE, int NT, bool GRP = false>
