@@ -32,8 +32,11 @@ def enc_weights(oracle, qt, rng, rows, cols):
 # (40, 72, 2304): K-slices of 5 and 4 superblocks (odd and even counts);
 # (200, 1000, 4096): Q4_K stream-K with every tile split over 4 workgroups and
 # ragged rows and tokens.
+# (33, 77, 768) and (5, 129, 256): an odd number of weight units, so the
+# last unit of a 2-byte-aligned format (IQ3_XXS, Q6_K, IQ3_S, IQ2_S) starts
+# 4-byte aligned and its last dword load ends past the matrix.
 SHAPES = [(1, 64, 256), (37, 200, 1024), (128, 256, 5120), (130, 136, 2048), (300, 384, 768), (40, 72, 2304),
-          (200, 1000, 4096)]
+          (200, 1000, 4096), (33, 77, 768), (5, 129, 256)]
 
 
 MFMA_TYPES = [Q4_K, Q5_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S, Q8_0]

@@ -130,6 +130,22 @@ def test_gemv_golden_baseline_widths(tc, dev, golden, name, qt, cols):
 
 
 @pytest.mark.parametrize("qt", ALL)
+@pytest.mark.parametrize("S", [1, 3])
+def test_gemv_odd_unit_count(tc, dev, oracle, qt, S):
+    """77 rows x 768 columns: an odd number of weight units, so the last
+    unit of a 2-byte-aligned format ends 2 bytes into a dword past the
+    matrix."""
+    rng = np.random.default_rng(300 + 10 * qt + S)
+    rows, cols = 77, 768
+    w = oracle.encode(qt, gaussian(rng, (rows, cols), 1.0 if qt == Q4_K else 0.02))
+    x = gaussian(rng, (S, cols))
+    got = tc.gemv(qt, to_dev(w, dev), to_dev(x, dev), rows, cols).cpu().numpy()
+    ref = oracle.matmul(qt, w, x, rows, cols)
+    ok, worst = close(got, ref)
+    assert ok, f"{NAMES[qt]} S={S}: worst err/bound {worst:.2f}"
+
+
+@pytest.mark.parametrize("qt", ALL)
 @pytest.mark.parametrize("S", [1, 2, 5, 8])
 def test_gemv_vs_oracle(tc, dev, oracle, qt, S):
     """Encoder-made weights (realistic scales). Random-byte blocks, whose

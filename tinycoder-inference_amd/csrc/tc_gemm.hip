@@ -176,7 +176,10 @@ template <int TYPE>
 __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t tid,
                                          const uint8_t *W = nullptr) {
     GSrc g;
-    g.w = grsrc(W != nullptr ? W : a.W, uint64_t(a.N) * a.row_bytes);
+    // whole dwords: the range check zeroes a dword that is only partly in
+    // range, and 2-byte-aligned units (Q6_K, IQ3_S, IQ2_S) end 2 bytes into
+    // one when their count is odd (it stays in the page of the last byte)
+    g.w = grsrc(W != nullptr ? W : a.W, (uint64_t(a.N) * a.row_bytes + 3) & ~uint64_t(3));
     g.q = grsrc(a.qs, uint64_t(a.M) * a.K);
     g.d = grsrc(a.d8, uint64_t(a.M) * (a.K / (TYPE == kQ8_0 ? 32 : 256)) * 4);
     g.bs = grsrc(a.bsums, TYPE == kQ8_0 ? 0 : uint64_t(a.M) * (a.K / 16) * 2);

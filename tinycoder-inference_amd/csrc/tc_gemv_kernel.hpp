@@ -1317,7 +1317,10 @@ __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(1, 2))) v
             base = wbase1 + (live ? uint64_t(e) * jb.wstride : 0);
         }
         const uint32_t soff = live ? tt * TILE_BYTES : 0u;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, live ? per_mat * UB : 0u);
+        // whole dwords: the range check zeroes a dword only partly in range,
+        // and 2-byte-aligned units end 2 bytes into one when a workgroup's
+        // unit count is odd (the matrix's last dword stays in its last page)
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, live ? (per_mat * UB + 3u) & ~3u : 0u);
         static_for<0, NX>([&](auto c) __attribute__((always_inline)) {
             uint32_t voff = lane * 16 + c.value * 1024;
             if constexpr (c.value == NX - 1 && TILE_BYTES % 1024 != 0) voff = voff < TILE_BYTES ? voff : 0x80000000u;

@@ -546,7 +546,11 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
         });
     }
     constexpr uint32_t CPR = T::UB / 16;  // 16-byte chunks per row
-    const v4i rw = rs4(W, a.N * a.row_bytes);
+    // the weight range rounded up to whole dwords: the range check zeroes a
+    // dword that is only partly in range, and the 2-byte-aligned IQ3_XXS
+    // units end 2 bytes into one when their count is odd (the dword stays in
+    // the same 4 KB page as the matrix's last byte)
+    const v4i rw = rs4(W, (a.N * a.row_bytes + 3) & ~3u);
     each_inst<T::PR * CPR / 64>(w, [&](uint32_t k) {
         const uint32_t c = 64 * k + ln, r = c / CPR, p = c - CPR * r;
         if constexpr (TYPE == kIQ3_XXS)  // the window from the unit's 4-byte-aligned start (slot 6: unused)
