@@ -1,6 +1,6 @@
 // tc_gemm.hip -- prefill GEMM: out[m][n] = W[n] . x[m] for M tokens against raw
-// GGUF weight rows of Q5_K, Q6_K, IQ3_S and IQ2_S, on the int8 matrix cores
-// (v_mfma_i32_32x32x32_i8). (Q4_K, Q8_0 and IQ3_XXS run the
+// GGUF weight rows of Q5_K, Q6_K and IQ2_S, on the int8 matrix cores
+// (v_mfma_i32_32x32x32_i8). (Q4_K, Q8_0, IQ3_XXS and IQ3_S run the
 // register-conversion kernel of tc_prefill.hip.)
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698) with
@@ -27,7 +27,7 @@
 //    more pair of MFMAs over 8 useful k-slots, with the activation pair sums
 //    split into int8 digits the same way. Per superblock and output: acc +=
 //    d8 * (d*main - dmin*min). (The Q4_K producer code is shared with it.)
-//  * Q6_K, IQ3_S and IQ2_S write their signed integer weights (sc*(q-32),
+//  * Q6_K and IQ2_S write their signed integer weights (sc*(q-32),
 //    (2ls+1)*(+-grid value)) as signed digits and have no min term.
 //
 // MFMA operands: lane l feeds row (l & 31) and the 16 bytes of k-group
@@ -52,17 +52,17 @@ constexpr int PL = 272;       // LDS plane row stride (256 + 16: conflict-free b
 // workgroups fit a CU and one's conversion / epilogue overlaps the other's
 // MFMA work.
 // Weight types whose products run on int8 digit planes: every weight of a
-// superblock becomes an exact integer e (Q4_K sc*q, Q6_K sc*(q-32), IQ3_S
-// and IQ2_S (2ls+1)*signed grid value) written as two int8 planes, 128*hi + lo.
+// superblock becomes an exact integer e (Q4_K sc*q, Q6_K sc*(q-32), IQ2_S
+// (2ls+1)*signed grid value) written as two int8 planes, 128*hi + lo.
 __host__ __device__ constexpr bool dig_type(int t) {
-    return t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ3_S || t == kIQ2_S;
+    return t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ2_S;
 }
 // K-quants with a per-sub-block min (w = d*sc*q - dmin*m): the min term runs
 // on one more MFMA pair against the activation pair sums.
 __host__ __device__ constexpr bool min_type(int t) { return t == kQ4_K || t == kQ5_K; }
 // Codebook bytes the converter reads from LDS (past the two stage buffers).
 __host__ __device__ constexpr uint32_t grid_bytes(int t) {
-    return t == kIQ3_S ? 512 * 4 : t == kIQ2_S ? 1024 * 8 : 0;
+    return t == kIQ2_S ? 1024 * 8 : 0;
 }
 
 template <int TYPE>
@@ -137,21 +137,20 @@ __device__ __forceinline__ void digits4(uint32_t q, uint32_t sc, uint32_t &hi, u
 template <int TYPE>
 struct GPrefetch {
     // Q4_K: the 16-byte header and the 32 quant bytes this thread converts
-    // (row tid/4, quarter tid%4); Q5_K: the same and the 32 qh bytes; IQ3_S
-    // and IQ2_S: the bytes of the two 32-chunks 2qq, 2qq+1 (4-byte-aligned
+    // (row tid/4, quarter tid%4); Q5_K: the same and the 32 qh bytes; IQ2_S:
+    // the bytes of the two 32-chunks 2qq, 2qq+1 (4-byte-aligned
     // words, realigned on conversion); Q6_K: its 16-byte runs of ql (two) and qh,
     // read from 4-byte-aligned addresses (blocks are 2-byte aligned) with
     // their fifth dwords in ex, then the scale bytes and d. Q8_0: raw 16-byte
     // chunks of the tile.
     static constexpr int RAWC = TYPE == kQ4_K || TYPE == kQ6_K       ? 3
                                 : TYPE == kQ5_K                       ? 5
-                                : TYPE == kIQ3_S                      ? 1
-                                : TYPE == kIQ2_S                      ? 0
+                                                                : TYPE == kIQ2_S                      ? 0
                                                                       : (GN * 272 / 16 + GT - 1) / GT;
-    static constexpr int EXC = TYPE == kQ6_K || TYPE == kIQ3_S ? 7 : TYPE == kIQ2_S ? 9 : 1;
+    static constexpr int EXC = TYPE == kQ6_K ? 7 : TYPE == kIQ2_S ? 9 : 1;
     u4 raw[RAWC > 0 ? RAWC : 1];
     uint32_t ex[EXC];
-    uint32_t sh;           // Q6_K, IQ3_S, IQ2_S: the block's byte offset mod 4
+    uint32_t sh;           // Q6_K, IQ2_S: the block's byte offset mod 4
     static constexpr int ACTC = TYPE == kQ8_0 ? GM * 16 / GT : 0;
     u4 act[ACTC > 0 ? ACTC : 1];  // 16-byte activation chunks (Q8_0; Q4_K loads them straight into LDS)
     u4 side;               // Q8_K bsums (256 chunks) or Q8_0 d (256 chunks)
@@ -177,7 +176,7 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
                                          const uint8_t *W = nullptr) {
     GSrc g;
     // whole dwords: the range check zeroes a dword that is only partly in
-    // range, and 2-byte-aligned units (Q6_K, IQ3_S, IQ2_S) end 2 bytes into
+    // range, and 2-byte-aligned units (Q6_K, IQ2_S) end 2 bytes into
     // one when their count is odd (it stays in the page of the last byte)
     g.w = grsrc(W != nullptr ? W : a.W, (uint64_t(a.N) * a.row_bytes + 3) & ~uint64_t(3));
     g.q = grsrc(a.qs, uint64_t(a.M) * a.K);
@@ -195,7 +194,7 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
         g.vo[3] = 192 + 8 * n;
     } else {
         g.vo[0] = g.vo[1] = g.vo[2] = 0;
-        g.vo[3] = tid & 3;  // IQ3_S / IQ2_S: the thread's quarter
+        g.vo[3] = tid & 3;  // IQ2_S: the thread's quarter
     }
     // Activations are block-major: 256-column block b of token m at b * M + m.
     g.vq = (m0 + tid / 16) * 256 + 16 * (tid & 15);
@@ -224,7 +223,7 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
         p.raw[2] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw + 32, b * UB, 0);
         p.raw[3] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2, b * UB, 0);
         p.raw[4] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2 + 16, b * UB, 0);
-    } else if constexpr (TYPE == kIQ3_S || TYPE == kIQ2_S) {
+    } else if constexpr (TYPE == kIQ2_S) {
         // 2-byte-aligned blocks; each piece from its 4-byte-aligned address
         // down, the block start's offset mod 4 in sh
         const uint32_t blk = g.vw + b * UB;
@@ -234,24 +233,14 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
             return __builtin_amdgcn_raw_buffer_load_b32(g.w, (blk + off) & ~3u, 0, 0);
         };
         const uint32_t qq = g.vo[3];
-        if constexpr (TYPE == kIQ3_S) {
-            p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, (blk + 2 + 16 * qq) & ~3u, 0, 0);  // qs
-            p.ex[0] = w32(2 + 16 * qq + 16);
-            p.ex[1] = w32(66 + 2 * qq);       // qh bytes 2qq, 2qq+1 (never straddle a word)
-            p.ex[2] = w32(74 + 8 * qq);       // signs
-            p.ex[3] = w32(74 + 8 * qq + 4);
-            p.ex[4] = w32(74 + 8 * qq + 8);
-            p.ex[5] = w32(106 + qq);          // scale byte
-        } else {
-            p.ex[0] = w32(2 + 8 * qq);        // qs (grid low bytes)
-            p.ex[1] = w32(2 + 8 * qq + 4);
-            p.ex[2] = w32(2 + 8 * qq + 8);
-            p.ex[3] = w32(34 + 8 * qq);       // signs
-            p.ex[4] = w32(34 + 8 * qq + 4);
-            p.ex[5] = w32(34 + 8 * qq + 8);
-            p.ex[7] = w32(66 + 2 * qq);       // qh bytes 2qq, 2qq+1
-            p.ex[8] = w32(74 + 2 * qq);       // scale bytes 2qq, 2qq+1
-        }
+        p.ex[0] = w32(2 + 8 * qq);        // qs (grid low bytes)
+        p.ex[1] = w32(2 + 8 * qq + 4);
+        p.ex[2] = w32(2 + 8 * qq + 8);
+        p.ex[3] = w32(34 + 8 * qq);       // signs
+        p.ex[4] = w32(34 + 8 * qq + 4);
+        p.ex[5] = w32(34 + 8 * qq + 8);
+        p.ex[7] = w32(66 + 2 * qq);       // qh bytes 2qq, 2qq+1
+        p.ex[8] = w32(74 + 2 * qq);       // scale bytes 2qq, 2qq+1
         p.ex[6] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al, 0, 0);  // d
     } else if constexpr (TYPE == kQ6_K) {
         const uint32_t blk = g.vw + b * UB;  // block start (2-byte aligned)
@@ -406,50 +395,6 @@ __device__ __forceinline__ void q6k_convert(const GPrefetch<kQ6_K> &p, unsigned 
     reinterpret_cast<float *>(lds + L::AS)[r] = h2f(dh);
 }
 
-// IQ3_S weights of this thread (row tid/4, 32-chunks ib = 2qq + c) -> the
-// digit planes and d. Group l (8 weights) of chunk ib: codebook entries
-// qs[8ib + 2l] and qs[8ib + 2l + 1] with bit 8 from bits 2l and 2l+1 of
-// qh[ib], negated by the bits of signs[4ib + l], times 2ls+1 with ls nibble
-// ib&1 of scales[ib/2] (reference include/GGMLDequantize.hpp:1164-1212 and
-// the integer block dot :2102-2145).
-__device__ __forceinline__ void iq3s_convert(const GPrefetch<kIQ3_S> &p, unsigned char *lds, const uint32_t *grid,
-                                             uint32_t tid) {
-    using L = GLds<kIQ3_S>;
-    const uint32_t r = tid / 4, qq = tid & 3;
-    const uint32_t s_qs = (p.sh + 2) & 3, s_sg = (p.sh + 2) & 3;  // qs at 2 + 16qq, signs at 74 + 8qq
-    const uint32_t v[5] = {p.raw[0].x, p.raw[0].y, p.raw[0].z, p.raw[0].w, p.ex[0]};
-    uint32_t qs[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) qs[j] = realign(v[j + 1], v[j], s_qs);
-    const uint32_t sg[2] = {realign(p.ex[3], p.ex[2], s_sg), realign(p.ex[4], p.ex[3], s_sg)};
-    const uint32_t qh2 = p.ex[1] >> (8 * ((p.sh + 66 + 2 * qq) & 3));      // qh[2qq] | qh[2qq+1] << 8
-    const uint32_t scb = (p.ex[5] >> (8 * ((p.sh + 106 + qq) & 3))) & 0xFFu;  // scales[qq]
-    const uint32_t dh = p.sh ? (p.ex[6] >> 16) : (p.ex[6] & 0xFFFFu);
-    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const int k = 2 * int((scb >> (4 * c)) & 15u) + 1;
-        const uint32_t qh = (qh2 >> (8 * c)) & 0xFFu;
-        uint32_t hi[8], lo[8];
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const uint32_t qw = qs[2 * c + (l >> 1)], sh8 = 16 * (l & 1);
-            const uint32_t i1 = ((qw >> sh8) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
-            const uint32_t i2 = ((qw >> (sh8 + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
-            const uint32_t s8 = (sg[c] >> (8 * l)) & 0xFFu;
-            const uint32_t m1 = spread_sign4(s8 & 15u), m2 = spread_sign4(s8 >> 4);
-            digits_i8((grid[i1] ^ m1) + (m1 & 0x01010101u), k, hi[2 * l], lo[2 * l]);
-            digits_i8((grid[i2] ^ m2) + (m2 & 0x01010101u), k, hi[2 * l + 1], lo[2 * l + 1]);
-        }
-        const uint32_t k0 = 64 * qq + 32 * c;
-        *reinterpret_cast<u4 *>(a0 + k0) = u4{hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<u4 *>(a0 + k0 + 16) = u4{hi[4], hi[5], hi[6], hi[7]};
-        *reinterpret_cast<u4 *>(a1 + k0) = u4{lo[0], lo[1], lo[2], lo[3]};
-        *reinterpret_cast<u4 *>(a1 + k0 + 16) = u4{lo[4], lo[5], lo[6], lo[7]};
-    }
-    reinterpret_cast<float *>(lds + L::AS)[r] = h2f(dh);
-}
-
 // IQ2_S weights of this thread (row tid/4, 32-chunks ib = 2qq + c) -> the
 // digit planes and d/8 (the row scale 0.125 of the reference's fused path,
 // include/GGMLDequantize.hpp:2148-2159, is a power of two: exact on d). Group
@@ -490,9 +435,6 @@ __device__ __forceinline__ void iq2s_convert(const GPrefetch<kIQ2_S> &p, unsigne
     reinterpret_cast<float *>(lds + L::AS)[r] = 0.125f * h2f(dh);
 }
 
-__constant__ uint32_t c_iq3s_grid[512] = {
-#include "iq3s_grid.inc"
-};
 __constant__ uint64_t c_iq2s_grid[1024] = {
 #include "iq2s_grid.inc"
 };
@@ -508,8 +450,6 @@ __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned ch
         q4k_convert<kQ4_K>(p.raw[0], p.raw[1], p.raw[2], lds, tid);
     } else if constexpr (TYPE == kQ5_K) {
         q4k_convert<kQ5_K>(p.raw[0], p.raw[3], p.raw[4], lds, tid, p.raw[1], p.raw[2]);
-    } else if constexpr (TYPE == kIQ3_S) {
-        iq3s_convert(p, lds, grid, tid);
     } else if constexpr (TYPE == kIQ2_S) {
         iq2s_convert(p, lds, grid, tid);
     } else if constexpr (TYPE == kQ6_K) {
@@ -744,10 +684,10 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
     const uint32_t li = lane & 31, lg = lane >> 5;
     const uint32_t ptid = tid - 64 * CW;  // producer thread index 0..255
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + (b & 1) * L::bytes; };
-    // IQ3_S / IQ2_S codebook in LDS, past the two buffers (read by the producers' conversion)
+    // IQ2_S codebook in LDS, past the two buffers (read by the producers' conversion)
     uint32_t *grid = reinterpret_cast<uint32_t *>(lds + 2 * L::bytes);
     if constexpr (grid_bytes(TYPE) != 0) {
-        const uint32_t *src = TYPE == kIQ3_S ? c_iq3s_grid : reinterpret_cast<const uint32_t *>(c_iq2s_grid);
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(c_iq2s_grid);
         for (uint32_t i = tid; i < grid_bytes(TYPE) / 4; i += blockDim.x) grid[i] = src[i];
         __syncthreads();
     }
@@ -965,7 +905,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
     // weight matrix must each stay below 4 GiB.
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
-    // Q4_K, Q8_0 and IQ3_XXS run k_prefill (tc_prefill.hip); the other MFMA types here.
+    // Q4_K, Q8_0, IQ3_XXS and IQ3_S run k_prefill (tc_prefill.hip); the other MFMA types here.
     if (!dig_type(type) || type == kQ4_K) return hipErrorInvalidValue;
     const uint32_t nsplit = gemm_splits(type, M, N, K, num_cu);
     if ((nsplit > 1 || dig_type(type)) && workspace == nullptr) return hipErrorInvalidValue;
@@ -990,7 +930,6 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
         const dim3 g{G, 1u, 1u};
         hipError_t e = type == kQ5_K     ? launch_gemm_t<kQ5_K>(a, g, st)
                        : type == kQ6_K   ? launch_gemm_t<kQ6_K>(a, g, st)
-                       : type == kIQ3_S  ? launch_gemm_t<kIQ3_S>(a, g, st)
                                          : launch_gemm_t<kIQ2_S>(a, g, st);
         if (e != hipSuccess) return e;
         // Any tile split over workgroups? (a range boundary inside a tile)

@@ -1,12 +1,13 @@
-// tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K, Q8_0 and
-// IQ3_XXS weights on the int8 matrix cores (v_mfma_i32_32x32x32_i8). The
-// weights of a tile are converted once per token tile of up to 128 tokens,
-// in the registers of the lanes that feed them to the MFMA.
+// tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K, Q8_0,
+// IQ3_XXS and IQ3_S weights on the int8 matrix cores
+// (v_mfma_i32_32x32x32_i8). The weights of a tile are converted once per
+// token tile of up to 128 tokens, in the registers of the lanes that feed
+// them to the MFMA.
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698 and
 // its stream-K kernel GemmKernels.cuh:3707-4030) with the CPU reference's
 // numerics: the activations are quantized by the bit-exact quantizers (Q8_K
-// for Q4_K and IQ3_XXS, the 32-wide Q8_0 rule for Q8_0), every integer dot
+// for Q4_K and the IQ types, the 32-wide Q8_0 rule for Q8_0), every integer dot
 // product of a weight block with an activation block is exact, and only the
 // scale combination runs in fp32.
 //
@@ -21,8 +22,8 @@
 //  * Q8_0: 128 rows per workgroup, waves w and w + 4 share rows and take one
 //    half of the tile's tokens each (the Q8_0 weight blocks take 272 bytes of
 //    LDS per row and superblock).
-//  * IQ3_XXS: as Q4_K (256 rows); the sign-applied codebook is built in LDS
-//    once per workgroup.
+//  * IQ3_XXS, IQ3_S: as Q4_K (256 rows); the sign-applied codebook is built
+//    in LDS once per workgroup.
 //
 // Q4_K (reference dequantizeQ4_KBlock, GGMLDequantize.hpp:436-477): a weight
 // of sub-block s is w = d*sc_s*q - dmin*m_s with q in 0..15 and sc_s, m_s in
@@ -94,6 +95,17 @@ template <>
 struct PfType<kIQ3_XXS> {
     static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 112, XB = 0;
 };
+// IQ3_S: the 110-byte unit (2-byte aligned) in the 112-byte window from its
+// 4-byte-aligned start (7 chunks; the last ends at most 2 bytes past the
+// unit, inside the dword-rounded range).
+template <>
+struct PfType<kIQ3_S> {
+    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 112, XB = 0;
+};
+// Codebook types: the sign-applied grid (entries x 16 sign nibbles x 4 bytes).
+__host__ __device__ constexpr uint32_t pf_grid_bytes(int type) {
+    return type == kIQ3_XXS ? 256 * 16 * 4 : type == kIQ3_S ? 512 * 16 * 4 : 0;
+}
 
 // One LDS buffer: [TT][256] activation values (16-byte chunk c of token t at
 // slot c ^ (t & 15)), [TT][XB] scale data, the Q8_K types' [max(TT, 64)]
@@ -105,7 +117,7 @@ struct PLds {
     using T = PfType<TYPE>;
     static constexpr uint32_t TT = 32 * NT;
     static constexpr uint32_t GRID = 0;  // IQ3_XXS's signed grid (before the two buffers)
-    static constexpr uint32_t BUF0 = TYPE == kIQ3_XXS ? 256 * 16 * 4 : 0;
+    static constexpr uint32_t BUF0 = pf_grid_bytes(TYPE);
     static constexpr uint32_t QS = 0;
     static constexpr uint32_t XS = TT * 256;
     static constexpr uint32_t D8 = XS + TT * T::XB;
@@ -403,6 +415,46 @@ __device__ __forceinline__ void i3_convert(const unsigned char *row, const unsig
     }
 }
 
+
+// ---- IQ3_S: B operands of one superblock ------------------------------------
+// Reference dequantizeIQ3_SBlock (GGMLDequantize.hpp:1164-1212) and the
+// fused dot (:2102-2145): per 32-block ib, 8 grid indices (qs bytes, bit 8
+// from qh[ib]) into the 512-word codebook (magnitudes <= 15), 32 sign bits
+// (signs[4 ib .. 4 ib + 3], one per weight) and the scale 2 ls + 1 (ls the
+// nibble ib % 2 of scales[ib / 2]); value = d * d8 * isum as for IQ3_XXS
+// (no 1/4 factor).
+
+__constant__ uint32_t c_pf_iq3s_grid[512] = {
+#include "iq3s_grid.inc"
+};
+
+// This lane's row: the 112-byte window (its unit at byte sh) in the row's
+// LDS chunks; fields read as 2-byte halves.
+__device__ __forceinline__ void is3_convert(const unsigned char *row, uint32_t sh, const uint32_t *sgrid, uint32_t g,
+                                            I3Frag &f) {
+    auto h16 = [&](uint32_t x) __attribute__((always_inline)) {  // window bytes x, x + 1 (x even)
+        return uint32_t(*reinterpret_cast<const uint16_t *>(row + x));
+    };
+    f.d = h2f(h16(sh));
+    const uint32_t scw = h16(sh + 106) | (h16(sh + 108) << 16);  // the 8 scale nibbles
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        const uint32_t qo = sh + 2 + 8 * ib + 4 * g;
+        const uint32_t qsw = h16(qo) | (h16(qo + 2) << 16);             // indices 4g .. 4g + 3 (low 8 bits)
+        const uint32_t qhb = h16(sh + 66 + (ib & ~1)) >> (8 * (ib & 1)); // qh[ib] (bits 8 of the 8 indices)
+        const uint32_t sgn = h16(sh + 74 + 4 * ib + 2 * g);            // sign bytes of groups 2g, 2g + 1
+        f.sc[ib] = 2 * int((scw >> (4 * ib)) & 15u) + 1;
+        uint32_t e[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {  // word k: index 4g + k, sign nibble k % 2 of group 2g + k / 2
+            const uint32_t idx = __builtin_amdgcn_ubfe(qsw, 8 * k, 8) | (__builtin_amdgcn_ubfe(qhb, 4 * g + k, 1) << 8);
+            const uint32_t nib = __builtin_amdgcn_ubfe(sgn, 4 * k, 4);
+            e[k] = sgrid[(idx << 4) | nib];
+        }
+        f.bw[ib] = v4i{int(e[0]), int(e[1]), int(e[2]), int(e[3])};
+    }
+}
+
 // P (1 or 2) 32-token blocks (activation rows arow[t], token scales d8[t]):
 // per 32-block the MFMAs of all P token blocks first, then their integer
 // multiply-adds (so that no multiply-add waits for the MFMA issued just
@@ -555,6 +607,8 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
         const uint32_t c = 64 * k + ln, r = c / CPR, p = c - CPR * r;
         if constexpr (TYPE == kIQ3_XXS)  // the window from the unit's 4-byte-aligned start (slot 6: unused)
             lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 98) & ~3u) + 16 * min(p, 5u));
+        else if constexpr (TYPE == kIQ3_S)
+            lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 110) & ~3u) + 16 * p);
         else
             lds_load16(base + L::W + 1024 * k, rw, (n0 + r) * a.row_bytes + b * T::UB + 16 * p);
     });
@@ -587,12 +641,13 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const uint32_t rg = w % RG, tg = w / RG;      // row group, token group
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + L::BUF0 + (b & 1) * L::bytes; };
 
-    if constexpr (TYPE == kIQ3_XXS) {
+    if constexpr (pf_grid_bytes(TYPE) != 0) {
         // the signed grid: entry 16 i + n = grid word i with the signs of
         // nibble n applied bytewise (grid bytes are nonzero: no carries)
         uint32_t *sg = reinterpret_cast<uint32_t *>(lds + L::GRID);
-        for (uint32_t e = tid; e < 256 * 16; e += 64 * PW) {
-            const uint32_t m = spread_sign4(e & 15u), gw = c_pf_iq3_grid[e >> 4];
+        for (uint32_t e = tid; e < pf_grid_bytes(TYPE) / 4; e += 64 * PW) {
+            const uint32_t m = spread_sign4(e & 15u);
+            const uint32_t gw = TYPE == kIQ3_XXS ? c_pf_iq3_grid[e >> 4] : c_pf_iq3s_grid[e >> 4];
             sg[e] = (gw ^ m) + (m & 0x01010101u);
         }
         // first read after the superblock loop's barrier
@@ -651,10 +706,14 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                              reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g, f, j, g,
                              acc[t]);
                 }
-            } else if constexpr (TYPE == kIQ3_XXS) {
+            } else if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S) {
                 I3Frag f;
-                i3_convert(bb + L::W + rl * T::UB, bb + L::TAIL + 4 * rl, ((n0 + rl) * a.row_bytes + b * 98) & 3u,
-                           reinterpret_cast<const uint32_t *>(lds + L::GRID), g, f);
+                if constexpr (TYPE == kIQ3_XXS)
+                    i3_convert(bb + L::W + rl * T::UB, bb + L::TAIL + 4 * rl, ((n0 + rl) * a.row_bytes + b * 98) & 3u,
+                               reinterpret_cast<const uint32_t *>(lds + L::GRID), g, f);
+                else
+                    is3_convert(bb + L::W + rl * T::UB, ((n0 + rl) * a.row_bytes + b * 110) & 3u,
+                                reinterpret_cast<const uint32_t *>(lds + L::GRID), g, f);
                 constexpr int P = NB >= 2 ? 2 : 1;
                 static_assert(NB % P == 0, "token blocks in pairs");
 #pragma unroll
@@ -862,13 +921,14 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
 // GemmDispatch.cu:634-643): the smallest of 32, 64, 128 tokens that holds M,
 // else 128 (Q8_0: 64 or 128, as its waves split the tile's tokens in two).
 int pf_nt(int type, uint32_t M) {
-    static_assert(PLds<kIQ3_XXS, 4>::total <= 160 * 1024 && PLds<kQ4_K, 4>::total <= 160 * 1024 &&
+    static_assert(PLds<kIQ3_XXS, 4>::total <= 160 * 1024 && PLds<kIQ3_S, 4>::total <= 160 * 1024 &&
+                      PLds<kQ4_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ8_0, 4>::total <= 160 * 1024,
                   "LDS of one workgroup");
     const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
     return type == kQ8_0 ? std::max(nt, 2) : nt;
 }
-uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // IQ3_XXS: 256 too
+uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // IQ3_XXS, IQ3_S: 256 too
 
 // Split tiles are summed inside the main kernel, by their last contributor,
 // when no tile has more than kFusedMax contributors: that workgroup reads the
@@ -932,7 +992,7 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
 
 }  // namespace
 
-bool prefill_type(int type) { return type == kQ4_K || type == kQ8_0 || type == kIQ3_XXS; }
+bool prefill_type(int type) { return type == kQ4_K || type == kQ8_0 || type == kIQ3_XXS || type == kIQ3_S; }
 
 // Workspace: the per-tile arrival counters (256-byte rounded), then the
 // partial tiles, two per workgroup.
@@ -951,7 +1011,7 @@ size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int
 hipError_t launch_prefill(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N,
                           uint32_t K, int num_cu, void *workspace, hipStream_t st) {
     if (!prefill_type(type) || M == 0 || N == 0 || K == 0 || K % 256 || workspace == nullptr ||
-        (type != kIQ3_XXS && act.dg == nullptr))
+        ((type == kQ4_K || type == kQ8_0) && act.dg == nullptr))
         return hipErrorInvalidValue;
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
@@ -980,6 +1040,13 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
             case 1: return pf_launch<kIQ3_XXS, 1>(a, st);
             case 2: return pf_launch<kIQ3_XXS, 2>(a, st);
             default: return pf_launch<kIQ3_XXS, 4>(a, st);
+        }
+    }
+    if (type == kIQ3_S) {
+        switch (g.nt) {
+            case 1: return pf_launch<kIQ3_S, 1>(a, st);
+            case 2: return pf_launch<kIQ3_S, 2>(a, st);
+            default: return pf_launch<kIQ3_S, 4>(a, st);
         }
     }
     switch (g.nt) {
