@@ -84,6 +84,12 @@ template <>
 struct PfType<kQ4_K> {
     static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 144, XB = 32;
 };
+// Q5_K: as Q4_K, 176-byte units; at most 64 tokens per tile (three digit
+// planes per sub-block, and 128-token stages would not fit LDS twice).
+template <>
+struct PfType<kQ5_K> {
+    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 176, XB = 32;
+};
 template <>
 struct PfType<kQ8_0> {
     static constexpr uint32_t PR = 128, TSPLIT = 2, UB = 272, XB = 64;
@@ -287,6 +293,77 @@ __device__ __forceinline__ void q4_block(const unsigned char *arow, const unsign
         }
         ch = mfma(af[s % 3], f.bh[s], ch);
         cl = mfma(af[s % 3], f.bl[s], cl);
+        if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ch[r] = (ch[r] << 3) + cl[r];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float dd[4] = {dv[q].x, dv[q].y, dv[q].z, dv[q].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = 4 * q + e;
+            acc[r] = fmaf(dd[e], fmaf(f.d, float(ch[r]), -f.dm * mn[r]), acc[r]);
+        }
+    }
+}
+
+
+// ---- Q5_K: B operands of one superblock ------------------------------------
+// Reference dequantizeQ5_KBlock (GGMLDequantize.hpp:392-402): the Q4_K
+// header and nibbles plus a fifth bit per weight, bit s of qh[i] for element
+// i of sub-block s; w = d*sc_s*q - dmin*m_s with q = nibble + 16 b. So
+// sc_s q = 8 (h_s n + 2 sc_s b) + l_s n: the bit plane 2 sc_s b (<= 126)
+// goes into the hi chain's accumulator after the h_s n plane, and C =
+// 8*hi + lo as for Q4_K.
+struct Q5Frag : Q4Frag {
+    v4i bb[8];
+};
+struct Q5Raw : Q4Raw {
+    u4 qh;
+};
+__device__ __forceinline__ void q5_read(Q5Raw &r, const unsigned char *blk, uint32_t g) {
+    r.h = lds4(blk);
+    r.qh = lds4(blk + 16 + 16 * g);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) r.q[p] = lds4(blk + 48 + 32 * p + 16 * g);
+}
+__device__ __forceinline__ void q5_convert(const Q5Raw &r, uint32_t g, Q5Frag &f) {
+    q4_convert(r, g, f);
+    const u4 h = r.h;
+    const uint32_t sc[2] = {h.y & 0x3F3F3F3Fu, (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u)};
+    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+        const uint32_t m2 = 2u * bcast16(sc[sb >> 2], sb & 3);  // 2 sc_s in both 16-bit halves (<= 126)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f.bb[sb][k] = pkmul((qh[k] >> sb) & 0x01010101u, m2);
+    }
+}
+__device__ __forceinline__ void q5_block(const unsigned char *arow, const unsigned char *dgp, const float *d8,
+                                         const Q5Frag &f, uint32_t j, uint32_t g, float (&acc)[16]) {
+    auto aread = [&](int s) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
+    };
+    const v4i dgv = as_v4i(lds4(dgp));
+    v4i af[3];
+    af[0] = aread(0);
+    af[1] = aread(1);
+    __builtin_amdgcn_sched_barrier(0);
+    v16i ch = {}, cl = {};
+    v16f mn;
+    float4 dv[4];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        if (s + 2 < 8) af[(s + 2) % 3] = aread(s + 2);
+        if (s == 2) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
+        }
+        ch = mfma(af[s % 3], f.bh[s], ch);
+        cl = mfma(af[s % 3], f.bl[s], cl);
+        ch = mfma(af[s % 3], f.bb[s], ch);
         if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -706,6 +783,21 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                              reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g, f, j, g,
                              acc[t]);
                 }
+            } else if constexpr (TYPE == kQ5_K) {
+                Q5Frag f;
+                {
+                    Q5Raw rr;
+                    q5_read(rr, bb + L::W + rl * T::UB, g);
+                    q5_convert(rr, g, f);
+                }
+#pragma unroll
+                for (int t = 0; t < NB; ++t) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    const uint32_t tok = 32 * (tg * NB + t) + j;
+                    q5_block(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g,
+                             reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g, f, j, g,
+                             acc[t]);
+                }
             } else if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S) {
                 I3Frag f;
                 if constexpr (TYPE == kIQ3_XXS)
@@ -922,13 +1014,14 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
 // else 128 (Q8_0: 64 or 128, as its waves split the tile's tokens in two).
 int pf_nt(int type, uint32_t M) {
     static_assert(PLds<kIQ3_XXS, 4>::total <= 160 * 1024 && PLds<kIQ3_S, 4>::total <= 160 * 1024 &&
+                      PLds<kQ5_K, 2>::total <= 160 * 1024 &&
                       PLds<kQ4_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ8_0, 4>::total <= 160 * 1024,
                   "LDS of one workgroup");
     const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
-    return type == kQ8_0 ? std::max(nt, 2) : nt;
+    return type == kQ8_0 ? std::max(nt, 2) : type == kQ5_K ? std::min(nt, 2) : nt;
 }
-uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // IQ3_XXS, IQ3_S: 256 too
+uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // Q5_K, IQ3_XXS, IQ3_S: 256 too
 
 // Split tiles are summed inside the main kernel, by their last contributor,
 // when no tile has more than kFusedMax contributors: that workgroup reads the
@@ -967,7 +1060,7 @@ PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_
 // tiles measured as fast or faster).
 PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     const PfGeom g = pf_geom_nt(type, pf_nt(type, M), M, N, K, num_cu);
-    if (g.nt != 4 || type == kQ8_0 || pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256)) return g;
+    if (g.nt != 4 || type == kQ8_0 || type == kQ5_K || pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256)) return g;
     const PfGeom h = pf_geom_nt(type, 2, M, N, K, num_cu);
     return pf_fused(uint64_t(h.ntiles) * (K / 256), h.G, K / 256) ? h : g;
 }
@@ -992,7 +1085,9 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
 
 }  // namespace
 
-bool prefill_type(int type) { return type == kQ4_K || type == kQ8_0 || type == kIQ3_XXS || type == kIQ3_S; }
+bool prefill_type(int type) {
+    return type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kIQ3_XXS || type == kIQ3_S;
+}
 
 // Workspace: the per-tile arrival counters (256-byte rounded), then the
 // partial tiles, two per workgroup.
@@ -1011,7 +1106,7 @@ size_t prefill_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int
 hipError_t launch_prefill(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N,
                           uint32_t K, int num_cu, void *workspace, hipStream_t st) {
     if (!prefill_type(type) || M == 0 || N == 0 || K == 0 || K % 256 || workspace == nullptr ||
-        ((type == kQ4_K || type == kQ8_0) && act.dg == nullptr))
+        ((type == kQ4_K || type == kQ5_K || type == kQ8_0) && act.dg == nullptr))
         return hipErrorInvalidValue;
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
@@ -1042,6 +1137,7 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
             default: return pf_launch<kIQ3_XXS, 4>(a, st);
         }
     }
+    if (type == kQ5_K) return g.nt == 1 ? pf_launch<kQ5_K, 1>(a, st) : pf_launch<kQ5_K, 2>(a, st);
     if (type == kIQ3_S) {
         switch (g.nt) {
             case 1: return pf_launch<kIQ3_S, 1>(a, st);
