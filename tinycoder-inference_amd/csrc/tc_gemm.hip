@@ -1,6 +1,6 @@
 // tc_gemm.hip -- prefill GEMM: out[m][n] = W[n] . x[m] for M tokens against raw
-// GGUF weight rows of Q5_K, Q6_K and IQ2_S, on the int8 matrix cores
-// (v_mfma_i32_32x32x32_i8). (Q4_K, Q8_0, IQ3_XXS and IQ3_S run the
+// GGUF weight rows of Q6_K and IQ2_S, on the int8 matrix cores
+// (v_mfma_i32_32x32x32_i8). (Q4_K, Q5_K, Q8_0, IQ3_XXS and IQ3_S run the
 // register-conversion kernel of tc_prefill.hip.)
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698) with
@@ -19,16 +19,11 @@
 // consumers (the activation plane loaded straight into LDS, MFMAs on the
 // other half).
 //
-// Every weight of a superblock becomes an exact integer e written to two int8
-// planes, e = 128*hi + lo, so that one MFMA chain over the hi plane, a shift
-// by 7 and the lo chain on top give sum_s e . x exactly:
-//  * Q5_K: a weight of sub-block s is w = d*sc_s*q - dmin*m_s with q 5-bit
-//    (sc_s*q <= 1953); the min term sum_s m_s * (x-sum of sub-block s) is one
-//    more pair of MFMAs over 8 useful k-slots, with the activation pair sums
-//    split into int8 digits the same way. Per superblock and output: acc +=
-//    d8 * (d*main - dmin*min). (The Q4_K producer code is shared with it.)
-//  * Q6_K and IQ2_S write their signed integer weights (sc*(q-32),
-//    (2ls+1)*(+-grid value)) as signed digits and have no min term.
+// Every weight of a superblock becomes an exact signed integer e (Q6_K
+// sc*(q-32), IQ2_S (2ls+1)*(+-grid value)) written to two int8 planes,
+// e = 128*hi + lo, so that one MFMA chain over the hi plane, a shift by 7 and
+// the lo chain on top give sum_s e . x exactly. Per superblock and output:
+// acc += d8 * d * main.
 //
 // MFMA operands: lane l feeds row (l & 31) and the 16 bytes of k-group
 // (l >> 5) of both A (weights) and B (activations), so each product pairs the
@@ -43,117 +38,57 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-constexpr int GT = 256;       // threads per workgroup (Q8_0; Q4_K has 2*GT, half producers)
+constexpr int GT = 256;       // producer threads per workgroup
 constexpr int GN = 64;        // weight rows per workgroup tile
 constexpr int GM = 128;       // tokens per workgroup tile
-constexpr int PL = 272;       // LDS plane row stride (256 + 16: conflict-free b128 reads)
+constexpr int PL = 272;       // LDS weight-plane row stride (256 + 16: conflict-free b128 reads)
 
-// LDS layout (bytes); at most 80 KB for either weight type, so that two
-// workgroups fit a CU and one's conversion / epilogue overlaps the other's
-// MFMA work.
-// Weight types whose products run on int8 digit planes: every weight of a
-// superblock becomes an exact integer e (Q4_K sc*q, Q6_K sc*(q-32), IQ2_S
-// (2ls+1)*signed grid value) written as two int8 planes, 128*hi + lo.
-__host__ __device__ constexpr bool dig_type(int t) {
-    return t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ2_S;
-}
-// K-quants with a per-sub-block min (w = d*sc*q - dmin*m): the min term runs
-// on one more MFMA pair against the activation pair sums.
-__host__ __device__ constexpr bool min_type(int t) { return t == kQ4_K || t == kQ5_K; }
 // Codebook bytes the converter reads from LDS (past the two stage buffers).
 __host__ __device__ constexpr uint32_t grid_bytes(int t) {
     return t == kIQ2_S ? 1024 * 8 : 0;
 }
 
-template <int TYPE>
+// One stage buffer (bytes).
 struct GLds {
-    static constexpr bool K = dig_type(TYPE);
-    static constexpr bool M4 = min_type(TYPE);  // the K-quant min term
-    static constexpr uint32_t A0 = 0;                                 // Q4_K hi plane / Q8_0 weights [GN][PL]
-    static constexpr uint32_t A1 = A0 + GN * PL;                      // Q4_K lo plane [GN][PL]
-    static constexpr uint32_t AM = A1 + (K ? GN * PL : 0);            // Q4_K mins, 8 bytes + 24 zero [GN][32]
-    static constexpr uint32_t AS = AM + (M4 ? GN * 32 : 0);           // row d [GN] (IQ2_S: d/8) | Q8_0 dw [GN][8]
-    static constexpr uint32_t AD = AS + (K ? GN * 4 : GN * 32);       // Q4_K dmin [GN]
-    // activation int8 [GM][BP]; Q4_K: 256-byte rows, 16-byte chunk j of
-    // token t at slot j ^ (t & 15) (written by direct-to-LDS loads)
-    static constexpr uint32_t BP = K ? 256 : PL;
-    static constexpr uint32_t B = AD + (M4 ? GN * 4 : 0);
-    static constexpr uint32_t BL = B + GM * BP;                       // Q4_K pair-sum low digits, 8 + 24 zero [GM][32]
-    static constexpr uint32_t BH = BL + (M4 ? GM * 32 : 0);           // Q4_K pair-sum high digits [GM][32]
-    static constexpr uint32_t BD = BH + (M4 ? GM * 32 : 0);           // Q8_K d [GM] | Q8_0 d [GM][8]
-    static constexpr uint32_t RAW = BD + (K ? GM * 4 : GM * 32);      // Q8_0 raw weight tile [GN][272]
-    static constexpr uint32_t bytes = RAW + (K ? 0 : GN * 272);
+    static constexpr uint32_t A0 = 0;                  // hi digit plane [GN][PL]
+    static constexpr uint32_t A1 = A0 + GN * PL;       // lo digit plane [GN][PL]
+    static constexpr uint32_t AS = A1 + GN * PL;       // row d [GN] (IQ2_S: d/8)
+    // activation int8 [GM][256]: 16-byte chunk j of token t at slot
+    // j ^ (t & 15) (written by direct-to-LDS loads)
+    static constexpr uint32_t BP = 256;
+    static constexpr uint32_t B = AS + GN * 4;
+    static constexpr uint32_t BD = B + GM * BP;        // Q8_K d [GM]
+    static constexpr uint32_t bytes = BD + GM * 4;
 };
 
 struct GemmArgs {
     const uint8_t *W;
     const int8_t *qs;       // activations [M][K]
-    const float *d8;        // [M][K/256] (Q8_K) or [M][K/32] (Q8_0)
-    const int16_t *bsums;   // [M][K/16] (Q8_K)
-    float *out;             // [M][N] when nsplit == 1, else partials [nsplit][M][N]
+    const float *d8;        // [M][K/256] (Q8_K)
+    float *out;             // [M][N]
     uint32_t M, N, K;
     uint32_t row_bytes;     // bytes per weight row
     uint32_t ntm;           // token tiles
     uint32_t nblk;          // superblocks per row
-    uint32_t split_blk;     // superblocks per K-slice (Q8_0 split-K)
-    uint32_t ntiles;        // output tiles (Q4_K stream-K)
+    uint32_t ntiles;        // output tiles
     uint32_t skg;           // stream-K workgroups
-    float *ws;              // Q4_K stream-K partial tiles [grid][2][GM][GN]
-    // Grouped (MoE) mode: token tile i covers rows [mt[3i], mt[3i+1]) of the
-    // expert-sorted activations and uses expert mt[3i+2]'s matrix at
-    // W + expert * wstride; the tile count is read from *ntm_dev (written on
-    // the device by the router).
-    const uint32_t *mt;
-    const uint32_t *ntm_dev;
-    uint64_t wstride;
-    uint32_t ntn;           // row blocks (N tiles)
+    float *ws;              // stream-K partial tiles [grid][2][GM][GN]
 };
 
 __device__ __forceinline__ u4 lds4(const unsigned char *p) { return *reinterpret_cast<const u4 *>(p); }
 __device__ __forceinline__ v4i as_v4i(u4 v) { return __builtin_bit_cast(v4i, v); }
 
-// Q4_K 6-bit scale/min of sub-block j (reference get_scale_min_k4,
-// GGMLDequantize.hpp:436-447), from the 12 scale bytes.
-__device__ __forceinline__ void q4k_scale_min(const uint8_t *q, int j, uint32_t &sc, uint32_t &mn) {
-    if (j < 4) {
-        sc = q[j] & 63;
-        mn = q[j + 4] & 63;
-    } else {
-        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-    }
-}
-
-// sc * (4 values of up to 5 bits packed one per byte) -> (hi, lo) digit
-// bytes: byte b of the result pair holds (sc*q_b) >> 7 and (sc*q_b) & 127
-// (sc*q_b <= 63*31 < 2048).
-__device__ __forceinline__ void digits4(uint32_t q, uint32_t sc, uint32_t &hi, uint32_t &lo) {
-    const uint32_t e = (q & 0x001F001Fu) * sc;          // bytes 0, 2 as 16-bit lanes
-    const uint32_t o = ((q >> 8) & 0x001F001Fu) * sc;   // bytes 1, 3
-    lo = (e & 0x007F007Fu) | ((o & 0x007F007Fu) << 8);
-    hi = ((e >> 7) & 0x000F000Fu) | (((o >> 7) & 0x000F000Fu) << 8);
-}
-
 template <int TYPE>
 struct GPrefetch {
-    // Q4_K: the 16-byte header and the 32 quant bytes this thread converts
-    // (row tid/4, quarter tid%4); Q5_K: the same and the 32 qh bytes; IQ2_S:
-    // the bytes of the two 32-chunks 2qq, 2qq+1 (4-byte-aligned
-    // words, realigned on conversion); Q6_K: its 16-byte runs of ql (two) and qh,
-    // read from 4-byte-aligned addresses (blocks are 2-byte aligned) with
-    // their fifth dwords in ex, then the scale bytes and d. Q8_0: raw 16-byte
-    // chunks of the tile.
-    static constexpr int RAWC = TYPE == kQ4_K || TYPE == kQ6_K       ? 3
-                                : TYPE == kQ5_K                       ? 5
-                                                                : TYPE == kIQ2_S                      ? 0
-                                                                      : (GN * 272 / 16 + GT - 1) / GT;
-    static constexpr int EXC = TYPE == kQ6_K ? 7 : TYPE == kIQ2_S ? 9 : 1;
-    u4 raw[RAWC > 0 ? RAWC : 1];
+    // IQ2_S: the bytes of the two 32-chunks 2qq, 2qq+1 (4-byte-aligned
+    // words, realigned on conversion); Q6_K: its 16-byte runs of ql (two) and
+    // qh, read from 4-byte-aligned addresses (blocks are 2-byte aligned) with
+    // their fifth dwords in ex, then the scale bytes and d.
+    static constexpr int RAWC = TYPE == kQ6_K ? 3 : 1;
+    static constexpr int EXC = TYPE == kQ6_K ? 7 : 9;
+    u4 raw[RAWC];
     uint32_t ex[EXC];
-    uint32_t sh;           // Q6_K, IQ2_S: the block's byte offset mod 4
-    static constexpr int ACTC = TYPE == kQ8_0 ? GM * 16 / GT : 0;
-    u4 act[ACTC > 0 ? ACTC : 1];  // 16-byte activation chunks (Q8_0; Q4_K loads them straight into LDS)
-    u4 side;               // Q8_K bsums (256 chunks) or Q8_0 d (256 chunks)
+    uint32_t sh;           // the block's byte offset mod 4
     float d8;              // Q8_K d (128 tokens)
 };
 
@@ -161,10 +96,9 @@ struct GPrefetch {
 // offsets; superblock b only moves the scalar offsets. Rows past N and tokens
 // past M fall outside the descriptors and load zeros (never stored).
 struct GSrc {
-    __amdgpu_buffer_rsrc_t w, q, d, bs;
-    uint32_t vw, vw2, vq, vd, vbs;  // per-lane offsets (vw2: Q4_K quant bytes / unused)
-    uint32_t vo[4];                 // Q6_K: this thread's byte offsets inside a block; IQ types: vo[3] the quarter
-    uint32_t vr[5];                 // Q8_0 raw chunks
+    __amdgpu_buffer_rsrc_t w, d;
+    uint32_t vw, vd;   // per-lane offsets
+    uint32_t vo[4];    // Q6_K: this thread's byte offsets inside a block; IQ2_S: vo[3] the quarter
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t grsrc(const void *p, uint64_t bytes) {
@@ -172,18 +106,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t grsrc(const void *p, uint64_t 
 }
 
 template <int TYPE>
-__device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t tid,
-                                         const uint8_t *W = nullptr) {
+__device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t tid) {
     GSrc g;
     // whole dwords: the range check zeroes a dword that is only partly in
     // range, and 2-byte-aligned units (Q6_K, IQ2_S) end 2 bytes into
     // one when their count is odd (it stays in the page of the last byte)
-    g.w = grsrc(W != nullptr ? W : a.W, (uint64_t(a.N) * a.row_bytes + 3) & ~uint64_t(3));
-    g.q = grsrc(a.qs, uint64_t(a.M) * a.K);
-    g.d = grsrc(a.d8, uint64_t(a.M) * (a.K / (TYPE == kQ8_0 ? 32 : 256)) * 4);
-    g.bs = grsrc(a.bsums, TYPE == kQ8_0 ? 0 : uint64_t(a.M) * (a.K / 16) * 2);
+    g.w = grsrc(a.W, (uint64_t(a.N) * a.row_bytes + 3) & ~uint64_t(3));
+    g.d = grsrc(a.d8, uint64_t(a.M) * (a.K / 256) * 4);
     g.vw = (n0 + tid / 4) * a.row_bytes;
-    g.vw2 = g.vw + (TYPE == kQ5_K ? 48 : 16) + 32 * (tid & 3);
     if constexpr (TYPE == kQ6_K) {
         // thread (row tid/4, half n = bit 1, part p = bit 0): ql[64n + 16p ..],
         // ql[64n + 32 + 16p ..], qh[32n + 16p ..] (16 bytes each), scales 8n..8n+7
@@ -196,34 +126,14 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
         g.vo[0] = g.vo[1] = g.vo[2] = 0;
         g.vo[3] = tid & 3;  // IQ2_S: the thread's quarter
     }
-    // Activations are block-major: 256-column block b of token m at b * M + m.
-    g.vq = (m0 + tid / 16) * 256 + 16 * (tid & 15);
-    const uint32_t ms = m0 + (tid & 255) / 2;
-    g.vbs = ms * 32 + 16 * (tid & 1);
     g.vd = (m0 + (tid & 127)) * 4;
-#pragma unroll
-    for (int i = 0; i < 5; ++i) {
-        const uint32_t c = tid + i * GT, r = c / 17, w = c - r * 17;
-        g.vr[i] = c < GN * 17 ? (n0 + r) * a.row_bytes + 16 * w : 0x80000000u;
-    }
     return g;
 }
 
 template <int TYPE>
 __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, uint32_t b, GPrefetch<TYPE> &p) {
     constexpr uint32_t UB = unit_bytes(TYPE);
-    if constexpr (TYPE == kQ4_K) {
-        p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw, b * UB, 0);
-        p.raw[1] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2, b * UB, 0);
-        p.raw[2] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2 + 16, b * UB, 0);
-    } else if constexpr (TYPE == kQ5_K) {
-        // 176-byte blocks: every piece 16-byte aligned
-        p.raw[0] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw, b * UB, 0);
-        p.raw[1] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw + 16, b * UB, 0);
-        p.raw[2] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw + 32, b * UB, 0);
-        p.raw[3] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2, b * UB, 0);
-        p.raw[4] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vw2 + 16, b * UB, 0);
-    } else if constexpr (TYPE == kIQ2_S) {
+    if constexpr (TYPE == kIQ2_S) {
         // 2-byte-aligned blocks; each piece from its 4-byte-aligned address
         // down, the block start's offset mod 4 in sh
         const uint32_t blk = g.vw + b * UB;
@@ -242,7 +152,8 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
         p.ex[7] = w32(66 + 2 * qq);       // qh bytes 2qq, 2qq+1
         p.ex[8] = w32(74 + 2 * qq);       // scale bytes 2qq, 2qq+1
         p.ex[6] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al, 0, 0);  // d
-    } else if constexpr (TYPE == kQ6_K) {
+    } else {
+        static_assert(TYPE == kQ6_K, "Q6_K and IQ2_S only");
         const uint32_t blk = g.vw + b * UB;  // block start (2-byte aligned)
         p.sh = blk & 3;
         const uint32_t al = blk & ~3u;  // every vo is a multiple of 4
@@ -254,72 +165,8 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
 #pragma unroll
         for (int i = 0; i < 3; ++i) p.ex[3 + i] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + g.vo[3] + 4 * i, 0, 0);
         p.ex[6] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + 208, 0, 0);  // d (bytes 208, 209)
-    } else {
-#pragma unroll
-        for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i)
-            p.raw[i] = __builtin_amdgcn_raw_buffer_load_b128(g.w, g.vr[i], b * UB, 0);
     }
-#pragma unroll
-    for (int i = 0; i < GPrefetch<TYPE>::ACTC; ++i)  // chunk tid + 256 i: token + 16 i
-        p.act[i] = __builtin_amdgcn_raw_buffer_load_b128(g.q, g.vq, b * a.M * 256 + i * 16 * 256, 0);
-    if constexpr (TYPE == kQ8_0)
-        p.side = __builtin_amdgcn_raw_buffer_load_b128(g.d, g.vbs, b * a.M * 32, 0);
-    else if constexpr (min_type(TYPE))
-        p.side = __builtin_amdgcn_raw_buffer_load_b128(g.bs, g.vbs, b * a.M * 32, 0);
-    if constexpr (dig_type(TYPE))
-        p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * a.M * 4, 0));
-}
-
-// Q4_K / Q5_K weights of this thread (row tid/4: header + qs[32qq .. 32qq+31],
-// Q5_K also bits 2qq, 2qq+1 of the 32 qh bytes) -> the two digit planes, the
-// mins and the row scales. Q5_K (reference dequantizeQ5_KBlock,
-// include/GGMLDequantize.hpp:392-402) shares Q4_K's header and scale
-// packing; its fifth bit of weight l of sub-block 2qq + h is bit 2qq + h of
-// qh[l].
-template <int TYPE>
-__device__ __forceinline__ void q4k_convert(const u4 &hdr, const u4 &qa, const u4 &qb, unsigned char *lds,
-                                            uint32_t tid, const u4 &qh0 = u4{}, const u4 &qh1 = u4{}) {
-    using L = GLds<TYPE>;
-    const uint32_t r = tid / 4, qq = tid & 3;
-    // the 8 6-bit scales / mins as bytes (reference get_scale_min_k4,
-    // GGMLDequantize.hpp:436-447): sub-blocks 0-3 from the low words, 4-7 from
-    // the packed high bits
-    const uint32_t scl = hdr.y & 0x3F3F3F3Fu, mnl = hdr.z & 0x3F3F3F3Fu;
-    const uint32_t sch = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
-    const uint32_t mnh = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
-    const uint32_t sh = 16 * (qq & 1);
-    const uint32_t scw = (qq < 2 ? scl : sch) >> sh, mnw = (qq < 2 ? mnl : mnh) >> sh;
-    const uint32_t sc0 = scw & 0xFF, sc1 = (scw >> 8) & 0xFF, mn0 = mnw & 0xFF, mn1 = (mnw >> 8) & 0xFF;
-    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-    const uint32_t qh[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
-    uint32_t hl[8], ll[8], hh[8], lh[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        uint32_t vl = q[k] & 0x0F0F0F0Fu, vh = (q[k] >> 4) & 0x0F0F0F0Fu;
-        if constexpr (TYPE == kQ5_K) {
-            vl |= ((qh[k] >> (2 * qq)) & 0x01010101u) << 4;
-            vh |= ((qh[k] >> (2 * qq + 1)) & 0x01010101u) << 4;
-        }
-        digits4(vl, sc0, hl[k], ll[k]);
-        digits4(vh, sc1, hh[k], lh[k]);
-    }
-    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
-    const uint32_t s0 = 64 * qq, s1 = 64 * qq + 32;  // k offsets of sub-blocks 2qq, 2qq+1
-    *reinterpret_cast<u4 *>(a0 + s0) = u4{hl[0], hl[1], hl[2], hl[3]};
-    *reinterpret_cast<u4 *>(a0 + s0 + 16) = u4{hl[4], hl[5], hl[6], hl[7]};
-    *reinterpret_cast<u4 *>(a1 + s0) = u4{ll[0], ll[1], ll[2], ll[3]};
-    *reinterpret_cast<u4 *>(a1 + s0 + 16) = u4{ll[4], ll[5], ll[6], ll[7]};
-    *reinterpret_cast<u4 *>(a0 + s1) = u4{hh[0], hh[1], hh[2], hh[3]};
-    *reinterpret_cast<u4 *>(a0 + s1 + 16) = u4{hh[4], hh[5], hh[6], hh[7]};
-    *reinterpret_cast<u4 *>(a1 + s1) = u4{lh[0], lh[1], lh[2], lh[3]};
-    *reinterpret_cast<u4 *>(a1 + s1 + 16) = u4{lh[4], lh[5], lh[6], lh[7]};
-    // 32-byte rows: bytes 0..7 the mins of sub-blocks 0..7, 8..31 zero
-    reinterpret_cast<uint16_t *>(lds + L::AM + r * 32)[qq] = uint16_t(mn0 | (mn1 << 8));
-    // Unconditional stores (the threads of a row that overlap write the same
-    // values), so no lane-masked branch splits the producer's wait counts.
-    *reinterpret_cast<uint2 *>(lds + L::AM + r * 32 + 8 + 8 * min(qq, 2u)) = uint2{0u, 0u};
-    reinterpret_cast<float *>(lds + L::AS)[r] = h2f(hdr.x & 0xFFFF);
-    reinterpret_cast<float *>(lds + L::AD)[r] = h2f(hdr.x >> 16);
+    p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * a.M * 4, 0));
 }
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
@@ -361,7 +208,7 @@ __device__ __forceinline__ uint32_t realign(uint32_t hi, uint32_t lo, uint32_t s
 // q = ql nibble | (qh 2-bit field) << 4 (reference dequantizeQ6_KBlock,
 // include/GGMLDequantize.hpp:503-527), e = sc[8n + 2c + p] * (q - 32).
 __device__ __forceinline__ void q6k_convert(const GPrefetch<kQ6_K> &p, unsigned char *lds, uint32_t tid) {
-    using L = GLds<kQ6_K>;
+    using L = GLds;
     const uint32_t r = tid / 4, n = (tid >> 1) & 1, pp = tid & 1;
     uint32_t w[3][4];
 #pragma unroll
@@ -404,7 +251,7 @@ __device__ __forceinline__ void q6k_convert(const GPrefetch<kQ6_K> &p, unsigned 
 // (GGMLDequantize.hpp:1215-1242, :2028-2057).
 __device__ __forceinline__ void iq2s_convert(const GPrefetch<kIQ2_S> &p, unsigned char *lds, const uint32_t *grid,
                                              uint32_t tid) {
-    using L = GLds<kIQ2_S>;
+    using L = GLds;
     const uint32_t r = tid / 4, qq = tid & 3;
     const uint32_t s8b = (p.sh + 2) & 3;  // qs at 2 + 8qq and signs at 34 + 8qq: the same offset mod 4
     const uint32_t qs[2] = {realign(p.ex[1], p.ex[0], s8b), realign(p.ex[2], p.ex[1], s8b)};
@@ -439,64 +286,17 @@ __constant__ uint64_t c_iq2s_grid[1024] = {
 #include "iq2s_grid.inc"
 };
 
-// Staged registers -> LDS: the activation plane and its side data; Q4_K
-// weights converted to the digit planes straight from registers, Q8_0 raw
-// rows to a staging area (converted after the barrier).
+// Staged registers -> LDS: the weights converted to the digit planes
+// straight from registers, and the activation scales.
 template <int TYPE>
 __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned char *lds, uint32_t tid,
                                            const uint32_t *grid = nullptr) {
-    using L = GLds<TYPE>;
-    if constexpr (TYPE == kQ4_K) {
-        q4k_convert<kQ4_K>(p.raw[0], p.raw[1], p.raw[2], lds, tid);
-    } else if constexpr (TYPE == kQ5_K) {
-        q4k_convert<kQ5_K>(p.raw[0], p.raw[3], p.raw[4], lds, tid, p.raw[1], p.raw[2]);
-    } else if constexpr (TYPE == kIQ2_S) {
+    using L = GLds;
+    if constexpr (TYPE == kIQ2_S)
         iq2s_convert(p, lds, grid, tid);
-    } else if constexpr (TYPE == kQ6_K) {
+    else
         q6k_convert(p, lds, tid);
-    } else {
-#pragma unroll
-        for (int i = 0; i < GPrefetch<TYPE>::RAWC; ++i) {
-            const uint32_t c = tid + i * GT;
-            if (c < GN * 272 / 16) *reinterpret_cast<u4 *>(lds + L::RAW + 16 * c) = p.raw[i];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < GPrefetch<TYPE>::ACTC; ++i) {
-        const uint32_t c = tid + i * GT;
-        *reinterpret_cast<u4 *>(lds + L::B + (c / 16) * PL + 16 * (c & 15)) = p.act[i];
-    }
-    if constexpr (TYPE == kQ8_0 || min_type(TYPE)) {
-        const uint32_t m = (tid & 255) / 2, h = tid & 1;
-        if constexpr (TYPE == kQ8_0) {
-            *reinterpret_cast<u4 *>(lds + L::BD + m * 32 + 16 * h) = p.side;
-        } else {
-            // bsums (16 int16) -> 8 pair sums, split into int8 digits; this
-            // thread has pairs 4h..4h+3
-            uint32_t lo = 0, hi = 0;
-            const uint32_t w[4] = {p.side.x, p.side.y, p.side.z, p.side.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int ps = int(int16_t(w[i] & 0xFFFF)) + int(int16_t(w[i] >> 16));
-                lo |= uint32_t(ps & 127) << (8 * i);
-                hi |= uint32_t(uint8_t(int8_t(ps >> 7))) << (8 * i);
-            }
-            // 32-byte rows: bytes 0..7 the digits, 8..31 zero (the k slots
-            // the min-term MFMA must not count)
-            uint32_t *bl = reinterpret_cast<uint32_t *>(lds + L::BL + m * 32);
-            uint32_t *bh = reinterpret_cast<uint32_t *>(lds + L::BH + m * 32);
-            bl[h] = lo;
-            bh[h] = hi;
-#pragma unroll
-            for (int z = 0; z < 3; ++z) {
-                bl[2 + 3 * h + z] = 0;
-                bh[2 + 3 * h + z] = 0;
-            }
-        }
-    }
-    if constexpr (dig_type(TYPE)) {
-        reinterpret_cast<float *>(lds + L::BD)[tid & (GM - 1)] = p.d8;  // threads tid and tid+128 hold the same d
-    }
+    reinterpret_cast<float *>(lds + L::BD)[tid & (GM - 1)] = p.d8;  // threads tid and tid+128 hold the same d
 }
 
 __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
@@ -511,7 +311,7 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
 template <int TYPE, int CW>
 __device__ __forceinline__ void dig_act_to_lds(const GemmArgs &a, uint32_t m0, uint32_t b, unsigned char *ldsb,
                                                uint32_t w, uint32_t lane) {
-    using L = GLds<TYPE>;
+    using L = GLds;
     typedef int v4i32 __attribute__((ext_vector_type(4)));
     const uint64_t base = reinterpret_cast<uint64_t>(a.qs);
     const v4i32 rs = {int(uint32_t(base)), int(uint32_t(base >> 32) & 0xFFFF), int(a.M * a.K), 0x00020000};
@@ -543,8 +343,7 @@ __device__ __forceinline__ void dig_act_to_lds(const GemmArgs &a, uint32_t m0, u
 template <int TYPE, int NTT>
 __device__ __forceinline__ void dig_consume(const unsigned char *lds, uint32_t wn, uint32_t tok0, uint32_t li,
                                             uint32_t lg, float (&acc)[NTT][16]) {
-    using L = GLds<TYPE>;
-    constexpr bool MIN = L::M4;
+    using L = GLds;
     const unsigned char *arow = lds + (32 * wn + li) * PL + 16 * lg;
     // token rows tok0 + 32t + li (all with t % 16 = li % 16)
     auto brow = [&](int t) __attribute__((always_inline)) { return lds + L::B + (tok0 + 32 * t + li) * L::BP; };
@@ -560,13 +359,10 @@ __device__ __forceinline__ void dig_consume(const unsigned char *lds, uint32_t w
     }
 #pragma unroll
     for (int s = 0; s < 8; ++s) al[s] = as_v4i(lds4(arow + L::A1 + 32 * s));
-    v4i am = v4i{0, 0, 0, 0};
-    if constexpr (MIN) am = as_v4i(lds4(lds + L::AM + (32 * wn + li) * 32 + 16 * lg));
     __builtin_amdgcn_sched_barrier(0);
     // One accumulator per token tile: the hi-digit chain, then C = hi << 7
-    // and the lo-digit chain on top (= 128*hi + lo exactly); the min term over
-    // the 8 useful k slots (k-group 0, bytes 0..7) folded the same way.
-    auto chain = [&](int t, v16i &c, v16i &m) __attribute__((always_inline)) {
+    // and the lo-digit chain on top (= 128*hi + lo exactly).
+    auto chain = [&](v16i &c) __attribute__((always_inline)) {
         c = v16i{};
 #pragma unroll
         for (int s = 0; s < 8; ++s) c = mfma(ah[s], x[s], c);
@@ -574,55 +370,36 @@ __device__ __forceinline__ void dig_consume(const unsigned char *lds, uint32_t w
         for (int r = 0; r < 16; ++r) c[r] <<= 7;
 #pragma unroll
         for (int s = 0; s < 8; ++s) c = mfma(al[s], x[s], c);
-        if constexpr (MIN) {
-            const uint32_t tb = tok0 + 32 * t + li;
-            const v4i bh = as_v4i(lds4(lds + L::BH + tb * 32 + 16 * lg));
-            const v4i bl = as_v4i(lds4(lds + L::BL + tb * 32 + 16 * lg));
-            m = mfma(am, bh, v16i{});
-#pragma unroll
-            for (int r = 0; r < 16; ++r) m[r] <<= 7;
-            m = mfma(am, bl, m);
-        }
     };
-    auto combine = [&](int t, const v16i &c, const v16i &m) __attribute__((always_inline)) {
+    auto combine = [&](int t, const v16i &c) __attribute__((always_inline)) {
         const float d8 = reinterpret_cast<const float *>(lds + L::BD)[tok0 + 32 * t + li];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t rr = 32 * wn + 8 * q + 4 * lg;
             const float4 dv = *reinterpret_cast<const float4 *>(lds + L::AS + 4 * rr);
             const float dd[4] = {dv.x, dv.y, dv.z, dv.w};
-            if constexpr (MIN) {
-                const float4 mv = *reinterpret_cast<const float4 *>(lds + L::AD + 4 * rr);
-                const float dm[4] = {mv.x, mv.y, mv.z, mv.w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * q + e;
-                    acc[t][r] = fmaf(d8, dd[e] * float(c[r]) - dm[e] * float(m[r]), acc[t][r]);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * q + e;
-                    acc[t][r] = fmaf(d8, dd[e] * float(c[r]), acc[t][r]);
-                }
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * q + e;
+                acc[t][r] = fmaf(d8, dd[e] * float(c[r]), acc[t][r]);
             }
         }
     };
-    v16i c0, m0;
-    chain(0, c0, m0);
+    v16i c0;
+    chain(c0);
     if constexpr (NTT == 2) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) x[s] = as_v4i(lds4(brow(1) + bslot(s)));
-        v16i c1, m1;
-        chain(1, c1, m1);
-        combine(0, c0, m0);
-        combine(1, c1, m1);
+        v16i c1;
+        chain(c1);
+        combine(0, c0);
+        combine(1, c1);
     } else {
-        combine(0, c0, m0);
+        combine(0, c0);
     }
 }
 
-// Q4_K with producer and consumer waves: 4 producer waves load superblock
+// Producer and consumer waves: 4 producer waves load superblock
 // b+2 and convert b+1 into one half of a double-buffered LDS while 4 consumer
 // waves run the MFMAs and the fp32 combination of superblock b from the other
 // half -- the conversion's VALU work overlaps the matrix work on the same
@@ -636,45 +413,22 @@ __device__ __forceinline__ void dig_consume(const unsigned char *lds, uint32_t w
 // Tile t -> (token tile, row block), token tiles fastest: a stream-K
 // workgroup's consecutive tiles reuse one block of weight rows. (Row blocks
 // fastest measured 3-13% slower.)
-// Grouped mode: the same order over the device tile table; mend bounds the
-// stored rows and W is the tile's expert matrix.
 struct TileGeom {
-    uint32_t m0, mend, n0;
-    const uint8_t *W;
+    uint32_t m0, n0;
 };
-template <bool GRP>
-__device__ __forceinline__ TileGeom sk_tile(const GemmArgs &a, uint32_t ntm, uint32_t t) {
-    const uint32_t tm = t % ntm, tn = t / ntm;
-    TileGeom g;
-    g.n0 = tn * GN;
-    if constexpr (GRP) {
-        g.m0 = a.mt[3 * tm];
-        g.mend = a.mt[3 * tm + 1];
-        g.W = a.W + uint64_t(a.mt[3 * tm + 2]) * a.wstride;
-    } else {
-        g.m0 = tm * GM;
-        g.mend = a.M;
-        g.W = a.W;
-    }
-    return g;
-}
-template <bool GRP>
-__device__ __forceinline__ uint32_t sk_ntm(const GemmArgs &a) {
-    if constexpr (GRP)
-        return *a.ntm_dev;
-    else
-        return a.ntm;
+__device__ __forceinline__ TileGeom sk_tile(const GemmArgs &a, uint32_t t) {
+    return TileGeom{(t % a.ntm) * GM, (t / a.ntm) * GN};
 }
 
 __host__ __device__ inline uint32_t sk_begin(uint32_t units, uint32_t grid, uint32_t w) {
     return uint32_t(uint64_t(units) * w / grid);
 }
 
-template <int TYPE, int CW, bool GRP>
+template <int TYPE, int CW>
 __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 + CW / 4, 1 + CW / 4))) void k_gemm_dig(
     GemmArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
-    using L = GLds<TYPE>;
+    using L = GLds;
     constexpr int NTT = 8 / CW;  // 32-token tiles per consumer wave
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -692,8 +446,7 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
         __syncthreads();
     }
 
-    const uint32_t ntm = sk_ntm<GRP>(a);
-    const uint32_t units = (GRP ? ntm * a.ntn : a.ntiles) * a.nblk;
+    const uint32_t units = a.ntiles * a.nblk;
     const uint32_t ub = sk_begin(units, gridDim.x, blockIdx.x), ue = sk_begin(units, gridDim.x, blockIdx.x + 1);
     for (uint32_t u = ub; u < ue;) {
         const uint32_t tile = u / a.nblk;
@@ -702,7 +455,7 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
         const bool whole = b0 == 0 && b1 == a.nblk;
         float *const part = whole ? nullptr : a.ws + (size_t(blockIdx.x) * 2 + (u == ub ? 0 : 1)) * (GM * GN);
         u += b1 - b0;
-        const TileGeom tg = sk_tile<GRP>(a, ntm, tile);
+        const TileGeom tg = sk_tile(a, tile);
         const uint32_t m0 = tg.m0, n0 = tg.n0;
         // Producers step in pairs of superblocks; both sides run bend - b0 barriers.
         const uint32_t bend = b0 + ((b1 - b0 + 1) & ~1u);
@@ -712,7 +465,7 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
         if (producer) {
             // Two superblocks of loads in flight per producer thread: global
             // latency under load exceeds one superblock's compute time.
-            const GSrc gs = gemm_src<TYPE>(a, n0, m0, ptid, tg.W);
+            const GSrc gs = gemm_src<TYPE>(a, n0, m0, ptid);
             GPrefetch<TYPE> pa, pb;
             gemm_prefetch<TYPE>(a, gs, b0, pa);
             gemm_stage<TYPE>(pa, buf(b0), ptid, grid);
@@ -760,7 +513,7 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
                 const float4 v = make_float4(acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]);
                 if (part != nullptr) {
                     *reinterpret_cast<float4 *>(part + ml * GN + nl) = v;  // [token][row] of the tile
-                } else if (m < tg.mend) {
+                } else if (m < a.M) {
                     float *o = a.out + size_t(m) * a.N + n;
                     if (n + 3 < a.N && (a.N & 3) == 0) {
                         *reinterpret_cast<float4 *>(o) = v;
@@ -777,37 +530,24 @@ __global__ __launch_bounds__(GT + 64 * CW) __attribute__((amdgpu_waves_per_eu(1 
 }
 
 // Tiles split over several stream-K workgroups: out = the partial segments
-// summed in workgroup order. Plain mode: kFixSlices workgroups per tile
-// (each a quarter of its entries), workgroup group j taking the tile that
-// holds range boundary j+1, when the boundary splits it and is the first to do
-// so; grouped mode (tile count on the device): one workgroup per possible
-// tile, whole tiles exit.
+// summed in workgroup order. kFixSlices workgroups per tile (each a quarter
+// of its entries), workgroup group j taking the tile that holds range
+// boundary j+1, when the boundary splits it and is the first to do so.
 constexpr uint32_t kFixSlices = 4;
-template <bool GRP>
 __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
-    const uint32_t ntm = sk_ntm<GRP>(a);
-    const uint32_t ntiles = GRP ? ntm * a.ntn : a.ntiles;
-    const uint32_t units = ntiles * a.nblk, G = a.skg;
-    // grouped mode: one workgroup per possible tile (most of them exit; four
-    // per tile made the exits cost more than the sums)
-    constexpr uint32_t SL = GRP ? 1u : kFixSlices;
-    const uint32_t slice = blockIdx.x % SL;
-    uint32_t tile = blockIdx.x / SL;
-    if constexpr (!GRP) {
-        const uint32_t wb = tile + 1, u = sk_begin(units, G, wb);
-        tile = u / a.nblk;
-        if (u % a.nblk == 0 || sk_begin(units, G, wb - 1) > tile * a.nblk) return;
-    }
-    if (tile >= ntiles) return;  // grouped mode: the grid covers the largest possible tile count
+    const uint32_t units = a.ntiles * a.nblk, G = a.skg;
+    const uint32_t slice = blockIdx.x % kFixSlices;
+    const uint32_t wb = blockIdx.x / kFixSlices + 1, ub = sk_begin(units, G, wb);
+    const uint32_t tile = ub / a.nblk;
+    if (ub % a.nblk == 0 || sk_begin(units, G, wb - 1) > tile * a.nblk) return;
     const uint32_t t0 = tile * a.nblk, t1 = t0 + a.nblk;
     // first workgroup whose range holds unit t0
     uint32_t w = uint32_t(uint64_t(t0) * G / units);
     while (w + 1 < G && sk_begin(units, G, w + 1) <= t0) ++w;
     while (w > 0 && sk_begin(units, G, w) > t0) --w;
-    if (sk_begin(units, G, w) <= t0 && sk_begin(units, G, w + 1) >= t1) return;  // one workgroup: stored directly
-    const TileGeom tg = sk_tile<GRP>(a, ntm, tile);
+    const TileGeom tg = sk_tile(a, tile);
     const uint32_t m0 = tg.m0, n0 = tg.n0;
-    constexpr uint32_t per = GM * GN / 4 / SL;  // float4 entries per slice
+    constexpr uint32_t per = GM * GN / 4 / kFixSlices;  // float4 entries per slice
     constexpr uint32_t NI = per / 256;                   // per thread
     static_assert(per % 256 == 0, "a fixup slice is a whole number of 256-thread rounds");
     float4 s[NI];
@@ -837,7 +577,7 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
         const uint32_t i = slice * per + k * 256 + threadIdx.x;
         const uint32_t ml = (4 * i) / GN, nl = (4 * i) % GN;
         const uint32_t m = m0 + ml, n = n0 + nl;
-        if (m >= tg.mend) continue;
+        if (m >= a.M) continue;
         float *o = a.out + size_t(m) * a.N + n;
         if (n + 3 < a.N && (a.N & 3) == 0) {
             *reinterpret_cast<float4 *>(o) = s[k];
@@ -850,97 +590,63 @@ __global__ __launch_bounds__(256) void k_gemm_fixup(GemmArgs a) {
     }
 }
 
-// Split-K partials [nsplit][M][N] -> out[M][N], summed in slice order.
-__global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part, float *__restrict__ out,
-                                                     size_t mn, uint32_t nsplit) {
-    const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= mn) return;
-    float s = part[i];
-    for (uint32_t k = 1; k < nsplit; ++k) s += part[k * mn + i];
-    out[i] = s;
-}
-
-template <int TYPE, bool GRP = false>
+template <int TYPE>
 hipError_t launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t st) {
-    if constexpr (dig_type(TYPE)) {
-        constexpr int CW = 8;  // consumer waves (4, one per SIMD with two token blocks each, measured within 3%)
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_dig<TYPE, CW, GRP>),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (attr != hipSuccess) return attr;
-        const uint32_t lds = 2 * GLds<TYPE>::bytes + grid_bytes(TYPE);
-        k_gemm_dig<TYPE, CW, GRP><<<grid, GT + 64 * CW, lds, st>>>(a);
-    }
+    constexpr int CW = 8;  // consumer waves (4, one per SIMD with two token blocks each, measured within 3%)
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemm_dig<TYPE, CW>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    const uint32_t lds = 2 * GLds::bytes + grid_bytes(TYPE);
+    k_gemm_dig<TYPE, CW><<<grid, GT + 64 * CW, lds, st>>>(a);
     return hipGetLastError();
 }
 
 }  // namespace
 
-// Q4_K stream-K grid: one workgroup per CU, each with at least 4 units.
+// Stream-K grid: one workgroup per CU, each with at least 4 units.
 uint32_t sk_grid(uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     const uint32_t units = ((M + GM - 1) / GM) * ((N + GN - 1) / GN) * (K / 256);
     return std::max(1u, std::min(uint32_t(num_cu), units / 4));
 }
 
-uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
-    if (dig_type(type)) return 1;  // stream-K instead
-    const uint32_t tiles = ((M + GM - 1) / GM) * ((N + GN - 1) / GN);
-    const uint32_t nblk = K / 256;
-    uint32_t s = 1;
-    // Fill the chip: split K while there are fewer tiles than CUs and each
-    // slice keeps at least 4 superblocks.
-    while (tiles * s * 2 <= uint32_t(num_cu) * 2 && nblk / (s * 2) >= 4 && tiles * s < uint32_t(num_cu)) s *= 2;
-    return s;
-}
-
-size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
-    if (dig_type(type)) return size_t(sk_grid(M, N, K, num_cu)) * 2 * GM * GN * 4;
-    const uint32_t s = gemm_splits(type, M, N, K, num_cu);
-    return s > 1 ? size_t(s) * M * N * 4 : 0;
+size_t gemm_workspace_bytes(int, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
+    return size_t(sk_grid(M, N, K, num_cu)) * 2 * GM * GN * 4;
 }
 
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
                        int num_cu, void *workspace, hipStream_t st) {
     if (M == 0 || N == 0 || K == 0 || K % 256) return hipErrorInvalidValue;
+    // Q6_K and IQ2_S here; the other MFMA types run k_prefill (tc_prefill.hip).
+    if (type != kQ6_K && type != kIQ2_S) return hipErrorInvalidValue;
     // 32-bit buffer offsets: the quantized activations (M*K bytes) and one
     // weight matrix must each stay below 4 GiB.
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
         return hipErrorInvalidValue;
-    // Q4_K, Q8_0, IQ3_XXS and IQ3_S run k_prefill (tc_prefill.hip); the other MFMA types here.
-    if (!dig_type(type) || type == kQ4_K) return hipErrorInvalidValue;
-    const uint32_t nsplit = gemm_splits(type, M, N, K, num_cu);
-    if ((nsplit > 1 || dig_type(type)) && workspace == nullptr) return hipErrorInvalidValue;
+    if (workspace == nullptr) return hipErrorInvalidValue;
     GemmArgs a{};
     a.W = static_cast<const uint8_t *>(W);
     a.qs = act.qs;
     a.d8 = act.d;
-    a.bsums = act.bsums;
     a.M = M;
     a.N = N;
     a.K = K;
     a.nblk = K / 256;
     a.row_bytes = a.nblk * unit_bytes(type);
     a.ntm = (M + GM - 1) / GM;
-    a.split_blk = (a.nblk + nsplit - 1) / nsplit;
     a.ntiles = a.ntm * ((N + GN - 1) / GN);
-    if (dig_type(type)) {
-        const uint32_t G = sk_grid(M, N, K, num_cu);
-        a.out = out;
-        a.ws = static_cast<float *>(workspace);
-        a.skg = G;
-        const dim3 g{G, 1u, 1u};
-        hipError_t e = type == kQ5_K     ? launch_gemm_t<kQ5_K>(a, g, st)
-                       : type == kQ6_K   ? launch_gemm_t<kQ6_K>(a, g, st)
-                                         : launch_gemm_t<kIQ2_S>(a, g, st);
-        if (e != hipSuccess) return e;
-        // Any tile split over workgroups? (a range boundary inside a tile)
-        bool split = false;
-        for (uint32_t w = 1; w < G && !split; ++w) split = sk_begin(a.ntiles * a.nblk, G, w) % a.nblk != 0;
-        if (!split) return hipSuccess;
-        k_gemm_fixup<false><<<dim3{(G - 1) * kFixSlices, 1u, 1u}, 256, 0, st>>>(a);
-        return hipGetLastError();
-    }
-    return hipErrorInvalidValue;
+    const uint32_t G = sk_grid(M, N, K, num_cu);
+    a.out = out;
+    a.ws = static_cast<float *>(workspace);
+    a.skg = G;
+    const dim3 g{G, 1u, 1u};
+    hipError_t e = type == kQ6_K ? launch_gemm_t<kQ6_K>(a, g, st) : launch_gemm_t<kIQ2_S>(a, g, st);
+    if (e != hipSuccess) return e;
+    // Any tile split over workgroups? (a range boundary inside a tile)
+    bool split = false;
+    for (uint32_t w = 1; w < G && !split; ++w) split = sk_begin(a.ntiles * a.nblk, G, w) % a.nblk != 0;
+    if (!split) return hipSuccess;
+    k_gemm_fixup<<<dim3{(G - 1) * kFixSlices, 1u, 1u}, 256, 0, st>>>(a);
+    return hipGetLastError();
 }
 
 }  // namespace tc
-

@@ -75,17 +75,17 @@ uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs);
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes);
 uint32_t gemv_max_tokens(int type, uint32_t cols);
 
-// Prefill GEMM (int8 MFMA) for Q5_K, Q6_K, IQ3_XXS, IQ3_S and IQ2_S (Q4_K and
-// Q8_0: launch_prefill): out[M][N] = W x^T with activations already
-// quantized (launch_quant_act over M tokens, block-major). Stream-K over one
-// workgroup per CU; the partial tiles need gemm_workspace_bytes() of scratch.
-uint32_t gemm_splits(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
+// Prefill GEMM (int8 MFMA) for Q6_K and IQ2_S (the other MFMA types:
+// launch_prefill): out[M][N] = W x^T with activations already quantized
+// (launch_quant_act over M tokens, block-major). Stream-K over one workgroup
+// per CU; the partial tiles need gemm_workspace_bytes() of scratch.
 size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
                        int num_cu, void *workspace, hipStream_t st);
 
 // Prefill GEMM with the weights converted in the MFMA lanes' registers, once
-// per token tile of up to 128 tokens (tc_prefill.hip; Q4_K, Q8_0). Needs the
+// per token tile of up to 128 tokens (tc_prefill.hip; Q4_K, Q5_K, Q8_0,
+// IQ3_XXS, IQ3_S). Needs the
 // activations' scale data (act.dg) and prefill_workspace_bytes() of scratch
 // whose first prefill_counter_words() 32-bit words are zero when the launch
 // starts (every launch leaves them zero again).
