@@ -861,8 +861,10 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         // A split tile: publish this segment's partial (system-scope stores
         // go through to memory, where other XCDs' loads find them), then
         // count the arrival. The last of the tile's contributors to arrive
-        // sums the partials in range order (its own from registers) and
-        // writes the tile; nobody waits for anybody.
+        // sums the partials in range order and writes the tile; nobody waits
+        // for anybody. (The stores of one instruction cover two whole 128-byte
+        // lines of the [token][row] partial; 16-byte stores of a [row][token]
+        // layout, partial lines each, measured slower.)
 #pragma unroll
         for (int t = 0; t < NB; ++t)
 #pragma unroll
@@ -886,8 +888,12 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         auto live = [&](uint32_t c) __attribute__((always_inline)) {
             return !GRP || sk_begin(units, a.G, c) != sk_begin(units, a.G, c + 1);
         };
-        uint32_t ncontrib = 0;
-        for (uint32_t c = vf; c <= vl; ++c) ncontrib += live(c) ? 1u : 0u;
+        uint32_t ncontrib = 0, other = v;
+        for (uint32_t c = vf; c <= vl; ++c)
+            if (live(c)) {
+                ++ncontrib;
+                if (c != v) other = c;
+            }
         uint32_t *const flag = reinterpret_cast<uint32_t *>(lds + L::BUF0);  // no reader of the buffers left (barrier above)
         if (tid == 0)
             *flag = __builtin_amdgcn_atomic_inc32(a.ctr + tile, ncontrib - 1, __ATOMIC_RELAXED, "");
@@ -895,14 +901,11 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const bool last = *flag == ncontrib - 1;  // the counter wrapped back to 0
         if (!last) continue;
         const uint32_t first_slot = sk_begin(units, a.G, vf) < t0 ? 1u : 0u;  // vf's second segment
-        // every contributor's partial from memory (this workgroup's too: it
-        // is there already, and acc's registers then hold the sum)
-        for (uint32_t c = vf; c <= vl; ++c) {
-            if (!live(c)) continue;
+        // this lane's partial of contributor c, into p
+        auto ld = [&](uint32_t c, float (&p)[NB][16]) __attribute__((always_inline)) {
             const float *src = a.ws + (size_t(c) * 2 + (c == vf ? first_slot : 0u)) * (TT * PR);
             uint32_t lo = 4 * g * PR + rl;  // this lane's offset, recomputed per contributor
             asm volatile("" : "+v"(lo));
-            float p[NB][16];
 #pragma unroll
             for (int t = 0; t < NB; ++t)
 #pragma unroll
@@ -911,10 +914,28 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     for (int e = 0; e < 4; ++e)
                         p[t][4 * q + e] = __hip_atomic_load(src + (32 * (tg * NB + t) + 8 * q + e) * PR + lo,
                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        };
+        if (ncontrib == 2) {
+            // own + other in either order: the same bits
+            float p[NB][16];
+            ld(other, p);
 #pragma unroll
             for (int t = 0; t < NB; ++t)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[t][r] = c == vf ? p[t][r] : acc[t][r] + p[t][r];
+                for (int r = 0; r < 16; ++r) acc[t][r] += p[t][r];
+        } else {
+            // every contributor's partial from memory in range order (this
+            // workgroup's too: it is there already, and acc's registers then
+            // hold the sum)
+            for (uint32_t c = vf; c <= vl; ++c) {
+                if (!live(c)) continue;
+                float p[NB][16];
+                ld(c, p);
+#pragma unroll
+                for (int t = 0; t < NB; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[t][r] = c == vf ? p[t][r] : acc[t][r] + p[t][r];
+            }
         }
 #pragma unroll
         for (int t = 0; t < NB; ++t)
@@ -1057,10 +1078,14 @@ PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_
 // inside the kernel (at most kFusedMax contributors) and 128 would not: the
 // weights are converted twice as often, but the fixup launch goes (Q4_K
 // 17408x5120, M = 128: 52.2 -> 49.7 us; where neither or both fuse, 128-token
-// tiles measured as fast or faster).
+// tiles measured as fast or faster). Only up to kNt2MaxM tokens: the fixup
+// launch costs the same at any M while the doubled conversion grows with it.
+constexpr uint32_t kNt2MaxM = 256;
 PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     const PfGeom g = pf_geom_nt(type, pf_nt(type, M), M, N, K, num_cu);
-    if (g.nt != 4 || type == kQ8_0 || type == kQ5_K || pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256)) return g;
+    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 || type == kQ5_K ||
+        pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256))
+        return g;
     const PfGeom h = pf_geom_nt(type, 2, M, N, K, num_cu);
     return pf_fused(uint64_t(h.ntiles) * (K / 256), h.G, K / 256) ? h : g;
 }
