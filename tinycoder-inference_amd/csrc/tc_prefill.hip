@@ -386,8 +386,9 @@ __device__ __forceinline__ void q5_block(const unsigned char *arow, const unsign
 // as the 16-byte chunks that hold them, conflict-free at the 272-byte row
 // stride): the 16 values of k-half g of each block as one B operand, and each block's
 // scale as bf16 pieces dw = h + l (l exact: dw has 11 significant bits) laid
-// out against the activation pieces [h8 m8 l8 0 h8 m8 l8 0]: slots 0-3 times
-// h, 4-7 times l (zero in k-half 1, which the activation side leaves free).
+// out against the activation pieces of a block pair, [h8 m8 l8 0] of the
+// even block then of the odd one, in both k-halves: k-half 0 holds h against
+// this block's pieces, k-half 1 holds l, and the other block's slots are zero.
 struct Q8Frag {
     v4i bw[8], bp[8];
 };
@@ -416,24 +417,43 @@ __device__ __forceinline__ void q8_convert(const unsigned char *row, uint32_t g,
         const uint32_t hb = __builtin_bit_cast(uint32_t, d) & 0xFFFF0000u;
         const uint32_t lb = __builtin_bit_cast(uint32_t, d - __builtin_bit_cast(float, hb));
         const uint32_t h16 = hb >> 16, l16 = lb >> 16;
-        f.bp[k] = g == 0 ? v4i{int(h16 | hb), int(h16), int(l16 | (l16 << 16)), int(l16)} : v4i{0, 0, 0, 0};
+        const int p0 = int(g == 0 ? h16 | hb : l16 | (l16 << 16)), p1 = int(g == 0 ? h16 : l16);
+        f.bp[k] = (k & 1) ? v4i{0, 0, p0, p1} : v4i{p0, p1, 0, 0};
     }
 }
 
-// One 32-token block (the token's activation pieces at prow, those of block
-// k at prow + 256 (k / 2) + 8 (k % 2)): per 32-wide weight block k, the
-// exact integer product I (int8 MFMA) and the scales dw*d8 of its 32x32
-// outputs (bf16 MFMA), then acc += I * scale.
+// One 32-token block (the token's activation pieces at prow, those of blocks
+// 2c, 2c + 1 at prow + 256 c): per 32-wide weight block k, the exact integer
+// product I (int8 MFMA) and the scales dw*d8 of its 32x32 outputs (bf16
+// MFMA), then acc += I * scale. Block k + 1's MFMAs are issued before block
+// k's fp32 combination, so that the matrix core works while the VALU does.
 __device__ __forceinline__ void q8_block(const unsigned char *arow, const unsigned char *prow, const Q8Frag &f,
                                          uint32_t j, uint32_t g, float (&acc)[16]) {
+    auto aread = [&](int k) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow + 16 * ((2 * k + g) ^ (j & 15))));
+    };
+    auto pread = [&](int c) __attribute__((always_inline)) { return as_v4i(lds4(prow + 256 * c)); };
+    v4i af[3], pp[2];
+    af[0] = aread(0);
+    af[1] = aread(1);
+    pp[0] = pread(0);
+    v16i I[2];
+    v16f S[2];
+    I[0] = mfma(af[0], f.bw[0], v16i{});
+    S[0] = mfma_bf16(pp[0], f.bp[0], v16f{});
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const v4i af = as_v4i(lds4(arow + 16 * ((2 * k + g) ^ (j & 15))));
-        const uint2 pp = *reinterpret_cast<const uint2 *>(prow + 256 * (k >> 1) + 8 * (k & 1));
-        const v16i I = mfma(af, f.bw[k], v16i{});
-        const v16f S = mfma_bf16(v4i{int(pp.x), int(pp.y), int(pp.x), int(pp.y)}, f.bp[k], v16f{});
+        if (k + 2 < 8) af[(k + 2) % 3] = aread(k + 2);
+        if (k + 1 < 8 && ((k + 1) & 1) == 0) pp[((k + 1) >> 1) & 1] = pread((k + 1) >> 1);
+        if (k + 1 < 8) {
+            I[(k + 1) & 1] = mfma(af[(k + 1) % 3], f.bw[k + 1], v16i{});
+            S[(k + 1) & 1] = mfma_bf16(pp[((k + 1) >> 1) & 1], f.bp[k + 1], v16f{});
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = fmaf(float(I[r]), S[r], acc[r]);
+        for (int r = 0; r < 16; ++r) acc[r] = fmaf(float(I[k & 1][r]), S[k & 1][r], acc[r]);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
