@@ -567,27 +567,35 @@ __device__ __forceinline__ void i3_blocks(const unsigned char *const (&arow)[P],
     auto aread = [&](int ib, int t) __attribute__((always_inline)) {
         return as_v4i(lds4(arow[t] + 16 * ((2 * ib + g) ^ (j & 15))));
     };
-    // activation fragments one 32-block ahead; the scheduling barriers keep
-    // that order (the scheduler otherwise reads each right before its MFMA
-    // and runs each block's multiply-adds right after its own MFMA)
-    v4i af[2][P];
+    // Activation fragments two 32-blocks ahead, and block ib + 1's MFMAs
+    // issued before block ib's multiply-adds (the matrix core works while
+    // the VALU does); the scheduling barriers keep that order (the scheduler
+    // otherwise reads each fragment right before its MFMA and runs each
+    // block's multiply-adds right after its own MFMA).
+    v4i af[3][P];
+    v16i I[2][P];
 #pragma unroll
-    for (int t = 0; t < P; ++t) af[0][t] = aread(0, t);
+    for (int t = 0; t < P; ++t) {
+        af[0][t] = aread(0, t);
+        af[1][t] = aread(1, t);
+    }
+#pragma unroll
+    for (int t = 0; t < P; ++t) I[0][t] = mfma(af[0][t], f.bw[0], v16i{});
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ib = 0; ib < 8; ++ib) {
+        if (ib + 2 < 8)
+#pragma unroll
+            for (int t = 0; t < P; ++t) af[(ib + 2) % 3][t] = aread(ib + 2, t);
         if (ib + 1 < 8)
 #pragma unroll
-            for (int t = 0; t < P; ++t) af[(ib + 1) & 1][t] = aread(ib + 1, t);
-        v16i I[P];
-#pragma unroll
-        for (int t = 0; t < P; ++t) I[t] = mfma(af[ib & 1][t], f.bw[ib], v16i{});
+            for (int t = 0; t < P; ++t) I[(ib + 1) & 1][t] = mfma(af[(ib + 1) % 3][t], f.bw[ib + 1], v16i{});
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < P; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                is[t][r] = __mul24(f.sc[ib], I[t][r]) + is[t][r];  // v_mad_i32_i24
+                is[t][r] = __mul24(f.sc[ib], I[ib & 1][t][r]) + is[t][r];  // v_mad_i32_i24
                 // kept as one multiply-add per 32-block: the compiler would
                 // otherwise reassociate the chain into multiplies and 3-way adds
                 asm("" : "+v"(is[t][r]));
