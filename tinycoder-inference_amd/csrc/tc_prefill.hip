@@ -264,51 +264,82 @@ __device__ __forceinline__ void q4_convert(const Q4Raw &r, uint32_t g, Q4Frag &f
 }
 
 // One 32-token block (activation row arow, this k-half's sum pieces at dgp,
-// scales at d8) against this wave's converted weights. The hi and lo chains
-// run interleaved as two independent accumulators (no MFMA waits on the
-// previous one's result); the min term's MFMA is issued first.
-__device__ __forceinline__ void q4_block(const unsigned char *arow, const unsigned char *dgp, const float *d8,
-                                         const Q4Frag &f, uint32_t j, uint32_t g, float (&acc)[16]) {
-    // LDS reads issued ahead of their use (the scheduler otherwise places each
-    // right before its consumer): activation fragments two sub-blocks ahead,
-    // the sum pieces before the chains, the token scales mid-chain; the min
-    // MFMA mid-chain so that its result is ready for the epilogue.
+// token scales at d8) against this wave's converted weights, in two parts so
+// that a wave can issue one token block's MFMAs while it combines the
+// previous block's results. q4_chain runs the MFMAs: the hi and lo chains as
+// two independent accumulators (no MFMA waits on the previous one's
+// result), activation fragments read one sub-block ahead, the min term
+// mid-chain; it leaves hi in ch, lo in cl and Mn in mn. q4_combine is the
+// fp32 combination acc += d8 * (d*C - dmin*Mn) with C = 8*hi + lo.
+__device__ __forceinline__ void q4_chain(const unsigned char *arow, const unsigned char *dgp, const Q4Frag &f,
+                                         uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn) {
     auto aread = [&](int s) __attribute__((always_inline)) {
         return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
     };
     const v4i dgv = as_v4i(lds4(dgp));
-    v4i af[3];
+    v4i af[2];
     af[0] = aread(0);
-    af[1] = aread(1);
-    __builtin_amdgcn_sched_barrier(0);
-    v16i ch = {}, cl = {};
-    v16f mn;
-    float4 dv[4];
+    ch = v16i{};
+    cl = v16i{};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        if (s + 2 < 8) af[(s + 2) % 3] = aread(s + 2);
-        if (s == 2) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
-        }
-        ch = mfma(af[s % 3], f.bh[s], ch);
-        cl = mfma(af[s % 3], f.bl[s], cl);
+        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
+        ch = mfma(af[s & 1], f.bh[s], ch);
+        cl = mfma(af[s & 1], f.bl[s], cl);
         if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
-        __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) ch[r] = (ch[r] << 3) + cl[r];
+}
+__device__ __forceinline__ void q4_combine(const float *d8, const Q4Frag &f, const v16i &c, const v16f &mn,
+                                           float (&acc)[16]) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const float dd[4] = {dv[q].x, dv[q].y, dv[q].z, dv[q].w};
+        const float4 dv = *reinterpret_cast<const float4 *>(d8 + 8 * q);
+        const float dd[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int r = 4 * q + e;
-            acc[r] = fmaf(dd[e], fmaf(f.d, float(ch[r]), -f.dm * mn[r]), acc[r]);
+            acc[r] = fmaf(dd[e], fmaf(f.d, float(c[r]), -f.dm * mn[r]), acc[r]);
         }
     }
 }
 
+// Block t + 1's MFMAs (as q4_chain) with block t's combination (as
+// q4_combine) in explicit slices: after the two MFMAs of sub-block s, the
+// combination of outputs 2s and 2s + 1. A wave issues in order, so VALU work
+// placed after the whole chain would wait for it; here it issues while the
+// matrix core runs.
+__device__ __forceinline__ void q4_chain_combine(const unsigned char *arow, const unsigned char *dgp, const Q4Frag &f,
+                                                 uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn,
+                                                 const float *d8, const v16i &c, const v16f &mnp,
+                                                 float (&acc)[16]) {
+    auto aread = [&](int s) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
+    };
+    const v4i dgv = as_v4i(lds4(dgp));
+    float4 dv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
+    v4i af[2];
+    af[0] = aread(0);
+    ch = v16i{};
+    cl = v16i{};
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
+        ch = mfma(af[s & 1], f.bh[s], ch);
+        cl = mfma(af[s & 1], f.bl[s], cl);
+        if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int r = 2 * s + e;
+            const float4 dq = dv[r >> 2];
+            const float dd = (r & 3) == 0 ? dq.x : (r & 3) == 1 ? dq.y : (r & 3) == 2 ? dq.z : dq.w;
+            acc[r] = fmaf(dd, fmaf(f.d, float(c[r]), -f.dm * mnp[r]), acc[r]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
 
 // ---- Q5_K: B operands of one superblock ------------------------------------
 // Reference dequantizeQ5_KBlock (GGMLDequantize.hpp:392-402): the Q4_K
@@ -801,15 +832,37 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     q4_read(rr, bb + L::W + rl * T::UB, g);
                     q4_convert(rr, g, f);
                 }
+                // token block t + 1's MFMAs issued before block t's fp32
+                // combination: the matrix core works while the VALU does
+                auto chain_t = [&](int t, v16i &ch, v16i &cl, v16f &mn) __attribute__((always_inline)) {
+                    const uint32_t tok = 32 * (tg * NB + t) + j;
+                    q4_chain(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, f, j, g, ch, cl, mn);
+                };
+                auto d8_t = [&](int t) __attribute__((always_inline)) {
+                    return reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g;
+                };
+                // (C = 8*hi + lo formed once block t + 1's MFMAs are done,
+                // so that only C and Mn of block t stay live across them)
+                v16i c[2], ch, cl;
+                v16f mn[2];
+                __builtin_amdgcn_sched_barrier(0);
+                chain_t(0, ch, cl, mn[0]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) c[0][r] = (ch[r] << 3) + cl[r];
 #pragma unroll
                 for (int t = 0; t < NB; ++t) {
-                    // one token block at a time in the scheduler's window (it
-                    // would otherwise hoist every block's operand reads)
+                    if (t + 1 < NB) {
+                        const uint32_t tok = 32 * (tg * NB + t + 1) + j;
+                        q4_chain_combine(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, f, j, g, ch, cl,
+                                         mn[(t + 1) & 1], d8_t(t), c[t & 1], mn[t & 1], acc[t]);
+                    } else {
+                        q4_combine(d8_t(t), f, c[t & 1], mn[t & 1], acc[t]);
+                    }
                     __builtin_amdgcn_sched_barrier(0);
-                    const uint32_t tok = 32 * (tg * NB + t) + j;
-                    q4_block(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g,
-                             reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g, f, j, g,
-                             acc[t]);
+                    if (t + 1 < NB) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) c[(t + 1) & 1][r] = (ch[r] << 3) + cl[r];
+                    }
                 }
             } else if constexpr (TYPE == kQ5_K) {
                 Q5Frag f;
