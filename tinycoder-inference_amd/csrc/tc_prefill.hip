@@ -264,31 +264,15 @@ __device__ __forceinline__ void q4_convert(const Q4Raw &r, uint32_t g, Q4Frag &f
 }
 
 // One 32-token block (activation row arow, this k-half's sum pieces at dgp,
-// token scales at d8) against this wave's converted weights, in two parts so
-// that a wave can issue one token block's MFMAs while it combines the
-// previous block's results. q4_chain runs the MFMAs: the hi and lo chains as
-// two independent accumulators (no MFMA waits on the previous one's
-// result), activation fragments read one sub-block ahead, the min term
-// mid-chain; it leaves hi in ch, lo in cl and Mn in mn. q4_combine is the
-// fp32 combination acc += d8 * (d*C - dmin*Mn) with C = 8*hi + lo.
-__device__ __forceinline__ void q4_chain(const unsigned char *arow, const unsigned char *dgp, const Q4Frag &f,
-                                         uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn) {
-    auto aread = [&](int s) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-    };
-    const v4i dgv = as_v4i(lds4(dgp));
-    v4i af[2];
-    af[0] = aread(0);
-    ch = v16i{};
-    cl = v16i{};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
-        ch = mfma(af[s & 1], f.bh[s], ch);
-        cl = mfma(af[s & 1], f.bl[s], cl);
-        if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
-    }
-}
+// token scales at d8) against this wave's converted weights: the MFMAs (the
+// hi and lo chains as two independent accumulators, activation fragments
+// read one sub-block ahead, the bf16 min term mid-chain) leave hi in ch, lo
+// in cl and Mn in mn; q4_combine is the fp32 combination acc += d8 * (d*C -
+// dmin*Mn) with C = 8*hi + lo. A wave issues in order, so VALU work placed
+// after a whole chain would wait for it: a block's MFMAs are interleaved in
+// program order with VALU work that does not depend on them, the weights'
+// conversion for a superblock's first block (q4_convert_chain) and the
+// previous block's combination for the others (q4_chain_combine).
 __device__ __forceinline__ void q4_combine(const float *d8, const Q4Frag &f, const v16i &c, const v16f &mn,
                                            float (&acc)[16]) {
 #pragma unroll
@@ -303,11 +287,57 @@ __device__ __forceinline__ void q4_combine(const float *d8, const Q4Frag &f, con
     }
 }
 
-// Block t + 1's MFMAs (as q4_chain) with block t's combination (as
-// q4_combine) in explicit slices: after the two MFMAs of sub-block s, the
-// combination of outputs 2s and 2s + 1. A wave issues in order, so VALU work
-// placed after the whole chain would wait for it; here it issues while the
-// matrix core runs.
+// The conversion of this wave's weights (as q4_convert) with the first token
+// block's MFMAs, in slices: after the two MFMAs of sub-block s, the digit
+// planes of sub-block s + 2.
+__device__ __forceinline__ void q4_convert_chain(const Q4Raw &r, Q4Frag &f, const unsigned char *arow,
+                                                 const unsigned char *dgp, uint32_t j, uint32_t g, v16i &ch,
+                                                 v16i &cl, v16f &mn) {
+    const u4 h = r.h;
+    const uint32_t scl = h.y & 0x3F3F3F3Fu, mnl = h.z & 0x3F3F3F3Fu;
+    const uint32_t sch = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t mnh = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    const uint32_t hw[2] = {(scl >> 3) & 0x07070707u, (sch >> 3) & 0x07070707u};
+    const uint32_t lw[2] = {scl & 0x07070707u, sch & 0x07070707u};
+    f.d = h2f(h.x & 0xFFFFu);
+    f.dm = h2f(h.x >> 16);
+    f.mb = v4i{bf16_pair(mnl, 0), bf16_pair(mnl, 1), bf16_pair(mnh, 0), bf16_pair(mnh, 1)};
+    auto conv = [&](int sb) __attribute__((always_inline)) {
+        const uint32_t mh = bcast16(hw[sb >> 2], sb & 3), ml = bcast16(lw[sb >> 2], sb & 3);
+        const u4 qv = r.q[sb >> 1];
+        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t nib = (sb & 1) ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
+            f.bh[sb][k] = pkmul(nib, mh);
+            f.bl[sb][k] = pkmul(nib, ml);
+        }
+    };
+    auto aread = [&](int s) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
+    };
+    const v4i dgv = as_v4i(lds4(dgp));
+    v4i af[2];
+    af[0] = aread(0);
+    conv(0);
+    conv(1);
+    ch = v16i{};
+    cl = v16i{};
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
+        ch = mfma(af[s & 1], f.bh[s], ch);
+        cl = mfma(af[s & 1], f.bl[s], cl);
+        if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
+        if (s + 2 < 8) conv(s + 2);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Block t + 1's MFMAs with block t's combination (as q4_combine) in slices:
+// after the two MFMAs of sub-block s, the combination of outputs 2s and
+// 2s + 1.
 __device__ __forceinline__ void q4_chain_combine(const unsigned char *arow, const unsigned char *dgp, const Q4Frag &f,
                                                  uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn,
                                                  const float *d8, const v16i &c, const v16f &mnp,
@@ -827,17 +857,8 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             const unsigned char *bb = buf(b);
             if constexpr (TYPE == kQ4_K) {
                 Q4Frag f;
-                {
-                    Q4Raw rr;
-                    q4_read(rr, bb + L::W + rl * T::UB, g);
-                    q4_convert(rr, g, f);
-                }
                 // token block t + 1's MFMAs issued before block t's fp32
                 // combination: the matrix core works while the VALU does
-                auto chain_t = [&](int t, v16i &ch, v16i &cl, v16f &mn) __attribute__((always_inline)) {
-                    const uint32_t tok = 32 * (tg * NB + t) + j;
-                    q4_chain(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, f, j, g, ch, cl, mn);
-                };
                 auto d8_t = [&](int t) __attribute__((always_inline)) {
                     return reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g;
                 };
@@ -846,7 +867,13 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 v16i c[2], ch, cl;
                 v16f mn[2];
                 __builtin_amdgcn_sched_barrier(0);
-                chain_t(0, ch, cl, mn[0]);
+                {
+                    Q4Raw rr;
+                    q4_read(rr, bb + L::W + rl * T::UB, g);
+                    const uint32_t tok = 32 * tg * NB + j;
+                    q4_convert_chain(rr, f, bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, j, g, ch, cl,
+                                     mn[0]);
+                }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) c[0][r] = (ch[r] << 3) + cl[r];
 #pragma unroll
