@@ -234,35 +234,6 @@ __device__ __forceinline__ int bf16_pair(uint32_t w, int i) {
     return int(__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u));
 }
 
-__device__ __forceinline__ void q4_convert(const Q4Raw &r, uint32_t g, Q4Frag &f) {
-    const u4 h = r.h;
-    // 6-bit scales and mins of the 8 sub-blocks as bytes (reference
-    // get_scale_min_k4, GGMLDequantize.hpp:436-447)
-    const uint32_t scl = h.y & 0x3F3F3F3Fu, mnl = h.z & 0x3F3F3F3Fu;
-    const uint32_t sch = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
-    const uint32_t mnh = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
-    const uint32_t hw[2] = {(scl >> 3) & 0x07070707u, (sch >> 3) & 0x07070707u};
-    const uint32_t lw[2] = {scl & 0x07070707u, sch & 0x07070707u};
-    f.d = h2f(h.x & 0xFFFFu);
-    f.dm = h2f(h.x >> 16);
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int s0 = 2 * p, s1 = 2 * p + 1;  // low nibbles: sub-block 2p, high: 2p+1
-        const uint32_t mh0 = bcast16(hw[s0 >> 2], s0 & 3), ml0 = bcast16(lw[s0 >> 2], s0 & 3);
-        const uint32_t mh1 = bcast16(hw[s1 >> 2], s1 & 3), ml1 = bcast16(lw[s1 >> 2], s1 & 3);
-        const uint32_t q[4] = {r.q[p].x, r.q[p].y, r.q[p].z, r.q[p].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
-            f.bh[s0][k] = pkmul(lo, mh0);
-            f.bl[s0][k] = pkmul(lo, ml0);
-            f.bh[s1][k] = pkmul(hi, mh1);
-            f.bl[s1][k] = pkmul(hi, ml1);
-        }
-    }
-    f.mb = v4i{bf16_pair(mnl, 0), bf16_pair(mnl, 1), bf16_pair(mnh, 0), bf16_pair(mnh, 1)};
-}
-
 // One 32-token block (activation row arow, this k-half's sum pieces at dgp,
 // token scales at d8) against this wave's converted weights: the MFMAs (the
 // hi and lo chains as two independent accumulators, activation fragments
@@ -271,8 +242,8 @@ __device__ __forceinline__ void q4_convert(const Q4Raw &r, uint32_t g, Q4Frag &f
 // dmin*Mn) with C = 8*hi + lo. A wave issues in order, so VALU work placed
 // after a whole chain would wait for it: a block's MFMAs are interleaved in
 // program order with VALU work that does not depend on them, the weights'
-// conversion for a superblock's first block (q4_convert_chain) and the
-// previous block's combination for the others (q4_chain_combine).
+// conversion for a superblock's first block (k_convert_chain) and the
+// previous block's combination for the others (k_chain_combine).
 __device__ __forceinline__ void q4_combine(const float *d8, const Q4Frag &f, const v16i &c, const v16f &mn,
                                            float (&acc)[16]) {
 #pragma unroll
@@ -284,90 +255,6 @@ __device__ __forceinline__ void q4_combine(const float *d8, const Q4Frag &f, con
             const int r = 4 * q + e;
             acc[r] = fmaf(dd[e], fmaf(f.d, float(c[r]), -f.dm * mn[r]), acc[r]);
         }
-    }
-}
-
-// The conversion of this wave's weights (as q4_convert) with the first token
-// block's MFMAs, in slices: after the two MFMAs of sub-block s, the digit
-// planes of sub-block s + 2.
-__device__ __forceinline__ void q4_convert_chain(const Q4Raw &r, Q4Frag &f, const unsigned char *arow,
-                                                 const unsigned char *dgp, uint32_t j, uint32_t g, v16i &ch,
-                                                 v16i &cl, v16f &mn) {
-    const u4 h = r.h;
-    const uint32_t scl = h.y & 0x3F3F3F3Fu, mnl = h.z & 0x3F3F3F3Fu;
-    const uint32_t sch = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
-    const uint32_t mnh = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
-    const uint32_t hw[2] = {(scl >> 3) & 0x07070707u, (sch >> 3) & 0x07070707u};
-    const uint32_t lw[2] = {scl & 0x07070707u, sch & 0x07070707u};
-    f.d = h2f(h.x & 0xFFFFu);
-    f.dm = h2f(h.x >> 16);
-    f.mb = v4i{bf16_pair(mnl, 0), bf16_pair(mnl, 1), bf16_pair(mnh, 0), bf16_pair(mnh, 1)};
-    auto conv = [&](int sb) __attribute__((always_inline)) {
-        const uint32_t mh = bcast16(hw[sb >> 2], sb & 3), ml = bcast16(lw[sb >> 2], sb & 3);
-        const u4 qv = r.q[sb >> 1];
-        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t nib = (sb & 1) ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
-            f.bh[sb][k] = pkmul(nib, mh);
-            f.bl[sb][k] = pkmul(nib, ml);
-        }
-    };
-    auto aread = [&](int s) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-    };
-    const v4i dgv = as_v4i(lds4(dgp));
-    v4i af[2];
-    af[0] = aread(0);
-    conv(0);
-    conv(1);
-    ch = v16i{};
-    cl = v16i{};
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
-        ch = mfma(af[s & 1], f.bh[s], ch);
-        cl = mfma(af[s & 1], f.bl[s], cl);
-        if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
-        if (s + 2 < 8) conv(s + 2);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// Block t + 1's MFMAs with block t's combination (as q4_combine) in slices:
-// after the two MFMAs of sub-block s, the combination of outputs 2s and
-// 2s + 1.
-__device__ __forceinline__ void q4_chain_combine(const unsigned char *arow, const unsigned char *dgp, const Q4Frag &f,
-                                                 uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn,
-                                                 const float *d8, const v16i &c, const v16f &mnp,
-                                                 float (&acc)[16]) {
-    auto aread = [&](int s) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-    };
-    const v4i dgv = as_v4i(lds4(dgp));
-    float4 dv[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
-    v4i af[2];
-    af[0] = aread(0);
-    ch = v16i{};
-    cl = v16i{};
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
-        ch = mfma(af[s & 1], f.bh[s], ch);
-        cl = mfma(af[s & 1], f.bl[s], cl);
-        if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int r = 2 * s + e;
-            const float4 dq = dv[r >> 2];
-            const float dd = (r & 3) == 0 ? dq.x : (r & 3) == 1 ? dq.y : (r & 3) == 2 ? dq.z : dq.w;
-            acc[r] = fmaf(dd, fmaf(f.d, float(c[r]), -f.dm * mnp[r]), acc[r]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -390,54 +277,103 @@ __device__ __forceinline__ void q5_read(Q5Raw &r, const unsigned char *blk, uint
 #pragma unroll
     for (int p = 0; p < 4; ++p) r.q[p] = lds4(blk + 48 + 32 * p + 16 * g);
 }
-__device__ __forceinline__ void q5_convert(const Q5Raw &r, uint32_t g, Q5Frag &f) {
-    q4_convert(r, g, f);
-    const u4 h = r.h;
-    const uint32_t sc[2] = {h.y & 0x3F3F3F3Fu, (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u)};
-    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-#pragma unroll
-    for (int sb = 0; sb < 8; ++sb) {
-        const uint32_t m2 = 2u * bcast16(sc[sb >> 2], sb & 3);  // 2 sc_s in both 16-bit halves (<= 126)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) f.bb[sb][k] = pkmul((qh[k] >> sb) & 0x01010101u, m2);
-    }
+// ---- Q4_K / Q5_K: MFMA chains interleaved with VALU work ------------------
+// (q4_combine describes the split.) One step of sub-block s: the hi and lo
+// MFMAs, for Q5_K the bit-plane MFMA into the hi chain.
+template <bool Q5, typename F>
+__device__ __forceinline__ void k_step(const v4i &a, const F &f, int s, v16i &ch, v16i &cl) {
+    ch = mfma(a, f.bh[s], ch);
+    cl = mfma(a, f.bl[s], cl);
+    if constexpr (Q5) ch = mfma(a, f.bb[s], ch);
 }
-__device__ __forceinline__ void q5_block(const unsigned char *arow, const unsigned char *dgp, const float *d8,
-                                         const Q5Frag &f, uint32_t j, uint32_t g, float (&acc)[16]) {
+
+// The conversion of this wave's weights with the first token block's MFMAs,
+// in slices: after the MFMAs of sub-block s, the planes of sub-block s + 2.
+// The 6-bit scales and mins of the 8 sub-blocks as bytes (reference
+// get_scale_min_k4, GGMLDequantize.hpp:436-447); sc = 8h + l with h, l in
+// 0..7, so h*q and l*q (q <= 15) are the bytewise products of pkmul; Q5_K's
+// bit plane is 2*sc*b (<= 126).
+template <bool Q5, typename R, typename F>
+__device__ __forceinline__ void k_convert_chain(const R &r, F &f, const unsigned char *arow, const unsigned char *dgp,
+                                                uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn) {
+    const u4 h = r.h;
+    const uint32_t scl = h.y & 0x3F3F3F3Fu, mnl = h.z & 0x3F3F3F3Fu;
+    const uint32_t sch = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t mnh = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    const uint32_t hw[2] = {(scl >> 3) & 0x07070707u, (sch >> 3) & 0x07070707u};
+    const uint32_t lw[2] = {scl & 0x07070707u, sch & 0x07070707u};
+    f.d = h2f(h.x & 0xFFFFu);
+    f.dm = h2f(h.x >> 16);
+    f.mb = v4i{bf16_pair(mnl, 0), bf16_pair(mnl, 1), bf16_pair(mnh, 0), bf16_pair(mnh, 1)};
+    auto conv = [&](int sb) __attribute__((always_inline)) {
+        const uint32_t mh = bcast16(hw[sb >> 2], sb & 3), ml = bcast16(lw[sb >> 2], sb & 3);
+        const u4 qv = r.q[sb >> 1];
+        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t nib = (sb & 1) ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
+            f.bh[sb][k] = pkmul(nib, mh);
+            f.bl[sb][k] = pkmul(nib, ml);
+        }
+        if constexpr (Q5) {
+            const uint32_t m2 = 2u * bcast16(sb < 4 ? scl : sch, sb & 3);  // 2 sc_s in both 16-bit halves
+            const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) f.bb[sb][k] = pkmul((qh[k] >> sb) & 0x01010101u, m2);
+        }
+    };
     auto aread = [&](int s) __attribute__((always_inline)) {
         return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
     };
     const v4i dgv = as_v4i(lds4(dgp));
-    v4i af[3];
+    v4i af[2];
     af[0] = aread(0);
-    af[1] = aread(1);
+    conv(0);
+    conv(1);
+    ch = v16i{};
+    cl = v16i{};
     __builtin_amdgcn_sched_barrier(0);
-    v16i ch = {}, cl = {};
-    v16f mn;
-    float4 dv[4];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        if (s + 2 < 8) af[(s + 2) % 3] = aread(s + 2);
-        if (s == 2) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
-        }
-        ch = mfma(af[s % 3], f.bh[s], ch);
-        cl = mfma(af[s % 3], f.bl[s], cl);
-        ch = mfma(af[s % 3], f.bb[s], ch);
+        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
+        k_step<Q5>(af[s & 1], f, s, ch, cl);
         if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
+        if (s + 2 < 8) conv(s + 2);
         __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+// Block t + 1's MFMAs with block t's combination (as q4_combine) in slices:
+// after the MFMAs of sub-block s, the combination of outputs 2s and 2s + 1.
+template <bool Q5, typename F>
+__device__ __forceinline__ void k_chain_combine(const unsigned char *arow, const unsigned char *dgp, const F &f,
+                                                uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn,
+                                                const float *d8, const v16i &c, const v16f &mnp, float (&acc)[16]) {
+    auto aread = [&](int s) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
+    };
+    const v4i dgv = as_v4i(lds4(dgp));
+    float4 dv[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ch[r] = (ch[r] << 3) + cl[r];
+    for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
+    v4i af[2];
+    af[0] = aread(0);
+    ch = v16i{};
+    cl = v16i{};
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float dd[4] = {dv[q].x, dv[q].y, dv[q].z, dv[q].w};
+    for (int s = 0; s < 8; ++s) {
+        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
+        k_step<Q5>(af[s & 1], f, s, ch, cl);
+        if (s == 3) mn = mfma_bf16(dgv, f.mb, v16f{});
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 4 * q + e;
-            acc[r] = fmaf(dd[e], fmaf(f.d, float(ch[r]), -f.dm * mn[r]), acc[r]);
+        for (int e = 0; e < 2; ++e) {
+            const int r = 2 * s + e;
+            const float4 dq = dv[r >> 2];
+            const float dd = (r & 3) == 0 ? dq.x : (r & 3) == 1 ? dq.y : (r & 3) == 2 ? dq.z : dq.w;
+            acc[r] = fmaf(dd, fmaf(f.d, float(c[r]), -f.dm * mnp[r]), acc[r]);
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -855,8 +791,10 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             __syncthreads();
             stage<TYPE, NT>(a, tg_.W, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
             const unsigned char *bb = buf(b);
-            if constexpr (TYPE == kQ4_K) {
-                Q4Frag f;
+            if constexpr (TYPE == kQ4_K || TYPE == kQ5_K) {
+                constexpr bool Q5 = TYPE == kQ5_K;
+                using Frag = std::conditional_t<Q5, Q5Frag, Q4Frag>;
+                Frag f;
                 // token block t + 1's MFMAs issued before block t's fp32
                 // combination: the matrix core works while the VALU does
                 auto d8_t = [&](int t) __attribute__((always_inline)) {
@@ -868,11 +806,14 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 v16f mn[2];
                 __builtin_amdgcn_sched_barrier(0);
                 {
-                    Q4Raw rr;
-                    q4_read(rr, bb + L::W + rl * T::UB, g);
+                    std::conditional_t<Q5, Q5Raw, Q4Raw> rr;
+                    if constexpr (Q5)
+                        q5_read(rr, bb + L::W + rl * T::UB, g);
+                    else
+                        q4_read(rr, bb + L::W + rl * T::UB, g);
                     const uint32_t tok = 32 * tg * NB + j;
-                    q4_convert_chain(rr, f, bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, j, g, ch, cl,
-                                     mn[0]);
+                    k_convert_chain<Q5>(rr, f, bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, j, g, ch,
+                                        cl, mn[0]);
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) c[0][r] = (ch[r] << 3) + cl[r];
@@ -880,8 +821,8 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 for (int t = 0; t < NB; ++t) {
                     if (t + 1 < NB) {
                         const uint32_t tok = 32 * (tg * NB + t + 1) + j;
-                        q4_chain_combine(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, f, j, g, ch, cl,
-                                         mn[(t + 1) & 1], d8_t(t), c[t & 1], mn[t & 1], acc[t]);
+                        k_chain_combine<Q5>(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, f, j, g, ch,
+                                            cl, mn[(t + 1) & 1], d8_t(t), c[t & 1], mn[t & 1], acc[t]);
                     } else {
                         q4_combine(d8_t(t), f, c[t & 1], mn[t & 1], acc[t]);
                     }
@@ -890,21 +831,6 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
                         for (int r = 0; r < 16; ++r) c[(t + 1) & 1][r] = (ch[r] << 3) + cl[r];
                     }
-                }
-            } else if constexpr (TYPE == kQ5_K) {
-                Q5Frag f;
-                {
-                    Q5Raw rr;
-                    q5_read(rr, bb + L::W + rl * T::UB, g);
-                    q5_convert(rr, g, f);
-                }
-#pragma unroll
-                for (int t = 0; t < NB; ++t) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    const uint32_t tok = 32 * (tg * NB + t) + j;
-                    q5_block(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g,
-                             reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g, f, j, g,
-                             acc[t]);
                 }
             } else if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S) {
                 I3Frag f;
