@@ -94,6 +94,14 @@ template <>
 struct PfType<kQ8_0> {
     static constexpr uint32_t PR = 128, TSPLIT = 2, UB = 272, XB = 64;
 };
+// Q6_K: the 210-byte unit (2-byte aligned) in the 224-byte window from its
+// 4-byte-aligned start (14 chunks, loaded as 15 at a 240-byte row stride:
+// conflict-free 16-byte reads); at most 64 tokens per tile (256 such rows
+// would not fit LDS twice with 128-token stages).
+template <>
+struct PfType<kQ6_K> {
+    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 240, XB = 0;
+};
 // IQ3_XXS: a row's 98-byte unit is 2-byte aligned; LDS holds the 100-byte
 // window from its 4-byte-aligned start down: 6 chunks at a 112-byte row
 // stride (conflict-free 16-byte reads) and the last dword in TAIL.
@@ -374,6 +382,138 @@ __device__ __forceinline__ void k_chain_combine(const unsigned char *arow, const
             acc[r] = fmaf(dd, fmaf(f.d, float(c[r]), -f.dm * mnp[r]), acc[r]);
         }
         __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// ---- Q6_K: B operands of one superblock ------------------------------------
+// Reference dequantizeQ6_KBlock (GGMLDequantize.hpp:503-527): per 128-element
+// half n, element l + 32k (l < 32, k < 4) has q = nibble k / 2 of
+// ql[64n + l + 32 (k % 2)] with bits 2k, 2k + 1 of qh[32n + l] above it, and
+// scale sc[8n + l / 16 + 2k] (int8); w = d * sc * (q - 32). The lane's k-half
+// g of 32-block s = 4n + k is l = 16g .. 16g + 15: 16 values under one scale.
+// e = sc * (q - 32) (|e| <= 4096) as signed digits e = 128 hi + lo (hi in
+// -32..31, lo in 0..127), so the hi chain, a shift by 7 and the lo chain on
+// top give C = sum_s e . x exactly; acc += d8 * (d * C).
+struct Q6Frag {
+    v4i bh[8], bl[8];
+    float d;
+};
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// 16 unit bytes from offset o (a multiple of 16) of the lane's 2-byte-aligned
+// unit at byte sh (0 or 2) of its LDS window: the 16-byte chunk and the next
+// dword, realigned; *next receives that dword.
+__device__ __forceinline__ u4 q6_read16(const unsigned char *win, uint32_t o, uint32_t sh, uint32_t *next = nullptr) {
+    const u4 c = lds4(win + o);
+    const uint32_t n = lds1(win + o + 16);
+    if (next) *next = n;
+    return u4{__builtin_amdgcn_alignbyte(c.y, c.x, sh), __builtin_amdgcn_alignbyte(c.z, c.y, sh),
+              __builtin_amdgcn_alignbyte(c.w, c.z, sh), __builtin_amdgcn_alignbyte(n, c.w, sh)};
+}
+
+// Signed byte digits of e = sc * (q - 32) for the four values of q (bytes,
+// 0..63): 16-bit products of the even and the odd bytes, hi = e >> 7
+// (arithmetic), lo = e & 127, packed back in byte order.
+__device__ __forceinline__ void q6_digits(uint32_t q, s16x2 sc2, s16x2 m32sc, uint32_t &hi, uint32_t &lo) {
+    const s16x2 ee = __builtin_bit_cast(s16x2, q & 0x00FF00FFu) * sc2 + m32sc;
+    const s16x2 eo = __builtin_bit_cast(s16x2, (q >> 8) & 0x00FF00FFu) * sc2 + m32sc;
+    const s16x2 he = ee >> s16x2{7, 7}, ho = eo >> s16x2{7, 7};
+    lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, eo) & 0x007F007Fu,
+                               __builtin_bit_cast(uint32_t, ee) & 0x007F007Fu, 0x06020400u);
+    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he), 0x06020400u);
+}
+
+struct Q6Raw {
+    u4 ql[4], qh[2], sc;  // ql[2n + (k % 2)], qh[n]
+    uint32_t dw;          // the dword after the scales (d)
+};
+__device__ __forceinline__ void q6_read(Q6Raw &r, const unsigned char *win, uint32_t sh, uint32_t g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.ql[i] = q6_read16(win, 64 * (i >> 1) + 32 * (i & 1) + 16 * g, sh);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) r.qh[n] = q6_read16(win, 128 + 32 * n + 16 * g, sh);
+    r.sc = q6_read16(win, 192, sh, &r.dw);
+}
+// The planes of 32-block s into f.
+__device__ __forceinline__ void q6_conv(const Q6Raw &r, uint32_t g, int s, Q6Frag &f) {
+    const int n = s >> 2, k = s & 3;
+    const u4 qlv = r.ql[2 * n + (k & 1)], qhv = r.qh[n];
+    const uint32_t ql[4] = {qlv.x, qlv.y, qlv.z, qlv.w}, qh[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+    const uint32_t scw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+    // the lane's scale byte 8n + 2k + g: in dword 2n + k / 2, byte 2 (k % 2) + g
+    const short sc = short(int8_t(__builtin_amdgcn_ubfe(scw[2 * n + (k >> 1)], 8 * (2 * (k & 1) + g), 8)));
+    const s16x2 sc2 = {sc, sc}, m32sc = {short(-32 * sc), short(-32 * sc)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t nib = (k >> 1) ? (ql[i] >> 4) & 0x0F0F0F0Fu : ql[i] & 0x0F0F0F0Fu;
+        const uint32_t q = nib | (((qh[i] >> (2 * k)) & 0x03030303u) << 4);
+        uint32_t hi, lo;
+        q6_digits(q, sc2, m32sc, hi, lo);
+        f.bh[s][i] = int(hi);
+        f.bl[s][i] = int(lo);
+    }
+}
+
+// The conversion with the first token block's MFMAs (after the MFMA pair of
+// block s, the planes of block s + 2), then each further block's MFMAs with
+// the previous block's combination (as for Q4_K).
+__device__ __forceinline__ void q6_convert_chain(const Q6Raw &r, uint32_t g, Q6Frag &f, const unsigned char *arow,
+                                                 uint32_t j, v16i &ch, v16i &cl) {
+    auto aread = [&](int s) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
+    };
+    v4i af[2];
+    af[0] = aread(0);
+    q6_conv(r, g, 0, f);
+    q6_conv(r, g, 1, f);
+    ch = v16i{};
+    cl = v16i{};
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
+        ch = mfma(af[s & 1], f.bh[s], ch);
+        cl = mfma(af[s & 1], f.bl[s], cl);
+        if (s + 2 < 8) q6_conv(r, g, s + 2, f);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+__device__ __forceinline__ void q6_chain_combine(const unsigned char *arow, const Q6Frag &f, uint32_t j, uint32_t g,
+                                                 v16i &ch, v16i &cl, const float *d8, const v16i &c,
+                                                 float (&acc)[16]) {
+    auto aread = [&](int s) __attribute__((always_inline)) {
+        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
+    };
+    float4 dv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
+    v4i af[2];
+    af[0] = aread(0);
+    ch = v16i{};
+    cl = v16i{};
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
+        ch = mfma(af[s & 1], f.bh[s], ch);
+        cl = mfma(af[s & 1], f.bl[s], cl);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int rr = 2 * s + e;
+            const float4 dq = dv[rr >> 2];
+            const float dd = (rr & 3) == 0 ? dq.x : (rr & 3) == 1 ? dq.y : (rr & 3) == 2 ? dq.z : dq.w;
+            acc[rr] = fmaf(dd, f.d * float(c[rr]), acc[rr]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+__device__ __forceinline__ void q6_combine(const float *d8, const Q6Frag &f, const v16i &c, float (&acc)[16]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 dv = *reinterpret_cast<const float4 *>(d8 + 8 * q);
+        const float dd[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[4 * q + e] = fmaf(dd[e], f.d * float(c[4 * q + e]), acc[4 * q + e]);
     }
 }
 
@@ -711,6 +851,8 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
             lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 98) & ~3u) + 16 * min(p, 5u));
         else if constexpr (TYPE == kIQ3_S)
             lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 110) & ~3u) + 16 * p);
+        else if constexpr (TYPE == kQ6_K)  // (slot 14: unused)
+            lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 210) & ~3u) + 16 * min(p, 13u));
         else
             lds_load16(base + L::W + 1024 * k, rw, (n0 + r) * a.row_bytes + b * T::UB + 16 * p);
     });
@@ -830,6 +972,37 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     if (t + 1 < NB) {
 #pragma unroll
                         for (int r = 0; r < 16; ++r) c[(t + 1) & 1][r] = (ch[r] << 3) + cl[r];
+                    }
+                }
+            } else if constexpr (TYPE == kQ6_K) {
+                Q6Frag f;
+                auto d8_t = [&](int t) __attribute__((always_inline)) {
+                    return reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g;
+                };
+                v16i c[2], ch, cl;
+                __builtin_amdgcn_sched_barrier(0);
+                {
+                    const uint32_t sh = ((n0 + rl) * a.row_bytes + b * 210) & 3u;
+                    Q6Raw rr;
+                    q6_read(rr, bb + L::W + rl * T::UB, sh, g);
+                    const uint32_t tok = 32 * tg * NB + j;
+                    q6_convert_chain(rr, g, f, bb + L::QS + tok * 256, j, ch, cl);
+                    f.d = h2f(sh ? rr.dw >> 16 : rr.dw & 0xFFFFu);
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) c[0][r] = (ch[r] << 7) + cl[r];
+#pragma unroll
+                for (int t = 0; t < NB; ++t) {
+                    if (t + 1 < NB) {
+                        const uint32_t tok = 32 * (tg * NB + t + 1) + j;
+                        q6_chain_combine(bb + L::QS + tok * 256, f, j, g, ch, cl, d8_t(t), c[t & 1], acc[t]);
+                    } else {
+                        q6_combine(d8_t(t), f, c[t & 1], acc[t]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (t + 1 < NB) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) c[(t + 1) & 1][r] = (ch[r] << 7) + cl[r];
                     }
                 }
             } else if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S) {
@@ -1069,12 +1242,12 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
 // else 128 (Q8_0: 64 or 128, as its waves split the tile's tokens in two).
 int pf_nt(int type, uint32_t M) {
     static_assert(PLds<kIQ3_XXS, 4>::total <= 160 * 1024 && PLds<kIQ3_S, 4>::total <= 160 * 1024 &&
-                      PLds<kQ5_K, 2>::total <= 160 * 1024 &&
+                      PLds<kQ5_K, 2>::total <= 160 * 1024 && PLds<kQ6_K, 2>::total <= 160 * 1024 &&
                       PLds<kQ4_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ8_0, 4>::total <= 160 * 1024,
                   "LDS of one workgroup");
     const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
-    return type == kQ8_0 ? std::max(nt, 2) : type == kQ5_K ? std::min(nt, 2) : nt;
+    return type == kQ8_0 ? std::max(nt, 2) : type == kQ5_K || type == kQ6_K ? std::min(nt, 2) : nt;
 }
 uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // Q5_K, IQ3_XXS, IQ3_S: 256 too
 
@@ -1117,7 +1290,7 @@ PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_
 constexpr uint32_t kNt2MaxM = 256;
 PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     const PfGeom g = pf_geom_nt(type, pf_nt(type, M), M, N, K, num_cu);
-    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 || type == kQ5_K ||
+    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 || type == kQ5_K || type == kQ6_K ||
         pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256))
         return g;
     const PfGeom h = pf_geom_nt(type, 2, M, N, K, num_cu);
@@ -1145,7 +1318,7 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
 }  // namespace
 
 bool prefill_type(int type) {
-    return type == kQ4_K || type == kQ5_K || type == kQ8_0 || type == kIQ3_XXS || type == kIQ3_S;
+    return type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0 || type == kIQ3_XXS || type == kIQ3_S;
 }
 
 // Workspace: the per-tile arrival counters (256-byte rounded), then the
@@ -1197,6 +1370,7 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
         }
     }
     if (type == kQ5_K) return g.nt == 1 ? pf_launch<kQ5_K, 1>(a, st) : pf_launch<kQ5_K, 2>(a, st);
+    if (type == kQ6_K) return g.nt == 1 ? pf_launch<kQ6_K, 1>(a, st) : pf_launch<kQ6_K, 2>(a, st);
     if (type == kIQ3_S) {
         switch (g.nt) {
             case 1: return pf_launch<kIQ3_S, 1>(a, st);
