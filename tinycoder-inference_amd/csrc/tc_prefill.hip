@@ -126,9 +126,16 @@ __host__ __device__ constexpr uint32_t pf_grid_bytes(int type) {
 // fp32 d, [PR][UB] raw weight blocks. IQ3_XXS's signed grid (256 x 16
 // words, one copy per workgroup, at offset 0 so that a lookup's address is
 // its index times 4), then the two buffers.
+// Q6_K at 128-token tiles keeps one weight region (WS, after the two
+// buffers): each wave reads its rows' raw bytes into registers first, and the
+// next superblock's weights are loaded only after a barrier that follows
+// those reads (the activations stay double-buffered).
+template <int TYPE, int NT>
+constexpr bool pf_shared_w() { return TYPE == kQ6_K && NT == 4; }
 template <int TYPE, int NT>
 struct PLds {
     using T = PfType<TYPE>;
+    static constexpr bool SW = pf_shared_w<TYPE, NT>();
     static constexpr uint32_t TT = 32 * NT;
     static constexpr uint32_t GRID = 0;  // IQ3_XXS's signed grid (before the two buffers)
     static constexpr uint32_t BUF0 = pf_grid_bytes(TYPE);
@@ -136,9 +143,10 @@ struct PLds {
     static constexpr uint32_t XS = TT * 256;
     static constexpr uint32_t D8 = XS + TT * T::XB;
     static constexpr uint32_t W = D8 + (TYPE != kQ8_0 ? (TT < 64 ? 64 : TT) * 4 : 0);
-    static constexpr uint32_t TAIL = W + T::PR * T::UB;
+    static constexpr uint32_t TAIL = W + (SW ? 0 : T::PR * T::UB);
     static constexpr uint32_t bytes = TAIL + (TYPE == kIQ3_XXS ? T::PR * 4 : 0);
-    static constexpr uint32_t total = BUF0 + 2 * bytes;
+    static constexpr uint32_t WS = BUF0 + 2 * bytes;  // the shared weight region (SW)
+    static constexpr uint32_t total = WS + (SW ? T::PR * T::UB : 0);
 };
 
 struct PfArgs {
@@ -810,11 +818,11 @@ __device__ __forceinline__ void each_inst(uint32_t w, F &&f) {
 // and rows past N lie outside the descriptor (zeros); neither is stored.
 template <int TYPE, int NT>
 __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_t m0, uint32_t n0, uint32_t b,
-                                      unsigned char *buf, uint32_t w, uint32_t lane) {
+                                      unsigned char *buf, uint32_t w, uint32_t lane, unsigned char *wbuf) {
     using L = PLds<TYPE, NT>;
     using T = PfType<TYPE>;
     constexpr uint32_t TT = L::TT;
-    const uint32_t base = lds_addr(buf);
+    const uint32_t base = lds_addr(buf), wbase = lds_addr(wbuf);
     const uint32_t tb = b * a.M + m0;  // first token record of the tile in this superblock
     uint32_t ln = lane;
     asm volatile("" : "+v"(ln));  // per-call lane arithmetic (not hoisted into held registers)
@@ -848,13 +856,13 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
     each_inst<T::PR * CPR / 64>(w, [&](uint32_t k) {
         const uint32_t c = 64 * k + ln, r = c / CPR, p = c - CPR * r;
         if constexpr (TYPE == kIQ3_XXS)  // the window from the unit's 4-byte-aligned start (slot 6: unused)
-            lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 98) & ~3u) + 16 * min(p, 5u));
+            lds_load16(wbase + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 98) & ~3u) + 16 * min(p, 5u));
         else if constexpr (TYPE == kIQ3_S)
-            lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 110) & ~3u) + 16 * p);
+            lds_load16(wbase + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 110) & ~3u) + 16 * p);
         else if constexpr (TYPE == kQ6_K)  // (slot 14: unused)
-            lds_load16(base + L::W + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 210) & ~3u) + 16 * min(p, 13u));
+            lds_load16(wbase + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 210) & ~3u) + 16 * min(p, 13u));
         else
-            lds_load16(base + L::W + 1024 * k, rw, (n0 + r) * a.row_bytes + b * T::UB + 16 * p);
+            lds_load16(wbase + 1024 * k, rw, (n0 + r) * a.row_bytes + b * T::UB + 16 * p);
     });
     if constexpr (TYPE == kIQ3_XXS)  // the window's 25th dword (ends at most 2 bytes past the unit)
         each_inst<T::PR / 64>(w, [&](uint32_t k) {
@@ -884,6 +892,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t rg = w % RG, tg = w / RG;      // row group, token group
     auto buf = [&](uint32_t b) __attribute__((always_inline)) { return lds + L::BUF0 + (b & 1) * L::bytes; };
+    auto wbuf = [&](uint32_t b) __attribute__((always_inline)) { return L::SW ? lds + L::WS : buf(b) + L::W; };
 
     if constexpr (pf_grid_bytes(TYPE) != 0) {
         // the signed grid: entry 16 i + n = grid word i with the signs of
@@ -924,15 +933,17 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 
         // Previous segment's readers of both buffers are done.
         __syncthreads();
-        stage<TYPE, NT>(a, tg_.W, m0, n0, b0, buf(b0), w, lane);
+        stage<TYPE, NT>(a, tg_.W, m0, n0, b0, buf(b0), w, lane, wbuf(b0));
         // Per superblock: its loads are waited for, the next superblock's
         // issued into the other LDS buffer, this lane's weights converted,
         // then the MFMAs.
         for (uint32_t b = b0; b < b1; ++b) {
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             __syncthreads();
-            stage<TYPE, NT>(a, tg_.W, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane);
+            // (SW: after this superblock's raw weight reads, below)
+            if constexpr (!L::SW) stage<TYPE, NT>(a, tg_.W, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane, wbuf(b + 1));
             const unsigned char *bb = buf(b);
+            const unsigned char *wb = wbuf(b);
             if constexpr (TYPE == kQ4_K || TYPE == kQ5_K) {
                 constexpr bool Q5 = TYPE == kQ5_K;
                 using Frag = std::conditional_t<Q5, Q5Frag, Q4Frag>;
@@ -950,9 +961,9 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 {
                     std::conditional_t<Q5, Q5Raw, Q4Raw> rr;
                     if constexpr (Q5)
-                        q5_read(rr, bb + L::W + rl * T::UB, g);
+                        q5_read(rr, wb + rl * T::UB, g);
                     else
-                        q4_read(rr, bb + L::W + rl * T::UB, g);
+                        q4_read(rr, wb + rl * T::UB, g);
                     const uint32_t tok = 32 * tg * NB + j;
                     k_convert_chain<Q5>(rr, f, bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, j, g, ch,
                                         cl, mn[0]);
@@ -984,7 +995,14 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 {
                     const uint32_t sh = ((n0 + rl) * a.row_bytes + b * 210) & 3u;
                     Q6Raw rr;
-                    q6_read(rr, bb + L::W + rl * T::UB, sh, g);
+                    q6_read(rr, wb + rl * T::UB, sh, g);
+                    if constexpr (L::SW) {
+                        // every wave's raw reads done, then the next
+                        // superblock's loads (into the one weight region)
+                        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                        __syncthreads();
+                        stage<TYPE, NT>(a, tg_.W, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane, wbuf(b + 1));
+                    }
                     const uint32_t tok = 32 * tg * NB + j;
                     q6_convert_chain(rr, g, f, bb + L::QS + tok * 256, j, ch, cl);
                     f.d = h2f(sh ? rr.dw >> 16 : rr.dw & 0xFFFFu);
@@ -1008,10 +1026,10 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             } else if constexpr (TYPE == kIQ3_XXS || TYPE == kIQ3_S) {
                 I3Frag f;
                 if constexpr (TYPE == kIQ3_XXS)
-                    i3_convert(bb + L::W + rl * T::UB, bb + L::TAIL + 4 * rl, ((n0 + rl) * a.row_bytes + b * 98) & 3u,
+                    i3_convert(wb + rl * T::UB, bb + L::TAIL + 4 * rl, ((n0 + rl) * a.row_bytes + b * 98) & 3u,
                                reinterpret_cast<const uint32_t *>(lds + L::GRID), g, f);
                 else
-                    is3_convert(bb + L::W + rl * T::UB, ((n0 + rl) * a.row_bytes + b * 110) & 3u,
+                    is3_convert(wb + rl * T::UB, ((n0 + rl) * a.row_bytes + b * 110) & 3u,
                                 reinterpret_cast<const uint32_t *>(lds + L::GRID), g, f);
                 constexpr int P = NB >= 2 ? 2 : 1;
                 static_assert(NB % P == 0, "token blocks in pairs");
@@ -1029,7 +1047,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 }
             } else {
                 Q8Frag f;
-                q8_convert(bb + L::W + rl * T::UB, g, f);
+                q8_convert(wb + rl * T::UB, g, f);
 #pragma unroll
                 for (int t = 0; t < NB; ++t) {
                     __builtin_amdgcn_sched_barrier(0);
@@ -1243,11 +1261,12 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
 int pf_nt(int type, uint32_t M) {
     static_assert(PLds<kIQ3_XXS, 4>::total <= 160 * 1024 && PLds<kIQ3_S, 4>::total <= 160 * 1024 &&
                       PLds<kQ5_K, 2>::total <= 160 * 1024 && PLds<kQ6_K, 2>::total <= 160 * 1024 &&
+                      PLds<kQ6_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ4_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ8_0, 4>::total <= 160 * 1024,
                   "LDS of one workgroup");
     const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
-    return type == kQ8_0 ? std::max(nt, 2) : type == kQ5_K || type == kQ6_K ? std::min(nt, 2) : nt;
+    return type == kQ8_0 ? std::max(nt, 2) : type == kQ5_K ? std::min(nt, 2) : nt;
 }
 uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // Q5_K, IQ3_XXS, IQ3_S: 256 too
 
@@ -1290,7 +1309,7 @@ PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_
 constexpr uint32_t kNt2MaxM = 256;
 PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     const PfGeom g = pf_geom_nt(type, pf_nt(type, M), M, N, K, num_cu);
-    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 || type == kQ5_K || type == kQ6_K ||
+    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 || type == kQ5_K ||
         pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256))
         return g;
     const PfGeom h = pf_geom_nt(type, 2, M, N, K, num_cu);
@@ -1370,7 +1389,13 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
         }
     }
     if (type == kQ5_K) return g.nt == 1 ? pf_launch<kQ5_K, 1>(a, st) : pf_launch<kQ5_K, 2>(a, st);
-    if (type == kQ6_K) return g.nt == 1 ? pf_launch<kQ6_K, 1>(a, st) : pf_launch<kQ6_K, 2>(a, st);
+    if (type == kQ6_K) {
+        switch (g.nt) {
+            case 1: return pf_launch<kQ6_K, 1>(a, st);
+            case 2: return pf_launch<kQ6_K, 2>(a, st);
+            default: return pf_launch<kQ6_K, 4>(a, st);
+        }
+    }
     if (type == kIQ3_S) {
         switch (g.nt) {
             case 1: return pf_launch<kIQ3_S, 1>(a, st);
