@@ -1,5 +1,5 @@
-// tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K, Q8_0,
-// IQ3_XXS and IQ3_S weights on the int8 matrix cores
+// tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K, Q5_K,
+// Q6_K, Q8_0, IQ3_XXS and IQ3_S weights on the int8 matrix cores
 // (v_mfma_i32_32x32x32_i8). The weights of a tile are converted once per
 // token tile of up to 128 tokens, in the registers of the lanes that feed
 // them to the MFMA.
@@ -21,7 +21,12 @@
 //    per workgroup), so no weight is converted twice for one tile.
 //  * Q8_0: 128 rows per workgroup, waves w and w + 4 share rows and take one
 //    half of the tile's tokens each (the Q8_0 weight blocks take 272 bytes of
-//    LDS per row and superblock).
+//    LDS per row and superblock); from 257 tokens 256 rows as Q4_K, with one
+//    weight region in LDS instead of two (as Q6_K at 128-token tiles: each
+//    wave reads its rows' raw bytes into registers, then a barrier, then the
+//    next superblock's weight loads).
+//  * Q5_K, Q6_K: as Q4_K (256 rows), at most 64 tokens per tile for Q5_K;
+//    Q6_K's 128-token tiles keep one weight region in LDS.
 //  * IQ3_XXS, IQ3_S: as Q4_K (256 rows); the sign-applied codebook is built
 //    in LDS once per workgroup.
 //
@@ -94,6 +99,14 @@ template <>
 struct PfType<kQ8_0> {
     static constexpr uint32_t PR = 128, TSPLIT = 2, UB = 272, XB = 64;
 };
+// Q8_0 from 257 tokens: 256 rows per workgroup (each wave 32 rows x 128
+// tokens, so a weight is converted once per 4 token blocks instead of 2),
+// with one weight region in LDS (see pf_shared_w). An id of this file only.
+constexpr int kQ8W = 108;
+template <>
+struct PfType<kQ8W> {
+    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 272, XB = 64;
+};
 // Q6_K: the 210-byte unit (2-byte aligned) in the 224-byte window from its
 // 4-byte-aligned start (14 chunks, loaded as 15 at a 240-byte row stride:
 // conflict-free 16-byte reads); at most 64 tokens per tile (256 such rows
@@ -131,7 +144,7 @@ __host__ __device__ constexpr uint32_t pf_grid_bytes(int type) {
 // next superblock's weights are loaded only after a barrier that follows
 // those reads (the activations stay double-buffered).
 template <int TYPE, int NT>
-constexpr bool pf_shared_w() { return TYPE == kQ6_K && NT == 4; }
+constexpr bool pf_shared_w() { return (TYPE == kQ6_K && NT == 4) || TYPE == kQ8W; }
 template <int TYPE, int NT>
 struct PLds {
     using T = PfType<TYPE>;
@@ -142,7 +155,7 @@ struct PLds {
     static constexpr uint32_t QS = 0;
     static constexpr uint32_t XS = TT * 256;
     static constexpr uint32_t D8 = XS + TT * T::XB;
-    static constexpr uint32_t W = D8 + (TYPE != kQ8_0 ? (TT < 64 ? 64 : TT) * 4 : 0);
+    static constexpr uint32_t W = D8 + (TYPE != kQ8_0 && TYPE != kQ8W ? (TT < 64 ? 64 : TT) * 4 : 0);
     static constexpr uint32_t TAIL = W + (SW ? 0 : T::PR * T::UB);
     static constexpr uint32_t bytes = TAIL + (TYPE == kIQ3_XXS ? T::PR * 4 : 0);
     static constexpr uint32_t WS = BUF0 + 2 * bytes;  // the shared weight region (SW)
@@ -832,7 +845,7 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
         lds_load16(base + L::QS + 1024 * k, rq, (tb + t) * 256 + 16 * ((ln & 15) ^ (t & 15)));
     });
     const v4i rx = rs4(a.xs, a.M * a.nblk * T::XB);
-    if constexpr (TYPE != kQ8_0) {
+    if constexpr (TYPE != kQ8_0 && TYPE != kQ8W) {
         if constexpr (T::XB != 0)
             each_inst<TT / 32>(w, [&](uint32_t k) {
                 lds_load16(base + L::XS + 1024 * k, rx, (tb + 32 * k) * T::XB + 16 * ln);
@@ -1048,6 +1061,11 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             } else {
                 Q8Frag f;
                 q8_convert(wb + rl * T::UB, g, f);
+                if constexpr (L::SW) {
+                    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every raw read done
+                    __syncthreads();
+                    stage<TYPE, NT>(a, tg_.W, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane, wbuf(b + 1));
+                }
 #pragma unroll
                 for (int t = 0; t < NB; ++t) {
                     __builtin_amdgcn_sched_barrier(0);
@@ -1263,12 +1281,12 @@ int pf_nt(int type, uint32_t M) {
                       PLds<kQ5_K, 2>::total <= 160 * 1024 && PLds<kQ6_K, 2>::total <= 160 * 1024 &&
                       PLds<kQ6_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ4_K, 4>::total <= 160 * 1024 &&
-                      PLds<kQ8_0, 4>::total <= 160 * 1024,
+                      PLds<kQ8_0, 4>::total <= 160 * 1024 && PLds<kQ8W, 4>::total <= 160 * 1024,
                   "LDS of one workgroup");
     const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
     return type == kQ8_0 ? std::max(nt, 2) : type == kQ5_K ? std::min(nt, 2) : nt;
 }
-uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // Q5_K, IQ3_XXS, IQ3_S: 256 too
+uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // the others: 256
 
 // Split tiles are summed inside the main kernel, by their last contributor,
 // when no tile has more than kFusedMax contributors: that workgroup reads the
@@ -1285,13 +1303,19 @@ bool pf_fused(uint64_t units, uint32_t G, uint32_t nblk) {
 
 struct PfGeom {
     int nt;
+    bool wide;  // Q8_0: the 256-row geometry (kQ8W)
     uint32_t tt, pr, ntm, ntn, ntiles, G;
 };
+// The wide Q8_0 geometry from this many tokens on (at 128: 65 against 58 us,
+// its 4-token-block tiles split over 5 workgroups each and needing the fixup
+// launch; from 512 on faster: M = 2048 586 -> 525 us).
+constexpr uint32_t kQ8WideMinM = 256;
 PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     PfGeom g;
     g.nt = nt;
+    g.wide = type == kQ8_0 && nt == 4 && M > kQ8WideMinM;
     g.tt = 32u * g.nt;
-    g.pr = pf_rows(type);
+    g.pr = g.wide ? PfType<kQ8W>::PR : pf_rows(type);
     g.ntm = (M + g.tt - 1) / g.tt;
     g.ntn = (N + g.pr - 1) / g.pr;
     g.ntiles = g.ntm * g.ntn;
@@ -1380,7 +1404,10 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
     a.ntiles = g.ntiles;
     a.G = g.G;
     a.fused = pf_fused(a.ntiles * a.nblk, a.G, a.nblk) ? 1u : 0u;
-    if (type == kQ8_0) return g.nt == 2 ? pf_launch<kQ8_0, 2>(a, st) : pf_launch<kQ8_0, 4>(a, st);
+    if (type == kQ8_0) {
+        if (g.wide) return pf_launch<kQ8W, 4>(a, st);
+        return g.nt == 2 ? pf_launch<kQ8_0, 2>(a, st) : pf_launch<kQ8_0, 4>(a, st);
+    }
     if (type == kIQ3_XXS) {
         switch (g.nt) {
             case 1: return pf_launch<kIQ3_XXS, 1>(a, st);
