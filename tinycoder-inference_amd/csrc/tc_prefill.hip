@@ -25,8 +25,8 @@
 //    weight region in LDS instead of two (as Q6_K at 128-token tiles: each
 //    wave reads its rows' raw bytes into registers, then a barrier, then the
 //    next superblock's weight loads).
-//  * Q5_K, Q6_K: as Q4_K (256 rows), at most 64 tokens per tile for Q5_K;
-//    Q6_K's 128-token tiles keep one weight region in LDS.
+//  * Q5_K, Q6_K: as Q4_K (256 rows); their 128-token tiles keep one weight
+//    region in LDS.
 //  * IQ3_XXS, IQ3_S: as Q4_K (256 rows); the sign-applied codebook is built
 //    in LDS once per workgroup.
 //
@@ -89,8 +89,8 @@ template <>
 struct PfType<kQ4_K> {
     static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 144, XB = 32;
 };
-// Q5_K: as Q4_K, 176-byte units; at most 64 tokens per tile (three digit
-// planes per sub-block, and 128-token stages would not fit LDS twice).
+// Q5_K: as Q4_K, 176-byte units; at 128-token tiles one weight region in
+// LDS (two stages of 256 such rows would not fit).
 template <>
 struct PfType<kQ5_K> {
     static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 176, XB = 32;
@@ -144,7 +144,7 @@ __host__ __device__ constexpr uint32_t pf_grid_bytes(int type) {
 // next superblock's weights are loaded only after a barrier that follows
 // those reads (the activations stay double-buffered).
 template <int TYPE, int NT>
-constexpr bool pf_shared_w() { return (TYPE == kQ6_K && NT == 4) || TYPE == kQ8W; }
+constexpr bool pf_shared_w() { return ((TYPE == kQ5_K || TYPE == kQ6_K) && NT == 4) || TYPE == kQ8W; }
 template <int TYPE, int NT>
 struct PLds {
     using T = PfType<TYPE>;
@@ -290,13 +290,10 @@ __device__ __forceinline__ void q4_combine(const float *d8, const Q4Frag &f, con
 // ---- Q5_K: B operands of one superblock ------------------------------------
 // Reference dequantizeQ5_KBlock (GGMLDequantize.hpp:392-402): the Q4_K
 // header and nibbles plus a fifth bit per weight, bit s of qh[i] for element
-// i of sub-block s; w = d*sc_s*q - dmin*m_s with q = nibble + 16 b. So
-// sc_s q = 8 (h_s n + 2 sc_s b) + l_s n: the bit plane 2 sc_s b (<= 126)
-// goes into the hi chain's accumulator after the h_s n plane, and C =
-// 8*hi + lo as for Q4_K.
-struct Q5Frag : Q4Frag {
-    v4i bb[8];
-};
+// i of sub-block s; w = d*sc_s*q - dmin*m_s with q = nibble + 16 b (0..31).
+// e = sc_s q <= 1953 as digits e = 128 hi + lo (hi <= 15, lo <= 127): the
+// same two MFMA chains as Q4_K, C = 128*hi + lo, and the same min term.
+using Q5Frag = Q4Frag;
 struct Q5Raw : Q4Raw {
     u4 qh;
 };
@@ -313,7 +310,13 @@ template <bool Q5, typename F>
 __device__ __forceinline__ void k_step(const v4i &a, const F &f, int s, v16i &ch, v16i &cl) {
     ch = mfma(a, f.bh[s], ch);
     cl = mfma(a, f.bl[s], cl);
-    if constexpr (Q5) ch = mfma(a, f.bb[s], ch);
+}
+// Q5_K digits of e = sc * q for four values q (bytes, <= 31) and sc <= 63
+// held in both 16-bit halves of m: hi = e >> 7, lo = e & 127, in byte order.
+__device__ __forceinline__ void q5_digits(uint32_t q, uint32_t m, int &hi, int &lo) {
+    const uint32_t ee = uint32_t(pkmul(q & 0x00FF00FFu, m)), eo = uint32_t(pkmul((q >> 8) & 0x00FF00FFu, m));
+    lo = int(__builtin_amdgcn_perm(eo & 0x007F007Fu, ee & 0x007F007Fu, 0x06020400u));
+    hi = int(__builtin_amdgcn_perm((eo >> 7) & 0x001F001Fu, (ee >> 7) & 0x001F001Fu, 0x06020400u));
 }
 
 // The conversion of this wave's weights with the first token block's MFMAs,
@@ -338,17 +341,24 @@ __device__ __forceinline__ void k_convert_chain(const R &r, F &f, const unsigned
         const uint32_t mh = bcast16(hw[sb >> 2], sb & 3), ml = bcast16(lw[sb >> 2], sb & 3);
         const u4 qv = r.q[sb >> 1];
         const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+        if constexpr (!Q5) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t nib = (sb & 1) ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
-            f.bh[sb][k] = pkmul(nib, mh);
-            f.bl[sb][k] = pkmul(nib, ml);
-        }
-        if constexpr (Q5) {
-            const uint32_t m2 = 2u * bcast16(sb < 4 ? scl : sch, sb & 3);  // 2 sc_s in both 16-bit halves
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t nib = (sb & 1) ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
+                f.bh[sb][k] = pkmul(nib, mh);
+                f.bl[sb][k] = pkmul(nib, ml);
+            }
+        } else {
+            const uint32_t msc = bcast16(sb < 4 ? scl : sch, sb & 3);  // sc_s in both 16-bit halves
             const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) f.bb[sb][k] = pkmul((qh[k] >> sb) & 0x01010101u, m2);
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t nib = (sb & 1) ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
+                int hi, lo;
+                q5_digits(nib | (((qh[k] >> sb) & 0x01010101u) << 4), msc, hi, lo);
+                f.bh[sb][k] = hi;
+                f.bl[sb][k] = lo;
+            }
         }
     };
     auto aread = [&](int s) __attribute__((always_inline)) {
@@ -977,12 +987,18 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                         q5_read(rr, wb + rl * T::UB, g);
                     else
                         q4_read(rr, wb + rl * T::UB, g);
+                    if constexpr (L::SW) {
+                        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every raw read done
+                        __syncthreads();
+                        stage<TYPE, NT>(a, tg_.W, m0, n0, min(b + 1, b1 - 1), buf(b + 1), w, lane, wbuf(b + 1));
+                    }
                     const uint32_t tok = 32 * tg * NB + j;
                     k_convert_chain<Q5>(rr, f, bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, j, g, ch,
                                         cl, mn[0]);
                 }
+                constexpr int CSH = Q5 ? 7 : 3;  // C = 128*hi + lo (Q5_K), 8*hi + lo (Q4_K)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) c[0][r] = (ch[r] << 3) + cl[r];
+                for (int r = 0; r < 16; ++r) c[0][r] = (ch[r] << CSH) + cl[r];
 #pragma unroll
                 for (int t = 0; t < NB; ++t) {
                     if (t + 1 < NB) {
@@ -995,7 +1011,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     __builtin_amdgcn_sched_barrier(0);
                     if (t + 1 < NB) {
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) c[(t + 1) & 1][r] = (ch[r] << 3) + cl[r];
+                        for (int r = 0; r < 16; ++r) c[(t + 1) & 1][r] = (ch[r] << CSH) + cl[r];
                     }
                 }
             } else if constexpr (TYPE == kQ6_K) {
@@ -1278,13 +1294,13 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
 // else 128 (Q8_0: 64 or 128, as its waves split the tile's tokens in two).
 int pf_nt(int type, uint32_t M) {
     static_assert(PLds<kIQ3_XXS, 4>::total <= 160 * 1024 && PLds<kIQ3_S, 4>::total <= 160 * 1024 &&
-                      PLds<kQ5_K, 2>::total <= 160 * 1024 && PLds<kQ6_K, 2>::total <= 160 * 1024 &&
+                      PLds<kQ5_K, 4>::total <= 160 * 1024 && PLds<kQ6_K, 2>::total <= 160 * 1024 &&
                       PLds<kQ6_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ4_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ8_0, 4>::total <= 160 * 1024 && PLds<kQ8W, 4>::total <= 160 * 1024,
                   "LDS of one workgroup");
     const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
-    return type == kQ8_0 ? std::max(nt, 2) : type == kQ5_K ? std::min(nt, 2) : nt;
+    return type == kQ8_0 ? std::max(nt, 2) : nt;
 }
 uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<kQ4_K>::PR; }  // the others: 256
 
@@ -1333,7 +1349,7 @@ PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_
 constexpr uint32_t kNt2MaxM = 256;
 PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
     const PfGeom g = pf_geom_nt(type, pf_nt(type, M), M, N, K, num_cu);
-    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 || type == kQ5_K ||
+    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 ||
         pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256))
         return g;
     const PfGeom h = pf_geom_nt(type, 2, M, N, K, num_cu);
@@ -1415,7 +1431,13 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
             default: return pf_launch<kIQ3_XXS, 4>(a, st);
         }
     }
-    if (type == kQ5_K) return g.nt == 1 ? pf_launch<kQ5_K, 1>(a, st) : pf_launch<kQ5_K, 2>(a, st);
+    if (type == kQ5_K) {
+        switch (g.nt) {
+            case 1: return pf_launch<kQ5_K, 1>(a, st);
+            case 2: return pf_launch<kQ5_K, 2>(a, st);
+            default: return pf_launch<kQ5_K, 4>(a, st);
+        }
+    }
     if (type == kQ6_K) {
         switch (g.nt) {
             case 1: return pf_launch<kQ6_K, 1>(a, st);
