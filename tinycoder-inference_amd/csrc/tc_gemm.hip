@@ -1,6 +1,6 @@
 // tc_gemm.hip -- prefill GEMM: out[m][n] = W[n] . x[m] for M tokens against raw
-// GGUF weight rows of Q6_K and IQ2_S, on the int8 matrix cores
-// (v_mfma_i32_32x32x32_i8). (Q4_K, Q5_K, Q8_0, IQ3_XXS and IQ3_S run the
+// GGUF weight rows of IQ2_S, on the int8 matrix cores
+// (v_mfma_i32_32x32x32_i8). (Q4_K, Q5_K, Q6_K, Q8_0, IQ3_XXS and IQ3_S run the
 // register-conversion kernel of tc_prefill.hip.)
 //
 // Replaces the reference prefill GEMM (int8Gemm, GemmDispatch.cu:595-698) with
@@ -19,8 +19,8 @@
 // consumers (the activation plane loaded straight into LDS, MFMAs on the
 // other half).
 //
-// Every weight of a superblock becomes an exact signed integer e (Q6_K
-// sc*(q-32), IQ2_S (2ls+1)*(+-grid value)) written to two int8 planes,
+// Every weight of a superblock becomes an exact signed integer e
+// ((2ls+1)*(+-grid value)) written to two int8 planes,
 // e = 128*hi + lo, so that one MFMA chain over the hi plane, a shift by 7 and
 // the lo chain on top give sum_s e . x exactly. Per superblock and output:
 // acc += d8 * d * main.
@@ -80,14 +80,9 @@ __device__ __forceinline__ v4i as_v4i(u4 v) { return __builtin_bit_cast(v4i, v);
 
 template <int TYPE>
 struct GPrefetch {
-    // IQ2_S: the bytes of the two 32-chunks 2qq, 2qq+1 (4-byte-aligned
-    // words, realigned on conversion); Q6_K: its 16-byte runs of ql (two) and
-    // qh, read from 4-byte-aligned addresses (blocks are 2-byte aligned) with
-    // their fifth dwords in ex, then the scale bytes and d.
-    static constexpr int RAWC = TYPE == kQ6_K ? 3 : 1;
-    static constexpr int EXC = TYPE == kQ6_K ? 7 : 9;
-    u4 raw[RAWC];
-    uint32_t ex[EXC];
+    // the bytes of the two 32-chunks 2qq, 2qq+1 (4-byte-aligned words,
+    // realigned on conversion)
+    uint32_t ex[9];
     uint32_t sh;           // the block's byte offset mod 4
     float d8;              // Q8_K d (128 tokens)
 };
@@ -98,7 +93,7 @@ struct GPrefetch {
 struct GSrc {
     __amdgpu_buffer_rsrc_t w, d;
     uint32_t vw, vd;   // per-lane offsets
-    uint32_t vo[4];    // Q6_K: this thread's byte offsets inside a block; IQ2_S: vo[3] the quarter
+    uint32_t qq;       // the thread's quarter
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t grsrc(const void *p, uint64_t bytes) {
@@ -109,23 +104,12 @@ template <int TYPE>
 __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_t m0, uint32_t tid) {
     GSrc g;
     // whole dwords: the range check zeroes a dword that is only partly in
-    // range, and 2-byte-aligned units (Q6_K, IQ2_S) end 2 bytes into
+    // range, and 2-byte-aligned units end 2 bytes into
     // one when their count is odd (it stays in the page of the last byte)
     g.w = grsrc(a.W, (uint64_t(a.N) * a.row_bytes + 3) & ~uint64_t(3));
     g.d = grsrc(a.d8, uint64_t(a.M) * (a.K / 256) * 4);
     g.vw = (n0 + tid / 4) * a.row_bytes;
-    if constexpr (TYPE == kQ6_K) {
-        // thread (row tid/4, half n = bit 1, part p = bit 0): ql[64n + 16p ..],
-        // ql[64n + 32 + 16p ..], qh[32n + 16p ..] (16 bytes each), scales 8n..8n+7
-        const uint32_t n = (tid >> 1) & 1, pp = tid & 1;
-        g.vo[0] = 64 * n + 16 * pp;
-        g.vo[1] = 64 * n + 32 + 16 * pp;
-        g.vo[2] = 128 + 32 * n + 16 * pp;
-        g.vo[3] = 192 + 8 * n;
-    } else {
-        g.vo[0] = g.vo[1] = g.vo[2] = 0;
-        g.vo[3] = tid & 3;  // IQ2_S: the thread's quarter
-    }
+    g.qq = tid & 3;
     g.vd = (m0 + (tid & 127)) * 4;
     return g;
 }
@@ -133,7 +117,8 @@ __device__ __forceinline__ GSrc gemm_src(const GemmArgs &a, uint32_t n0, uint32_
 template <int TYPE>
 __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, uint32_t b, GPrefetch<TYPE> &p) {
     constexpr uint32_t UB = unit_bytes(TYPE);
-    if constexpr (TYPE == kIQ2_S) {
+    static_assert(TYPE == kIQ2_S, "IQ2_S only");
+    {
         // 2-byte-aligned blocks; each piece from its 4-byte-aligned address
         // down, the block start's offset mod 4 in sh
         const uint32_t blk = g.vw + b * UB;
@@ -142,7 +127,7 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
         auto w32 = [&](uint32_t off) __attribute__((always_inline)) {
             return __builtin_amdgcn_raw_buffer_load_b32(g.w, (blk + off) & ~3u, 0, 0);
         };
-        const uint32_t qq = g.vo[3];
+        const uint32_t qq = g.qq;
         p.ex[0] = w32(2 + 8 * qq);        // qs (grid low bytes)
         p.ex[1] = w32(2 + 8 * qq + 4);
         p.ex[2] = w32(2 + 8 * qq + 8);
@@ -152,19 +137,6 @@ __device__ __forceinline__ void gemm_prefetch(const GemmArgs &a, const GSrc &g, 
         p.ex[7] = w32(66 + 2 * qq);       // qh bytes 2qq, 2qq+1
         p.ex[8] = w32(74 + 2 * qq);       // scale bytes 2qq, 2qq+1
         p.ex[6] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al, 0, 0);  // d
-    } else {
-        static_assert(TYPE == kQ6_K, "Q6_K and IQ2_S only");
-        const uint32_t blk = g.vw + b * UB;  // block start (2-byte aligned)
-        p.sh = blk & 3;
-        const uint32_t al = blk & ~3u;  // every vo is a multiple of 4
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            p.raw[i] = __builtin_amdgcn_raw_buffer_load_b128(g.w, al + g.vo[i], 0, 0);
-            p.ex[i] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + g.vo[i] + 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 3; ++i) p.ex[3 + i] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + g.vo[3] + 4 * i, 0, 0);
-        p.ex[6] = __builtin_amdgcn_raw_buffer_load_b32(g.w, al + 208, 0, 0);  // d (bytes 208, 209)
     }
     p.d8 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(g.d, g.vd, b * a.M * 4, 0));
 }
@@ -184,13 +156,6 @@ __device__ __forceinline__ void digits_s16(s16x2 ve, s16x2 vo, short k, uint32_t
     hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he), 0x06020400u);
 }
 
-// Four unsigned 6-bit values per word (Q6_K q) -> digits of sc * (q - 32).
-__device__ __forceinline__ void digits_q6(uint32_t q, int sc, uint32_t &hi, uint32_t &lo) {
-    const s16x2 ve = __builtin_bit_cast(s16x2, q & 0x00FF00FFu) - s16x2{32, 32};
-    const s16x2 vo = __builtin_bit_cast(s16x2, (q >> 8) & 0x00FF00FFu) - s16x2{32, 32};
-    digits_s16(ve, vo, short(sc), hi, lo);
-}
-
 // Four signed bytes per word (signed grid values) -> digits of k * v.
 __device__ __forceinline__ void digits_i8(uint32_t v, int k, uint32_t &hi, uint32_t &lo) {
     // sign extension per 16-bit lane: (b ^ 0x80) - 0x80
@@ -201,45 +166,6 @@ __device__ __forceinline__ void digits_i8(uint32_t v, int k, uint32_t &hi, uint3
 
 __device__ __forceinline__ uint32_t realign(uint32_t hi, uint32_t lo, uint32_t sh) {
     return __builtin_amdgcn_alignbyte(hi, lo, sh);
-}
-
-// Q6_K weights of this thread (row tid/4, half n, part p: positions
-// 128n + 32c + 16p + j of the four families c) -> the digit planes and d.
-// q = ql nibble | (qh 2-bit field) << 4 (reference dequantizeQ6_KBlock,
-// include/GGMLDequantize.hpp:503-527), e = sc[8n + 2c + p] * (q - 32).
-__device__ __forceinline__ void q6k_convert(const GPrefetch<kQ6_K> &p, unsigned char *lds, uint32_t tid) {
-    using L = GLds;
-    const uint32_t r = tid / 4, n = (tid >> 1) & 1, pp = tid & 1;
-    uint32_t w[3][4];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const uint32_t v[5] = {p.raw[i].x, p.raw[i].y, p.raw[i].z, p.raw[i].w, p.ex[i]};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[i][j] = realign(v[j + 1], v[j], p.sh);
-    }
-    const uint32_t s0 = realign(p.ex[4], p.ex[3], p.sh), s1 = realign(p.ex[5], p.ex[4], p.sh);  // scales 8n..8n+7
-    const uint32_t dh = p.sh ? (p.ex[6] >> 16) : (p.ex[6] & 0xFFFFu);
-    unsigned char *a0 = lds + L::A0 + r * PL, *a1 = lds + L::A1 + r * PL;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t sb = 2 * c + pp;  // scale byte index within the 8
-        const int sc = int(int8_t(((sb < 4 ? s0 : s1) >> (8 * (sb & 3))) & 0xFFu));
-        uint32_t hi[4], lo[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t la = w[0][j], lb = w[1][j], qh = w[2][j];
-            uint32_t q;
-            if (c == 0) q = (la & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
-            else if (c == 1) q = (lb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
-            else if (c == 2) q = ((la >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
-            else q = ((lb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
-            digits_q6(q, sc, hi[j], lo[j]);
-        }
-        const uint32_t k0 = 128 * n + 32 * c + 16 * pp;
-        *reinterpret_cast<u4 *>(a0 + k0) = u4{hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<u4 *>(a1 + k0) = u4{lo[0], lo[1], lo[2], lo[3]};
-    }
-    reinterpret_cast<float *>(lds + L::AS)[r] = h2f(dh);
 }
 
 // IQ2_S weights of this thread (row tid/4, 32-chunks ib = 2qq + c) -> the
@@ -292,10 +218,7 @@ template <int TYPE>
 __device__ __forceinline__ void gemm_stage(const GPrefetch<TYPE> &p, unsigned char *lds, uint32_t tid,
                                            const uint32_t *grid = nullptr) {
     using L = GLds;
-    if constexpr (TYPE == kIQ2_S)
-        iq2s_convert(p, lds, grid, tid);
-    else
-        q6k_convert(p, lds, tid);
+    iq2s_convert(p, lds, grid, tid);
     reinterpret_cast<float *>(lds + L::BD)[tid & (GM - 1)] = p.d8;  // threads tid and tid+128 hold the same d
 }
 
@@ -616,8 +539,8 @@ size_t gemm_workspace_bytes(int, uint32_t M, uint32_t N, uint32_t K, int num_cu)
 hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
                        int num_cu, void *workspace, hipStream_t st) {
     if (M == 0 || N == 0 || K == 0 || K % 256) return hipErrorInvalidValue;
-    // Q6_K and IQ2_S here; the other MFMA types run k_prefill (tc_prefill.hip).
-    if (type != kQ6_K && type != kIQ2_S) return hipErrorInvalidValue;
+    // IQ2_S here; the other MFMA types run k_prefill (tc_prefill.hip).
+    if (type != kIQ2_S) return hipErrorInvalidValue;
     // 32-bit buffer offsets: the quantized activations (M*K bytes) and one
     // weight matrix must each stay below 4 GiB.
     if (uint64_t(M) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * unit_bytes(type) >= (uint64_t(1) << 32))
@@ -639,7 +562,7 @@ hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, 
     a.ws = static_cast<float *>(workspace);
     a.skg = G;
     const dim3 g{G, 1u, 1u};
-    hipError_t e = type == kQ6_K ? launch_gemm_t<kQ6_K>(a, g, st) : launch_gemm_t<kIQ2_S>(a, g, st);
+    hipError_t e = launch_gemm_t<kIQ2_S>(a, g, st);
     if (e != hipSuccess) return e;
     // Any tile split over workgroups? (a range boundary inside a tile)
     bool split = false;

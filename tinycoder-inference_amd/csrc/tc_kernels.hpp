@@ -75,7 +75,7 @@ uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs);
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes);
 uint32_t gemv_max_tokens(int type, uint32_t cols);
 
-// Prefill GEMM (int8 MFMA) for Q6_K and IQ2_S (the other MFMA types:
+// Prefill GEMM (int8 MFMA) for IQ2_S (the other MFMA types:
 // launch_prefill): out[M][N] = W x^T with activations already quantized
 // (launch_quant_act over M tokens, block-major). Stream-K over one workgroup
 // per CU; the partial tiles need gemm_workspace_bytes() of scratch.
