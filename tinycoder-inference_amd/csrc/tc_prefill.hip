@@ -172,8 +172,6 @@ struct PfArgs {
     float *ws;          // partial tiles [G][2][TT][PR]
     uint32_t *ctr;      // per tile: contributors arrived (zero before the launch, zero after it)
     uint32_t fused;     // split tiles summed by their last contributor (else by k_pf_fixup)
-    uint32_t xpf;       // a segment's last iteration stages the next segment's first superblock (else
-                        // each segment stages its own first one after a barrier)
     uint32_t M, N, K;
     uint32_t row_bytes, nblk;
     uint32_t ntm, ntn, ntiles;  // token tiles, row blocks, tiles
@@ -939,8 +937,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const uint32_t units = pf_ntiles<GRP>(a) * a.nblk;
     const uint32_t ub = sk_begin(units, a.G, v), ue = sk_begin(units, a.G, v + 1);
     uint32_t ph = 0;
-    const bool xpf = a.xpf != 0;
-    if (xpf && ub < ue) {
+    if (ub < ue) {
         const uint32_t tile = ub / a.nblk;
         const PfTile t0 = pf_tile<GRP>(a, tile, TT, PR);
         stage<TYPE, NT>(a, t0.W, t0.m0, t0.n0, ub - tile * a.nblk, buf(ph), w, lane, wbuf(ph));
@@ -968,30 +965,20 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
-        // With xpf, the segment's first superblock is staged already (before
-        // the loop, or by the previous segment's last iteration) and the last
-        // iteration stages the next segment's first, so that its loads
-        // overlap this segment's final MFMAs and epilogue; without, each
-        // segment stages its first superblock after a barrier.
+        // The segment's first superblock is staged already (before the loop,
+        // or by the previous segment's last iteration); the last iteration
+        // stages the next segment's first, so that its loads overlap this
+        // segment's final MFMAs and epilogue (M = 128: 1-7% faster; MoE
+        // grouped launches 4-5%).
         const uint32_t ntile = u / a.nblk;  // (u < ue: the next segment's tile, starting at superblock 0)
         auto stage_next = [&](uint32_t b) __attribute__((always_inline)) {
             if (b + 1 < b1) {
                 stage<TYPE, NT>(a, tg_.W, m0, n0, b + 1, buf(ph + 1), w, lane, wbuf(ph + 1));
-            } else if (xpf) {
-                if (u < ue) {
-                    const PfTile nt_ = pf_tile<GRP>(a, ntile, TT, PR);
-                    stage<TYPE, NT>(a, nt_.W, nt_.m0, nt_.n0, 0, buf(ph + 1), w, lane, wbuf(ph + 1));
-                }
-            } else {
-                // (the same superblock again: measured faster than no load
-                // here, for reasons not understood)
-                stage<TYPE, NT>(a, tg_.W, m0, n0, b, buf(ph + 1), w, lane, wbuf(ph + 1));
+            } else if (u < ue) {
+                const PfTile nt_ = pf_tile<GRP>(a, ntile, TT, PR);
+                stage<TYPE, NT>(a, nt_.W, nt_.m0, nt_.n0, 0, buf(ph + 1), w, lane, wbuf(ph + 1));
             }
         };
-        if (!xpf) {
-            __syncthreads();  // previous segment's readers of both buffers are done
-            stage<TYPE, NT>(a, tg_.W, m0, n0, b0, buf(ph), w, lane, wbuf(ph));
-        }
         // Per superblock: its loads are waited for, the next superblock's
         // issued into the other LDS buffer, this lane's weights converted,
         // then the MFMAs.
@@ -1127,7 +1114,6 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             __builtin_amdgcn_sched_barrier(0);
             ph ^= 1;
         }
-        if (!xpf) __builtin_amdgcn_s_waitcnt(0x0F70);  // nothing of this segment left in flight
 
         // lane: row n0 + rl, tokens m0 + 32 (tg NB + t) + 8q + 4g + e
         const uint32_t n = n0 + rl;
@@ -1456,10 +1442,6 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
     a.ntiles = g.ntiles;
     a.G = g.G;
     a.fused = pf_fused(a.ntiles * a.nblk, a.G, a.nblk) ? 1u : 0u;
-    // each segment's last iteration stages the next segment's first
-    // superblock (Q4_K/Q5_K/Q8_0 at M = 128: 3-7% faster; M = 512 and 2048
-    // within +-2%); grouped launches stage at each segment's start
-    a.xpf = 1;
     if (type == kQ8_0) {
         if (g.wide) return pf_launch<kQ8W, 4>(a, st);
         return g.nt == 2 ? pf_launch<kQ8_0, 2>(a, st) : pf_launch<kQ8_0, 4>(a, st);
