@@ -257,8 +257,7 @@ size_t gemm_mfma_scratch(int type, uint32_t S, uint32_t rows, uint32_t cols, int
     // last superblock run up to one token tile past the buffer (values never
     // stored; the buffer range check covers only the per-lane offset).
     *act_bytes = tc::act_layout(type, S, cols).bytes + kGemmActSlack;
-    if (tc::prefill_type(type)) return tc::prefill_workspace_bytes(type, S, rows, cols, num_cu);
-    return tc::gemm_workspace_bytes(type, S, rows, cols, num_cu);
+    return tc::prefill_workspace_bytes(type, S, rows, cols, num_cu);
 }
 
 // Quantize all tokens once (block-major, into act), then the MFMA kernel
@@ -271,10 +270,7 @@ int gemm_mfma_into(int type, const void *w, const float *x, float *out, uint32_t
     const uint32_t nctr = ws ? tc::prefill_counter_words(type, S, rows, cols, num_cu) : 0;
     hipError_t e = tc::launch_quant_act(type, x, S, cols, L, act, st, true, static_cast<uint32_t *>(ws), nctr);
     if (e != hipSuccess) return hip_fail(e, "activation quantizer");
-    if (tc::prefill_type(type))
-        e = tc::launch_prefill(type, w, act_view(act, L, 0, type, cols), out, S, rows, cols, num_cu, ws, st);
-    else
-        e = tc::launch_gemm(type, w, act_view(act, L, 0, type, cols), out, S, rows, cols, num_cu, ws, st);
+    e = tc::launch_prefill(type, w, act_view(act, L, 0, type, cols), out, S, rows, cols, num_cu, ws, st);
     if (e != hipSuccess) return hip_fail(e, "int8 MFMA GEMM");
     return TC_OK;
 }

@@ -10,7 +10,7 @@ namespace tc {
 // IQ3_XXS, 32-wide Q8_0-style for Q8_0) of x[S][cols] into `buf` laid out by
 // act_layout(wtype, S, cols).
 // With block_major the blocks are stored block-major (block j of token t at
-// j * S + t), the layout launch_gemm reads.
+// j * S + t), the layout launch_prefill reads.
 // The launch also zeroes zero[0 .. nzero) (the prefill GEMM's arrival
 // counters, which must be zero when the GEMM that follows starts).
 hipError_t launch_quant_act(int wtype, const float *x, uint32_t S, uint32_t cols, const ActLayout &L,
@@ -75,18 +75,12 @@ uint64_t jobs_weight_bytes(int type, const GemvJob *jobs, uint32_t njobs);
 uint32_t gemv_fused_quant_limit(int type, uint64_t weight_bytes);
 uint32_t gemv_max_tokens(int type, uint32_t cols);
 
-// Prefill GEMM (int8 MFMA) for IQ2_S (the other MFMA types:
-// launch_prefill): out[M][N] = W x^T with activations already quantized
-// (launch_quant_act over M tokens, block-major). Stream-K over one workgroup
-// per CU; the partial tiles need gemm_workspace_bytes() of scratch.
-size_t gemm_workspace_bytes(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu);
-hipError_t launch_gemm(int type, const void *W, const ActView &act, float *out, uint32_t M, uint32_t N, uint32_t K,
-                       int num_cu, void *workspace, hipStream_t st);
-
-// Prefill GEMM with the weights converted in the MFMA lanes' registers, once
-// per token tile of up to 128 tokens (tc_prefill.hip; Q4_K, Q5_K, Q8_0,
-// IQ3_XXS, IQ3_S). Needs the
-// activations' scale data (act.dg) and prefill_workspace_bytes() of scratch
+// Prefill GEMM (int8 MFMA): out[M][N] = W x^T with the activations already
+// quantized (launch_quant_act over M tokens, block-major) and the weights
+// converted in the MFMA lanes' registers, once per token tile of up to 128
+// tokens (tc_prefill.hip; Q4_K, Q5_K, Q6_K, Q8_0, IQ3_XXS, IQ3_S, IQ2_S).
+// Stream-K over one workgroup per CU. Q4_K, Q5_K and Q8_0 need the
+// activations' scale data (act.dg); every type prefill_workspace_bytes() of scratch
 // whose first prefill_counter_words() 32-bit words are zero when the launch
 // starts (every launch leaves them zero again).
 bool prefill_type(int type);

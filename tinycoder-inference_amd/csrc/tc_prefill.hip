@@ -129,9 +129,16 @@ template <>
 struct PfType<kIQ3_S> {
     static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 112, XB = 0;
 };
-// Codebook types: the sign-applied grid (entries x 16 sign nibbles x 4 bytes).
+// IQ2_S: the 82-byte unit (2-byte aligned) in the 84-byte window from its
+// 4-byte-aligned start (6 chunks at a 112-byte row stride, slot 6 unused).
+template <>
+struct PfType<kIQ2_S> {
+    static constexpr uint32_t PR = 256, TSPLIT = 1, UB = 112, XB = 0;
+};
+// Codebook types: IQ3_XXS / IQ3_S the sign-applied grid (entries x 16 sign
+// nibbles x 4 bytes), IQ2_S its 1024 8-byte entries as they are.
 __host__ __device__ constexpr uint32_t pf_grid_bytes(int type) {
-    return type == kIQ3_XXS ? 256 * 16 * 4 : type == kIQ3_S ? 512 * 16 * 4 : 0;
+    return type == kIQ3_XXS ? 256 * 16 * 4 : type == kIQ3_S ? 512 * 16 * 4 : type == kIQ2_S ? 1024 * 8 : 0;
 }
 
 // One LDS buffer: [TT][256] activation values (16-byte chunk c of token t at
@@ -491,15 +498,17 @@ __device__ __forceinline__ void q6_conv(const Q6Raw &r, uint32_t g, int s, Q6Fra
 // The conversion with the first token block's MFMAs (after the MFMA pair of
 // block s, the planes of block s + 2), then each further block's MFMAs with
 // the previous block's combination (as for Q4_K).
-__device__ __forceinline__ void q6_convert_chain(const Q6Raw &r, uint32_t g, Q6Frag &f, const unsigned char *arow,
-                                                 uint32_t j, v16i &ch, v16i &cl) {
+// conv(s): the planes of 32-block s into f.bh[s], f.bl[s]
+template <typename Conv>
+__device__ __forceinline__ void dig_convert_chain(Conv &&conv, uint32_t g, Q6Frag &f, const unsigned char *arow,
+                                                  uint32_t j, v16i &ch, v16i &cl) {
     auto aread = [&](int s) __attribute__((always_inline)) {
         return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
     };
     v4i af[2];
     af[0] = aread(0);
-    q6_conv(r, g, 0, f);
-    q6_conv(r, g, 1, f);
+    conv(0);
+    conv(1);
     ch = v16i{};
     cl = v16i{};
     __builtin_amdgcn_sched_barrier(0);
@@ -508,7 +517,7 @@ __device__ __forceinline__ void q6_convert_chain(const Q6Raw &r, uint32_t g, Q6F
         if (s + 1 < 8) af[(s + 1) & 1] = aread(s + 1);
         ch = mfma(af[s & 1], f.bh[s], ch);
         cl = mfma(af[s & 1], f.bl[s], cl);
-        if (s + 2 < 8) q6_conv(r, g, s + 2, f);
+        if (s + 2 < 8) conv(s + 2);
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -550,6 +559,61 @@ __device__ __forceinline__ void q6_combine(const float *d8, const Q6Frag &f, con
         for (int e = 0; e < 4; ++e) acc[4 * q + e] = fmaf(dd[e], f.d * float(c[4 * q + e]), acc[4 * q + e]);
     }
 }
+
+// ---- IQ2_S: B operands of one superblock -----------------------------------
+// Reference dequantizeIQ2_SBlock and its fused block dot
+// (GGMLDequantize.hpp:1215-1242, :2028-2057): group l (8 weights) of 32-block
+// ib has the 8 magnitudes (8, 25 or 43) of codebook entry qs[4ib + l] | bits
+// 2l, 2l+1 of qh[ib] << 8, negated by the bits of signs[4ib + l], times
+// 2ls + 1 with ls nibble l / 2 of scales[ib]; the row is scaled by d/8. The
+// lane's k-half g of 32-block s is groups 2g and 2g + 1: one scale k. With the
+// signs applied bytewise and the sign bit flipped, q = w + 128 (85..171), so
+// e = k*q - 128k (|e| <= 1333) takes Q6_K's signed digits, C = 128 hi + lo,
+// acc += d8 * ((d/8) * C).
+struct I2Raw {
+    uint32_t qs[8], sg[8];  // the lane's index and sign byte pairs per 32-block
+    uint32_t qh[2], sc[2];  // qh[0..7], scales[0..7]
+    uint32_t d;
+};
+__device__ __forceinline__ void i2_read(I2Raw &r, const unsigned char *win, uint32_t sh, uint32_t g) {
+    const uint16_t *u = reinterpret_cast<const uint16_t *>(win + sh);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        r.qs[s] = u[1 + 2 * s + g];
+        r.sg[s] = u[17 + 2 * s + g];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        r.qh[i] = uint32_t(u[33 + 2 * i]) | (uint32_t(u[34 + 2 * i]) << 16);
+        r.sc[i] = uint32_t(u[37 + 2 * i]) | (uint32_t(u[38 + 2 * i]) << 16);
+    }
+    r.d = u[0];
+}
+__device__ __forceinline__ void i2_conv(const I2Raw &r, const unsigned char *grid, uint32_t g, int s, Q6Frag &f) {
+    const uint32_t qhb = __builtin_amdgcn_ubfe(r.qh[s >> 2], 8 * (s & 3) + 4 * g, 4);  // bits of groups 2g, 2g + 1
+    const short k = short(2 * __builtin_amdgcn_ubfe(r.sc[s >> 2], 8 * (s & 3) + 4 * g, 4) + 1);
+    const s16x2 k2 = {k, k}, off = {short(-128 * k), short(-128 * k)};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t idx = __builtin_amdgcn_ubfe(r.qs[s], 8 * h, 8) | (((qhb >> (2 * h)) & 3u) << 8);
+        const uint2 gv = *reinterpret_cast<const uint2 *>(grid + 8 * idx);
+        const uint32_t sb = __builtin_amdgcn_ubfe(r.sg[s], 8 * h, 8);
+        const uint32_t m1 = spread_sign4(sb & 15u), m2 = spread_sign4(sb >> 4);
+        const uint32_t q0 = ((gv.x ^ m1) + (m1 & 0x01010101u)) ^ 0x80808080u;
+        const uint32_t q1 = ((gv.y ^ m2) + (m2 & 0x01010101u)) ^ 0x80808080u;
+        uint32_t hi, lo;
+        q6_digits(q0, k2, off, hi, lo);
+        f.bh[s][2 * h] = int(hi);
+        f.bl[s][2 * h] = int(lo);
+        q6_digits(q1, k2, off, hi, lo);
+        f.bh[s][2 * h + 1] = int(hi);
+        f.bl[s][2 * h + 1] = int(lo);
+    }
+}
+
+__constant__ uint64_t c_pf_iq2s_grid[1024] = {
+#include "iq2s_grid.inc"
+};
 
 // ---- Q8_0: B operands of one superblock ------------------------------------
 
@@ -885,6 +949,8 @@ __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_
             lds_load16(wbase + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 98) & ~3u) + 16 * min(p, 5u));
         else if constexpr (TYPE == kIQ3_S)
             lds_load16(wbase + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 110) & ~3u) + 16 * p);
+        else if constexpr (TYPE == kIQ2_S)  // (slot 6: unused)
+            lds_load16(wbase + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 82) & ~3u) + 16 * min(p, 5u));
         else if constexpr (TYPE == kQ6_K)  // (slot 14: unused)
             lds_load16(wbase + 1024 * k, rw, (((n0 + r) * a.row_bytes + b * 210) & ~3u) + 16 * min(p, 13u));
         else
@@ -922,7 +988,13 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     auto buf = [&](uint32_t p) __attribute__((always_inline)) { return lds + L::BUF0 + (p & 1) * L::bytes; };
     auto wbuf = [&](uint32_t p) __attribute__((always_inline)) { return L::SW ? lds + L::WS : buf(p) + L::W; };
 
-    if constexpr (pf_grid_bytes(TYPE) != 0) {
+    if constexpr (TYPE == kIQ2_S) {
+        uint2 *gr = reinterpret_cast<uint2 *>(lds + L::GRID);
+        for (uint32_t e = tid; e < 1024; e += 64 * PW) {
+            const uint64_t v = c_pf_iq2s_grid[e];
+            gr[e] = make_uint2(uint32_t(v), uint32_t(v >> 32));
+        }
+    } else if constexpr (pf_grid_bytes(TYPE) != 0) {
         // the signed grid: entry 16 i + n = grid word i with the signs of
         // nibble n applied bytewise (grid bytes are nonzero: no carries)
         uint32_t *sg = reinterpret_cast<uint32_t *>(lds + L::GRID);
@@ -1036,14 +1108,14 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                         for (int r = 0; r < 16; ++r) c[(t + 1) & 1][r] = (ch[r] << CSH) + cl[r];
                     }
                 }
-            } else if constexpr (TYPE == kQ6_K) {
+            } else if constexpr (TYPE == kQ6_K || TYPE == kIQ2_S) {
                 Q6Frag f;
                 auto d8_t = [&](int t) __attribute__((always_inline)) {
                     return reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t) + 4 * g;
                 };
                 v16i c[2], ch, cl;
                 __builtin_amdgcn_sched_barrier(0);
-                {
+                if constexpr (TYPE == kQ6_K) {
                     const uint32_t sh = ((n0 + rl) * a.row_bytes + b * 210) & 3u;
                     Q6Raw rr;
                     q6_read(rr, wb + rl * T::UB, sh, g);
@@ -1055,8 +1127,19 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                         stage_next(b);
                     }
                     const uint32_t tok = 32 * tg * NB + j;
-                    q6_convert_chain(rr, g, f, bb + L::QS + tok * 256, j, ch, cl);
+                    dig_convert_chain([&](int s) __attribute__((always_inline)) { q6_conv(rr, g, s, f); }, g, f,
+                                      bb + L::QS + tok * 256, j, ch, cl);
                     f.d = h2f(sh ? rr.dw >> 16 : rr.dw & 0xFFFFu);
+                } else {
+                    static_assert(!L::SW, "IQ2_S: two weight stages");
+                    const uint32_t sh = ((n0 + rl) * a.row_bytes + b * 82) & 3u;
+                    I2Raw rr;
+                    i2_read(rr, wb + rl * T::UB, sh, g);
+                    const uint32_t tok = 32 * tg * NB + j;
+                    const unsigned char *grid = lds + L::GRID;
+                    dig_convert_chain([&](int s) __attribute__((always_inline)) { i2_conv(rr, grid, g, s, f); }, g,
+                                      f, bb + L::QS + tok * 256, j, ch, cl);
+                    f.d = 0.125f * h2f(rr.d);  // (a power of two: exact)
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) c[0][r] = (ch[r] << 7) + cl[r];
@@ -1319,7 +1402,8 @@ int pf_nt(int type, uint32_t M) {
                       PLds<kQ5_K, 4>::total <= 160 * 1024 && PLds<kQ6_K, 2>::total <= 160 * 1024 &&
                       PLds<kQ6_K, 4>::total <= 160 * 1024 &&
                       PLds<kQ4_K, 4>::total <= 160 * 1024 &&
-                      PLds<kQ8_0, 4>::total <= 160 * 1024 && PLds<kQ8W, 4>::total <= 160 * 1024,
+                      PLds<kQ8_0, 4>::total <= 160 * 1024 && PLds<kQ8W, 4>::total <= 160 * 1024 &&
+                      PLds<kIQ2_S, 4>::total <= 160 * 1024,
                   "LDS of one workgroup");
     const int nt = M <= 32 ? 1 : M <= 64 ? 2 : 4;
     return type == kQ8_0 ? std::max(nt, 2) : nt;
@@ -1399,7 +1483,8 @@ hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
 }  // namespace
 
 bool prefill_type(int type) {
-    return type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0 || type == kIQ3_XXS || type == kIQ3_S;
+    return type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0 || type == kIQ3_XXS || type == kIQ3_S ||
+           type == kIQ2_S;
 }
 
 // Workspace: the per-tile arrival counters (256-byte rounded), then the
@@ -1465,6 +1550,13 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
             case 1: return pf_launch<kQ6_K, 1>(a, st);
             case 2: return pf_launch<kQ6_K, 2>(a, st);
             default: return pf_launch<kQ6_K, 4>(a, st);
+        }
+    }
+    if (type == kIQ2_S) {
+        switch (g.nt) {
+            case 1: return pf_launch<kIQ2_S, 1>(a, st);
+            case 2: return pf_launch<kIQ2_S, 2>(a, st);
+            default: return pf_launch<kIQ2_S, 4>(a, st);
         }
     }
     if (type == kIQ3_S) {
