@@ -234,6 +234,23 @@ __device__ __forceinline__ u4 lds4(const unsigned char *p) { return *reinterpret
 __device__ __forceinline__ uint32_t lds1(const unsigned char *p) { return *reinterpret_cast<const uint32_t *>(p); }
 __device__ __forceinline__ v4i as_v4i(u4 v) { return __builtin_bit_cast(v4i, v); }
 
+// The lane's activation chunk 2s + g of sub-block s (s < 8) for its token of
+// the first token block (chunks XOR-swizzled by token): one address per
+// sub-block, formed once per superblock; token block t lies 8192*t bytes on,
+// which the LDS reads take as an immediate offset.
+// (32-bit byte offsets into the workgroup's LDS array)
+struct ASet {
+    const unsigned char *lds;
+    uint32_t o[8];
+};
+__device__ __forceinline__ ASet aset(const unsigned char *lds, uint32_t row0, uint32_t j, uint32_t g) {
+    ASet a;
+    a.lds = lds;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) a.o[s] = row0 + 16 * ((2 * s + g) ^ (j & 15));
+    return a;
+}
+
 // Bytewise products of four values (each <= 15) with one multiplier <= 7
 // held in both 16-bit halves of m: no product exceeds a byte, so the 16-bit
 // multiplies carry nothing into the neighbouring byte.
@@ -336,7 +353,7 @@ __device__ __forceinline__ void q5_digits(uint32_t q, uint32_t m, int &hi, int &
 // 0..7, so h*q and l*q (q <= 15) are the bytewise products of pkmul; Q5_K's
 // bit plane is 2*sc*b (<= 126).
 template <bool Q5, typename R, typename F>
-__device__ __forceinline__ void k_convert_chain(const R &r, F &f, const unsigned char *arow, const unsigned char *dgp,
+__device__ __forceinline__ void k_convert_chain(const R &r, F &f, const ASet &as, uint32_t toff, const unsigned char *dgp,
                                                 uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn) {
     const u4 h = r.h;
     const uint32_t scl = h.y & 0x3F3F3F3Fu, mnl = h.z & 0x3F3F3F3Fu;
@@ -371,9 +388,7 @@ __device__ __forceinline__ void k_convert_chain(const R &r, F &f, const unsigned
             }
         }
     };
-    auto aread = [&](int s) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-    };
+    auto aread = [&](int s) __attribute__((always_inline)) { return as_v4i(lds4(as.lds + (as.o[s] + toff))); };
     const v4i dgv = as_v4i(lds4(dgp));
     v4i af[2];
     af[0] = aread(0);
@@ -395,12 +410,10 @@ __device__ __forceinline__ void k_convert_chain(const R &r, F &f, const unsigned
 // Block t + 1's MFMAs with block t's combination (as q4_combine) in slices:
 // after the MFMAs of sub-block s, the combination of outputs 2s and 2s + 1.
 template <bool Q5, typename F>
-__device__ __forceinline__ void k_chain_combine(const unsigned char *arow, const unsigned char *dgp, const F &f,
+__device__ __forceinline__ void k_chain_combine(const ASet &as, uint32_t toff, const unsigned char *dgp, const F &f,
                                                 uint32_t j, uint32_t g, v16i &ch, v16i &cl, v16f &mn,
                                                 const float *d8, const v16i &c, const v16f &mnp, float (&acc)[16]) {
-    auto aread = [&](int s) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-    };
+    auto aread = [&](int s) __attribute__((always_inline)) { return as_v4i(lds4(as.lds + (as.o[s] + toff))); };
     const v4i dgv = as_v4i(lds4(dgp));
     float4 dv[4];
 #pragma unroll
@@ -500,11 +513,9 @@ __device__ __forceinline__ void q6_conv(const Q6Raw &r, uint32_t g, int s, Q6Fra
 // the previous block's combination (as for Q4_K).
 // conv(s): the planes of 32-block s into f.bh[s], f.bl[s]
 template <typename Conv>
-__device__ __forceinline__ void dig_convert_chain(Conv &&conv, uint32_t g, Q6Frag &f, const unsigned char *arow,
-                                                  uint32_t j, v16i &ch, v16i &cl) {
-    auto aread = [&](int s) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-    };
+__device__ __forceinline__ void dig_convert_chain(Conv &&conv, Q6Frag &f, const ASet &as, uint32_t toff, v16i &ch,
+                                                  v16i &cl) {
+    auto aread = [&](int s) __attribute__((always_inline)) { return as_v4i(lds4(as.lds + (as.o[s] + toff))); };
     v4i af[2];
     af[0] = aread(0);
     conv(0);
@@ -521,12 +532,10 @@ __device__ __forceinline__ void dig_convert_chain(Conv &&conv, uint32_t g, Q6Fra
         __builtin_amdgcn_sched_barrier(0);
     }
 }
-__device__ __forceinline__ void q6_chain_combine(const unsigned char *arow, const Q6Frag &f, uint32_t j, uint32_t g,
+__device__ __forceinline__ void q6_chain_combine(const ASet &as, uint32_t toff, const Q6Frag &f, uint32_t g,
                                                  v16i &ch, v16i &cl, const float *d8, const v16i &c,
                                                  float (&acc)[16]) {
-    auto aread = [&](int s) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow + 16 * ((2 * s + g) ^ (j & 15))));
-    };
+    auto aread = [&](int s) __attribute__((always_inline)) { return as_v4i(lds4(as.lds + (as.o[s] + toff))); };
     float4 dv[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) dv[q] = *reinterpret_cast<const float4 *>(d8 + 8 * q);
@@ -662,11 +671,9 @@ __device__ __forceinline__ void q8_convert(const unsigned char *row, uint32_t g,
 // product I (int8 MFMA) and the scales dw*d8 of its 32x32 outputs (bf16
 // MFMA), then acc += I * scale. Block k + 1's MFMAs are issued before block
 // k's fp32 combination, so that the matrix core works while the VALU does.
-__device__ __forceinline__ void q8_block(const unsigned char *arow, const unsigned char *prow, const Q8Frag &f,
+__device__ __forceinline__ void q8_block(const ASet &as, uint32_t toff, const unsigned char *prow, const Q8Frag &f,
                                          uint32_t j, uint32_t g, float (&acc)[16]) {
-    auto aread = [&](int k) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow + 16 * ((2 * k + g) ^ (j & 15))));
-    };
+    auto aread = [&](int k) __attribute__((always_inline)) { return as_v4i(lds4(as.lds + (as.o[k] + toff))); };
     auto pread = [&](int c) __attribute__((always_inline)) { return as_v4i(lds4(prow + 256 * c)); };
     v4i af[3], pp[2];
     af[0] = aread(0);
@@ -792,15 +799,15 @@ __device__ __forceinline__ void is3_convert(const unsigned char *row, uint32_t s
 // multiply-adds (so that no multiply-add waits for the MFMA issued just
 // before it).
 template <int P>
-__device__ __forceinline__ void i3_blocks(const unsigned char *const (&arow)[P], const float *const (&d8)[P],
-                                          const I3Frag &f, uint32_t j, uint32_t g, float (&acc)[P][16]) {
+__device__ __forceinline__ void i3_blocks(const ASet &as, uint32_t toff, const float *const (&d8)[P], const I3Frag &f,
+                                          float (&acc)[P][16]) {
     int is[P][16];
 #pragma unroll
     for (int t = 0; t < P; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) is[t][r] = 0;
     auto aread = [&](int ib, int t) __attribute__((always_inline)) {
-        return as_v4i(lds4(arow[t] + 16 * ((2 * ib + g) ^ (j & 15))));
+        return as_v4i(lds4(as.lds + (as.o[ib] + toff + 8192u * t)));
     };
     // Activation fragments two 32-blocks ahead, and block ib + 1's MFMAs
     // issued before block ib's multiply-adds (the matrix core works while
@@ -851,6 +858,16 @@ __device__ __forceinline__ void i3_blocks(const unsigned char *const (&arow)[P],
             for (int e = 0; e < 4; ++e)
                 acc[t][4 * q + e] = fmaf(dd[e] * f.d, float(is[t][4 * q + e]), acc[t][4 * q + e]);
         }
+}
+
+// The lane's index recomputed where it is used (v_mbcnt on an opaque zero):
+// a value the compiler cannot hoist, so that no register holds the lane
+// across the kernel's loops (held, it was spilled, and the reload's wait also
+// waited for the stage loads just issued).
+__device__ __forceinline__ uint32_t lane_now() {
+    uint32_t z = 0;
+    asm volatile("" : "+s"(z));
+    return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, z));
 }
 
 // ---- loads into LDS ---------------------------------------------------------
@@ -908,14 +925,13 @@ __device__ __forceinline__ void each_inst(uint32_t w, F &&f) {
 // and rows past N lie outside the descriptor (zeros); neither is stored.
 template <int TYPE, int NT>
 __device__ __forceinline__ void stage(const PfArgs &a, const uint8_t *W, uint32_t m0, uint32_t n0, uint32_t b,
-                                      unsigned char *buf, uint32_t w, uint32_t lane, unsigned char *wbuf) {
+                                      unsigned char *buf, uint32_t w, unsigned char *wbuf) {
     using L = PLds<TYPE, NT>;
     using T = PfType<TYPE>;
     constexpr uint32_t TT = L::TT;
     const uint32_t base = lds_addr(buf), wbase = lds_addr(wbuf);
     const uint32_t tb = b * a.M + m0;  // first token record of the tile in this superblock
-    uint32_t ln = lane;
-    asm volatile("" : "+v"(ln));  // per-call lane arithmetic (not hoisted into held registers)
+    const uint32_t ln = lane_now();  // per-call lane arithmetic (not hoisted into held registers)
     const v4i rq = rs4(a.qs, a.M * a.K);
     each_inst<TT / 4>(w, [&](uint32_t k) {
         const uint32_t t = 4 * k + ln / 16;
@@ -1012,7 +1028,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (ub < ue) {
         const uint32_t tile = ub / a.nblk;
         const PfTile t0 = pf_tile<GRP>(a, tile, TT, PR);
-        stage<TYPE, NT>(a, t0.W, t0.m0, t0.n0, ub - tile * a.nblk, buf(ph), w, lane, wbuf(ph));
+        stage<TYPE, NT>(a, t0.W, t0.m0, t0.n0, ub - tile * a.nblk, buf(ph), w, wbuf(ph));
     }
     for (uint32_t u = ub; u < ue;) {
         const uint32_t tile = u / a.nblk;
@@ -1024,8 +1040,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         // The lane's row and k-half, recomputed per segment: the opaque copy
         // keeps the compiler from hoisting the address arithmetic of the
         // final stores out of the segment loop into registers held throughout.
-        uint32_t ln = lane;
-        asm volatile("" : "+v"(ln));
+        const uint32_t ln = lane_now();
         const uint32_t j = ln & 31, g = ln >> 5;
         const PfTile tg_ = pf_tile<GRP>(a, tile, TT, PR);
         const uint32_t n0 = tg_.n0, m0 = tg_.m0;
@@ -1045,10 +1060,10 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const uint32_t ntile = u / a.nblk;  // (u < ue: the next segment's tile, starting at superblock 0)
         auto stage_next = [&](uint32_t b) __attribute__((always_inline)) {
             if (b + 1 < b1) {
-                stage<TYPE, NT>(a, tg_.W, m0, n0, b + 1, buf(ph + 1), w, lane, wbuf(ph + 1));
+                stage<TYPE, NT>(a, tg_.W, m0, n0, b + 1, buf(ph + 1), w, wbuf(ph + 1));
             } else if (u < ue) {
                 const PfTile nt_ = pf_tile<GRP>(a, ntile, TT, PR);
-                stage<TYPE, NT>(a, nt_.W, nt_.m0, nt_.n0, 0, buf(ph + 1), w, lane, wbuf(ph + 1));
+                stage<TYPE, NT>(a, nt_.W, nt_.m0, nt_.n0, 0, buf(ph + 1), w, wbuf(ph + 1));
             }
         };
         // Per superblock: its loads are waited for, the next superblock's
@@ -1061,6 +1076,8 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             if constexpr (!L::SW) stage_next(b);
             const unsigned char *bb = buf(ph);
             const unsigned char *wb = wbuf(ph);
+            // this lane's activation addresses of the wave's first token block
+            const ASet as = aset(lds, uint32_t(bb - lds) + L::QS + (32 * tg * NB + j) * 256, j, g);
             if constexpr (TYPE == kQ4_K || TYPE == kQ5_K) {
                 constexpr bool Q5 = TYPE == kQ5_K;
                 using Frag = std::conditional_t<Q5, Q5Frag, Q4Frag>;
@@ -1077,18 +1094,20 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 __builtin_amdgcn_sched_barrier(0);
                 {
                     std::conditional_t<Q5, Q5Raw, Q4Raw> rr;
+                    // (the row's offset recomputed here: held across the
+                    // segment, it was spilled)
+                    const unsigned char *wrow = wb + (32 * rg + (lane_now() & 31)) * T::UB;
                     if constexpr (Q5)
-                        q5_read(rr, wb + rl * T::UB, g);
+                        q5_read(rr, wrow, g);
                     else
-                        q4_read(rr, wb + rl * T::UB, g);
+                        q4_read(rr, wrow, g);
                     if constexpr (L::SW) {
                         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every raw read done
                         __syncthreads();
                         stage_next(b);
                     }
                     const uint32_t tok = 32 * tg * NB + j;
-                    k_convert_chain<Q5>(rr, f, bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, j, g, ch,
-                                        cl, mn[0]);
+                    k_convert_chain<Q5>(rr, f, as, 0u, bb + L::XS + tok * T::XB + 16 * g, j, g, ch, cl, mn[0]);
                 }
                 constexpr int CSH = Q5 ? 7 : 3;  // C = 128*hi + lo (Q5_K), 8*hi + lo (Q4_K)
 #pragma unroll
@@ -1097,8 +1116,8 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 for (int t = 0; t < NB; ++t) {
                     if (t + 1 < NB) {
                         const uint32_t tok = 32 * (tg * NB + t + 1) + j;
-                        k_chain_combine<Q5>(bb + L::QS + tok * 256, bb + L::XS + tok * T::XB + 16 * g, f, j, g, ch,
-                                            cl, mn[(t + 1) & 1], d8_t(t), c[t & 1], mn[t & 1], acc[t]);
+                        k_chain_combine<Q5>(as, 8192u * (t + 1), bb + L::XS + tok * T::XB + 16 * g, f, j, g, ch, cl,
+                                            mn[(t + 1) & 1], d8_t(t), c[t & 1], mn[t & 1], acc[t]);
                     } else {
                         q4_combine(d8_t(t), f, c[t & 1], mn[t & 1], acc[t]);
                     }
@@ -1126,19 +1145,17 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                         __syncthreads();
                         stage_next(b);
                     }
-                    const uint32_t tok = 32 * tg * NB + j;
-                    dig_convert_chain([&](int s) __attribute__((always_inline)) { q6_conv(rr, g, s, f); }, g, f,
-                                      bb + L::QS + tok * 256, j, ch, cl);
+                    dig_convert_chain([&](int s) __attribute__((always_inline)) { q6_conv(rr, g, s, f); }, f, as, 0u,
+                                      ch, cl);
                     f.d = h2f(sh ? rr.dw >> 16 : rr.dw & 0xFFFFu);
                 } else {
                     static_assert(!L::SW, "IQ2_S: two weight stages");
                     const uint32_t sh = ((n0 + rl) * a.row_bytes + b * 82) & 3u;
                     I2Raw rr;
                     i2_read(rr, wb + rl * T::UB, sh, g);
-                    const uint32_t tok = 32 * tg * NB + j;
                     const unsigned char *grid = lds + L::GRID;
-                    dig_convert_chain([&](int s) __attribute__((always_inline)) { i2_conv(rr, grid, g, s, f); }, g,
-                                      f, bb + L::QS + tok * 256, j, ch, cl);
+                    dig_convert_chain([&](int s) __attribute__((always_inline)) { i2_conv(rr, grid, g, s, f); }, f,
+                                      as, 0u, ch, cl);
                     f.d = 0.125f * h2f(rr.d);  // (a power of two: exact)
                 }
 #pragma unroll
@@ -1146,8 +1163,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
                 for (int t = 0; t < NB; ++t) {
                     if (t + 1 < NB) {
-                        const uint32_t tok = 32 * (tg * NB + t + 1) + j;
-                        q6_chain_combine(bb + L::QS + tok * 256, f, j, g, ch, cl, d8_t(t), c[t & 1], acc[t]);
+                        q6_chain_combine(as, 8192u * (t + 1), f, g, ch, cl, d8_t(t), c[t & 1], acc[t]);
                     } else {
                         q6_combine(d8_t(t), f, c[t & 1], acc[t]);
                     }
@@ -1170,14 +1186,11 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
                 for (int t = 0; t < NB; t += P) {
                     __builtin_amdgcn_sched_barrier(0);
-                    const unsigned char *ar[P];
                     const float *dp[P];
 #pragma unroll
-                    for (int i = 0; i < P; ++i) {
-                        ar[i] = bb + L::QS + (32 * (tg * NB + t + i) + j) * 256;
+                    for (int i = 0; i < P; ++i)
                         dp[i] = reinterpret_cast<const float *>(bb + L::D8) + 32 * (tg * NB + t + i) + 4 * g;
-                    }
-                    i3_blocks<P>(ar, dp, f, j, g, reinterpret_cast<float(&)[P][16]>(acc[t]));
+                    i3_blocks<P>(as, 8192u * t, dp, f, reinterpret_cast<float(&)[P][16]>(acc[t]));
                 }
             } else {
                 Q8Frag f;
@@ -1191,7 +1204,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 for (int t = 0; t < NB; ++t) {
                     __builtin_amdgcn_sched_barrier(0);
                     const uint32_t tok = 32 * (tg * NB + t) + j;
-                    q8_block(bb + L::QS + tok * 256, bb + L::XS + 1024 * (tok >> 4) + 16 * (tok & 15), f, j, g, acc[t]);
+                    q8_block(as, 8192u * t, bb + L::XS + 1024 * (tok >> 4) + 16 * (tok & 15), f, j, g, acc[t]);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
