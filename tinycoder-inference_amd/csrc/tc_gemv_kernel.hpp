@@ -750,35 +750,50 @@ struct TDot<kIQ3_XXS, S> {
         int tot[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) tot[s] = 0;
+        // The codebook lookups of IB 32-runs are issued before their dot
+        // products, so that several LDS round trips overlap (gate/up pair
+        // 18944x3584: 20.2 -> 19.6 us with 4; 2 and 8 measured no better).
+        constexpr int IB = 4;
 #pragma unroll
-        for (int ib = 0; ib < 8; ++ib) {
-            const uint32_t aux = uint32_t(u16[33 + 2 * ib]) | (uint32_t(u16[34 + 2 * ib]) << 16);
-            const uint32_t gi0 = uint32_t(u16[1 + 4 * ib]) | (uint32_t(u16[2 + 4 * ib]) << 16);
-            const uint32_t gi1 = uint32_t(u16[3 + 4 * ib]) | (uint32_t(u16[4 + 4 * ib]) << 16);
-            uint32_t w[8];
+        for (int ib0 = 0; ib0 < 8; ib0 += IB) {
+            uint32_t w[IB][8];
+            uint32_t auxs[IB];
 #pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                const uint32_t idx7 = (aux >> (7 * l)) & 127u;
-                const uint32_t s8 = idx7 | ((__builtin_popcount(idx7) & 1u) << 7);
-                const uint32_t gw = l < 2 ? gi0 : gi1;
-                // signed-grid entries (16 * index + sign nibble)
-                w[2 * l] = sgrid[((gw >> (16 * (l & 1))) & 0xFF) * 16 + (s8 & 15u)];
-                w[2 * l + 1] = sgrid[((gw >> (16 * (l & 1) + 8)) & 0xFF) * 16 + (s8 >> 4)];
+            for (int i = 0; i < IB; ++i) {
+                const int ib = ib0 + i;
+                const uint32_t aux = uint32_t(u16[33 + 2 * ib]) | (uint32_t(u16[34 + 2 * ib]) << 16);
+                const uint32_t gi0 = uint32_t(u16[1 + 4 * ib]) | (uint32_t(u16[2 + 4 * ib]) << 16);
+                const uint32_t gi1 = uint32_t(u16[3 + 4 * ib]) | (uint32_t(u16[4 + 4 * ib]) << 16);
+                auxs[i] = aux;
+#pragma unroll
+                for (int l = 0; l < 4; ++l) {
+                    const uint32_t idx7 = (aux >> (7 * l)) & 127u;
+                    const uint32_t s8 = idx7 | ((__builtin_popcount(idx7) & 1u) << 7);
+                    const uint32_t gw = l < 2 ? gi0 : gi1;
+                    // signed-grid entries (16 * index + sign nibble)
+                    w[i][2 * l] = sgrid[((gw >> (16 * (l & 1))) & 0xFF) * 16 + (s8 & 15u)];
+                    w[i][2 * l + 1] = sgrid[((gw >> (16 * (l & 1) + 8)) & 0xFF) * 16 + (s8 >> 4)];
+                }
             }
-            const int mult = 2 * int(aux >> 28) + 1;
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int s = 0; s < S; ++s) {
-                const unsigned char *xr = xr0 + s * xtok + 32 * ib;
-                const u32x4 x0 = lds128(xr), x1 = lds128(xr + 16);
-                int p = sdot4(int(w[0]), int(x0.x), 0);
-                p = sdot4(int(w[1]), int(x0.y), p);
-                p = sdot4(int(w[2]), int(x0.z), p);
-                p = sdot4(int(w[3]), int(x0.w), p);
-                p = sdot4(int(w[4]), int(x1.x), p);
-                p = sdot4(int(w[5]), int(x1.y), p);
-                p = sdot4(int(w[6]), int(x1.z), p);
-                p = sdot4(int(w[7]), int(x1.w), p);
-                tot[s] += mult * p;
+            for (int i = 0; i < IB; ++i) {
+                const int ib = ib0 + i;
+                const int mult = 2 * int(auxs[i] >> 28) + 1;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const unsigned char *xr = xr0 + s * xtok + 32 * ib;
+                    const u32x4 x0 = lds128(xr), x1 = lds128(xr + 16);
+                    int p = sdot4(int(w[i][0]), int(x0.x), 0);
+                    p = sdot4(int(w[i][1]), int(x0.y), p);
+                    p = sdot4(int(w[i][2]), int(x0.z), p);
+                    p = sdot4(int(w[i][3]), int(x0.w), p);
+                    p = sdot4(int(w[i][4]), int(x1.x), p);
+                    p = sdot4(int(w[i][5]), int(x1.y), p);
+                    p = sdot4(int(w[i][6]), int(x1.z), p);
+                    p = sdot4(int(w[i][7]), int(x1.w), p);
+                    tot[s] += mult * p;
+                }
             }
         }
         const float d = h2f(u16[0]);
