@@ -244,7 +244,48 @@ def test_moe_grouped_vs_oracle(tc, dev, oracle, grouped, S):
                                 h_step_bound(oracle, x, ids, wts, wg, wu, wd, E, H, FF))
     assert ok, worst
     again = tc.moe_ffn(*args).cpu().numpy()
-    assert np.array_equal(got, again)  # row order within an expert does not change any value
+    assert np.array_equal(got, again)  # an expert's rows take pair order: repeated calls agree bit for bit
+
+
+def test_moe_grouped_deterministic_many_tiles(tc, dev, grouped):
+    """Config-5 experts at 1024 tokens (~64 rows per expert, so experts span
+    two 64-row tiles whose K ranges split differently): a row's tile decides
+    the rounding of its sums, so the rows of an expert must land in a fixed
+    order. Three calls agree bit for bit."""
+    import torch
+    E, K, H, FF, S = 128, 8, 2048, 768, 1024
+    gen = torch.Generator(device=dev).manual_seed(777)
+
+    def enc(rows, cols):
+        return tc.encode(Q4_K, torch.randn((rows, cols), generator=gen, device=dev) * 0.02)
+
+    wg, wu, wd = enc(E * FF, H), enc(E * FF, H), enc(E * H, FF)
+    ids, wts = routing(np.random.default_rng(778), S, E, K)
+    x = torch.randn((S, H), generator=gen, device=dev)
+    args = [x, to_dev(ids, dev), to_dev(wts, dev), wg, wu, wd, E, H, FF]
+    first = tc.moe_ffn(*args).cpu().numpy()
+    for _ in range(2):
+        assert np.array_equal(first, tc.moe_ffn(*args).cpu().numpy())
+
+
+def test_moe_grouped_repeated_expert(tc, dev, oracle, grouped):
+    """An expert named twice for one token (the router never does this; the
+    kernel's fallback row assignment): both pairs computed, as the oracle
+    does, and repeated calls agree."""
+    E, K, H, FF, S = 8, 4, 512, 256, 40
+    wg, wu, wd = moe_weights(lambda x: oracle.encode(Q4_K, x), E, H, FF, seed=91)
+    rng = np.random.default_rng(92)
+    ids, wts = routing(rng, S, E, K)
+    ids[0, 1] = ids[0, 0]
+    ids[7, 3] = ids[7, 2]
+    x = rng.standard_normal((S, H)).astype(np.float32)
+    args = [to_dev(x, dev), to_dev(ids, dev), to_dev(wts, dev), to_dev(wg, dev), to_dev(wu, dev), to_dev(wd, dev),
+            E, H, FF]
+    got = tc.moe_ffn(*args).cpu().numpy()
+    ok, worst = close_moe_flips(got, oracle.moe_ffn(x, ids, wts, wg, wu, wd, E, H, FF),
+                                h_step_bound(oracle, x, ids, wts, wg, wu, wd, E, H, FF))
+    assert ok, worst
+    assert np.array_equal(got, tc.moe_ffn(*args).cpu().numpy())
 
 
 def test_moe_grouped_all_ids_invalid(tc, dev, oracle, grouped):

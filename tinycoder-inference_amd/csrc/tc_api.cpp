@@ -568,8 +568,7 @@ int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wt
         e = tc::launch_prefill_grouped(wu, gstride, ax, u, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, ctr,
                                        b + o_ws, st);
     if (e != hipSuccess) return hip_fail(e, "MoE gate/up GEMM");
-    e = tc::launch_moe_swiglu(g, u, P, FF, st);
-    if (e == hipSuccess) e = tc::launch_quant_act(TC_Q4_K, g, P, FF, LH, b + o_ah, st, true);
+    e = tc::launch_swiglu_quant_q8k(g, u, P, FF, LH, b + o_ah, st);
     if (e != hipSuccess) return hip_fail(e, "MoE SwiGLU");
     const tc::ActView ah = act_view(b + o_ah, LH, 0, TC_Q4_K, FF);
     e = tc::launch_prefill_grouped(wd, dstride, ah, y, P, H, FF, mt, ntm, ntm_max, tile, dev->num_cu, ctr, b + o_ws,

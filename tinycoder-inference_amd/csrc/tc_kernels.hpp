@@ -117,7 +117,11 @@ hipError_t launch_moe_route(const int32_t *ids, uint32_t npairs, uint32_t top_k,
                             hipStream_t st);
 // h = silu(g) * u elementwise over nrows_max rows of ff values, written over g
 // (rows past the routed ones hold values nothing reads).
-hipError_t launch_moe_swiglu(float *g, const float *u, uint32_t nrows_max, uint32_t ff, hipStream_t st);
+// MoE: h = silu(g) * u over g, u [S][cols] quantized to Q8_K block-major
+// into buf (layout L, as launch_quant_act with block_major); h itself is not
+// stored.
+hipError_t launch_swiglu_quant_q8k(const float *g, const float *u, uint32_t S, uint32_t cols, const ActLayout &L,
+                                   void *buf, hipStream_t st);
 // out[t] = sum over r in rank order of wts[t*top_k+r] * y[pos[t*top_k+r]]
 // (pairs with pos < 0 skipped), from 0.
 hipError_t launch_moe_combine_rows(const float *y, const int32_t *pos, const float *wts, float *out, uint32_t T,

@@ -9,6 +9,7 @@
 // done on the device from the router's ids, and ONE grouped GEMM launch per
 // matrix covers every expert (tiles never straddle two experts), so no host
 // round trip or per-expert launch sits between the router and the experts.
+#include "tc_actquant.hpp"
 #include "tc_kernels.hpp"
 
 namespace tc {
@@ -16,27 +17,75 @@ namespace {
 
 constexpr uint32_t kRouteThreads = 1024;
 constexpr uint32_t kRouteMaxExperts = 4096;
+constexpr uint32_t kRouteMapWords = 8192;  // per-expert token bitmaps kept in LDS up to E * ceil(T / 32) words
+constexpr uint32_t kRouteLdsIds = 8192;    // ids read once into LDS up to this many pairs
 
 // One workgroup: per-expert counts (LDS atomics), their prefix sums, the tile
-// table, then each pair's row (an LDS cursor per expert). An expert's segment
-// starts at a multiple of `pad` rows and is cut into tiles of `tile` rows.
-// Rows of one expert come in no fixed order, which changes nothing: every row
-// is computed alone and the combination reads rows by pair.
+// table, then each pair's row. An expert's segment starts at a multiple of
+// `pad` rows and is cut into tiles of `tile` rows. Within its segment an
+// expert's pairs take rows in pair order (token order): a row's place in the
+// tiles decides how the GEMM splits its K range, and so the rounding of its
+// sum, so the order is fixed rather than left to the atomics. A pair's row is
+// its segment start plus the number of earlier tokens routed to its expert:
+// from a bitmap per expert over the tokens and its per-word prefix counts in
+// LDS. (Calls whose bitmaps exceed LDS, or whose ids repeat an expert within
+// a token, count the earlier pairs of the segment instead.)
 __global__ __launch_bounds__(kRouteThreads) void k_moe_route(const int32_t *__restrict__ ids, uint32_t npairs,
                                                              uint32_t top_k, uint32_t E, uint32_t pad, uint32_t tile,
                                                              uint32_t rows_max,
                                                              int32_t *__restrict__ pos, uint32_t *__restrict__ row_tok,
                                                              uint32_t *__restrict__ mt, uint32_t *__restrict__ ntm) {
     __shared__ uint32_t cnt[kRouteMaxExperts], start[kRouteMaxExperts];
+    __shared__ uint32_t bmap[kRouteMapWords], bpre[kRouteMapWords];
     __shared__ uint32_t wsum[kRouteThreads / 64], wtile[kRouteThreads / 64];
+    __shared__ uint32_t dup;
+    __shared__ int32_t sids[kRouteLdsIds];
     const uint32_t tid = threadIdx.x;
+    // the pairs' experts, read once (every loop below walks them; from
+    // global memory each iteration waited a full round trip)
+    const bool ids_lds = npairs <= kRouteLdsIds;
+    if (ids_lds) {
+        constexpr uint32_t NI = kRouteLdsIds / kRouteThreads;
+        int32_t v[NI];  // all loads in flight before the first store
+#pragma unroll
+        for (uint32_t k = 0; k < NI; ++k) {
+            const uint32_t p = tid + k * kRouteThreads;
+            v[k] = p < npairs ? ids[p] : 0;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < NI; ++k) {
+            const uint32_t p = tid + k * kRouteThreads;
+            if (p < npairs) sids[p] = v[k];
+        }
+    }
+    const int32_t *const eid = ids_lds ? sids : ids;
+    // bitmap words per expert, padded to an odd count: a wave's lanes reading
+    // one word index of different experts then fall on different banks
+    const uint32_t ntok = npairs / top_k, W = ((ntok + 31) / 32) | 1u;  // npairs = tokens x top_k
+    // token of pair p: p / top_k as a multiply-high by ceil(2^32 / top_k)
+    // (exact for p < 2^32 / top_k: the error term p * (m*top_k - 2^32) / 2^32
+    // stays below the gap to the next multiple)
+    const uint32_t tdiv = 0xFFFFFFFFu / top_k + 1u;
+    auto tok_of = [&](uint32_t p) __attribute__((always_inline)) {
+        return top_k == 1 ? p : __umulhi(p, tdiv);
+    };
+    const bool use_map = uint64_t(E) * W <= kRouteMapWords;
     for (uint32_t e = tid; e < E; e += kRouteThreads) cnt[e] = 0;
+    if (use_map)
+        for (uint32_t i = tid; i < E * W; i += kRouteThreads) bmap[i] = 0;
+    if (tid == 0) dup = 0;
     // rows that no pair lands on (padding, skipped pairs) are marked ~0
     for (uint32_t i = tid; i < rows_max; i += kRouteThreads) row_tok[i] = ~0u;
     __syncthreads();
     for (uint32_t p = tid; p < npairs; p += kRouteThreads) {
-        const int32_t e = ids[p];
-        if (e >= 0 && uint32_t(e) < E) atomicAdd(&cnt[e], 1u);
+        const int32_t e = eid[p];
+        if (e >= 0 && uint32_t(e) < E) {
+            atomicAdd(&cnt[e], 1u);
+            if (use_map) {
+                const uint32_t t = tok_of(p), bit = 1u << (t & 31);
+                if (atomicOr(&bmap[uint32_t(e) * W + t / 32], bit) & bit) dup = 1;  // the expert twice in a token
+            }
+        }
     }
     __syncthreads();
     // Exclusive prefix sums of rows and of tiles over the experts: each thread
@@ -84,22 +133,74 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(const int32_t *__re
     if (tid == kRouteThreads - 1) *ntm = t0;  // the last thread's end is the total
     // (the row_tok marks above are ordered before the stores below by this barrier)
     __syncthreads();
-    for (uint32_t p = tid; p < npairs; p += kRouteThreads) {
-        const int32_t e = ids[p];
-        int32_t q = -1;
-        if (e >= 0 && uint32_t(e) < E) {
-            q = int32_t(atomicAdd(&start[e], 1u));
-            row_tok[q] = p / top_k;
+    if (use_map && dup == 0) {
+        // per expert, the earlier tokens' count at each bitmap word
+        for (uint32_t e = tid; e < E; e += kRouteThreads) {
+            uint32_t run = 0;
+            for (uint32_t w = 0; w < W; ++w) {
+                bpre[e * W + w] = run;
+                run += __builtin_popcount(bmap[e * W + w]);
+            }
         }
-        pos[p] = q;
+        __syncthreads();
+        for (uint32_t p = tid; p < npairs; p += kRouteThreads) {
+            const int32_t e = eid[p];
+            int32_t q = -1;
+            if (e >= 0 && uint32_t(e) < E) {
+                const uint32_t t = tok_of(p), i = uint32_t(e) * W + t / 32;
+                q = int32_t(start[e] + bpre[i] + __builtin_popcount(bmap[i] & ((1u << (t & 31)) - 1u)));
+                row_tok[q] = t;
+            }
+            pos[p] = q;
+        }
+    } else {
+        // the pair index at some row of its expert's segment (row_tok as
+        // scratch), then each pair's rank among the segment's pairs
+        for (uint32_t p = tid; p < npairs; p += kRouteThreads) {
+            const int32_t e = eid[p];
+            if (e >= 0 && uint32_t(e) < E) row_tok[atomicAdd(&start[e], 1u)] = p;
+        }
+        __syncthreads();
+        for (uint32_t p = tid; p < npairs; p += kRouteThreads) {
+            const int32_t e = eid[p];
+            int32_t q = -1;
+            if (e >= 0 && uint32_t(e) < E) {
+                const uint32_t s1 = start[e], s0 = s1 - cnt[e];  // start[e] is now the segment's end
+                uint32_t rank = 0;
+                for (uint32_t r = s0; r < s1; ++r) rank += row_tok[r] < p ? 1u : 0u;
+                q = int32_t(s0 + rank);
+            }
+            pos[p] = q;
+        }
+        __syncthreads();  // every scratch record read before row_tok is written
+        for (uint32_t p = tid; p < npairs; p += kRouteThreads) {
+            const int32_t q = pos[p];
+            if (q >= 0) row_tok[q] = p / top_k;
+        }
     }
 }
 
-__global__ __launch_bounds__(256) void k_moe_swiglu(float *__restrict__ g, const float *__restrict__ u, size_t n) {
-    const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= n) return;
-    const float gv = g[i];
-    g[i] = gv / (1.0f + expf(-gv)) * u[i];
+// MoE: h = silu(g) * u elementwise (the FFN's SwiGLU, as the decode kernels'
+// epilogue forms it) quantized to Q8_K straight from registers, one wave per
+// 256-element block of h, block-major: h never goes to memory. (Compiled with
+// the mat-vec kernels' flags, so that h is bit for bit the decode SwiGLU
+// epilogue's; the quantizer keeps its one sum apart from its product itself.)
+__global__ __launch_bounds__(256) void k_swiglu_quant_q8k(const float *__restrict__ g, const float *__restrict__ u,
+                                                          int8_t *__restrict__ qs, float *__restrict__ d,
+                                                          int16_t *__restrict__ bsums, uint16_t *__restrict__ dg,
+                                                          uint32_t nblk_total, uint32_t nbk, uint32_t bm_S) {
+    const uint32_t gb = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (gb >= nblk_total) return;
+    const uint32_t lane = threadIdx.x & 63;
+    const float4 gv = reinterpret_cast<const float4 *>(g + size_t(gb) * 256)[lane];
+    const float4 uv = reinterpret_cast<const float4 *>(u + size_t(gb) * 256)[lane];
+    float4 h;
+    h.x = gv.x / (1.0f + expf(-gv.x)) * uv.x;
+    h.y = gv.y / (1.0f + expf(-gv.y)) * uv.y;
+    h.z = gv.z / (1.0f + expf(-gv.z)) * uv.z;
+    h.w = gv.w / (1.0f + expf(-gv.w)) * uv.w;
+    const uint32_t o = (gb % nbk) * bm_S + gb / nbk;  // block-major
+    quant_q8k_block_wave_v(h, qs + size_t(o) * 256, d + o, bsums + size_t(o) * 16, dg + size_t(o) * 16);
 }
 
 // Rank-order weighted sum (ModelMoE.cpp:990-1002): from 0, fma per rank.
@@ -131,17 +232,23 @@ uint32_t moe_max_rows(uint32_t npairs, uint32_t n_experts, uint32_t pad) {
 hipError_t launch_moe_route(const int32_t *ids, uint32_t npairs, uint32_t top_k, uint32_t n_experts, uint32_t pad,
                             uint32_t tile, int32_t *pos, uint32_t *row_tok, uint32_t *mt, uint32_t *ntm,
                             hipStream_t st) {
-    if (npairs == 0 || top_k == 0 || n_experts == 0 || n_experts > kRouteMaxExperts || pad == 0 || tile == 0)
+    if (npairs == 0 || top_k == 0 || n_experts == 0 || n_experts > kRouteMaxExperts || pad == 0 || tile == 0 ||
+        uint64_t(npairs) * top_k >= (uint64_t(1) << 32))  // (the kernel's token-of-pair division)
         return hipErrorInvalidValue;
     k_moe_route<<<1, kRouteThreads, 0, st>>>(ids, npairs, top_k, n_experts, pad, tile,
                                              moe_max_rows(npairs, n_experts, pad), pos, row_tok, mt, ntm);
     return hipGetLastError();
 }
 
-hipError_t launch_moe_swiglu(float *g, const float *u, uint32_t nrows_max, uint32_t ff, hipStream_t st) {
-    const size_t n = size_t(nrows_max) * ff;
-    if (n == 0) return hipErrorInvalidValue;
-    k_moe_swiglu<<<uint32_t((n + 255) / 256), 256, 0, st>>>(g, u, n);
+hipError_t launch_swiglu_quant_q8k(const float *g, const float *u, uint32_t S, uint32_t cols, const ActLayout &L,
+                                   void *buf, hipStream_t st) {
+    if (S == 0 || cols == 0 || cols % 256) return hipErrorInvalidValue;
+    const uint32_t nbk = cols / 256, nb = S * nbk;
+    char *b = static_cast<char *>(buf);
+    k_swiglu_quant_q8k<<<(nb + 3) / 4, 256, 0, st>>>(g, u, reinterpret_cast<int8_t *>(b + L.qs_off),
+                                                     reinterpret_cast<float *>(b + L.d_off),
+                                                     reinterpret_cast<int16_t *>(b + L.bs_off),
+                                                     reinterpret_cast<uint16_t *>(b + L.dg_off), nb, nbk, S);
     return hipGetLastError();
 }
 
