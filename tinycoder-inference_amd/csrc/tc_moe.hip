@@ -204,18 +204,48 @@ __global__ __launch_bounds__(256) void k_swiglu_quant_q8k(const float *__restric
 }
 
 // Rank-order weighted sum (ModelMoE.cpp:990-1002): from 0, fma per rank.
+// A thread sums 4 consecutive outputs (16-byte loads); with top_k <= 8 the
+// loads of every rank are issued before the first fma (the same fma order).
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_moe_combine_rows(const float *__restrict__ y, const int32_t *__restrict__ pos,
                                                           const float *__restrict__ wts, float *__restrict__ out,
                                                           uint32_t top_k, uint32_t H, uint32_t nchunk) {
     const uint32_t t = blockIdx.x / nchunk;
-    const uint32_t i = (blockIdx.x - t * nchunk) * 256 + threadIdx.x;
+    const uint32_t i = ((blockIdx.x - t * nchunk) * 256 + threadIdx.x) * 4;
     if (i >= H) return;
-    float acc = 0.0f;
-    for (uint32_t r = 0; r < top_k; ++r) {
-        const int32_t q = pos[size_t(t) * top_k + r];
-        if (q >= 0) acc = fmaf(wts[size_t(t) * top_k + r], y[size_t(q) * H + i], acc);
+    const int32_t *pt = pos + size_t(t) * top_k;
+    const float *wt = wts + size_t(t) * top_k;
+    if constexpr (VEC) {
+        // H % 4 == 0 and top_k <= 8
+        float4 v[8];
+        float w[8];
+#pragma unroll
+        for (uint32_t r = 0; r < 8; ++r) {
+            const int32_t q = r < top_k ? pt[r] : -1;
+            w[r] = q >= 0 ? wt[r] : 0.0f;
+            v[r] = q >= 0 ? *reinterpret_cast<const float4 *>(y + size_t(q) * H + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (uint32_t r = 0; r < 8; ++r) {
+            if (r < top_k && pt[r] >= 0) {
+                acc.x = fmaf(w[r], v[r].x, acc.x);
+                acc.y = fmaf(w[r], v[r].y, acc.y);
+                acc.z = fmaf(w[r], v[r].z, acc.z);
+                acc.w = fmaf(w[r], v[r].w, acc.w);
+            }
+        }
+        *reinterpret_cast<float4 *>(out + size_t(t) * H + i) = acc;
+    } else {
+        for (uint32_t e = 0; e < 4 && i + e < H; ++e) {
+            float acc = 0.0f;
+            for (uint32_t r = 0; r < top_k; ++r) {
+                const int32_t q = pt[r];
+                if (q >= 0) acc = fmaf(wt[r], y[size_t(q) * H + i + e], acc);
+            }
+            out[size_t(t) * H + i + e] = acc;
+        }
     }
-    out[size_t(t) * H + i] = acc;
 }
 
 }  // namespace
@@ -254,9 +284,13 @@ hipError_t launch_swiglu_quant_q8k(const float *g, const float *u, uint32_t S, u
 
 hipError_t launch_moe_combine_rows(const float *y, const int32_t *pos, const float *wts, float *out, uint32_t T,
                                    uint32_t top_k, uint32_t H, hipStream_t st) {
-    const uint32_t nchunk = (H + 255) / 256;
+    const uint32_t nchunk = (H + 1023) / 1024;  // 4 outputs per thread
     if (T == 0 || H == 0 || uint64_t(T) * nchunk >= (uint64_t(1) << 31)) return hipErrorInvalidValue;
-    k_moe_combine_rows<<<T * nchunk, 256, 0, st>>>(y, pos, wts, out, top_k, H, nchunk);
+    // (y is the library's own buffer: 16-byte aligned; out is the caller's)
+    if (H % 4 == 0 && top_k <= 8 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0)
+        k_moe_combine_rows<true><<<T * nchunk, 256, 0, st>>>(y, pos, wts, out, top_k, H, nchunk);
+    else
+        k_moe_combine_rows<false><<<T * nchunk, 256, 0, st>>>(y, pos, wts, out, top_k, H, nchunk);
     return hipGetLastError();
 }
 
