@@ -530,7 +530,7 @@ int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wt
     const uint32_t ntm_max = tc::moe_max_tiles(P, E, tile);
     auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
     const tc::ActLayout LX = tc::act_layout(TC_Q4_K, P, H), LH = tc::act_layout(TC_Q4_K, P, FF);
-    const size_t ws = std::max(tc::prefill_grouped_workspace_bytes(tile, ntm_max, FF, H, dev->num_cu),
+    const size_t ws = std::max(tc::prefill_grouped_workspace_bytes(tile, ntm_max, FF, H, dev->num_cu, 2),
                                tc::prefill_grouped_workspace_bytes(tile, ntm_max, H, FF, dev->num_cu));
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -545,7 +545,7 @@ int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wt
     // the GEMMs' arrival counters (zeroed by the gather below; each GEMM
     // launch leaves them zero for the next)
     const uint32_t nctr =
-        std::max(tc::prefill_grouped_counter_words(ntm_max, FF), tc::prefill_grouped_counter_words(ntm_max, H));
+        std::max(tc::prefill_grouped_counter_words(ntm_max, FF, 2), tc::prefill_grouped_counter_words(ntm_max, H));
     const size_t o_ctr = take(size_t(nctr) * 4);
     if (!ensure(dev->aux, dev->aux_bytes, off)) return fail(TC_E_LAUNCH, "hipMalloc(%zu) failed", off);
     char *b = static_cast<char *>(dev->aux);
@@ -562,11 +562,9 @@ int moe_grouped(Device *dev, const float *x, const int32_t *ids, const float *wt
     e = tc::launch_quant_act_rows(x, tok, P, H, LX, b + o_ax, st, ctr, nctr);
     if (e != hipSuccess) return hip_fail(e, "MoE activation gather");
     const tc::ActView ax = act_view(b + o_ax, LX, 0, TC_Q4_K, H);
+    // gate and up in one launch (their tiles share the activations)
     e = tc::launch_prefill_grouped(wg, gstride, ax, g, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, ctr, b + o_ws,
-                                   st);
-    if (e == hipSuccess)
-        e = tc::launch_prefill_grouped(wu, gstride, ax, u, P, FF, H, mt, ntm, ntm_max, tile, dev->num_cu, ctr,
-                                       b + o_ws, st);
+                                   st, wu, u);
     if (e != hipSuccess) return hip_fail(e, "MoE gate/up GEMM");
     e = tc::launch_swiglu_quant_q8k(g, u, P, FF, LH, b + o_ah, st);
     if (e != hipSuccess) return hip_fail(e, "MoE SwiGLU");

@@ -94,14 +94,17 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
 // most `tile` rows, tile from prefill_grouped_tile). ctr: the arrival
 // counters, prefill_grouped_counter_words() of them, zero when the launch
 // starts (every launch leaves them zero again); workspace:
-// prefill_grouped_workspace_bytes() for the partial tiles.
+// prefill_grouped_workspace_bytes() for the partial tiles. With W2 and
+// out2 (mats = 2) a second matrix of the same shape and expert stride (MoE
+// gate and up) goes in the same launch: out2 = act . W2.
 uint32_t prefill_grouped_tile(uint32_t rows_total, uint32_t n_experts);
-uint32_t prefill_grouped_counter_words(uint32_t ntm_max, uint32_t N);
-size_t prefill_grouped_workspace_bytes(uint32_t tile, uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu);
+uint32_t prefill_grouped_counter_words(uint32_t ntm_max, uint32_t N, uint32_t mats = 1);
+size_t prefill_grouped_workspace_bytes(uint32_t tile, uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu,
+                                       uint32_t mats = 1);
 hipError_t launch_prefill_grouped(const void *W, uint64_t wstride, const ActView &act, float *out,
                                   uint32_t rows_total, uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm,
                                   uint32_t ntm_max, uint32_t tile, int num_cu, uint32_t *ctr, void *workspace,
-                                  hipStream_t st);
+                                  hipStream_t st, const void *W2 = nullptr, float *out2 = nullptr);
 
 // ---- MoE prefill over expert-sorted rows ----
 // Device-side router: pairs p = t*top_k + r (ids[p] in [0, E), others

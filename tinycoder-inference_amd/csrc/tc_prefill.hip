@@ -190,35 +190,47 @@ struct PfArgs {
     const uint32_t *mt;
     const uint32_t *ntm_dev;
     uint64_t wstride;
+    // Grouped mode with two matrices of one shape (MoE gate and up): the
+    // tiles of W2 / out2 follow those of W / out in one launch.
+    const uint8_t *W2;
+    float *out2;
 };
 
-// A tile's token rows [m0, mend) and weight matrix.
+// A tile's token rows [m0, mend), weight matrix and output.
 struct PfTile {
     uint32_t m0, mend, n0;
     const uint8_t *W;
+    float *out;
 };
 template <bool GRP>
 __device__ __forceinline__ PfTile pf_tile(const PfArgs &a, uint32_t tile, uint32_t TT, uint32_t PR) {
-    const uint32_t tn = tile % a.ntn, tm = tile / a.ntn;
     PfTile t;
-    t.n0 = tn * PR;
     if constexpr (GRP) {
+        const uint32_t nt1 = *a.ntm_dev * a.ntn;  // tiles of one matrix
+        const bool second = a.W2 != nullptr && tile >= nt1;
+        if (second) tile -= nt1;
+        const uint32_t tn = tile % a.ntn, tm = tile / a.ntn;
+        t.n0 = tn * PR;
         // (wave-uniform: readfirstlane keeps them, and the load descriptors
         // built from them, in scalar registers)
         t.m0 = __builtin_amdgcn_readfirstlane(a.mt[3 * tm]);
         t.mend = __builtin_amdgcn_readfirstlane(a.mt[3 * tm + 1]);
-        t.W = a.W + uint64_t(__builtin_amdgcn_readfirstlane(a.mt[3 * tm + 2])) * a.wstride;
+        t.W = (second ? a.W2 : a.W) + uint64_t(__builtin_amdgcn_readfirstlane(a.mt[3 * tm + 2])) * a.wstride;
+        t.out = second ? a.out2 : a.out;
     } else {
+        const uint32_t tn = tile % a.ntn, tm = tile / a.ntn;
+        t.n0 = tn * PR;
         t.m0 = tm * TT;
         t.mend = a.M;
         t.W = a.W;
+        t.out = a.out;
     }
     return t;
 }
 template <bool GRP>
 __device__ __forceinline__ uint32_t pf_ntiles(const PfArgs &a) {
     if constexpr (GRP)
-        return *a.ntm_dev * a.ntn;
+        return *a.ntm_dev * a.ntn * (a.W2 != nullptr ? 2u : 1u);
     else
         return a.ntiles;
 }
@@ -1221,7 +1233,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const uint32_t ml = 32 * (tg * NB + t) + 8 * q + 4 * g + e, m = m0 + ml;
-                        if (m < tg_.mend && n < a.N) a.out[size_t(m) * a.N + n] = acc[t][4 * q + e];
+                        if (m < tg_.mend && n < a.N) tg_.out[size_t(m) * a.N + n] = acc[t][4 * q + e];
                     }
             continue;
         }
@@ -1321,7 +1333,7 @@ __global__ __launch_bounds__(64 * PW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t ml = 32 * (tg * NB + t) + 8 * q + 4 * g + e, m = m0 + ml;
-                    if (m < tg_.mend && n < a.N) a.out[size_t(m) * a.N + n] = acc[t][4 * q + e];
+                    if (m < tg_.mend && n < a.N) tg_.out[size_t(m) * a.N + n] = acc[t][4 * q + e];
                 }
     }
 }
@@ -1398,7 +1410,7 @@ __global__ __launch_bounds__(256) void k_pf_fixup(PfArgs a) {
         const uint32_t ml = (4 * i) / PR, nl = (4 * i) % PR;
         const uint32_t m = m0 + ml, n = n0 + nl;
         if (m >= tg_.mend) continue;
-        float *o = a.out + size_t(m) * a.N + n;
+        float *o = tg_.out + size_t(m) * a.N + n;
         const float sv[4] = {s[k].x, s[k].y, s[k].z, s[k].w};
         if (n + 3 < a.N && (a.N & 3) == 0) {
             *reinterpret_cast<float4 *>(o) = s[k];
@@ -1598,28 +1610,29 @@ uint32_t prefill_grouped_tile(uint32_t rows_total, uint32_t n_experts) {
     return 32u * pf_grouped_nt(rows_total, n_experts);
 }
 namespace {
-uint32_t pf_grouped_grid(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
-    const uint64_t units = uint64_t(ntm_max) * ((N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR) * (K / 256);
+uint32_t pf_grouped_grid(uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu, uint32_t mats) {
+    const uint64_t units = uint64_t(mats) * ntm_max * ((N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR) * (K / 256);
     return uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(uint64_t(num_cu), units / 2)));
 }
 }  // namespace
-uint32_t prefill_grouped_counter_words(uint32_t ntm_max, uint32_t N) {
-    return ntm_max * ((N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR);
+uint32_t prefill_grouped_counter_words(uint32_t ntm_max, uint32_t N, uint32_t mats) {
+    return mats * ntm_max * ((N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR);
 }
-size_t prefill_grouped_workspace_bytes(uint32_t tile, uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu) {
-    return size_t(pf_grouped_grid(ntm_max, N, K, num_cu)) * 2 * tile * PfType<kQ4_K>::PR * 4;
+size_t prefill_grouped_workspace_bytes(uint32_t tile, uint32_t ntm_max, uint32_t N, uint32_t K, int num_cu,
+                                       uint32_t mats) {
+    return size_t(pf_grouped_grid(ntm_max, N, K, num_cu, mats)) * 2 * tile * PfType<kQ4_K>::PR * 4;
 }
 
 hipError_t launch_prefill_grouped(const void *W, uint64_t wstride, const ActView &act, float *out,
                                   uint32_t rows_total, uint32_t N, uint32_t K, const uint32_t *mt, const uint32_t *ntm,
                                   uint32_t ntm_max, uint32_t tile, int num_cu, uint32_t *ctr, void *workspace,
-                                  hipStream_t st) {
+                                  hipStream_t st, const void *W2, float *out2) {
     if (rows_total == 0 || N == 0 || K == 0 || K % 256 || ntm_max == 0 || workspace == nullptr || ctr == nullptr ||
         act.dg == nullptr)
         return hipErrorInvalidValue;
     const uint32_t ntn = (N + PfType<kQ4_K>::PR - 1) / PfType<kQ4_K>::PR;
     if (uint64_t(rows_total) * K >= (uint64_t(1) << 32) || uint64_t(N) * (K / 256) * 144 >= (uint64_t(1) << 32) ||
-        uint64_t(ntm_max) * ntn * (K / 256) >= (uint64_t(1) << 32))
+        uint64_t(ntm_max) * ntn * (K / 256) * 2 >= (uint64_t(1) << 32) || (W2 == nullptr) != (out2 == nullptr))
         return hipErrorInvalidValue;
     PfArgs a{};
     a.W = static_cast<const uint8_t *>(W);
@@ -1639,7 +1652,9 @@ hipError_t launch_prefill_grouped(const void *W, uint64_t wstride, const ActView
     a.mt = mt;
     a.ntm_dev = ntm;
     a.wstride = wstride;
-    a.G = pf_grouped_grid(ntm_max, N, K, num_cu);
+    a.W2 = static_cast<const uint8_t *>(W2);
+    a.out2 = out2;
+    a.G = pf_grouped_grid(ntm_max, N, K, num_cu, W2 != nullptr ? 2u : 1u);
     switch (tile) {
         case 32: return pf_launch<kQ4_K, 1, true>(a, st);
         case 64: return pf_launch<kQ4_K, 2, true>(a, st);
