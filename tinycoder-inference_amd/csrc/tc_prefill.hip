@@ -1,5 +1,5 @@
 // tc_prefill.hip -- prefill GEMM out[m][n] = W[n] . x[m] for Q4_K, Q5_K,
-// Q6_K, Q8_0, IQ3_XXS and IQ3_S weights on the int8 matrix cores
+// Q6_K, Q8_0, IQ3_XXS, IQ3_S and IQ2_S weights on the int8 matrix cores
 // (v_mfma_i32_32x32x32_i8). The weights of a tile are converted once per
 // token tile of up to 128 tokens, in the registers of the lanes that feed
 // them to the MFMA.
@@ -29,6 +29,8 @@
 //    region in LDS.
 //  * IQ3_XXS, IQ3_S: as Q4_K (256 rows); the sign-applied codebook is built
 //    in LDS once per workgroup.
+//  * IQ2_S: as Q4_K (256 rows); its codebook (8-byte entries) in LDS, the
+//    signs applied in registers.
 //
 // Q4_K (reference dequantizeQ4_KBlock, GGMLDequantize.hpp:436-477): a weight
 // of sub-block s is w = d*sc_s*q - dmin*m_s with q in 0..15 and sc_s, m_s in
@@ -62,7 +64,9 @@
 // them to finish its part, in workgroup order (deterministic); the others
 // leave their partial tiles in memory (system-scope stores) and count their
 // arrival on the tile's counter. Tiles split over more workgroups are summed
-// by k_pf_fixup, a second launch, in the same order.
+// by k_pf_fixup, a second launch, in the same order. A workgroup's range falls
+// into one segment per tile; each segment's last superblock iteration stages
+// the next segment's first superblock.
 #include <type_traits>
 
 #include "tc_kernels.hpp"
