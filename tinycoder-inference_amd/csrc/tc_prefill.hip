@@ -1449,15 +1449,16 @@ uint32_t pf_rows(int type) { return type == kQ8_0 ? PfType<kQ8_0>::PR : PfType<k
 // (measured: Q4_K 17408x5120, M=512 (2 per tile) 120 -> 115 us; M=128 (5
 // per tile) 47 -> 56 us).
 constexpr uint32_t kFusedMax = 3;
-bool pf_fused(uint64_t units, uint32_t G, uint32_t nblk) {
+bool pf_fused(uint64_t units, uint32_t G, uint32_t nblk, uint32_t fmax) {
     const uint64_t len = units / G;  // shortest range
     if (len == 0) return false;
-    return (nblk - 1 + len - 1) / len + 1 <= kFusedMax;
+    return (nblk - 1 + len - 1) / len + 1 <= fmax;
 }
 
 struct PfGeom {
     int nt;
-    bool wide;  // Q8_0: the 256-row geometry (kQ8W)
+    bool wide;   // Q8_0: the 256-row geometry (kQ8W)
+    bool fused;  // split tiles summed inside the kernel (else by the fixup launch)
     uint32_t tt, pr, ntm, ntn, ntiles, G;
 };
 // The wide Q8_0 geometry from this many tokens on (at 128: 65 against 58 us,
@@ -1476,6 +1477,7 @@ PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_
     const uint64_t units = uint64_t(g.ntiles) * (K / 256);
     // one workgroup per CU, each with at least 2 superblocks of work
     g.G = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(uint64_t(num_cu), units / 2)));
+    g.fused = pf_fused(units, g.G, K / 256, kFusedMax);
     return g;
 }
 // 64-token tiles instead of 128 where that lets the split tiles be summed
@@ -1485,13 +1487,23 @@ PfGeom pf_geom_nt(int type, int nt, uint32_t M, uint32_t N, uint32_t K, int num_
 // tiles measured as fast or faster). Only up to kNt2MaxM tokens: the fixup
 // launch costs the same at any M while the doubled conversion grows with it.
 constexpr uint32_t kNt2MaxM = 256;
+// Up to kNt2MaxM tokens, the types whose weight conversion costs most per
+// superblock (all but Q4_K and Q8_0) keep their 128-token tiles where the
+// tiles' split has at most 6 contributors, summed in the kernel (18944x3584,
+// M = 128: Q5_K 50.9 -> 48.2 us, Q6_K 51.1 -> 47.0, IQ3_XXS 49.5 -> 47.5,
+// IQ2_S 55.5 -> 47.5; Q4_K at 17408x5120 measured 45.3 -> 55.9 that way). The
+// 64-token fallback keeps the limit of 3 (with 6 it took 3584x18944 at M = 256
+// from 72 to 90 us).
+constexpr uint32_t kFusedMaxKeep = 6;
 PfGeom pf_geom(int type, uint32_t M, uint32_t N, uint32_t K, int num_cu) {
-    const PfGeom g = pf_geom_nt(type, pf_nt(type, M), M, N, K, num_cu);
-    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 ||
-        pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256))
+    PfGeom g = pf_geom_nt(type, pf_nt(type, M), M, N, K, num_cu);
+    if (g.nt != 4 || M > kNt2MaxM || type == kQ8_0 || g.fused) return g;
+    if (type != kQ4_K && pf_fused(uint64_t(g.ntiles) * (K / 256), g.G, K / 256, kFusedMaxKeep)) {
+        g.fused = true;
         return g;
+    }
     const PfGeom h = pf_geom_nt(type, 2, M, N, K, num_cu);
-    return pf_fused(uint64_t(h.ntiles) * (K / 256), h.G, K / 256) ? h : g;
+    return h.fused ? h : g;
 }
 
 template <int TYPE, int NT, bool GRP = false>
@@ -1558,7 +1570,7 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
     a.ntn = g.ntn;
     a.ntiles = g.ntiles;
     a.G = g.G;
-    a.fused = pf_fused(a.ntiles * a.nblk, a.G, a.nblk) ? 1u : 0u;
+    a.fused = g.fused ? 1u : 0u;
     if (type == kQ8_0) {
         if (g.wide) return pf_launch<kQ8W, 4>(a, st);
         return g.nt == 2 ? pf_launch<kQ8_0, 2>(a, st) : pf_launch<kQ8_0, 4>(a, st);
