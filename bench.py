@@ -423,7 +423,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
-              "(the hot path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the hot path runs on one GPU: each GPU of a sharded deployment would run this same "
+              "single-GPU launch on its own shard of the weight rows)", file=sys.stderr)
         sys.exit(2)
 
     import torch
