@@ -1620,7 +1620,9 @@ hipError_t launch_prefill(int type, const void *W, const ActView &act, float *ou
 // Grouped (MoE) mode: token-tile width from the average rows per expert.
 int pf_grouped_nt(uint32_t rows_total, uint32_t n_experts) {
     const uint32_t avg = (rows_total + n_experts - 1) / n_experts;
-    return avg <= 32 ? 1 : avg <= 64 ? 2 : 4;
+    // (128-row tiles from 49 rows per expert on: 1024 tokens x top-8 over 128
+    // experts, 64 rows each, 255 -> 249 us with them against 64-row tiles)
+    return avg <= 32 ? 1 : avg <= 48 ? 2 : 4;
 }
 uint32_t prefill_grouped_tile(uint32_t rows_total, uint32_t n_experts) {
     return 32u * pf_grouped_nt(rows_total, n_experts);
